@@ -1,0 +1,171 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Synthetic MoE layer data in WARP's container layout, built with numpy.
+
+Small, fast and deterministic: random codebooks, random index streams,
+random f16 row scales, and trunk tensors (router, bias, shared expert) in
+F32 / Q8G / Q4G.  The byte layout is the container's (expert record:
+[48 B header][gate idx][up idx][down idx][f16 scales], 4 KiB padded;
+src/waste_format.h:98-130, docs/FORMAT.md:171-263; Q-format rows:
+tools/convert.py:893-924).  Used by the CPU tests, the golden-vector
+script and the GPU parity tests at small sizes.
+"""
+import struct
+import zlib
+
+import numpy as np
+
+MAGIC_EXPERT = 0x50584557
+MAGIC_CODEBOOK = 0x4B424357
+FMT_F32, FMT_Q8G, FMT_Q4G, FMT_VQ3R = 0, 2, 3, 4
+STAGES, ENTRIES, VEC_DIM, BLOCK = 3, 256, 8, 64
+
+
+def block_indices(idx, M, N):
+    """idx [M][N/8][stages] u8 -> [ceil(M/64)][N/8][64][stages], zero-padded
+    rows (tools/convert.py:777-792)."""
+    nv = N // VEC_DIM
+    nb = (M + BLOCK - 1) // BLOCK
+    pad = np.zeros((nb * BLOCK, nv, STAGES), np.uint8)
+    pad[:M] = idx
+    return pad.reshape(nb, BLOCK, nv, STAGES).transpose(0, 2, 1, 3).copy()
+
+
+def unblock_indices(raw, M, N):
+    nv = N // VEC_DIM
+    nb = (M + BLOCK - 1) // BLOCK
+    t = np.frombuffer(raw, np.uint8, nb * nv * BLOCK * STAGES)
+    return t.reshape(nb, nv, BLOCK, STAGES).transpose(0, 2, 1, 3).reshape(nb * BLOCK, nv, STAGES)[:M]
+
+
+def make_record(layer, eid, cb_base, shapes, idx_list, scale_list):
+    """One WEXP record.  shapes = [(I,H),(I,H),(H,I)]; idx_list[k] is
+    [M][N/8][3] u8; scale_list[k] is [M] f16 bits (u16)."""
+    body = bytearray()
+    offs = []
+    off = 48
+    for (M, N), idx in zip(shapes, idx_list):
+        offs.append(off)
+        b = block_indices(idx, M, N).tobytes()
+        body += b
+        off += len(b)
+    corr = off
+    for s in scale_list:
+        body += np.asarray(s, np.uint16).tobytes()
+    total = 48 + len(body)
+    blocks = (total + 4095) // 4096
+    hdr = struct.pack("<IHHBBHHHIIIIIIII", MAGIC_EXPERT, layer, eid, FMT_VQ3R, 0,
+                      cb_base, 0, 0, blocks, offs[0], offs[1], offs[2], corr,
+                      zlib.crc32(bytes(body)) & 0xFFFFFFFF, 0, 0)
+    rec = bytearray(blocks * 4096)
+    rec[:48] = hdr
+    rec[48:48 + len(body)] = body
+    return bytes(rec)
+
+
+def f16_bits(a):
+    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+
+
+def quant_q8g(W, group=128):
+    """int8 + f16 scale per group (tools/convert.py:913-924): scale =
+    amax/127 in fp32, q = clamp(round_half_even(w / scale)), stored scale
+    rounded to f16."""
+    rows, N = W.shape
+    ng = (N + group - 1) // group
+    Wp = np.zeros((rows, ng * group), np.float32)
+    Wp[:, :N] = W
+    g = Wp.reshape(rows, ng, group)
+    sc = np.maximum(np.abs(g).max(-1, keepdims=True), np.float32(1e-8)) / np.float32(127.0)
+    q = np.clip(np.rint(g / sc), -127, 127).astype(np.int8).reshape(rows, ng * group)
+    return q, f16_bits(sc.reshape(rows, ng)), ng * group
+
+
+def quant_q4g(W, group=128):
+    """int4 two per byte, low nibble first, +8 bias, f16 scale per group
+    (tools/convert.py:893-910): scale = amax/7."""
+    rows, N = W.shape
+    ng = (N + group - 1) // group
+    Wp = np.zeros((rows, ng * group), np.float32)
+    Wp[:, :N] = W
+    g = Wp.reshape(rows, ng, group)
+    sc = np.maximum(np.abs(g).max(-1, keepdims=True), np.float32(1e-8)) / np.float32(7.0)
+    q = np.clip(np.rint(g / sc), -8, 7).astype(np.int32).reshape(rows, ng * group)
+    nib = (q + 8).astype(np.uint8) & 0x0F
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
+    return packed.view(np.int8), f16_bits(sc.reshape(rows, ng)), ng * group // 2
+
+
+class Tensor:
+    """A trunk tensor: fmt, rows, cols, group, payload (np array), f16
+    scales (np u16 or None), rowbytes."""
+
+    def __init__(self, fmt, rows, cols, group, q, qs, rowbytes):
+        self.fmt, self.rows, self.cols, self.group = fmt, rows, cols, group
+        self.q, self.qs, self.rowbytes = q, qs, rowbytes
+
+    @staticmethod
+    def absent():
+        return Tensor(FMT_F32, 0, 0, 0, None, None, 0)
+
+    @staticmethod
+    def make(fmt, W):
+        rows, cols = W.shape
+        if fmt == FMT_F32:
+            return Tensor(fmt, rows, cols, 0, np.ascontiguousarray(W, np.float32), None, cols * 4)
+        if fmt == FMT_Q8G:
+            q, qs, rb = quant_q8g(W)
+            return Tensor(fmt, rows, cols, 128, q, qs, rb)
+        q, qs, rb = quant_q4g(W)
+        return Tensor(fmt, rows, cols, 128, q, qs, rb)
+
+
+class Layer:
+    """One synthetic MoE layer."""
+
+    def __init__(self, H, I, E, K, *, score_func=0, renorm=0, routed_scale=1.0,
+                 n_group=1, topk_group=1, n_shared=0, router_fmt=FMT_F32,
+                 shared_fmt=FMT_Q8G, bias=False, seed=0, cb_base=0,
+                 book_scale=0.3, subnormal_books=0):
+        rng = np.random.default_rng(seed)
+        self.H, self.I, self.E, self.K = H, I, E, K
+        self.score_func, self.renorm, self.routed_scale = score_func, renorm, routed_scale
+        self.n_group, self.topk_group, self.n_shared = n_group, topk_group, n_shared
+        self.cb_base = cb_base
+        self.n_books = cb_base + 3 * STAGES
+        books = (rng.standard_normal((self.n_books, ENTRIES, VEC_DIM)) * book_scale).astype(np.float32)
+        self.books_f16 = f16_bits(books)
+        if subnormal_books:
+            # plant fp16 subnormals: the loader flushes them to signed zero
+            flat = self.books_f16.reshape(-1)
+            pos = rng.choice(flat.size, subnormal_books, replace=False)
+            flat[pos] = (rng.integers(1, 1024, subnormal_books) |
+                         (rng.integers(0, 2, subnormal_books) << 15)).astype(np.uint16)
+        shapes = [(I, H), (I, H), (H, I)]
+        self.shapes = shapes
+        self.records = []
+        self.idx = []
+        self.scales = []
+        for e in range(E):
+            il = [rng.integers(0, ENTRIES, (M, N // VEC_DIM, STAGES), dtype=np.uint8) for M, N in shapes]
+            sl = [f16_bits(rng.uniform(0.01, 0.05, M)) for M, _ in shapes]
+            self.idx.append(il)
+            self.scales.append(sl)
+            self.records.append(make_record(0, e, cb_base, shapes, il, sl))
+        self.rec_bytes = len(self.records[0])
+        self.router = Tensor.make(router_fmt, (rng.standard_normal((E, H)) * 0.02).astype(np.float32))
+        self.bias = (rng.standard_normal(E) * 0.02).astype(np.float32) if bias else None
+        SI = I * (n_shared if n_shared else 1)
+        if n_shared:
+            self.sh = [Tensor.make(shared_fmt, (rng.standard_normal((SI, H)) * 0.02).astype(np.float32)),
+                       Tensor.make(shared_fmt, (rng.standard_normal((SI, H)) * 0.02).astype(np.float32)),
+                       Tensor.make(shared_fmt, (rng.standard_normal((H, SI)) * 0.02).astype(np.float32))]
+        else:
+            self.sh = [Tensor.absent()] * 3
+        self.rng = rng
+
+    def bank(self):
+        return b"".join(self.records)
+
+    def inputs(self, T, seed=1):
+        r = np.random.default_rng(seed)
+        return r.standard_normal((T, self.H)).astype(np.float32)
