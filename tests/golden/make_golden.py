@@ -1,0 +1,110 @@
+# SPDX-License-Identifier: Apache-2.0
+"""Writes tests/golden/*.npz from the reference engine compiled from its own
+sources (oracle/_ref/libwasteref.so, built by `make -C oracle` where the
+reference tree is present).
+
+Each case is a seeded synthetic layer from tests/records.py.  A fixture
+stores the case's configuration, a sha256 of every input byte (so a test can
+regenerate the inputs and prove they are the ones the vectors were made
+from), and the reference's outputs:
+
+  lut{0,1}      LUT of token 0 against the gate books, portable / AVX-512
+  vq{0,1}       vq_rows of expert 0's gate on that LUT
+  mvq{0,1}      shared-expert gate matvec (Q8G/Q4G cases)
+  scores        router_scores of the oracle's logits of token 0
+  layer_out{o}, layer_ids{o}      moe_layer, token 0, order o
+  chunk_out{o}, chunk_ids{o}, chunk_w{o}   moe_chunk over all tokens
+  act           waste_act_pair_range on seeded vectors
+  exp_x, exp_y  glibc expf on 65,536 seeded inputs and the special values
+
+  python tests/golden/make_golden.py
+"""
+import hashlib
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(HERE))
+from records import FMT_F32, FMT_Q4G, FMT_Q8G, Layer  # noqa: E402
+from oracle_lib import Oracle, Ref  # noqa: E402
+
+# name -> (H, I, E, K, kwargs, T)
+CASES = {
+    "softmax_f32": (256, 128, 16, 4, dict(score_func=1, seed=11), 3),
+    "sigmoid_q8g": (256, 128, 16, 4, dict(score_func=0, renorm=1, routed_scale=2.446, bias=True,
+                                          n_shared=1, shared_fmt=FMT_Q8G, router_fmt=FMT_Q8G, seed=12), 4),
+    "sigmoid_q4g": (384, 128, 32, 8, dict(score_func=0, renorm=1, routed_scale=2.5, bias=True,
+                                          n_shared=1, shared_fmt=FMT_Q4G, router_fmt=FMT_F32, seed=13,
+                                          subnormal_books=40), 3),
+}
+
+
+def case_layer(name):
+    H, I, E, K, kw, T = CASES[name]
+    L = Layer(H, I, E, K, **kw)
+    return L, L.inputs(T, seed=kw["seed"] + 100)
+
+
+def input_digest(L, X):
+    h = hashlib.sha256()
+    h.update(L.bank())
+    h.update(L.books_f16.tobytes())
+    for t in [L.router] + list(L.sh):
+        if t.rows:
+            h.update(t.q.tobytes())
+            if t.qs is not None:
+                h.update(t.qs.tobytes())
+    if L.bias is not None:
+        h.update(L.bias.tobytes())
+    h.update(X.tobytes())
+    return h.hexdigest()
+
+
+def main():
+    orc, ref = Oracle(), Ref()
+    if ref.isa != 2:
+        print("warning: this host does not run the reference's AVX-512 kernels; order 1 = portable")
+    for name in CASES:
+        L, X = case_layer(name)
+        _, bT = orc.books(L.books_f16)
+        out = {"digest": np.array(input_digest(L, X)), "isa": np.array(ref.isa)}
+        for o in (0, 1):
+            ref.set_order(o)
+            lut = ref.lutb(bT, X[0], L.cb_base)
+            out[f"lut{o}"] = lut
+            out[f"vq{o}"] = ref.vq_rows(L.records[0][48:], L.scales[0][0], lut, L.I, L.H // 8)
+            if L.sh[0].rows:
+                out[f"mvq{o}"] = ref.mvq_rows(L.sh[0], X[0])
+            rc, lo, lr, _ = ref.moe(L, X[:1], bT)
+            assert rc == 0, rc
+            out[f"layer_out{o}"], out[f"layer_ids{o}"] = lo[0], lr[0]
+            rc, co, cr, cw = ref.moe(L, X, bT)
+            assert rc == 0, rc
+            out[f"chunk_out{o}"], out[f"chunk_ids{o}"], out[f"chunk_w{o}"] = co, cr, cw
+        if L.router.fmt == FMT_F32:
+            out["logits"] = ref.matvec_f32(L.router.q, X[0])
+        else:
+            ref.set_order(1)
+            out["logits"] = ref.mvq_rows(L.router, X[0])
+        out["scores"] = ref.router_scores(L.score_func, out["logits"])
+        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **out)
+        print(name, "written")
+
+    # activation and expf
+    r = np.random.default_rng(5)
+    g = (r.standard_normal(4096) * 4).astype(np.float32)
+    u = r.standard_normal(4096).astype(np.float32)
+    specials = np.array([0.0, -0.0, 1.0, -1.0, 88.0, 88.72283, 88.7229, -87.0, -103.0, -103.97,
+                         -104.0, 30.0, -30.0, np.inf, -np.inf, 1e-30, -1e-30, float.fromhex("0x1.04845ep+5"),
+                         float.fromhex("-0x1.f8cbb2p+5")], np.float32)
+    ex = np.concatenate([specials, (r.standard_normal(65536) * 20).astype(np.float32)])
+    ey = np.array([ref.lib.ref_expf(float(v)) for v in ex], np.float32)
+    np.savez_compressed(os.path.join(HERE, "scalars.npz"), act_g=g, act_u=u,
+                        act=ref.act_pair(g, u), exp_x=ex, exp_y=ey)
+    print("scalars written")
+
+
+if __name__ == "__main__":
+    main()
