@@ -1,0 +1,153 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * waste_hip.h — the MI355X (gfx950) backend for WARP's MoE expert path.
+ *
+ * A C ABI: plain pointers and sizes, no C++ or framework types.  Three
+ * levels, matching the three things a WARP engine would bind:
+ *
+ *   1. waste_register_hip  — a waste_kernels registration, the slot the
+ *      engine's backend init already reserves for a device backend
+ *      (src/backend.c:44-62, 206-216; semantics of waste_register_metal,
+ *      src/metal.m:464-519).
+ *   2. waste_hip_vq3r      — the VQ3R batch apply (waste_metal_vq3r,
+ *      src/waste_metal.h:31-44): host jobs in, host rows out,
+ *      all-or-nothing.
+ *   3. waste_hip_moe_*     — a device-resident MoE layer that takes over
+ *      moe_layer (src/model.c:5488-5939) and moe_chunk
+ *      (src/model.c:7110-7285) from router logits to the combined output,
+ *      with expert records resident in HBM.
+ *
+ * Return codes: 0 success; WASTE_HIP_E* (negative) on failure.
+ */
+#ifndef WASTE_HIP_H
+#define WASTE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "waste_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WASTE_HIP_OK          0
+#define WASTE_HIP_EINVAL    (-1)   /* bad argument or shape              */
+#define WASTE_HIP_ENODEV    (-2)   /* no gfx950 device                   */
+#define WASTE_HIP_ENOMEM    (-3)   /* device allocation failed           */
+#define WASTE_HIP_ERECORD   (-4)   /* record failed its header checks    */
+#define WASTE_HIP_ECRC      (-5)   /* record payload checksum mismatch   */
+#define WASTE_HIP_EUNBOUND  (-6)   /* a routed expert has no record      */
+#define WASTE_HIP_EROUTE    (-7)   /* a selection pass found no expert   */
+#define WASTE_HIP_EDEVICE   (-8)   /* a HIP runtime call failed          */
+
+/* Library name and device check.  NULL when no usable gfx950 device. */
+const char *waste_hip_device_name(void);
+
+/* ---- 1. kernel-table registration ------------------------------------- */
+
+/* Fills t->mvq_rows_f32 with a device implementation (whole range in one
+ * call: t->on_device = 1) and t->device_min_bytes; leaves every other slot
+ * as it was.  Returns "HIP (gfx950)" or NULL to decline (no device).
+ * Replaces: the accelerator registration of src/backend.c:206-216. */
+const char *waste_register_hip(waste_kernels *t);
+
+/* Drops the device copies of host tensors the slots have cached (keyed by
+ * host address).  Call before the engine frees the host buffers.
+ * Replaces: waste_metal_release_host_buffers, src/metal.m:521-531. */
+void waste_hip_release_host_buffers(void);
+
+/* ---- 2. VQ3R batch ----------------------------------------------------- */
+
+/* Runs every job on the device: y[r] for r < m, each row's sum in the
+ * engine's exact vq_rows order (bit-identical to the CPU path).  Host
+ * pointers in, host rows out.  0 if every job ran; nonzero means nothing
+ * was written and the caller must do them itself.
+ * Replaces: waste_metal_vq3r, src/waste_metal.h:31-44. */
+int waste_hip_vq3r(const waste_vq_job *jobs, int n);
+
+/* ---- 3. device MoE layer ------------------------------------------------ */
+
+typedef struct waste_hip_moe waste_hip_moe;
+
+typedef struct {
+    int hidden;          /* H                                               */
+    int n_experts;       /* E                                               */
+    int top_k;           /* K                                               */
+    int moe_inter;       /* I (routed expert width)                         */
+    int n_shared;        /* shared experts fused into one of width I*n (0)  */
+    int score_func;      /* WASTE_SCORE_SIGMOID / _SOFTMAX / _SQRTSOFTPLUS  */
+    int renorm;          /* moe_renormalize                                 */
+    float routed_scale;  /* routed_scaling_factor                           */
+    int n_group;         /* group-limited routing: groups (<= 1: off)       */
+    int topk_group;      /* groups kept                                     */
+    int layer;           /* the layer id records must carry                 */
+    int max_tokens;      /* largest T forward() will see                    */
+    int verify_records;  /* check each record's crc32 when it is loaded     */
+} waste_hip_moe_cfg;
+
+/* A trunk tensor as the engine holds it (waste_tensor, src/model.h:32-50):
+ * fmt WQ_F32 (q = float rows), WQ_Q8G or WQ_Q4G (q = packed rows, qs = f16
+ * group scales, one per `group` inputs).  Host pointers; copied. */
+typedef struct {
+    int fmt, rows, cols, group;
+    const void *q;
+    const uint16_t *qs;
+    size_t rowbytes;
+} waste_hip_tensor;
+
+int  waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out);
+void waste_hip_moe_destroy(waste_hip_moe *m);
+
+/* Router gate.weight and e_score_correction_bias (bias may be NULL). */
+int waste_hip_moe_set_router(waste_hip_moe *m, const waste_hip_tensor *gate,
+                             const float *bias);
+/* Shared expert gate/up/down; all NULL for none. */
+int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
+                             const waste_hip_tensor *up,
+                             const waste_hip_tensor *down);
+/* codebooks.bin payloads, fp16 [n_books][256][8], converted as the engine's
+ * loader does (subnormals flushed; src/model.c:2906-2941). */
+int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16,
+                                int n_books);
+/* One expert record (host memory), checked as record_check does
+ * (src/model.c:3645-3692) and copied into the layer's HBM slab. */
+int waste_hip_moe_set_expert(waste_hip_moe *m, int expert,
+                             const void *record, size_t rec_bytes);
+/* The same for a record already in device memory (an expert-cache slot):
+ * the header is checked, the bytes are not copied. NULL unbinds. */
+int waste_hip_moe_bind_expert(waste_hip_moe *m, int expert,
+                              const void *dev_record, size_t rec_bytes);
+
+/* One forward over T tokens of device activations.
+ *   x       [T][H], fp32 (x_bf16 = 0) or bf16 (x_bf16 = 1), device
+ *   y       [T][H] fp32, device: routed sum + shared expert
+ *   ids, w  [T][K] selection (device, may be NULL)
+ *   logits  [T][E] router logits (device, may be NULL)
+ * T == 1 follows moe_layer (combine in selection order); T > 1 follows
+ * moe_chunk (ascending expert order, zero weights skipped).  Enqueued on
+ * `stream` (a hipStream_t; NULL = the null stream).  Device-side failures
+ * (an unbound expert, a routing pass with no candidate) are sticky: read
+ * them with waste_hip_moe_status. */
+int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T,
+                          float *y, int32_t *ids, float *w, float *logits,
+                          void *stream);
+
+/* Waits for the layer's work and returns the sticky device error (0, or
+ * WASTE_HIP_EUNBOUND / WASTE_HIP_EROUTE), clearing it. */
+int waste_hip_moe_status(waste_hip_moe *m, void *stream);
+
+/* Bytes the layer reads from HBM for one forward that touches `n_distinct`
+ * experts (index + scales, router, shared expert, codebooks, activations)
+ * — the algorithmic traffic a roofline divides by. */
+size_t waste_hip_moe_bytes(const waste_hip_moe *m, int T, int n_distinct);
+
+/* Materialises one bound expert matrix (kind 0 gate, 1 up, 2 down) as
+ * fp32 [M][N] in device memory W: the format's closed form, bit-exact. */
+int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W,
+                          void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WASTE_HIP_H */

@@ -675,3 +675,87 @@ int orc_moe_chunk(const orc_moe *m, const float *x, int T, float *out,
     free(lut_gu); free(lut_d); free(ga); free(ub); free(acc); free(logit); free(route); free(rw);
     return rcode;
 }
+
+/* The expert part of the layer with the routing given: moe_layer's serial
+ * loop (chunk == 0: one token, selection order, decode shared expert
+ * through matvec_t) or moe_chunk's (chunk == 1: ascending expert order,
+ * zero weights skipped, shared expert through waste_matmul_t).  Lets a
+ * device result be compared on the device's own routing, which is checked
+ * bit for bit separately. */
+int orc_moe_apply(const orc_moe *m, const float *x, int T, const int *idx,
+                  const float *w, int chunk, float *out)
+{
+    const int K = m->top_k, H = m->hidden, I = m->moe_inter;
+    const int st = m->stages, en = m->entries, vd = m->vec_dim, E = m->n_experts;
+    const size_t lut_sz = (size_t)((H > I ? H : I) / vd) * st * en;
+    float *lut_g = (float *)malloc(lut_sz * sizeof(float));
+    float *lut_u = (float *)malloc(lut_sz * sizeof(float));
+    float *lut_d = (float *)malloc(lut_sz * sizeof(float));
+    float *ga = (float *)malloc((size_t)I * sizeof(float));
+    float *ub = (float *)malloc((size_t)I * sizeof(float));
+    float *acc = (float *)malloc((size_t)H * sizeof(float));
+    int rc = 0;
+    memset(out, 0, (size_t)T * H * sizeof(float));
+    for (int t = 0; t < T; t++) {
+        const float *xt = x + (size_t)t * H;
+        int order[64];
+        for (int j = 0; j < K; j++) order[j] = j;
+        if (chunk)       /* ascending expert id */
+            for (int a = 1; a < K; a++)
+                for (int b = a; b > 0 && idx[t * K + order[b]] < idx[t * K + order[b - 1]]; b--) {
+                    const int tmp = order[b]; order[b] = order[b - 1]; order[b - 1] = tmp;
+                }
+        int lut_ready = 0;
+        for (int jj = 0; jj < K; jj++) {
+            const int j = order[jj], e = idx[t * K + j];
+            const float wj = w[t * K + j];
+            if (chunk && wj == 0.0f) continue;
+            if (e < 0 || e >= E || !m->recs[e]) { rc = -2; continue; }
+            const uint8_t *rec = m->recs[e];
+            const rec_view h = view(rec);
+            const uint16_t *sc = (const uint16_t *)(rec + h.co);
+            if (!lut_ready) {
+                orc_lutb(lut_g, m->booksT, xt, h.cbid, st, en, vd, 0, H / vd, m->order);
+                orc_lutb(lut_u, m->booksT, xt, h.cbid + st, st, en, vd, 0, H / vd, m->order);
+                lut_ready = 1;
+            }
+            orc_vq_rows(ga, rec + h.go, sc, lut_g, 0, I, H / vd, st, en);
+            orc_vq_rows(ub, rec + h.uo, sc + I, lut_u, 0, I, H / vd, st, en);
+            orc_act_pair(ga, ub, I);
+            orc_lutb(lut_d, m->booksT, ga, h.cbid + 2 * st, st, en, vd, 0, I / vd, m->order);
+            orc_vq_rows(acc, rec + h.dof, sc + 2 * I, lut_d, 0, H, I / vd, st, en);
+            float *dst = out + (size_t)t * H;
+            for (int i = 0; i < H; i++) dst[i] += wj * acc[i];
+        }
+    }
+    const int SI = I * (m->n_shared ? m->n_shared : 1);
+    float *a = (float *)calloc((size_t)T * SI, sizeof(float));
+    float *b = (float *)calloc((size_t)T * SI, sizeof(float));
+    float *sh = (float *)calloc((size_t)T * H, sizeof(float));
+    if (chunk) {
+        tensor_mm(&m->sh_gate, x, a, T);
+        tensor_mm(&m->sh_up, x, b, T);
+        orc_act_pair(a, b, T * SI);
+        tensor_mm(&m->sh_down, a, sh, T);
+    } else {
+        for (int t = 0; t < T; t++) {
+            tensor_mv(&m->sh_gate, x + (size_t)t * H, a + (size_t)t * SI, m->order);
+            tensor_mv(&m->sh_up, x + (size_t)t * H, b + (size_t)t * SI, m->order);
+            orc_act_pair(a + (size_t)t * SI, b + (size_t)t * SI, SI);
+            tensor_mv(&m->sh_down, a + (size_t)t * SI, sh + (size_t)t * H, m->order);
+        }
+    }
+    for (size_t i = 0; i < (size_t)T * H; i++) out[i] += sh[i];
+    free(a); free(b); free(sh);
+    free(lut_g); free(lut_u); free(lut_d); free(ga); free(ub); free(acc);
+    return rc;
+}
+
+/* Router logits for T tokens (matvec_t per token). */
+void orc_router_logits(const orc_moe *m, const float *x, int T, float *logits)
+{
+    for (int t = 0; t < T; t++) {
+        memset(logits + (size_t)t * m->n_experts, 0, (size_t)m->n_experts * sizeof(float));
+        tensor_mv(&m->router, x + (size_t)t * m->hidden, logits + (size_t)t * m->n_experts, m->order);
+    }
+}

@@ -120,6 +120,13 @@ int orc_moe_layer(const orc_moe *m, const float *x, float *out, int *idx,
 int orc_moe_chunk(const orc_moe *m, const float *x, int T, float *out,
                   int *idx, float *w);
 
+/* The experts and shared expert with the routing given (idx/w [T][K]);
+ * chunk selects moe_chunk's order and shared-expert path.  0, or -2 when a
+ * routed record is missing. */
+int orc_moe_apply(const orc_moe *m, const float *x, int T, const int *idx,
+                  const float *w, int chunk, float *out);
+void orc_router_logits(const orc_moe *m, const float *x, int T, float *logits);
+
 /* Threaded CPU baseline of orc_moe_layer (same bits): nthreads row-split
  * workers, as the reference's pool does.  Returns as orc_moe_layer. */
 int orc_moe_layer_mt(const orc_moe *m, const float *x, float *out, int *idx,

@@ -81,6 +81,8 @@ class Oracle:
         _sig(L, "orc_moe_chunk", C.c_int, [C.POINTER(OrcMoe), fp, C.c_int, fp, i32p, fp])
         _sig(L, "orc_moe_layer_mt", C.c_int, [C.POINTER(OrcMoe), fp, fp, i32p, fp, C.c_int])
         _sig(L, "orc_cpu_isa", C.c_int, [])
+        _sig(L, "orc_moe_apply", C.c_int, [C.POINTER(OrcMoe), fp, C.c_int, i32p, fp, C.c_int, fp])
+        _sig(L, "orc_router_logits", None, [C.POINTER(OrcMoe), fp, C.c_int, fp])
 
     def expf(self, x):
         return self.lib.orc_expf(float(x))
@@ -190,6 +192,23 @@ class _OrcLayer:
         rc = self.orc.lib.orc_moe_layer_mt(C.byref(self.m), ptr(np.ascontiguousarray(x, np.float32), fp),
                                            ptr(out, fp), ptr(idx, i32p), ptr(w, fp), nthreads)
         return rc, out, idx, w
+
+    def apply(self, X, idx, w, chunk):
+        L = self.L
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, L.H)
+        T = X.shape[0]
+        out = np.zeros((T, L.H), np.float32)
+        rc = self.orc.lib.orc_moe_apply(C.byref(self.m), ptr(X, fp), T,
+                                        ptr(np.ascontiguousarray(idx, np.int32), i32p),
+                                        ptr(np.ascontiguousarray(w, np.float32), fp), int(chunk), ptr(out, fp))
+        return rc, out
+
+    def logits(self, X):
+        L = self.L
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, L.H)
+        out = np.zeros((X.shape[0], L.E), np.float32)
+        self.orc.lib.orc_router_logits(C.byref(self.m), ptr(X, fp), X.shape[0], ptr(out, fp))
+        return out
 
     def chunk(self, X):
         L = self.L

@@ -1,0 +1,171 @@
+# SPDX-License-Identifier: Apache-2.0
+"""warp_amd — the MI355X (gfx950) backend for WARP's MoE expert path.
+
+The product is the C-ABI library libwaste_hip.so (include/waste_hip.h).
+This module is its Python mirror: ctypes bindings plus MoeLayer, a thin
+owner of one waste_hip_moe handle, used by the tests and bench.py.  Device
+buffers are passed as integer addresses (e.g. torch tensors' data_ptr()).
+
+There is no fallback: without the built library, or without a gfx950
+device, everything here raises.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwaste_hip.so")
+
+WQ_F32, WQ_Q8G, WQ_Q4G, WQ_VQ3R = 0, 2, 3, 4
+SCORE_SIGMOID, SCORE_SOFTMAX, SCORE_SQRTSOFTPLUS = 0, 1, 2
+
+ERRORS = {0: "ok", -1: "EINVAL", -2: "ENODEV", -3: "ENOMEM", -4: "ERECORD", -5: "ECRC",
+          -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE"}
+
+# Every symbol include/waste_hip.h declares.
+EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_host_buffers",
+           "waste_hip_vq3r", "waste_hip_moe_create", "waste_hip_moe_destroy",
+           "waste_hip_moe_set_router", "waste_hip_moe_set_shared", "waste_hip_moe_set_codebooks",
+           "waste_hip_moe_set_expert", "waste_hip_moe_bind_expert", "waste_hip_moe_forward",
+           "waste_hip_moe_status", "waste_hip_moe_bytes", "waste_hip_moe_dequant"]
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class MoeCfg(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("n_experts", C.c_int), ("top_k", C.c_int),
+                ("moe_inter", C.c_int), ("n_shared", C.c_int), ("score_func", C.c_int),
+                ("renorm", C.c_int), ("routed_scale", C.c_float), ("n_group", C.c_int),
+                ("topk_group", C.c_int), ("layer", C.c_int), ("max_tokens", C.c_int),
+                ("verify_records", C.c_int)]
+
+
+class HipTensor(C.Structure):
+    _fields_ = [("fmt", C.c_int), ("rows", C.c_int), ("cols", C.c_int), ("group", C.c_int),
+                ("q", C.c_void_p), ("qs", C.c_void_p), ("rowbytes", C.c_size_t)]
+
+
+class VqJob(C.Structure):
+    """waste_vq_job (src/waste_metal.h:31-40)."""
+    _fields_ = [("y", C.c_void_p), ("rec", C.c_void_p), ("rec_bytes", C.c_size_t),
+                ("idx_off", C.c_uint32), ("sc_off", C.c_uint32), ("lut", C.c_void_p),
+                ("lut_bytes", C.c_size_t), ("lut_off", C.c_uint32), ("m", C.c_int),
+                ("nv", C.c_int), ("stages", C.c_int), ("entries", C.c_int)]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded C-ABI library; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise HipError(f"{LIB_PATH} is missing: build it with `python -m warp_amd.build`")
+    L = C.CDLL(LIB_PATH)
+    vp, i = C.c_void_p, C.c_int
+    sig = {
+        "waste_hip_device_name": (C.c_char_p, []),
+        "waste_register_hip": (C.c_char_p, [vp]),
+        "waste_hip_release_host_buffers": (None, []),
+        "waste_hip_vq3r": (i, [vp, i]),
+        "waste_hip_moe_create": (i, [C.POINTER(MoeCfg), C.POINTER(vp)]),
+        "waste_hip_moe_destroy": (None, [vp]),
+        "waste_hip_moe_set_router": (i, [vp, C.POINTER(HipTensor), vp]),
+        "waste_hip_moe_set_shared": (i, [vp, C.POINTER(HipTensor), C.POINTER(HipTensor), C.POINTER(HipTensor)]),
+        "waste_hip_moe_set_codebooks": (i, [vp, vp, i]),
+        "waste_hip_moe_set_expert": (i, [vp, i, vp, C.c_size_t]),
+        "waste_hip_moe_bind_expert": (i, [vp, i, vp, C.c_size_t]),
+        "waste_hip_moe_forward": (i, [vp, vp, i, i, vp, vp, vp, vp, vp]),
+        "waste_hip_moe_status": (i, [vp, vp]),
+        "waste_hip_moe_bytes": (C.c_size_t, [vp, i, i]),
+        "waste_hip_moe_dequant": (i, [vp, i, i, vp, vp]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype, f.argtypes = res, args
+    _lib = L
+    return L
+
+
+def check(rc, what):
+    if rc != 0:
+        raise HipError(f"{what}: {ERRORS.get(rc, rc)}")
+
+
+def device_name():
+    n = lib().waste_hip_device_name()
+    return n.decode() if n else None
+
+
+def _tensor(t):
+    """A HipTensor from an object with fmt/rows/cols/group/q/qs/rowbytes
+    (numpy payloads); the caller keeps the arrays alive."""
+    return HipTensor(t.fmt, t.rows, t.cols, t.group, t.q.ctypes.data,
+                     t.qs.ctypes.data if t.qs is not None else None, t.rowbytes)
+
+
+class MoeLayer:
+    """One device MoE layer (waste_hip_moe)."""
+
+    def __init__(self, *, hidden, n_experts, top_k, moe_inter, n_shared=0, score_func=0,
+                 renorm=0, routed_scale=1.0, n_group=1, topk_group=1, layer=0,
+                 max_tokens=1, verify_records=0):
+        self.L = lib()
+        self.cfg = MoeCfg(hidden, n_experts, top_k, moe_inter, n_shared, score_func, renorm,
+                          routed_scale, n_group, topk_group, layer, max_tokens, verify_records)
+        h = C.c_void_p()
+        check(self.L.waste_hip_moe_create(C.byref(self.cfg), C.byref(h)), "waste_hip_moe_create")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.L.waste_hip_moe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_router(self, t, bias=None):
+        ht = _tensor(t)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        check(self.L.waste_hip_moe_set_router(self.h, C.byref(ht), b.ctypes.data if b is not None else None),
+              "set_router")
+
+    def set_shared(self, g, u, d):
+        if g is None or g.rows == 0:
+            check(self.L.waste_hip_moe_set_shared(self.h, None, None, None), "set_shared")
+            return
+        a, b, c = _tensor(g), _tensor(u), _tensor(d)
+        check(self.L.waste_hip_moe_set_shared(self.h, C.byref(a), C.byref(b), C.byref(c)), "set_shared")
+
+    def set_codebooks(self, books_f16):
+        b = np.ascontiguousarray(books_f16, np.uint16)
+        check(self.L.waste_hip_moe_set_codebooks(self.h, b.ctypes.data, b.shape[0]), "set_codebooks")
+
+    def set_expert(self, e, record):
+        buf = np.frombuffer(record, np.uint8)
+        return self.L.waste_hip_moe_set_expert(self.h, e, buf.ctypes.data, buf.size)
+
+    def bind_expert(self, e, dev_ptr, nbytes):
+        return self.L.waste_hip_moe_bind_expert(self.h, e, dev_ptr, nbytes)
+
+    def forward(self, x_ptr, T, y_ptr, ids_ptr=None, w_ptr=None, logits_ptr=None, bf16=False,
+                stream=None):
+        check(self.L.waste_hip_moe_forward(self.h, x_ptr, int(bf16), T, y_ptr, ids_ptr, w_ptr,
+                                           logits_ptr, stream), "forward")
+
+    def status(self, stream=None):
+        return self.L.waste_hip_moe_status(self.h, stream)
+
+    def bytes(self, T, n_distinct):
+        return self.L.waste_hip_moe_bytes(self.h, T, n_distinct)
+
+    def dequant(self, e, kind, W_ptr, stream=None):
+        return self.L.waste_hip_moe_dequant(self.h, e, kind, W_ptr, stream)

@@ -1,0 +1,105 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * launch.h — the thin C-ABI between the C host code and the gfx950 kernels.
+ * Each whip_* call enqueues kernels on `s` and returns a hipError_t as int
+ * (0 on success).  Pointers are device pointers unless said otherwise.
+ */
+#ifndef WARP_HIP_LAUNCH_H
+#define WARP_HIP_LAUNCH_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* bf16 activations to fp32 (exact). */
+int whip_bf16_to_f32(const uint16_t *x, float *y, size_t n, hipStream_t s);
+
+/* y[t*y_ld + r] = W[r] . x[t*x_ld + 0..cols) for r < rows, t < T, for up to
+ * two matrices in one launch (W1 may be NULL).  fmt 0 F32, 2 Q8G, 3 Q4G. */
+typedef struct {
+    int fmt, rows, cols, group;
+    const void *q;
+    const uint16_t *qs;
+    size_t rowbytes;
+} whip_mat;
+int whip_gemv(const whip_mat *W0, const whip_mat *W1, const float *x, int x_ld,
+              int T, float *y0, float *y1, int y_ld, hipStream_t s);
+
+/* Routing, one wavefront per token: scores, group limit, top-k with the
+ * engine's tie rule, renormalisation, scaling.  When T == 1 it also lays
+ * out the pair list (selection order) that the expert kernels walk. */
+typedef struct {
+    int E, K, score_func, renorm;
+    float routed_scale;
+    int n_group, topk_group;
+} whip_route_cfg;
+int whip_route(const whip_route_cfg *c, const float *logits, const float *bias,
+               int T, int32_t *ids, float *w, int32_t *pair_tok,
+               int32_t *pair_exp, float *pair_w, int32_t *tok_pairs,
+               int *err, hipStream_t s);
+/* T > 1: pairs ordered by (expert, token) ascending; each token's pairs in
+ * ascending expert order (the chunk's combine order). */
+int whip_pairs(const int32_t *ids, const float *w, int T, int K, int E,
+               int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
+               int32_t *tok_pairs, hipStream_t s);
+
+/* One VQ3R apply stage over P (source row, expert) pairs:
+ *   part[((p*kinds + k)*nch + c)*M + r] = sum over chunk c's positions of
+ *       L_k[v][0][i0] + L_k[v][1][i1] + L_k[v][2][i2]
+ * with L_k built in LDS from src[pair_src[p]] and books cb + 3k. */
+typedef struct {
+    const uint8_t *const *recs;      /* [E] record bases, NULL if unbound   */
+    const int32_t *pair_exp;         /* [P]                                 */
+    const int32_t *pair_src;         /* [P] row of src; NULL = p            */
+    const float *src;
+    int src_ld;
+    const float *booksT;             /* [n_books][8][256] fp32              */
+    int cb;                          /* first book of kind 0                */
+    uint32_t idx_off[2];             /* byte offset of kind k's indices     */
+    int kinds, M, nv, P, rsplit;
+    float *part;
+    int *err;
+} whip_vq_args;
+int whip_vq_apply(const whip_vq_args *a, hipStream_t s);
+int whip_vq_chunks(int nv);          /* nch for a given nv                  */
+
+/* h[p*I + r] = silu(scale_g[r]*sum_c gpart) * (scale_u[r]*sum_c upart) for
+ * the routed pairs, and h_sh[t*SI + r] = silu(a)*b for the shared expert. */
+int whip_vq_act(const uint8_t *const *recs, const int32_t *pair_exp, int P,
+                const float *part, int nch, int I, uint32_t sc_off, float *h,
+                const float *sh_a, const float *sh_b, int T, int SI,
+                float *h_sh, hipStream_t s);
+
+/* y[t*H + i] = sum over token t's pairs (combine order) of
+ *   w * (scale_d[i] * sum_c part_d) + sh[t*H + i] (sh may be NULL). */
+int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
+                 const float *pair_w, const int32_t *tok_pairs, int T, int K,
+                 const float *part_d, int nch, int H, uint32_t sc_off_down,
+                 int skip_zero, const float *sh, float *y, hipStream_t s);
+
+/* Materialised dequantisation of one VQ3R matrix (fp32 [M][N]). */
+int whip_dequant(const uint8_t *idx, const uint16_t *scale, const float *books,
+                 int cb, int M, int N, float *W, hipStream_t s);
+
+/* The engine's LUT build, fma chain over the 8 dims per entry. */
+int whip_lutb(const float *booksT, const float *x, int cb, int stages,
+              int entries, int vec_dim, int nv, float *lut, hipStream_t s);
+
+/* One VQ3R apply per job, each row's sum in the engine's exact order. */
+typedef struct {
+    float *y;
+    const uint8_t *idx;
+    const uint16_t *scale;
+    const float *lut;
+    int m, nv;
+} whip_vq_job;
+int whip_vq3r_jobs(const whip_vq_job *jobs, int n, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,243 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * backend.c — the engine-facing registration and the VQ3R batch entry.
+ *
+ * waste_register_hip fills the waste_kernels slot a device backend is
+ * meant to fill (the trunk matvec, mvq_rows_f32), marks it on_device so
+ * the engine hands it whole row ranges (src/model.c:805-812), and sets
+ * device_min_bytes below which the engine keeps the CPU kernel.  It does
+ * not touch lutb_range: a host-in/host-out LUT build would spend more on
+ * moving the table than the build costs, so that slot stays on the CPU,
+ * as it does under the Metal backend (src/metal.m:503-516).
+ *
+ * Host weights are immutable trunk tensors, so the slot keeps an HBM copy
+ * of each one it has seen, keyed by host address and size; the engine
+ * drops them with waste_hip_release_host_buffers before freeing the
+ * tensors (the contract of src/waste_backend.h:129-131).  Activations and
+ * outputs cross PCIe per call.
+ *
+ * waste_hip_vq3r copies each job's record and table to HBM, runs every job
+ * in the engine's exact row order, and copies the rows back — only when
+ * all of it succeeded (all-or-nothing, src/waste_metal.h:42-44).  Records
+ * are not cached: an expert-cache slot is reused for other experts under
+ * the same address.
+ */
+#include "waste_hip.h"
+#include "../hip/launch.h"
+
+#include <hip/hip_runtime_api.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+static pthread_mutex_t g_mu = PTHREAD_MUTEX_INITIALIZER;
+
+#define MIRRORS 256
+static struct { const void *key; size_t bytes; void *dev; } g_mirror[MIRRORS];
+static int g_ready;              /* 1 registered, -1 declined              */
+static hipStream_t g_stream;
+static void *g_io;               /* staging: x in, y out                   */
+static size_t g_io_cap;
+static void *g_job;              /* staging for the vq3r batch             */
+static size_t g_job_cap;
+
+static void *mirror(const void *host, size_t bytes)
+{
+    int free_slot = -1;
+    for (int i = 0; i < MIRRORS; i++) {
+        if (g_mirror[i].key == host && g_mirror[i].bytes >= bytes) return g_mirror[i].dev;
+        if (g_mirror[i].key == host) {                /* grew: replace      */
+            hipFree(g_mirror[i].dev);
+            g_mirror[i].key = NULL;
+        }
+        if (!g_mirror[i].key && free_slot < 0) free_slot = i;
+    }
+    if (free_slot < 0) {                               /* evict the first    */
+        hipFree(g_mirror[0].dev);
+        g_mirror[0].key = NULL;
+        free_slot = 0;
+    }
+    void *d = NULL;
+    if (hipMalloc(&d, bytes) != hipSuccess) return NULL;
+    if (hipMemcpy(d, host, bytes, hipMemcpyHostToDevice) != hipSuccess) { hipFree(d); return NULL; }
+    g_mirror[free_slot].key = host;
+    g_mirror[free_slot].bytes = bytes;
+    g_mirror[free_slot].dev = d;
+    return d;
+}
+
+static void *staging(void **buf, size_t *cap, size_t bytes)
+{
+    if (*cap >= bytes) return *buf;
+    if (*buf) hipFree(*buf);
+    *buf = NULL;
+    *cap = 0;
+    if (hipMalloc(buf, bytes) != hipSuccess) return NULL;
+    *cap = bytes;
+    return *buf;
+}
+
+/* Q3G rows (3-bit codes at bit 3i, minus 4; waste_q3_at, src/simd.h:101-106)
+ * are decoded on the host into Q8G-shaped int8 rows once, then mirrored. */
+static void *mirror_q3(const mvq_arg *a, int rows, size_t *rowbytes_out)
+{
+    const size_t rb8 = (size_t)a->ng * a->group;
+    const size_t bytes = (size_t)rows * rb8;
+    for (int i = 0; i < MIRRORS; i++)
+        if (g_mirror[i].key == (const void *)((const uint8_t *)a->W + 1) && g_mirror[i].bytes >= bytes) {
+            *rowbytes_out = rb8;
+            return g_mirror[i].dev;
+        }
+    int8_t *tmp = (int8_t *)malloc(bytes);
+    if (!tmp) return NULL;
+    for (int r = 0; r < rows; r++) {
+        const uint8_t *p = (const uint8_t *)a->W + (size_t)r * a->rowbytes;
+        for (size_t i = 0; i < rb8; i++) {
+            const long off = (long)i * 3;
+            const int v = (p[off >> 3] >> (off & 7)) | (p[(off >> 3) + 1] << (8 - (off & 7)));
+            tmp[(size_t)r * rb8 + i] = (int8_t)((v & 7) - 4);
+        }
+    }
+    /* keyed one byte past the packed tensor so it cannot alias its mirror */
+    void *d = mirror((const uint8_t *)a->W + 1, bytes);
+    if (d) hipMemcpy(d, tmp, bytes, hipMemcpyHostToDevice);
+    free(tmp);
+    *rowbytes_out = rb8;
+    return d;
+}
+
+/* The mvq_rows_f32 slot: rows [b, e) of a quantized tensor against fp32
+ * activations (mvq_arg, src/simd.h:35-39; xs carries the activations). */
+static void mvq_rows_hip(int b, int e, void *p)
+{
+    mvq_arg *a = (mvq_arg *)p;
+    if (e <= b) return;
+    pthread_mutex_lock(&g_mu);
+    const int rows = e;          /* on_device: the engine passes [0, n)      */
+    const size_t sbytes = (size_t)rows * a->ng * 2;
+    whip_mat w;
+    w.rows = rows; w.cols = a->in; w.group = a->group;
+    w.fmt = a->bits == 4 ? WQ_Q4G : WQ_Q8G;
+    w.rowbytes = a->rowbytes;
+    if (a->bits == 3) w.q = mirror_q3(a, rows, &w.rowbytes);
+    else w.q = mirror(a->W, (size_t)rows * a->rowbytes);
+    w.qs = (const uint16_t *)mirror(a->ws, sbytes);
+    const size_t xb = ((size_t)a->in * 4 + 255) / 256 * 256;
+    uint8_t *io = (uint8_t *)staging(&g_io, &g_io_cap, xb + (size_t)rows * 4);
+    int ok = w.q && w.qs && io && (w.rowbytes % 16 == 0) && (a->group % 32 == 0);
+    if (ok) ok = hipMemcpyAsync(io, a->xs, (size_t)a->in * 4, hipMemcpyHostToDevice, g_stream) == hipSuccess;
+    if (ok) ok = whip_gemv(&w, NULL, (const float *)io, 0, 1, (float *)(io + xb), NULL, 0, g_stream) == 0;
+    if (ok) ok = hipMemcpyAsync(a->y + b, io + xb + (size_t)b * 4, (size_t)(e - b) * 4,
+                                hipMemcpyDeviceToHost, g_stream) == hipSuccess;
+    if (ok) ok = hipStreamSynchronize(g_stream) == hipSuccess;
+    pthread_mutex_unlock(&g_mu);
+    if (!ok) {
+        /* The slot has no error channel (src/waste_backend.h:69-107): a row
+         * range the device could not compute is NaN, never stale data. */
+        const float nan = __builtin_nanf("");
+        for (int r = b; r < e; r++) a->y[r] = nan;
+    }
+}
+
+const char *waste_register_hip(waste_kernels *t)
+{
+    pthread_mutex_lock(&g_mu);
+    if (!g_ready) {
+        if (!waste_hip_device_name() || hipStreamCreate(&g_stream) != hipSuccess) g_ready = -1;
+        else g_ready = 1;
+    }
+    const int ok = g_ready > 0;
+    pthread_mutex_unlock(&g_mu);
+    if (!ok) return NULL;
+    t->mvq_rows_f32 = mvq_rows_hip;
+    t->on_device = 1;
+    /* A synchronous dispatch with two PCIe copies costs tens of us; below
+     * a megabyte of weights the CPU pool finishes first. */
+    const char *env = getenv("WASTE_HIP_MIN_KB");
+    t->device_min_bytes = (size_t)(env ? atoi(env) : 1024) << 10;
+    return "HIP (gfx950)";
+}
+
+void waste_hip_release_host_buffers(void)
+{
+    pthread_mutex_lock(&g_mu);
+    for (int i = 0; i < MIRRORS; i++) {
+        if (g_mirror[i].key) hipFree(g_mirror[i].dev);
+        g_mirror[i].key = NULL;
+        g_mirror[i].dev = NULL;
+        g_mirror[i].bytes = 0;
+    }
+    pthread_mutex_unlock(&g_mu);
+}
+
+int waste_hip_vq3r(const waste_vq_job *jobs, int n)
+{
+    if (n <= 0 || !jobs) return -1;
+    for (int i = 0; i < n; i++)
+        if (jobs[i].stages != 3 || jobs[i].entries != 256 || jobs[i].m <= 0 || jobs[i].nv <= 0 ||
+            (size_t)jobs[i].idx_off + (size_t)((jobs[i].m + 63) / 64) * 64 * jobs[i].nv * 3 >= jobs[i].rec_bytes ||
+            (size_t)jobs[i].sc_off + (size_t)jobs[i].m * 2 > jobs[i].rec_bytes ||
+            ((size_t)jobs[i].lut_off + (size_t)jobs[i].nv * 768) * 4 > jobs[i].lut_bytes)
+            return -1;
+    pthread_mutex_lock(&g_mu);
+    if (g_ready == 0) {
+        if (!waste_hip_device_name() || hipStreamCreate(&g_stream) != hipSuccess) g_ready = -1;
+        else g_ready = 1;
+    }
+    if (g_ready < 0) { pthread_mutex_unlock(&g_mu); return -1; }
+    /* stage every distinct record and table once */
+    size_t total = 0, ytotal = 0;
+    size_t *roff = (size_t *)malloc(sizeof(size_t) * 2 * (size_t)n);
+    whip_vq_job *dj = (whip_vq_job *)malloc(sizeof(whip_vq_job) * (size_t)n);
+    int ok = roff && dj;
+    for (int i = 0; ok && i < n; i++) {
+        int seen = -1;
+        for (int k = 0; k < i; k++) if (jobs[k].rec == jobs[i].rec) { seen = k; break; }
+        if (seen >= 0) roff[2 * i] = roff[2 * seen];
+        else { roff[2 * i] = total; total += (jobs[i].rec_bytes + 255) / 256 * 256; }
+        seen = -1;
+        for (int k = 0; k < i; k++) if (jobs[k].lut == jobs[i].lut) { seen = k; break; }
+        if (seen >= 0) roff[2 * i + 1] = roff[2 * seen + 1];
+        else { roff[2 * i + 1] = total; total += (jobs[i].lut_bytes + 255) / 256 * 256; }
+        ytotal += (size_t)jobs[i].m;
+    }
+    uint8_t *d = ok ? (uint8_t *)staging(&g_job, &g_job_cap, total + ytotal * 4) : NULL;
+    ok = d != NULL;
+    for (int i = 0; ok && i < n; i++) {
+        int first_rec = 1, first_lut = 1;
+        for (int k = 0; k < i; k++) {
+            if (jobs[k].rec == jobs[i].rec) first_rec = 0;
+            if (jobs[k].lut == jobs[i].lut) first_lut = 0;
+        }
+        if (first_rec)
+            ok = hipMemcpyAsync(d + roff[2 * i], jobs[i].rec, jobs[i].rec_bytes,
+                                hipMemcpyHostToDevice, g_stream) == hipSuccess;
+        if (ok && first_lut)
+            ok = hipMemcpyAsync(d + roff[2 * i + 1], jobs[i].lut, jobs[i].lut_bytes,
+                                hipMemcpyHostToDevice, g_stream) == hipSuccess;
+    }
+    size_t yoff = total;
+    for (int i = 0; ok && i < n; i++) {
+        dj[i].y = (float *)(d + yoff);
+        dj[i].idx = d + roff[2 * i] + jobs[i].idx_off;
+        dj[i].scale = (const uint16_t *)(d + roff[2 * i] + jobs[i].sc_off);
+        dj[i].lut = (const float *)(d + roff[2 * i + 1]) + jobs[i].lut_off;
+        dj[i].m = jobs[i].m;
+        dj[i].nv = jobs[i].nv;
+        yoff += (size_t)jobs[i].m * 4;
+    }
+    if (ok) ok = whip_vq3r_jobs(dj, n, g_stream) == 0;
+    float *ybuf = ok ? (float *)malloc(ytotal * 4) : NULL;
+    if (ok) ok = ybuf && hipMemcpyAsync(ybuf, d + total, ytotal * 4, hipMemcpyDeviceToHost, g_stream) == hipSuccess;
+    if (ok) ok = hipStreamSynchronize(g_stream) == hipSuccess;
+    if (ok) {
+        const float *src = ybuf;
+        for (int i = 0; i < n; i++) {
+            memcpy(jobs[i].y, src, (size_t)jobs[i].m * 4);
+            src += jobs[i].m;
+        }
+    }
+    free(ybuf); free(roff); free(dj);
+    pthread_mutex_unlock(&g_mu);
+    return ok ? 0 : -1;
+}

@@ -1,0 +1,435 @@
+/* SPDX-License-Identifier: Apache-2.0 */
+/*
+ * moe.c — the device MoE layer: host orchestration of the gfx950 kernels.
+ *
+ * One forward enqueues, on the caller's stream:
+ *   [bf16->fp32] -> router GEMV -> route (+ pair list) -> shared gate/up
+ *   GEMV -> VQ3R gate/up apply -> SwiGLU (routed + shared) -> VQ3R down
+ *   apply -> shared down GEMV -> combine.
+ * Everything it reads is resident in HBM: expert records in a slab owned
+ * by the layer (or bound from an expert-cache slot), codebooks as fp32,
+ * the router and shared expert in their stored formats.
+ *
+ * Host-side semantics follow the engine: records are checked as
+ * record_check does before the device ever reads them
+ * (src/model.c:3645-3692); the layer's gate/up tables use the codebook id
+ * of the records (src/model.c:5844-5849), which must agree across the
+ * layer's experts; an unbound or unroutable expert is reported through a
+ * sticky error, as the engine's read_error is (src/model.c:3698-3712).
+ */
+#include "waste_hip.h"
+#include "../hip/launch.h"
+
+#include <hip/hip_runtime_api.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define CK(call) do { if ((call) != hipSuccess) return WASTE_HIP_EDEVICE; } while (0)
+
+struct waste_hip_moe {
+    waste_hip_moe_cfg c;
+    int E, K, H, I, SI, T;
+    int nv_gu, nv_d, nch_gu, nch_d, rsplit_gu, rsplit_d;
+    size_t idx_gu, idx_d, rec_min, rec_bytes;
+    uint32_t off_gate, off_up, off_down, off_sc;
+    int cb;                      /* codebook id shared by the layer (-1)   */
+    int bound;                   /* records bound                          */
+    /* device */
+    const uint8_t **d_recs;      /* [E + 1]; entry E stays NULL            */
+    const uint8_t **h_recs;
+    uint8_t *slab;               /* owned records, E x rec_bytes (lazy)    */
+    float *d_books, *d_booksT;
+    int n_books;
+    whip_mat router, sh[3];
+    void *router_mem, *sh_mem[3];
+    float *d_bias;
+    int has_router, has_shared;
+    float *xf, *logits, *w, *pair_w, *part_gu, *h, *part_d, *sh_a, *sh_b, *h_sh, *sh_out;
+    int32_t *ids, *pair_tok, *pair_exp, *tok_pairs;
+    int *err;
+};
+
+static float f16_book(uint16_t h)
+{
+    const uint32_t sign = (uint32_t)(h >> 15) << 31;
+    const uint32_t e = (h >> 10) & 0x1f, mn = h & 0x3ff;
+    const uint32_t b = e ? (sign | ((e + 112u) << 23) | (mn << 13)) : sign;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+static uint32_t crc32_z(const uint8_t *p, size_t n)
+{
+    static uint32_t tab[256];
+    static int ready = 0;
+    if (!ready) {
+        for (uint32_t i = 0; i < 256; i++) {
+            uint32_t c = i;
+            for (int k = 0; k < 8; k++) c = (c & 1) ? 0xEDB88320u ^ (c >> 1) : c >> 1;
+            tab[i] = c;
+        }
+        ready = 1;
+    }
+    uint32_t c = 0xFFFFFFFFu;
+    for (size_t i = 0; i < n; i++) c = tab[(c ^ p[i]) & 0xff] ^ (c >> 8);
+    return c ^ 0xFFFFFFFFu;
+}
+
+static int dmalloc(void **p, size_t n)
+{
+    *p = NULL;
+    if (n == 0) return 0;
+    return hipMalloc(p, n) == hipSuccess ? 0 : WASTE_HIP_ENOMEM;
+}
+
+const char *waste_hip_device_name(void)
+{
+    static char name[300];
+    int n = 0, dev = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return NULL;
+    if (hipGetDevice(&dev) != hipSuccess) return NULL;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return NULL;
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) return NULL;
+    snprintf(name, sizeof name, "HIP %s", p.gcnArchName);
+    return name;
+}
+
+void waste_hip_moe_destroy(waste_hip_moe *m)
+{
+    if (!m) return;
+    void *bufs[] = { m->d_recs, m->slab, m->d_books, m->d_booksT, m->router_mem,
+                     m->sh_mem[0], m->sh_mem[1], m->sh_mem[2], m->d_bias, m->xf,
+                     m->logits, m->w, m->pair_w, m->part_gu, m->h, m->part_d, m->sh_a,
+                     m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
+                     m->tok_pairs, m->err };
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
+    free(m->h_recs);
+    free(m);
+}
+
+static int pick_rsplit(int work_groups, int row_blocks)
+{
+    /* enough workgroups to cover 256 CUs a few times, at least one row
+     * block per wavefront of a 4-wave workgroup */
+    int r = (1024 + work_groups - 1) / (work_groups > 0 ? work_groups : 1);
+    const int cap = row_blocks / 4 > 0 ? row_blocks / 4 : 1;
+    if (r > cap) r = cap;
+    return r < 1 ? 1 : r;
+}
+
+int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
+{
+    *out = NULL;
+    if (!cfg || cfg->hidden <= 0 || cfg->hidden % 64 || cfg->moe_inter <= 0 ||
+        cfg->moe_inter % 64 || cfg->n_experts <= 0 || cfg->n_experts > 1024 ||
+        cfg->top_k <= 0 || cfg->top_k > 64 || cfg->top_k > cfg->n_experts ||
+        cfg->max_tokens <= 0 || cfg->score_func < 0 || cfg->score_func > 2)
+        return WASTE_HIP_EINVAL;
+    if (cfg->n_group > 1 && (cfg->n_experts % cfg->n_group || cfg->n_group > 64 ||
+                             cfg->topk_group < 1 || cfg->topk_group > cfg->n_group ||
+                             cfg->topk_group * (cfg->n_experts / cfg->n_group) < cfg->top_k))
+        return WASTE_HIP_EINVAL;
+    if (!waste_hip_device_name()) return WASTE_HIP_ENODEV;
+    waste_hip_moe *m = (waste_hip_moe *)calloc(1, sizeof *m);
+    if (!m) return WASTE_HIP_ENOMEM;
+    m->c = *cfg;
+    m->E = cfg->n_experts; m->K = cfg->top_k; m->H = cfg->hidden; m->I = cfg->moe_inter;
+    m->SI = cfg->moe_inter * (cfg->n_shared > 0 ? cfg->n_shared : 1);
+    m->T = cfg->max_tokens;
+    m->nv_gu = m->H / 8; m->nv_d = m->I / 8;
+    m->nch_gu = whip_vq_chunks(m->nv_gu);
+    m->nch_d = whip_vq_chunks(m->nv_d);
+    /* canonical record layout (tools/convert.py:942-977): 48 B header,
+     * gate, up, down index streams, then f16 scales gate|up|down */
+    m->idx_gu = (size_t)m->I * m->nv_gu * 3;
+    m->idx_d = (size_t)m->H * m->nv_d * 3;
+    m->off_gate = 48;
+    m->off_up = (uint32_t)(48 + m->idx_gu);
+    m->off_down = (uint32_t)(48 + 2 * m->idx_gu);
+    m->off_sc = (uint32_t)(48 + 2 * m->idx_gu + m->idx_d);
+    m->rec_min = m->off_sc + 2 * (size_t)(2 * m->I + m->H);
+    m->rec_bytes = (m->rec_min + 4095) / 4096 * 4096;
+    m->cb = -1;
+    const int P = m->T * m->K;
+    m->rsplit_gu = pick_rsplit(m->nch_gu * 2 * m->K, m->I / 64);
+    m->rsplit_d = pick_rsplit(m->nch_d * m->K, m->H / 64);
+    m->h_recs = (const uint8_t **)calloc((size_t)m->E + 1, sizeof(void *));
+    int rc = 0;
+    rc |= dmalloc((void **)&m->d_recs, ((size_t)m->E + 1) * sizeof(void *));
+    rc |= dmalloc((void **)&m->xf, (size_t)m->T * m->H * 4);
+    rc |= dmalloc((void **)&m->logits, (size_t)m->T * m->E * 4);
+    rc |= dmalloc((void **)&m->ids, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->w, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->pair_tok, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->pair_exp, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->pair_w, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->tok_pairs, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->part_gu, (size_t)P * 2 * m->nch_gu * m->I * 4);
+    rc |= dmalloc((void **)&m->h, (size_t)P * m->I * 4);
+    rc |= dmalloc((void **)&m->part_d, (size_t)P * m->nch_d * m->H * 4);
+    rc |= dmalloc((void **)&m->err, 64);
+    if (rc || !m->h_recs) { waste_hip_moe_destroy(m); return WASTE_HIP_ENOMEM; }
+    if (hipMemset(m->d_recs, 0, ((size_t)m->E + 1) * sizeof(void *)) != hipSuccess ||
+        hipMemset(m->err, 0, 64) != hipSuccess) {
+        waste_hip_moe_destroy(m);
+        return WASTE_HIP_EDEVICE;
+    }
+    *out = m;
+    return 0;
+}
+
+/* Uploads a trunk tensor: payload (+ scales) in one allocation. */
+static int upload_tensor(const waste_hip_tensor *t, int rows, int cols, whip_mat *dst, void **mem)
+{
+    if (!t || !t->q || t->rows != rows || t->cols != cols) return WASTE_HIP_EINVAL;
+    if (t->fmt != WQ_F32 && t->fmt != WQ_Q8G && t->fmt != WQ_Q4G) return WASTE_HIP_EINVAL;
+    size_t qbytes = (size_t)rows * t->rowbytes, sbytes = 0;
+    if (t->fmt == WQ_F32) {
+        if (t->rowbytes < (size_t)cols * 4 || cols % 4 || t->rowbytes % 16) return WASTE_HIP_EINVAL;
+    } else {
+        if (t->group <= 0 || t->group % 32 || t->rowbytes % 16 || !t->qs) return WASTE_HIP_EINVAL;
+        const int ng = (cols + t->group - 1) / t->group;
+        const size_t need = t->fmt == WQ_Q8G ? (size_t)ng * t->group : (size_t)ng * t->group / 2;
+        if (t->rowbytes < need) return WASTE_HIP_EINVAL;
+        sbytes = (size_t)rows * ng * 2;
+    }
+    if (*mem) { hipFree(*mem); *mem = NULL; }
+    const size_t qpad = (qbytes + 255) / 256 * 256;
+    if (dmalloc(mem, qpad + sbytes)) return WASTE_HIP_ENOMEM;
+    CK(hipMemcpy(*mem, t->q, qbytes, hipMemcpyHostToDevice));
+    if (sbytes) CK(hipMemcpy((uint8_t *)*mem + qpad, t->qs, sbytes, hipMemcpyHostToDevice));
+    dst->fmt = t->fmt; dst->rows = rows; dst->cols = cols; dst->group = t->group;
+    dst->q = *mem;
+    dst->qs = sbytes ? (const uint16_t *)((uint8_t *)*mem + qpad) : NULL;
+    dst->rowbytes = t->rowbytes;
+    return 0;
+}
+
+int waste_hip_moe_set_router(waste_hip_moe *m, const waste_hip_tensor *gate, const float *bias)
+{
+    if (!m) return WASTE_HIP_EINVAL;
+    int rc = upload_tensor(gate, m->E, m->H, &m->router, &m->router_mem);
+    if (rc) return rc;
+    if (m->d_bias) { hipFree(m->d_bias); m->d_bias = NULL; }
+    if (bias) {
+        if (dmalloc((void **)&m->d_bias, (size_t)m->E * 4)) return WASTE_HIP_ENOMEM;
+        CK(hipMemcpy(m->d_bias, bias, (size_t)m->E * 4, hipMemcpyHostToDevice));
+    }
+    m->has_router = 1;
+    return 0;
+}
+
+int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
+                             const waste_hip_tensor *up, const waste_hip_tensor *down)
+{
+    if (!m) return WASTE_HIP_EINVAL;
+    if (!gate && !up && !down) { m->has_shared = 0; return 0; }
+    int rc = upload_tensor(gate, m->SI, m->H, &m->sh[0], &m->sh_mem[0]);
+    if (!rc) rc = upload_tensor(up, m->SI, m->H, &m->sh[1], &m->sh_mem[1]);
+    if (!rc) rc = upload_tensor(down, m->H, m->SI, &m->sh[2], &m->sh_mem[2]);
+    if (rc) return rc;
+    if (gate->fmt != up->fmt || gate->group != up->group) return WASTE_HIP_EINVAL;
+    if (!m->sh_a) {
+        rc |= dmalloc((void **)&m->sh_a, (size_t)m->T * m->SI * 4);
+        rc |= dmalloc((void **)&m->sh_b, (size_t)m->T * m->SI * 4);
+        rc |= dmalloc((void **)&m->h_sh, (size_t)m->T * m->SI * 4);
+        rc |= dmalloc((void **)&m->sh_out, (size_t)m->T * m->H * 4);
+        if (rc) return WASTE_HIP_ENOMEM;
+    }
+    m->has_shared = 1;
+    return 0;
+}
+
+int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16, int n_books)
+{
+    if (!m || !f16 || n_books < 9) return WASTE_HIP_EINVAL;
+    const size_t per = 256 * 8;
+    float *b = (float *)malloc((size_t)n_books * per * 4);
+    float *bt = (float *)malloc((size_t)n_books * per * 4);
+    if (!b || !bt) { free(b); free(bt); return WASTE_HIP_ENOMEM; }
+    for (size_t i = 0; i < (size_t)n_books * per; i++) b[i] = f16_book(f16[i]);
+    for (int k = 0; k < n_books; k++)
+        for (int c = 0; c < 256; c++)
+            for (int d = 0; d < 8; d++)
+                bt[(size_t)k * per + (size_t)d * 256 + c] = b[(size_t)k * per + (size_t)c * 8 + d];
+    int rc = 0;
+    if (m->d_books) { hipFree(m->d_books); hipFree(m->d_booksT); m->d_books = m->d_booksT = NULL; }
+    rc |= dmalloc((void **)&m->d_books, (size_t)n_books * per * 4);
+    rc |= dmalloc((void **)&m->d_booksT, (size_t)n_books * per * 4);
+    if (!rc && (hipMemcpy(m->d_books, b, (size_t)n_books * per * 4, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(m->d_booksT, bt, (size_t)n_books * per * 4, hipMemcpyHostToDevice) != hipSuccess))
+        rc = WASTE_HIP_EDEVICE;
+    free(b); free(bt);
+    if (rc) return rc;
+    m->n_books = n_books;
+    return 0;
+}
+
+/* record_check (src/model.c:3645-3692) plus this layer's canonical
+ * offsets.  Returns 0, WASTE_HIP_ERECORD or WASTE_HIP_ECRC. */
+static int check_record(const waste_hip_moe *m, int expert, const uint8_t *rec, size_t rec_bytes,
+                        int verify)
+{
+    waste_expert_hdr h;
+    if (rec_bytes < sizeof h) return WASTE_HIP_ERECORD;
+    memcpy(&h, rec, sizeof h);
+    if (h.magic != WASTE_MAGIC_EXPERT) return WASTE_HIP_ERECORD;
+    if (h.layer != (uint16_t)m->c.layer || h.expert_id != (uint16_t)expert) return WASTE_HIP_ERECORD;
+    if ((size_t)h.rec_4k_blocks * WASTE_ALIGN != rec_bytes) return WASTE_HIP_ERECORD;
+    if (h.fmt != WQ_VQ3R || h.lowrank_id != 0) return WASTE_HIP_ERECORD;
+    if (m->n_books && (long)h.codebook_id + 9L > m->n_books) return WASTE_HIP_ERECORD;
+    if (!(h.gate_off == 48 && h.gate_off < h.up_off && h.up_off < h.down_off &&
+          h.down_off < h.chan_corr_off && h.chan_corr_off <= rec_bytes))
+        return WASTE_HIP_ERECORD;
+    const size_t scales = 2u * (size_t)(2 * m->I + m->H);
+    if (scales > rec_bytes - h.chan_corr_off) return WASTE_HIP_ERECORD;
+    /* the kernels read the canonical layout */
+    if (h.up_off != m->off_up || h.down_off != m->off_down || h.chan_corr_off != m->off_sc)
+        return WASTE_HIP_ERECORD;
+    if (m->cb >= 0 && h.codebook_id != m->cb) return WASTE_HIP_ERECORD;
+    if (verify) {
+        const size_t payload = (size_t)h.chan_corr_off + scales - sizeof h;
+        if (crc32_z(rec + sizeof h, payload) != h.crc32) return WASTE_HIP_ECRC;
+    }
+    return 0;
+}
+
+static int set_ptr(waste_hip_moe *m, int expert, const uint8_t *dev)
+{
+    if (m->h_recs[expert] && !dev) m->bound--;
+    if (!m->h_recs[expert] && dev) m->bound++;
+    m->h_recs[expert] = dev;
+    CK(hipMemcpy(m->d_recs + expert, &m->h_recs[expert], sizeof(void *), hipMemcpyHostToDevice));
+    return 0;
+}
+
+int waste_hip_moe_set_expert(waste_hip_moe *m, int expert, const void *record, size_t rec_bytes)
+{
+    if (!m || !record || expert < 0 || expert >= m->E) return WASTE_HIP_EINVAL;
+    if (rec_bytes != m->rec_bytes) return WASTE_HIP_ERECORD;
+    const int rc = check_record(m, expert, (const uint8_t *)record, rec_bytes, m->c.verify_records);
+    if (rc) return rc;
+    if (!m->slab && dmalloc((void **)&m->slab, (size_t)m->E * m->rec_bytes)) return WASTE_HIP_ENOMEM;
+    uint8_t *dst = m->slab + (size_t)expert * m->rec_bytes;
+    CK(hipMemcpy(dst, record, rec_bytes, hipMemcpyHostToDevice));
+    uint16_t cbid;
+    memcpy(&cbid, (const uint8_t *)record + 10, 2);
+    m->cb = cbid;
+    return set_ptr(m, expert, dst);
+}
+
+int waste_hip_moe_bind_expert(waste_hip_moe *m, int expert, const void *dev_record, size_t rec_bytes)
+{
+    if (!m || expert < 0 || expert >= m->E) return WASTE_HIP_EINVAL;
+    if (!dev_record) return set_ptr(m, expert, NULL);
+    if (rec_bytes != m->rec_bytes) return WASTE_HIP_ERECORD;
+    uint8_t hdr[48];
+    CK(hipMemcpy(hdr, dev_record, 48, hipMemcpyDeviceToHost));
+    /* header only: the payload checksum needs the bytes on the host */
+    const int rc = check_record(m, expert, hdr, rec_bytes, 0);
+    if (rc) return rc;
+    uint16_t cbid;
+    memcpy(&cbid, hdr + 10, 2);
+    m->cb = cbid;
+    return set_ptr(m, expert, (const uint8_t *)dev_record);
+}
+
+int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
+                          int32_t *ids, float *w, float *logits, void *stream)
+{
+    if (!m || !x || !y || T <= 0 || T > m->T) return WASTE_HIP_EINVAL;
+    if (!m->has_router || !m->d_booksT || m->cb < 0 || m->cb + 9 > m->n_books)
+        return WASTE_HIP_EINVAL;
+    hipStream_t s = (hipStream_t)stream;
+    const int E = m->E, K = m->K, H = m->H, I = m->I, P = T * K;
+    const float *xf = (const float *)x;
+    if (x_bf16) {
+        CK((hipError_t)whip_bf16_to_f32((const uint16_t *)x, m->xf, (size_t)T * H, s));
+        xf = m->xf;
+    }
+    float *lg = logits ? logits : m->logits;
+    CK((hipError_t)whip_gemv(&m->router, NULL, xf, H, T, lg, NULL, E, s));
+    whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
+                          m->c.n_group, m->c.topk_group };
+    int32_t *d_ids = ids ? ids : m->ids;
+    float *d_w = w ? w : m->w;
+    CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, m->pair_tok, m->pair_exp,
+                              m->pair_w, m->tok_pairs, m->err, s));
+    if (T > 1)
+        CK((hipError_t)whip_pairs(d_ids, d_w, T, K, E, m->pair_tok, m->pair_exp, m->pair_w,
+                                  m->tok_pairs, s));
+    if (m->has_shared)
+        CK((hipError_t)whip_gemv(&m->sh[0], &m->sh[1], xf, H, T, m->sh_a, m->sh_b, m->SI, s));
+
+    whip_vq_args a;
+    memset(&a, 0, sizeof a);
+    a.recs = m->d_recs; a.pair_exp = m->pair_exp; a.pair_src = m->pair_tok;
+    a.src = xf; a.src_ld = H; a.booksT = m->d_booksT; a.cb = m->cb;
+    a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
+    a.kinds = 2; a.M = I; a.nv = m->nv_gu; a.P = P; a.rsplit = m->rsplit_gu;
+    a.part = m->part_gu; a.err = m->err;
+    CK((hipError_t)whip_vq_apply(&a, s));
+    CK((hipError_t)whip_vq_act(m->d_recs, m->pair_exp, P, m->part_gu, m->nch_gu, I, m->off_sc,
+                               m->h, m->sh_a, m->sh_b, T, m->SI, m->has_shared ? m->h_sh : NULL, s));
+    a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.cb = m->cb + 6;
+    a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
+    a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
+    CK((hipError_t)whip_vq_apply(&a, s));
+    if (m->has_shared)
+        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
+    CK((hipError_t)whip_combine(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
+                                m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1,
+                                m->has_shared ? m->sh_out : NULL, y, s));
+    return 0;
+}
+
+int waste_hip_moe_status(waste_hip_moe *m, void *stream)
+{
+    if (!m) return WASTE_HIP_EINVAL;
+    int e = 0;
+    CK(hipStreamSynchronize((hipStream_t)stream));
+    CK(hipMemcpy(&e, m->err, sizeof e, hipMemcpyDeviceToHost));
+    CK(hipMemset(m->err, 0, sizeof e));
+    if (e & 1) return WASTE_HIP_EUNBOUND;
+    if (e & 2) return WASTE_HIP_EROUTE;
+    return 0;
+}
+
+size_t waste_hip_moe_bytes(const waste_hip_moe *m, int T, int n_distinct)
+{
+    if (!m) return 0;
+    size_t b = (size_t)n_distinct * (2 * m->idx_gu + m->idx_d + 2 * (size_t)(2 * m->I + m->H));
+    if (m->has_router) {
+        const whip_mat *r = &m->router;
+        b += (size_t)r->rows * r->rowbytes;
+        if (r->fmt != WQ_F32) b += (size_t)r->rows * ((r->cols + r->group - 1) / r->group) * 2;
+        if (m->d_bias) b += (size_t)m->E * 4;
+    }
+    if (m->has_shared)
+        for (int k = 0; k < 3; k++) {
+            const whip_mat *t = &m->sh[k];
+            b += (size_t)t->rows * t->rowbytes;
+            if (t->fmt != WQ_F32) b += (size_t)t->rows * ((t->cols + t->group - 1) / t->group) * 2;
+        }
+    b += 9 * 256 * 8 * 2;                      /* the layer's nine codebooks */
+    b += (size_t)T * m->H * 4 * 2;             /* activations in and out     */
+    return b;
+}
+
+int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W, void *stream)
+{
+    if (!m || expert < 0 || expert >= m->E || kind < 0 || kind > 2 || !W || !m->d_books ||
+        m->cb < 0 || m->cb + 9 > m->n_books)
+        return WASTE_HIP_EINVAL;
+    const uint8_t *rec = m->h_recs[expert];
+    if (!rec) return WASTE_HIP_EUNBOUND;
+    const int M = kind == 2 ? m->H : m->I, N = kind == 2 ? m->I : m->H;
+    const uint32_t off = kind == 0 ? m->off_gate : kind == 1 ? m->off_up : m->off_down;
+    const uint16_t *sc = (const uint16_t *)(rec + m->off_sc) + (kind == 0 ? 0 : kind == 1 ? m->I : 2 * m->I);
+    CK((hipError_t)whip_dequant(rec + off, sc, m->d_books, m->cb + 3 * kind, M, N, W,
+                                (hipStream_t)stream));
+    return 0;
+}
