@@ -1,0 +1,266 @@
+# SPDX-License-Identifier: Apache-2.0
+"""MoE layer decode benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 20] [--config dsv3] [--batch 1]
+
+A step is one MoE layer forward over one batch of synthetic tokens:
+router logits -> group-limited top-8 -> VQ3R gate/up -> SwiGLU -> VQ3R
+down -> weighted combine + shared expert, everything resident in HBM.
+
+The workload is the DeepSeek-V3-shaped layer (hidden 7168, 256 routed
+experts of width 2048 in 3-bit residual VQ, sigmoid + bias, 8 groups / 4
+kept, top-8, routed scale 2.5, one 4-bit shared expert, F32 router, bf16
+activations), batch 1, seed 0.  Steps cycle over --layers layer objects
+that share one expert slab but each hold their own router and shared
+expert, and every step routes a fresh token, so no step finds its weights
+in the 256 MB Infinity Cache from the step before — as in a real decode,
+where 58 other layers run between two visits to the same one.
+
+Printed: one JSON line with the metric (MoE layer us/token at batch 1),
+HBM GB/s of algorithmic bytes, the dominant kernel's roofline from HIP
+events on its stream, and the reference CPU path (C restatement,
+AVX-512, all threads) timed on this host on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "MoE layer µs/token + HBM GB/s (% of peak) at batch 1; prefill tokens/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_layers(torch, warp_amd, synth, cfg, n_layers, max_tokens, seed=0):
+    H, E, I = cfg["hidden"], cfg["n_experts"], cfg["moe_inter"]
+    t0 = time.time()
+    books = synth.codebooks(seed, H, I)
+    rb = synth.record_bytes(H, I)
+    slab = torch.empty(E * rb, dtype=torch.uint8, device="cuda:0")
+    synth.records(seed, 0, H, I, books, 0, E, slab.data_ptr())
+    torch.cuda.synchronize()
+    log(f"[bench] {E} expert records ({E * rb / 1e9:.2f} GB) generated in {time.time() - t0:.1f}s")
+    router, bias, sh = synth.trunk(cfg, seed + 1)
+    layers = []
+    for li in range(n_layers):
+        m = warp_amd.MoeLayer(hidden=H, n_experts=E, top_k=cfg["top_k"], moe_inter=I,
+                              n_shared=cfg["n_shared"], score_func=cfg["score_func"],
+                              renorm=cfg["renorm"], routed_scale=cfg["routed_scale"],
+                              n_group=cfg["n_group"], topk_group=cfg["topk_group"],
+                              max_tokens=max_tokens)
+        m.set_codebooks(books)
+        m.set_router(router, bias)
+        if sh:
+            m.set_shared(*sh)
+        for e in range(E):
+            rc = m.bind_expert(e, slab.data_ptr() + e * rb, rb)
+            if rc != 0:
+                raise RuntimeError(f"bind_expert {e}: {rc}")
+        layers.append(m)
+    log(f"[bench] {n_layers} layer objects ready in {time.time() - t0:.1f}s")
+    return layers, slab, books, rb, (router, bias, sh)
+
+
+def cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, budget_s, nthreads):
+    """The reference's CPU decode path (the oracle's AVX-512-order C
+    restatement, threaded) on the same layer, timed on a bounded sample of
+    the same tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_lib import Oracle, OrcMoe, OrcTensor, fp, ptr, u16p, u8p
+    import ctypes as C
+    orc = Oracle()
+    H, E, I, K = cfg["hidden"], cfg["n_experts"], cfg["moe_inter"], cfg["top_k"]
+    host = slab.cpu().numpy()
+    _, bT = orc.books(books)
+    router, bias, sh = trunk
+
+    def ot(t):
+        if t is None or t.rows == 0:
+            return OrcTensor(0, 0, 0, 0, None, None, 0)
+        return OrcTensor(t.fmt, t.rows, t.cols, t.group, t.q.ctypes.data_as(C.c_void_p),
+                         ptr(t.qs, u16p) if t.qs is not None else None, t.rowbytes)
+    recs = (u8p * E)(*[ptr(host[e * rb:(e + 1) * rb], u8p) for e in range(E)])
+    m = OrcMoe(H, E, K, I, cfg["n_shared"], cfg["score_func"], cfg["renorm"], cfg["routed_scale"],
+               cfg["n_group"], cfg["topk_group"], 3, 256, 8, 1, ot(router),
+               ptr(bias, fp) if bias is not None else None,
+               ot(sh[0] if sh else None), ot(sh[1] if sh else None), ot(sh[2] if sh else None),
+               ptr(bT, fp), 9, recs, rb)
+    out = np.zeros(H, np.float32)
+    idx = np.zeros(K, np.int32)
+    w = np.zeros(K, np.float32)
+    n, t_used = 0, 0.0
+    first = True
+    for x in xs:
+        x = np.ascontiguousarray(x, np.float32)
+        t0 = time.perf_counter()
+        orc.lib.orc_moe_layer_mt(C.byref(m), ptr(x, fp), ptr(out, fp), idx.ctypes.data_as(C.POINTER(C.c_int)),
+                                 ptr(w, fp), nthreads)
+        dt = time.perf_counter() - t0
+        if first:                   # warm caches and the thread pool; not timed
+            first = False
+            continue
+        n += 1
+        t_used += dt
+        if t_used >= budget_s and n >= 3:
+            break
+    isa = {2: "AVX-512", 0: "portable C"}[orc.lib.orc_cpu_isa()]
+    return n, t_used, isa
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="dsv3")
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build's MoE path runs on a single MI355X and "
+              f"--gpus {a.gpus} is not supported (expert-parallel sharding is described in DESIGN.md).",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    import warp_amd
+    from warp_amd import synth
+    assert torch.cuda.is_available(), "bench.py needs an MI355X"
+    cfg = synth.CONFIGS[a.config]
+    H, E, K, I = cfg["hidden"], cfg["n_experts"], cfg["top_k"], cfg["moe_inter"]
+    B = a.batch
+    layers, slab, books, rb, trunk = build_layers(torch, warp_amd, synth, cfg, a.layers, B)
+
+    gen = torch.Generator(device="cpu").manual_seed(0)
+    n_tok = (a.warmup + a.steps + 8) * B
+    x_all = torch.randn((n_tok, H), generator=gen, dtype=torch.float32)
+    if cfg["bf16"]:
+        x_all = x_all.to(torch.bfloat16)
+    xd = x_all.to("cuda:0")
+    esz = xd.element_size()
+    y = torch.empty((B, H), dtype=torch.float32, device="cuda:0")
+    ids = torch.empty((a.warmup + a.steps, B, K), dtype=torch.int32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(i, rec_ids=True):
+        m = layers[i % len(layers)]
+        m.forward(xd.data_ptr() + i * B * H * esz, B, y.data_ptr(),
+                  ids[i].data_ptr() if rec_ids else None, None, None, bf16=cfg["bf16"], stream=sp)
+
+    for i in range(a.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    for m in layers:
+        st = m.status(sp)
+        if st != 0:
+            raise RuntimeError(f"device error {st}")
+
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(a.warmup, a.warmup + a.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = gpu_ms / a.steps
+    for m in layers:
+        st = m.status(sp)
+        if st != 0:
+            raise RuntimeError(f"device error {st}")
+
+    # algorithmic bytes: distinct experts per step from the routed ids
+    ids_h = ids[a.warmup:].cpu().numpy()
+    distinct = [len(np.unique(ids_h[s].reshape(-1))) for s in range(a.steps)]
+    bytes_steps = [layers[0].bytes(B, u) for u in distinct]
+    bytes_per_step = float(np.mean(bytes_steps))
+    gbps = bytes_per_step / (ms_per_step * 1e-3) / 1e9
+    us_per_token = ms_per_step * 1e3 / B
+
+    # live per-stage timing (HIP events on the forward's stream), a second
+    # pass over the same steps with profiling on
+    for m in layers:
+        m.profile(True)
+    for i in range(a.warmup, a.warmup + a.steps):
+        step(i, rec_ids=False)
+    torch.cuda.synchronize()
+    tot, nfw = {}, 0
+    for m in layers:
+        n, st = m.profile_read()
+        nfw += n
+        for k, v in st.items():
+            tot[k] = tot.get(k, 0.0) + v
+        m.profile(False)
+    stage_ms = {k: v / nfw for k, v in tot.items()}
+    dom = max(("routed_gate_up", "routed_down"), key=lambda k: stage_ms[k])
+    idx_gu = I * (H // 8) * 3
+    idx_d = H * (I // 8) * 3
+    u_mean = float(np.mean(distinct))
+    # per-launch algorithmic bytes of the dominant kernel: the index streams
+    # it reads (gate+up of every routed (token, expert) pair, or down)
+    dom_bytes = (2 * idx_gu if dom == "routed_gate_up" else idx_d) * u_mean
+    dom_ms = stage_ms[dom]
+    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+
+    cpu = None
+    if not a.no_cpu and B == 1:
+        nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        xs = x_all[a.warmup:].to(torch.float32).numpy()
+        n, t_used, isa = cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, a.cpu_seconds, nthreads)
+        cpu = {"value": round(t_used / n * 1e6, 1), "unit": "us/token", "cores": nthreads,
+               "kind": "port",
+               "sample": f"{n} tokens of the same {a.config} batch-1 layer (fresh token each), "
+                         f"{isa} kernels, after one untimed warm-up token"}
+
+    out = {
+        "metric": METRIC,
+        "value": round(us_per_token, 2),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights VQ3R-encoded on device; bf16 N(0,1) tokens)"
+                if cfg["bf16"] else "synthetic (seeded N(0,0.02) weights VQ3R-encoded on device; "
+                                    "fp32 N(0,1) tokens)",
+        "config": {"workload": f"{a.config} MoE layer decode, batch {B}", "hidden": H,
+                   "experts": E, "top_k": K, "moe_inter": I, "batch": B,
+                   "layers_cycled": a.layers},
+        "hbm_gbps": round(gbps, 1),
+        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "bytes_per_step": int(bytes_per_step),
+        "distinct_experts_per_step": round(u_mean, 2),
+        "wall_ms_per_step": round(wall * 1e3 / a.steps, 5),
+        "stage_us": {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
+        "roofline": {"bound": "hbm", "kernel": "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_down",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "launch_us": round(dom_ms * 1e3, 2), "algorithmic_bytes": int(dom_bytes)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    for m in layers:
+        m.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -142,6 +142,19 @@ int waste_hip_moe_status(waste_hip_moe *m, void *stream);
  * — the algorithmic traffic a roofline divides by. */
 size_t waste_hip_moe_bytes(const waste_hip_moe *m, int T, int n_distinct);
 
+/* Per-stage device time of forward(), from HIP events recorded on the
+ * forward's stream around each stage while profiling is on (it then waits
+ * for each forward to finish).  Stages: 0 activations, 1 router, 2 route,
+ * 3 shared gate/up, 4 routed gate/up, 5 SwiGLU, 6 routed down, 7 shared
+ * down, 8 combine.  Milliseconds summed over `forwards` calls. */
+#define WASTE_HIP_STAGES 9
+typedef struct {
+    int forwards;
+    float ms[WASTE_HIP_STAGES];
+} waste_hip_moe_prof;
+int waste_hip_moe_profile(waste_hip_moe *m, int on);
+int waste_hip_moe_profile_read(waste_hip_moe *m, waste_hip_moe_prof *out);
+
 /* Materialises one bound expert matrix (kind 0 gate, 1 up, 2 down) as
  * fp32 [M][N] in device memory W: the format's closed form, bit-exact. */
 int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W,

@@ -62,61 +62,7 @@ def make_record(layer, eid, cb_base, shapes, idx_list, scale_list):
     return bytes(rec)
 
 
-def f16_bits(a):
-    return np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
-
-
-def quant_q8g(W, group=128):
-    """int8 + f16 scale per group (tools/convert.py:913-924): scale =
-    amax/127 in fp32, q = clamp(round_half_even(w / scale)), stored scale
-    rounded to f16."""
-    rows, N = W.shape
-    ng = (N + group - 1) // group
-    Wp = np.zeros((rows, ng * group), np.float32)
-    Wp[:, :N] = W
-    g = Wp.reshape(rows, ng, group)
-    sc = np.maximum(np.abs(g).max(-1, keepdims=True), np.float32(1e-8)) / np.float32(127.0)
-    q = np.clip(np.rint(g / sc), -127, 127).astype(np.int8).reshape(rows, ng * group)
-    return q, f16_bits(sc.reshape(rows, ng)), ng * group
-
-
-def quant_q4g(W, group=128):
-    """int4 two per byte, low nibble first, +8 bias, f16 scale per group
-    (tools/convert.py:893-910): scale = amax/7."""
-    rows, N = W.shape
-    ng = (N + group - 1) // group
-    Wp = np.zeros((rows, ng * group), np.float32)
-    Wp[:, :N] = W
-    g = Wp.reshape(rows, ng, group)
-    sc = np.maximum(np.abs(g).max(-1, keepdims=True), np.float32(1e-8)) / np.float32(7.0)
-    q = np.clip(np.rint(g / sc), -8, 7).astype(np.int32).reshape(rows, ng * group)
-    nib = (q + 8).astype(np.uint8) & 0x0F
-    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).astype(np.uint8)
-    return packed.view(np.int8), f16_bits(sc.reshape(rows, ng)), ng * group // 2
-
-
-class Tensor:
-    """A trunk tensor: fmt, rows, cols, group, payload (np array), f16
-    scales (np u16 or None), rowbytes."""
-
-    def __init__(self, fmt, rows, cols, group, q, qs, rowbytes):
-        self.fmt, self.rows, self.cols, self.group = fmt, rows, cols, group
-        self.q, self.qs, self.rowbytes = q, qs, rowbytes
-
-    @staticmethod
-    def absent():
-        return Tensor(FMT_F32, 0, 0, 0, None, None, 0)
-
-    @staticmethod
-    def make(fmt, W):
-        rows, cols = W.shape
-        if fmt == FMT_F32:
-            return Tensor(fmt, rows, cols, 0, np.ascontiguousarray(W, np.float32), None, cols * 4)
-        if fmt == FMT_Q8G:
-            q, qs, rb = quant_q8g(W)
-            return Tensor(fmt, rows, cols, 128, q, qs, rb)
-        q, qs, rb = quant_q4g(W)
-        return Tensor(fmt, rows, cols, 128, q, qs, rb)
+from warp_amd.synth import Tensor, f16_bits, quant_q4g, quant_q8g  # noqa: E402,F401
 
 
 class Layer:

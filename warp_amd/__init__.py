@@ -27,7 +27,12 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_vq3r", "waste_hip_moe_create", "waste_hip_moe_destroy",
            "waste_hip_moe_set_router", "waste_hip_moe_set_shared", "waste_hip_moe_set_codebooks",
            "waste_hip_moe_set_expert", "waste_hip_moe_bind_expert", "waste_hip_moe_forward",
-           "waste_hip_moe_status", "waste_hip_moe_bytes", "waste_hip_moe_dequant"]
+           "waste_hip_moe_status", "waste_hip_moe_bytes", "waste_hip_moe_dequant",
+           "waste_hip_moe_profile", "waste_hip_moe_profile_read", "waste_hip_record_bytes",
+           "waste_hip_synth_codebooks", "waste_hip_synth_records"]
+
+STAGES = ["activations", "router", "route", "shared_gate_up", "routed_gate_up", "swiglu",
+          "routed_down", "shared_down", "combine"]
 
 
 class HipError(RuntimeError):
@@ -45,6 +50,10 @@ class MoeCfg(C.Structure):
 class HipTensor(C.Structure):
     _fields_ = [("fmt", C.c_int), ("rows", C.c_int), ("cols", C.c_int), ("group", C.c_int),
                 ("q", C.c_void_p), ("qs", C.c_void_p), ("rowbytes", C.c_size_t)]
+
+
+class MoeProf(C.Structure):
+    _fields_ = [("forwards", C.c_int), ("ms", C.c_float * 9)]
 
 
 class VqJob(C.Structure):
@@ -83,6 +92,8 @@ def lib():
         "waste_hip_moe_status": (i, [vp, vp]),
         "waste_hip_moe_bytes": (C.c_size_t, [vp, i, i]),
         "waste_hip_moe_dequant": (i, [vp, i, i, vp, vp]),
+        "waste_hip_moe_profile": (i, [vp, i]),
+        "waste_hip_moe_profile_read": (i, [vp, C.POINTER(MoeProf)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -166,6 +177,14 @@ class MoeLayer:
 
     def bytes(self, T, n_distinct):
         return self.L.waste_hip_moe_bytes(self.h, T, n_distinct)
+
+    def profile(self, on):
+        check(self.L.waste_hip_moe_profile(self.h, int(on)), "profile")
+
+    def profile_read(self):
+        p = MoeProf()
+        check(self.L.waste_hip_moe_profile_read(self.h, C.byref(p)), "profile_read")
+        return p.forwards, dict(zip(STAGES, list(p.ms)))
 
     def dequant(self, e, kind, W_ptr, stream=None):
         return self.L.waste_hip_moe_dequant(self.h, e, kind, W_ptr, stream)

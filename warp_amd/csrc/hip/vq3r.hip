@@ -30,12 +30,12 @@
 
 extern "C" int whip_vq_chunks(int nv) { return (nv + VC - 1) / VC; }
 
-__global__ void __launch_bounds__(256)
-k_vq_apply(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
-           const int32_t *__restrict__ pair_src, const float *__restrict__ src, int src_ld,
-           const float *__restrict__ booksT, int cb, uint32_t off0, uint32_t off1,
-           int kinds, int M, int nv, int nch, int rsplit, float *__restrict__ part,
-           int *__restrict__ err)
+__device__ __forceinline__ void
+vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
+              const int32_t *__restrict__ pair_src, const float *__restrict__ src, int src_ld,
+              const float *__restrict__ booksT, int cb, uint32_t off0, uint32_t off1,
+              int kinds, int M, int nv, int nch, int rsplit, float *__restrict__ part,
+              int *__restrict__ err)
 {
     __shared__ float lut[VC * LUT_PER_V];
     __shared__ float xs[VC * 8];
@@ -105,13 +105,29 @@ k_vq_apply(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ 
     }
 }
 
+// Two symbols for one body, so that profiles tell the gate/up pass (two
+// kinds per pair, the hidden-wide tables) from the down pass.
+#define VQ_KERNEL(NAME)                                                                         \
+    __global__ void __launch_bounds__(256)                                                      \
+    NAME(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,         \
+         const int32_t *__restrict__ pair_src, const float *__restrict__ src, int src_ld,       \
+         const float *__restrict__ booksT, int cb, uint32_t off0, uint32_t off1, int kinds,     \
+         int M, int nv, int nch, int rsplit, float *__restrict__ part, int *__restrict__ err)   \
+    {                                                                                           \
+        vq_apply_body(recs, pair_exp, pair_src, src, src_ld, booksT, cb, off0, off1, kinds, M,  \
+                      nv, nch, rsplit, part, err);                                              \
+    }
+VQ_KERNEL(k_vq_gate_up)
+VQ_KERNEL(k_vq_down)
+
 extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
 {
     const int nch = whip_vq_chunks(a->nv);
     dim3 grid(nch, a->kinds * a->rsplit, a->P);
-    hipLaunchKernelGGL(k_vq_apply, grid, dim3(256), 0, s, a->recs, a->pair_exp, a->pair_src,
-                       a->src, a->src_ld, a->booksT, a->cb, a->idx_off[0], a->idx_off[1],
-                       a->kinds, a->M, a->nv, nch, a->rsplit, a->part, a->err);
+    hipLaunchKernelGGL(a->kinds == 2 ? k_vq_gate_up : k_vq_down, grid, dim3(256), 0, s, a->recs,
+                       a->pair_exp, a->pair_src, a->src, a->src_ld, a->booksT, a->cb,
+                       a->idx_off[0], a->idx_off[1], a->kinds, a->M, a->nv, nch, a->rsplit,
+                       a->part, a->err);
     return (int)hipGetLastError();
 }
 

@@ -48,6 +48,9 @@ struct waste_hip_moe {
     float *xf, *logits, *w, *pair_w, *part_gu, *h, *part_d, *sh_a, *sh_b, *h_sh, *sh_out;
     int32_t *ids, *pair_tok, *pair_exp, *tok_pairs;
     int *err;
+    int prof_on;
+    hipEvent_t ev[WASTE_HIP_STAGES + 1];
+    waste_hip_moe_prof prof;
 };
 
 static float f16_book(uint16_t h)
@@ -106,6 +109,8 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
                      m->tok_pairs, m->err };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
+    if (m->ev[0])
+        for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
     free(m->h_recs);
     free(m);
 }
@@ -346,12 +351,16 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     hipStream_t s = (hipStream_t)stream;
     const int E = m->E, K = m->K, H = m->H, I = m->I, P = T * K;
     const float *xf = (const float *)x;
+#define MARK(i) do { if (m->prof_on) CK(hipEventRecord(m->ev[i], s)); } while (0)
+    MARK(0);
     if (x_bf16) {
         CK((hipError_t)whip_bf16_to_f32((const uint16_t *)x, m->xf, (size_t)T * H, s));
         xf = m->xf;
     }
+    MARK(1);
     float *lg = logits ? logits : m->logits;
     CK((hipError_t)whip_gemv(&m->router, NULL, xf, H, T, lg, NULL, E, s));
+    MARK(2);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
     int32_t *d_ids = ids ? ids : m->ids;
@@ -361,8 +370,10 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     if (T > 1)
         CK((hipError_t)whip_pairs(d_ids, d_w, T, K, E, m->pair_tok, m->pair_exp, m->pair_w,
                                   m->tok_pairs, s));
+    MARK(3);
     if (m->has_shared)
         CK((hipError_t)whip_gemv(&m->sh[0], &m->sh[1], xf, H, T, m->sh_a, m->sh_b, m->SI, s));
+    MARK(4);
 
     whip_vq_args a;
     memset(&a, 0, sizeof a);
@@ -372,17 +383,50 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     a.kinds = 2; a.M = I; a.nv = m->nv_gu; a.P = P; a.rsplit = m->rsplit_gu;
     a.part = m->part_gu; a.err = m->err;
     CK((hipError_t)whip_vq_apply(&a, s));
+    MARK(5);
     CK((hipError_t)whip_vq_act(m->d_recs, m->pair_exp, P, m->part_gu, m->nch_gu, I, m->off_sc,
                                m->h, m->sh_a, m->sh_b, T, m->SI, m->has_shared ? m->h_sh : NULL, s));
     a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.cb = m->cb + 6;
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
+    MARK(6);
     a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
     CK((hipError_t)whip_vq_apply(&a, s));
+    MARK(7);
     if (m->has_shared)
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
+    MARK(8);
     CK((hipError_t)whip_combine(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
                                 m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1,
                                 m->has_shared ? m->sh_out : NULL, y, s));
+    MARK(9);
+#undef MARK
+    if (m->prof_on) {
+        CK(hipEventSynchronize(m->ev[WASTE_HIP_STAGES]));
+        for (int i = 0; i < WASTE_HIP_STAGES; i++) {
+            float ms = 0;
+            CK(hipEventElapsedTime(&ms, m->ev[i], m->ev[i + 1]));
+            m->prof.ms[i] += ms;
+        }
+        m->prof.forwards++;
+    }
+    return 0;
+}
+
+int waste_hip_moe_profile(waste_hip_moe *m, int on)
+{
+    if (!m) return WASTE_HIP_EINVAL;
+    if (on && !m->ev[0])
+        for (int i = 0; i <= WASTE_HIP_STAGES; i++)
+            CK(hipEventCreate(&m->ev[i]));
+    memset(&m->prof, 0, sizeof m->prof);
+    m->prof_on = on;
+    return 0;
+}
+
+int waste_hip_moe_profile_read(waste_hip_moe *m, waste_hip_moe_prof *out)
+{
+    if (!m || !out) return WASTE_HIP_EINVAL;
+    *out = m->prof;
     return 0;
 }
 
