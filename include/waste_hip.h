@@ -144,10 +144,10 @@ size_t waste_hip_moe_bytes(const waste_hip_moe *m, int T, int n_distinct);
 
 /* Per-stage device time of forward(), from HIP events recorded on the
  * forward's stream around each stage while profiling is on (it then waits
- * for each forward to finish).  Stages: 0 activations, 1 router, 2 route,
- * 3 shared gate/up, 4 routed gate/up, 5 SwiGLU, 6 routed down, 7 shared
- * down, 8 combine.  Milliseconds summed over `forwards` calls. */
-#define WASTE_HIP_STAGES 9
+ * for each forward to finish).  Stages: 0 router logits + shared expert
+ * gate/up, 1 routing, 2 routed gate/up, 3 SwiGLU, 4 routed down, 5 shared
+ * down, 6 combine.  Milliseconds summed over `forwards` calls. */
+#define WASTE_HIP_STAGES 7
 typedef struct {
     int forwards;
     float ms[WASTE_HIP_STAGES];

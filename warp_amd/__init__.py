@@ -31,8 +31,8 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_moe_profile", "waste_hip_moe_profile_read", "waste_hip_record_bytes",
            "waste_hip_synth_codebooks", "waste_hip_synth_records"]
 
-STAGES = ["activations", "router", "route", "shared_gate_up", "routed_gate_up", "swiglu",
-          "routed_down", "shared_down", "combine"]
+STAGES = ["router_shared_gate_up", "route", "routed_gate_up", "swiglu", "routed_down",
+          "shared_down", "combine"]
 
 
 class HipError(RuntimeError):
@@ -53,7 +53,7 @@ class HipTensor(C.Structure):
 
 
 class MoeProf(C.Structure):
-    _fields_ = [("forwards", C.c_int), ("ms", C.c_float * 9)]
+    _fields_ = [("forwards", C.c_int), ("ms", C.c_float * 7)]
 
 
 class VqJob(C.Structure):

@@ -4,138 +4,248 @@
 // logits and the shared expert (F32, Q8G int8 + f16 group scale, Q4G two
 // signed nibbles per byte, low first, minus 8; tools/convert.py:893-924).
 //
-// One wavefront per output row; each lane streams 16-byte chunks of the
-// row (coalesced 128-bit loads) and keeps a partial per token; a chunk
-// never straddles a quantisation group, so its group scale multiplies the
-// chunk's partial once.  Up to TB tokens share every weight load; larger
-// batches take further passes over the (L2-resident) row.
+// One launch runs up to three independent products ("jobs"), each over its
+// own range of workgroups, so the router and the shared expert's gate/up
+// leave in one dispatch.  A job may pair two matrices of one shape (gate
+// and up): the wavefronts that own row r of both then write
+// silu(gate.x) * (up.x) directly, so the shared expert needs no separate
+// activation pass.
+//
+// A row is split across wpr wavefronts; each lane streams 16-byte chunks
+// (coalesced 128-bit loads), UNROLL of them in flight at once, and keeps a
+// partial per token; a chunk never straddles a quantisation group, so the
+// group scale multiplies the chunk's partial once.  Activations may be
+// fp32 or bf16 (converted as they are read).
 #include "common.h"
 #include "launch.h"
 
-#define TB 4
+#define TB 4          // tokens sharing one pass over the weights
+#define UNROLL 4      // 16-byte chunks in flight per lane
+
+template <int FMT> struct chunk_of;
+template <> struct chunk_of<0> { static constexpr int NE = 4; };
+template <> struct chunk_of<2> { static constexpr int NE = 16; };
+template <> struct chunk_of<3> { static constexpr int NE = 32; };
 
 template <int FMT>
-__device__ __forceinline__ void decode_chunk(const uint8_t *row, int k, float *w);
-
-template <> __device__ __forceinline__ void decode_chunk<0>(const uint8_t *row, int k, float *w)
+__device__ __forceinline__ void decode_chunk(const uint4 v, float *w)
 {
-    const float4 v = *(const float4 *)(row + (size_t)k * 16);
-    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
-}
-
-template <> __device__ __forceinline__ void decode_chunk<2>(const uint8_t *row, int k, float *w)
-{
-    const uint4 v = *(const uint4 *)(row + (size_t)k * 16);
     const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+    if (FMT == 0) {
 #pragma unroll
-    for (int i = 0; i < 16; i++) w[i] = (float)(int8_t)((u[i >> 2] >> ((i & 3) * 8)) & 0xff);
-}
-
-template <> __device__ __forceinline__ void decode_chunk<3>(const uint8_t *row, int k, float *w)
-{
-    const uint4 v = *(const uint4 *)(row + (size_t)k * 16);
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+        for (int i = 0; i < 4; i++) w[i] = __uint_as_float(u[i]);
+    } else if (FMT == 2) {
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const uint32_t b = (u[i >> 2] >> ((i & 3) * 8)) & 0xff;
-        w[2 * i] = (float)((int)(b & 15) - 8);
-        w[2 * i + 1] = (float)((int)(b >> 4) - 8);
+        for (int i = 0; i < 16; i++) w[i] = (float)(int8_t)((u[i >> 2] >> ((i & 3) * 8)) & 0xff);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t b = (u[i >> 2] >> ((i & 3) * 8)) & 0xff;
+            w[2 * i] = (float)((int)(b & 15) - 8);
+            w[2 * i + 1] = (float)((int)(b >> 4) - 8);
+        }
     }
 }
 
-template <int FMT>
-__global__ void __launch_bounds__(256)
-k_gemv(const uint8_t *__restrict__ W0, const uint16_t *__restrict__ S0, size_t rb0,
-       const uint8_t *__restrict__ W1, const uint16_t *__restrict__ S1, size_t rb1,
-       int rows, int cols, int group, const float *__restrict__ x, int x_ld, int T,
-       float *__restrict__ y0, float *__restrict__ y1, int y_ld)
+// n activations starting at element e of token row xr (fp32 or bf16)
+template <int N>
+__device__ __forceinline__ void load_x(const void *xr, int bf16, int e, float *x)
 {
-    constexpr int NE = FMT == 0 ? 4 : FMT == 2 ? 16 : 32;   // elements per 16 B chunk
-    const int which = blockIdx.y;
-    const uint8_t *W = which ? W1 : W0;
-    const uint16_t *S = which ? S1 : S0;
-    const size_t rowbytes = which ? rb1 : rb0;
-    float *y = which ? y1 : y0;
-    const int r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (r >= rows) return;
-    const int ng = FMT == 0 ? 1 : (cols + group - 1) / group;
-    const int padded = FMT == 0 ? cols : ng * group;
-    const int nchunk = (padded + NE - 1) / NE;
-    const uint8_t *row = W + (size_t)r * rowbytes;
-    const uint16_t *sr = FMT == 0 ? nullptr : S + (size_t)r * ng;
+    if (bf16) {
+        const uint16_t *p = (const uint16_t *)xr + e;
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const uint2 v = *(const uint2 *)(p + i);
+            x[i] = wh_bf16(v.x & 0xffff); x[i + 1] = wh_bf16(v.x >> 16);
+            x[i + 2] = wh_bf16(v.y & 0xffff); x[i + 3] = wh_bf16(v.y >> 16);
+        }
+    } else {
+        const float *p = (const float *)xr + e;
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const float4 v = *(const float4 *)(p + i);
+            x[i] = v.x; x[i + 1] = v.y; x[i + 2] = v.z; x[i + 3] = v.w;
+        }
+    }
+}
 
-    for (int t0 = 0; t0 < T; t0 += TB) {
-        const int tn = min(TB, T - t0);
-        float acc[TB] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int k = lane; k < nchunk; k += 64) {
+struct gemv_job {
+    const uint8_t *W0, *W1;
+    const uint16_t *S0, *S1;
+    size_t rowbytes;
+    int fmt, rows, cols, group;
+    const void *x;
+    int x_ld, x_bf16;
+    float *y;
+    int y_ld;
+    int wpr, blk0, nblk;
+};
+struct gemv_pack {
+    gemv_job j[3];
+    int n, T;
+};
+
+// partial dot products of one wavefront's share of row r, for TB tokens
+template <int FMT>
+__device__ __forceinline__ void row_partial(const gemv_job &J, const uint8_t *W, const uint16_t *S,
+                                            int r, int part, int lane, int t0, int tn, float *acc)
+{
+    constexpr int NE = chunk_of<FMT>::NE;
+    const int ng = FMT == 0 ? 1 : (J.cols + J.group - 1) / J.group;
+    const int padded = FMT == 0 ? J.cols : ng * J.group;
+    const int nchunk = (padded + NE - 1) / NE;
+    const uint8_t *row = W + (size_t)r * J.rowbytes;
+    const uint16_t *sr = FMT == 0 ? nullptr : S + (size_t)r * ng;
+    const int stride = 64 * J.wpr;
+    for (int k0 = part * 64 + lane; k0 < nchunk; k0 += stride * UNROLL) {
+        uint4 raw[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            const int k = k0 + u * stride;
+            raw[u] = k < nchunk ? *(const uint4 *)(row + (size_t)k * 16) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            const int k = k0 + u * stride;
+            if (k >= nchunk) break;
             float w[NE];
-            decode_chunk<FMT>(row, k, w);
+            decode_chunk<FMT>(raw[u], w);
             const int e0 = k * NE;
-            const float sc = FMT == 0 ? 1.0f : wh_f16_scale(sr[e0 / group]);
+            const float sc = FMT == 0 ? 1.0f : wh_f16_scale(sr[e0 / J.group]);
 #pragma unroll
             for (int t = 0; t < TB; t++) {
                 if (t >= tn) break;
-                const float *xt = x + (size_t)(t0 + t) * x_ld + e0;
-                float part = 0.0f;
-                if (e0 + NE <= cols) {
+                const uint8_t *xr = (const uint8_t *)J.x + (size_t)(t0 + t) * J.x_ld * (J.x_bf16 ? 2 : 4);
+                float part_t = 0.0f;
+                if (e0 + NE <= J.cols) {
+                    float xv[NE];
+                    load_x<NE>(xr, J.x_bf16, e0, xv);
 #pragma unroll
-                    for (int i = 0; i < NE; i += 4) {
-                        const float4 xv = *(const float4 *)(xt + i);
-                        part = __fmaf_rn(w[i], xv.x, part);
-                        part = __fmaf_rn(w[i + 1], xv.y, part);
-                        part = __fmaf_rn(w[i + 2], xv.z, part);
-                        part = __fmaf_rn(w[i + 3], xv.w, part);
-                    }
+                    for (int i = 0; i < NE; i++) part_t = __fmaf_rn(w[i], xv[i], part_t);
                 } else {
-                    for (int i = 0; i < NE && e0 + i < cols; i++) part = __fmaf_rn(w[i], xt[i], part);
+                    for (int i = 0; i < NE && e0 + i < J.cols; i++) {
+                        const float xi = J.x_bf16 ? wh_bf16(((const uint16_t *)xr)[e0 + i])
+                                                  : ((const float *)xr)[e0 + i];
+                        part_t = __fmaf_rn(w[i], xi, part_t);
+                    }
                 }
-                acc[t] = __fmaf_rn(sc, part, acc[t]);
+                acc[t] = __fmaf_rn(sc, part_t, acc[t]);
             }
+        }
+    }
+}
+
+template <int FMT>
+__device__ void run_job(const gemv_job &J, int T, int blk, float (*red)[2][TB])
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rows_per_blk = 4 / J.wpr;
+    const int r = blk * rows_per_blk + wave / J.wpr, part = wave % J.wpr;
+    const bool live = r < J.rows;
+    for (int t0 = 0; t0 < T; t0 += TB) {
+        const int tn = min(TB, T - t0);
+        float a0[TB] = {0.0f, 0.0f, 0.0f, 0.0f}, a1[TB] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (live) {
+            row_partial<FMT>(J, J.W0, J.S0, r, part, lane, t0, tn, a0);
+            if (J.W1) row_partial<FMT>(J, J.W1, J.S1, r, part, lane, t0, tn, a1);
         }
 #pragma unroll
         for (int t = 0; t < TB; t++) {
-            if (t >= tn) break;
-            const float v = wave_sum(acc[t]);
-            if (lane == 0) y[(size_t)(t0 + t) * y_ld + r] = v;
+            a0[t] = wave_sum(a0[t]);
+            a1[t] = wave_sum(a1[t]);
         }
+        if (J.wpr > 1) {
+            __syncthreads();
+            if (lane == 0)
+#pragma unroll
+                for (int t = 0; t < TB; t++) { red[wave][0][t] = a0[t]; red[wave][1][t] = a1[t]; }
+            __syncthreads();
+            if (part == 0 && lane == 0)
+#pragma unroll
+                for (int t = 0; t < TB; t++) {
+                    float s0 = red[wave][0][t], s1 = red[wave][1][t];
+                    for (int q = 1; q < J.wpr; q++) { s0 += red[wave + q][0][t]; s1 += red[wave + q][1][t]; }
+                    a0[t] = s0; a1[t] = s1;
+                }
+        }
+        if (live && part == 0 && lane == 0)
+            for (int t = 0; t < tn; t++)
+                J.y[(size_t)(t0 + t) * J.y_ld + r] = J.W1 ? wh_silu_mul(a0[t], a1[t]) : a0[t];
     }
+}
+
+__global__ void __launch_bounds__(256) k_gemv_multi(gemv_pack pk)
+{
+    __shared__ float red[4][2][TB];
+    int ji = 0;
+    for (int i = 1; i < pk.n; i++) if ((int)blockIdx.x >= pk.j[i].blk0) ji = i;
+    const gemv_job &J = pk.j[ji];
+    const int blk = blockIdx.x - J.blk0;
+    switch (J.fmt) {
+    case 0: run_job<0>(J, pk.T, blk, red); break;
+    case 2: run_job<2>(J, pk.T, blk, red); break;
+    default: run_job<3>(J, pk.T, blk, red); break;
+    }
+}
+
+static int waves_per_row(const whip_mat *A)
+{
+    // about UNROLL chunks per lane and at least one full pass of loads
+    const int ne = A->fmt == 0 ? 4 : A->fmt == 2 ? 16 : 32;
+    const int ng = A->fmt == 0 ? 1 : (A->cols + A->group - 1) / A->group;
+    const int padded = A->fmt == 0 ? A->cols : ng * A->group;
+    const int nchunk = (padded + ne - 1) / ne;
+    if (nchunk >= 64 * UNROLL * 4 && A->rows <= 1024) return 4;
+    if (nchunk >= 64 * UNROLL * 2 && A->rows <= 2048) return 2;
+    return 1;
+}
+
+static int check_mat(const whip_mat *A)
+{
+    if (A->fmt == 0) return (A->cols % 4 || A->rowbytes % 16) ? -1 : 0;
+    if (A->fmt != 2 && A->fmt != 3) return -1;
+    return (A->group % 32 || A->rowbytes % 16) ? -1 : 0;
+}
+
+extern "C" int whip_gemv_multi(const whip_gemv_job *jobs, int n, int T, hipStream_t s)
+{
+    if (n < 1 || n > 3 || T < 1) return (int)hipErrorInvalidValue;
+    gemv_pack pk;
+    int blk = 0;
+    for (int i = 0; i < n; i++) {
+        const whip_gemv_job *q = &jobs[i];
+        if (check_mat(&q->A) || (q->B && (q->B->fmt != q->A.fmt || q->B->rows != q->A.rows ||
+                                          q->B->cols != q->A.cols || q->B->group != q->A.group ||
+                                          q->B->rowbytes != q->A.rowbytes)))
+            return (int)hipErrorInvalidValue;
+        if (q->x_ld % 4) return (int)hipErrorInvalidValue;
+        gemv_job &J = pk.j[i];
+        J.W0 = (const uint8_t *)q->A.q; J.S0 = q->A.qs;
+        J.W1 = q->B ? (const uint8_t *)q->B->q : nullptr; J.S1 = q->B ? q->B->qs : nullptr;
+        J.rowbytes = q->A.rowbytes; J.fmt = q->A.fmt; J.rows = q->A.rows; J.cols = q->A.cols;
+        J.group = q->A.group; J.x = q->x; J.x_ld = q->x_ld; J.x_bf16 = q->x_bf16;
+        J.y = q->y; J.y_ld = q->y_ld;
+        J.wpr = waves_per_row(&q->A);
+        J.blk0 = blk;
+        J.nblk = (J.rows + (4 / J.wpr) - 1) / (4 / J.wpr);
+        blk += J.nblk;
+    }
+    pk.n = n;
+    pk.T = T;
+    hipLaunchKernelGGL(k_gemv_multi, dim3(blk), dim3(256), 0, s, pk);
+    return (int)hipGetLastError();
 }
 
 extern "C" int whip_gemv(const whip_mat *A, const whip_mat *B, const float *x, int x_ld, int T,
                          float *y0, float *y1, int y_ld, hipStream_t s)
 {
-    if (B && (B->fmt != A->fmt || B->rows != A->rows || B->cols != A->cols || B->group != A->group))
-        return (int)hipErrorInvalidValue;
-    if (A->fmt == 0 && (A->cols % 4 || A->rowbytes % 16)) return (int)hipErrorInvalidValue;
-    if (A->fmt != 0 && (A->group % 32 || A->rowbytes % 16)) return (int)hipErrorInvalidValue;
-    if (x_ld % 4) return (int)hipErrorInvalidValue;
-    dim3 grid((A->rows + 3) / 4, B ? 2 : 1);
-    const uint8_t *w1 = B ? (const uint8_t *)B->q : nullptr;
-    const uint16_t *s1 = B ? B->qs : nullptr;
-    const size_t rb1 = B ? B->rowbytes : 0;
-#define GEMV_LAUNCH(F)                                                                       \
-    hipLaunchKernelGGL(k_gemv<F>, grid, dim3(256), 0, s, (const uint8_t *)A->q, A->qs,       \
-                       A->rowbytes, w1, s1, rb1, A->rows, A->cols, A->group, x, x_ld, T, y0, \
-                       y1, y_ld)
-    switch (A->fmt) {
-    case 0: GEMV_LAUNCH(0); break;
-    case 2: GEMV_LAUNCH(2); break;
-    case 3: GEMV_LAUNCH(3); break;
-    default: return (int)hipErrorInvalidValue;
+    whip_gemv_job j[2];
+    int n = 0;
+    j[n].A = *A; j[n].B = NULL; j[n].x = x; j[n].x_ld = x_ld; j[n].x_bf16 = 0; j[n].y = y0;
+    j[n].y_ld = y_ld; n++;
+    if (B) {
+        j[n].A = *B; j[n].B = NULL; j[n].x = x; j[n].x_ld = x_ld; j[n].x_bf16 = 0; j[n].y = y1;
+        j[n].y_ld = y_ld; n++;
     }
-#undef GEMV_LAUNCH
-    return (int)hipGetLastError();
-}
-
-__global__ void k_bf16_to_f32(const uint16_t *__restrict__ x, float *__restrict__ y, size_t n)
-{
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) y[i] = wh_bf16(x[i]);
-}
-
-extern "C" int whip_bf16_to_f32(const uint16_t *x, float *y, size_t n, hipStream_t s)
-{
-    hipLaunchKernelGGL(k_bf16_to_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, y, n);
-    return (int)hipGetLastError();
+    return whip_gemv_multi(j, n, T, s);
 }

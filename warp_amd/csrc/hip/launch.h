@@ -29,6 +29,18 @@ typedef struct {
 int whip_gemv(const whip_mat *W0, const whip_mat *W1, const float *x, int x_ld,
               int T, float *y0, float *y1, int y_ld, hipStream_t s);
 
+/* Up to three independent products in one launch.  With B set, the job is
+ * a SwiGLU pair: y = silu(A.x) * (B.x).  x is fp32 or bf16 (x_bf16). */
+typedef struct {
+    whip_mat A;
+    const whip_mat *B;
+    const void *x;
+    int x_ld, x_bf16;
+    float *y;
+    int y_ld;
+} whip_gemv_job;
+int whip_gemv_multi(const whip_gemv_job *jobs, int n, int T, hipStream_t s);
+
 /* Routing, one wavefront per token: scores, group limit, top-k with the
  * engine's tie rule, renormalisation, scaling.  When T == 1 it also lays
  * out the pair list (selection order) that the expert kernels walk. */
@@ -55,8 +67,8 @@ typedef struct {
     const uint8_t *const *recs;      /* [E] record bases, NULL if unbound   */
     const int32_t *pair_exp;         /* [P]                                 */
     const int32_t *pair_src;         /* [P] row of src; NULL = p            */
-    const float *src;
-    int src_ld;
+    const void *src;                 /* fp32, or bf16 when src_bf16         */
+    int src_ld, src_bf16;
     const float *booksT;             /* [n_books][8][256] fp32              */
     int cb;                          /* first book of kind 0                */
     uint32_t idx_off[2];             /* byte offset of kind k's indices     */
@@ -67,12 +79,11 @@ typedef struct {
 int whip_vq_apply(const whip_vq_args *a, hipStream_t s);
 int whip_vq_chunks(int nv);          /* nch for a given nv                  */
 
-/* h[p*I + r] = silu(scale_g[r]*sum_c gpart) * (scale_u[r]*sum_c upart) for
- * the routed pairs, and h_sh[t*SI + r] = silu(a)*b for the shared expert. */
+/* h[p*I + r] = silu(scale_g[r]*sum_c gpart) * (scale_u[r]*sum_c upart)
+ * for the routed pairs. */
 int whip_vq_act(const uint8_t *const *recs, const int32_t *pair_exp, int P,
                 const float *part, int nch, int I, uint32_t sc_off, float *h,
-                const float *sh_a, const float *sh_b, int T, int SI,
-                float *h_sh, hipStream_t s);
+                hipStream_t s);
 
 /* y[t*H + i] = sum over token t's pairs (combine order) of
  *   w * (scale_d[i] * sum_c part_d) + sh[t*H + i] (sh may be NULL). */

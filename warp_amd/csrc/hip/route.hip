@@ -28,123 +28,169 @@ __device__ __forceinline__ bool better(float ov, int oe, float bv, int be)
     return oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be));
 }
 
+#define NPL 16                       // experts per lane: E <= 1024
+#define NEG_INF (-__int_as_float(0x7f800000))
+
+// top-2 of a multiset of values (NaN never counts, as in a strict-greater scan)
+__device__ __forceinline__ void top2_merge(float &a1, float &a2, float b1, float b2)
+{
+    const float hi = b1 > a1 ? b1 : a1;
+    const float lo = b1 > a1 ? a1 : b1;
+    const float r2 = b2 > a2 ? b2 : a2;
+    a1 = hi;
+    a2 = r2 > lo ? r2 : lo;
+}
+
 __global__ void __launch_bounds__(64)
 k_route(whip_route_cfg c, const float *__restrict__ logits, const float *__restrict__ bias,
         int T, int32_t *__restrict__ ids, float *__restrict__ wout, int32_t *__restrict__ pair_tok,
         int32_t *__restrict__ pair_exp, float *__restrict__ pair_w, int32_t *__restrict__ tok_pairs,
         int *__restrict__ err)
 {
-    __shared__ float sc[MAXE], sel[MAXE], gsc[64];
-    __shared__ float red;
-    __shared__ int keep[64];
-    __shared__ int sid[64];
-    __shared__ float sw[64];
+    __shared__ float lds[MAXE];
+    __shared__ float gsc[64];
     const int t = blockIdx.x, lane = threadIdx.x, E = c.E, K = c.K;
+    const int npl = (E + 63) >> 6;
     const float *lg = logits + (size_t)t * E;
+    float sc[NPL], sel[NPL];
 
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+        const int e = lane + 64 * i;
+        sc[i] = (i < npl && e < E) ? lg[e] : 0.0f;
+    }
     if (c.score_func == 1) {
         float mx = -1e30f;
-        for (int e = lane; e < E; e += 64) if (lg[e] > mx) mx = lg[e];
+#pragma unroll
+        for (int i = 0; i < NPL; i++)
+            if (i < npl && lane + 64 * i < E && sc[i] > mx) mx = sc[i];
         for (int o = 32; o > 0; o >>= 1) {
             const float m2 = __shfl_xor(mx, o, 64);
             if (m2 > mx) mx = m2;
         }
-        for (int e = lane; e < E; e += 64) sc[e] = wh_expf(__fsub_rn(lg[e], mx));
+#pragma unroll
+        for (int i = 0; i < NPL; i++)
+            if (i < npl && lane + 64 * i < E) {
+                sc[i] = wh_expf(__fsub_rn(sc[i], mx));
+                lds[lane + 64 * i] = sc[i];
+            }
         __syncthreads();
-        if (lane == 0) {
+        if (lane == 0) {                 // the engine's sum, in expert order
             float sum = 0.0f;
-            for (int e = 0; e < E; e++) sum = __fadd_rn(sum, sc[e]);
-            red = sum;
+            for (int e = 0; e < E; e++) sum = __fadd_rn(sum, lds[e]);
+            gsc[0] = sum;
         }
         __syncthreads();
-        const float sum = red;
-        for (int e = lane; e < E; e += 64) sc[e] = __fdiv_rn(sc[e], sum);
+        const float sum = gsc[0];
+#pragma unroll
+        for (int i = 0; i < NPL; i++) sc[i] = __fdiv_rn(sc[i], sum);
     } else if (c.score_func == 2) {
-        for (int e = lane; e < E; e += 64) {
-            const float x = lg[e];
+#pragma unroll
+        for (int i = 0; i < NPL; i++) {
+            const float x = sc[i];
             const float sp = x > 30.0f ? x : log1pf(wh_expf(x));
-            sc[e] = __fsqrt_rn(sp);
+            sc[i] = __fsqrt_rn(sp);
         }
     } else {
-        for (int e = lane; e < E; e += 64) sc[e] = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf(-lg[e])));
+#pragma unroll
+        for (int i = 0; i < NPL; i++) sc[i] = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf(-sc[i])));
     }
-    for (int e = lane; e < E; e += 64) sel[e] = __fadd_rn(sc[e], bias ? bias[e] : 0.0f);
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+        const int e = lane + 64 * i;
+        sel[i] = (i < npl && e < E) ? __fadd_rn(sc[i], bias ? bias[e] : 0.0f) : NEG_INF;
+    }
 
     if (c.n_group > 1) {
         const int G = c.n_group, gs = E / G;
-        if (lane < G) {
-            const float *p = sel + lane * gs;
-            int a = -1, b = -1;
-            float av = -__int_as_float(0x7f800000), bv2 = av;
-            for (int i = 0; i < gs; i++) if (p[i] > av) { av = p[i]; a = i; }
-            for (int i = 0; i < gs; i++) if (i != a && p[i] > bv2) { bv2 = p[i]; b = i; }
-            const float ninf = -__int_as_float(0x7f800000);
-            gsc[lane] = __fadd_rn(a >= 0 ? p[a] : ninf, b >= 0 ? p[b] : (gs > 1 ? ninf : 0.0f));
-            keep[lane] = 0;
-        }
-        __syncthreads();
-        if (lane == 0) {
-            unsigned long long taken = 0;
-            for (int j = 0; j < c.topk_group; j++) {
-                int best = -1;
-                float bv = -__int_as_float(0x7f800000);
-                for (int g = 0; g < G; g++)
-                    if (!((taken >> g) & 1) && gsc[g] > bv) { bv = gsc[g]; best = g; }
-                if (best < 0) break;
-                taken |= 1ull << best;
-                keep[best] = 1;
+        if (gs <= 64 && (64 % gs) == 0) {
+            // groups tile the wave: a segmented top-2 merge over gs lanes
+#pragma unroll
+            for (int i = 0; i < NPL; i++) {
+                if (i >= npl) break;
+                float a1 = sel[i] == sel[i] ? sel[i] : NEG_INF, a2 = NEG_INF;
+                for (int o = 1; o < gs; o <<= 1) {
+                    const float b1 = __shfl_xor(a1, o, 64), b2 = __shfl_xor(a2, o, 64);
+                    top2_merge(a1, a2, b1, b2);
+                }
+                const int e = lane + 64 * i;
+                if (e % gs == 0 && e < E) gsc[e / gs] = __fadd_rn(a1, gs > 1 ? a2 : 0.0f);
+            }
+        } else {
+            // wide groups: scan each group from LDS
+#pragma unroll
+            for (int i = 0; i < NPL; i++)
+                if (i < npl && lane + 64 * i < E) lds[lane + 64 * i] = sel[i];
+            __syncthreads();
+            if (lane < G) {
+                float a1 = NEG_INF, a2 = NEG_INF;
+                for (int k = 0; k < gs; k++) {
+                    const float v = lds[lane * gs + k];
+                    if (v == v) top2_merge(a1, a2, v, NEG_INF);
+                }
+                gsc[lane] = __fadd_rn(a1, gs > 1 ? a2 : 0.0f);
             }
         }
         __syncthreads();
-        for (int e = lane; e < E; e += 64) if (!keep[e / gs]) sel[e] = -__int_as_float(0x7f800000);
-        __syncthreads();
+        // keep topk_group groups: strict-greater passes, lowest index first
+        uint64_t keep = 0;
+        for (int j = 0; j < c.topk_group; j++) {
+            int best = -1;
+            float bv = NEG_INF;
+            for (int g = 0; g < G; g++)
+                if (!((keep >> g) & 1) && gsc[g] > bv) { bv = gsc[g]; best = g; }
+            if (best < 0) break;
+            keep |= 1ull << best;
+        }
+#pragma unroll
+        for (int i = 0; i < NPL; i++) {
+            const int e = lane + 64 * i;
+            if (i < npl && e < E && !((keep >> (e / gs)) & 1)) sel[i] = NEG_INF;
+        }
     }
 
-    uint32_t taken = 0;                 // bit i: expert lane + 64 i taken
+    // K selection passes; lane j keeps pass j's expert and weight
+    uint32_t taken = 0;
+    int my_id = -1;
+    float my_w = 0.0f;
     int bad = 0;
     for (int j = 0; j < K; j++) {
         float bv = -1e30f;
         int be = -1;
-        for (int i = 0, e = lane; e < E; i++, e += 64)
-            if (!((taken >> i) & 1) && sel[e] > bv) { bv = sel[e]; be = e; }
+        float bs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPL; i++)
+            if (i < npl && !((taken >> i) & 1) && sel[i] > bv) { bv = sel[i]; be = lane + 64 * i; bs = sc[i]; }
         for (int o = 32; o > 0; o >>= 1) {
             const float ov = __shfl_xor(bv, o, 64);
             const int oe = __shfl_xor(be, o, 64);
-            if (better(ov, oe, bv, be)) { bv = ov; be = oe; }
+            const float os = __shfl_xor(bs, o, 64);
+            if (better(ov, oe, bv, be)) { bv = ov; be = oe; bs = os; }
         }
-        if (be < 0) {
-            bad = 1;
-            if (lane == 0) { sid[j] = -1; sw[j] = 0.0f; }
-            continue;
-        }
+        if (be < 0) { bad = 1; continue; }
         if ((be & 63) == lane) taken |= 1u << (be >> 6);
-        if (lane == 0) { sid[j] = be; sw[j] = sc[be]; }
+        if (lane == j) { my_id = be; my_w = bs; }
     }
-    if (lane != 0) return;
-    int *myid = sid;
-    float *myw = sw;
     if (!bad) {
         if (c.renorm && K > 1) {
-            float s = 0.0f;
-            for (int j = 0; j < K; j++) s = __fadd_rn(s, myw[j]);
-            const float d = __fadd_rn(s, 1e-20f);
-            for (int j = 0; j < K; j++) myw[j] = __fdiv_rn(myw[j], d);
+            float s = 0.0f;                  // selection order
+            for (int j = 0; j < K; j++) s = __fadd_rn(s, __shfl(my_w, j, 64));
+            my_w = __fdiv_rn(my_w, __fadd_rn(s, 1e-20f));
         }
-        for (int j = 0; j < K; j++) myw[j] = __fmul_rn(myw[j], c.routed_scale);
+        my_w = __fmul_rn(my_w, c.routed_scale);
     } else {
-        atomicOr(err, 2);
+        my_id = -1;
+        my_w = 0.0f;
+        if (lane == 0) atomicOr(err, 2);
     }
-    for (int j = 0; j < K; j++) {
-        ids[(size_t)t * K + j] = myid[j];
-        wout[(size_t)t * K + j] = myw[j];
-    }
-    if (pair_exp && T == 1) {
-        for (int j = 0; j < K; j++) {
-            pair_tok[j] = 0;
-            pair_exp[j] = myid[j] < 0 ? E : myid[j];     // E: the table's NULL sentinel
-            pair_w[j] = myw[j];
-            tok_pairs[j] = j;
+    if (lane < K) {
+        ids[(size_t)t * K + lane] = my_id;
+        wout[(size_t)t * K + lane] = my_w;
+        if (pair_exp && T == 1) {
+            pair_tok[lane] = 0;
+            pair_exp[lane] = my_id < 0 ? E : my_id;    // E: the table's NULL sentinel
+            pair_w[lane] = my_w;
+            tok_pairs[lane] = lane;
         }
     }
 }

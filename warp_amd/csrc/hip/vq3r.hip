@@ -30,12 +30,32 @@
 
 extern "C" int whip_vq_chunks(int nv) { return (nv + VC - 1) / VC; }
 
+__device__ __forceinline__ void load_block(const uint8_t *pp, int vcount, uint32_t *wv)
+{
+#pragma unroll
+    for (int v = 0; v < VC; v++) wv[v] = v < vcount ? ld_u32_unaligned(pp + v * 192) : 0u;
+}
+
+__device__ __forceinline__ float apply_block(const float *lut, int vcount, const uint32_t *wv)
+{
+    float acc = 0.0f;
+#pragma unroll
+    for (int v = 0; v < VC; v++) {
+        if (v >= vcount) break;
+        const float *L = lut + v * LUT_PER_V;
+        const uint32_t w = wv[v];
+        const float t = (L[w & 255] + L[256 + ((w >> 8) & 255)]) + L[512 + ((w >> 16) & 255)];
+        acc += t;
+    }
+    return acc;
+}
+
 __device__ __forceinline__ void
 vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
-              const int32_t *__restrict__ pair_src, const float *__restrict__ src, int src_ld,
-              const float *__restrict__ booksT, int cb, uint32_t off0, uint32_t off1,
-              int kinds, int M, int nv, int nch, int rsplit, float *__restrict__ part,
-              int *__restrict__ err)
+              const int32_t *__restrict__ pair_src, const void *__restrict__ src, int src_ld,
+              int src_bf16, const float *__restrict__ booksT, int cb, uint32_t off0,
+              uint32_t off1, int kinds, int M, int nv, int nch, int rsplit,
+              float *__restrict__ part, int *__restrict__ err)
 {
     __shared__ float lut[VC * LUT_PER_V];
     __shared__ float xs[VC * 8];
@@ -53,9 +73,17 @@ vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict
         for (int r = rb_lo * 64 + tid; r < min(rb_hi * 64, M); r += blockDim.x) out[r] = 0.0f;
         return;
     }
+    // the first row block's indices are in flight while the table is built
+    const uint8_t *idx = rec + (kind ? off1 : off0) + (size_t)v0 * 192 + lane * 3;
+    uint32_t cur[VC], nxt[VC];
+    int rb = rb_lo + wave;
+    if (rb < rb_hi) load_block(idx + (size_t)rb * nv * 192, vcount, cur);
+
     const int srow = pair_src ? pair_src[p] : p;
-    const float *xv = src + (size_t)srow * src_ld + (size_t)v0 * 8;
-    if (tid < vcount * 8) xs[tid] = xv[tid];
+    if (tid < vcount * 8) {
+        const size_t o = (size_t)srow * src_ld + (size_t)v0 * 8 + tid;
+        xs[tid] = src_bf16 ? wh_bf16(((const uint16_t *)src)[o]) : ((const float *)src)[o];
+    }
     __syncthreads();
 
     // L[v][s][c] = fma chain over d from 0 (the engine's AVX-512 order).
@@ -77,31 +105,16 @@ vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict
     }
     __syncthreads();
 
-    const uint8_t *idx = rec + (kind ? off1 : off0);
-    for (int rb = rb_lo + wave; rb < rb_hi; rb += nw) {
-        const uint8_t *pp = idx + ((size_t)rb * nv + v0) * 192 + lane * 3;
-        float acc = 0.0f;
-        if (vcount == VC) {
-            uint32_t wv[VC];
-#pragma unroll
-            for (int v = 0; v < VC; v++) wv[v] = ld_u32_unaligned(pp + v * 192);
-#pragma unroll
-            for (int v = 0; v < VC; v++) {
-                const float *L = lut + v * LUT_PER_V;
-                const uint32_t w = wv[v];
-                const float t = (L[w & 255] + L[256 + ((w >> 8) & 255)]) + L[512 + ((w >> 16) & 255)];
-                acc += t;
-            }
-        } else {
-            for (int v = 0; v < vcount; v++) {
-                const float *L = lut + v * LUT_PER_V;
-                const uint32_t w = ld_u32_unaligned(pp + v * 192);
-                const float t = (L[w & 255] + L[256 + ((w >> 8) & 255)]) + L[512 + ((w >> 16) & 255)];
-                acc += t;
-            }
-        }
+    // two row blocks in flight per wavefront: the next one's loads are
+    // issued before the current one's lookups
+    for (; rb < rb_hi; rb += nw) {
+        const int rn = rb + nw;
+        if (rn < rb_hi) load_block(idx + (size_t)rn * nv * 192, vcount, nxt);
+        const float acc = apply_block(lut, vcount, cur);
         const int r = rb * 64 + lane;
         if (r < M) out[r] = acc;
+#pragma unroll
+        for (int v = 0; v < VC; v++) cur[v] = nxt[v];
     }
 }
 
@@ -110,12 +123,13 @@ vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict
 #define VQ_KERNEL(NAME)                                                                         \
     __global__ void __launch_bounds__(256)                                                      \
     NAME(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,         \
-         const int32_t *__restrict__ pair_src, const float *__restrict__ src, int src_ld,       \
-         const float *__restrict__ booksT, int cb, uint32_t off0, uint32_t off1, int kinds,     \
-         int M, int nv, int nch, int rsplit, float *__restrict__ part, int *__restrict__ err)   \
+         const int32_t *__restrict__ pair_src, const void *__restrict__ src, int src_ld,        \
+         int src_bf16, const float *__restrict__ booksT, int cb, uint32_t off0, uint32_t off1,  \
+         int kinds, int M, int nv, int nch, int rsplit, float *__restrict__ part,               \
+         int *__restrict__ err)                                                                 \
     {                                                                                           \
-        vq_apply_body(recs, pair_exp, pair_src, src, src_ld, booksT, cb, off0, off1, kinds, M,  \
-                      nv, nch, rsplit, part, err);                                              \
+        vq_apply_body(recs, pair_exp, pair_src, src, src_ld, src_bf16, booksT, cb, off0, off1,  \
+                      kinds, M, nv, nch, rsplit, part, err);                                    \
     }
 VQ_KERNEL(k_vq_gate_up)
 VQ_KERNEL(k_vq_down)
@@ -125,78 +139,142 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
     const int nch = whip_vq_chunks(a->nv);
     dim3 grid(nch, a->kinds * a->rsplit, a->P);
     hipLaunchKernelGGL(a->kinds == 2 ? k_vq_gate_up : k_vq_down, grid, dim3(256), 0, s, a->recs,
-                       a->pair_exp, a->pair_src, a->src, a->src_ld, a->booksT, a->cb,
+                       a->pair_exp, a->pair_src, a->src, a->src_ld, a->src_bf16, a->booksT, a->cb,
                        a->idx_off[0], a->idx_off[1], a->kinds, a->M, a->nv, nch, a->rsplit,
                        a->part, a->err);
     return (int)hipGetLastError();
 }
 
 // ---- SwiGLU over the reduced gate/up partials ------------------------------
+// A workgroup owns 128 rows of one pair: 32 float4 row groups x 8 slices of
+// the chunk range, so every thread has its whole slice's loads in flight;
+// the slices are then added in chunk order.
+#define ACT_ROWS 128
+#define ACT_SLICES 8
+
 __global__ void __launch_bounds__(256)
-k_vq_act(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp, int P,
-         const float *__restrict__ part, int nch, int I, uint32_t sc_off, float *__restrict__ h,
-         const float *__restrict__ sh_a, const float *__restrict__ sh_b, int SI,
-         float *__restrict__ h_sh)
+k_vq_act(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
+         const float *__restrict__ part, int nch, int I, uint32_t sc_off, float *__restrict__ h)
 {
-    const int p = blockIdx.y;
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (p < P) {
-        if (r >= I) return;
-        const uint8_t *rec = recs[pair_exp[p]];
-        const float *gp = part + ((size_t)p * 2 + 0) * nch * (size_t)I + r;
-        const float *up = part + ((size_t)p * 2 + 1) * nch * (size_t)I + r;
-        float g = 0.0f, u = 0.0f;
-        for (int c = 0; c < nch; c++) { g += gp[(size_t)c * I]; u += up[(size_t)c * I]; }
-        float sg = 0.0f, su = 0.0f;
+    __shared__ float4 red[2][ACT_SLICES][ACT_ROWS / 4];
+    const int p = blockIdx.y, tid = threadIdx.x;
+    const int g = tid & 31, sl = tid >> 5;
+    const int r0 = blockIdx.x * ACT_ROWS + g * 4;
+    const int per = (nch + ACT_SLICES - 1) / ACT_SLICES;
+    const int c0 = sl * per, c1 = min(nch, c0 + per);
+    float4 sg = make_float4(0, 0, 0, 0), su = sg;
+    if (r0 < I) {
+        const float *gp = part + ((size_t)p * 2 + 0) * nch * (size_t)I + r0;
+        const float *up = part + ((size_t)p * 2 + 1) * nch * (size_t)I + r0;
+        float4 vg[8], vu[8];
+        for (int cb = c0; cb < c1; cb += 8) {
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (cb + k < c1) {
+                    vg[k] = *(const float4 *)(gp + (size_t)(cb + k) * I);
+                    vu[k] = *(const float4 *)(up + (size_t)(cb + k) * I);
+                }
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (cb + k < c1) {
+                    sg.x += vg[k].x; sg.y += vg[k].y; sg.z += vg[k].z; sg.w += vg[k].w;
+                    su.x += vu[k].x; su.y += vu[k].y; su.z += vu[k].z; su.w += vu[k].w;
+                }
+        }
+    }
+    red[0][sl][g] = sg;
+    red[1][sl][g] = su;
+    __syncthreads();
+    if (tid >= 32 || r0 >= I) return;
+    float gg[4] = {0, 0, 0, 0}, uu[4] = {0, 0, 0, 0};
+    for (int k = 0; k < ACT_SLICES; k++) {
+        const float4 a = red[0][k][g], b = red[1][k][g];
+        gg[0] += a.x; gg[1] += a.y; gg[2] += a.z; gg[3] += a.w;
+        uu[0] += b.x; uu[1] += b.y; uu[2] += b.z; uu[3] += b.w;
+    }
+    const uint8_t *rec = recs[pair_exp[p]];
+    float out[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        float sgc = 0.0f, suc = 0.0f;
         if (rec) {
             const uint16_t *sc = (const uint16_t *)(rec + sc_off);
-            sg = wh_f16_scale(sc[r]);
-            su = wh_f16_scale(sc[I + r]);
+            sgc = wh_f16_scale(sc[r0 + q]);
+            suc = wh_f16_scale(sc[I + r0 + q]);
         }
-        h[(size_t)p * I + r] = wh_silu_mul(__fmul_rn(g, sg), __fmul_rn(u, su));
-    } else {
-        const int t = p - P;
-        if (r >= SI) return;
-        const size_t o = (size_t)t * SI + r;
-        h_sh[o] = wh_silu_mul(sh_a[o], sh_b[o]);
+        out[q] = wh_silu_mul(__fmul_rn(gg[q], sgc), __fmul_rn(uu[q], suc));
     }
+    *(float4 *)(h + (size_t)p * I + r0) = make_float4(out[0], out[1], out[2], out[3]);
 }
 
 extern "C" int whip_vq_act(const uint8_t *const *recs, const int32_t *pair_exp, int P,
                            const float *part, int nch, int I, uint32_t sc_off, float *h,
-                           const float *sh_a, const float *sh_b, int T, int SI,
-                           float *h_sh, hipStream_t s)
+                           hipStream_t s)
 {
-    const int rows = I > SI ? I : SI;
-    dim3 grid((rows + 255) / 256, P + (h_sh ? T : 0));
-    hipLaunchKernelGGL(k_vq_act, grid, dim3(256), 0, s, recs, pair_exp, P, part, nch, I, sc_off,
-                       h, sh_a, sh_b, SI, h_sh);
+    if (I % 4) return (int)hipErrorInvalidValue;
+    dim3 grid((I + ACT_ROWS - 1) / ACT_ROWS, P);
+    hipLaunchKernelGGL(k_vq_act, grid, dim3(256), 0, s, recs, pair_exp, part, nch, I, sc_off, h);
     return (int)hipGetLastError();
 }
 
 // ---- weighted combine + shared expert --------------------------------------
+// A workgroup owns 128 output rows of one token: thread (row group, pair
+// slot j) reduces pair j's chunk partials for 4 rows (all loads in flight)
+// and scales them; the pairs are then added in the token's combine order.
+#define CMB_ROWS 128
+
 __global__ void __launch_bounds__(256)
 k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
           const float *__restrict__ pair_w, const int32_t *__restrict__ tok_pairs, int K,
           const float *__restrict__ part_d, int nch, int H, uint32_t sc_off_down,
           int skip_zero, const float *__restrict__ sh, float *__restrict__ y)
 {
-    const int t = blockIdx.y;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= H) return;
-    float acc = 0.0f;
-    for (int j = 0; j < K; j++) {
+    extern __shared__ float4 cred[];                 // [K][32]
+    const int t = blockIdx.y, tid = threadIdx.x;
+    const int g = tid & 31;
+    const int r0 = blockIdx.x * CMB_ROWS + g * 4;
+    for (int j = tid >> 5; j < K; j += 8) {
+        float4 acc = make_float4(0, 0, 0, 0);
         const int p = tok_pairs[t * K + j];
         const float wj = pair_w[p];
-        if (skip_zero && wj == 0.0f) continue;
-        const uint8_t *rec = recs[pair_exp[p]];
-        const float *pd = part_d + (size_t)p * nch * H + i;
-        float s = 0.0f;
-        for (int c = 0; c < nch; c++) s += pd[(size_t)c * H];
-        const float sc = rec ? wh_f16_scale(((const uint16_t *)(rec + sc_off_down))[i]) : 0.0f;
-        acc = __fadd_rn(acc, __fmul_rn(wj, __fmul_rn(s, sc)));
+        if (r0 < H && !(skip_zero && wj == 0.0f)) {
+            const uint8_t *rec = recs[pair_exp[p]];
+            const float *pd = part_d + (size_t)p * nch * H + r0;
+            float4 s = make_float4(0, 0, 0, 0);
+            for (int cb = 0; cb < nch; cb += 8) {
+                float4 v[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if (cb + k < nch) v[k] = *(const float4 *)(pd + (size_t)(cb + k) * H);
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if (cb + k < nch) { s.x += v[k].x; s.y += v[k].y; s.z += v[k].z; s.w += v[k].w; }
+            }
+            if (rec) {
+                const uint16_t *sc = (const uint16_t *)(rec + sc_off_down) + r0;
+                acc.x = __fmul_rn(wj, __fmul_rn(s.x, wh_f16_scale(sc[0])));
+                acc.y = __fmul_rn(wj, __fmul_rn(s.y, wh_f16_scale(sc[1])));
+                acc.z = __fmul_rn(wj, __fmul_rn(s.z, wh_f16_scale(sc[2])));
+                acc.w = __fmul_rn(wj, __fmul_rn(s.w, wh_f16_scale(sc[3])));
+            }
+        }
+        cred[j * 32 + g] = acc;
     }
-    y[(size_t)t * H + i] = __fadd_rn(acc, sh ? sh[(size_t)t * H + i] : 0.0f);
+    __syncthreads();
+    if (tid >= 32 || r0 >= H) return;
+    float o[4] = {0, 0, 0, 0};
+    for (int j = 0; j < K; j++) {                    // combine order
+        const float4 a = cred[j * 32 + g];
+        o[0] = __fadd_rn(o[0], a.x); o[1] = __fadd_rn(o[1], a.y);
+        o[2] = __fadd_rn(o[2], a.z); o[3] = __fadd_rn(o[3], a.w);
+    }
+    float4 r;
+    const float *shr = sh ? sh + (size_t)t * H + r0 : nullptr;
+    r.x = __fadd_rn(o[0], shr ? shr[0] : 0.0f);
+    r.y = __fadd_rn(o[1], shr ? shr[1] : 0.0f);
+    r.z = __fadd_rn(o[2], shr ? shr[2] : 0.0f);
+    r.w = __fadd_rn(o[3], shr ? shr[3] : 0.0f);
+    *(float4 *)(y + (size_t)t * H + r0) = r;
 }
 
 extern "C" int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
@@ -204,9 +282,10 @@ extern "C" int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                             const float *part_d, int nch, int H, uint32_t sc_off_down,
                             int skip_zero, const float *sh, float *y, hipStream_t s)
 {
-    dim3 grid((H + 255) / 256, T);
-    hipLaunchKernelGGL(k_combine, grid, dim3(256), 0, s, recs, pair_exp, pair_w, tok_pairs, K,
-                       part_d, nch, H, sc_off_down, skip_zero, sh, y);
+    if (H % 4) return (int)hipErrorInvalidValue;
+    dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
+    hipLaunchKernelGGL(k_combine, grid, dim3(256), (size_t)K * 32 * sizeof(float4), s, recs,
+                       pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, sh, y);
     return (int)hipGetLastError();
 }
 

@@ -350,17 +350,20 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
         return WASTE_HIP_EINVAL;
     hipStream_t s = (hipStream_t)stream;
     const int E = m->E, K = m->K, H = m->H, I = m->I, P = T * K;
-    const float *xf = (const float *)x;
 #define MARK(i) do { if (m->prof_on) CK(hipEventRecord(m->ev[i], s)); } while (0)
     MARK(0);
-    if (x_bf16) {
-        CK((hipError_t)whip_bf16_to_f32((const uint16_t *)x, m->xf, (size_t)T * H, s));
-        xf = m->xf;
-    }
-    MARK(1);
+    /* router logits and the shared expert's silu(gate.x)*(up.x): one launch */
     float *lg = logits ? logits : m->logits;
-    CK((hipError_t)whip_gemv(&m->router, NULL, xf, H, T, lg, NULL, E, s));
-    MARK(2);
+    whip_gemv_job jobs[2];
+    int nj = 0;
+    jobs[nj].A = m->router; jobs[nj].B = NULL; jobs[nj].x = x; jobs[nj].x_ld = H;
+    jobs[nj].x_bf16 = x_bf16; jobs[nj].y = lg; jobs[nj].y_ld = E; nj++;
+    if (m->has_shared) {
+        jobs[nj].A = m->sh[0]; jobs[nj].B = &m->sh[1]; jobs[nj].x = x; jobs[nj].x_ld = H;
+        jobs[nj].x_bf16 = x_bf16; jobs[nj].y = m->h_sh; jobs[nj].y_ld = m->SI; nj++;
+    }
+    CK((hipError_t)whip_gemv_multi(jobs, nj, T, s));
+    MARK(1);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
     int32_t *d_ids = ids ? ids : m->ids;
@@ -370,35 +373,32 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     if (T > 1)
         CK((hipError_t)whip_pairs(d_ids, d_w, T, K, E, m->pair_tok, m->pair_exp, m->pair_w,
                                   m->tok_pairs, s));
-    MARK(3);
-    if (m->has_shared)
-        CK((hipError_t)whip_gemv(&m->sh[0], &m->sh[1], xf, H, T, m->sh_a, m->sh_b, m->SI, s));
-    MARK(4);
+    MARK(2);
 
     whip_vq_args a;
     memset(&a, 0, sizeof a);
     a.recs = m->d_recs; a.pair_exp = m->pair_exp; a.pair_src = m->pair_tok;
-    a.src = xf; a.src_ld = H; a.booksT = m->d_booksT; a.cb = m->cb;
+    a.src = x; a.src_ld = H; a.src_bf16 = x_bf16; a.booksT = m->d_booksT; a.cb = m->cb;
     a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.kinds = 2; a.M = I; a.nv = m->nv_gu; a.P = P; a.rsplit = m->rsplit_gu;
     a.part = m->part_gu; a.err = m->err;
     CK((hipError_t)whip_vq_apply(&a, s));
-    MARK(5);
+    MARK(3);
     CK((hipError_t)whip_vq_act(m->d_recs, m->pair_exp, P, m->part_gu, m->nch_gu, I, m->off_sc,
-                               m->h, m->sh_a, m->sh_b, T, m->SI, m->has_shared ? m->h_sh : NULL, s));
-    a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.cb = m->cb + 6;
+                               m->h, s));
+    MARK(4);
+    a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb + 6;
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
-    MARK(6);
     a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
     CK((hipError_t)whip_vq_apply(&a, s));
-    MARK(7);
+    MARK(5);
     if (m->has_shared)
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
-    MARK(8);
+    MARK(6);
     CK((hipError_t)whip_combine(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
                                 m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1,
                                 m->has_shared ? m->sh_out : NULL, y, s));
-    MARK(9);
+    MARK(7);
 #undef MARK
     if (m->prof_on) {
         CK(hipEventSynchronize(m->ev[WASTE_HIP_STAGES]));
