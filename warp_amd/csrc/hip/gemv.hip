@@ -27,26 +27,6 @@ template <> struct chunk_of<0> { static constexpr int NE = 4; };
 template <> struct chunk_of<2> { static constexpr int NE = 16; };
 template <> struct chunk_of<3> { static constexpr int NE = 32; };
 
-template <int FMT>
-__device__ __forceinline__ void decode_chunk(const uint4 v, float *w)
-{
-    const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-    if (FMT == 0) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) w[i] = __uint_as_float(u[i]);
-    } else if (FMT == 2) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) w[i] = (float)(int8_t)((u[i >> 2] >> ((i & 3) * 8)) & 0xff);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t b = (u[i >> 2] >> ((i & 3) * 8)) & 0xff;
-            w[2 * i] = (float)((int)(b & 15) - 8);
-            w[2 * i + 1] = (float)((int)(b >> 4) - 8);
-        }
-    }
-}
-
 // n activations starting at element e of token row xr (fp32 or bf16)
 template <int N>
 __device__ __forceinline__ void load_x(const void *xr, int bf16, int e, float *x)
@@ -85,8 +65,9 @@ struct gemv_pack {
     int n, T;
 };
 
-// partial dot products of one wavefront's share of row r, for TB tokens
-template <int FMT>
+// partial dot products of one wavefront's share of row r, for TBT tokens;
+// a chunk is decoded eight weights at a time to keep registers low
+template <int FMT, int TBT>
 __device__ __forceinline__ void row_partial(const gemv_job &J, const uint8_t *W, const uint16_t *S,
                                             int r, int part, int lane, int t0, int tn, float *acc)
 {
@@ -97,6 +78,7 @@ __device__ __forceinline__ void row_partial(const gemv_job &J, const uint8_t *W,
     const uint8_t *row = W + (size_t)r * J.rowbytes;
     const uint16_t *sr = FMT == 0 ? nullptr : S + (size_t)r * ng;
     const int stride = 64 * J.wpr;
+    const size_t xstride = (size_t)J.x_ld * (J.x_bf16 ? 2 : 4);
     for (int k0 = part * 64 + lane; k0 < nchunk; k0 += stride * UNROLL) {
         uint4 raw[UNROLL];
 #pragma unroll
@@ -108,49 +90,77 @@ __device__ __forceinline__ void row_partial(const gemv_job &J, const uint8_t *W,
         for (int u = 0; u < UNROLL; u++) {
             const int k = k0 + u * stride;
             if (k >= nchunk) break;
-            float w[NE];
-            decode_chunk<FMT>(raw[u], w);
             const int e0 = k * NE;
             const float sc = FMT == 0 ? 1.0f : wh_f16_scale(sr[e0 / J.group]);
+            const uint32_t uw[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+            float part_t[TBT];
 #pragma unroll
-            for (int t = 0; t < TB; t++) {
-                if (t >= tn) break;
-                const uint8_t *xr = (const uint8_t *)J.x + (size_t)(t0 + t) * J.x_ld * (J.x_bf16 ? 2 : 4);
-                float part_t = 0.0f;
-                if (e0 + NE <= J.cols) {
-                    float xv[NE];
-                    load_x<NE>(xr, J.x_bf16, e0, xv);
+            for (int t = 0; t < TBT; t++) part_t[t] = 0.0f;
 #pragma unroll
-                    for (int i = 0; i < NE; i++) part_t = __fmaf_rn(w[i], xv[i], part_t);
+            for (int sub = 0; sub < (NE + 7) / 8; sub++) {
+                constexpr int SN = NE < 8 ? NE : 8;
+                float w[SN];
+                if (FMT == 0) {
+#pragma unroll
+                    for (int i = 0; i < SN; i++) w[i] = __uint_as_float(uw[i]);
+                } else if (FMT == 2) {
+#pragma unroll
+                    for (int i = 0; i < SN; i++) {
+                        const int q = sub * 8 + i;
+                        w[i] = (float)(int8_t)((uw[q >> 2] >> ((q & 3) * 8)) & 0xff);
+                    }
                 } else {
-                    for (int i = 0; i < NE && e0 + i < J.cols; i++) {
-                        const float xi = J.x_bf16 ? wh_bf16(((const uint16_t *)xr)[e0 + i])
-                                                  : ((const float *)xr)[e0 + i];
-                        part_t = __fmaf_rn(w[i], xi, part_t);
+#pragma unroll
+                    for (int i = 0; i < SN; i += 2) {
+                        const int q = (sub * 8 + i) >> 1;
+                        const uint32_t b = (uw[q >> 2] >> ((q & 3) * 8)) & 0xff;
+                        w[i] = (float)((int)(b & 15) - 8);
+                        w[i + 1] = (float)((int)(b >> 4) - 8);
                     }
                 }
-                acc[t] = __fmaf_rn(sc, part_t, acc[t]);
+                const int es = e0 + sub * 8;
+#pragma unroll
+                for (int t = 0; t < TBT; t++) {
+                    if (t >= tn) break;
+                    const uint8_t *xr = (const uint8_t *)J.x + (size_t)(t0 + t) * xstride;
+                    if (es + SN <= J.cols) {
+                        float xv[SN];
+                        load_x<SN>(xr, J.x_bf16, es, xv);
+#pragma unroll
+                        for (int i = 0; i < SN; i++) part_t[t] = __fmaf_rn(w[i], xv[i], part_t[t]);
+                    } else {
+                        for (int i = 0; i < SN && es + i < J.cols; i++) {
+                            const float xi = J.x_bf16 ? wh_bf16(((const uint16_t *)xr)[es + i])
+                                                      : ((const float *)xr)[es + i];
+                            part_t[t] = __fmaf_rn(w[i], xi, part_t[t]);
+                        }
+                    }
+                }
             }
+#pragma unroll
+            for (int t = 0; t < TBT; t++) acc[t] = __fmaf_rn(sc, part_t[t], acc[t]);
         }
     }
 }
 
-template <int FMT>
-__device__ void run_job(const gemv_job &J, int T, int blk, float (*red)[2][TB])
+template <int FMT, int TBT>
+__device__ __forceinline__ void run_job(const gemv_job &J, int T, int blk, float (*red)[2][TB])
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rows_per_blk = 4 / J.wpr;
     const int r = blk * rows_per_blk + wave / J.wpr, part = wave % J.wpr;
     const bool live = r < J.rows;
-    for (int t0 = 0; t0 < T; t0 += TB) {
-        const int tn = min(TB, T - t0);
-        float a0[TB] = {0.0f, 0.0f, 0.0f, 0.0f}, a1[TB] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t0 = 0; t0 < T; t0 += TBT) {
+        const int tn = min(TBT, T - t0);
+        float a0[TBT], a1[TBT];
+#pragma unroll
+        for (int t = 0; t < TBT; t++) { a0[t] = 0.0f; a1[t] = 0.0f; }
         if (live) {
-            row_partial<FMT>(J, J.W0, J.S0, r, part, lane, t0, tn, a0);
-            if (J.W1) row_partial<FMT>(J, J.W1, J.S1, r, part, lane, t0, tn, a1);
+            row_partial<FMT, TBT>(J, J.W0, J.S0, r, part, lane, t0, tn, a0);
+            if (J.W1) row_partial<FMT, TBT>(J, J.W1, J.S1, r, part, lane, t0, tn, a1);
         }
 #pragma unroll
-        for (int t = 0; t < TB; t++) {
+        for (int t = 0; t < TBT; t++) {
             a0[t] = wave_sum(a0[t]);
             a1[t] = wave_sum(a1[t]);
         }
@@ -158,34 +168,43 @@ __device__ void run_job(const gemv_job &J, int T, int blk, float (*red)[2][TB])
             __syncthreads();
             if (lane == 0)
 #pragma unroll
-                for (int t = 0; t < TB; t++) { red[wave][0][t] = a0[t]; red[wave][1][t] = a1[t]; }
+                for (int t = 0; t < TBT; t++) { red[wave][0][t] = a0[t]; red[wave][1][t] = a1[t]; }
             __syncthreads();
             if (part == 0 && lane == 0)
 #pragma unroll
-                for (int t = 0; t < TB; t++) {
+                for (int t = 0; t < TBT; t++) {
                     float s0 = red[wave][0][t], s1 = red[wave][1][t];
                     for (int q = 1; q < J.wpr; q++) { s0 += red[wave + q][0][t]; s1 += red[wave + q][1][t]; }
                     a0[t] = s0; a1[t] = s1;
                 }
         }
         if (live && part == 0 && lane == 0)
-            for (int t = 0; t < tn; t++)
-                J.y[(size_t)(t0 + t) * J.y_ld + r] = J.W1 ? wh_silu_mul(a0[t], a1[t]) : a0[t];
+#pragma unroll
+            for (int t = 0; t < TBT; t++)
+                if (t < tn)
+                    J.y[(size_t)(t0 + t) * J.y_ld + r] = J.W1 ? wh_silu_mul(a0[t], a1[t]) : a0[t];
     }
 }
 
+template <int TBT>
 __global__ void __launch_bounds__(256) k_gemv_multi(gemv_pack pk)
 {
     __shared__ float red[4][2][TB];
-    int ji = 0;
-    for (int i = 1; i < pk.n; i++) if ((int)blockIdx.x >= pk.j[i].blk0) ji = i;
-    const gemv_job &J = pk.j[ji];
-    const int blk = blockIdx.x - J.blk0;
-    switch (J.fmt) {
-    case 0: run_job<0>(J, pk.T, blk, red); break;
-    case 2: run_job<2>(J, pk.T, blk, red); break;
-    default: run_job<3>(J, pk.T, blk, red); break;
-    }
+    const int b = blockIdx.x;
+    // the job is copied field by field from the argument block: a reference
+    // into it, or a whole-struct select, would put the block in scratch
+    const int ji = (pk.n > 2 && b >= pk.j[2].blk0) ? 2 : (pk.n > 1 && b >= pk.j[1].blk0) ? 1 : 0;
+#define SEL(f) (ji == 2 ? pk.j[2].f : ji == 1 ? pk.j[1].f : pk.j[0].f)
+    gemv_job J;
+    J.W0 = SEL(W0); J.W1 = SEL(W1); J.S0 = SEL(S0); J.S1 = SEL(S1); J.rowbytes = SEL(rowbytes);
+    J.fmt = SEL(fmt); J.rows = SEL(rows); J.cols = SEL(cols); J.group = SEL(group);
+    J.x = SEL(x); J.x_ld = SEL(x_ld); J.x_bf16 = SEL(x_bf16); J.y = SEL(y); J.y_ld = SEL(y_ld);
+    J.wpr = SEL(wpr); J.blk0 = SEL(blk0); J.nblk = SEL(nblk);
+#undef SEL
+    const int blk = b - J.blk0;
+    if (J.fmt == 0) run_job<0, TBT>(J, pk.T, blk, red);
+    else if (J.fmt == 2) run_job<2, TBT>(J, pk.T, blk, red);
+    else run_job<3, TBT>(J, pk.T, blk, red);
 }
 
 static int waves_per_row(const whip_mat *A)
@@ -232,7 +251,8 @@ extern "C" int whip_gemv_multi(const whip_gemv_job *jobs, int n, int T, hipStrea
     }
     pk.n = n;
     pk.T = T;
-    hipLaunchKernelGGL(k_gemv_multi, dim3(blk), dim3(256), 0, s, pk);
+    if (T == 1) hipLaunchKernelGGL(k_gemv_multi<1>, dim3(blk), dim3(256), 0, s, pk);
+    else hipLaunchKernelGGL(k_gemv_multi<TB>, dim3(blk), dim3(256), 0, s, pk);
     return (int)hipGetLastError();
 }
 

@@ -28,7 +28,6 @@ __device__ __forceinline__ bool better(float ov, int oe, float bv, int be)
     return oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be));
 }
 
-#define NPL 16                       // experts per lane: E <= 1024
 #define NEG_INF (-__int_as_float(0x7f800000))
 
 // top-2 of a multiset of values (NaN never counts, as in a strict-greater scan)
@@ -41,6 +40,10 @@ __device__ __forceinline__ void top2_merge(float &a1, float &a2, float b1, float
     a2 = r2 > lo ? r2 : lo;
 }
 
+// NPL experts per lane (E <= 64 * NPL), a template so that the unrolled
+// per-lane loops hold only what the layer's E needs: the kernel runs once
+// per token on a cold instruction cache.
+template <int NPL>
 __global__ void __launch_bounds__(64)
 k_route(whip_route_cfg c, const float *__restrict__ logits, const float *__restrict__ bias,
         int T, int32_t *__restrict__ ids, float *__restrict__ wout, int32_t *__restrict__ pair_tok,
@@ -202,8 +205,16 @@ extern "C" int whip_route(const whip_route_cfg *c, const float *logits, const fl
     if (c->E > MAXE || c->E <= 0 || c->K <= 0 || c->K > 64 || c->K > c->E) return (int)hipErrorInvalidValue;
     if (c->n_group > 1 && (c->n_group > 64 || c->E % c->n_group || c->topk_group < 1))
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_route, dim3(T), dim3(64), 0, s, *c, logits, bias, T, ids, w, pair_tok,
-                       pair_exp, pair_w, tok_pairs, err);
+#define ROUTE_LAUNCH(N)                                                                        \
+    hipLaunchKernelGGL(k_route<N>, dim3(T), dim3(64), 0, s, *c, logits, bias, T, ids, w, pair_tok, \
+                       pair_exp, pair_w, tok_pairs, err)
+    const int npl = (c->E + 63) / 64;
+    if (npl <= 1) ROUTE_LAUNCH(1);
+    else if (npl <= 2) ROUTE_LAUNCH(2);
+    else if (npl <= 4) ROUTE_LAUNCH(4);
+    else if (npl <= 8) ROUTE_LAUNCH(8);
+    else ROUTE_LAUNCH(16);
+#undef ROUTE_LAUNCH
     return (int)hipGetLastError();
 }
 

@@ -120,8 +120,9 @@ vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict
 
 // Two symbols for one body, so that profiles tell the gate/up pass (two
 // kinds per pair, the hidden-wide tables) from the down pass.
+#define VQ_THREADS 512
 #define VQ_KERNEL(NAME)                                                                         \
-    __global__ void __launch_bounds__(256)                                                      \
+    __global__ void __launch_bounds__(VQ_THREADS)                                               \
     NAME(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,         \
          const int32_t *__restrict__ pair_src, const void *__restrict__ src, int src_ld,        \
          int src_bf16, const float *__restrict__ booksT, int cb, uint32_t off0, uint32_t off1,  \
@@ -138,7 +139,7 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
 {
     const int nch = whip_vq_chunks(a->nv);
     dim3 grid(nch, a->kinds * a->rsplit, a->P);
-    hipLaunchKernelGGL(a->kinds == 2 ? k_vq_gate_up : k_vq_down, grid, dim3(256), 0, s, a->recs,
+    hipLaunchKernelGGL(a->kinds == 2 ? k_vq_gate_up : k_vq_down, grid, dim3(VQ_THREADS), 0, s, a->recs,
                        a->pair_exp, a->pair_src, a->src, a->src_ld, a->src_bf16, a->booksT, a->cb,
                        a->idx_off[0], a->idx_off[1], a->kinds, a->M, a->nv, nch, a->rsplit,
                        a->part, a->err);

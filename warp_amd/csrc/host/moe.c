@@ -118,9 +118,9 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
 static int pick_rsplit(int work_groups, int row_blocks)
 {
     /* enough workgroups to cover 256 CUs a few times, at least one row
-     * block per wavefront of a 4-wave workgroup */
-    int r = (1024 + work_groups - 1) / (work_groups > 0 ? work_groups : 1);
-    const int cap = row_blocks / 4 > 0 ? row_blocks / 4 : 1;
+     * block per wavefront of an 8-wave workgroup */
+    int r = (768 + work_groups - 1) / (work_groups > 0 ? work_groups : 1);
+    const int cap = row_blocks / 8 > 0 ? row_blocks / 8 : 1;
     if (r > cap) r = cap;
     return r < 1 ? 1 : r;
 }
