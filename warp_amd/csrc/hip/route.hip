@@ -23,177 +23,139 @@
 
 #define MAXE 1024
 
-__device__ __forceinline__ bool better(float ov, int oe, float bv, int be)
-{
-    return oe >= 0 && (be < 0 || ov > bv || (ov == bv && oe < be));
-}
-
 #define NEG_INF (-__int_as_float(0x7f800000))
 
-// top-2 of a multiset of values (NaN never counts, as in a strict-greater scan)
-__device__ __forceinline__ void top2_merge(float &a1, float &a2, float b1, float b2)
+// (a, ea) precedes (b, eb) in the engine's selection order: larger value
+// first, the lower id among equal values (a strict-greater scan keeps the
+// first maximum it meets).
+__device__ __forceinline__ bool before(float a, int ea, float b, int eb)
 {
-    const float hi = b1 > a1 ? b1 : a1;
-    const float lo = b1 > a1 ? a1 : b1;
-    const float r2 = b2 > a2 ? b2 : a2;
-    a1 = hi;
-    a2 = r2 > lo ? r2 : lo;
+    return a > b || (a == b && ea < eb);
 }
 
-// NPL experts per lane (E <= 64 * NPL), a template so that the unrolled
-// per-lane loops hold only what the layer's E needs: the kernel runs once
-// per token on a cold instruction cache.
-template <int NPL>
-__global__ void __launch_bounds__(64)
+// One workgroup per token, one thread per expert.  K strict-greater passes
+// select, in order, the experts that come first under `before`; so expert e
+// is selected in pass j exactly when j experts precede it, and this kernel
+// computes that rank directly, every thread against the table in LDS
+// (broadcast reads), instead of running K dependent reductions.
+__global__ void __launch_bounds__(1024)
 k_route(whip_route_cfg c, const float *__restrict__ logits, const float *__restrict__ bias,
         int T, int32_t *__restrict__ ids, float *__restrict__ wout, int32_t *__restrict__ pair_tok,
         int32_t *__restrict__ pair_exp, float *__restrict__ pair_w, int32_t *__restrict__ tok_pairs,
         int *__restrict__ err)
 {
-    __shared__ float lds[MAXE];
-    __shared__ float gsc[64];
-    const int t = blockIdx.x, lane = threadIdx.x, E = c.E, K = c.K;
-    const int npl = (E + 63) >> 6;
+    __shared__ float s_sel[MAXE], s_tmp[MAXE];
+    __shared__ float s_g1[64], s_g2[64], s_g[64];
+    __shared__ int s_id[64], s_ncand;
+    __shared__ float s_w[64], s_red;
+    const int t = blockIdx.x, e = threadIdx.x, E = c.E, K = c.K;
+    const bool valid = e < E;
     const float *lg = logits + (size_t)t * E;
-    float sc[NPL], sel[NPL];
+    const float l = valid ? lg[e] : 0.0f;
+    if (e == 0) s_ncand = 0;
 
-#pragma unroll
-    for (int i = 0; i < NPL; i++) {
-        const int e = lane + 64 * i;
-        sc[i] = (i < npl && e < E) ? lg[e] : 0.0f;
-    }
+    float sc;
     if (c.score_func == 1) {
-        float mx = -1e30f;
-#pragma unroll
-        for (int i = 0; i < NPL; i++)
-            if (i < npl && lane + 64 * i < E && sc[i] > mx) mx = sc[i];
-        for (int o = 32; o > 0; o >>= 1) {
-            const float m2 = __shfl_xor(mx, o, 64);
-            if (m2 > mx) mx = m2;
-        }
-#pragma unroll
-        for (int i = 0; i < NPL; i++)
-            if (i < npl && lane + 64 * i < E) {
-                sc[i] = wh_expf(__fsub_rn(sc[i], mx));
-                lds[lane + 64 * i] = sc[i];
+        // max (order-free), then the engine's sequential sum
+        s_tmp[e] = valid ? l : -1e30f;
+        __syncthreads();
+        if (e < 64) {
+            float mx = -1e30f;
+            for (int k = e; k < E; k += 64) if (s_tmp[k] > mx) mx = s_tmp[k];
+            for (int o = 32; o > 0; o >>= 1) {
+                const float m2 = __shfl_xor(mx, o, 64);
+                if (m2 > mx) mx = m2;
             }
+            if (e == 0) s_red = mx;
+        }
         __syncthreads();
-        if (lane == 0) {                 // the engine's sum, in expert order
+        const float ex = valid ? wh_expf(__fsub_rn(l, s_red)) : 0.0f;
+        __syncthreads();
+        s_tmp[e] = ex;
+        __syncthreads();
+        if (e == 0) {
             float sum = 0.0f;
-            for (int e = 0; e < E; e++) sum = __fadd_rn(sum, lds[e]);
-            gsc[0] = sum;
+            for (int k = 0; k < E; k++) sum = __fadd_rn(sum, s_tmp[k]);
+            s_red = sum;
         }
         __syncthreads();
-        const float sum = gsc[0];
-#pragma unroll
-        for (int i = 0; i < NPL; i++) sc[i] = __fdiv_rn(sc[i], sum);
+        sc = __fdiv_rn(ex, s_red);
     } else if (c.score_func == 2) {
-#pragma unroll
-        for (int i = 0; i < NPL; i++) {
-            const float x = sc[i];
-            const float sp = x > 30.0f ? x : log1pf(wh_expf(x));
-            sc[i] = __fsqrt_rn(sp);
-        }
+        const float sp = l > 30.0f ? l : log1pf(wh_expf(l));
+        sc = __fsqrt_rn(sp);
     } else {
-#pragma unroll
-        for (int i = 0; i < NPL; i++) sc[i] = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf(-sc[i])));
+        sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf(-l)));
     }
-#pragma unroll
-    for (int i = 0; i < NPL; i++) {
-        const int e = lane + 64 * i;
-        sel[i] = (i < npl && e < E) ? __fadd_rn(sc[i], bias ? bias[e] : 0.0f) : NEG_INF;
-    }
+    float sel = valid ? __fadd_rn(sc, bias ? bias[e] : 0.0f) : NEG_INF;
+    s_sel[e] = sel;
+    __syncthreads();
 
     if (c.n_group > 1) {
-        const int G = c.n_group, gs = E / G;
-        if (gs <= 64 && (64 % gs) == 0) {
-            // groups tile the wave: a segmented top-2 merge over gs lanes
-#pragma unroll
-            for (int i = 0; i < NPL; i++) {
-                if (i >= npl) break;
-                float a1 = sel[i] == sel[i] ? sel[i] : NEG_INF, a2 = NEG_INF;
-                for (int o = 1; o < gs; o <<= 1) {
-                    const float b1 = __shfl_xor(a1, o, 64), b2 = __shfl_xor(a2, o, 64);
-                    top2_merge(a1, a2, b1, b2);
-                }
-                const int e = lane + 64 * i;
-                if (e % gs == 0 && e < E) gsc[e / gs] = __fadd_rn(a1, gs > 1 ? a2 : 0.0f);
+        // group score: the sum of the group's two largest values (NaN never
+        // counts); keep the topk_group groups that come first under
+        // `before`, never one scored -inf; mask the rest to -inf
+        const int G = c.n_group, gs = E / G, g = e / gs;
+        const float gv = sel == sel ? sel : NEG_INF;
+        if (valid) {
+            int rk = 0;
+            for (int k = g * gs; k < (g + 1) * gs; k++) {
+                const float o = s_sel[k];
+                rk += before(o == o ? o : NEG_INF, k, gv, e);
             }
-        } else {
-            // wide groups: scan each group from LDS
-#pragma unroll
-            for (int i = 0; i < NPL; i++)
-                if (i < npl && lane + 64 * i < E) lds[lane + 64 * i] = sel[i];
-            __syncthreads();
-            if (lane < G) {
-                float a1 = NEG_INF, a2 = NEG_INF;
-                for (int k = 0; k < gs; k++) {
-                    const float v = lds[lane * gs + k];
-                    if (v == v) top2_merge(a1, a2, v, NEG_INF);
-                }
-                gsc[lane] = __fadd_rn(a1, gs > 1 ? a2 : 0.0f);
-            }
+            if (rk == 0) s_g1[g] = gv;
+            if (rk == 1) s_g2[g] = gv;
         }
         __syncthreads();
-        // keep topk_group groups: strict-greater passes, lowest index first
-        uint64_t keep = 0;
-        for (int j = 0; j < c.topk_group; j++) {
-            int best = -1;
-            float bv = NEG_INF;
-            for (int g = 0; g < G; g++)
-                if (!((keep >> g) & 1) && gsc[g] > bv) { bv = gsc[g]; best = g; }
-            if (best < 0) break;
-            keep |= 1ull << best;
+        if (e < G) s_g[e] = __fadd_rn(s_g1[e], gs > 1 ? s_g2[e] : 0.0f);
+        __syncthreads();
+        if (valid) {
+            const float mine = s_g[g];
+            int grk = 0;
+            for (int k = 0; k < G; k++) grk += before(s_g[k], k, mine, g);
+            if (!(grk < c.topk_group && mine > NEG_INF)) sel = NEG_INF;
         }
-#pragma unroll
-        for (int i = 0; i < NPL; i++) {
-            const int e = lane + 64 * i;
-            if (i < npl && e < E && !((keep >> (e / gs)) & 1)) sel[i] = NEG_INF;
-        }
+        __syncthreads();
+        s_sel[e] = sel;
+        __syncthreads();
     }
 
-    // K selection passes; lane j keeps pass j's expert and weight
-    uint32_t taken = 0;
-    int my_id = -1;
-    float my_w = 0.0f;
-    int bad = 0;
-    for (int j = 0; j < K; j++) {
-        float bv = -1e30f;
-        int be = -1;
-        float bs = 0.0f;
-#pragma unroll
-        for (int i = 0; i < NPL; i++)
-            if (i < npl && !((taken >> i) & 1) && sel[i] > bv) { bv = sel[i]; be = lane + 64 * i; bs = sc[i]; }
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oe = __shfl_xor(be, o, 64);
-            const float os = __shfl_xor(bs, o, 64);
-            if (better(ov, oe, bv, be)) { bv = ov; be = oe; bs = os; }
+    // candidates: strictly above the scan's floor -1e30 (never NaN)
+    const bool cand = valid && sel > -1e30f;
+    if (cand) {
+        atomicAdd(&s_ncand, 1);
+        int rk = 0;
+        for (int k = 0; k < E; k++) {
+            const float o = s_sel[k];
+            rk += (o > -1e30f) && before(o, k, sel, e);
         }
-        if (be < 0) { bad = 1; continue; }
-        if ((be & 63) == lane) taken |= 1u << (be >> 6);
-        if (lane == j) { my_id = be; my_w = bs; }
+        if (rk < K) { s_id[rk] = e; s_w[rk] = sc; }
     }
-    if (!bad) {
-        if (c.renorm && K > 1) {
-            float s = 0.0f;                  // selection order
-            for (int j = 0; j < K; j++) s = __fadd_rn(s, __shfl(my_w, j, 64));
-            my_w = __fdiv_rn(my_w, __fadd_rn(s, 1e-20f));
+    __syncthreads();
+    const int bad = s_ncand < K;
+    if (e == 0) {
+        if (!bad) {
+            if (c.renorm && K > 1) {
+                float s = 0.0f;              // selection order
+                for (int j = 0; j < K; j++) s = __fadd_rn(s, s_w[j]);
+                const float d = __fadd_rn(s, 1e-20f);
+                for (int j = 0; j < K; j++) s_w[j] = __fdiv_rn(s_w[j], d);
+            }
+            for (int j = 0; j < K; j++) s_w[j] = __fmul_rn(s_w[j], c.routed_scale);
+        } else {
+            atomicOr(err, 2);
         }
-        my_w = __fmul_rn(my_w, c.routed_scale);
-    } else {
-        my_id = -1;
-        my_w = 0.0f;
-        if (lane == 0) atomicOr(err, 2);
     }
-    if (lane < K) {
-        ids[(size_t)t * K + lane] = my_id;
-        wout[(size_t)t * K + lane] = my_w;
+    __syncthreads();
+    if (e < K) {
+        const int id = bad ? -1 : s_id[e];
+        const float wv = bad ? 0.0f : s_w[e];
+        ids[(size_t)t * K + e] = id;
+        wout[(size_t)t * K + e] = wv;
         if (pair_exp && T == 1) {
-            pair_tok[lane] = 0;
-            pair_exp[lane] = my_id < 0 ? E : my_id;    // E: the table's NULL sentinel
-            pair_w[lane] = my_w;
-            tok_pairs[lane] = lane;
+            pair_tok[e] = 0;
+            pair_exp[e] = id < 0 ? E : id;       // E: the table's NULL sentinel
+            pair_w[e] = wv;
+            tok_pairs[e] = e;
         }
     }
 }
@@ -205,16 +167,9 @@ extern "C" int whip_route(const whip_route_cfg *c, const float *logits, const fl
     if (c->E > MAXE || c->E <= 0 || c->K <= 0 || c->K > 64 || c->K > c->E) return (int)hipErrorInvalidValue;
     if (c->n_group > 1 && (c->n_group > 64 || c->E % c->n_group || c->topk_group < 1))
         return (int)hipErrorInvalidValue;
-#define ROUTE_LAUNCH(N)                                                                        \
-    hipLaunchKernelGGL(k_route<N>, dim3(T), dim3(64), 0, s, *c, logits, bias, T, ids, w, pair_tok, \
-                       pair_exp, pair_w, tok_pairs, err)
-    const int npl = (c->E + 63) / 64;
-    if (npl <= 1) ROUTE_LAUNCH(1);
-    else if (npl <= 2) ROUTE_LAUNCH(2);
-    else if (npl <= 4) ROUTE_LAUNCH(4);
-    else if (npl <= 8) ROUTE_LAUNCH(8);
-    else ROUTE_LAUNCH(16);
-#undef ROUTE_LAUNCH
+    const int threads = (c->E + 63) / 64 * 64;
+    hipLaunchKernelGGL(k_route, dim3(T), dim3(threads), 0, s, *c, logits, bias, T, ids, w, pair_tok,
+                       pair_exp, pair_w, tok_pairs, err);
     return (int)hipGetLastError();
 }
 

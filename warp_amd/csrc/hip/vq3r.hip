@@ -73,11 +73,19 @@ vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict
         for (int r = rb_lo * 64 + tid; r < min(rb_hi * 64, M); r += blockDim.x) out[r] = 0.0f;
         return;
     }
-    // the first row block's indices are in flight while the table is built
+    // The wavefront's row blocks are rb_lo + wave + nw*k.  Up to four of
+    // them are in flight at once, the first four issued before the table
+    // is built, so the index stream is moving while the LUT is computed.
     const uint8_t *idx = rec + (kind ? off1 : off0) + (size_t)v0 * 192 + lane * 3;
-    uint32_t cur[VC], nxt[VC];
-    int rb = rb_lo + wave;
-    if (rb < rb_hi) load_block(idx + (size_t)rb * nv * 192, vcount, cur);
+    uint32_t cur[2][VC], nxt[2][VC];
+    const int rb0 = rb_lo + wave;
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int rb = rb0 + q * nw;
+        if (rb < rb_hi) load_block(idx + (size_t)rb * nv * 192, vcount, cur[q]);
+        const int rn = rb0 + (q + 2) * nw;
+        if (rn < rb_hi) load_block(idx + (size_t)rn * nv * 192, vcount, nxt[q]);
+    }
 
     const int srow = pair_src ? pair_src[p] : p;
     if (tid < vcount * 8) {
@@ -105,16 +113,22 @@ vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict
     }
     __syncthreads();
 
-    // two row blocks in flight per wavefront: the next one's loads are
-    // issued before the current one's lookups
-    for (; rb < rb_hi; rb += nw) {
-        const int rn = rb + nw;
-        if (rn < rb_hi) load_block(idx + (size_t)rn * nv * 192, vcount, nxt);
-        const float acc = apply_block(lut, vcount, cur);
-        const int r = rb * 64 + lane;
-        if (r < M) out[r] = acc;
+    for (int k = 0; rb0 + k * nw < rb_hi; k += 2) {
 #pragma unroll
-        for (int v = 0; v < VC; v++) cur[v] = nxt[v];
+        for (int q = 0; q < 2; q++) {
+            const int rb = rb0 + (k + q) * nw;
+            if (rb >= rb_hi) break;
+            const float acc = apply_block(lut, vcount, cur[q]);
+            const int r = rb * 64 + lane;
+            if (r < M) out[r] = acc;
+        }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+#pragma unroll
+            for (int v = 0; v < VC; v++) cur[q][v] = nxt[q][v];
+            const int rn = rb0 + (k + 4 + q) * nw;
+            if (rn < rb_hi) load_block(idx + (size_t)rn * nv * 192, vcount, nxt[q]);
+        }
     }
 }
 
