@@ -18,7 +18,7 @@ import pytest
 
 from gpu_util import LAYER_RTOL, LOGIT_RTOL, gpu_layer, rel_err, run_forward
 from oracle_lib import Oracle
-from records import FMT_F32, FMT_Q4G, FMT_Q8G, Layer
+from records import FMT_F32, FMT_Q4G, FMT_Q8G, Layer, Tensor
 
 pytestmark = pytest.mark.gpu
 
@@ -156,6 +156,59 @@ def test_route_ties(orc):
         assert st == 0
         check_routing(orc, L, lg, ids, w)
         m.close()
+
+
+def _planted_layer(E, K, sf, bias, ng, tg, seed):
+    """A layer whose router is the identity (F32, H = E), so each token's
+    logits are its input vector exactly: planted ties, signed zeros and
+    values far outside the sigmoid's range reach the router unchanged."""
+    L = Layer(E, 64, E, K, score_func=sf, renorm=1, routed_scale=2.5, bias=bias,
+              n_group=ng, topk_group=tg, seed=seed)
+    L.router = Tensor.make(FMT_F32, np.eye(E, dtype=np.float32))
+    r = np.random.default_rng(seed)
+    if bias:
+        L.bias = r.choice(np.array([-0.25, 0.0, 0.125, 0.5], np.float32), E)
+    return L, r
+
+
+@pytest.mark.parametrize("E,K,sf,bias,ng,tg", [
+    (64, 8, 0, False, 1, 1), (64, 64, 0, True, 1, 1), (64, 8, 1, False, 1, 1),
+    (128, 6, 0, True, 16, 5), (256, 8, 0, True, 8, 4), (256, 8, 1, True, 8, 4),
+    (256, 8, 0, True, 64, 8), (512, 8, 0, True, 1, 1), (1024, 16, 0, True, 16, 3)])
+def test_route_planted(orc, E, K, sf, bias, ng, tg):
+    """Top-k over planted logits: few distinct values (so most experts tie
+    with several others), +-0, and +-40 (sigmoid saturates to exactly 0 and
+    1), for every lanes-per-expert width of the router kernel and for
+    group-limited selection with 1 to 64 groups.  ids and weights are
+    bit-exact against the oracle on the device's logits."""
+    say("test_route_planted", E, K, sf, bias, ng, tg)
+    L, r = _planted_layer(E, K, sf, bias, ng, tg, seed=E + K + sf + ng)
+    vals = np.array([-40, -3, -1, -0.5, -0.0, 0.0, 0.5, 1, 2, 3, 40], np.float32)
+    X = r.choice(vals, (16, E))
+    m = gpu_layer(L, max_tokens=16)
+    st, y, ids, w, lg = run_forward(torch, m, L, X)
+    m.close()
+    assert st == 0
+    assert np.array_equal(lg.view(np.uint32) & 0x7fffffff, X.view(np.uint32) & 0x7fffffff)
+    check_routing(orc, L, lg, ids, w)
+
+
+def test_route_too_few_candidates(orc):
+    """Fewer than K experts above the engine's -1e30 floor: the layer
+    reports WASTE_HIP_EROUTE and every id is -1 (the engine would index
+    score[-1]); the oracle also refuses the token."""
+    say("test_route_too_few_candidates")
+    L, r = _planted_layer(64, 8, 0, True, 1, 1, seed=5)
+    L.bias = np.full(64, -1e31, np.float32)
+    L.bias[[3, 9, 40, 41]] = 0.0
+    X = r.standard_normal((1, 64)).astype(np.float32)
+    m = gpu_layer(L, max_tokens=1)
+    st, y, ids, w, lg = run_forward(torch, m, L, X)
+    m.close()
+    assert st == warp_amd.EROUTE
+    assert np.all(ids == -1) and np.all(w == 0)
+    rc, _, _, _ = orc.route(lg[0], L.bias, 64, 8, 0, 1, 2.5, 1, 1)
+    assert rc < 0
 
 
 def test_vq3r_batch_bit_exact(orc):

@@ -22,6 +22,8 @@ SCORE_SIGMOID, SCORE_SOFTMAX, SCORE_SQRTSOFTPLUS = 0, 1, 2
 ERRORS = {0: "ok", -1: "EINVAL", -2: "ENODEV", -3: "ENOMEM", -4: "ERECORD", -5: "ECRC",
           -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE"}
 
+OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE = 0, -1, -2, -3, -4, -5, -6, -7, -8
+
 # Every symbol include/waste_hip.h declares.
 EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_host_buffers",
            "waste_hip_vq3r", "waste_hip_moe_create", "waste_hip_moe_destroy",

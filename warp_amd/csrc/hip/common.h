@@ -90,12 +90,46 @@ WH_INLINE float wh_silu_mul(float g, float u)
     return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, wh_expf(-g))), u);
 }
 
+/* Cross-lane moves of a full-wave butterfly: DPP inside rows of 16 lanes
+ * (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror),
+ * then the row swaps permlane16 and permlane32.  Each pairs every lane
+ * with one partner outside the set it has already combined, so six steps
+ * of an order-free op reduce over all 64 lanes.  The caller's wave must be
+ * fully active. */
+template <int CTRL> WH_INLINE uint32_t dpp32(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+
 WH_INLINE float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += __uint_as_float(dpp32<0xB1>(__float_as_uint(v)));
+    v += __uint_as_float(dpp32<0x4E>(__float_as_uint(v)));
+    v += __uint_as_float(dpp32<0x141>(__float_as_uint(v)));
+    v += __uint_as_float(dpp32<0x140>(__float_as_uint(v)));
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
     return v;
 }
+
+/* A pointer read from memory (a record table entry) is generic to the
+ * compiler, which then emits flat loads: those count against the LDS wait
+ * counter too, so every LDS read would also wait for the loads in flight.
+ * Device records live in global memory; say so. */
+#if defined(__HIP_DEVICE_COMPILE__)
+#define WH_GLOBAL __attribute__((address_space(1)))
+#else
+#define WH_GLOBAL
+#endif
+typedef const uint8_t WH_GLOBAL g_u8;
+typedef const uint16_t WH_GLOBAL g_u16;
+WH_INLINE g_u8 *as_global(const uint8_t *p) { return (g_u8 *)p; }
 
 /* Unaligned 4-byte read (gfx950 global loads accept any byte address). */
 WH_INLINE uint32_t ld_u32_unaligned(const uint8_t *p)

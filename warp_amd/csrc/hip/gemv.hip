@@ -59,6 +59,7 @@ struct gemv_job {
     float *y;
     int y_ld;
     int wpr, blk0, nblk;
+    int rpw;                   // rows per wavefront (one-token kernel)
 };
 struct gemv_pack {
     gemv_job j[3];
@@ -207,6 +208,249 @@ __global__ void __launch_bounds__(256) k_gemv_multi(gemv_pack pk)
     else run_job<3, TBT>(J, pk.T, blk, red);
 }
 
+// ---- one token --------------------------------------------------------------
+// The decode products are latency-bound unless every load a lane needs is in
+// flight at once.  A lane issues its weight chunks (and their group scales)
+// and the matching slices of x together, then computes: one memory round
+// trip per batch of U chunks.  A wavefront owns RPW rows (RPW = 4 when a row
+// is at most one chunk per lane, so x is read once for four rows).
+
+// chunks per lane per batch (about 124 VGPRs: four workgroups per CU); fp32
+// x slices are twice the registers of bf16
+template <int FMT, bool XBF> struct u_of { static constexpr int U = (FMT == 0 ? 8 : 2) / (XBF ? 1 : 2) > 0 ? (FMT == 0 ? 8 : 2) / (XBF ? 1 : 2) : 1; };
+
+// x slice of one chunk as raw 16-byte words: NE elements, bf16 or fp32
+template <int FMT, bool XBF> struct xw_of {
+    static constexpr int N = (chunk_of<FMT>::NE * (XBF ? 2 : 4) + 15) / 16;
+};
+
+// Loads take a clamped, always valid address and no branch: a load behind a
+// divergent branch, or a value converted right after its load, makes the
+// compiler wait for every load in flight before issuing the next.
+template <int FMT, bool XBF>
+__device__ __forceinline__ void load_xs(const void *x, int cols, int k, uint4 *xw)
+{
+    constexpr int NE = chunk_of<FMT>::NE, NW = xw_of<FMT, XBF>::N;
+    const int e0 = k * NE;
+    if (NE * (XBF ? 2 : 4) < 16) {                        // F32 weights, bf16 x: 8 bytes
+        const uint2 v = *(const uint2 *)((const uint16_t *)x + (e0 < cols ? e0 : 0));
+        xw[0] = make_uint4(v.x, v.y, 0, 0);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+        const int e = e0 + i * (XBF ? 8 : 4);
+        xw[i] = *(const uint4 *)((const uint8_t *)x + (size_t)(e < cols ? e : 0) * (XBF ? 2 : 4));
+    }
+}
+
+// zero the x words past the last column (a padded row's tail multiplies 0)
+template <int FMT, bool XBF>
+__device__ __forceinline__ void mask_xs(int cols, int k, uint4 *xw)
+{
+    constexpr int NE = chunk_of<FMT>::NE, NW = xw_of<FMT, XBF>::N;
+    const int e0 = k * NE;
+    if (NE * (XBF ? 2 : 4) < 16) {
+        if (e0 >= cols) xw[0] = make_uint4(0, 0, 0, 0);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+        if (e0 + i * (XBF ? 8 : 4) >= cols) xw[i] = make_uint4(0, 0, 0, 0);
+}
+
+template <int FMT, bool XBF>
+__device__ __forceinline__ float chunk_dot(uint4 raw, const uint4 *xw)
+{
+    constexpr int NE = chunk_of<FMT>::NE;
+    const uint32_t uw[4] = {raw.x, raw.y, raw.z, raw.w};
+    float a = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NE / 4; q++) {
+        float x[4];
+        if (XBF) {
+            const uint4 v = xw[q >> 1];
+            const uint32_t lo = (q & 1) ? v.z : v.x, hi = (q & 1) ? v.w : v.y;
+            x[0] = wh_bf16(lo & 0xffff); x[1] = wh_bf16(lo >> 16);
+            x[2] = wh_bf16(hi & 0xffff); x[3] = wh_bf16(hi >> 16);
+        } else {
+            const uint4 v = xw[q];
+            x[0] = __uint_as_float(v.x); x[1] = __uint_as_float(v.y);
+            x[2] = __uint_as_float(v.z); x[3] = __uint_as_float(v.w);
+        }
+        float w[4];
+        if (FMT == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[i] = __uint_as_float(uw[i]);
+        } else if (FMT == 2) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[i] = (float)(int8_t)((uw[q] >> (i * 8)) & 0xff);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+                const uint32_t b = (uw[q >> 1] >> (((q & 1) * 2 + (i >> 1)) * 8)) & 0xff;
+                w[i] = (float)((int)(b & 15) - 8);
+                w[i + 1] = (float)((int)(b >> 4) - 8);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) a = __fmaf_rn(w[i], x[i], a);
+    }
+    return a;
+}
+
+template <int FMT, int RPW, bool XBF>
+__device__ __forceinline__ void run_job1(const gemv_job &J, int blk, float (*red)[4][2])
+{
+    constexpr int NE = chunk_of<FMT>::NE, NW = xw_of<FMT, XBF>::N;
+    constexpr int U = u_of<FMT, XBF>::U / RPW > 0 ? u_of<FMT, XBF>::U / RPW : 1;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wpr = J.wpr, groups = 4 / wpr;
+    const int rg = blk * groups + wave / wpr, part = wave % wpr;
+    const int r0 = rg * RPW;
+    const int ng = FMT == 0 ? 1 : (J.cols + J.group - 1) / J.group;
+    const int nchunk = (FMT == 0 ? J.cols : ng * J.group) / NE;
+    const int stride = 64 * wpr;
+    const bool pair = J.W1 != nullptr;
+
+    float a0[RPW], a1[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) { a0[i] = 0.0f; a1[i] = 0.0f; }
+    for (int k0 = part * 64 + lane; k0 - lane < nchunk; k0 += stride * U) {   // wave-uniform test
+        uint4 w0[RPW][U], w1[RPW][U], xw[U][NW];
+        uint16_t s0[RPW][U], s1[RPW][U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = k0 + u * stride, kc = k < nchunk ? k : 0;
+            load_xs<FMT, XBF>(J.x, J.cols, kc, xw[u]);
+#pragma unroll
+            for (int i = 0; i < RPW; i++) {
+                const int rc = r0 + i < J.rows ? r0 + i : 0;
+                const size_t o = (size_t)rc * J.rowbytes + (size_t)kc * 16;
+                w0[i][u] = *(const uint4 *)(J.W0 + o);
+                if (FMT != 0) s0[i][u] = J.S0[(size_t)rc * ng + (size_t)kc * NE / J.group];
+            }
+        }
+        if (pair) {                                    // uniform
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int k = k0 + u * stride, kc = k < nchunk ? k : 0;
+#pragma unroll
+                for (int i = 0; i < RPW; i++) {
+                    const int rc = r0 + i < J.rows ? r0 + i : 0;
+                    const size_t o = (size_t)rc * J.rowbytes + (size_t)kc * 16;
+                    w1[i][u] = *(const uint4 *)(J.W1 + o);
+                    if (FMT != 0) s1[i][u] = J.S1[(size_t)rc * ng + (size_t)kc * NE / J.group];
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = k0 + u * stride;
+            if (k >= nchunk) continue;                 // rows past the end are never written
+            mask_xs<FMT, XBF>(J.cols, k, xw[u]);
+#pragma unroll
+            for (int i = 0; i < RPW; i++) {
+                const float d0 = chunk_dot<FMT, XBF>(w0[i][u], xw[u]);
+                a0[i] = FMT == 0 ? a0[i] + d0 : __fmaf_rn(wh_f16_scale(s0[i][u]), d0, a0[i]);
+                if (pair) {
+                    const float d1 = chunk_dot<FMT, XBF>(w1[i][u], xw[u]);
+                    a1[i] = FMT == 0 ? a1[i] + d1 : __fmaf_rn(wh_f16_scale(s1[i][u]), d1, a1[i]);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        a0[i] = wave_sum(a0[i]);
+        if (pair) a1[i] = wave_sum(a1[i]);
+    }
+    if (wpr > 1) {
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < RPW; i++) { red[wave][i][0] = a0[i]; red[wave][i][1] = a1[i]; }
+        __syncthreads();
+        if (part == 0 && lane == 0)
+#pragma unroll
+            for (int i = 0; i < RPW; i++) {
+                float t0 = red[wave][i][0], t1 = red[wave][i][1];
+                for (int q = 1; q < wpr; q++) { t0 += red[wave + q][i][0]; t1 += red[wave + q][i][1]; }
+                a0[i] = t0; a1[i] = t1;
+            }
+    }
+    if (part == 0 && lane == 0)
+#pragma unroll
+        for (int i = 0; i < RPW; i++)
+            if (r0 + i < J.rows) J.y[r0 + i] = pair ? wh_silu_mul(a0[i], a1[i]) : a0[i];
+}
+
+template <int FMT, bool XBF>
+__device__ __forceinline__ void run_fmt1(const gemv_job &J, int blk, float (*red)[4][2])
+{
+    if (J.rpw == 4) run_job1<FMT, 4, XBF>(J, blk, red);
+    else run_job1<FMT, 1, XBF>(J, blk, red);
+}
+
+// every job of one launch reads x of one type (bf16 or fp32)
+template <bool XBF>
+__global__ void __launch_bounds__(256) k_gemv1(gemv_pack pk)
+{
+    __shared__ float red[4][4][2];
+    const int b = blockIdx.x;
+    const int ji = (pk.n > 2 && b >= pk.j[2].blk0) ? 2 : (pk.n > 1 && b >= pk.j[1].blk0) ? 1 : 0;
+#define SEL(f) (ji == 2 ? pk.j[2].f : ji == 1 ? pk.j[1].f : pk.j[0].f)
+    gemv_job J;
+    J.W0 = SEL(W0); J.W1 = SEL(W1); J.S0 = SEL(S0); J.S1 = SEL(S1); J.rowbytes = SEL(rowbytes);
+    J.fmt = SEL(fmt); J.rows = SEL(rows); J.cols = SEL(cols); J.group = SEL(group);
+    J.x = SEL(x); J.x_ld = SEL(x_ld); J.x_bf16 = SEL(x_bf16); J.y = SEL(y); J.y_ld = SEL(y_ld);
+    J.wpr = SEL(wpr); J.blk0 = SEL(blk0); J.nblk = SEL(nblk); J.rpw = SEL(rpw);
+#undef SEL
+    const int blk = b - J.blk0;
+    if (J.fmt == 0) run_fmt1<0, XBF>(J, blk, red);
+    else if (J.fmt == 2) run_fmt1<2, XBF>(J, blk, red);
+    else run_fmt1<3, XBF>(J, blk, red);
+}
+
+// padded columns of a matrix (whole quantisation groups)
+static int padded_cols(const whip_mat *A)
+{
+    if (A->fmt == 0) return A->cols;
+    return (A->cols + A->group - 1) / A->group * A->group;
+}
+
+static int launch_gemv1(const whip_gemv_job *jobs, int n, hipStream_t s)
+{
+    gemv_pack pk;
+    int blk = 0;
+    for (int i = 0; i < n; i++) {
+        const whip_gemv_job *q = &jobs[i];
+        const int ne = q->A.fmt == 0 ? 4 : q->A.fmt == 2 ? 16 : 32;
+        const int nchunk = padded_cols(&q->A) / ne;
+        gemv_job &J = pk.j[i];
+        J.W0 = (const uint8_t *)q->A.q; J.S0 = q->A.qs;
+        J.W1 = q->B ? (const uint8_t *)q->B->q : nullptr; J.S1 = q->B ? q->B->qs : nullptr;
+        J.rowbytes = q->A.rowbytes; J.fmt = q->A.fmt; J.rows = q->A.rows; J.cols = q->A.cols;
+        J.group = q->A.group; J.x = q->x; J.x_bf16 = q->x_bf16; J.y = q->y; J.y_ld = q->y_ld;
+        const int U = q->A.fmt == 0 ? (q->x_bf16 ? 8 : 4) : (q->x_bf16 ? 2 : 1);
+        int rpw = 1, wpr = 1;
+        if (nchunk <= 64) rpw = 4;
+        else wpr = nchunk > 64 * U * 2 ? 4 : nchunk > 64 * U ? 2 : 1;
+        J.x_ld = q->x_ld;
+        J.rpw = rpw;
+        J.wpr = wpr;
+        const int groups = (J.rows + rpw - 1) / rpw;
+        J.nblk = (groups + 4 / wpr - 1) / (4 / wpr);
+        J.blk0 = blk;
+        blk += J.nblk;
+    }
+    pk.n = n;
+    pk.T = 1;
+    if (jobs[0].x_bf16) hipLaunchKernelGGL(k_gemv1<true>, dim3(blk), dim3(256), 0, s, pk);
+    else hipLaunchKernelGGL(k_gemv1<false>, dim3(blk), dim3(256), 0, s, pk);
+    return (int)hipGetLastError();
+}
+
 static int waves_per_row(const whip_mat *A)
 {
     // about UNROLL chunks per lane and at least one full pass of loads
@@ -245,12 +489,21 @@ extern "C" int whip_gemv_multi(const whip_gemv_job *jobs, int n, int T, hipStrea
         J.group = q->A.group; J.x = q->x; J.x_ld = q->x_ld; J.x_bf16 = q->x_bf16;
         J.y = q->y; J.y_ld = q->y_ld;
         J.wpr = waves_per_row(&q->A);
+        J.rpw = 1;
         J.blk0 = blk;
         J.nblk = (J.rows + (4 / J.wpr) - 1) / (4 / J.wpr);
         blk += J.nblk;
     }
     pk.n = n;
     pk.T = T;
+    if (T == 1) {
+        bool fits = true;
+        for (int i = 0; i < n; i++)
+            // x slices are read 16 bytes at a time and never past the last column
+            fits = fits && (uintptr_t)jobs[i].x % 16 == 0 && (jobs[i].A.fmt == 0 || jobs[i].A.cols % 8 == 0) &&
+                   jobs[i].x_bf16 == jobs[0].x_bf16;
+        if (fits) return launch_gemv1(jobs, n, s);
+    }
     if (T == 1) hipLaunchKernelGGL(k_gemv_multi<1>, dim3(blk), dim3(256), 0, s, pk);
     else hipLaunchKernelGGL(k_gemv_multi<TB>, dim3(blk), dim3(256), 0, s, pk);
     return (int)hipGetLastError();

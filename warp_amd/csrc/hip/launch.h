@@ -62,7 +62,11 @@ int whip_pairs(const int32_t *ids, const float *w, int T, int K, int E,
 /* One VQ3R apply stage over P (source row, expert) pairs:
  *   part[((p*kinds + k)*nch + c)*M + r] = sum over chunk c's positions of
  *       L_k[v][0][i0] + L_k[v][1][i1] + L_k[v][2][i2]
- * with L_k built in LDS from src[pair_src[p]] and books cb + 3k. */
+ * with L_k built in LDS from src[pair_src[p]] and books cb + 3k.
+ * span = P (<= 64) declares that every pair reads the same source row:
+ * one table then serves all pairs, and rsplit divides the P*M/64 row
+ * blocks of all pairs; span <= 1 splits each pair's M/64 row blocks.
+ * part holds P*kinds*nch*M floats plus 64 (a sink for dead stores). */
 typedef struct {
     const uint8_t *const *recs;      /* [E] record bases, NULL if unbound   */
     const int32_t *pair_exp;         /* [P]                                 */
@@ -72,7 +76,7 @@ typedef struct {
     const float *booksT;             /* [n_books][8][256] fp32              */
     int cb;                          /* first book of kind 0                */
     uint32_t idx_off[2];             /* byte offset of kind k's indices     */
-    int kinds, M, nv, P, rsplit;
+    int kinds, M, nv, P, rsplit, span;
     float *part;
     int *err;
 } whip_vq_args;

@@ -11,161 +11,220 @@
 //
 // Layout in HBM (the container's, unchanged): one record per expert,
 // indices blocked [row/64][v][row%64][stage] (docs/FORMAT.md:216-223), so a
-// 64-row block at one position is 192 contiguous bytes.  A wavefront owns a
-// row block: lane r reads its 3 index bytes for position v with one 4-byte
-// load (gfx950 global loads take any byte address), the 64 lanes together
-// covering the block's 192 bytes, which the memory system coalesces.
+// 64-row block at one position is 192 contiguous bytes.  Lane (g, rq) of a
+// wavefront reads the 12 bytes of rows 4rq..4rq+3 of row block g of its
+// group of four, one dwordx3 per position: the four 16-lane groups take
+// four row blocks at the same position.  The table address is then the
+// same for the whole wave (its position) and folds into the LDS read's
+// offset; each lane keeps its four rows' sums over the chunk's positions,
+// so no cross-lane reduction is needed.
 //
-// A workgroup owns a chunk of VC positions for one (pair, kind) and all of
-// that matrix's rows (or a 1/rsplit share).  It builds the chunk's table
-// in LDS — VC*3*256 fp32 — once, then streams the rows through it: the
-// table costs 6144 FMAs per position, amortised over every row.  Row sums
-// leave as per-chunk partials; the next kernel reduces them.  The split is
-// what lets a decode token's eight experts fill 256 CUs.
+// A workgroup owns a chunk of VC positions for one kind and a share of the
+// row blocks of one pair (or, when every pair reads the same source row,
+// of all pairs).  It builds the chunk's table in LDS — VC*3*256 fp32 —
+// once, then streams the rows through it: the table costs 6144 FMAs per
+// position, amortised over every row.  Row sums leave as per-chunk
+// partials; the next kernel reduces them.  The split is what lets a decode
+// token's eight experts fill 256 CUs.
 #include "common.h"
 #include "launch.h"
 
-#define VC 16                       // positions per workgroup chunk
+#define VC 8                        // positions per workgroup chunk
 #define LUT_PER_V (3 * 256)
 
 extern "C" int whip_vq_chunks(int nv) { return (nv + VC - 1) / VC; }
 
-__device__ __forceinline__ void load_block(const uint8_t *pp, int vcount, uint32_t *wv)
-{
-#pragma unroll
-    for (int v = 0; v < VC; v++) wv[v] = v < vcount ? ld_u32_unaligned(pp + v * 192) : 0u;
-}
+typedef const uint3 WH_GLOBAL g_uint3;
 
-__device__ __forceinline__ float apply_block(const float *lut, int vcount, const uint32_t *wv)
-{
-    float acc = 0.0f;
-#pragma unroll
-    for (int v = 0; v < VC; v++) {
-        if (v >= vcount) break;
-        const float *L = lut + v * LUT_PER_V;
-        const uint32_t w = wv[v];
-        const float t = (L[w & 255] + L[256 + ((w >> 8) & 255)]) + L[512 + ((w >> 16) & 255)];
-        acc += t;
-    }
-    return acc;
-}
+// Row blocks are numbered over the pairs a workgroup may span: vb = q*nb + rb
+// is row block rb of pair p0 + q.  With span 1 a workgroup owns (a share of)
+// one pair's rows; with span = P every pair reads the same source row (a
+// one-token decode's gate/up), so one table serves all of their rows and a
+// workgroup's share runs across experts.
+#define SPAN_MAX 64
+#define VQ_THREADS 512
+#define LUT_ITERS ((LUT_PER_V + VQ_THREADS - 1) / VQ_THREADS)
 
 __device__ __forceinline__ void
 vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
               const int32_t *__restrict__ pair_src, const void *__restrict__ src, int src_ld,
               int src_bf16, const float *__restrict__ booksT, int cb, uint32_t off0,
-              uint32_t off1, int kinds, int M, int nv, int nch, int rsplit,
+              uint32_t off1, int kinds, int M, int nv, int nch, int rsplit, int P, int span,
               float *__restrict__ part, int *__restrict__ err)
 {
     __shared__ float lut[VC * LUT_PER_V];
     __shared__ float xs[VC * 8];
+    __shared__ const uint8_t *s_rec[SPAN_MAX];
     const int c = blockIdx.x, kind = blockIdx.y / rsplit, rs = blockIdx.y % rsplit;
-    const int p = blockIdx.z, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    const int v0 = c * VC, vcount = min(VC, nv - v0);
-    const int nb = (M + 63) >> 6;
-    const int rb_lo = rs * nb / rsplit, rb_hi = (rs + 1) * nb / rsplit;
-    float *out = part + (((size_t)p * kinds + kind) * nch + c) * (size_t)M;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, nw = VQ_THREADS >> 6;
+    const int v0 = c * VC;                       // nv % VC == 0 (host contract)
+    const int nb = M >> 6;                       // M % 64 == 0 (host contract)
+    const int p0 = span > 1 ? 0 : blockIdx.z, np = span > 1 ? P : 1;
+    const int V = np * nb;
+    const int vlo = (int)((long)rs * V / rsplit), vhi = (int)((long)(rs + 1) * V / rsplit);
 
-    const uint8_t *rec = recs[pair_exp[p]];
-    if (rec == nullptr) {                       // unbound expert: zeros + flag
-        if (tid == 0) atomicOr(err, 1);
-        for (int r = rb_lo * 64 + tid; r < min(rb_hi * 64, M); r += blockDim.x) out[r] = 0.0f;
-        return;
-    }
-    // The wavefront's row blocks are rb_lo + wave + nw*k.  Up to four of
-    // them are in flight at once, the first four issued before the table
-    // is built, so the index stream is moving while the LUT is computed.
-    const uint8_t *idx = rec + (kind ? off1 : off0) + (size_t)v0 * 192 + lane * 3;
-    uint32_t cur[2][VC], nxt[2][VC];
-    const int rb0 = rb_lo + wave;
+    // everything the table needs is requested before the first barrier
+    if (tid < np) s_rec[tid] = recs[pair_exp[p0 + tid]];
+    const float *bT = booksT + (size_t)(cb + kind * 3) * 8 * 256;
+    float cv[LUT_ITERS][8];
 #pragma unroll
-    for (int q = 0; q < 2; q++) {
-        const int rb = rb0 + q * nw;
-        if (rb < rb_hi) load_block(idx + (size_t)rb * nv * 192, vcount, cur[q]);
-        const int rn = rb0 + (q + 2) * nw;
-        if (rn < rb_hi) load_block(idx + (size_t)rn * nv * 192, vcount, nxt[q]);
+    for (int i = 0; i < LUT_ITERS; i++) {
+        const int q = tid + i * VQ_THREADS < LUT_PER_V ? tid + i * VQ_THREADS : 0;
+        const float *cr = bT + (size_t)(q >> 8) * 8 * 256 + (q & 255);
+#pragma unroll
+        for (int d = 0; d < 8; d++) cv[i][d] = cr[d * 256];
     }
-
-    const int srow = pair_src ? pair_src[p] : p;
-    if (tid < vcount * 8) {
+    const int srow = pair_src ? pair_src[p0] : p0;
+    if (tid < VC * 8) {
         const size_t o = (size_t)srow * src_ld + (size_t)v0 * 8 + tid;
         xs[tid] = src_bf16 ? wh_bf16(((const uint16_t *)src)[o]) : ((const float *)src)[o];
     }
     __syncthreads();
 
+    // A wavefront takes groups of four row blocks: vlo + 4*(wave + nw*it) + g.
+    // The buffer rolls: position k of the next group is requested as soon as
+    // position k of this one is consumed, so a load has a whole group's
+    // compute to arrive, in VC registers' worth of buffer.  Loads are never
+    // behind a branch (the compiler, unsure how many are in flight, would
+    // wait for all): a row block past the share's end or with no record
+    // reads a fixed in-bounds dummy, the codebook buffer (73 KB, beyond the
+    // 1.6 KB a lane's offsets reach), stores into the sink after the
+    // partials, and counts as dead.
+    const int g = lane >> 4, rq = lane & 15;
+    const uint32_t off = kind ? off1 : off0;
+    const size_t rstride = (size_t)nv * 192;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    g_u8 *dummy = as_global((const uint8_t *)booksT) + rq * 12;
+    float *sink = part + (size_t)(span > 1 ? P : gridDim.z) * kinds * nch * M;
+    auto src_of = [&](int vb, bool &lv, float *&out) -> g_u8 * {
+        const uint8_t *r = nullptr;
+        int q = 0, rb = 0;
+        if (vb < vhi) { q = vb / nb; rb = vb - q * nb; r = s_rec[q]; }
+        lv = r != nullptr;
+        out = vb < vhi ? part + (((size_t)(p0 + q) * kinds + kind) * nch + c) * (size_t)M + rb * 64 + rq * 4
+                       : sink + rq * 4;
+        return r ? as_global(r) + off + (size_t)v0 * 192 + (size_t)rb * rstride + rq * 12 : dummy;
+    };
+    uint3 buf[VC];
+    bool live;
+    float *outp;
+    {
+        g_u8 *pp = src_of(vlo + 4 * wv + g, live, outp);
+#pragma unroll
+        for (int k = 0; k < VC; k++) buf[k] = *(g_uint3 *)(pp + k * 192);
+    }
+
     // L[v][s][c] = fma chain over d from 0 (the engine's AVX-512 order).
-    // A thread owns one (stage, code): its 8 codebook values stay in
-    // registers while it sweeps the chunk's positions.
-    const float *bT = booksT + (size_t)(cb + kind * 3) * 8 * 256;
-    for (int q = tid; q < LUT_PER_V; q += blockDim.x) {
-        const float *cr = bT + (size_t)(q >> 8) * 8 * 256 + (q & 255);
-        float cv[8];
+    // A thread owns one (stage, code) per pass: its 8 codebook values stay
+    // in registers while it sweeps the chunk's positions.
 #pragma unroll
-        for (int d = 0; d < 8; d++) cv[d] = cr[d * 256];
-        for (int v = 0; v < vcount; v++) {
-            const float *xx = xs + v * 8;
-            float a = 0.0f;
+    for (int i = 0; i < LUT_ITERS; i++) {
+        const int q = tid + i * VQ_THREADS;
+        if (q < LUT_PER_V) {
+#pragma unroll 1
+            for (int v = 0; v < VC; v++) {
+                float a = 0.0f;
 #pragma unroll
-            for (int d = 0; d < 8; d++) a = __fmaf_rn(xx[d], cv[d], a);
-            lut[v * LUT_PER_V + q] = a;
+                for (int d = 0; d < 8; d++) a = __fmaf_rn(xs[v * 8 + d], cv[i][d], a);
+                lut[v * LUT_PER_V + q] = a;
+            }
         }
     }
     __syncthreads();
 
-    for (int k = 0; rb0 + k * nw < rb_hi; k += 2) {
+    bool unbound = false;
+    const int iters = (vhi - vlo + 4 * nw - 1) / (4 * nw);
+    for (int it = 0; it < iters; it++) {
+        const bool was = live;
+        float *o = outp;
+        bool ln;
+        float *on;
+        g_u8 *pn = src_of(vlo + 4 * (wv + (it + 1) * nw) + g, ln, on);
+        float acc[4];
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int rb = rb0 + (k + q) * nw;
-            if (rb >= rb_hi) break;
-            const float acc = apply_block(lut, vcount, cur[q]);
-            const int r = rb * 64 + lane;
-            if (r < M) out[r] = acc;
+        for (int k = 0; k < VC; k++) {
+            const float *L = lut + k * LUT_PER_V;
+            const uint32_t u[3] = {buf[k].x, buf[k].y, buf[k].z};
+            buf[k] = *(g_uint3 *)(pn + k * 192);                   // next group, same position
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int b0 = 3 * r, b1 = 3 * r + 1, b2 = 3 * r + 2;
+                const uint32_t i0 = (u[b0 >> 2] >> ((b0 & 3) * 8)) & 255;
+                const uint32_t i1 = (u[b1 >> 2] >> ((b1 & 3) * 8)) & 255;
+                const uint32_t i2 = (u[b2 >> 2] >> ((b2 & 3) * 8)) & 255;
+                const float t = (L[i0] + L[256 + i1]) + L[512 + i2];
+                acc[r] = k == 0 ? t : acc[r] + t;
+            }
         }
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-#pragma unroll
-            for (int v = 0; v < VC; v++) cur[q][v] = nxt[q][v];
-            const int rn = rb0 + (k + 4 + q) * nw;
-            if (rn < rb_hi) load_block(idx + (size_t)rn * nv * 192, vcount, nxt[q]);
-        }
+        *(float4 *)o = was ? make_float4(acc[0], acc[1], acc[2], acc[3]) : make_float4(0, 0, 0, 0);
+        unbound |= !was && o < sink;
+        live = ln;
+        outp = on;
     }
+    if (unbound) atomicOr(err, 1);
 }
 
 // Two symbols for one body, so that profiles tell the gate/up pass (two
 // kinds per pair, the hidden-wide tables) from the down pass.
-#define VQ_THREADS 512
 #define VQ_KERNEL(NAME)                                                                         \
-    __global__ void __launch_bounds__(VQ_THREADS)                                               \
+    __global__ void __launch_bounds__(VQ_THREADS) __attribute__((amdgpu_waves_per_eu(8)))       \
     NAME(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,         \
          const int32_t *__restrict__ pair_src, const void *__restrict__ src, int src_ld,        \
          int src_bf16, const float *__restrict__ booksT, int cb, uint32_t off0, uint32_t off1,  \
-         int kinds, int M, int nv, int nch, int rsplit, float *__restrict__ part,               \
-         int *__restrict__ err)                                                                 \
+         int kinds, int M, int nv, int nch, int rsplit, int P, int span,                        \
+         float *__restrict__ part, int *__restrict__ err)                                       \
     {                                                                                           \
         vq_apply_body(recs, pair_exp, pair_src, src, src_ld, src_bf16, booksT, cb, off0, off1,  \
-                      kinds, M, nv, nch, rsplit, part, err);                                    \
+                      kinds, M, nv, nch, rsplit, P, span, part, err);                           \
     }
 VQ_KERNEL(k_vq_gate_up)
 VQ_KERNEL(k_vq_down)
 
 extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
 {
+    // whole row blocks and chunks; 4-byte aligned index streams; a spanning
+    // launch covers every pair (all read one source row)
+    const int span = a->span > 1 ? a->span : 1;
+    const int rows = (a->M / 64) * (span > 1 ? a->P : 1);
+    if (a->M <= 0 || a->M % 64 || a->nv <= 0 || a->nv % VC || a->idx_off[0] % 4 || a->idx_off[1] % 4 ||
+        a->P < 1 || a->rsplit < 1 || a->rsplit > rows || (span > 1 && (span != a->P || span > SPAN_MAX)))
+        return (int)hipErrorInvalidValue;
     const int nch = whip_vq_chunks(a->nv);
-    dim3 grid(nch, a->kinds * a->rsplit, a->P);
+    dim3 grid(nch, a->kinds * a->rsplit, span > 1 ? 1 : a->P);
     hipLaunchKernelGGL(a->kinds == 2 ? k_vq_gate_up : k_vq_down, grid, dim3(VQ_THREADS), 0, s, a->recs,
                        a->pair_exp, a->pair_src, a->src, a->src_ld, a->src_bf16, a->booksT, a->cb,
-                       a->idx_off[0], a->idx_off[1], a->kinds, a->M, a->nv, nch, a->rsplit,
+                       a->idx_off[0], a->idx_off[1], a->kinds, a->M, a->nv, nch, a->rsplit, a->P, span,
                        a->part, a->err);
     return (int)hipGetLastError();
 }
 
 // ---- SwiGLU over the reduced gate/up partials ------------------------------
-// A workgroup owns 128 rows of one pair: 32 float4 row groups x 8 slices of
-// the chunk range, so every thread has its whole slice's loads in flight;
-// the slices are then added in chunk order.
-#define ACT_ROWS 128
-#define ACT_SLICES 8
+// A workgroup owns 64 rows of one pair: thread (slice, row group of 4) sums
+// its slice of the chunk partials for gate and up with every load in flight
+// (clamped addresses, no branches around loads); the slices then meet in
+// chunk order through LDS.
+#define ACT_ROWS 64
+#define ACT_SLICES 16
+#define RED_BATCH 8
+
+// sum of partial rows [c0, c1) of a [nch][ld] block at column r0 (float4)
+__device__ __forceinline__ float4 sum_chunks(const float *__restrict__ base, size_t ld, int c0, int c1)
+{
+    float4 acc = make_float4(0, 0, 0, 0);
+    for (int cb = c0; cb < c1; cb += RED_BATCH) {
+        float4 v[RED_BATCH];
+#pragma unroll
+        for (int k = 0; k < RED_BATCH; k++) {
+            const int c = cb + k < c1 ? cb + k : c0;
+            v[k] = *(const float4 *)(base + (size_t)c * ld);
+        }
+#pragma unroll
+        for (int k = 0; k < RED_BATCH; k++)
+            if (cb + k < c1) { acc.x += v[k].x; acc.y += v[k].y; acc.z += v[k].z; acc.w += v[k].w; }
+    }
+    return acc;
+}
 
 __global__ void __launch_bounds__(256)
 k_vq_act(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
@@ -173,50 +232,38 @@ k_vq_act(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pa
 {
     __shared__ float4 red[2][ACT_SLICES][ACT_ROWS / 4];
     const int p = blockIdx.y, tid = threadIdx.x;
-    const int g = tid & 31, sl = tid >> 5;
+    const int g = tid & (ACT_ROWS / 4 - 1), sl = tid / (ACT_ROWS / 4);
     const int r0 = blockIdx.x * ACT_ROWS + g * 4;
     const int per = (nch + ACT_SLICES - 1) / ACT_SLICES;
-    const int c0 = sl * per, c1 = min(nch, c0 + per);
+    const int c0 = min(nch, sl * per), c1 = min(nch, c0 + per);
+    // the record (uniform per workgroup) and this row group's scales are
+    // fetched before the partials, so they are in hand after the barrier
+    const uint8_t *rec = recs[pair_exp[p]];
+    uint16_t rsg[4] = {0, 0, 0, 0}, rsu[4] = {0, 0, 0, 0};
+    if (rec && r0 < I) {
+        g_u16 *sc = (g_u16 *)(as_global(rec) + sc_off);
+#pragma unroll
+        for (int q = 0; q < 4; q++) { rsg[q] = sc[r0 + q]; rsu[q] = sc[I + r0 + q]; }
+    }
     float4 sg = make_float4(0, 0, 0, 0), su = sg;
     if (r0 < I) {
-        const float *gp = part + ((size_t)p * 2 + 0) * nch * (size_t)I + r0;
-        const float *up = part + ((size_t)p * 2 + 1) * nch * (size_t)I + r0;
-        float4 vg[8], vu[8];
-        for (int cb = c0; cb < c1; cb += 8) {
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-                if (cb + k < c1) {
-                    vg[k] = *(const float4 *)(gp + (size_t)(cb + k) * I);
-                    vu[k] = *(const float4 *)(up + (size_t)(cb + k) * I);
-                }
-#pragma unroll
-            for (int k = 0; k < 8; k++)
-                if (cb + k < c1) {
-                    sg.x += vg[k].x; sg.y += vg[k].y; sg.z += vg[k].z; sg.w += vg[k].w;
-                    su.x += vu[k].x; su.y += vu[k].y; su.z += vu[k].z; su.w += vu[k].w;
-                }
-        }
+        sg = sum_chunks(part + ((size_t)p * 2 + 0) * nch * (size_t)I + r0, I, c0, c1);
+        su = sum_chunks(part + ((size_t)p * 2 + 1) * nch * (size_t)I + r0, I, c0, c1);
     }
     red[0][sl][g] = sg;
     red[1][sl][g] = su;
     __syncthreads();
-    if (tid >= 32 || r0 >= I) return;
+    if (tid >= ACT_ROWS / 4 || r0 >= I) return;
     float gg[4] = {0, 0, 0, 0}, uu[4] = {0, 0, 0, 0};
     for (int k = 0; k < ACT_SLICES; k++) {
         const float4 a = red[0][k][g], b = red[1][k][g];
         gg[0] += a.x; gg[1] += a.y; gg[2] += a.z; gg[3] += a.w;
         uu[0] += b.x; uu[1] += b.y; uu[2] += b.z; uu[3] += b.w;
     }
-    const uint8_t *rec = recs[pair_exp[p]];
     float out[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        float sgc = 0.0f, suc = 0.0f;
-        if (rec) {
-            const uint16_t *sc = (const uint16_t *)(rec + sc_off);
-            sgc = wh_f16_scale(sc[r0 + q]);
-            suc = wh_f16_scale(sc[I + r0 + q]);
-        }
+        const float sgc = rec ? wh_f16_scale(rsg[q]) : 0.0f, suc = rec ? wh_f16_scale(rsu[q]) : 0.0f;
         out[q] = wh_silu_mul(__fmul_rn(gg[q], sgc), __fmul_rn(uu[q], suc));
     }
     *(float4 *)(h + (size_t)p * I + r0) = make_float4(out[0], out[1], out[2], out[3]);
@@ -233,10 +280,14 @@ extern "C" int whip_vq_act(const uint8_t *const *recs, const int32_t *pair_exp, 
 }
 
 // ---- weighted combine + shared expert --------------------------------------
-// A workgroup owns 128 output rows of one token: thread (row group, pair
-// slot j) reduces pair j's chunk partials for 4 rows (all loads in flight)
-// and scales them; the pairs are then added in the token's combine order.
-#define CMB_ROWS 128
+// A workgroup owns 32 output rows of one token.  Work item (pair slot j,
+// chunk slice) of a row group of 4 sums its slice of pair j's down partials;
+// items are spread over the workgroup's threads so that every load of a
+// thread is in flight at once.  Then the first threads add, per row group,
+// the slices of each pair, scale by f16(scale) and the route weight, and add
+// the pairs in the token's combine order, then the shared expert.
+#define CMB_ROWS 32
+#define CMB_SLICES 4
 
 __global__ void __launch_bounds__(256)
 k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
@@ -244,44 +295,54 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
           const float *__restrict__ part_d, int nch, int H, uint32_t sc_off_down,
           int skip_zero, const float *__restrict__ sh, float *__restrict__ y)
 {
-    extern __shared__ float4 cred[];                 // [K][32]
+    // [K][CMB_SLICES][G] slice sums, [K][G] row scales, [K] weights, [K] live
+    extern __shared__ float4 cred[];
+    constexpr int G = CMB_ROWS / 4;
+    float4 *csc = cred + K * CMB_SLICES * G;
+    float *cw = (float *)(csc + K * G);
+    int *cl = (int *)(cw + K);
     const int t = blockIdx.y, tid = threadIdx.x;
-    const int g = tid & 31;
+    const int g = tid % G;
     const int r0 = blockIdx.x * CMB_ROWS + g * 4;
-    for (int j = tid >> 5; j < K; j += 8) {
-        float4 acc = make_float4(0, 0, 0, 0);
+    const int per = (nch + CMB_SLICES - 1) / CMB_SLICES;
+    for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G) {
+        const int j = it / CMB_SLICES, sl = it % CMB_SLICES;
         const int p = tok_pairs[t * K + j];
         const float wj = pair_w[p];
-        if (r0 < H && !(skip_zero && wj == 0.0f)) {
-            const uint8_t *rec = recs[pair_exp[p]];
-            const float *pd = part_d + (size_t)p * nch * H + r0;
-            float4 s = make_float4(0, 0, 0, 0);
-            for (int cb = 0; cb < nch; cb += 8) {
-                float4 v[8];
+        const uint8_t *rec = recs[pair_exp[p]];
+        const bool live = rec && !(skip_zero && wj == 0.0f);   // else the pair adds nothing
+        uint16_t rs[4] = {0, 0, 0, 0};
+        if (sl == 0 && live && r0 < H) {
+            g_u16 *sc = (g_u16 *)(as_global(rec) + sc_off_down) + r0;
 #pragma unroll
-                for (int k = 0; k < 8; k++)
-                    if (cb + k < nch) v[k] = *(const float4 *)(pd + (size_t)(cb + k) * H);
-#pragma unroll
-                for (int k = 0; k < 8; k++)
-                    if (cb + k < nch) { s.x += v[k].x; s.y += v[k].y; s.z += v[k].z; s.w += v[k].w; }
-            }
-            if (rec) {
-                const uint16_t *sc = (const uint16_t *)(rec + sc_off_down) + r0;
-                acc.x = __fmul_rn(wj, __fmul_rn(s.x, wh_f16_scale(sc[0])));
-                acc.y = __fmul_rn(wj, __fmul_rn(s.y, wh_f16_scale(sc[1])));
-                acc.z = __fmul_rn(wj, __fmul_rn(s.z, wh_f16_scale(sc[2])));
-                acc.w = __fmul_rn(wj, __fmul_rn(s.w, wh_f16_scale(sc[3])));
-            }
+            for (int q = 0; q < 4; q++) rs[q] = sc[q];
         }
-        cred[j * 32 + g] = acc;
+        const int c0 = min(nch, sl * per), c1 = min(nch, c0 + per);
+        float4 v = make_float4(0, 0, 0, 0);
+        if (r0 < H && live) v = sum_chunks(part_d + (size_t)p * nch * H + r0, H, c0, c1);
+        cred[(j * CMB_SLICES + sl) * G + g] = v;
+        if (sl == 0) {
+            csc[j * G + g] = make_float4(wh_f16_scale(rs[0]), wh_f16_scale(rs[1]), wh_f16_scale(rs[2]),
+                                         wh_f16_scale(rs[3]));
+            if (g == 0) { cw[j] = wj; cl[j] = live; }
+        }
     }
     __syncthreads();
-    if (tid >= 32 || r0 >= H) return;
+    if (tid >= G || r0 >= H) return;
     float o[4] = {0, 0, 0, 0};
     for (int j = 0; j < K; j++) {                    // combine order
-        const float4 a = cred[j * 32 + g];
-        o[0] = __fadd_rn(o[0], a.x); o[1] = __fadd_rn(o[1], a.y);
-        o[2] = __fadd_rn(o[2], a.z); o[3] = __fadd_rn(o[3], a.w);
+        if (!cl[j]) continue;                        // unbound, or a skipped zero weight
+        const float wj = cw[j];
+        float sum[4] = {0, 0, 0, 0};
+        for (int sl = 0; sl < CMB_SLICES; sl++) {
+            const float4 a = cred[(j * CMB_SLICES + sl) * G + g];
+            sum[0] += a.x; sum[1] += a.y; sum[2] += a.z; sum[3] += a.w;
+        }
+        const float4 sc = csc[j * G + g];
+        o[0] = __fadd_rn(o[0], __fmul_rn(wj, __fmul_rn(sum[0], sc.x)));
+        o[1] = __fadd_rn(o[1], __fmul_rn(wj, __fmul_rn(sum[1], sc.y)));
+        o[2] = __fadd_rn(o[2], __fmul_rn(wj, __fmul_rn(sum[2], sc.z)));
+        o[3] = __fadd_rn(o[3], __fmul_rn(wj, __fmul_rn(sum[3], sc.w)));
     }
     float4 r;
     const float *shr = sh ? sh + (size_t)t * H + r0 : nullptr;
@@ -297,10 +358,11 @@ extern "C" int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                             const float *part_d, int nch, int H, uint32_t sc_off_down,
                             int skip_zero, const float *sh, float *y, hipStream_t s)
 {
-    if (H % 4) return (int)hipErrorInvalidValue;
+    if (H % 4 || K < 1 || K > 64) return (int)hipErrorInvalidValue;
     dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
-    hipLaunchKernelGGL(k_combine, grid, dim3(256), (size_t)K * 32 * sizeof(float4), s, recs,
-                       pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, sh, y);
+    const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
+    hipLaunchKernelGGL(k_combine, grid, dim3(256), lds, s,
+                       recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, sh, y);
     return (int)hipGetLastError();
 }
 

@@ -115,6 +115,16 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
     free(m);
 }
 
+/* splits of a spanning launch: about 1024 workgroups (four 512-thread
+ * workgroups on each of 256 CUs), at least one row block per wavefront */
+static int pick_span_split(int work_groups, int row_blocks)
+{
+    int r = (1024 + work_groups - 1) / (work_groups > 0 ? work_groups : 1);
+    const int cap = row_blocks / 8 > 0 ? row_blocks / 8 : 1;
+    if (r > cap) r = cap;
+    return r < 1 ? 1 : r;
+}
+
 static int pick_rsplit(int work_groups, int row_blocks)
 {
     /* enough workgroups to cover 256 CUs a few times, at least one row
@@ -172,9 +182,10 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->pair_exp, (size_t)P * 4);
     rc |= dmalloc((void **)&m->pair_w, (size_t)P * 4);
     rc |= dmalloc((void **)&m->tok_pairs, (size_t)P * 4);
-    rc |= dmalloc((void **)&m->part_gu, (size_t)P * 2 * m->nch_gu * m->I * 4);
+    /* + 64 floats: the apply kernels' sink for rows past a split's end */
+    rc |= dmalloc((void **)&m->part_gu, ((size_t)P * 2 * m->nch_gu * m->I + 64) * 4);
     rc |= dmalloc((void **)&m->h, (size_t)P * m->I * 4);
-    rc |= dmalloc((void **)&m->part_d, (size_t)P * m->nch_d * m->H * 4);
+    rc |= dmalloc((void **)&m->part_d, ((size_t)P * m->nch_d * m->H + 64) * 4);
     rc |= dmalloc((void **)&m->err, 64);
     if (rc || !m->h_recs) { waste_hip_moe_destroy(m); return WASTE_HIP_ENOMEM; }
     if (hipMemset(m->d_recs, 0, ((size_t)m->E + 1) * sizeof(void *)) != hipSuccess ||
@@ -330,6 +341,7 @@ int waste_hip_moe_bind_expert(waste_hip_moe *m, int expert, const void *dev_reco
 {
     if (!m || expert < 0 || expert >= m->E) return WASTE_HIP_EINVAL;
     if (!dev_record) return set_ptr(m, expert, NULL);
+    if ((uintptr_t)dev_record % 16) return WASTE_HIP_EINVAL;   /* the kernels' 12-byte loads */
     if (rec_bytes != m->rec_bytes) return WASTE_HIP_ERECORD;
     uint8_t hdr[48];
     CK(hipMemcpy(hdr, dev_record, 48, hipMemcpyDeviceToHost));
@@ -382,6 +394,11 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.kinds = 2; a.M = I; a.nv = m->nv_gu; a.P = P; a.rsplit = m->rsplit_gu;
     a.part = m->part_gu; a.err = m->err;
+    if (T == 1 && P <= 64) {
+        /* one token: every pair's gate/up table is the same */
+        a.span = P;
+        a.rsplit = pick_span_split(m->nch_gu * 2, P * (I / 64));
+    }
     CK((hipError_t)whip_vq_apply(&a, s));
     MARK(3);
     CK((hipError_t)whip_vq_act(m->d_recs, m->pair_exp, P, m->part_gu, m->nch_gu, I, m->off_sc,
@@ -390,6 +407,7 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb + 6;
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
     a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
+    a.span = 0;
     CK((hipError_t)whip_vq_apply(&a, s));
     MARK(5);
     if (m->has_shared)
@@ -437,8 +455,10 @@ int waste_hip_moe_status(waste_hip_moe *m, void *stream)
     CK(hipStreamSynchronize((hipStream_t)stream));
     CK(hipMemcpy(&e, m->err, sizeof e, hipMemcpyDeviceToHost));
     CK(hipMemset(m->err, 0, sizeof e));
-    if (e & 1) return WASTE_HIP_EUNBOUND;
+    /* a failed route leaves ids of -1, which the expert kernels then see
+     * as unbound: report the cause */
     if (e & 2) return WASTE_HIP_EROUTE;
+    if (e & 1) return WASTE_HIP_EUNBOUND;
     return 0;
 }
 
