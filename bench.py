@@ -116,6 +116,22 @@ def cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, budget_s, nthreads):
     return n, t_used, isa
 
 
+def measured_traffic(dom, config, batch):
+    """HBM bytes per launch of the dominant kernel, as measured by the two
+    rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE, each scaled by a copy of
+    known size) whose summary is kept in profiles/; None without one."""
+    kernel = "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_down"
+    path = os.path.join(ROOT, "profiles", f"{kernel}-{config}-decode-b{batch}-hbm-traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,6 +142,9 @@ def main():
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MB",
+                    help="first copy MB megabytes device to device (a plain copy kernel of known "
+                         "size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build's MoE path runs on a single MI355X and "
@@ -141,6 +160,15 @@ def main():
     H, E, K, I = cfg["hidden"], cfg["n_experts"], cfg["top_k"], cfg["moe_inter"]
     B = a.batch
     layers, slab, books, rb, trunk = build_layers(torch, warp_amd, synth, cfg, a.layers, B)
+    if a.copy_calibrate:
+        n = a.copy_calibrate << 20
+        src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copied {a.copy_calibrate} MiB device to device 3 times (counter scale)")
+        del src, dst
 
     gen = torch.Generator(device="cpu").manual_seed(0)
     n_tok = (a.warmup + a.steps + 8) * B
@@ -215,6 +243,7 @@ def main():
     dom_bytes = (2 * idx_gu if dom == "routed_gate_up" else idx_d) * u_mean
     dom_ms = stage_ms[dom]
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
+    traffic = measured_traffic(dom, a.config, B)
 
     cpu = None
     if not a.no_cpu and B == 1:
@@ -252,7 +281,7 @@ def main():
         "stage_us": {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
         "roofline": {"bound": "hbm", "kernel": "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_down",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "launch_us": round(dom_ms * 1e3, 2), "algorithmic_bytes": int(dom_bytes)},
         "cpu_baseline": cpu,
     }
