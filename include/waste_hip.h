@@ -40,6 +40,8 @@ extern "C" {
 #define WASTE_HIP_EUNBOUND  (-6)   /* a routed expert has no record      */
 #define WASTE_HIP_EROUTE    (-7)   /* a selection pass found no expert   */
 #define WASTE_HIP_EDEVICE   (-8)   /* a HIP runtime call failed          */
+#define WASTE_HIP_ERANGE    (-9)   /* an fp16 operand of the many-token
+                                      path was out of range              */
 
 /* Library name and device check.  NULL when no usable gfx950 device. */
 const char *waste_hip_device_name(void);
@@ -84,6 +86,8 @@ typedef struct {
     int layer;           /* the layer id records must carry                 */
     int max_tokens;      /* largest T forward() will see                    */
     int verify_records;  /* check each record's crc32 when it is loaded     */
+    int prefill_min_tokens; /* T above this runs the grouped matrix-core
+                            path (0: 32); T up to it the decode kernels   */
 } waste_hip_moe_cfg;
 
 /* A trunk tensor as the engine holds it (waste_tensor, src/model.h:32-50):
@@ -125,7 +129,10 @@ int waste_hip_moe_bind_expert(waste_hip_moe *m, int expert,
  *   ids, w  [T][K] selection (device, may be NULL)
  *   logits  [T][E] router logits (device, may be NULL)
  * T == 1 follows moe_layer (combine in selection order); T > 1 follows
- * moe_chunk (ascending expert order, zero weights skipped).  Enqueued on
+ * moe_chunk (ascending expert order, zero weights skipped).  T above
+ * prefill_min_tokens sorts the pairs by expert and runs each expert's
+ * tokens as one product on the matrix cores (fp16 operands, fp32
+ * accumulation; the router in fp32).  Enqueued on
  * `stream` (a hipStream_t; NULL = the null stream).  Device-side failures
  * (an unbound expert, a routing pass with no candidate) are sticky: read
  * them with waste_hip_moe_status. */
@@ -134,7 +141,7 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T,
                           void *stream);
 
 /* Waits for the layer's work and returns the sticky device error (0, or
- * WASTE_HIP_EUNBOUND / WASTE_HIP_EROUTE), clearing it. */
+ * WASTE_HIP_EROUTE / WASTE_HIP_EUNBOUND / WASTE_HIP_ERANGE), clearing it. */
 int waste_hip_moe_status(waste_hip_moe *m, void *stream);
 
 /* Bytes the layer reads from HBM for one forward that touches `n_distinct`

@@ -20,9 +20,10 @@ WQ_F32, WQ_Q8G, WQ_Q4G, WQ_VQ3R = 0, 2, 3, 4
 SCORE_SIGMOID, SCORE_SOFTMAX, SCORE_SQRTSOFTPLUS = 0, 1, 2
 
 ERRORS = {0: "ok", -1: "EINVAL", -2: "ENODEV", -3: "ENOMEM", -4: "ERECORD", -5: "ECRC",
-          -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE"}
+          -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE", -9: "ERANGE"}
 
-OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE = 0, -1, -2, -3, -4, -5, -6, -7, -8
+OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE, ERANGE = \
+    0, -1, -2, -3, -4, -5, -6, -7, -8, -9
 
 # Every symbol include/waste_hip.h declares.
 EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_host_buffers",
@@ -46,7 +47,7 @@ class MoeCfg(C.Structure):
                 ("moe_inter", C.c_int), ("n_shared", C.c_int), ("score_func", C.c_int),
                 ("renorm", C.c_int), ("routed_scale", C.c_float), ("n_group", C.c_int),
                 ("topk_group", C.c_int), ("layer", C.c_int), ("max_tokens", C.c_int),
-                ("verify_records", C.c_int)]
+                ("verify_records", C.c_int), ("prefill_min_tokens", C.c_int)]
 
 
 class HipTensor(C.Structure):
@@ -126,10 +127,11 @@ class MoeLayer:
 
     def __init__(self, *, hidden, n_experts, top_k, moe_inter, n_shared=0, score_func=0,
                  renorm=0, routed_scale=1.0, n_group=1, topk_group=1, layer=0,
-                 max_tokens=1, verify_records=0):
+                 max_tokens=1, verify_records=0, prefill_min_tokens=0):
         self.L = lib()
         self.cfg = MoeCfg(hidden, n_experts, top_k, moe_inter, n_shared, score_func, renorm,
-                          routed_scale, n_group, topk_group, layer, max_tokens, verify_records)
+                          routed_scale, n_group, topk_group, layer, max_tokens, verify_records,
+                          prefill_min_tokens)
         h = C.c_void_p()
         check(self.L.waste_hip_moe_create(C.byref(self.cfg), C.byref(h)), "waste_hip_moe_create")
         self.h = h

@@ -96,6 +96,59 @@ int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                  const float *part_d, int nch, int H, uint32_t sc_off_down,
                  int skip_zero, const float *sh, float *y, hipStream_t s);
 
+/* ---- many tokens (prefill.hip) ---- */
+
+/* Stable sort of the T*K pairs by expert (id -1 after the last expert);
+ * each token's pairs in ascending expert order in tok_pairs; seg_off[e] ..
+ * seg_off[e+1] is expert e's segment (E+2 entries); order[] the experts by
+ * descending pair count. */
+int whip_sort_pairs(const int32_t *ids, const float *w, int T, int K, int E,
+                    int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
+                    int32_t *tok_pairs, int32_t *pair_pos, int32_t *seg_off,
+                    int32_t *order, hipStream_t s);
+
+/* One grouped product on the matrix cores (fp16 in, fp32 accumulate).
+ * B: VQ3R records (recs set; kind k's indices at idx_off[k], row scales at
+ * sc_off[k], books cb + 3k of books16) or trunk matrices W0/W1 (fmt
+ * F32/Q8G/Q4G).  A: rows of x (fp32, bf16 or fp16) — segment position p
+ * reads row tok[p] (tok NULL: p).  pair = 1: out[p][n] = silu(gate) * up
+ * as fp16; pair = 0: out[p][n] fp32 (times the VQ3R row scale).
+ * Segments: seg_off/order as whip_sort_pairs writes them (segs of them),
+ * or seg_off NULL for one segment of `rows` rows.  mblocks: 128-row blocks
+ * per segment the grid covers. */
+typedef struct {
+    const uint8_t *const *recs;
+    uint32_t idx_off[2], sc_off[2];
+    const uint16_t *books16;     /* fp16 [n_books][256][8], subnormals flushed */
+    int cb;
+    const uint8_t *W0, *W1;
+    const uint16_t *S0, *S1;
+    size_t rowbytes;
+    int group;
+    int N, Kd;                   /* rows per matrix, reduction length        */
+    const void *x;
+    int x_mode, x_ld;            /* 0 fp32, 1 bf16, 2 fp16                   */
+    const int32_t *tok;
+    const int32_t *seg_off, *order;
+    int rows;
+    void *out;
+    int out_ld;
+    int *err;
+} whip_pf_args;
+int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int segs, int mblocks, hipStream_t s);
+
+/* Router logits for T tokens on the matrix cores (fp32 products), through
+ * part[whip_pf_router_part_floats(T, E)]. */
+size_t whip_pf_router_part_floats(int T, int E);
+int whip_pf_router(const whip_mat *W, const void *x, int x_bf16, int T, float *part,
+                   float *logits, hipStream_t s);
+
+/* y[t] = sum over t's pairs (tok_pairs order; zero weights and unbound
+ * experts skipped) of w * Y[p], + sh[t] (sh may be NULL). */
+int whip_pf_combine(const int32_t *tok_pairs, const int32_t *pair_exp, const float *pair_w,
+                    const uint8_t *const *recs, int T, int K, int E, const float *Y, int H,
+                    const float *sh, float *y, hipStream_t s);
+
 /* Materialised dequantisation of one VQ3R matrix (fp32 [M][N]). */
 int whip_dequant(const uint8_t *idx, const uint16_t *scale, const float *books,
                  int cb, int M, int N, float *W, hipStream_t s);

@@ -1,0 +1,464 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// prefill.hip — the MoE layer over many tokens (moe_chunk,
+// src/model.c:7110-7285) as grouped GEMMs on the matrix cores.
+//
+// Pairs (token, selected expert) are sorted by expert, so each expert's
+// tokens form one segment; every expert's weights are then read once per
+// block of up to 128 of its tokens, not once per pair.  Per segment:
+//
+//   h[p]  = silu(X[tok(p)] . Wg^T * sg) * (X[tok(p)] . Wu^T * su)   (fp16)
+//   Y[p]  = h[p] . Wd^T * sd                                         (fp32)
+//   y[t]  = sum over t's pairs, ascending expert, zero weights skipped,
+//           of w * Y[p]; plus the shared expert
+//
+// The products run on v_mfma_f32_32x32x16_f16: tokens on M (32 per tile,
+// four tiles per workgroup), output rows on N, fp32 accumulation.  Lane l
+// of the B operand holds W[n0 + l%32][k0 + 8(l/32) .. +8): exactly one
+// (row, position) vector of the container, which the lane decodes itself —
+// VQ3R: C0[i0] + (C1[i1] + C2[i2]) from the fp16 codebooks in LDS (the
+// container stores them in fp16, subnormals flushed as the engine's loader
+// does); Q4G / Q8G: the integer times its group scale.  Row scales of VQ3R
+// apply in the epilogue, exactly, in fp32.  A (activations) is staged in LDS
+// per 64-wide k chunk, converted to fp16; a value outside fp16's range
+// raises the sticky range error instead of turning into inf.
+//
+// The router runs on v_mfma_f32_32x32x2_f32 (fp32 products, so the logits
+// stay within the decode path's 1e-5 and routing decisions keep their
+// meaning), split over k with the partial sums added in a fixed order.
+#include "common.h"
+#include "launch.h"
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float acc16 __attribute__((ext_vector_type(16)));
+
+#define ERR_RANGE 4                  // sticky error bit: fp16 range exceeded
+
+// ---- pair sort ---------------------------------------------------------------
+// Stable counting sort of the T*K pairs by expert (failed selections, id -1,
+// go to the segment after the last expert), in (token, slot) order within
+// an expert; each token's pairs listed in ascending expert order (the
+// chunk's combine order); experts ranked by size, largest first, so the
+// longest segments are dispatched first.
+#define SORT_THREADS 1024
+
+__global__ void __launch_bounds__(SORT_THREADS)
+k_sort_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T, int K, int E,
+             int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp, float *__restrict__ pair_w,
+             int32_t *__restrict__ tok_pairs, int32_t *__restrict__ pair_pos,
+             int32_t *__restrict__ seg_off, int32_t *__restrict__ order)
+{
+    extern __shared__ int sm[];
+    const int NE = E + 1, P = T * K, tid = threadIdx.x;
+    int *cnt = sm, *off = sm + NE, *run = sm + 2 * NE;
+    for (int i = tid; i < NE; i += SORT_THREADS) { cnt[i] = 0; run[i] = 0; }
+    __syncthreads();
+    for (int q = tid; q < P; q += SORT_THREADS) atomicAdd(&cnt[ids[q] < 0 ? E : ids[q]], 1);
+    __syncthreads();
+    if (tid < 64) {                                   // exclusive scan, one wave
+        const int per = (NE + 63) / 64;
+        int s = 0;
+        for (int i = 0; i < per; i++) { const int k = tid * per + i; if (k < NE) s += cnt[k]; }
+        int inc = s;
+        for (int o = 1; o < 64; o <<= 1) { const int v = __shfl_up(inc, o, 64); if (tid >= o) inc += v; }
+        int base = inc - s;
+        for (int i = 0; i < per; i++) {
+            const int k = tid * per + i;
+            if (k < NE) { off[k] = base; base += cnt[k]; }
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {                                   // stable scatter, 64 pairs at a time, in order
+        const uint64_t lt = (1ull << tid) - 1, gt = ~lt & ~(1ull << tid);
+        for (int c0 = 0; c0 < P; c0 += 64) {
+            const int q = c0 + tid;
+            const bool valid = q < P;
+            const int e = valid ? (ids[q] < 0 ? E : ids[q]) : 0;
+            uint64_t m = __ballot(valid);
+            for (int b = 0; b < 11; b++) {            // lanes holding the same expert
+                const bool bit = (e >> b) & 1;
+                const uint64_t bb = __ballot(bit);
+                m &= bit ? bb : ~bb;
+            }
+            if (valid) {
+                const int base = run[e];
+                const int p = off[e] + base + __popcll(m & lt);
+                pair_pos[q] = p;
+                pair_tok[p] = q / K;
+                pair_exp[p] = e;
+                pair_w[p] = w[q];
+                if (!(m & gt)) run[e] = base + __popcll(m);
+            }
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < P; q += SORT_THREADS) {
+        const int t = q / K, j = q - t * K;
+        const int e = ids[q] < 0 ? E : ids[q];
+        int rk = 0;
+        for (int j2 = 0; j2 < K; j2++) {
+            const int e2 = ids[t * K + j2] < 0 ? E : ids[t * K + j2];
+            rk += e2 < e || (e2 == e && j2 < j);
+        }
+        tok_pairs[t * K + rk] = pair_pos[q];
+    }
+    for (int i = tid; i <= NE; i += SORT_THREADS) seg_off[i] = i < NE ? off[i] : P;
+    for (int e = tid; e < E; e += SORT_THREADS) {
+        const int c = cnt[e];
+        int r = 0;
+        for (int e2 = 0; e2 < E; e2++) {
+            const int c2 = cnt[e2];
+            r += c2 > c || (c2 == c && e2 < e);
+        }
+        order[r] = e;
+    }
+}
+
+extern "C" int whip_sort_pairs(const int32_t *ids, const float *w, int T, int K, int E,
+                               int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
+                               int32_t *tok_pairs, int32_t *pair_pos, int32_t *seg_off,
+                               int32_t *order, hipStream_t s)
+{
+    if (T < 1 || K < 1 || E < 1 || E > 1024) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(SORT_THREADS), (size_t)3 * (E + 1) * sizeof(int), s,
+                       ids, w, T, K, E, pair_tok, pair_exp, pair_w, tok_pairs, pair_pos, seg_off, order);
+    return (int)hipGetLastError();
+}
+
+// ---- grouped GEMM ----------------------------------------------------------
+#define PF_THREADS 512
+#define PF_MT 4                      // M tiles of 32 rows per workgroup
+#define PF_KC 64                     // k per LDS chunk
+#define PF_ALD (PF_KC + 8)           // A row stride in halves (144 B: rows fall on different banks)
+
+enum { DEC_F32 = 0, DEC_Q8 = 2, DEC_Q4 = 3, DEC_VQ = 4 };
+
+WH_INLINE _Float16 to_h(float v, bool &bad)
+{
+    bad |= !(fabsf(v) <= 65504.0f);                  // also NaN
+    return (_Float16)v;
+}
+
+WH_INLINE h8 as_h8(uint4 u) { return __builtin_bit_cast(h8, u); }
+WH_INLINE uint4 as_u4(h8 h) { return __builtin_bit_cast(uint4, h); }
+
+template <int DEC, int EPI>
+__global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
+{
+    // EPI 0: gate/up pair, N tile 128 (waves 0-3 gate, 4-7 up), SwiGLU -> fp16
+    // EPI 1: one matrix, N tile 256, fp32 rows (times the VQ3R row scale)
+    constexpr int NBOOK = DEC == DEC_VQ ? (EPI == 0 ? 6 : 3) : 1;
+    __shared__ uint4 cbk[NBOOK * 256];
+    __shared__ __attribute__((aligned(16))) _Float16 As[PF_MT * 32 * PF_ALD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int seg = a.order ? a.order[blockIdx.y] : (int)blockIdx.y;
+    const int s0 = a.seg_off ? a.seg_off[seg] : 0;
+    const int n_seg = a.seg_off ? a.seg_off[seg + 1] - s0 : a.rows;
+    const int r0 = blockIdx.z * (PF_MT * 32);        // this workgroup's rows of the segment
+    if (r0 >= n_seg) return;
+    const int mrows = min(PF_MT * 32, n_seg - r0);
+    const int kind = EPI == 0 ? wave >> 2 : 0;
+    const int ncol = blockIdx.x * (EPI == 0 ? 128 : 256) + (EPI == 0 ? (wave & 3) : wave) * 32 + (lane & 31);
+    const bool ncol_ok = ncol < a.N;
+    const int nc = ncol_ok ? ncol : 0;               // clamped row for loads
+
+    const uint8_t *rec = nullptr;
+    if (DEC == DEC_VQ) {
+        rec = a.recs[seg];
+        if (rec == nullptr) {                        // unbound expert: zeros + flag
+            for (int m = wave; m < mrows; m += PF_THREADS / 64) {
+                const size_t row = (size_t)(s0 + r0 + m);
+                if (ncol_ok) {
+                    if (EPI == 0) { if (kind == 0) ((_Float16 *)a.out)[row * a.out_ld + ncol] = (_Float16)0.0f; }
+                    else ((float *)a.out)[row * a.out_ld + ncol] = 0.0f;
+                }
+            }
+            if (tid == 0) atomicOr(a.err, 1);
+            return;
+        }
+        for (int i = tid; i < NBOOK * 256; i += PF_THREADS)
+            cbk[i] = *(const uint4 *)(a.books16 + ((size_t)(a.cb + i / 256) * 256 + (i & 255)) * 8);
+    }
+    const int nv = a.Kd / 8;
+    const size_t rstride = (size_t)nv * 192;
+    g_u8 *ib = DEC == DEC_VQ ? as_global(rec) + (kind ? a.idx_off[1] : a.idx_off[0]) + (size_t)(nc >> 6) * rstride +
+                                   (nc & 63) * 3
+                             : nullptr;
+    const uint8_t *Wrow = DEC != DEC_VQ ? (kind ? a.W1 : a.W0) + (size_t)nc * a.rowbytes : nullptr;
+    const uint16_t *Srow = (DEC == DEC_Q4 || DEC == DEC_Q8) ? (kind ? a.S1 : a.S0) + (size_t)nc * ((a.Kd + a.group - 1) / a.group)
+                                                             : nullptr;
+    bool bad = false;
+
+    acc16 acc[PF_MT];
+#pragma unroll
+    for (int t = 0; t < PF_MT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+
+    const int nchunk = a.Kd / PF_KC;
+    for (int kc = 0; kc < nchunk; kc++) {
+        // this chunk's B inputs: 4 steps of 16 k, position k0/8 + lane/32
+        uint32_t bw[4][2];
+        uint16_t bs[4];
+        float4 bf[DEC == DEC_F32 ? 4 : 1][2];
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int k = kc * PF_KC + st * 16 + 8 * (lane >> 5);
+            if (DEC == DEC_VQ) {
+                bw[st][0] = ld_u32_unaligned((const uint8_t *)(ib + (size_t)(k >> 3) * 192));
+            } else if (DEC == DEC_Q4) {
+                bw[st][0] = *(const uint32_t *)(Wrow + (k >> 1));
+                bs[st] = Srow[k / a.group];
+            } else if (DEC == DEC_Q8) {
+                const uint2 v = *(const uint2 *)(Wrow + k);
+                bw[st][0] = v.x; bw[st][1] = v.y;
+                bs[st] = Srow[k / a.group];
+            } else {                                 // F32: 8 floats, converted at use
+                const float4 f0 = *(const float4 *)(Wrow + (size_t)k * 4);
+                const float4 f1 = *(const float4 *)(Wrow + (size_t)k * 4 + 16);
+                bf[st][0] = f0; bf[st][1] = f1;
+            }
+        }
+        __syncthreads();                             // the previous chunk's A reads are done
+        // A chunk: rows r0 .. r0+mrows of the segment, 64 k, as fp16
+        for (int i = tid; i < PF_MT * 32 * (PF_KC / 8); i += PF_THREADS) {
+            const int m = i >> 3, part = i & 7;
+            h8 v;
+            if (m < mrows) {
+                const int row = a.tok ? a.tok[s0 + r0 + m] : s0 + r0 + m;
+                const size_t e0 = (size_t)row * a.x_ld + (size_t)kc * PF_KC + part * 8;
+                if (a.x_mode == 2) {
+                    v = as_h8(*(const uint4 *)((const _Float16 *)a.x + e0));
+                } else if (a.x_mode == 1) {
+                    const uint4 u = *(const uint4 *)((const uint16_t *)a.x + e0);
+                    const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        v[2 * q] = to_h(wh_bf16(uu[q] & 0xffff), bad);
+                        v[2 * q + 1] = to_h(wh_bf16(uu[q] >> 16), bad);
+                    }
+                } else {
+                    const float4 f0 = *(const float4 *)((const float *)a.x + e0);
+                    const float4 f1 = *(const float4 *)((const float *)a.x + e0 + 4);
+                    v[0] = to_h(f0.x, bad); v[1] = to_h(f0.y, bad); v[2] = to_h(f0.z, bad); v[3] = to_h(f0.w, bad);
+                    v[4] = to_h(f1.x, bad); v[5] = to_h(f1.y, bad); v[6] = to_h(f1.z, bad); v[7] = to_h(f1.w, bad);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; q++) v[q] = (_Float16)0.0f;
+            }
+            *(uint4 *)(As + m * PF_ALD + part * 8) = as_u4(v);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            h8 b;
+            if (DEC == DEC_VQ) {
+                const uint32_t u = bw[st][0];
+                const uint4 *bk = cbk + kind * 3 * 256;
+                const h8 c0 = as_h8(bk[u & 255]);
+                const h8 c1 = as_h8(bk[256 + ((u >> 8) & 255)]);
+                const h8 c2 = as_h8(bk[512 + ((u >> 16) & 255)]);
+                b = c0 + (c1 + c2);
+            } else if (DEC == DEC_Q4) {
+                const _Float16 sc = __builtin_bit_cast(_Float16, bs[st]);
+                const uint32_t u = bw[st][0];
+#pragma unroll
+                for (int q = 0; q < 8; q++) b[q] = (_Float16)(float)((int)((u >> (4 * q)) & 15) - 8) * sc;
+            } else if (DEC == DEC_Q8) {
+                const _Float16 sc = __builtin_bit_cast(_Float16, bs[st]);
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    b[q] = (_Float16)(float)(int8_t)((bw[st][q >> 2] >> (8 * (q & 3))) & 0xff) * sc;
+            } else {
+                const float4 f0 = bf[DEC == DEC_F32 ? st : 0][0], f1 = bf[DEC == DEC_F32 ? st : 0][1];
+                b[0] = to_h(f0.x, bad); b[1] = to_h(f0.y, bad); b[2] = to_h(f0.z, bad); b[3] = to_h(f0.w, bad);
+                b[4] = to_h(f1.x, bad); b[5] = to_h(f1.y, bad); b[6] = to_h(f1.z, bad); b[7] = to_h(f1.w, bad);
+            }
+#pragma unroll
+            for (int t = 0; t < PF_MT; t++) {
+                if (t * 32 >= mrows) continue;        // uniform
+                const h8 av = as_h8(*(const uint4 *)(As + (t * 32 + (lane & 31)) * PF_ALD + st * 16 + 8 * (lane >> 5)));
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b, acc[t], 0, 0, 0);
+            }
+        }
+    }
+
+    // epilogue: lane l, register r of tile t holds row t*32 + (r/4)*8 + (l/32)*4 + r%4, column ncol
+    float rsc = 1.0f;
+    if (DEC == DEC_VQ && ncol_ok) {
+        g_u16 *sc = (g_u16 *)(as_global(rec) + a.sc_off[kind]);
+        rsc = wh_f16_scale(sc[ncol]);
+    }
+    if (EPI == 0) {
+        float *ex = (float *)As;                      // [4 waves][16][64]: the gate values
+#pragma unroll
+        for (int t = 0; t < PF_MT; t++) {
+            if (t * 32 >= mrows) continue;            // uniform
+            __syncthreads();
+            if (kind == 0)
+#pragma unroll
+                for (int r = 0; r < 16; r++) ex[((wave & 3) * 16 + r) * 64 + lane] = acc[t][r] * rsc;
+            __syncthreads();
+            if (kind == 1 && ncol_ok)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int m = t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                    if (m < mrows) {
+                        const float h = wh_silu_mul(ex[((wave & 3) * 16 + r) * 64 + lane], acc[t][r] * rsc);
+                        ((_Float16 *)a.out)[(size_t)(s0 + r0 + m) * a.out_ld + ncol] = to_h(h, bad);
+                    }
+                }
+        }
+    } else if (ncol_ok) {
+#pragma unroll
+        for (int t = 0; t < PF_MT; t++) {
+            if (t * 32 >= mrows) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                if (m < mrows) ((float *)a.out)[(size_t)(s0 + r0 + m) * a.out_ld + ncol] = acc[t][r] * rsc;
+            }
+        }
+    }
+    if (bad) atomicOr(a.err, ERR_RANGE);
+}
+
+extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int segs, int mblocks, hipStream_t s)
+{
+    if (a->Kd <= 0 || a->Kd % PF_KC || a->N <= 0 || segs < 1 || mblocks < 1) return (int)hipErrorInvalidValue;
+    if ((dec == DEC_Q4 || dec == DEC_Q8) && (a->group <= 0 || a->group % 8)) return (int)hipErrorInvalidValue;
+    if (dec != DEC_VQ && a->rowbytes % 16) return (int)hipErrorInvalidValue;
+    if (dec == DEC_VQ && a->N % 64) return (int)hipErrorInvalidValue;
+    if (a->x_ld % 8) return (int)hipErrorInvalidValue;
+    const int ntile = pair ? 128 : 256;
+    dim3 grid((a->N + ntile - 1) / ntile, segs, mblocks);
+#define PF(D, E) hipLaunchKernelGGL((k_pf_gemm<D, E>), grid, dim3(PF_THREADS), 0, s, *a)
+    if (dec == DEC_VQ) { if (pair) PF(DEC_VQ, 0); else PF(DEC_VQ, 1); }
+    else if (dec == DEC_Q4) { if (pair) PF(DEC_Q4, 0); else PF(DEC_Q4, 1); }
+    else if (dec == DEC_Q8) { if (pair) PF(DEC_Q8, 0); else PF(DEC_Q8, 1); }
+    else if (dec == DEC_F32) { if (pair) PF(DEC_F32, 0); else PF(DEC_F32, 1); }
+    else return (int)hipErrorInvalidValue;
+#undef PF
+    return (int)hipGetLastError();
+}
+
+// ---- router on the matrix cores (fp32) -------------------------------------
+// logits[t][e] = W[e] . x[t] with fp32 products (v_mfma_f32_32x32x2_f32),
+// split over k into RT_KS ranges whose partial sums are then added in
+// range order.  A workgroup: 4 waves x 32 experts, 32 tokens, one k range.
+#define RT_KS 8
+#define RT_KC 64
+
+__global__ void __launch_bounds__(256)
+k_pf_router(whip_mat W, const void *__restrict__ x, int x_bf16, int T, float *__restrict__ part)
+{
+    __shared__ float Xs[32][RT_KC + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e = blockIdx.x * 128 + wave * 32 + (lane & 31);
+    const int t0 = blockIdx.y * 32, ks = blockIdx.z;
+    const int H = W.cols;
+    const int klen = ((H / RT_KS) + RT_KC - 1) / RT_KC * RT_KC;
+    const int k_lo = ks * klen, k_hi = min(H, k_lo + klen);
+    const int ec = e < W.rows ? e : 0;
+    const int ng = W.fmt == 0 ? 1 : (H + W.group - 1) / W.group;
+    const uint8_t *wr = (const uint8_t *)W.q + (size_t)ec * W.rowbytes;
+    const uint16_t *sr = W.fmt == 0 ? nullptr : W.qs + (size_t)ec * ng;
+    acc16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    for (int k0 = k_lo; k0 < k_hi; k0 += RT_KC) {
+        __syncthreads();
+        for (int i = tid; i < 32 * RT_KC; i += 256) {
+            const int m = i / RT_KC, kk = i % RT_KC, t = t0 + m, k = k0 + kk;
+            float v = 0.0f;
+            if (t < T && k < k_hi) {
+                const size_t o = (size_t)t * H + k;
+                v = x_bf16 ? wh_bf16(((const uint16_t *)x)[o]) : ((const float *)x)[o];
+            }
+            Xs[m][kk] = v;
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int kk = 0; kk < RT_KC; kk += 2) {
+            const int k = k0 + kk + (lane >> 5);
+            float wv = 0.0f;
+            if (k < k_hi) {
+                if (W.fmt == 0) wv = ((const float *)wr)[k];
+                else if (W.fmt == 2) wv = (float)(int8_t)wr[k] * wh_f16_scale(sr[k / W.group]);
+                else {
+                    const uint8_t b = wr[k >> 1];
+                    wv = (float)((int)((k & 1) ? (b >> 4) : (b & 15)) - 8) * wh_f16_scale(sr[k / W.group]);
+                }
+            }
+            const float av = Xs[lane & 31][kk + (lane >> 5)];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, wv, acc, 0, 0, 0);
+        }
+    }
+    if (e < W.rows)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int t = t0 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            if (t < T) part[((size_t)ks * T + t) * W.rows + e] = acc[r];
+        }
+}
+
+__global__ void __launch_bounds__(256)
+k_pf_router_sum(const float *__restrict__ part, int n, float *__restrict__ logits)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)n) return;
+    float s = part[i];
+    for (int ks = 1; ks < RT_KS; ks++) s += part[(size_t)ks * n + i];
+    logits[i] = s;
+}
+
+extern "C" size_t whip_pf_router_part_floats(int T, int E) { return (size_t)RT_KS * T * E; }
+
+extern "C" int whip_pf_router(const whip_mat *W, const void *x, int x_bf16, int T, float *part,
+                              float *logits, hipStream_t s)
+{
+    if (W->fmt != 0 && W->fmt != 2 && W->fmt != 3) return (int)hipErrorInvalidValue;
+    dim3 grid((W->rows + 127) / 128, (T + 31) / 32, RT_KS);
+    hipLaunchKernelGGL(k_pf_router, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
+    const int n = T * W->rows;
+    hipLaunchKernelGGL(k_pf_router_sum, dim3((n + 255) / 256), dim3(256), 0, s, part, n, logits);
+    return (int)hipGetLastError();
+}
+
+// ---- combine ---------------------------------------------------------------
+// y[t][c] = sum over t's pairs in ascending expert order (zero weights and
+// unbound experts skipped) of w * Y[p][c], then + sh[t][c].
+__global__ void __launch_bounds__(256)
+k_pf_combine(const int32_t *__restrict__ tok_pairs, const int32_t *__restrict__ pair_exp,
+             const float *__restrict__ pair_w, const uint8_t *const *__restrict__ recs, int K, int E,
+             const float *__restrict__ Y, int H, const float *__restrict__ sh, float *__restrict__ y)
+{
+    const int t = blockIdx.y, c = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (c >= H) return;
+    float4 o = make_float4(0, 0, 0, 0);
+    for (int j = 0; j < K; j++) {
+        const int p = tok_pairs[t * K + j];
+        const float w = pair_w[p];
+        const int e = pair_exp[p];
+        if (w == 0.0f || e >= E || recs[e] == nullptr) continue;
+        const float4 v = *(const float4 *)(Y + (size_t)p * H + c);
+        o.x = __fadd_rn(o.x, __fmul_rn(w, v.x)); o.y = __fadd_rn(o.y, __fmul_rn(w, v.y));
+        o.z = __fadd_rn(o.z, __fmul_rn(w, v.z)); o.w = __fadd_rn(o.w, __fmul_rn(w, v.w));
+    }
+    if (sh) {
+        const float4 v = *(const float4 *)(sh + (size_t)t * H + c);
+        o.x = __fadd_rn(o.x, v.x); o.y = __fadd_rn(o.y, v.y); o.z = __fadd_rn(o.z, v.z); o.w = __fadd_rn(o.w, v.w);
+    }
+    *(float4 *)(y + (size_t)t * H + c) = o;
+}
+
+extern "C" int whip_pf_combine(const int32_t *tok_pairs, const int32_t *pair_exp, const float *pair_w,
+                               const uint8_t *const *recs, int T, int K, int E, const float *Y, int H,
+                               const float *sh, float *y, hipStream_t s)
+{
+    if (H % 4) return (int)hipErrorInvalidValue;
+    dim3 grid((H / 4 + 255) / 256, T);
+    hipLaunchKernelGGL(k_pf_combine, grid, dim3(256), 0, s, tok_pairs, pair_exp, pair_w, recs, K, E, Y, H, sh, y);
+    return (int)hipGetLastError();
+}

@@ -30,6 +30,7 @@
 struct waste_hip_moe {
     waste_hip_moe_cfg c;
     int E, K, H, I, SI, T;
+    int Td;                      /* most tokens the decode kernels take    */
     int nv_gu, nv_d, nch_gu, nch_d, rsplit_gu, rsplit_d;
     size_t idx_gu, idx_d, rec_min, rec_bytes;
     uint32_t off_gate, off_up, off_down, off_sc;
@@ -40,6 +41,7 @@ struct waste_hip_moe {
     const uint8_t **h_recs;
     uint8_t *slab;               /* owned records, E x rec_bytes (lazy)    */
     float *d_books, *d_booksT;
+    uint16_t *d_books16;         /* fp16, subnormals flushed (prefill)     */
     int n_books;
     whip_mat router, sh[3];
     void *router_mem, *sh_mem[3];
@@ -47,6 +49,10 @@ struct waste_hip_moe {
     int has_router, has_shared;
     float *xf, *logits, *w, *pair_w, *part_gu, *h, *part_d, *sh_a, *sh_b, *h_sh, *sh_out;
     int32_t *ids, *pair_tok, *pair_exp, *tok_pairs;
+    /* many-token path (T > Td) */
+    int32_t *pair_pos, *seg_off, *order;
+    uint16_t *h16, *sh_h16;      /* fp16 [P][I], [T][SI]                   */
+    float *ypair, *rpart;        /* [P][H]; router partial sums            */
     int *err;
     int prof_on;
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
@@ -107,7 +113,8 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->sh_mem[0], m->sh_mem[1], m->sh_mem[2], m->d_bias, m->xf,
                      m->logits, m->w, m->pair_w, m->part_gu, m->h, m->part_d, m->sh_a,
                      m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
-                     m->tok_pairs, m->err };
+                     m->tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
+                     m->sh_h16, m->ypair, m->rpart, m->d_books16 };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0])
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -154,6 +161,10 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     m->E = cfg->n_experts; m->K = cfg->top_k; m->H = cfg->hidden; m->I = cfg->moe_inter;
     m->SI = cfg->moe_inter * (cfg->n_shared > 0 ? cfg->n_shared : 1);
     m->T = cfg->max_tokens;
+    {
+        const int pm = cfg->prefill_min_tokens > 0 ? cfg->prefill_min_tokens : 32;
+        m->Td = m->T < pm ? m->T : pm;
+    }
     m->nv_gu = m->H / 8; m->nv_d = m->I / 8;
     m->nch_gu = whip_vq_chunks(m->nv_gu);
     m->nch_d = whip_vq_chunks(m->nv_d);
@@ -168,7 +179,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     m->rec_min = m->off_sc + 2 * (size_t)(2 * m->I + m->H);
     m->rec_bytes = (m->rec_min + 4095) / 4096 * 4096;
     m->cb = -1;
-    const int P = m->T * m->K;
+    const int P = m->T * m->K, Pd = m->Td * m->K;
     m->rsplit_gu = pick_rsplit(m->nch_gu * 2 * m->K, m->I / 64);
     m->rsplit_d = pick_rsplit(m->nch_d * m->K, m->H / 64);
     m->h_recs = (const uint8_t **)calloc((size_t)m->E + 1, sizeof(void *));
@@ -183,10 +194,18 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->pair_w, (size_t)P * 4);
     rc |= dmalloc((void **)&m->tok_pairs, (size_t)P * 4);
     /* + 64 floats: the apply kernels' sink for rows past a split's end */
-    rc |= dmalloc((void **)&m->part_gu, ((size_t)P * 2 * m->nch_gu * m->I + 64) * 4);
-    rc |= dmalloc((void **)&m->h, (size_t)P * m->I * 4);
-    rc |= dmalloc((void **)&m->part_d, ((size_t)P * m->nch_d * m->H + 64) * 4);
+    rc |= dmalloc((void **)&m->part_gu, ((size_t)Pd * 2 * m->nch_gu * m->I + 64) * 4);
+    rc |= dmalloc((void **)&m->h, (size_t)Pd * m->I * 4);
+    rc |= dmalloc((void **)&m->part_d, ((size_t)Pd * m->nch_d * m->H + 64) * 4);
     rc |= dmalloc((void **)&m->err, 64);
+    if (m->T > m->Td) {
+        rc |= dmalloc((void **)&m->pair_pos, (size_t)P * 4);
+        rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
+        rc |= dmalloc((void **)&m->order, (size_t)m->E * 4);
+        rc |= dmalloc((void **)&m->h16, (size_t)P * m->I * 2);
+        rc |= dmalloc((void **)&m->ypair, (size_t)P * m->H * 4);
+        rc |= dmalloc((void **)&m->rpart, whip_pf_router_part_floats(m->T, m->E) * 4);
+    }
     if (rc || !m->h_recs) { waste_hip_moe_destroy(m); return WASTE_HIP_ENOMEM; }
     if (hipMemset(m->d_recs, 0, ((size_t)m->E + 1) * sizeof(void *)) != hipSuccess ||
         hipMemset(m->err, 0, 64) != hipSuccess) {
@@ -249,10 +268,11 @@ int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
     if (rc) return rc;
     if (gate->fmt != up->fmt || gate->group != up->group) return WASTE_HIP_EINVAL;
     if (!m->sh_a) {
-        rc |= dmalloc((void **)&m->sh_a, (size_t)m->T * m->SI * 4);
-        rc |= dmalloc((void **)&m->sh_b, (size_t)m->T * m->SI * 4);
-        rc |= dmalloc((void **)&m->h_sh, (size_t)m->T * m->SI * 4);
+        rc |= dmalloc((void **)&m->sh_a, (size_t)m->Td * m->SI * 4);
+        rc |= dmalloc((void **)&m->sh_b, (size_t)m->Td * m->SI * 4);
+        rc |= dmalloc((void **)&m->h_sh, (size_t)m->Td * m->SI * 4);
         rc |= dmalloc((void **)&m->sh_out, (size_t)m->T * m->H * 4);
+        if (m->T > m->Td) rc |= dmalloc((void **)&m->sh_h16, (size_t)m->T * m->SI * 2);
         if (rc) return WASTE_HIP_ENOMEM;
     }
     m->has_shared = 1;
@@ -271,14 +291,23 @@ int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16, int n_boo
         for (int c = 0; c < 256; c++)
             for (int d = 0; d < 8; d++)
                 bt[(size_t)k * per + (size_t)d * 256 + c] = b[(size_t)k * per + (size_t)c * 8 + d];
+    /* the fp16 copy the matrix-core path decodes from: the loader's flush of
+     * subnormals to a signed zero, the rest bit for bit */
+    uint16_t *h16 = (uint16_t *)malloc((size_t)n_books * per * 2);
+    if (!h16) { free(b); free(bt); return WASTE_HIP_ENOMEM; }
+    for (size_t i = 0; i < (size_t)n_books * per; i++)
+        h16[i] = ((f16[i] >> 10) & 0x1f) ? f16[i] : (uint16_t)(f16[i] & 0x8000);
     int rc = 0;
     if (m->d_books) { hipFree(m->d_books); hipFree(m->d_booksT); m->d_books = m->d_booksT = NULL; }
+    if (m->d_books16) { hipFree(m->d_books16); m->d_books16 = NULL; }
     rc |= dmalloc((void **)&m->d_books, (size_t)n_books * per * 4);
     rc |= dmalloc((void **)&m->d_booksT, (size_t)n_books * per * 4);
+    rc |= dmalloc((void **)&m->d_books16, (size_t)n_books * per * 2);
     if (!rc && (hipMemcpy(m->d_books, b, (size_t)n_books * per * 4, hipMemcpyHostToDevice) != hipSuccess ||
-                hipMemcpy(m->d_booksT, bt, (size_t)n_books * per * 4, hipMemcpyHostToDevice) != hipSuccess))
+                hipMemcpy(m->d_booksT, bt, (size_t)n_books * per * 4, hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(m->d_books16, h16, (size_t)n_books * per * 2, hipMemcpyHostToDevice) != hipSuccess))
         rc = WASTE_HIP_EDEVICE;
-    free(b); free(bt);
+    free(b); free(bt); free(h16);
     if (rc) return rc;
     m->n_books = n_books;
     return 0;
@@ -354,6 +383,81 @@ int waste_hip_moe_bind_expert(waste_hip_moe *m, int expert, const void *dev_reco
     return set_ptr(m, expert, (const uint8_t *)dev_record);
 }
 
+static int prof_end(waste_hip_moe *m)
+{
+    if (!m->prof_on) return 0;
+    CK(hipEventSynchronize(m->ev[WASTE_HIP_STAGES]));
+    for (int i = 0; i < WASTE_HIP_STAGES; i++) {
+        float ms = 0;
+        CK(hipEventElapsedTime(&ms, m->ev[i], m->ev[i + 1]));
+        m->prof.ms[i] += ms;
+    }
+    m->prof.forwards++;
+    return 0;
+}
+
+/* T > Td: moe_chunk (src/model.c:7110-7285) as grouped products on the
+ * matrix cores.  Stages as forward(): 0 router (+ shared gate/up), 1
+ * routing and the pair sort, 2 routed gate/up with SwiGLU, 3 (empty),
+ * 4 routed down, 5 shared down, 6 combine. */
+static int forward_many(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
+                        int32_t *ids, float *w, float *logits, hipStream_t s)
+{
+    const int E = m->E, K = m->K, H = m->H, I = m->I;
+    const int mb = (T + 127) / 128;
+    if ((uintptr_t)x % 16) return WASTE_HIP_EINVAL;
+#define MARK(i) do { if (m->prof_on) CK(hipEventRecord(m->ev[i], s)); } while (0)
+    MARK(0);
+    float *lg = logits ? logits : m->logits;
+    CK((hipError_t)whip_pf_router(&m->router, x, x_bf16, T, m->rpart, lg, s));
+    whip_pf_args a;
+    if (m->has_shared) {
+        memset(&a, 0, sizeof a);
+        a.W0 = (const uint8_t *)m->sh[0].q; a.W1 = (const uint8_t *)m->sh[1].q;
+        a.S0 = m->sh[0].qs; a.S1 = m->sh[1].qs; a.rowbytes = m->sh[0].rowbytes; a.group = m->sh[0].group;
+        a.N = m->SI; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H;
+        a.rows = T; a.out = m->sh_h16; a.out_ld = m->SI; a.err = m->err;
+        CK((hipError_t)whip_pf_gemm(&a, m->sh[0].fmt, 1, 1, mb, s));
+    }
+    MARK(1);
+    whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
+                          m->c.n_group, m->c.topk_group };
+    int32_t *d_ids = ids ? ids : m->ids;
+    float *d_w = w ? w : m->w;
+    CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, NULL, NULL, NULL, NULL, m->err, s));
+    CK((hipError_t)whip_sort_pairs(d_ids, d_w, T, K, E, m->pair_tok, m->pair_exp, m->pair_w,
+                                   m->tok_pairs, m->pair_pos, m->seg_off, m->order, s));
+    MARK(2);
+    memset(&a, 0, sizeof a);
+    a.recs = m->d_recs; a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
+    a.sc_off[0] = m->off_sc; a.sc_off[1] = m->off_sc + 2u * (uint32_t)I;
+    a.books16 = m->d_books16; a.cb = m->cb;
+    a.N = I; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H; a.tok = m->pair_tok;
+    a.seg_off = m->seg_off; a.order = m->order; a.out = m->h16; a.out_ld = I; a.err = m->err;
+    CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 1, E, mb, s));
+    MARK(3);
+    MARK(4);
+    a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
+    a.sc_off[0] = m->off_sc + 4u * (uint32_t)I; a.sc_off[1] = 0; a.cb = m->cb + 6;
+    a.N = H; a.Kd = I; a.x = m->h16; a.x_mode = 2; a.x_ld = I; a.tok = NULL;
+    a.out = m->ypair; a.out_ld = H;
+    CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 0, E, mb, s));
+    MARK(5);
+    if (m->has_shared) {
+        memset(&a, 0, sizeof a);
+        a.W0 = (const uint8_t *)m->sh[2].q; a.S0 = m->sh[2].qs; a.rowbytes = m->sh[2].rowbytes;
+        a.group = m->sh[2].group; a.N = H; a.Kd = m->SI; a.x = m->sh_h16; a.x_mode = 2;
+        a.x_ld = m->SI; a.rows = T; a.out = m->sh_out; a.out_ld = H; a.err = m->err;
+        CK((hipError_t)whip_pf_gemm(&a, m->sh[2].fmt, 0, 1, mb, s));
+    }
+    MARK(6);
+    CK((hipError_t)whip_pf_combine(m->tok_pairs, m->pair_exp, m->pair_w, m->d_recs, T, K, E, m->ypair, H,
+                                   m->has_shared ? m->sh_out : NULL, y, s));
+    MARK(7);
+#undef MARK
+    return prof_end(m);
+}
+
 int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
                           int32_t *ids, float *w, float *logits, void *stream)
 {
@@ -361,6 +465,7 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     if (!m->has_router || !m->d_booksT || m->cb < 0 || m->cb + 9 > m->n_books)
         return WASTE_HIP_EINVAL;
     hipStream_t s = (hipStream_t)stream;
+    if (T > m->Td) return forward_many(m, x, x_bf16, T, y, ids, w, logits, s);
     const int E = m->E, K = m->K, H = m->H, I = m->I, P = T * K;
 #define MARK(i) do { if (m->prof_on) CK(hipEventRecord(m->ev[i], s)); } while (0)
     MARK(0);
@@ -418,16 +523,7 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
                                 m->has_shared ? m->sh_out : NULL, y, s));
     MARK(7);
 #undef MARK
-    if (m->prof_on) {
-        CK(hipEventSynchronize(m->ev[WASTE_HIP_STAGES]));
-        for (int i = 0; i < WASTE_HIP_STAGES; i++) {
-            float ms = 0;
-            CK(hipEventElapsedTime(&ms, m->ev[i], m->ev[i + 1]));
-            m->prof.ms[i] += ms;
-        }
-        m->prof.forwards++;
-    }
-    return 0;
+    return prof_end(m);
 }
 
 int waste_hip_moe_profile(waste_hip_moe *m, int on)
@@ -459,6 +555,7 @@ int waste_hip_moe_status(waste_hip_moe *m, void *stream)
      * as unbound: report the cause */
     if (e & 2) return WASTE_HIP_EROUTE;
     if (e & 1) return WASTE_HIP_EUNBOUND;
+    if (e & 4) return WASTE_HIP_ERANGE;
     return 0;
 }
 
