@@ -33,6 +33,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0        # dense fp16 / bf16
 METRIC = "MoE layer µs/token + HBM GB/s (% of peak) at batch 1; prefill tokens/s"
 
 
@@ -116,6 +117,84 @@ def cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, budget_s, nthreads):
     return n, t_used, isa
 
 
+def bench_prefill(torch, warp_amd, synth, cfg, slab, books, rb, trunk, T, reps, hot=False):
+    """One T-token chunk of the layer (moe_chunk on the matrix cores).  Tokens
+    are planted so per-expert counts follow Zipf(1.1) (synth.zipf_tokens), or
+    with hot=True a bias sends every token to the same eight experts (two in
+    each of four groups), so every routed group has T >= 128 tokens."""
+    H, E, K, I = cfg["hidden"], cfg["n_experts"], cfg["top_k"], cfg["moe_inter"]
+    router, bias, sh = trunk
+    m = warp_amd.MoeLayer(hidden=H, n_experts=E, top_k=K, moe_inter=I, n_shared=cfg["n_shared"],
+                          score_func=cfg["score_func"], renorm=cfg["renorm"],
+                          routed_scale=cfg["routed_scale"], n_group=cfg["n_group"],
+                          topk_group=cfg["topk_group"], max_tokens=T)
+    m.set_codebooks(books)
+    b = None if bias is None else bias.copy()
+    if hot:
+        gs = E // cfg["n_group"]
+        b[[g * gs + o for g in (0, 2, 5, 7) for o in (1, gs - 2)]] += 5.0
+    m.set_router(router, b)
+    if sh:
+        m.set_shared(*sh)
+    for e in range(E):
+        assert m.bind_expert(e, slab.data_ptr() + e * rb, rb) == 0
+    X = synth.zipf_tokens(router, T, seed=7)
+    xd = torch.from_numpy(X).to("cuda:0")
+    if cfg["bf16"]:
+        xd = xd.to(torch.bfloat16)
+    y = torch.empty((T, H), dtype=torch.float32, device="cuda:0")
+    ids = torch.empty((T, K), dtype=torch.int32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    fwd = lambda: m.forward(xd.data_ptr(), T, y.data_ptr(), ids.data_ptr(), None, None, bf16=cfg["bf16"],
+                            stream=sp)
+    for _ in range(2):
+        fwd()
+    torch.cuda.synchronize()
+    if m.status(sp) != 0:
+        raise RuntimeError("prefill device error")
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(reps):
+        fwd()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / reps
+    m.profile(True)
+    for _ in range(reps):
+        fwd()
+    torch.cuda.synchronize()
+    n, st = m.profile_read()
+    m.profile(False)
+    st = {k: v / n for k, v in st.items()}
+    if m.status(sp) != 0:
+        raise RuntimeError("prefill device error")
+    ih = ids.cpu().numpy()
+    cnt = np.bincount(ih.reshape(-1), minlength=E)
+    U = int((cnt > 0).sum())
+    P = T * K
+    SI = I * max(cfg["n_shared"], 1)
+    f_gu, f_d = 2.0 * P * 2 * I * H, 2.0 * P * H * I
+    f_sh = 2.0 * T * 3 * SI * H if sh else 0.0
+    f_all = f_gu + f_d + f_sh + 2.0 * T * E * H
+    routed_ms = st["routed_gate_up"] + st["routed_down"]
+    nbytes = m.bytes(T, U)
+    m.close()
+    return {
+        "tokens": T, "routing": "8 hot experts (every routed group = all tokens)" if hot
+        else "Zipf(1.1) planted logits, seed 7",
+        "ms_per_chunk": round(ms, 3), "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "experts_touched": U, "experts_ge128": int((cnt >= 128).sum()),
+        "pairs_in_ge128": round(float(cnt[cnt >= 128].sum()) / P, 3),
+        "flops": f_all, "hbm_bytes": int(nbytes),
+        "floor_ms": round(max(nbytes / (HBM_PEAK_GBPS * 1e9), f_all / (MFMA_PEAK_TFLOPS * 1e12)) * 1e3, 3),
+        "routed_grouped_gemm": {"ms": round(routed_ms, 3),
+                                "tflops": round((f_gu + f_d) / (routed_ms * 1e-3) / 1e12, 1),
+                                "mfma_frac": round((f_gu + f_d) / (routed_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4)},
+        "stage_ms": {k: round(v, 3) for k, v in st.items()},
+    }
+
+
 def measured_traffic(dom, config, batch):
     """HBM bytes per launch of the dominant kernel, as measured by the two
     rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE, each scaled by a copy of
@@ -142,6 +221,8 @@ def main():
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="tokens of the prefill chunk measured beside decode (0: skip)")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device (a plain copy kernel of known "
                          "size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -245,6 +326,13 @@ def main():
     achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
     traffic = measured_traffic(dom, a.config, B)
 
+    prefill = None
+    if a.prefill_tokens and B == 1:
+        prefill = bench_prefill(torch, warp_amd, synth, cfg, slab, books, rb, trunk, a.prefill_tokens, 5)
+        prefill["ge128_groups"] = bench_prefill(torch, warp_amd, synth, cfg, slab, books, rb, trunk,
+                                                a.prefill_tokens, 5, hot=True)["routed_grouped_gemm"]
+        log(f"[bench] prefill {prefill['tokens_per_s']} tok/s")
+
     cpu = None
     if not a.no_cpu and B == 1:
         nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
@@ -284,6 +372,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "launch_us": round(dom_ms * 1e3, 2), "algorithmic_bytes": int(dom_bytes)},
         "cpu_baseline": cpu,
+        "prefill": prefill,
     }
     print(json.dumps(out))
     for m in layers:

@@ -114,8 +114,9 @@ int whip_sort_pairs(const int32_t *ids, const float *w, int T, int K, int E,
  * reads row tok[p] (tok NULL: p).  pair = 1: out[p][n] = silu(gate) * up
  * as fp16; pair = 0: out[p][n] fp32 (times the VQ3R row scale).
  * Segments: seg_off/order as whip_sort_pairs writes them (segs of them),
- * or seg_off NULL for one segment of `rows` rows.  mblocks: 128-row blocks
- * per segment the grid covers. */
+ * or seg_off NULL for one segment of `rows` rows.  mt: 32-row tiles per
+ * workgroup (1 or 4); mblocks: (32*mt)-row blocks per segment the grid
+ * covers. */
 typedef struct {
     const uint8_t *const *recs;
     uint32_t idx_off[2], sc_off[2];
@@ -135,7 +136,7 @@ typedef struct {
     int out_ld;
     int *err;
 } whip_pf_args;
-int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int segs, int mblocks, hipStream_t s);
+int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, int segs, int mblocks, hipStream_t s);
 
 /* Router logits for T tokens on the matrix cores (fp32 products), through
  * part[whip_pf_router_part_floats(T, E)]. */

@@ -41,6 +41,7 @@ typedef float acc16 __attribute__((ext_vector_type(16)));
 // chunk's combine order); experts ranked by size, largest first, so the
 // longest segments are dispatched first.
 #define SORT_THREADS 1024
+#define SORT_LDS_PAIRS 8192
 
 __global__ void __launch_bounds__(SORT_THREADS)
 k_sort_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T, int K, int E,
@@ -51,9 +52,15 @@ k_sort_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T
     extern __shared__ int sm[];
     const int NE = E + 1, P = T * K, tid = threadIdx.x;
     int *cnt = sm, *off = sm + NE, *run = sm + 2 * NE;
+    // the pairs' experts (failed selections mapped to E), staged once: the
+    // ordered scatter below reads them from LDS, not with a global round
+    // trip per 64 pairs (P <= SORT_LDS_PAIRS; else read from global)
+    int *eid = sm + 3 * NE, *pos = eid + (P <= SORT_LDS_PAIRS ? P : 0);
+    const bool staged = P <= SORT_LDS_PAIRS;
     for (int i = tid; i < NE; i += SORT_THREADS) { cnt[i] = 0; run[i] = 0; }
+    for (int q = tid; staged && q < P; q += SORT_THREADS) eid[q] = ids[q] < 0 ? E : ids[q];
     __syncthreads();
-    for (int q = tid; q < P; q += SORT_THREADS) atomicAdd(&cnt[ids[q] < 0 ? E : ids[q]], 1);
+    for (int q = tid; q < P; q += SORT_THREADS) atomicAdd(&cnt[staged ? eid[q] : (ids[q] < 0 ? E : ids[q])], 1);
     __syncthreads();
     if (tid < 64) {                                   // exclusive scan, one wave
         const int per = (NE + 63) / 64;
@@ -73,7 +80,7 @@ k_sort_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T
         for (int c0 = 0; c0 < P; c0 += 64) {
             const int q = c0 + tid;
             const bool valid = q < P;
-            const int e = valid ? (ids[q] < 0 ? E : ids[q]) : 0;
+            const int e = valid ? (staged ? eid[q] : (ids[q] < 0 ? E : ids[q])) : 0;
             uint64_t m = __ballot(valid);
             for (int b = 0; b < 11; b++) {            // lanes holding the same expert
                 const bool bit = (e >> b) & 1;
@@ -83,15 +90,19 @@ k_sort_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T
             if (valid) {
                 const int base = run[e];
                 const int p = off[e] + base + __popcll(m & lt);
-                pair_pos[q] = p;
-                pair_tok[p] = q / K;
-                pair_exp[p] = e;
-                pair_w[p] = w[q];
+                if (staged) pos[q] = p; else pair_pos[q] = p;
                 if (!(m & gt)) run[e] = base + __popcll(m);
             }
         }
     }
     __syncthreads();
+    for (int q = tid; q < P; q += SORT_THREADS) {
+        const int p = staged ? pos[q] : pair_pos[q];
+        if (staged) pair_pos[q] = p;
+        pair_tok[p] = q / K;
+        pair_exp[p] = staged ? eid[q] : (ids[q] < 0 ? E : ids[q]);
+        pair_w[p] = w[q];
+    }
     for (int q = tid; q < P; q += SORT_THREADS) {
         const int t = q / K, j = q - t * K;
         const int e = ids[q] < 0 ? E : ids[q];
@@ -100,7 +111,7 @@ k_sort_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T
             const int e2 = ids[t * K + j2] < 0 ? E : ids[t * K + j2];
             rk += e2 < e || (e2 == e && j2 < j);
         }
-        tok_pairs[t * K + rk] = pair_pos[q];
+        tok_pairs[t * K + rk] = staged ? pos[q] : pair_pos[q];
     }
     for (int i = tid; i <= NE; i += SORT_THREADS) seg_off[i] = i < NE ? off[i] : P;
     for (int e = tid; e < E; e += SORT_THREADS) {
@@ -120,14 +131,14 @@ extern "C" int whip_sort_pairs(const int32_t *ids, const float *w, int T, int K,
                                int32_t *order, hipStream_t s)
 {
     if (T < 1 || K < 1 || E < 1 || E > 1024) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(SORT_THREADS), (size_t)3 * (E + 1) * sizeof(int), s,
+    const size_t lds = ((size_t)3 * (E + 1) + (T * K <= SORT_LDS_PAIRS ? (size_t)2 * T * K : 0)) * sizeof(int);
+    hipLaunchKernelGGL(k_sort_pairs, dim3(1), dim3(SORT_THREADS), lds, s,
                        ids, w, T, K, E, pair_tok, pair_exp, pair_w, tok_pairs, pair_pos, seg_off, order);
     return (int)hipGetLastError();
 }
 
 // ---- grouped GEMM ----------------------------------------------------------
 #define PF_THREADS 512
-#define PF_MT 4                      // M tiles of 32 rows per workgroup
 #define PF_KC 64                     // k per LDS chunk
 #define PF_ALD (PF_KC + 8)           // A row stride in halves (144 B: rows fall on different banks)
 
@@ -142,21 +153,26 @@ WH_INLINE _Float16 to_h(float v, bool &bad)
 WH_INLINE h8 as_h8(uint4 u) { return __builtin_bit_cast(h8, u); }
 WH_INLINE uint4 as_u4(h8 h) { return __builtin_bit_cast(uint4, h); }
 
-template <int DEC, int EPI>
+template <int DEC, int EPI, int MT>
 __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
 {
     // EPI 0: gate/up pair, N tile 128 (waves 0-3 gate, 4-7 up), SwiGLU -> fp16
     // EPI 1: one matrix, N tile 256, fp32 rows (times the VQ3R row scale)
+    // MT: M tiles of 32 rows per workgroup (4 for expert segments; 1 for one
+    // long segment, which then spreads over more workgroups)
     constexpr int NBOOK = DEC == DEC_VQ ? (EPI == 0 ? 6 : 3) : 1;
+    constexpr int ABUF = MT * 32 * PF_ALD;                          // halves per A buffer
+    constexpr int SMEM = 2 * ABUF * 2 > 16384 ? 2 * ABUF * 2 : 16384; // A double buffer / SwiGLU exchange
     __shared__ uint4 cbk[NBOOK * 256];
-    __shared__ __attribute__((aligned(16))) _Float16 As[PF_MT * 32 * PF_ALD];
+    __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
+    _Float16 *As = (_Float16 *)smem;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int seg = a.order ? a.order[blockIdx.y] : (int)blockIdx.y;
     const int s0 = a.seg_off ? a.seg_off[seg] : 0;
     const int n_seg = a.seg_off ? a.seg_off[seg + 1] - s0 : a.rows;
-    const int r0 = blockIdx.z * (PF_MT * 32);        // this workgroup's rows of the segment
+    const int r0 = blockIdx.z * (MT * 32);           // this workgroup's rows of the segment
     if (r0 >= n_seg) return;
-    const int mrows = min(PF_MT * 32, n_seg - r0);
+    const int mrows = min(MT * 32, n_seg - r0);
     const int kind = EPI == 0 ? wave >> 2 : 0;
     const int ncol = blockIdx.x * (EPI == 0 ? 128 : 256) + (EPI == 0 ? (wave & 3) : wave) * 32 + (lane & 31);
     const bool ncol_ok = ncol < a.N;
@@ -189,67 +205,113 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
                                                              : nullptr;
     bool bad = false;
 
-    acc16 acc[PF_MT];
+    acc16 acc[MT];
 #pragma unroll
-    for (int t = 0; t < PF_MT; t++)
+    for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
 
+    // Software pipeline over 64-wide k chunks: chunk kc+1's A rows (raw, in
+    // registers) and B inputs are requested before chunk kc's products, so
+    // their latency hides behind the matrix work; the A tile is double
+    // buffered, one barrier per chunk.  Loads take clamped addresses and no
+    // branch; rows past the segment's end are zeroed when stored.  A thread
+    // owns A items tid + 512q (row item/8, 8 k) below MT*32*8.
     const int nchunk = a.Kd / PF_KC;
-    for (int kc = 0; kc < nchunk; kc++) {
-        // this chunk's B inputs: 4 steps of 16 k, position k0/8 + lane/32
-        uint32_t bw[4][2];
-        uint16_t bs[4];
-        float4 bf[DEC == DEC_F32 ? 4 : 1][2];
+    constexpr int NITEM = MT * 32 * (PF_KC / 8);
+    constexpr int NA = (NITEM + PF_THREADS - 1) / PF_THREADS;
+    size_t abase[NA];
+    bool alive[NA];
+#pragma unroll
+    for (int q = 0; q < NA; q++) {
+        const int it = tid + q * PF_THREADS, m = it >> 3;
+        alive[q] = it < NITEM && m < mrows;
+        const int mm = alive[q] ? m : 0;
+        const int row = a.tok ? a.tok[s0 + r0 + mm] : s0 + r0 + mm;
+        abase[q] = (size_t)row * a.x_ld + (it & 7) * 8;
+    }
+    uint4 ra[NA][2];
+    auto load_a = [&](int kc) {
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            const size_t e0 = abase[q] + (size_t)kc * PF_KC;
+            if (a.x_mode == 0) {
+                ra[q][0] = *(const uint4 *)((const float *)a.x + e0);
+                ra[q][1] = *(const uint4 *)((const float *)a.x + e0 + 4);
+            } else {
+                ra[q][0] = *(const uint4 *)((const uint16_t *)a.x + e0);
+            }
+        }
+    };
+    uint32_t bw[4][2], bwn[4][2];
+    uint16_t bs[4], bsn[4];
+    float4 bf[DEC == DEC_F32 ? 4 : 1][2], bfn[DEC == DEC_F32 ? 4 : 1][2];
+    auto load_b = [&](int kc) {
 #pragma unroll
         for (int st = 0; st < 4; st++) {
             const int k = kc * PF_KC + st * 16 + 8 * (lane >> 5);
             if (DEC == DEC_VQ) {
-                bw[st][0] = ld_u32_unaligned((const uint8_t *)(ib + (size_t)(k >> 3) * 192));
+                bwn[st][0] = ld_u32_unaligned((const uint8_t *)(ib + (size_t)(k >> 3) * 192));
             } else if (DEC == DEC_Q4) {
-                bw[st][0] = *(const uint32_t *)(Wrow + (k >> 1));
-                bs[st] = Srow[k / a.group];
+                bwn[st][0] = *(const uint32_t *)(Wrow + (k >> 1));
+                bsn[st] = Srow[k / a.group];
             } else if (DEC == DEC_Q8) {
                 const uint2 v = *(const uint2 *)(Wrow + k);
-                bw[st][0] = v.x; bw[st][1] = v.y;
-                bs[st] = Srow[k / a.group];
+                bwn[st][0] = v.x; bwn[st][1] = v.y;
+                bsn[st] = Srow[k / a.group];
             } else {                                 // F32: 8 floats, converted at use
-                const float4 f0 = *(const float4 *)(Wrow + (size_t)k * 4);
-                const float4 f1 = *(const float4 *)(Wrow + (size_t)k * 4 + 16);
-                bf[st][0] = f0; bf[st][1] = f1;
+                bfn[DEC == DEC_F32 ? st : 0][0] = *(const float4 *)(Wrow + (size_t)k * 4);
+                bfn[DEC == DEC_F32 ? st : 0][1] = *(const float4 *)(Wrow + (size_t)k * 4 + 16);
             }
         }
-        __syncthreads();                             // the previous chunk's A reads are done
-        // A chunk: rows r0 .. r0+mrows of the segment, 64 k, as fp16
-        for (int i = tid; i < PF_MT * 32 * (PF_KC / 8); i += PF_THREADS) {
-            const int m = i >> 3, part = i & 7;
-            h8 v;
-            if (m < mrows) {
-                const int row = a.tok ? a.tok[s0 + r0 + m] : s0 + r0 + m;
-                const size_t e0 = (size_t)row * a.x_ld + (size_t)kc * PF_KC + part * 8;
-                if (a.x_mode == 2) {
-                    v = as_h8(*(const uint4 *)((const _Float16 *)a.x + e0));
-                } else if (a.x_mode == 1) {
-                    const uint4 u = *(const uint4 *)((const uint16_t *)a.x + e0);
-                    const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+    };
+    load_a(0);
+    load_b(0);
+    for (int kc = 0; kc < nchunk; kc++) {
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        v[2 * q] = to_h(wh_bf16(uu[q] & 0xffff), bad);
-                        v[2 * q + 1] = to_h(wh_bf16(uu[q] >> 16), bad);
-                    }
-                } else {
-                    const float4 f0 = *(const float4 *)((const float *)a.x + e0);
-                    const float4 f1 = *(const float4 *)((const float *)a.x + e0 + 4);
-                    v[0] = to_h(f0.x, bad); v[1] = to_h(f0.y, bad); v[2] = to_h(f0.z, bad); v[3] = to_h(f0.w, bad);
-                    v[4] = to_h(f1.x, bad); v[5] = to_h(f1.y, bad); v[6] = to_h(f1.z, bad); v[7] = to_h(f1.w, bad);
+        for (int st = 0; st < 4; st++) {
+            bw[st][0] = bwn[st][0]; bw[st][1] = bwn[st][1]; bs[st] = bsn[st];
+            if (DEC == DEC_F32) { bf[st][0] = bfn[st][0]; bf[st][1] = bfn[st][1]; }
+        }
+        h8 av8[NA];
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            h8 v;
+            if (a.x_mode == 2) {
+                v = as_h8(ra[q][0]);
+            } else if (a.x_mode == 1) {
+                const uint32_t uu[4] = {ra[q][0].x, ra[q][0].y, ra[q][0].z, ra[q][0].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v[2 * i] = to_h(wh_bf16(uu[i] & 0xffff), bad);
+                    v[2 * i + 1] = to_h(wh_bf16(uu[i] >> 16), bad);
                 }
             } else {
+                const float f[8] = {__uint_as_float(ra[q][0].x), __uint_as_float(ra[q][0].y),
+                                    __uint_as_float(ra[q][0].z), __uint_as_float(ra[q][0].w),
+                                    __uint_as_float(ra[q][1].x), __uint_as_float(ra[q][1].y),
+                                    __uint_as_float(ra[q][1].z), __uint_as_float(ra[q][1].w)};
 #pragma unroll
-                for (int q = 0; q < 8; q++) v[q] = (_Float16)0.0f;
+                for (int i = 0; i < 8; i++) v[i] = to_h(f[i], bad);
             }
-            *(uint4 *)(As + m * PF_ALD + part * 8) = as_u4(v);
+            if (!alive[q])
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = (_Float16)0.0f;
+            av8[q] = v;
+        }
+        // buffer kc&1 was last read two chunks ago; the barrier of the chunk
+        // between guarantees every wave is done with it
+        _Float16 *Ab = As + (kc & 1) * ABUF;
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            const int it = tid + q * PF_THREADS;
+            if (it < NITEM) *(uint4 *)(Ab + (it >> 3) * PF_ALD + (it & 7) * 8) = as_u4(av8[q]);
         }
         __syncthreads();
+        if (kc + 1 < nchunk) {                       // uniform: the next chunk's loads fly now
+            load_a(kc + 1);
+            load_b(kc + 1);
+        }
 #pragma unroll
         for (int st = 0; st < 4; st++) {
             h8 b;
@@ -276,9 +338,9 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
                 b[4] = to_h(f1.x, bad); b[5] = to_h(f1.y, bad); b[6] = to_h(f1.z, bad); b[7] = to_h(f1.w, bad);
             }
 #pragma unroll
-            for (int t = 0; t < PF_MT; t++) {
+            for (int t = 0; t < MT; t++) {
                 if (t * 32 >= mrows) continue;        // uniform
-                const h8 av = as_h8(*(const uint4 *)(As + (t * 32 + (lane & 31)) * PF_ALD + st * 16 + 8 * (lane >> 5)));
+                const h8 av = as_h8(*(const uint4 *)(Ab + (t * 32 + (lane & 31)) * PF_ALD + st * 16 + 8 * (lane >> 5)));
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b, acc[t], 0, 0, 0);
             }
         }
@@ -291,9 +353,9 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
         rsc = wh_f16_scale(sc[ncol]);
     }
     if (EPI == 0) {
-        float *ex = (float *)As;                      // [4 waves][16][64]: the gate values
+        float *ex = (float *)smem;                    // [4 waves][16][64]: the gate values
 #pragma unroll
-        for (int t = 0; t < PF_MT; t++) {
+        for (int t = 0; t < MT; t++) {
             if (t * 32 >= mrows) continue;            // uniform
             __syncthreads();
             if (kind == 0)
@@ -312,7 +374,7 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
         }
     } else if (ncol_ok) {
 #pragma unroll
-        for (int t = 0; t < PF_MT; t++) {
+        for (int t = 0; t < MT; t++) {
             if (t * 32 >= mrows) continue;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
@@ -324,8 +386,10 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
     if (bad) atomicOr(a.err, ERR_RANGE);
 }
 
-extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int segs, int mblocks, hipStream_t s)
+extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, int segs, int mblocks,
+                            hipStream_t s)
 {
+    if (mt != 1 && mt != 4) return (int)hipErrorInvalidValue;
     if (a->Kd <= 0 || a->Kd % PF_KC || a->N <= 0 || segs < 1 || mblocks < 1) return (int)hipErrorInvalidValue;
     if ((dec == DEC_Q4 || dec == DEC_Q8) && (a->group <= 0 || a->group % 8)) return (int)hipErrorInvalidValue;
     if (dec != DEC_VQ && a->rowbytes % 16) return (int)hipErrorInvalidValue;
@@ -333,7 +397,11 @@ extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int segs, 
     if (a->x_ld % 8) return (int)hipErrorInvalidValue;
     const int ntile = pair ? 128 : 256;
     dim3 grid((a->N + ntile - 1) / ntile, segs, mblocks);
-#define PF(D, E) hipLaunchKernelGGL((k_pf_gemm<D, E>), grid, dim3(PF_THREADS), 0, s, *a)
+#define PF(D, E)                                                                                 \
+    do {                                                                                         \
+        if (mt == 4) hipLaunchKernelGGL((k_pf_gemm<D, E, 4>), grid, dim3(PF_THREADS), 0, s, *a); \
+        else hipLaunchKernelGGL((k_pf_gemm<D, E, 1>), grid, dim3(PF_THREADS), 0, s, *a);         \
+    } while (0)
     if (dec == DEC_VQ) { if (pair) PF(DEC_VQ, 0); else PF(DEC_VQ, 1); }
     else if (dec == DEC_Q4) { if (pair) PF(DEC_Q4, 0); else PF(DEC_Q4, 1); }
     else if (dec == DEC_Q8) { if (pair) PF(DEC_Q8, 0); else PF(DEC_Q8, 1); }
@@ -346,53 +414,92 @@ extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int segs, 
 // ---- router on the matrix cores (fp32) -------------------------------------
 // logits[t][e] = W[e] . x[t] with fp32 products (v_mfma_f32_32x32x2_f32),
 // split over k into RT_KS ranges whose partial sums are then added in
-// range order.  A workgroup: 4 waves x 32 experts, 32 tokens, one k range.
+// range order.  A workgroup: 4 waves x 32 experts, 32 tokens, one k range,
+// in 64-wide chunks.  Within a chunk lane half h takes k0 + 32h + j at
+// product j, so a lane's weights are 32 consecutive values of its row:
+// 8 16-byte loads (F32), requested a chunk ahead.
 #define RT_KS 8
 #define RT_KC 64
 
+template <int FMT>
+__device__ __forceinline__ void rt_load(const uint8_t *wr, int k, uint4 *raw)
+{
+    if (FMT == 0) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) raw[i] = *(const uint4 *)(wr + (size_t)(k + 4 * i) * 4);
+    } else if (FMT == 2) {
+        raw[0] = *(const uint4 *)(wr + k);
+        raw[1] = *(const uint4 *)(wr + k + 16);
+    } else {
+        raw[0] = *(const uint4 *)(wr + k / 2);
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ float rt_w(const uint4 *raw, int j, float sc)
+{
+    if (FMT == 0) {
+        const uint4 v = raw[j >> 2];
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+        return __uint_as_float(u[j & 3]);
+    } else if (FMT == 2) {
+        const uint4 v = raw[j >> 4];
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+        return (float)(int8_t)((u[(j >> 2) & 3] >> (8 * (j & 3))) & 0xff) * sc;
+    } else {
+        const uint4 v = raw[0];
+        const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+        return (float)((int)((u[j >> 3] >> (4 * (j & 7))) & 15) - 8) * sc;
+    }
+}
+
+template <int FMT>
 __global__ void __launch_bounds__(256)
 k_pf_router(whip_mat W, const void *__restrict__ x, int x_bf16, int T, float *__restrict__ part)
 {
     __shared__ float Xs[32][RT_KC + 1];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5;
     const int e = blockIdx.x * 128 + wave * 32 + (lane & 31);
     const int t0 = blockIdx.y * 32, ks = blockIdx.z;
-    const int H = W.cols;
+    const int H = W.cols;                        // H % 64 == 0
     const int klen = ((H / RT_KS) + RT_KC - 1) / RT_KC * RT_KC;
     const int k_lo = ks * klen, k_hi = min(H, k_lo + klen);
     const int ec = e < W.rows ? e : 0;
-    const int ng = W.fmt == 0 ? 1 : (H + W.group - 1) / W.group;
+    const int ng = FMT == 0 ? 1 : (H + W.group - 1) / W.group;
     const uint8_t *wr = (const uint8_t *)W.q + (size_t)ec * W.rowbytes;
-    const uint16_t *sr = W.fmt == 0 ? nullptr : W.qs + (size_t)ec * ng;
+    const uint16_t *sr = FMT == 0 ? nullptr : W.qs + (size_t)ec * ng;
     acc16 acc;
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    uint4 raw[8], rawn[8];
+    float sc = 1.0f, scn = 1.0f;
+    if (k_lo < k_hi) {
+        rt_load<FMT>(wr, k_lo + 32 * h, rawn);
+        if (FMT != 0) scn = wh_f16_scale(sr[(k_lo + 32 * h) / W.group]);
+    }
     for (int k0 = k_lo; k0 < k_hi; k0 += RT_KC) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) raw[i] = rawn[i];
+        sc = scn;
         __syncthreads();
         for (int i = tid; i < 32 * RT_KC; i += 256) {
-            const int m = i / RT_KC, kk = i % RT_KC, t = t0 + m, k = k0 + kk;
+            const int m = i / RT_KC, kk = i % RT_KC, t = t0 + m;
             float v = 0.0f;
-            if (t < T && k < k_hi) {
-                const size_t o = (size_t)t * H + k;
+            if (t < T) {
+                const size_t o = (size_t)t * H + k0 + kk;
                 v = x_bf16 ? wh_bf16(((const uint16_t *)x)[o]) : ((const float *)x)[o];
             }
             Xs[m][kk] = v;
         }
         __syncthreads();
-#pragma unroll 4
-        for (int kk = 0; kk < RT_KC; kk += 2) {
-            const int k = k0 + kk + (lane >> 5);
-            float wv = 0.0f;
-            if (k < k_hi) {
-                if (W.fmt == 0) wv = ((const float *)wr)[k];
-                else if (W.fmt == 2) wv = (float)(int8_t)wr[k] * wh_f16_scale(sr[k / W.group]);
-                else {
-                    const uint8_t b = wr[k >> 1];
-                    wv = (float)((int)((k & 1) ? (b >> 4) : (b & 15)) - 8) * wh_f16_scale(sr[k / W.group]);
-                }
-            }
-            const float av = Xs[lane & 31][kk + (lane >> 5)];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, wv, acc, 0, 0, 0);
+        if (k0 + RT_KC < k_hi) {                // uniform: the next chunk's weights fly now
+            rt_load<FMT>(wr, k0 + RT_KC + 32 * h, rawn);
+            if (FMT != 0) scn = wh_f16_scale(sr[(k0 + RT_KC + 32 * h) / W.group]);
+        }
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const float av = Xs[lane & 31][32 * h + j];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, rt_w<FMT>(raw, j, sc), acc, 0, 0, 0);
         }
     }
     if (e < W.rows)
@@ -418,9 +525,13 @@ extern "C" size_t whip_pf_router_part_floats(int T, int E) { return (size_t)RT_K
 extern "C" int whip_pf_router(const whip_mat *W, const void *x, int x_bf16, int T, float *part,
                               float *logits, hipStream_t s)
 {
-    if (W->fmt != 0 && W->fmt != 2 && W->fmt != 3) return (int)hipErrorInvalidValue;
+    // 32-wide k runs: a Q8G/Q4G run stays inside one scale group
+    if (W->cols % RT_KC || (W->fmt != 0 && (W->group % 32 || (W->fmt != 2 && W->fmt != 3))))
+        return (int)hipErrorInvalidValue;
     dim3 grid((W->rows + 127) / 128, (T + 31) / 32, RT_KS);
-    hipLaunchKernelGGL(k_pf_router, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
+    if (W->fmt == 0) hipLaunchKernelGGL(k_pf_router<0>, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
+    else if (W->fmt == 2) hipLaunchKernelGGL(k_pf_router<2>, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
+    else hipLaunchKernelGGL(k_pf_router<3>, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
     const int n = T * W->rows;
     hipLaunchKernelGGL(k_pf_router_sum, dim3((n + 255) / 256), dim3(256), 0, s, part, n, logits);
     return (int)hipGetLastError();

@@ -417,7 +417,7 @@ static int forward_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
         a.S0 = m->sh[0].qs; a.S1 = m->sh[1].qs; a.rowbytes = m->sh[0].rowbytes; a.group = m->sh[0].group;
         a.N = m->SI; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H;
         a.rows = T; a.out = m->sh_h16; a.out_ld = m->SI; a.err = m->err;
-        CK((hipError_t)whip_pf_gemm(&a, m->sh[0].fmt, 1, 1, mb, s));
+        CK((hipError_t)whip_pf_gemm(&a, m->sh[0].fmt, 1, 1, 1, (T + 31) / 32, s));
     }
     MARK(1);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
@@ -434,21 +434,21 @@ static int forward_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
     a.books16 = m->d_books16; a.cb = m->cb;
     a.N = I; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H; a.tok = m->pair_tok;
     a.seg_off = m->seg_off; a.order = m->order; a.out = m->h16; a.out_ld = I; a.err = m->err;
-    CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 1, E, mb, s));
+    CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 1, 4, E, mb, s));
     MARK(3);
     MARK(4);
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
     a.sc_off[0] = m->off_sc + 4u * (uint32_t)I; a.sc_off[1] = 0; a.cb = m->cb + 6;
     a.N = H; a.Kd = I; a.x = m->h16; a.x_mode = 2; a.x_ld = I; a.tok = NULL;
     a.out = m->ypair; a.out_ld = H;
-    CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 0, E, mb, s));
+    CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 0, 4, E, mb, s));
     MARK(5);
     if (m->has_shared) {
         memset(&a, 0, sizeof a);
         a.W0 = (const uint8_t *)m->sh[2].q; a.S0 = m->sh[2].qs; a.rowbytes = m->sh[2].rowbytes;
         a.group = m->sh[2].group; a.N = H; a.Kd = m->SI; a.x = m->sh_h16; a.x_mode = 2;
         a.x_ld = m->SI; a.rows = T; a.out = m->sh_out; a.out_ld = H; a.err = m->err;
-        CK((hipError_t)whip_pf_gemm(&a, m->sh[2].fmt, 0, 1, mb, s));
+        CK((hipError_t)whip_pf_gemm(&a, m->sh[2].fmt, 0, 1, 1, (T + 31) / 32, s));
     }
     MARK(6);
     CK((hipError_t)whip_pf_combine(m->tok_pairs, m->pair_exp, m->pair_w, m->d_recs, T, K, E, m->ypair, H,

@@ -131,3 +131,40 @@ def trunk(cfg, seed):
     else:
         sh = None
     return router, bias, sh
+
+
+def dense(t):
+    """A trunk tensor's values as float64 [rows][cols] (F32 or Q8G)."""
+    if t.fmt == WQ_F32:
+        return np.frombuffer(np.ascontiguousarray(t.q).tobytes(), np.float32).reshape(
+            t.rows, t.rowbytes // 4)[:, :t.cols].astype(np.float64)
+    if t.fmt == WQ_Q8G:
+        q = np.frombuffer(np.ascontiguousarray(t.q).tobytes(), np.int8).reshape(t.rows, t.rowbytes)
+        s = np.ascontiguousarray(t.qs).view(np.float16).astype(np.float64).reshape(t.rows, -1)
+        W = q[:, :t.cols].astype(np.float64)
+        return W * np.repeat(s, t.group, axis=1)[:, :t.cols]
+    raise ValueError("dense(): F32 or Q8G trunk tensors")
+
+
+def zipf_tokens(router, T, seed, s=1.1):
+    """Tokens whose router logits make per-expert counts follow Zipf(s).
+
+    Expert e gets popularity p_e ~ rank_e^-s (ranks a seeded permutation, so
+    popular experts fall in every group); token t's logits are planted as
+    log(p_e / p_max) + Gumbel noise, the Gumbel-max form of drawing top-k
+    without replacement with probabilities p (the sigmoid score keeps their
+    order).  The token is the exact least-squares preimage of those logits
+    under the router (x = W^T (W W^T)^-1 l) plus N(0,1) noise orthogonal to
+    the router's rows, so every coordinate still looks like N(0,1) noise.
+    Returns float32 [T][H]."""
+    rng = np.random.default_rng(seed)
+    W = dense(router)
+    E, H = W.shape
+    rank = rng.permutation(E) + 1
+    lp = -s * np.log(rank.astype(np.float64))
+    L = (lp - lp.max())[None, :] + rng.gumbel(size=(T, E))
+    G = W @ W.T
+    X = np.linalg.solve(G, L.T).T @ W                          # W X^T = L^T
+    Z = rng.standard_normal((T, H))
+    Z -= np.linalg.solve(G, (Z @ W.T).T).T @ W                 # remove the row-space part
+    return (X + Z).astype(np.float32)
