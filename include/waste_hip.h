@@ -140,8 +140,44 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T,
                           float *y, int32_t *ids, float *w, float *logits,
                           void *stream);
 
+/* forward() in two halves, for a caller that must see the selection
+ * before the experts run (an expert cache: moe_layer's hint and holds sit
+ * between its router and its experts, src/model.c:5639-5700).
+ *   route:   router logits, the shared expert's gate/up, the selection
+ *            (ids/w as in forward; NULL keeps them internal)
+ *   experts: the routed experts on the selection of the last route() of
+ *            this layer, the shared down projection and the combine.  x and
+ *            T must be the route's.  Records are read as bound when the
+ *            stream reaches this call. */
+int waste_hip_moe_route(waste_hip_moe *m, const void *x, int x_bf16, int T,
+                        int32_t *ids, float *w, float *logits, void *stream);
+int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T,
+                          float *y, void *stream);
+
+/* Binds n device records (expert-cache slots) in stream order, with no
+ * host wait: the table entries change when the stream reaches the call,
+ * after the work enqueued before it.  Each header is checked on the device
+ * as record_check does (src/model.c:3645-3692, the checksum aside); a
+ * record that fails is left unbound and status() reports
+ * WASTE_HIP_ERECORD.  NULL unbinds.  codebook_id: the id the layer's records
+ * carry (-1: the one already known from a bound record).  n <= 64, experts
+ * distinct, records 16-byte aligned.
+ * Replaces: the pointers waste_ecache_hold hands moe_layer,
+ * src/model.c:5695-5700. */
+int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts,
+                             const void *const *dev_records, int n,
+                             int codebook_id, void *stream);
+
+/* The lookahead: this layer's router on the previous layer's input x (one
+ * token), scored, bias added, and the n best experts without the group
+ * limit, into ids[n] (device).  Bit-exact with predict_next_moe
+ * (src/model.c:5419-5449) on the same logits. n <= 64. */
+int waste_hip_moe_predict(waste_hip_moe *m, const void *x, int x_bf16, int n,
+                          int32_t *ids, void *stream);
+
 /* Waits for the layer's work and returns the sticky device error (0, or
- * WASTE_HIP_EROUTE / WASTE_HIP_EUNBOUND / WASTE_HIP_ERANGE), clearing it. */
+ * WASTE_HIP_EROUTE / WASTE_HIP_ERECORD / WASTE_HIP_EUNBOUND /
+ * WASTE_HIP_ERANGE), clearing it. */
 int waste_hip_moe_status(waste_hip_moe *m, void *stream);
 
 /* Bytes the layer reads from HBM for one forward that touches `n_distinct`
@@ -166,6 +202,60 @@ int waste_hip_moe_profile_read(waste_hip_moe *m, waste_hip_moe_prof *out);
  * fp32 [M][N] in device memory W: the format's closed form, bit-exact. */
 int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W,
                           void *stream);
+
+/* ---- 4. expert cache in HBM ------------------------------------------- */
+
+/* The engine's expert cache (waste_ecache, src/ecache.h:64-106) with its
+ * slots in one device allocation: budget / rec_bytes slots, filled from
+ * host records by hipMemcpyAsync on the cache's own stream.  Every decision
+ * (which slot, which victim, what counts as a hit) is the engine's: LFRU or
+ * LRU over 16 sampled victims, hints that pin their records and keep
+ * `depth` reads in flight, speculative lookahead reads counted as bytes
+ * only.  Not thread-safe: one host thread drives it, as moe_layer does.
+ *
+ * Pointers get/hold return are device addresses.  The caller's stream is
+ * made to wait for the slot's fill; the caller enqueues its readers and
+ * then calls release(stream), after which a refill of the slot waits for
+ * them.  A get() pointer is good until the next get/hold; a hold()
+ * pointer until release.  Releases go on one stream.
+ *
+ * dry = 1: the policy alone, no device (slot pointers are tokens, nothing
+ * is copied) — for replaying a routing trace.
+ * Replaces: waste_ecache_init/get/hold/release/hint/prefetch/admit/
+ * resident_mask/resident_all, src/ecache.h:128-230. */
+typedef struct waste_hip_ecache waste_hip_ecache;
+typedef struct {
+    uint64_t hits, misses, evictions;
+    uint64_t prefetched;     /* misses the hint's read-ahead issued        */
+    uint64_t spec_issued;    /* lookahead reads (not misses)               */
+    uint64_t reads, bytes_read;
+} waste_hip_ecache_counts;
+
+/* policy 0 LFRU, 1 LRU; depth 0 = no read-ahead (the engine's synchronous
+ * cache: hint and prefetch do nothing), else reads kept in flight
+ * (clamped to a quarter of the slots). */
+int  waste_hip_ecache_create(size_t rec_bytes, size_t budget_bytes, int policy,
+                             int depth, int dry, waste_hip_ecache **out);
+void waste_hip_ecache_destroy(waste_hip_ecache *c);
+/* Host copies of every record, records[layer * n_experts + expert]:
+ * pinned memory for the copies to be asynchronous. Kept, not copied. */
+int  waste_hip_ecache_set_source(waste_hip_ecache *c, const void *const *records,
+                                 int n_layers, int n_experts);
+int  waste_hip_ecache_hint(waste_hip_ecache *c, int layer, const int *ids, int n);
+int  waste_hip_ecache_prefetch(waste_hip_ecache *c, int layer, const int *ids, int n);
+const void *waste_hip_ecache_get(waste_hip_ecache *c, int layer, int expert, void *stream);
+const void *waste_hip_ecache_hold(waste_hip_ecache *c, int layer, int expert, void *stream);
+int  waste_hip_ecache_release(waste_hip_ecache *c, void *stream);
+/* 1 when the record went into an empty slot, 0 when nothing was done */
+int  waste_hip_ecache_admit(waste_hip_ecache *c, int layer, int expert);
+int  waste_hip_ecache_resident_mask(const waste_hip_ecache *c, int layer, int n, uint8_t *out);
+int  waste_hip_ecache_resident_all(const waste_hip_ecache *c, int layer, const int *ids, int n);
+int  waste_hip_ecache_stats(const waste_hip_ecache *c, waste_hip_ecache_counts *out);
+/* the slot holding (layer, expert), or -1 */
+int  waste_hip_ecache_slot(const waste_hip_ecache *c, int layer, int expert);
+int  waste_hip_ecache_n_slots(const waste_hip_ecache *c);
+/* waits for every fill issued so far */
+int  waste_hip_ecache_sync(waste_hip_ecache *c);
 
 #ifdef __cplusplus
 }

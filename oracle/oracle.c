@@ -759,3 +759,250 @@ void orc_router_logits(const orc_moe *m, const float *x, int T, float *logits)
         tensor_mv(&m->router, x + (size_t)t * m->hidden, logits + (size_t)t * m->n_experts, m->order);
     }
 }
+
+/* ---- expert cache policy ----------------------------------------------------
+ * src/ecache.c: victim choice (ec_victim, 454-485), claims (ec_claim
+ * 510-526, ec_claim_spec 490-508), the hint pipeline (ec_issue_next
+ * 538-576, waste_ecache_hint 599-616), speculative reads
+ * (waste_ecache_prefetch 578-597) and the demand path
+ * (waste_ecache_get 693-766).  Test infrastructure. */
+enum { OE_EMPTY = 0, OE_READY, OE_INFLIGHT };
+typedef struct { int32_t key; uint8_t state, fresh; uint32_t hits; uint64_t last, pin; } orc_eslot;
+struct orc_ecache {
+    orc_eslot *slot;
+    int32_t *where;                  /* key -> slot, direct: 128 x 1024     */
+    int n_slots, depth, io, lru;
+    uint64_t clock, hits, misses, evictions, prefetched, spec_issued, reads, pf_gen;
+    uint32_t rng;
+    int pf_ids[64], pf_layer, pf_n, pf_issued, last_used;
+    int held[64], n_held, fill_cursor;
+};
+#define OE_KEY(l, e) (((l) << 16) | (e))
+#define OE_IDX(k) (((k) >> 16) * 1024 + ((k) & 0xffff))
+
+orc_ecache *orc_ecache_new(int n_slots, int depth, int readahead, int lru)
+{
+    orc_ecache *c = (orc_ecache *)calloc(1, sizeof *c);
+    c->n_slots = n_slots;
+    c->slot = (orc_eslot *)calloc((size_t)(n_slots > 0 ? n_slots : 1), sizeof *c->slot);
+    c->where = (int32_t *)malloc(128 * 1024 * sizeof(int32_t));
+    for (int i = 0; i < 128 * 1024; i++) c->where[i] = -1;
+    for (int i = 0; i < n_slots; i++) c->slot[i].key = -1;
+    if (depth < 1) depth = 1;
+    if (depth > n_slots / 4) depth = n_slots / 4;
+    c->io = readahead && depth >= 1;
+    c->depth = depth;
+    c->lru = lru;
+    c->rng = 0x9e3779b9u;
+    c->pf_gen = 1;
+    c->last_used = -1;
+    return c;
+}
+
+void orc_ecache_free(orc_ecache *c)
+{
+    if (!c) return;
+    free(c->slot);
+    free(c->where);
+    free(c);
+}
+
+static int oe_lookup(const orc_ecache *c, int32_t key) { return c->where[OE_IDX(key)]; }
+
+static int oe_is_held(const orc_ecache *c, int i)
+{
+    for (int k = 0; k < c->n_held; k++)
+        if (c->held[k] == i) return 1;
+    return 0;
+}
+
+static int oe_pinned(const orc_ecache *c, int i)
+{
+    return c->slot[i].state == OE_INFLIGHT || c->slot[i].pin == c->pf_gen || i == c->last_used ||
+           oe_is_held(c, i);
+}
+
+static int oe_victim(orc_ecache *c)
+{
+    for (int i = 0; i < c->n_slots; i++)
+        if (c->slot[i].state == OE_EMPTY) return i;
+    int best = -1;
+    uint32_t bh = 0;
+    uint64_t bl = 0;
+    for (int s = 0; s < 16; s++) {
+        c->rng = c->rng * 1664525u + 1013904223u;
+        const int i = (int)(c->rng % (uint32_t)c->n_slots);
+        if (oe_pinned(c, i)) continue;
+        const orc_eslot *sl = &c->slot[i];
+        const int better = c->lru ? (best < 0 || sl->last < bl)
+                                  : (best < 0 || sl->hits < bh || (sl->hits == bh && sl->last < bl));
+        if (better) { best = i; bh = sl->hits; bl = sl->last; }
+    }
+    if (best < 0)
+        for (int i = 0; i < c->n_slots; i++)
+            if (!oe_pinned(c, i)) { best = i; break; }
+    return best;
+}
+
+static void oe_take(orc_ecache *c, int vi, int32_t key)
+{
+    if (c->slot[vi].key >= 0) { c->where[OE_IDX(c->slot[vi].key)] = -1; c->evictions++; }
+    c->slot[vi].key = key;
+    c->where[OE_IDX(key)] = vi;
+    c->slot[vi].state = OE_INFLIGHT;
+    c->slot[vi].hits = 1;
+    c->slot[vi].last = c->clock;
+    c->reads++;
+}
+
+static void oe_issue_next(orc_ecache *c)
+{
+    if (!c->io) return;
+    while (c->pf_issued < c->pf_n) {
+        const int32_t key = OE_KEY(c->pf_layer, c->pf_ids[c->pf_issued++]);
+        const int si = oe_lookup(c, key);
+        if (si >= 0) { c->slot[si].pin = c->pf_gen; continue; }
+        const int vi = oe_victim(c);
+        if (vi < 0) { c->pf_issued--; return; }
+        oe_take(c, vi, key);
+        c->slot[vi].fresh = 1;
+        c->slot[vi].pin = c->pf_gen;
+        c->misses++;
+        c->prefetched++;
+        return;
+    }
+}
+
+void orc_ecache_hint(orc_ecache *c, int layer, const int *ids, int n)
+{
+    if (!c->io || c->n_slots <= 0 || n <= 0) return;
+    c->pf_gen++;
+    c->pf_layer = layer;
+    c->pf_n = n > 64 ? 64 : n;
+    if (c->pf_n > c->n_slots / 4) c->pf_n = c->n_slots / 4;
+    for (int i = 0; i < c->pf_n; i++) c->pf_ids[i] = ids[i];
+    c->pf_issued = 0;
+    for (int d = 0; d < c->depth; d++) oe_issue_next(c);
+}
+
+void orc_ecache_prefetch(orc_ecache *c, int layer, const int *ids, int n)
+{
+    if (!c->io || c->n_slots <= 0 || n <= 0) return;
+    for (int i = 0; i < n; i++) {
+        if (ids[i] < 0) continue;
+        const int32_t key = OE_KEY(layer, ids[i]);
+        if (oe_lookup(c, key) >= 0) continue;
+        const int vi = oe_victim(c);
+        if (vi < 0) break;
+        oe_take(c, vi, key);
+        c->slot[vi].fresh = 0;
+        c->slot[vi].pin = 0;
+        c->spec_issued++;
+    }
+}
+
+int orc_ecache_get(orc_ecache *c, int layer, int expert)
+{
+    const int32_t key = OE_KEY(layer, expert);
+    c->clock++;
+    c->last_used = -1;
+    for (int i = 0; i < c->n_slots; i++)                   /* reads issued so far are done */
+        if (c->slot[i].state == OE_INFLIGHT) c->slot[i].state = OE_READY;
+    if (c->n_slots <= 0) { c->misses++; c->reads++; return -1; }
+    const int si = oe_lookup(c, key);
+    if (si >= 0) {
+        if (c->slot[si].fresh) c->slot[si].fresh = 0;
+        else { c->hits++; c->slot[si].hits++; }
+        c->slot[si].last = c->clock;
+        c->last_used = si;
+        oe_issue_next(c);
+        return si;
+    }
+    const int vi = oe_victim(c);
+    if (vi < 0) return -1;
+    oe_take(c, vi, key);
+    c->slot[vi].fresh = 0;
+    c->slot[vi].pin = 0;
+    c->misses++;
+    c->slot[vi].state = OE_READY;
+    c->last_used = vi;
+    oe_issue_next(c);
+    return vi;
+}
+
+/* src/ecache.c:768-798 */
+int orc_ecache_hold(orc_ecache *c, int layer, int expert)
+{
+    if (c->n_slots <= 0 || c->n_held >= 64) return -1;
+    const int si = orc_ecache_get(c, layer, expert);
+    if (si < 0) return -1;
+    if (c->last_used >= 0) {
+        if (!oe_is_held(c, c->last_used)) c->held[c->n_held++] = c->last_used;
+        c->last_used = -1;
+    }
+    return si;
+}
+
+void orc_ecache_release(orc_ecache *c) { c->n_held = 0; }
+
+/* src/ecache.c:635-678: an empty slot by a monotone cursor, nothing
+ * evicted, no hit or miss counted; needs read-ahead. */
+int orc_ecache_admit(orc_ecache *c, int layer, int expert)
+{
+    if (c->n_slots <= 0 || !c->io) return 0;
+    const int32_t key = OE_KEY(layer, expert);
+    if (oe_lookup(c, key) >= 0) return 0;
+    int si = -1;
+    while (c->fill_cursor < c->n_slots) {
+        const int i = c->fill_cursor++;
+        if (c->slot[i].key < 0) { si = i; break; }
+    }
+    if (si < 0) return 0;
+    c->slot[si].key = key;
+    c->where[OE_IDX(key)] = si;
+    c->slot[si].state = OE_READY;
+    c->slot[si].fresh = 0;
+    c->slot[si].pin = 0;
+    c->slot[si].hits = 1;
+    c->slot[si].last = c->clock;
+    c->reads++;
+    return 1;
+}
+
+/* src/ecache.c:618-633: READY only */
+void orc_ecache_resident_mask(const orc_ecache *c, int layer, int n, uint8_t *out)
+{
+    for (int e = 0; e < n; e++) {
+        const int si = c->n_slots > 0 ? oe_lookup(c, OE_KEY(layer, e)) : -1;
+        out[e] = si >= 0 && c->slot[si].state == OE_READY;
+    }
+}
+
+/* src/model.c:5419-5449 */
+int orc_predict_next(int score_func, int E, const float *logit, const float *bias, int n, int *out)
+{
+    if (n <= 0 || E <= 0) return 0;
+    if (n > E) n = E;
+    float *p = (float *)malloc((size_t)E * sizeof *p);
+    orc_router_scores(score_func, logit, p, E);
+    for (int e = 0; e < E; e++) p[e] += bias ? bias[e] : 0.0f;
+    for (int j = 0; j < n; j++) {
+        int best = -1;
+        float bv = -1e30f;
+        for (int e = 0; e < E; e++) {
+            int taken = 0;
+            for (int q = 0; q < j; q++)
+                if (out[q] == e) { taken = 1; break; }
+            if (!taken && p[e] > bv) { bv = p[e]; best = e; }
+        }
+        out[j] = best;
+    }
+    free(p);
+    return n;
+}
+
+void orc_ecache_stats(const orc_ecache *c, uint64_t out[6])
+{
+    out[0] = c->hits; out[1] = c->misses; out[2] = c->evictions;
+    out[3] = c->prefetched; out[4] = c->spec_issued; out[5] = c->reads;
+}

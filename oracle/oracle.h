@@ -133,6 +133,33 @@ int orc_moe_layer_mt(const orc_moe *m, const float *x, float *out, int *idx,
                      float *w, int nthreads);
 int orc_cpu_isa(void);           /* 2 AVX-512 kernels in use, 1 AVX2, 0 C  */
 
+/* ---- expert cache policy (src/ecache.c) ------------------------------------
+ * The decisions of waste_ecache with read-ahead on or off, made
+ * deterministic: a read the hint or the lookahead issues is in flight
+ * (and so never a victim) until the next demand get(), when it is done.
+ * Keys are (layer << 16) | expert, layers < 128, experts < 1024. */
+typedef struct orc_ecache orc_ecache;
+orc_ecache *orc_ecache_new(int n_slots, int depth, int readahead, int lru);
+void orc_ecache_free(orc_ecache *c);
+void orc_ecache_hint(orc_ecache *c, int layer, const int *ids, int n);
+void orc_ecache_prefetch(orc_ecache *c, int layer, const int *ids, int n);
+/* the slot now holding (layer, expert), or -1 (no slots / all pinned) */
+int orc_ecache_get(orc_ecache *c, int layer, int expert);
+/* get, and keep the slot claimed until release (at most 64 held) */
+int orc_ecache_hold(orc_ecache *c, int layer, int expert);
+void orc_ecache_release(orc_ecache *c);
+/* 1 when a record went into an empty slot, else 0 */
+int orc_ecache_admit(orc_ecache *c, int layer, int expert);
+void orc_ecache_resident_mask(const orc_ecache *c, int layer, int n, uint8_t *out);
+/* hits, misses, evictions, prefetched, spec_issued, reads */
+void orc_ecache_stats(const orc_ecache *c, uint64_t out[6]);
+
+/* The lookahead: the next layer's router on this layer's input, scored,
+ * bias added, top n without the group limit (src/model.c:5419-5449).
+ * Returns n (clamped to E). */
+int orc_predict_next(int score_func, int E, const float *logit, const float *bias, int n,
+                     int *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -199,3 +199,100 @@ int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
     free(m);
     return err;
 }
+
+/* ---- the engine's expert cache, scripted --------------------------------
+ *
+ * ref_ecache_run() drives src/ecache.c itself through a script of calls and
+ * reports the slot each demand call returned.  With readers (depth > 0) the
+ * engine's in-flight reads finish whenever the threads get to them; to make
+ * a run repeatable, the reader threads' fetch waits on a gate that opens
+ * only just before each get/hold, until every in-flight read has landed.
+ * Reads therefore finish exactly "by the next demand get", which is the
+ * order the deterministic restatement assumes.  Demand and admit reads run
+ * on the calling thread and return at once.
+ *
+ * Script words: 0 L e get | 1 L e hold | 2 release | 3 L n ids.. hint |
+ * 4 L n ids.. prefetch | 5 L e admit.  out[] gets one int per get/hold
+ * (slot, -1 NULL) and per admit (its return).  stats: hits, misses,
+ * evictions, prefetched, spec_issued, bytes_read / rec_bytes.
+ * Returns the number of out[] entries, or -1. */
+static pthread_t ref_main;
+static int ref_gate;
+
+static int ref_fetch(void *user, int layer, int expert, uint8_t *dst)
+{
+    (void)user;
+    if (!pthread_equal(pthread_self(), ref_main))
+        while (!__atomic_load_n(&ref_gate, __ATOMIC_ACQUIRE)) usleep(20);
+    const int32_t key = (layer << 16) | expert;
+    memcpy(dst, &key, sizeof key);
+    return 0;
+}
+
+static void ref_quiesce(waste_ecache *c)
+{
+    if (!c->io) return;
+    __atomic_store_n(&ref_gate, 1, __ATOMIC_RELEASE);
+    for (;;) {
+        int busy = 0;
+        for (int i = 0; i < c->n_slots && !busy; i++)
+            busy = __atomic_load_n(&c->slot[i].state, __ATOMIC_ACQUIRE) == EC_INFLIGHT;
+        if (!busy) break;
+        usleep(20);
+    }
+    __atomic_store_n(&ref_gate, 0, __ATOMIC_RELEASE);
+}
+
+static int ref_slot_of(const waste_ecache *c, const uint8_t *p)
+{
+    if (!p) return -1;
+    for (int i = 0; i < c->n_slots; i++)
+        if (c->slot[i].data == p) return i;
+    return -2;
+}
+
+int ref_ecache_run(int n_slots, int depth, int policy, const int *ops, int n_words, int *out,
+                   uint64_t stats[6])
+{
+    const size_t rec = 4096;
+    waste_ecache c;
+    memset(&c, 0, sizeof c);
+    if (waste_ecache_init(&c, (size_t)n_slots * rec, rec, policy)) return -1;
+    ref_main = pthread_self();
+    __atomic_store_n(&ref_gate, 0, __ATOMIC_RELEASE);
+    if (depth > 0) waste_ecache_io_start(&c, ref_fetch, NULL, 2, depth);
+    int n_out = 0, bad = 0;
+    for (int w = 0; w < n_words && !bad;) {
+        const int op = ops[w];
+        if (op == 0 || op == 1) {
+            ref_quiesce(&c);
+            const uint8_t *p = op == 0 ? waste_ecache_get(&c, ops[w + 1], ops[w + 2], ref_fetch, NULL)
+                                       : waste_ecache_hold(&c, ops[w + 1], ops[w + 2], ref_fetch, NULL);
+            const int si = ref_slot_of(&c, p);
+            int32_t k;
+            if (p) memcpy(&k, p, sizeof k);
+            if (si == -2 || (p && k != ((ops[w + 1] << 16) | ops[w + 2]))) bad = 1;
+            out[n_out++] = si;
+            w += 3;
+        } else if (op == 2) {
+            waste_ecache_release(&c);
+            w += 1;
+        } else if (op == 3 || op == 4) {
+            const int n = ops[w + 2];
+            if (op == 3) waste_ecache_hint(&c, ops[w + 1], ops + w + 3, n);
+            else waste_ecache_prefetch(&c, ops[w + 1], ops + w + 3, n);
+            w += 3 + n;
+        } else if (op == 5) {
+            out[n_out++] = waste_ecache_admit(&c, ops[w + 1], ops[w + 2], ref_fetch, NULL);
+            w += 3;
+        } else {
+            bad = 1;
+        }
+    }
+    ref_quiesce(&c);
+    stats[0] = c.hits; stats[1] = c.misses; stats[2] = c.evictions;
+    stats[3] = c.prefetched; stats[4] = c.spec_issued; stats[5] = c.bytes_read / rec;
+    waste_ecache_io_stop(&c);
+    waste_ecache_free(&c);
+    return bad ? -1 : n_out;
+}

@@ -83,6 +83,56 @@ class Oracle:
         _sig(L, "orc_cpu_isa", C.c_int, [])
         _sig(L, "orc_moe_apply", C.c_int, [C.POINTER(OrcMoe), fp, C.c_int, i32p, fp, C.c_int, fp])
         _sig(L, "orc_router_logits", None, [C.POINTER(OrcMoe), fp, C.c_int, fp])
+        _sig(L, "orc_ecache_new", C.c_void_p, [C.c_int, C.c_int, C.c_int, C.c_int])
+        _sig(L, "orc_ecache_free", None, [C.c_void_p])
+        for n in ("orc_ecache_hint", "orc_ecache_prefetch"):
+            _sig(L, n, None, [C.c_void_p, C.c_int, i32p, C.c_int])
+        for n in ("orc_ecache_get", "orc_ecache_hold", "orc_ecache_admit"):
+            _sig(L, n, C.c_int, [C.c_void_p, C.c_int, C.c_int])
+        _sig(L, "orc_ecache_release", None, [C.c_void_p])
+        _sig(L, "orc_ecache_resident_mask", None, [C.c_void_p, C.c_int, C.c_int, u8p])
+        _sig(L, "orc_ecache_stats", None, [C.c_void_p, C.POINTER(C.c_uint64)])
+        _sig(L, "orc_predict_next", C.c_int, [C.c_int, C.c_int, fp, fp, C.c_int, i32p])
+
+    def ecache_run(self, ops, n_slots, depth, policy, masks=None):
+        """Runs a cache script (tests/ecache_script.py) through the
+        restatement: (outputs, [hits, misses, evictions, prefetched,
+        spec_issued, reads]).  masks: {word index: (layer, n)} to record
+        resident_mask before that op."""
+        L = self.lib
+        c = L.orc_ecache_new(n_slots, depth if depth > 0 else 1, 1 if depth > 0 else 0, policy)
+        out, got = [], {}
+        w = 0
+        while w < len(ops):
+            if masks and w in masks:
+                layer, n = masks[w]
+                m = np.zeros(n, np.uint8)
+                L.orc_ecache_resident_mask(c, layer, n, ptr(m, u8p))
+                got[w] = m
+            op = ops[w]
+            if op in (0, 1, 5):
+                f = (L.orc_ecache_get, L.orc_ecache_hold, None, None, None, L.orc_ecache_admit)[op]
+                out.append(f(c, ops[w + 1], ops[w + 2]))
+                w += 3
+            elif op == 2:
+                L.orc_ecache_release(c)
+                w += 1
+            else:
+                n = ops[w + 2]
+                a = np.array(ops[w + 3:w + 3 + n] or [0], np.int32)
+                (L.orc_ecache_hint if op == 3 else L.orc_ecache_prefetch)(c, ops[w + 1], ptr(a, i32p), n)
+                w += 3 + n
+        st = (C.c_uint64 * 6)()
+        L.orc_ecache_stats(c, st)
+        L.orc_ecache_free(c)
+        return (out, list(st), got) if masks else (out, list(st))
+
+    def predict_next(self, score_func, logits, bias, n):
+        lg = np.ascontiguousarray(logits, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        out = np.full(max(n, 1), -7, np.int32)
+        k = self.lib.orc_predict_next(score_func, lg.size, ptr(lg, fp), ptr(b, fp), n, ptr(out, i32p))
+        return out[:k]
 
     def expf(self, x):
         return self.lib.orc_expf(float(x))
@@ -245,7 +295,21 @@ class Ref:
         rt = C.POINTER(RefTensor)
         _sig(L, "ref_moe", C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                      rt, fp, rt, rt, rt, fp, C.c_int, u8p, C.c_size_t, fp, C.c_int, fp, i32p, fp])
+        _sig(L, "ref_ecache_run", C.c_int, [C.c_int, C.c_int, C.c_int, i32p, C.c_int, i32p,
+                                            C.POINTER(C.c_uint64)])
         self.isa = L.ref_init()
+
+    def ecache_run(self, ops, n_slots, depth, policy):
+        """The engine's own src/ecache.c on a cache script, reads landing by
+        the next demand get: (outputs, [hits, misses, evictions,
+        prefetched, spec_issued, reads])."""
+        a = np.ascontiguousarray(ops, np.int32)
+        out = np.zeros(max(len(ops), 1), np.int32)
+        st = (C.c_uint64 * 6)()
+        k = self.lib.ref_ecache_run(n_slots, depth, policy, ptr(a, i32p), len(ops), ptr(out, i32p), st)
+        if k < 0:
+            raise RuntimeError("ref_ecache_run failed")
+        return [int(v) for v in out[:k]], list(st)
 
     def set_order(self, order):
         self.lib.ref_set_order(order)

@@ -32,7 +32,15 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_moe_set_expert", "waste_hip_moe_bind_expert", "waste_hip_moe_forward",
            "waste_hip_moe_status", "waste_hip_moe_bytes", "waste_hip_moe_dequant",
            "waste_hip_moe_profile", "waste_hip_moe_profile_read", "waste_hip_record_bytes",
-           "waste_hip_synth_codebooks", "waste_hip_synth_records"]
+           "waste_hip_synth_codebooks", "waste_hip_synth_records",
+           "waste_hip_moe_route", "waste_hip_moe_experts", "waste_hip_moe_bind_table",
+           "waste_hip_moe_predict",
+           "waste_hip_ecache_create", "waste_hip_ecache_destroy", "waste_hip_ecache_set_source",
+           "waste_hip_ecache_hint", "waste_hip_ecache_prefetch", "waste_hip_ecache_get",
+           "waste_hip_ecache_hold", "waste_hip_ecache_release", "waste_hip_ecache_admit",
+           "waste_hip_ecache_resident_mask", "waste_hip_ecache_resident_all",
+           "waste_hip_ecache_stats", "waste_hip_ecache_slot", "waste_hip_ecache_n_slots",
+           "waste_hip_ecache_sync"]
 
 STAGES = ["router_shared_gate_up", "route", "routed_gate_up", "swiglu", "routed_down",
           "shared_down", "combine"]
@@ -59,6 +67,12 @@ class MoeProf(C.Structure):
     _fields_ = [("forwards", C.c_int), ("ms", C.c_float * 7)]
 
 
+class EcacheCounts(C.Structure):
+    _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("evictions", C.c_uint64),
+                ("prefetched", C.c_uint64), ("spec_issued", C.c_uint64), ("reads", C.c_uint64),
+                ("bytes_read", C.c_uint64)]
+
+
 class VqJob(C.Structure):
     """waste_vq_job (src/waste_metal.h:31-40)."""
     _fields_ = [("y", C.c_void_p), ("rec", C.c_void_p), ("rec_bytes", C.c_size_t),
@@ -78,7 +92,7 @@ def lib():
     if not os.path.exists(LIB_PATH):
         raise HipError(f"{LIB_PATH} is missing: build it with `python -m warp_amd.build`")
     L = C.CDLL(LIB_PATH)
-    vp, i = C.c_void_p, C.c_int
+    vp, i, ip = C.c_void_p, C.c_int, C.POINTER(C.c_int)
     sig = {
         "waste_hip_device_name": (C.c_char_p, []),
         "waste_register_hip": (C.c_char_p, [vp]),
@@ -97,6 +111,25 @@ def lib():
         "waste_hip_moe_dequant": (i, [vp, i, i, vp, vp]),
         "waste_hip_moe_profile": (i, [vp, i]),
         "waste_hip_moe_profile_read": (i, [vp, C.POINTER(MoeProf)]),
+        "waste_hip_moe_route": (i, [vp, vp, i, i, vp, vp, vp, vp]),
+        "waste_hip_moe_experts": (i, [vp, vp, i, i, vp, vp]),
+        "waste_hip_moe_bind_table": (i, [vp, ip, C.POINTER(vp), i, i, vp]),
+        "waste_hip_moe_predict": (i, [vp, vp, i, i, vp, vp]),
+        "waste_hip_ecache_create": (i, [C.c_size_t, C.c_size_t, i, i, i, C.POINTER(vp)]),
+        "waste_hip_ecache_destroy": (None, [vp]),
+        "waste_hip_ecache_set_source": (i, [vp, C.POINTER(vp), i, i]),
+        "waste_hip_ecache_hint": (i, [vp, i, ip, i]),
+        "waste_hip_ecache_prefetch": (i, [vp, i, ip, i]),
+        "waste_hip_ecache_get": (vp, [vp, i, i, vp]),
+        "waste_hip_ecache_hold": (vp, [vp, i, i, vp]),
+        "waste_hip_ecache_release": (i, [vp, vp]),
+        "waste_hip_ecache_admit": (i, [vp, i, i]),
+        "waste_hip_ecache_resident_mask": (i, [vp, i, i, C.POINTER(C.c_uint8)]),
+        "waste_hip_ecache_resident_all": (i, [vp, i, ip, i]),
+        "waste_hip_ecache_stats": (i, [vp, C.POINTER(EcacheCounts)]),
+        "waste_hip_ecache_slot": (i, [vp, i, i]),
+        "waste_hip_ecache_n_slots": (i, [vp]),
+        "waste_hip_ecache_sync": (i, [vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -192,3 +225,99 @@ class MoeLayer:
 
     def dequant(self, e, kind, W_ptr, stream=None):
         return self.L.waste_hip_moe_dequant(self.h, e, kind, W_ptr, stream)
+
+    def route(self, x_ptr, T, ids_ptr=None, w_ptr=None, logits_ptr=None, bf16=False, stream=None):
+        check(self.L.waste_hip_moe_route(self.h, x_ptr, int(bf16), T, ids_ptr, w_ptr, logits_ptr,
+                                         stream), "route")
+
+    def experts(self, x_ptr, T, y_ptr, bf16=False, stream=None):
+        check(self.L.waste_hip_moe_experts(self.h, x_ptr, int(bf16), T, y_ptr, stream), "experts")
+
+    def bind_table(self, experts, dev_ptrs, codebook_id=-1, stream=None):
+        n = len(experts)
+        ids = (C.c_int * max(n, 1))(*experts)
+        ptrs = (C.c_void_p * max(n, 1))(*dev_ptrs)
+        return self.L.waste_hip_moe_bind_table(self.h, ids, ptrs, n, codebook_id, stream)
+
+    def predict(self, x_ptr, n, ids_ptr, bf16=False, stream=None):
+        check(self.L.waste_hip_moe_predict(self.h, x_ptr, int(bf16), n, ids_ptr, stream), "predict")
+
+
+def _ids(ids):
+    a = (C.c_int * max(len(ids), 1))(*[int(v) for v in ids])
+    return a, len(ids)
+
+
+class ExpertCache:
+    """The HBM expert cache (waste_hip_ecache).  dry=True runs the policy
+    alone, with no device."""
+
+    def __init__(self, rec_bytes, budget_bytes, *, policy=0, depth=2, dry=False):
+        self.L = lib()
+        h = C.c_void_p()
+        check(self.L.waste_hip_ecache_create(rec_bytes, budget_bytes, policy, depth, int(dry),
+                                             C.byref(h)), "waste_hip_ecache_create")
+        self.h = h
+        self.dry = dry
+        self.rec_bytes = rec_bytes
+        self._src = None
+
+    def close(self):
+        if self.h:
+            self.L.waste_hip_ecache_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def n_slots(self):
+        return self.L.waste_hip_ecache_n_slots(self.h)
+
+    def set_source(self, ptrs, n_layers, n_experts):
+        """Host record addresses, [layer][expert] flattened; kept alive here."""
+        self._src = (C.c_void_p * len(ptrs))(*ptrs)
+        check(self.L.waste_hip_ecache_set_source(self.h, self._src, n_layers, n_experts), "set_source")
+
+    def hint(self, layer, ids):
+        a, n = _ids(ids)
+        check(self.L.waste_hip_ecache_hint(self.h, layer, a, n), "hint")
+
+    def prefetch(self, layer, ids):
+        a, n = _ids(ids)
+        check(self.L.waste_hip_ecache_prefetch(self.h, layer, a, n), "prefetch")
+
+    def get(self, layer, expert, stream=None):
+        return self.L.waste_hip_ecache_get(self.h, layer, expert, stream)
+
+    def hold(self, layer, expert, stream=None):
+        return self.L.waste_hip_ecache_hold(self.h, layer, expert, stream)
+
+    def release(self, stream=None):
+        check(self.L.waste_hip_ecache_release(self.h, stream), "release")
+
+    def admit(self, layer, expert):
+        return self.L.waste_hip_ecache_admit(self.h, layer, expert)
+
+    def resident_mask(self, layer, n):
+        out = (C.c_uint8 * max(n, 1))()
+        check(self.L.waste_hip_ecache_resident_mask(self.h, layer, n, out), "resident_mask")
+        return [int(v) for v in out[:n]]
+
+    def resident_all(self, layer, ids):
+        a, n = _ids(ids)
+        return self.L.waste_hip_ecache_resident_all(self.h, layer, a, n)
+
+    def slot(self, layer, expert):
+        return self.L.waste_hip_ecache_slot(self.h, layer, expert)
+
+    def stats(self):
+        c = EcacheCounts()
+        check(self.L.waste_hip_ecache_stats(self.h, C.byref(c)), "stats")
+        return {k: int(getattr(c, k)) for k, _ in EcacheCounts._fields_}
+
+    def sync(self):
+        check(self.L.waste_hip_ecache_sync(self.h), "sync")

@@ -168,6 +168,19 @@ typedef struct {
 } whip_vq_job;
 int whip_vq3r_jobs(const whip_vq_job *jobs, int n, hipStream_t s);
 
+/* Table entries written in stream order, each header checked on the
+ * device (bit 8 of err when one fails; that entry is left NULL). */
+#define WHIP_BIND_MAX 64
+typedef struct {
+    int n;
+    int expert[WHIP_BIND_MAX];
+    const uint8_t *rec[WHIP_BIND_MAX];
+    uint32_t layer, rec_4k_blocks, off_up, off_down, off_sc;
+    int cb;                        /* required codebook id, -1 any          */
+    int n_books;
+} whip_bind_args;
+int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err, hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,7 +53,9 @@ struct waste_hip_moe {
     int32_t *pair_pos, *seg_off, *order;
     uint16_t *h16, *sh_h16;      /* fp16 [P][I], [T][SI]                   */
     float *ypair, *rpart;        /* [P][H]; router partial sums            */
-    int *err;
+    int *err;                    /* [0] status bits; [4] the lookahead's    */
+    float *plogits, *pw;         /* the lookahead's logits and weights      */
+    int routed_T;                /* T of the last route(), 0 none          */
     int prof_on;
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
     waste_hip_moe_prof prof;
@@ -114,7 +116,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->logits, m->w, m->pair_w, m->part_gu, m->h, m->part_d, m->sh_a,
                      m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
                      m->tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
-                     m->sh_h16, m->ypair, m->rpart, m->d_books16 };
+                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0])
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -198,6 +200,8 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->h, (size_t)Pd * m->I * 4);
     rc |= dmalloc((void **)&m->part_d, ((size_t)Pd * m->nch_d * m->H + 64) * 4);
     rc |= dmalloc((void **)&m->err, 64);
+    rc |= dmalloc((void **)&m->plogits, (size_t)m->E * 4);
+    rc |= dmalloc((void **)&m->pw, 64 * 4);
     if (m->T > m->Td) {
         rc |= dmalloc((void **)&m->pair_pos, (size_t)P * 4);
         rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
@@ -396,22 +400,21 @@ static int prof_end(waste_hip_moe *m)
     return 0;
 }
 
+#define MARK(i) do { if (m->prof_on) CK(hipEventRecord(m->ev[i], s)); } while (0)
+
 /* T > Td: moe_chunk (src/model.c:7110-7285) as grouped products on the
  * matrix cores.  Stages as forward(): 0 router (+ shared gate/up), 1
  * routing and the pair sort, 2 routed gate/up with SwiGLU, 3 (empty),
  * 4 routed down, 5 shared down, 6 combine. */
-static int forward_many(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
-                        int32_t *ids, float *w, float *logits, hipStream_t s)
+static int route_many(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t *d_ids,
+                      float *d_w, float *lg, hipStream_t s)
 {
-    const int E = m->E, K = m->K, H = m->H, I = m->I;
-    const int mb = (T + 127) / 128;
+    const int E = m->E, K = m->K, H = m->H;
     if ((uintptr_t)x % 16) return WASTE_HIP_EINVAL;
-#define MARK(i) do { if (m->prof_on) CK(hipEventRecord(m->ev[i], s)); } while (0)
     MARK(0);
-    float *lg = logits ? logits : m->logits;
     CK((hipError_t)whip_pf_router(&m->router, x, x_bf16, T, m->rpart, lg, s));
-    whip_pf_args a;
     if (m->has_shared) {
+        whip_pf_args a;
         memset(&a, 0, sizeof a);
         a.W0 = (const uint8_t *)m->sh[0].q; a.W1 = (const uint8_t *)m->sh[1].q;
         a.S0 = m->sh[0].qs; a.S1 = m->sh[1].qs; a.rowbytes = m->sh[0].rowbytes; a.group = m->sh[0].group;
@@ -422,12 +425,18 @@ static int forward_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
     MARK(1);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
-    int32_t *d_ids = ids ? ids : m->ids;
-    float *d_w = w ? w : m->w;
     CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, NULL, NULL, NULL, NULL, m->err, s));
     CK((hipError_t)whip_sort_pairs(d_ids, d_w, T, K, E, m->pair_tok, m->pair_exp, m->pair_w,
                                    m->tok_pairs, m->pair_pos, m->seg_off, m->order, s));
+    return 0;
+}
+
+static int experts_many(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
+{
+    const int E = m->E, K = m->K, H = m->H, I = m->I;
+    const int mb = (T + 127) / 128;
     MARK(2);
+    whip_pf_args a;
     memset(&a, 0, sizeof a);
     a.recs = m->d_recs; a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.sc_off[0] = m->off_sc; a.sc_off[1] = m->off_sc + 2u * (uint32_t)I;
@@ -454,23 +463,17 @@ static int forward_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
     CK((hipError_t)whip_pf_combine(m->tok_pairs, m->pair_exp, m->pair_w, m->d_recs, T, K, E, m->ypair, H,
                                    m->has_shared ? m->sh_out : NULL, y, s));
     MARK(7);
-#undef MARK
     return prof_end(m);
 }
 
-int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
-                          int32_t *ids, float *w, float *logits, void *stream)
+/* T <= Td: moe_layer (T = 1, src/model.c:5488-5939) and moe_chunk's order
+ * for small chunks, on the decode kernels. */
+static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t *d_ids, float *d_w,
+                     float *lg, hipStream_t s)
 {
-    if (!m || !x || !y || T <= 0 || T > m->T) return WASTE_HIP_EINVAL;
-    if (!m->has_router || !m->d_booksT || m->cb < 0 || m->cb + 9 > m->n_books)
-        return WASTE_HIP_EINVAL;
-    hipStream_t s = (hipStream_t)stream;
-    if (T > m->Td) return forward_many(m, x, x_bf16, T, y, ids, w, logits, s);
-    const int E = m->E, K = m->K, H = m->H, I = m->I, P = T * K;
-#define MARK(i) do { if (m->prof_on) CK(hipEventRecord(m->ev[i], s)); } while (0)
+    const int E = m->E, K = m->K, H = m->H;
     MARK(0);
     /* router logits and the shared expert's silu(gate.x)*(up.x): one launch */
-    float *lg = logits ? logits : m->logits;
     whip_gemv_job jobs[2];
     int nj = 0;
     jobs[nj].A = m->router; jobs[nj].B = NULL; jobs[nj].x = x; jobs[nj].x_ld = H;
@@ -483,15 +486,18 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     MARK(1);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
-    int32_t *d_ids = ids ? ids : m->ids;
-    float *d_w = w ? w : m->w;
     CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, m->pair_tok, m->pair_exp,
                               m->pair_w, m->tok_pairs, m->err, s));
     if (T > 1)
         CK((hipError_t)whip_pairs(d_ids, d_w, T, K, E, m->pair_tok, m->pair_exp, m->pair_w,
                                   m->tok_pairs, s));
-    MARK(2);
+    return 0;
+}
 
+static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
+{
+    const int K = m->K, H = m->H, I = m->I, P = T * K;
+    MARK(2);
     whip_vq_args a;
     memset(&a, 0, sizeof a);
     a.recs = m->d_recs; a.pair_exp = m->pair_exp; a.pair_src = m->pair_tok;
@@ -522,8 +528,103 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
                                 m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1,
                                 m->has_shared ? m->sh_out : NULL, y, s));
     MARK(7);
-#undef MARK
     return prof_end(m);
+}
+#undef MARK
+
+static int ready(const waste_hip_moe *m, const void *x, int T)
+{
+    if (!m || !x || T <= 0 || T > m->T) return WASTE_HIP_EINVAL;
+    if (!m->has_router || !m->d_booksT || m->n_books < 9) return WASTE_HIP_EINVAL;
+    return 0;
+}
+
+int waste_hip_moe_route(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t *ids, float *w,
+                        float *logits, void *stream)
+{
+    const int rc = ready(m, x, T);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    int32_t *d_ids = ids ? ids : m->ids;
+    float *d_w = w ? w : m->w;
+    float *lg = logits ? logits : m->logits;
+    m->routed_T = 0;
+    const int r = T > m->Td ? route_many(m, x, x_bf16, T, d_ids, d_w, lg, s)
+                            : route_few(m, x, x_bf16, T, d_ids, d_w, lg, s);
+    if (r) return r;
+    m->routed_T = T;
+    return 0;
+}
+
+int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, void *stream)
+{
+    const int rc = ready(m, x, T);
+    if (rc) return rc;
+    if (!y || T != m->routed_T) return WASTE_HIP_EINVAL;
+    if (m->cb < 0 || m->cb + 9 > m->n_books) return WASTE_HIP_EINVAL;
+    hipStream_t s = (hipStream_t)stream;
+    return T > m->Td ? experts_many(m, x, x_bf16, T, y, s) : experts_few(m, x, x_bf16, T, y, s);
+}
+
+int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
+                          int32_t *ids, float *w, float *logits, void *stream)
+{
+    int rc = ready(m, x, T);
+    if (rc) return rc;
+    if (!y || m->cb < 0 || m->cb + 9 > m->n_books) return WASTE_HIP_EINVAL;
+    rc = waste_hip_moe_route(m, x, x_bf16, T, ids, w, logits, stream);
+    return rc ? rc : waste_hip_moe_experts(m, x, x_bf16, T, y, stream);
+}
+
+int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *const *dev_records, int n,
+                             int codebook_id, void *stream)
+{
+    if (!m || n < 0 || n > WHIP_BIND_MAX || (n && (!experts || !dev_records))) return WASTE_HIP_EINVAL;
+    if (codebook_id < -1 || codebook_id > 65535) return WASTE_HIP_EINVAL;
+    whip_bind_args a;
+    memset(&a, 0, sizeof a);
+    for (int i = 0; i < n; i++) {
+        const int e = experts[i];
+        if (e < 0 || e >= m->E || (uintptr_t)dev_records[i] % 16) return WASTE_HIP_EINVAL;
+        for (int j = 0; j < i; j++)
+            if (experts[j] == e) return WASTE_HIP_EINVAL;
+        a.expert[i] = e;
+        a.rec[i] = (const uint8_t *)dev_records[i];
+    }
+    if (codebook_id >= 0) {
+        if (m->cb >= 0 && m->cb != codebook_id) return WASTE_HIP_ERECORD;
+        m->cb = codebook_id;
+    }
+    a.n = n;
+    a.layer = (uint16_t)m->c.layer;
+    a.rec_4k_blocks = (uint32_t)(m->rec_bytes / 4096);
+    a.off_up = m->off_up; a.off_down = m->off_down; a.off_sc = m->off_sc;
+    a.cb = m->cb;
+    a.n_books = m->n_books > 0 ? m->n_books : 65536 + 9;
+    CK((hipError_t)whip_bind(m->d_recs, &a, m->err, (hipStream_t)stream));
+    for (int i = 0; i < n; i++) {
+        const int e = a.expert[i];
+        if (m->h_recs[e] && !a.rec[i]) m->bound--;
+        if (!m->h_recs[e] && a.rec[i]) m->bound++;
+        m->h_recs[e] = a.rec[i];
+    }
+    return 0;
+}
+
+int waste_hip_moe_predict(waste_hip_moe *m, const void *x, int x_bf16, int n, int32_t *ids, void *stream)
+{
+    if (!m || !x || !ids || n <= 0 || n > 64 || !m->has_router) return WASTE_HIP_EINVAL;
+    if (n > m->E) n = m->E;
+    hipStream_t s = (hipStream_t)stream;
+    whip_gemv_job j;
+    j.A = m->router; j.B = NULL; j.x = x; j.x_ld = m->H; j.x_bf16 = x_bf16; j.y = m->plogits;
+    j.y_ld = m->E;
+    CK((hipError_t)whip_gemv_multi(&j, 1, 1, s));
+    /* selection order only: no group limit, weights unused */
+    whip_route_cfg rc = { m->E, n, m->c.score_func, 0, 1.0f, 0, 0 };
+    CK((hipError_t)whip_route(&rc, m->plogits, m->d_bias, 1, ids, m->pw, NULL, NULL, NULL, NULL,
+                              m->err + 4, s));
+    return 0;
 }
 
 int waste_hip_moe_profile(waste_hip_moe *m, int on)
@@ -554,6 +655,7 @@ int waste_hip_moe_status(waste_hip_moe *m, void *stream)
     /* a failed route leaves ids of -1, which the expert kernels then see
      * as unbound: report the cause */
     if (e & 2) return WASTE_HIP_EROUTE;
+    if (e & 8) return WASTE_HIP_ERECORD;
     if (e & 1) return WASTE_HIP_EUNBOUND;
     if (e & 4) return WASTE_HIP_ERANGE;
     return 0;
