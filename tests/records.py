@@ -71,12 +71,13 @@ class Layer:
     def __init__(self, H, I, E, K, *, score_func=0, renorm=0, routed_scale=1.0,
                  n_group=1, topk_group=1, n_shared=0, router_fmt=FMT_F32,
                  shared_fmt=FMT_Q8G, bias=False, seed=0, cb_base=0,
-                 book_scale=0.3, subnormal_books=0):
+                 book_scale=0.3, subnormal_books=0, layer=0):
         rng = np.random.default_rng(seed)
         self.H, self.I, self.E, self.K = H, I, E, K
         self.score_func, self.renorm, self.routed_scale = score_func, renorm, routed_scale
         self.n_group, self.topk_group, self.n_shared = n_group, topk_group, n_shared
         self.cb_base = cb_base
+        self.layer = layer
         self.n_books = cb_base + 3 * STAGES
         books = (rng.standard_normal((self.n_books, ENTRIES, VEC_DIM)) * book_scale).astype(np.float32)
         self.books_f16 = f16_bits(books)
@@ -96,7 +97,7 @@ class Layer:
             sl = [f16_bits(rng.uniform(0.01, 0.05, M)) for M, _ in shapes]
             self.idx.append(il)
             self.scales.append(sl)
-            self.records.append(make_record(0, e, cb_base, shapes, il, sl))
+            self.records.append(make_record(layer, e, cb_base, shapes, il, sl))
         self.rec_bytes = len(self.records[0])
         self.router = Tensor.make(router_fmt, (rng.standard_normal((E, H)) * 0.02).astype(np.float32))
         self.bias = (rng.standard_normal(E) * 0.02).astype(np.float32) if bias else None

@@ -1,0 +1,250 @@
+# SPDX-License-Identifier: Apache-2.0
+"""The layer driven through an expert cache, on an MI355X, through the C ABI.
+
+  route + experts          bit-identical to forward (same kernels, split)
+  bind_table               bit-identical to set_expert; a record with the
+                           wrong header is refused on the device (ERECORD)
+  predict                  the lookahead's ids bit-exact against the
+                           oracle's predict_next_moe on the device logits
+  cache-fed layers         every layer output within 1e-3 of the oracle's
+                           moe_layer on the full record set, ids bit-exact,
+                           dequantised slot contents bit-exact; the cache's
+                           decisions equal its dry replay
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import ecache_script as es
+from gpu_util import LAYER_RTOL, gpu_layer, rel_err
+from oracle_lib import Oracle
+from records import FMT_F32, FMT_Q4G, Layer
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+import warp_amd  # noqa: E402
+from test_gpu_parity import bits, check_routing, make_case  # noqa: E402
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return Oracle()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dsv3_layer(layer, seed):
+    return Layer(1024, 256, 64, 8, score_func=0, renorm=1, routed_scale=2.5, bias=True,
+                 n_group=8, topk_group=4, n_shared=1, shared_fmt=FMT_Q4G, router_fmt=FMT_F32,
+                 seed=seed, layer=layer)
+
+
+def bf16_inputs(L, T, seed):
+    X = L.inputs(T, seed=seed)
+    return torch.from_numpy(X).to(torch.bfloat16).to(torch.float32).numpy()
+
+
+@pytest.mark.parametrize("T,prefill_min", [(1, 0), (8, 0), (64, 16)])
+def test_route_experts_equal_forward(orc, T, prefill_min):
+    say("test_route_experts_equal_forward", T)
+    L, X, bf16 = make_case("dsv3_small", T)
+    m = gpu_layer(L, max_tokens=T, prefill_min=prefill_min)
+    dev = torch.device("cuda:0")
+    xd = torch.from_numpy(X).to(dev).to(torch.bfloat16)
+    outs = []
+    for split in (False, True):
+        y = torch.full((T, L.H), float("nan"), device=dev)
+        ids = torch.empty((T, L.K), dtype=torch.int32, device=dev)
+        w = torch.empty((T, L.K), dtype=torch.float32, device=dev)
+        if split:
+            m.route(xd.data_ptr(), T, ids.data_ptr(), w.data_ptr(), None, bf16=True, stream=stream())
+            m.experts(xd.data_ptr(), T, y.data_ptr(), bf16=True, stream=stream())
+        else:
+            m.forward(xd.data_ptr(), T, y.data_ptr(), ids.data_ptr(), w.data_ptr(), None, bf16=True,
+                      stream=stream())
+        assert m.status(stream()) == 0
+        outs.append((y.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy()))
+    assert np.array_equal(bits(outs[0][0]), bits(outs[1][0]))
+    assert np.array_equal(outs[0][1], outs[1][1])
+    assert np.array_equal(bits(outs[0][2]), bits(outs[1][2]))
+    # experts() needs the route of the same T first
+    m2 = gpu_layer(L, max_tokens=T, prefill_min=prefill_min)
+    y = torch.empty((T, L.H), device=dev)
+    with pytest.raises(warp_amd.HipError):
+        m2.experts(xd.data_ptr(), T, y.data_ptr(), bf16=True, stream=stream())
+    m.close()
+    m2.close()
+
+
+def test_bind_table_equals_set_expert(orc):
+    say("test_bind_table_equals_set_expert")
+    L, X, bf16 = make_case("dsv3_small", 1)
+    dev = torch.device("cuda:0")
+    ref = gpu_layer(L)
+    slab = torch.from_numpy(np.frombuffer(L.bank(), np.uint8).copy()).to(dev)
+    base = slab.data_ptr()
+    assert base % 256 == 0
+    m = gpu_layer(L, records=False)
+    xd = torch.from_numpy(X).to(dev).to(torch.bfloat16)
+
+    def run(layer):
+        y = torch.full((1, L.H), float("nan"), device=dev)
+        ids = torch.empty((1, L.K), dtype=torch.int32, device=dev)
+        layer.forward(xd.data_ptr(), 1, y.data_ptr(), ids.data_ptr(), None, None, bf16=True,
+                      stream=stream())
+        return layer.status(stream()), y.cpu().numpy(), ids.cpu().numpy()
+
+    # the whole table, in two calls of 32, stream-ordered (no host wait)
+    for lo in (0, 32):
+        es_ = list(range(lo, lo + 32))
+        assert m.bind_table(es_, [base + e * L.rec_bytes for e in es_], codebook_id=L.cb_base,
+                            stream=stream()) == 0
+    st0, y0, i0 = run(ref)
+    st1, y1, i1 = run(m)
+    assert st0 == 0 and st1 == 0
+    assert np.array_equal(i0, i1) and np.array_equal(bits(y0), bits(y1))
+
+    # a record whose header names another expert is refused on the device
+    e = int(i1[0, 0])
+    wrong = (e + 1) % L.E
+    assert m.bind_table([e], [base + wrong * L.rec_bytes], stream=stream()) == 0
+    st, y, _ = run(m)
+    assert st == warp_amd.ERECORD
+    assert m.bind_table([e], [base + e * L.rec_bytes], stream=stream()) == 0
+    st, y, _ = run(m)
+    assert st == 0 and np.array_equal(bits(y), bits(y1))
+    # unbinding a routed expert: its rows are zeros and status says so
+    assert m.bind_table([e], [None], stream=stream()) == 0
+    st, y, _ = run(m)
+    assert st == warp_amd.EUNBOUND
+    # host-side argument checks
+    assert m.bind_table([1, 1], [base + L.rec_bytes] * 2) == warp_amd.EINVAL
+    assert m.bind_table([1], [base + L.rec_bytes + 8]) == warp_amd.EINVAL
+    assert m.bind_table([1], [base + L.rec_bytes], codebook_id=L.cb_base + 1) == warp_amd.ERECORD
+    m.close()
+    ref.close()
+
+
+@pytest.mark.parametrize("name,n", [("dsv3_small", 6), ("dsv3_small", 64), ("kimi_small", 16),
+                                    ("olmoe_small", 5)])
+def test_predict_matches_oracle(orc, name, n):
+    say("test_predict_matches_oracle", name, n)
+    L, X, bf16 = make_case(name, 4)
+    m = gpu_layer(L)
+    dev = torch.device("cuda:0")
+    for t in range(X.shape[0]):
+        xd = torch.from_numpy(X[t:t + 1]).to(dev)
+        if bf16:
+            xd = xd.to(torch.bfloat16)
+        lg = torch.empty((1, L.E), device=dev)
+        y = torch.empty((1, L.H), device=dev)
+        m.forward(xd.data_ptr(), 1, y.data_ptr(), None, None, lg.data_ptr(), bf16=bf16, stream=stream())
+        ids = torch.full((64,), -5, dtype=torch.int32, device=dev)
+        m.predict(xd.data_ptr(), n, ids.data_ptr(), bf16=bf16, stream=stream())
+        assert m.status(stream()) == 0
+        got = ids.cpu().numpy()
+        want = orc.predict_next(L.score_func, lg.cpu().numpy()[0], L.bias, n)
+        k = min(n, L.E)
+        assert np.array_equal(got[:k], want), (t, got[:k], want)
+        assert np.all(got[k:] == -5)
+    m.close()
+
+
+@pytest.mark.parametrize("n_slots,depth,look,own", [(20, 2, 6, False), (72, 2, 6, True),
+                                                   (200, 2, 0, False), (24, 4, 16, True)])
+def test_cache_fed_layers(orc, n_slots, depth, look, own):
+    """Three layers, 10 tokens, the cache smaller than the expert set: every
+    output against the oracle on the full record set.  own: on a stream of
+    its own rather than the null stream."""
+    say("test_cache_fed_layers", n_slots, depth, look, own)
+    if own:
+        with torch.cuda.stream(torch.cuda.Stream()):
+            _cache_fed_layers(orc, n_slots, depth, look)
+    else:
+        _cache_fed_layers(orc, n_slots, depth, look)
+
+
+def _cache_fed_layers(orc, n_slots, depth, look):
+    n_layers, T = 3, 10
+    dev = torch.device("cuda:0")
+    Ls = [dsv3_layer(l, 300 + l) for l in range(n_layers)]
+    rec = Ls[0].rec_bytes
+    host = torch.empty((n_layers * Ls[0].E, rec), dtype=torch.uint8, pin_memory=True)
+    for l, L in enumerate(Ls):
+        host[l * L.E:(l + 1) * L.E] = torch.from_numpy(np.frombuffer(L.bank(), np.uint8).reshape(L.E, rec).copy())
+    cache = warp_amd.ExpertCache(rec, n_slots * rec, policy=0, depth=depth)
+    cache.set_source([host.data_ptr() + i * rec for i in range(n_layers * Ls[0].E)], n_layers, Ls[0].E)
+    ms = [gpu_layer(L, records=False) for L in Ls]
+    ols = [orc.moe(L, 1) for L in Ls]
+    ops = []
+    s = stream()
+    ids_d = torch.empty((1, 8), dtype=torch.int32, device=dev)
+    look_d = torch.empty((64,), dtype=torch.int32, device=dev)
+    worst = 0.0
+    books = [orc.books(L.books_f16)[0] for L in Ls]
+    for t in range(T):
+        xs = [bf16_inputs(L, 1, 1000 * t + l) for l, L in enumerate(Ls)]
+        for l, (L, m) in enumerate(zip(Ls, ms)):
+            xd = torch.from_numpy(xs[l]).to(dev).to(torch.bfloat16)
+            lg = torch.empty((1, L.E), device=dev)
+            w_d = torch.empty((1, 8), device=dev)
+            m.route(xd.data_ptr(), 1, ids_d.data_ptr(), w_d.data_ptr(), lg.data_ptr(), bf16=True, stream=s)
+            if look and l + 1 < n_layers:
+                ms[l + 1].predict(xd.data_ptr(), look, look_d.data_ptr(), bf16=True, stream=s)
+            ids = ids_d.cpu().numpy()[0].tolist()            # waits for the route
+            cache.hint(l, ids)
+            ops += [es.HINT, l, len(ids)] + ids
+            ptrs = []
+            for e in ids:
+                p = cache.hold(l, e, s)
+                assert p, (t, l, e)
+                ptrs.append(p)
+                ops += [es.HOLD, l, e]
+            assert m.bind_table(ids, ptrs, codebook_id=L.cb_base, stream=s) == 0
+            y = torch.full((1, L.H), float("nan"), device=dev)
+            m.experts(xd.data_ptr(), 1, y.data_ptr(), bf16=True, stream=s)
+            if t == T - 1:
+                # the slot bytes themselves, through the bound table
+                e = ids[0]
+                for kind, (M, N) in enumerate(L.shapes):
+                    W = torch.empty((M, N), device=dev)
+                    assert m.dequant(e, kind, W.data_ptr(), s) == 0
+                    off = [48, 48 + L.I * L.H * 3 // 8, 48 + 2 * L.I * L.H * 3 // 8][kind]
+                    want = orc.dequant(L.records[e][off:], L.scales[e][kind], books[l], 3 * kind, M, N)
+                    assert np.array_equal(bits(W.cpu().numpy()), bits(want)), (l, e, kind)
+            cache.release(s)
+            ops += [es.RELEASE]
+            if look and l + 1 < n_layers:
+                guess = look_d.cpu().numpy()[:look].tolist()
+                cache.prefetch(l + 1, guess)
+                ops += [es.PREFETCH, l + 1, len(guess)] + guess
+            st = m.status(s)
+            assert st == 0, (t, l, st)
+            check_routing(orc, L, lg.cpu().numpy(), ids_d.cpu().numpy(), w_d.cpu().numpy())
+            rc, ref = ols[l].apply(xs[l], ids_d.cpu().numpy(), w_d.cpu().numpy(), chunk=0)
+            assert rc == 0
+            e_ = rel_err(y.cpu().numpy(), ref)
+            worst = max(worst, e_)
+            assert e_ <= LAYER_RTOL, (t, l, e_)
+    cache.sync()
+    got = cache.stats()
+    dry = warp_amd.ExpertCache(rec, n_slots * rec, policy=0, depth=depth, dry=True)
+    _, dst = es.run_product(dry, ops)
+    assert [got[k] for k in ("hits", "misses", "evictions", "prefetched", "spec_issued", "reads")] == dst
+    say(f"  slots {n_slots}: hits {got['hits']} misses {got['misses']} evictions {got['evictions']} "
+        f"spec {got['spec_issued']}, worst layer rel err {worst:.2e}")
+    if n_slots < n_layers * 64:
+        assert got["evictions"] > 0
+    for m in ms:
+        m.close()
+    cache.close()

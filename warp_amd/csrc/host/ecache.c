@@ -45,7 +45,8 @@ typedef struct {
     uint64_t use;                    /* release that last covered a reader */
     hipEvent_t filled;
     int has_fill;
-    void *waited;                    /* a stream already ordered after it  */
+    int has_waiter;                  /* `waited` is ordered after the fill */
+    void *waited;                    /* (the null stream is a value too)   */
 } slot_t;
 
 struct waste_hip_ecache {
@@ -169,7 +170,7 @@ static int start_fill(waste_hip_ecache *c, int si, int layer, int expert)
         goto fail;
     if (hipEventRecord(q->filled, c->fill) != hipSuccess) goto fail;
     q->has_fill = 1;
-    q->waited = NULL;
+    q->has_waiter = 0;
     return 0;
 fail:
     c->failed = 1;
@@ -351,8 +352,9 @@ static const void *hand_out(waste_hip_ecache *c, int si, void *stream)
         c->out_list[c->n_out++] = si;
     }
     if (c->dry) return (const void *)(uintptr_t)(((size_t)si + 1) * c->rec_bytes);
-    if (q->has_fill && q->waited != stream) {
+    if (q->has_fill && !(q->has_waiter && q->waited == stream)) {
         if (hipStreamWaitEvent((hipStream_t)stream, q->filled, 0) != hipSuccess) return NULL;
+        q->has_waiter = 1;
         q->waited = stream;
     }
     return c->slab + (size_t)si * c->rec_bytes;
