@@ -175,6 +175,22 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts,
 int waste_hip_moe_predict(waste_hip_moe *m, const void *x, int x_bf16, int n,
                           int32_t *ids, void *stream);
 
+/* Forward declaration; the cache is section 4. */
+typedef struct waste_hip_ecache waste_hip_ecache;
+
+/* One decode token through an expert cache, moe_layer's order
+ * (src/model.c:5639-5700, 5921-5930): route; the lookahead (next's router
+ * on this x, `lookahead` ids, 0 = none); the selection to the host (the
+ * one host wait); hint and hold each expert (misses fill on the cache's
+ * stream, which `stream` then waits for); bind; experts; release; the
+ * lookahead's reads for layer + 1.  `layer` is the cache key's layer (the
+ * engine's layer index); the layer's codebook id must be known (a bound
+ * record, or bind_table with n = 0).  ids, w as in forward. */
+int waste_hip_moe_forward_cached(waste_hip_moe *m, waste_hip_ecache *c, int layer,
+                                 waste_hip_moe *next, int lookahead, const void *x,
+                                 int x_bf16, float *y, int32_t *ids, float *w,
+                                 void *stream);
+
 /* Waits for the layer's work and returns the sticky device error (0, or
  * WASTE_HIP_EROUTE / WASTE_HIP_ERECORD / WASTE_HIP_EUNBOUND /
  * WASTE_HIP_ERANGE), clearing it. */
@@ -223,7 +239,6 @@ int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W,
  * is copied) — for replaying a routing trace.
  * Replaces: waste_ecache_init/get/hold/release/hint/prefetch/admit/
  * resident_mask/resident_all, src/ecache.h:128-230. */
-typedef struct waste_hip_ecache waste_hip_ecache;
 typedef struct {
     uint64_t hits, misses, evictions;
     uint64_t prefetched;     /* misses the hint's read-ahead issued        */

@@ -248,3 +248,60 @@ def _cache_fed_layers(orc, n_slots, depth, look):
     for m in ms:
         m.close()
     cache.close()
+
+
+@pytest.mark.parametrize("n_slots,look", [(24, 6), (100, 0)])
+def test_forward_cached(orc, n_slots, look):
+    """The native cache path (one call per layer) against the oracle, and
+    its cache decisions against a dry replay of the same calls."""
+    say("test_forward_cached", n_slots, look)
+    n_layers, T = 3, 8
+    dev = torch.device("cuda:0")
+    Ls = [dsv3_layer(l, 400 + l) for l in range(n_layers)]
+    rec = Ls[0].rec_bytes
+    host = torch.empty((n_layers * Ls[0].E, rec), dtype=torch.uint8, pin_memory=True)
+    for l, L in enumerate(Ls):
+        host[l * L.E:(l + 1) * L.E] = torch.from_numpy(
+            np.frombuffer(L.bank(), np.uint8).reshape(L.E, rec).copy())
+    cache = warp_amd.ExpertCache(rec, n_slots * rec, policy=0, depth=2)
+    cache.set_source([host.data_ptr() + i * rec for i in range(n_layers * Ls[0].E)], n_layers, Ls[0].E)
+    ms = [gpu_layer(L, records=False) for L in Ls]
+    for m, L in zip(ms, Ls):
+        assert m.bind_table([], [], codebook_id=L.cb_base) == 0
+    ols = [orc.moe(L, 1) for L in Ls]
+    s = stream()
+    ops = []
+    look_d = torch.empty((64,), dtype=torch.int32, device=dev)
+    for t in range(T):
+        for l, (L, m) in enumerate(zip(Ls, ms)):
+            x = bf16_inputs(L, 1, 2000 * t + l)
+            xd = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+            y = torch.full((1, L.H), float("nan"), device=dev)
+            ids = torch.empty((1, 8), dtype=torch.int32, device=dev)
+            w = torch.empty((1, 8), device=dev)
+            nxt = ms[l + 1] if l + 1 < n_layers else None
+            m.forward_cached(cache, l, xd.data_ptr(), y.data_ptr(), nxt=nxt, lookahead=look,
+                             ids_ptr=ids.data_ptr(), w_ptr=w.data_ptr(), bf16=True, stream=s)
+            assert m.status(s) == 0, (t, l)
+            idh = ids.cpu().numpy()[0].tolist()
+            ops += [es.HINT, l, 8] + idh
+            for e in idh:
+                ops += [es.HOLD, l, e]
+            ops += [es.RELEASE]
+            if nxt is not None and look:
+                nxt.predict(xd.data_ptr(), look, look_d.data_ptr(), bf16=True, stream=s)
+                g = look_d.cpu().numpy()[:look].tolist()
+                ops += [es.PREFETCH, l + 1, len(g)] + g
+            rc, ref = ols[l].apply(x, ids.cpu().numpy(), w.cpu().numpy(), chunk=0)
+            assert rc == 0
+            e_ = rel_err(y.cpu().numpy(), ref)
+            assert e_ <= LAYER_RTOL, (t, l, e_)
+    cache.sync()
+    got = cache.stats()
+    dry = warp_amd.ExpertCache(rec, n_slots * rec, policy=0, depth=2, dry=True)
+    _, dst = es.run_product(dry, ops)
+    assert [got[k] for k in ("hits", "misses", "evictions", "prefetched", "spec_issued", "reads")] == dst
+    say(f"  hits {got['hits']} misses {got['misses']} spec {got['spec_issued']}")
+    for m in ms:
+        m.close()
+    cache.close()

@@ -34,7 +34,7 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_moe_profile", "waste_hip_moe_profile_read", "waste_hip_record_bytes",
            "waste_hip_synth_codebooks", "waste_hip_synth_records",
            "waste_hip_moe_route", "waste_hip_moe_experts", "waste_hip_moe_bind_table",
-           "waste_hip_moe_predict",
+           "waste_hip_moe_predict", "waste_hip_moe_forward_cached",
            "waste_hip_ecache_create", "waste_hip_ecache_destroy", "waste_hip_ecache_set_source",
            "waste_hip_ecache_hint", "waste_hip_ecache_prefetch", "waste_hip_ecache_get",
            "waste_hip_ecache_hold", "waste_hip_ecache_release", "waste_hip_ecache_admit",
@@ -115,6 +115,7 @@ def lib():
         "waste_hip_moe_experts": (i, [vp, vp, i, i, vp, vp]),
         "waste_hip_moe_bind_table": (i, [vp, ip, C.POINTER(vp), i, i, vp]),
         "waste_hip_moe_predict": (i, [vp, vp, i, i, vp, vp]),
+        "waste_hip_moe_forward_cached": (i, [vp, vp, i, vp, i, vp, i, vp, vp, vp, vp]),
         "waste_hip_ecache_create": (i, [C.c_size_t, C.c_size_t, i, i, i, C.POINTER(vp)]),
         "waste_hip_ecache_destroy": (None, [vp]),
         "waste_hip_ecache_set_source": (i, [vp, C.POINTER(vp), i, i]),
@@ -241,6 +242,14 @@ class MoeLayer:
 
     def predict(self, x_ptr, n, ids_ptr, bf16=False, stream=None):
         check(self.L.waste_hip_moe_predict(self.h, x_ptr, int(bf16), n, ids_ptr, stream), "predict")
+
+    def forward_cached(self, cache, layer, x_ptr, y_ptr, nxt=None, lookahead=0, ids_ptr=None,
+                       w_ptr=None, bf16=False, stream=None):
+        """One decode token through an ExpertCache (layer: the cache key's
+        layer; nxt: the next MoeLayer, whose router makes the lookahead)."""
+        check(self.L.waste_hip_moe_forward_cached(self.h, cache.h, layer, nxt.h if nxt else None,
+                                                  lookahead, x_ptr, int(bf16), y_ptr, ids_ptr, w_ptr,
+                                                  stream), "forward_cached")
 
 
 def _ids(ids):

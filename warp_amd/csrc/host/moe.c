@@ -56,6 +56,8 @@ struct waste_hip_moe {
     int *err;                    /* [0] status bits; [4] the lookahead's    */
     float *plogits, *pw;         /* the lookahead's logits and weights      */
     int routed_T;                /* T of the last route(), 0 none          */
+    int32_t *h_sel;              /* pinned: selection [0,64), lookahead [64,128) */
+    int32_t *d_look;             /* the lookahead's ids                    */
     int prof_on;
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
     waste_hip_moe_prof prof;
@@ -116,10 +118,11 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->logits, m->w, m->pair_w, m->part_gu, m->h, m->part_d, m->sh_a,
                      m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
                      m->tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
-                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw };
+                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0])
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
+    if (m->h_sel) hipHostFree(m->h_sel);
     free(m->h_recs);
     free(m);
 }
@@ -202,6 +205,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->err, 64);
     rc |= dmalloc((void **)&m->plogits, (size_t)m->E * 4);
     rc |= dmalloc((void **)&m->pw, 64 * 4);
+    rc |= dmalloc((void **)&m->d_look, 64 * 4);
     if (m->T > m->Td) {
         rc |= dmalloc((void **)&m->pair_pos, (size_t)P * 4);
         rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
@@ -643,6 +647,57 @@ int waste_hip_moe_profile_read(waste_hip_moe *m, waste_hip_moe_prof *out)
     if (!m || !out) return WASTE_HIP_EINVAL;
     *out = m->prof;
     return 0;
+}
+
+/* moe_layer's cache path (src/model.c:5639-5700 and 5926-5930) for one
+ * token: route, the lookahead on the next layer's router, the selection
+ * to the host, hint and hold, bind, experts, release, lookahead reads. */
+int waste_hip_moe_forward_cached(waste_hip_moe *m, waste_hip_ecache *c, int layer, waste_hip_moe *next,
+                                 int lookahead, const void *x, int x_bf16, float *y, int32_t *ids,
+                                 float *w, void *stream)
+{
+    if (!m || !c || !x || !y || layer < 0 || layer > 32767 || lookahead < 0 || lookahead > 64)
+        return WASTE_HIP_EINVAL;
+    if (m->cb < 0) return WASTE_HIP_EINVAL;
+    hipStream_t s = (hipStream_t)stream;
+    const int K = m->K;
+    if (!m->h_sel && hipHostMalloc((void **)&m->h_sel, 128 * sizeof(int32_t), hipHostMallocDefault) != hipSuccess) {
+        m->h_sel = NULL;
+        return WASTE_HIP_ENOMEM;
+    }
+    int32_t *d_ids = ids ? ids : m->ids;
+    float *d_w = w ? w : m->w;
+    int rc = waste_hip_moe_route(m, x, x_bf16, 1, d_ids, d_w, NULL, stream);
+    if (rc) return rc;
+    int nl = next && lookahead > 0 ? (lookahead < next->E ? lookahead : next->E) : 0;
+    if (nl && (rc = waste_hip_moe_predict(next, x, x_bf16, nl, m->d_look, stream))) return rc;
+    CK(hipMemcpyAsync(m->h_sel, d_ids, (size_t)K * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    if (nl) CK(hipMemcpyAsync(m->h_sel + 64, m->d_look, (size_t)nl * sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    CK(hipStreamSynchronize(s));
+    int routed = 1;
+    for (int j = 0; j < K; j++) routed &= m->h_sel[j] >= 0 && m->h_sel[j] < m->E;
+    if (routed) {
+        /* a failed route leaves -1 ids: the experts then report it */
+        const void *recs[64];
+        if ((rc = waste_hip_ecache_hint(c, layer, m->h_sel, K))) return rc;
+        for (int j = 0; j < K; j++) {
+            recs[j] = waste_hip_ecache_hold(c, layer, m->h_sel[j], stream);
+            if (!recs[j]) {
+                waste_hip_ecache_release(c, stream);
+                return WASTE_HIP_EDEVICE;
+            }
+        }
+        if ((rc = waste_hip_moe_bind_table(m, m->h_sel, recs, K, -1, stream))) return rc;
+    }
+    rc = waste_hip_moe_experts(m, x, x_bf16, 1, y, stream);
+    const int rr = waste_hip_ecache_release(c, stream);
+    if (rc) return rc;
+    if (rr) return rr;
+    /* the guess goes out after this layer's reads (src/model.c:5921-5930) */
+    int guess[64], ng = 0;
+    for (int j = 0; j < nl; j++)
+        if (m->h_sel[64 + j] >= 0) guess[ng++] = m->h_sel[64 + j];
+    return ng ? waste_hip_ecache_prefetch(c, layer + 1, guess, ng) : 0;
 }
 
 int waste_hip_moe_status(waste_hip_moe *m, void *stream)
