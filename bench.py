@@ -195,6 +195,141 @@ def bench_prefill(torch, warp_amd, synth, cfg, slab, books, rb, trunk, T, reps, 
     }
 
 
+def stack_inputs(torch, T, n_layers, H, rho, gamma, seed):
+    """A synthetic residual stream, bf16 [T][n_layers][H] on the device.
+
+    Layer L's input is gamma * (layer L-1's input) + sqrt(1-gamma^2) * z_L,
+    and each z_L is an AR(1) over tokens with coefficient rho; every input
+    is N(0,1) per coordinate.  rho sets how much of a layer's selection the
+    next token reuses, gamma how well the next layer's router applied to
+    this layer's input predicts the next layer's selection (the lookahead).
+    """
+    g = torch.Generator(device="cuda:0").manual_seed(seed)
+    c = (1.0 - gamma * gamma) ** 0.5
+    A = torch.zeros((n_layers, n_layers), device="cuda:0")
+    for L in range(n_layers):
+        for j in range(L + 1):
+            A[L, j] = gamma ** (L - j) * (1.0 if j == 0 else c)
+    X = torch.empty((T, n_layers, H), dtype=torch.bfloat16, device="cuda:0")
+    z = torch.randn((n_layers, H), generator=g, device="cuda:0")
+    r = (1.0 - rho * rho) ** 0.5
+    for t in range(T):
+        if t:
+            z = rho * z + r * torch.randn((n_layers, H), generator=g, device="cuda:0")
+        X[t] = (A @ z).to(torch.bfloat16)
+    return X
+
+
+def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_gb=64.0,
+                lookahead=6, depth=2, seed=0, rho=0.80, gamma=0.96, zipf_s=1.1, beta=0.125):
+    """58 DeepSeek-V3-shaped MoE layers decoding `tokens` tokens at batch 1
+    through the HBM expert cache (64 GB of slots), the expert records in
+    pinned host memory, misses filled by hipMemcpyAsync on the cache's
+    stream, the lookahead's guesses (the next layer's router on this
+    layer's input, 6 ids) read after each layer's experts.
+
+    Popularity: each layer's e_score_correction_bias is beta * log of a
+    Zipf(1.1) rank over a seeded permutation of the experts; reuse and
+    lookahead precision come from the residual stream (stack_inputs).
+
+    The host bank: one set of 256 records (4.2 GB pinned); layer L's expert
+    e is a byte copy of record e, so every layer object carries layer id 0
+    (the records' header) while the cache keys are (L, e): each miss still
+    moves its own 16.5 MB over PCIe into its own slot."""
+    H, E, I, K = cfg["hidden"], cfg["n_experts"], cfg["moe_inter"], cfg["top_k"]
+    t0 = time.time()
+    rb = synth.record_bytes(H, I)
+    dev = torch.empty(E * rb, dtype=torch.uint8, device="cuda:0")
+    synth.records(seed, 0, H, I, books, 0, E, dev.data_ptr())
+    host = torch.empty(E * rb, dtype=torch.uint8, pin_memory=True)
+    host.copy_(dev)
+    del dev
+    torch.cuda.synchronize()
+    _, _, sh = synth.trunk(cfg, seed + 1)
+    rng = np.random.default_rng(seed + 7)
+    layers = []
+    for L in range(n_layers):
+        W = (rng.standard_normal((E, H), np.float32) * 0.02).astype(np.float32)
+        b = np.zeros(E, np.float64)
+        b[rng.permutation(E)] = -zipf_s * np.log(np.arange(1, E + 1))
+        b = (beta * (b - b.mean())).astype(np.float32)
+        m = warp_amd.MoeLayer(hidden=H, n_experts=E, top_k=K, moe_inter=I,
+                              n_shared=cfg["n_shared"], score_func=cfg["score_func"],
+                              renorm=cfg["renorm"], routed_scale=cfg["routed_scale"],
+                              n_group=cfg["n_group"], topk_group=cfg["topk_group"], layer=0,
+                              max_tokens=1)
+        m.set_codebooks(books)
+        m.set_router(synth.Tensor.make(cfg["router_fmt"], W), b)
+        if sh:
+            m.set_shared(*sh)
+        warp_amd.check(m.bind_table([], [], codebook_id=0), "bind_table")
+        layers.append(m)
+    budget = int(budget_gb * 1e9)
+    cache = warp_amd.ExpertCache(rb, budget, policy=0, depth=depth)
+    cache.set_source([host.data_ptr() + e * rb for _ in range(n_layers) for e in range(E)], n_layers, E)
+    X = stack_inputs(torch, tokens, n_layers, H, rho, gamma, seed + 11)
+    y = torch.empty((1, H), dtype=torch.float32, device="cuda:0")
+    ids = torch.empty((tokens, n_layers, K), dtype=torch.int32, device="cuda:0")
+    torch.cuda.synchronize()
+    log(f"[bench] stack: {n_layers} layers, {cache.n_slots} slots of {rb} B, bank in pinned host "
+        f"memory, set up in {time.time() - t0:.1f}s")
+    s = torch.cuda.current_stream().cuda_stream
+    esz = X.element_size()
+    tok_s, marks = [], []
+    t_start = time.perf_counter()
+    for t in range(tokens):
+        for L in range(n_layers):
+            nxt = layers[L + 1] if L + 1 < n_layers else None
+            layers[L].forward_cached(cache, L, X.data_ptr() + (t * n_layers + L) * H * esz, y.data_ptr(),
+                                     nxt=nxt, lookahead=lookahead if nxt else 0,
+                                     ids_ptr=ids[t, L].data_ptr(), bf16=True, stream=s)
+        marks.append(time.perf_counter())
+        if t % 50 == 49:
+            st = cache.stats()
+            log(f"[bench] stack token {t + 1}: hit rate {st['hits'] / max(1, st['hits'] + st['misses']):.3f}")
+    torch.cuda.synchronize()
+    cache.sync()
+    wall = time.perf_counter() - t_start
+    for m in layers:
+        st = m.status(s)
+        if st != 0:
+            raise RuntimeError(f"stack: device error {st}")
+    st = cache.stats()
+    hit = st["hits"] / max(1, st["hits"] + st["misses"])
+    half = tokens // 2
+    steady = (tokens - half) / (marks[-1] - marks[half - 1]) if half else None
+    # the routing the layers actually made
+    ih = ids.cpu().numpy()
+    reuse = float(np.mean([len(set(ih[t, L]) & set(ih[t - 1, L])) / K
+                           for t in range(1, tokens) for L in range(n_layers)]))
+    cnt = np.zeros((n_layers, E))
+    for L in range(n_layers):
+        np.add.at(cnt[L], ih[:, L].reshape(-1), 1)
+    f = np.sort(cnt, axis=1)[:, ::-1].mean(0)
+    r = np.arange(1, 65)
+    slope = float(np.polyfit(np.log(r), np.log(f[:64] + 1e-9), 1)[0])
+    out = {
+        "workload": f"{n_layers}-layer dsv3 MoE stack, batch-1 decode of {tokens} tokens through the "
+                    f"HBM expert cache", "layers": n_layers, "tokens": tokens,
+        "budget_gb": budget_gb, "slots": cache.n_slots, "records": n_layers * E, "rec_bytes": rb,
+        "policy": "lfru", "readahead_depth": depth, "lookahead": lookahead,
+        "hit_rate": round(hit, 4), "hits": st["hits"], "misses": st["misses"],
+        "evictions": st["evictions"], "hint_reads": st["prefetched"],
+        "lookahead_reads": st["spec_issued"], "gb_read": round(st["bytes_read"] / 1e9, 2),
+        "tok_s": round(tokens / wall, 3), "ms_per_token": round(wall * 1e3 / tokens, 2),
+        "tok_s_second_half": round(steady, 3) if steady else None,
+        "host_to_device_gbps": round(st["bytes_read"] / wall / 1e9, 2),
+        "routing": {"token_to_token_reuse": round(reuse, 3), "zipf_slope_top64": round(slope, 3),
+                    "distinct_experts_per_layer": round(float((cnt > 0).sum(1).mean()), 1),
+                    "rho": rho, "gamma": gamma, "bias_scale": beta},
+    }
+    for m in layers:
+        m.close()
+    cache.close()
+    del host, X
+    return out
+
+
 def measured_traffic(dom, config, batch):
     """HBM bytes per launch of the dominant kernel, as measured by the two
     rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE, each scaled by a copy of
@@ -223,6 +358,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="tokens of the prefill chunk measured beside decode (0: skip)")
+    ap.add_argument("--stack-tokens", type=int, default=200,
+                    help="tokens the 58-layer stack decodes through the HBM expert cache (0: skip)")
+    ap.add_argument("--stack-budget-gb", type=float, default=64.0)
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device (a plain copy kernel of known "
                          "size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -333,6 +471,12 @@ def main():
                                                 a.prefill_tokens, 5, hot=True)["routed_grouped_gemm"]
         log(f"[bench] prefill {prefill['tokens_per_s']} tok/s")
 
+    stack = None
+    if a.stack_tokens and B == 1 and a.config == "dsv3":
+        stack = bench_stack(torch, warp_amd, synth, cfg, books, a.stack_tokens,
+                            budget_gb=a.stack_budget_gb)
+        log(f"[bench] stack {stack['tok_s']} tok/s, hit rate {stack['hit_rate']}")
+
     cpu = None
     if not a.no_cpu and B == 1:
         nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
@@ -373,6 +517,7 @@ def main():
                      "launch_us": round(dom_ms * 1e3, 2), "algorithmic_bytes": int(dom_bytes)},
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "expert_cache": stack,
     }
     print(json.dumps(out))
     for m in layers:
