@@ -14,7 +14,10 @@ import os
 
 import numpy as np
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libwaste_hip.so")
+# WARP_AMD_LIB names another build of the same library (an A/B comparison);
+# the default is the in-tree build.
+LIB_PATH = os.environ.get("WARP_AMD_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)),
+                                                          "libwaste_hip.so")
 
 WQ_F32, WQ_Q8G, WQ_Q4G, WQ_VQ3R = 0, 2, 3, 4
 SCORE_SIGMOID, SCORE_SOFTMAX, SCORE_SQRTSOFTPLUS = 0, 1, 2

@@ -29,10 +29,16 @@
 #include "common.h"
 #include "launch.h"
 
-#define VC 8                        // positions per workgroup chunk
+#ifndef WH_VC
+#define WH_VC 8
+#endif
+#define VC WH_VC                    // positions per workgroup chunk
+#ifndef WH_LANES
+#define WH_LANES 1                  // the positions-across-lanes kernel when nv % 32 == 0
+#endif
 #define LUT_PER_V (3 * 256)
 
-extern "C" int whip_vq_chunks(int nv) { return (nv + VC - 1) / VC; }
+extern "C" int whip_vq_chunks(int nv) { return (WH_LANES && nv % 32 == 0) ? nv / 32 : (nv + VC - 1) / VC; }
 
 typedef const uint3 WH_GLOBAL g_uint3;
 
@@ -181,6 +187,294 @@ vq_apply_body(const uint8_t *const *__restrict__ recs, const int32_t *__restrict
 VQ_KERNEL(k_vq_gate_up)
 VQ_KERNEL(k_vq_down)
 
+// ---- positions across lanes ------------------------------------------------
+// The same products with the lanes laid across positions instead of rows.
+// In the kernel above every lane of a wavefront reads the same position's
+// table at its own random code, so the 64 reads of one LDS instruction land
+// on random banks and the instruction replays about five times.  Here lane
+// (v, h) owns position v of a 32-position chunk and row half h of a 64-row
+// block: it reads only position v's tables, and the tables are laid out
+// [code][64 slots] with stage 0 in slots 0-31, stage 1 in slots 32-63
+// (table A) and stage 2 twice (table B), so a lookup's bank is its slot.
+// Row half 1 swaps each row's stage-0 and stage-1 index bytes once per tile;
+// in every lookup the two halves then read different slot halves and all
+// 64 lanes hit 64 different banks.  A lookup's address is one byte permute:
+// the code into byte 1 of a per-lane base that holds the slot (byte 0) and
+// the table (byte 2).
+//
+// Each lane ends a tile with its position's contribution to its 32 rows; a
+// transpose-reduce across the 32 lanes of its half (a lane swap at offset
+// 16, then offsets 8, mirror-4, 1, 2, each halving the registers kept)
+// leaves every lane one row's sum over the chunk.  A workgroup owns a run
+// of tiles (64 rows x 32 positions) in table order and rebuilds the tables
+// when the run crosses from one (kind, chunk[, pair]) to the next.
+#define PW 32
+#define LT 1024
+#define LW (LT / 64)
+#define LUT_B 16384                 // floats: table B after table A
+
+typedef const uint4 WH_GLOBAL g_uint4;
+typedef float acc16 __attribute__((ext_vector_type(16)));
+
+struct tile_buf { uint4 q[6]; };
+
+__device__ __forceinline__ void load_tile(tile_buf &b, g_u8 *base, uint32_t loff)
+{
+#pragma unroll
+    for (int i = 0; i < 6; i++) b.q[i] = *(g_uint4 *)(base + loff + 16 * i);
+}
+
+// one tile: 32 rows of this lane's half at its position, then the reduce.
+// The buffer is consumed in place (row half 1's byte swap overwrites it).
+__device__ __forceinline__ float lookup3(const char *L, const uint32_t *d, int j, uint32_t bA0,
+                                         uint32_t bA1, uint32_t bB)
+{
+    float t[3];
+#pragma unroll
+    for (int st = 0; st < 3; st++) {
+        const int byte = 3 * j + st;
+        const uint32_t base = st == 0 ? bA0 : st == 1 ? bA1 : bB;
+        const uint32_t a = __builtin_amdgcn_perm(d[byte >> 2], base, 0x03020000u | ((4u + (byte & 3)) << 8));
+        t[st] = *(const float *)(L + a);
+    }
+    return (t[0] + t[1]) + t[2];
+}
+
+__device__ __forceinline__ float tile_sum(tile_buf &b, const float *smem, uint32_t bA0, uint32_t bA1,
+                                          uint32_t bB, uint32_t s0, uint32_t s1, uint32_t s2, int lane)
+{
+    uint32_t d[24];
+#pragma unroll
+    for (int i = 0; i < 6; i++) { d[4 * i] = b.q[i].x; d[4 * i + 1] = b.q[i].y; d[4 * i + 2] = b.q[i].z; d[4 * i + 3] = b.q[i].w; }
+    // half 1: stage-0 and stage-1 bytes of every row swap places
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+        const uint32_t x0 = d[3 * g], x1 = d[3 * g + 1], x2 = d[3 * g + 2];
+        d[3 * g] = __builtin_amdgcn_perm(x1, x0, s0);
+        d[3 * g + 1] = __builtin_amdgcn_perm(x1, x0, s1);
+        d[3 * g + 2] = __builtin_amdgcn_perm(x2, x2, s2);
+    }
+    const char *L = (const char *)smem;
+    // rows j and 16 + j, folded at once by the first reduce step (a lane
+    // swap at offset 16): e[j] is row j on lanes 0-15, row 16 + j on 16-31
+    float e[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float lo = lookup3(L, d, j, bA0, bA1, bB), hi = lookup3(L, d, 16 + j, bA0, bA1, bB);
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+        e[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b3 = (lane >> 3) & 1, b2 = (lane >> 2) & 1, b0 = lane & 1, b1 = (lane >> 1) & 1;
+    float f[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float keep = b3 ? e[8 + j] : e[j], send = b3 ? e[j] : e[8 + j];
+        f[j] = keep + __uint_as_float(dpp32<0x128>(__float_as_uint(send)));
+    }
+    float g4[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float keep = b2 ? f[4 + j] : f[j], send = b2 ? f[j] : f[4 + j];
+        g4[j] = keep + __uint_as_float(dpp32<0x141>(__float_as_uint(send)));
+    }
+    float g2[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const float keep = b0 ? g4[2 + j] : g4[j], send = b0 ? g4[j] : g4[2 + j];
+        g2[j] = keep + __uint_as_float(dpp32<0xB1>(__float_as_uint(send)));
+    }
+    const float keep = b1 ? g2[1] : g2[0], send = b1 ? g2[0] : g2[1];
+    return keep + __uint_as_float(dpp32<0x4E>(__float_as_uint(send)));
+}
+
+// A workgroup's tiles in table order: t -> (pair, kind, chunk, row block).
+// span: classes (kind, chunk), each over every pair's row blocks; else
+// classes (pair, kind, chunk), each over one pair's row blocks.
+struct tile_map {
+    int span, nch, kinds, nb, tpc;
+    __device__ __forceinline__ void at(int t, int &p, int &kind, int &chunk, int &rb) const
+    {
+        const int cls = t / tpc, within = t - cls * tpc;
+        if (span) { kind = cls / nch; chunk = cls - kind * nch; p = within / nb; rb = within - p * nb; }
+        else { p = cls / (kinds * nch); const int r = cls - p * kinds * nch; kind = r / nch; chunk = r - kind * nch; rb = within; }
+    }
+};
+
+// Every global load below is unconditional (clamped addresses, selects
+// instead of branches): the hardware counts loads in issue order, and a
+// load on only one side of a branch leaves the compiler unsure how many are
+// in flight, so it would wait for all of them, the prefetched tiles too.
+__global__ void __launch_bounds__(LT)
+k_vq_lanes(whip_vq_args a, int nch, int span, int tiles, int per_wg, int shares)
+{
+    __shared__ float smem[2 * 256 * 64];             // table A | table B
+    __shared__ float sbook[3 * 8 * 256];             // a kind's books, [stage][dim][code]
+    __shared__ const uint8_t *s_rec[SPAN_MAX];       // records of pairs p_lo ..
+    __shared__ int s_xr[SPAN_MAX];                   // and their source rows
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int v = lane & 31, h = lane >> 5;
+    tile_map tm;
+    tm.span = span; tm.nch = nch; tm.kinds = a.kinds; tm.nb = a.M >> 6;
+    tm.tpc = span ? a.P * tm.nb : tm.nb;
+    // shares > 0: workgroup = (class, share), a share never leaves its class
+    int t0, t1;
+    if (shares > 0) {
+        const int cls = blockIdx.x / shares, j = blockIdx.x - cls * shares;
+        t0 = cls * tm.tpc + j * per_wg;
+        t1 = min(t0 + per_wg, (cls + 1) * tm.tpc);
+    } else {
+        t0 = blockIdx.x * per_wg;
+        t1 = min(tiles, t0 + per_wg);
+    }
+    if (t0 >= t1) return;                            // whole workgroup
+    const size_t rstride = (size_t)a.nv * 192;
+    const uint32_t bA0 = (h ? 128u : 0u) + 4u * v, bA1 = (h ? 0u : 128u) + 4u * v;
+    const uint32_t bB = 65536u + 128u * h + 4u * v;
+    const uint32_t s0 = h ? 0x04020001u : 0x03020100u, s1 = h ? 0x06070503u : 0x07060504u;
+    const uint32_t s2 = h ? 0x03010200u : 0x03020100u;
+    const int rho = 16 * ((v >> 4) & 1) + 8 * ((v >> 3) & 1) + 4 * ((v >> 2) & 1) + 2 * (v & 1) + ((v >> 1) & 1);
+    // every address is a wave-uniform base plus one of two per-lane offsets
+    const uint32_t loff = v * 192 + h * 96;          // index bytes of a tile
+    const uint32_t lrow = 32 * h + rho;              // output row in a block
+    g_u8 *dummy = as_global((const uint8_t *)a.booksT);
+    float *sink = a.part + (size_t)a.P * a.kinds * nch * a.M;
+    int p_lo = 0, p_hi = a.P - 1, u0, u1, u2, p_first;
+    if (!span) {                                     // p_hi - p_lo < SPAN_MAX (host)
+        tm.at(t0, p_lo, u0, u1, u2);
+        tm.at(t1 - 1, p_hi, u0, u1, u2);
+    }
+    tm.at(t0, p_first, u0, u1, u2);
+
+    auto uni = [](const void *q) -> const uint8_t * {
+        const uint64_t u = (uint64_t)q;
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+        return (const uint8_t *)(((uint64_t)hi << 32) | lo);
+    };
+    // tile t -> uniform bases of its index bytes (or the dummy) and output block
+    auto where = [&](int t, g_u8 *&src, float *&out, bool &live) {
+        if (t >= t1) { src = dummy; out = sink; live = true; return; }
+        int p, kind, chunk, rb;
+        tm.at(t, p, kind, chunk, rb);
+        const uint8_t *rec = uni(s_rec[p - p_lo]);
+        live = rec != nullptr;
+        src = rec ? as_global(rec) + a.idx_off[kind] + (size_t)rb * rstride + (size_t)chunk * PW * 192 : dummy;
+        out = a.part + (((size_t)p * a.kinds + kind) * nch + chunk) * (size_t)a.M + rb * 64;
+    };
+
+    // the build's loads for the class of tile t: the kind's books and x
+    float bv[3 * 8 * 256 / LT];
+    uint4 xq0, xq1;
+    auto build_loads = [&](int t, int xr) {
+        int p, kind, chunk, rb;
+        tm.at(t, p, kind, chunk, rb);
+        const float *bk = a.booksT + (size_t)(a.cb + kind * 3) * 8 * 256;
+#pragma unroll
+        for (int i = 0; i < 3 * 8 * 256 / LT; i++) bv[i] = bk[tid + i * LT];
+        const size_t e0 = (size_t)xr * a.src_ld + (size_t)(chunk * PW + v) * 8;
+        const uint8_t *xb = (const uint8_t *)a.src + e0 * (a.src_bf16 ? 2 : 4);
+        xq0 = *(const uint4 *)xb;
+        xq1 = *(const uint4 *)(xb + (a.src_bf16 ? 0 : 16));
+    };
+    // the tables: books to LDS, then 24 products of 32 codes x 32 positions
+    // on the matrix cores (books[code][dim] x x[dim][position])
+    auto build = [&]() {
+#pragma unroll
+        for (int i = 0; i < 3 * 8 * 256 / LT; i++) sbook[tid + i * LT] = bv[i];
+        float xv[8];
+        const uint32_t w8[8] = {xq0.x, xq0.y, xq0.z, xq0.w, xq1.x, xq1.y, xq1.z, xq1.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float lo16 = wh_bf16(w8[i] & 0xffff), hi16 = wh_bf16(w8[i] >> 16);
+            xv[2 * i] = a.src_bf16 ? lo16 : __uint_as_float(w8[2 * i]);
+            xv[2 * i + 1] = a.src_bf16 ? hi16 : __uint_as_float(w8[2 * i + 1]);
+        }
+        float xb[4];                                 // B operand: x[position v][dim 2i + h]
+#pragma unroll
+        for (int i = 0; i < 4; i++) xb[i] = h ? xv[2 * i + 1] : xv[2 * i];
+        __syncthreads();
+        for (int tile = wv; tile < 24; tile += LW) { // uniform per wavefront
+            const int st = tile >> 3, c0 = (tile & 7) * 32;
+            acc16 acc;
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float av = sbook[(st * 8 + 2 * i + h) * 256 + c0 + v];
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, xb[i], acc, 0, 0, 0);
+            }
+            // acc[r]: code c0 + 8(r/4) + 4h + r%4, position v
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int c = c0 + (r >> 2) * 8 + 4 * h + (r & 3);
+                if (st < 2) smem[c * 64 + 32 * st + v] = acc[r];
+                else { smem[LUT_B + c * 64 + v] = acc[r]; smem[LUT_B + c * 64 + 32 + v] = acc[r]; }
+            }
+        }
+        __syncthreads();
+    };
+
+    // prologue.  Round 1: each thread's pair (its expert and source row)
+    // and the first class's source row.  Round 2: the records, the first
+    // build's books and x.  Then the records to LDS, the first tile's
+    // index bytes, and the first build, whose loads were issued before the
+    // tile's and so are waited for without it.
+    {
+        const int q = p_lo + min(tid, p_hi - p_lo);
+        const int32_t *psrc = a.pair_src ? a.pair_src : a.pair_exp;
+        const int e = a.pair_exp[q];
+        const int xq = psrc[q], xf = psrc[p_first];
+        const int myxr = a.pair_src ? xq : q, xr0 = a.pair_src ? xf : p_first;
+        const uint8_t *myrec = a.recs[e];
+        build_loads(t0, xr0);
+        if (tid <= p_hi - p_lo) { s_rec[tid] = myrec; s_xr[tid] = myxr; }
+    }
+    __syncthreads();
+    int t = t0 + wv;
+    tile_buf A, B;
+    g_u8 *src;
+    float *outA, *outB;
+    bool liveA, liveB, unbound = false;
+    bool inA = true;                                 // the next tile is in A
+    where(t, src, outA, liveA);
+    load_tile(A, src, loff);
+    build();
+
+    for (int lo = t0; lo < t1;) {
+        int p, kind, chunk, rb;
+        tm.at(lo, p, kind, chunk, rb);
+        const int hi = min(t1, (lo / tm.tpc + 1) * tm.tpc);
+        // this wavefront's tiles of the class, the next one always in flight
+        while (t < hi) {
+            float r;
+            if (inA) {
+                where(t + LW, src, outB, liveB);
+                load_tile(B, src, loff);
+                r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
+                outA[lrow] = liveA ? r : 0.0f;
+                unbound |= !liveA;
+            } else {
+                where(t + LW, src, outA, liveA);
+                load_tile(A, src, loff);
+                r = tile_sum(B, smem, bA0, bA1, bB, s0, s1, s2, lane);
+                outB[lrow] = liveB ? r : 0.0f;
+                unbound |= !liveB;
+            }
+            inA = !inA;
+            t += LW;
+        }
+        lo = hi;
+        if (lo < t1) {                               // uniform: the next class
+            int pn, k_, c_, r_;
+            tm.at(lo, pn, k_, c_, r_);
+            build_loads(lo, s_xr[pn - p_lo]);
+            __syncthreads();                         // the old tables are done with
+            build();
+        }
+    }
+    if (unbound) atomicOr(a.err, 1);
+}
+
 extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
 {
     // whole row blocks and chunks; 4-byte aligned index streams; a spanning
@@ -191,6 +485,42 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
         a->P < 1 || a->rsplit < 1 || a->rsplit > rows || (span > 1 && (span != a->P || span > SPAN_MAX)))
         return (int)hipErrorInvalidValue;
     const int nch = whip_vq_chunks(a->nv);
+    if (WH_LANES && a->nv % PW == 0) {
+        // 16-byte aligned tiles (the kernel's 128-bit loads)
+        if (a->idx_off[0] % 16 || a->idx_off[1] % 16) return (int)hipErrorInvalidValue;
+        static int n_cu = 0;
+        if (!n_cu) {
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu < 1)
+                n_cu = 256;
+        }
+        const int nb = a->M / 64, sp = span > 1;
+        const long tpc = sp ? (long)a->P * nb : nb;
+        const long classes = (long)a->kinds * nch * (sp ? 1 : a->P);
+        const long tiles = classes * tpc;
+        if (tiles > (1L << 30)) return (int)hipErrorInvalidValue;
+        long G, per_wg, shares = 0;
+        if (classes <= n_cu) {
+            // whole classes: `shares` workgroups per class, one build each
+            const long k = n_cu / classes;
+            per_wg = (tpc + k - 1) / k;
+            shares = (tpc + per_wg - 1) / per_wg;
+            G = classes * shares;
+        } else {
+            G = n_cu;
+            per_wg = (tiles + G - 1) / G;
+        }
+        // a workgroup's records fit its table (at most SPAN_MAX pairs)
+        const long tiles_per_pair = sp ? tiles : (long)a->kinds * nch * nb;
+        if (!sp && shares == 0 && per_wg > (long)(SPAN_MAX - 1) * tiles_per_pair) {
+            per_wg = (long)(SPAN_MAX - 1) * tiles_per_pair;
+            G = (tiles + per_wg - 1) / per_wg;
+        }
+        hipLaunchKernelGGL(k_vq_lanes, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles, (int)per_wg,
+                           (int)shares);
+        return (int)hipGetLastError();
+    }
     dim3 grid(nch, a->kinds * a->rsplit, span > 1 ? 1 : a->P);
     hipLaunchKernelGGL(a->kinds == 2 ? k_vq_gate_up : k_vq_down, grid, dim3(VQ_THREADS), 0, s, a->recs,
                        a->pair_exp, a->pair_src, a->src, a->src_ld, a->src_bf16, a->booksT, a->cb,

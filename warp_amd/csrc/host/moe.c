@@ -477,16 +477,18 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
 {
     const int E = m->E, K = m->K, H = m->H;
     MARK(0);
-    /* router logits and the shared expert's silu(gate.x)*(up.x): one launch */
-    whip_gemv_job jobs[2];
-    int nj = 0;
-    jobs[nj].A = m->router; jobs[nj].B = NULL; jobs[nj].x = x; jobs[nj].x_ld = H;
-    jobs[nj].x_bf16 = x_bf16; jobs[nj].y = lg; jobs[nj].y_ld = E; nj++;
+    /* router logits and the shared expert's silu(gate.x)*(up.x): one launch
+     * (the shared expert on a second stream measured slower: its kernels
+     * then compete with the routed path for the same CUs and bandwidth) */
+    whip_gemv_job r[2];
+    int nr = 0;
+    r[nr].A = m->router; r[nr].B = NULL; r[nr].x = x; r[nr].x_ld = H; r[nr].x_bf16 = x_bf16;
+    r[nr].y = lg; r[nr].y_ld = E; nr++;
     if (m->has_shared) {
-        jobs[nj].A = m->sh[0]; jobs[nj].B = &m->sh[1]; jobs[nj].x = x; jobs[nj].x_ld = H;
-        jobs[nj].x_bf16 = x_bf16; jobs[nj].y = m->h_sh; jobs[nj].y_ld = m->SI; nj++;
+        r[nr].A = m->sh[0]; r[nr].B = &m->sh[1]; r[nr].x = x; r[nr].x_ld = H; r[nr].x_bf16 = x_bf16;
+        r[nr].y = m->h_sh; r[nr].y_ld = m->SI; nr++;
     }
-    CK((hipError_t)whip_gemv_multi(jobs, nj, T, s));
+    CK((hipError_t)whip_gemv_multi(r, nr, T, s));
     MARK(1);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
