@@ -18,6 +18,7 @@
 // fp32 or bf16 (converted as they are read).
 #include "common.h"
 #include "launch.h"
+#include "route.h"
 
 #define TB 4          // tokens sharing one pass over the weights
 #define UNROLL 4      // 16-byte chunks in flight per lane
@@ -392,12 +393,10 @@ __device__ __forceinline__ void run_fmt1(const gemv_job &J, int blk, float (*red
     else run_job1<FMT, 1, XBF>(J, blk, red);
 }
 
-// every job of one launch reads x of one type (bf16 or fp32)
+// block b of a batch-1 launch; every job of one launch reads x of one type
 template <bool XBF>
-__global__ void __launch_bounds__(256) k_gemv1(gemv_pack pk)
+__device__ __forceinline__ void gemv1_block(const gemv_pack &pk, int b, float (*red)[4][2])
 {
-    __shared__ float red[4][4][2];
-    const int b = blockIdx.x;
     const int ji = (pk.n > 2 && b >= pk.j[2].blk0) ? 2 : (pk.n > 1 && b >= pk.j[1].blk0) ? 1 : 0;
 #define SEL(f) (ji == 2 ? pk.j[2].f : ji == 1 ? pk.j[1].f : pk.j[0].f)
     gemv_job J;
@@ -412,6 +411,34 @@ __global__ void __launch_bounds__(256) k_gemv1(gemv_pack pk)
     else run_fmt1<3, XBF>(J, blk, red);
 }
 
+template <bool XBF>
+__global__ void __launch_bounds__(256) k_gemv1(gemv_pack pk)
+{
+    __shared__ float red[4][4][2];
+    gemv1_block<XBF>(pk, blockIdx.x, red);
+}
+
+// One token's routing in block 0 (all four wavefronts compute the same
+// selection, see route.h) beside a batch-1 product that needs no routing
+// (the shared expert's down projection) in the other blocks: the one
+// wavefront of routing hides behind the product instead of running alone.
+template <int NPL, bool XBF>
+__global__ void __launch_bounds__(256)
+k_route_gemv1(whip_route_cfg c, const float *__restrict__ logits, const float *__restrict__ bias,
+              int32_t *__restrict__ ids, float *__restrict__ wout, int32_t *__restrict__ pair_tok,
+              int32_t *__restrict__ pair_exp, float *__restrict__ pair_w, int32_t *__restrict__ tok_pairs,
+              const uint8_t *const *__restrict__ recs, const uint8_t **__restrict__ pair_rec,
+              int *__restrict__ err, gemv_pack pk)
+{
+    __shared__ float red[4][4][2];
+    if (blockIdx.x == 0) {
+        route_body<NPL>(c, logits, bias, 1, 0, threadIdx.x & 63, ids, wout, pair_tok, pair_exp, pair_w,
+                        tok_pairs, recs, pair_rec, err);
+        return;
+    }
+    gemv1_block<XBF>(pk, blockIdx.x - 1, red);
+}
+
 // padded columns of a matrix (whole quantisation groups)
 static int padded_cols(const whip_mat *A)
 {
@@ -419,9 +446,9 @@ static int padded_cols(const whip_mat *A)
     return (A->cols + A->group - 1) / A->group * A->group;
 }
 
-static int launch_gemv1(const whip_gemv_job *jobs, int n, hipStream_t s)
+// the batch-1 launch's job table; returns its block count
+static int pack_gemv1(const whip_gemv_job *jobs, int n, gemv_pack &pk)
 {
-    gemv_pack pk;
     int blk = 0;
     for (int i = 0; i < n; i++) {
         const whip_gemv_job *q = &jobs[i];
@@ -446,6 +473,13 @@ static int launch_gemv1(const whip_gemv_job *jobs, int n, hipStream_t s)
     }
     pk.n = n;
     pk.T = 1;
+    return blk;
+}
+
+static int launch_gemv1(const whip_gemv_job *jobs, int n, hipStream_t s)
+{
+    gemv_pack pk;
+    const int blk = pack_gemv1(jobs, n, pk);
     if (jobs[0].x_bf16) hipLaunchKernelGGL(k_gemv1<true>, dim3(blk), dim3(256), 0, s, pk);
     else hipLaunchKernelGGL(k_gemv1<false>, dim3(blk), dim3(256), 0, s, pk);
     return (int)hipGetLastError();
@@ -521,4 +555,34 @@ extern "C" int whip_gemv(const whip_mat *A, const whip_mat *B, const float *x, i
         j[n].y_ld = y_ld; n++;
     }
     return whip_gemv_multi(j, n, T, s);
+}
+
+// One token: routing plus a batch-1 product independent of it, in one launch.
+extern "C" int whip_route_gemv(const whip_route_cfg *c, const float *logits, const float *bias,
+                               int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp,
+                               float *pair_w, int32_t *tok_pairs, const uint8_t *const *recs,
+                               const uint8_t **pair_rec, int *err, const whip_gemv_job *job,
+                               hipStream_t s)
+{
+    if (c->E > MAXE || c->E <= 0 || c->K <= 0 || c->K > 64 || c->K > c->E || !pair_exp)
+        return (int)hipErrorInvalidValue;
+    if (c->n_group > 1 && (c->n_group > 64 || c->E % c->n_group || c->topk_group < 1))
+        return (int)hipErrorInvalidValue;
+    if (check_mat(&job->A) || job->B || job->x_ld % 4 || (uintptr_t)job->x % 16 ||
+        (job->A.fmt != 0 && job->A.cols % 8))
+        return (int)hipErrorInvalidValue;
+    gemv_pack pk;
+    const int blk = pack_gemv1(job, 1, pk);
+    const int E = c->E;
+#define RG(N, XB) hipLaunchKernelGGL((k_route_gemv1<N, XB>), dim3(blk + 1), dim3(256), 0, s, *c, logits, bias, \
+                                     ids, w, pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err, pk)
+#define RGX(N) do { if (job->x_bf16) RG(N, true); else RG(N, false); } while (0)
+    if (E <= 64) RGX(1);
+    else if (E <= 128) RGX(2);
+    else if (E <= 256) RGX(4);
+    else if (E <= 512) RGX(8);
+    else RGX(16);
+#undef RGX
+#undef RG
+    return (int)hipGetLastError();
 }

@@ -79,6 +79,7 @@ typedef struct {
     int kinds, M, nv, P, rsplit, span;
     float *part;
     int *err;
+    const uint8_t *const *pair_rec;  /* [P] the pairs' records, or NULL     */
 } whip_vq_args;
 int whip_vq_apply(const whip_vq_args *a, hipStream_t s);
 int whip_vq_chunks(int nv);          /* nch for a given nv                  */
@@ -180,6 +181,15 @@ typedef struct {
     int n_books;
 } whip_bind_args;
 int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err, hipStream_t s);
+
+/* One token's routing (as whip_route with T = 1, plus pair_rec[j] = the
+ * selected expert's record) and a batch-1 product that does not depend on
+ * it (job; no paired matrix), in one launch. */
+int whip_route_gemv(const whip_route_cfg *c, const float *logits, const float *bias,
+                    int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp,
+                    float *pair_w, int32_t *tok_pairs, const uint8_t *const *recs,
+                    const uint8_t **pair_rec, int *err, const whip_gemv_job *job,
+                    hipStream_t s);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,250 @@
+// SPDX-License-Identifier: Apache-2.0
+//
+// route.h — the routing body (scores, group limit, top-k) shared by the
+// routing kernel and the launch that pairs routing with the shared
+// expert's down projection.  See route.hip for the engine semantics.
+#pragma once
+#include "common.h"
+#include "launch.h"
+
+#define MAXE 1024
+
+#define NEG_INF (-__int_as_float(0x7f800000))
+
+// (a, ea) precedes (b, eb) in the engine's selection order: larger value
+// first, the lower id among equal values (a strict-greater scan keeps the
+// first maximum it meets).
+__device__ __forceinline__ bool before(float a, int ea, float b, int eb)
+{
+    return a > b || (a == b && ea < eb);
+}
+
+// Selection key: one unsigned 64-bit number whose order is the selection
+// order.  High word: the value's bits mapped so unsigned order is float
+// order (-0 is first folded into +0, which compares equal to it); low word:
+// ~e, so the lower id is the larger key among equal values.  0 marks "not a
+// candidate" (value not above the scan's floor -1e30, NaN, or taken).
+__device__ __forceinline__ uint64_t sel_key(float v, int e)
+{
+    if (!(v > -1e30f)) return 0;
+    const uint32_t u = __float_as_uint(__fadd_rn(v, 0.0f));
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)e;
+}
+
+// Wave maxima over the butterfly of common.h's wave_sum.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k)
+{
+    uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    auto mx = [&](uint32_t l2, uint32_t h2) {
+        const uint64_t a = ((uint64_t)hi << 32) | lo, b = ((uint64_t)h2 << 32) | l2;
+        if (b > a) { lo = l2; hi = h2; }
+    };
+    mx(dpp32<0xB1>(lo), dpp32<0xB1>(hi));     // quad_perm [1,0,3,2]
+    mx(dpp32<0x4E>(lo), dpp32<0x4E>(hi));     // quad_perm [2,3,0,1]
+    mx(dpp32<0x141>(lo), dpp32<0x141>(hi));   // row_half_mirror
+    mx(dpp32<0x140>(lo), dpp32<0x140>(hi));   // row_mirror
+    {
+        auto a = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        auto b = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        lo = a[0]; hi = b[0];
+        mx(a[1], b[1]);
+    }
+    {
+        auto a = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+        auto b = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+        lo = a[0]; hi = b[0];
+        mx(a[1], b[1]);
+    }
+    return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v)
+{
+    // values are never NaN here, so the order-free max is exact
+    uint32_t u = __float_as_uint(v);
+    auto mx = [&](uint32_t o) { const float a = __uint_as_float(o); if (a > __uint_as_float(u)) u = o; };
+    mx(dpp32<0xB1>(u));
+    mx(dpp32<0x4E>(u));
+    mx(dpp32<0x141>(u));
+    mx(dpp32<0x140>(u));
+    { auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false); u = a[0]; mx(a[1]); }
+    { auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false); u = a[0]; mx(a[1]); }
+    return __uint_as_float(u);
+}
+
+// One wavefront per token; lane L holds experts L*NPL .. L*NPL+NPL-1 in
+// registers.  Each of the K selection passes is one wave max over the
+// selection keys, which picks exactly the expert the engine's pass picks.
+// Every wavefront that runs it for one token computes the same values and
+// writes them to the same places, so a workgroup of several wavefronts may
+// run it (its barriers then meet).
+template <int NPL>
+__device__ __forceinline__ void
+route_body(const whip_route_cfg &c, const float *__restrict__ logits, const float *__restrict__ bias,
+           int T, int t, int L, int32_t *__restrict__ ids, float *__restrict__ wout,
+           int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp, float *__restrict__ pair_w,
+           int32_t *__restrict__ tok_pairs, const uint8_t *const *__restrict__ recs,
+           const uint8_t **__restrict__ pair_rec, int *__restrict__ err)
+{
+    __shared__ float s_v[64 * NPL];
+    __shared__ float s_g[64];
+    __shared__ int s_keep[64];
+    const int E = c.E, K = c.K;
+    const float *lg = logits + (size_t)t * E;
+    float sc[NPL], sel[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; j++) {
+        const int e = L * NPL + j;
+        sc[j] = e < E ? lg[e] : 0.0f;
+    }
+
+    if (c.score_func == 1) {
+        // max (order-free), then the engine's sum in expert order
+        float mx = -1e30f;
+#pragma unroll
+        for (int j = 0; j < NPL; j++)
+            if (L * NPL + j < E && sc[j] > mx) mx = sc[j];
+        mx = wave_max_f32(mx);
+#pragma unroll
+        for (int j = 0; j < NPL; j++) {
+            const int e = L * NPL + j;
+            sc[j] = e < E ? wh_expf(__fsub_rn(sc[j], mx)) : 0.0f;
+            if (e < E) s_v[e] = sc[j];
+        }
+        __syncthreads();
+        float sum = 0.0f;
+        for (int k = 0; k < E; k++) sum = __fadd_rn(sum, s_v[k]);
+#pragma unroll
+        for (int j = 0; j < NPL; j++) sc[j] = __fdiv_rn(sc[j], sum);
+    } else if (c.score_func == 2) {
+#pragma unroll
+        for (int j = 0; j < NPL; j++) {
+            const float l = sc[j];
+            const float sp = l > 30.0f ? l : log1pf(wh_expf(l));
+            sc[j] = __fsqrt_rn(sp);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NPL; j++) sc[j] = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf(-sc[j])));
+    }
+#pragma unroll
+    for (int j = 0; j < NPL; j++) {
+        const int e = L * NPL + j;
+        sel[j] = e < E ? __fadd_rn(sc[j], bias ? bias[e] : 0.0f) : NEG_INF;
+    }
+
+    if (c.n_group > 1) {
+        // a group's score: the sum of its two largest values above -inf
+        // (-inf when it has fewer); keep the topk_group groups that come
+        // first under `before` among those above -inf; mask the rest
+        const int G = c.n_group, gs = E / G;
+        const int lpg = gs % NPL == 0 ? gs / NPL : 0;           // lanes per group
+        int keep;
+        if (lpg > 0 && (lpg & (lpg - 1)) == 0) {
+            // groups tile the wave in aligned runs of lpg lanes: lane-local
+            // top two, then a butterfly inside the run (values only: which
+            // expert holds them does not matter)
+            float a = NEG_INF, b = NEG_INF;
+#pragma unroll
+            for (int j = 0; j < NPL; j++) {
+                const float v = sel[j];
+                if (v > a) { b = a; a = v; }
+                else if (v > b) b = v;
+            }
+            for (int o = 1; o < lpg; o <<= 1) {
+                const float pa = __shfl_xor(a, o, 64), pb = __shfl_xor(b, o, 64);
+                const float hi = fmaxf(a, pa), lo = fminf(a, pa);
+                b = fmaxf(lo, fmaxf(b, pb));
+                a = hi;
+            }
+            const float mine = __fadd_rn(a, gs > 1 ? b : 0.0f);
+            const int g = L / lpg;
+            int rk = 0;
+            for (int k = 0; k < G; k++) {
+                const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), k * lpg));
+                rk += (o > NEG_INF) && before(o, k, mine, g);
+            }
+            keep = mine > NEG_INF && rk < c.topk_group;
+        } else {
+            __syncthreads();                                     // softmax's reads of s_v
+#pragma unroll
+            for (int j = 0; j < NPL; j++)
+                if (L * NPL + j < E) s_v[L * NPL + j] = sel[j];
+            __syncthreads();
+            if (L < G) {
+                float a = NEG_INF, b = NEG_INF;
+                for (int k = L * gs; k < (L + 1) * gs; k++) {
+                    const float v = s_v[k];
+                    if (v > a) { b = a; a = v; }
+                    else if (v > b) b = v;
+                }
+                s_g[L] = __fadd_rn(a, gs > 1 ? b : 0.0f);
+            }
+            __syncthreads();
+            if (L < G) {
+                const float mine = s_g[L];
+                int rk = 0;
+                for (int k = 0; k < G; k++) {
+                    const float o = s_g[k];
+                    rk += (o > NEG_INF) && before(o, k, mine, L);
+                }
+                s_keep[L] = mine > NEG_INF && rk < c.topk_group;
+            }
+            __syncthreads();
+            keep = -1;
+        }
+#pragma unroll
+        for (int j = 0; j < NPL; j++) {
+            const int e = L * NPL + j;
+            if (e < E && !(keep >= 0 ? keep : s_keep[e / gs])) sel[j] = NEG_INF;
+        }
+    }
+
+    uint64_t key[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; j++) key[j] = L * NPL + j < E ? sel_key(sel[j], L * NPL + j) : 0;
+
+    float wsum = 0.0f, myw = 0.0f;
+    int myid = -1, ok = 1;
+    for (int p = 0; p < K; p++) {
+        uint64_t best = key[0];
+#pragma unroll
+        for (int j = 1; j < NPL; j++) best = key[j] > best ? key[j] : best;
+        best = wave_max_u64(best);
+        if (best == 0) { ok = 0; break; }
+        const int e = __builtin_amdgcn_readfirstlane((int)~(uint32_t)best);
+        const int owner = e / NPL, slot = e - owner * NPL;
+        float v = sc[0];
+#pragma unroll
+        for (int j = 1; j < NPL; j++) v = j == slot ? sc[j] : v;
+        const float wf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), owner));
+        if (L == owner) {
+#pragma unroll
+            for (int j = 0; j < NPL; j++) if (j == slot) key[j] = 0;
+        }
+        wsum = __fadd_rn(wsum, wf);
+        if (L == p) { myid = e; myw = wf; }
+    }
+    if (ok) {
+        if (c.renorm && K > 1) myw = __fdiv_rn(myw, __fadd_rn(wsum, 1e-20f));
+        myw = __fmul_rn(myw, c.routed_scale);
+    } else {
+        myid = -1;
+        myw = 0.0f;
+        if (L == 0) atomicOr(err, 2);
+    }
+    if (L < K) {
+        ids[(size_t)t * K + L] = myid;
+        wout[(size_t)t * K + L] = myw;
+        if (pair_exp && T == 1) {
+            pair_tok[L] = 0;
+            pair_exp[L] = myid < 0 ? E : myid;       // E: the table's NULL sentinel
+            pair_w[L] = myw;
+            tok_pairs[L] = L;
+            // the pair's record, for kernels that start on it at once
+            if (pair_rec) pair_rec[L] = myid < 0 ? nullptr : recs[myid];
+        }
+    }
+}
+

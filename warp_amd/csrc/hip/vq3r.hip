@@ -422,10 +422,17 @@ k_vq_lanes(whip_vq_args a, int nch, int span, int tiles, int per_wg, int shares)
     {
         const int q = p_lo + min(tid, p_hi - p_lo);
         const int32_t *psrc = a.pair_src ? a.pair_src : a.pair_exp;
-        const int e = a.pair_exp[q];
-        const int xq = psrc[q], xf = psrc[p_first];
+        const uint8_t *myrec;
+        int xq, xf;
+        if (a.pair_rec) {                           // one load: the router wrote them
+            myrec = a.pair_rec[q];
+            xq = psrc[q]; xf = psrc[p_first];
+        } else {
+            const int e = a.pair_exp[q];
+            xq = psrc[q]; xf = psrc[p_first];
+            myrec = a.recs[e];
+        }
         const int myxr = a.pair_src ? xq : q, xr0 = a.pair_src ? xf : p_first;
-        const uint8_t *myrec = a.recs[e];
         build_loads(t0, xr0);
         if (tid <= p_hi - p_lo) { s_rec[tid] = myrec; s_xr[tid] = myxr; }
     }

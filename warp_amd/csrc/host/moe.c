@@ -57,6 +57,9 @@ struct waste_hip_moe {
     float *plogits, *pw;         /* the lookahead's logits and weights      */
     int routed_T;                /* T of the last route(), 0 none          */
     int32_t *h_sel;              /* pinned: selection [0,64), lookahead [64,128) */
+    const uint8_t **pair_rec;    /* [64] records of a T = 1 route's pairs   */
+    int pair_rec_ok;             /* pair_rec matches the table (no bind since) */
+    int sh_done;                 /* the route's launch ran the shared down  */
     int32_t *d_look;             /* the lookahead's ids                    */
     int prof_on;
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
@@ -118,7 +121,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->logits, m->w, m->pair_w, m->part_gu, m->h, m->part_d, m->sh_a,
                      m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
                      m->tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
-                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look };
+                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->pair_rec };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0])
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -206,6 +209,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->plogits, (size_t)m->E * 4);
     rc |= dmalloc((void **)&m->pw, 64 * 4);
     rc |= dmalloc((void **)&m->d_look, 64 * 4);
+    rc |= dmalloc((void **)&m->pair_rec, 64 * sizeof(void *));
     if (m->T > m->Td) {
         rc |= dmalloc((void **)&m->pair_pos, (size_t)P * 4);
         rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
@@ -352,6 +356,7 @@ static int check_record(const waste_hip_moe *m, int expert, const uint8_t *rec, 
 
 static int set_ptr(waste_hip_moe *m, int expert, const uint8_t *dev)
 {
+    m->pair_rec_ok = 0;
     if (m->h_recs[expert] && !dev) m->bound--;
     if (!m->h_recs[expert] && dev) m->bound++;
     m->h_recs[expert] = dev;
@@ -492,6 +497,20 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
     MARK(1);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
+    m->sh_done = 0;
+    m->pair_rec_ok = 0;
+    if (T == 1 && m->has_shared) {
+        /* routing and the shared expert's down projection in one launch;
+         * the route also writes the pairs' records */
+        whip_gemv_job j;
+        j.A = m->sh[2]; j.B = NULL; j.x = m->h_sh; j.x_ld = m->SI; j.x_bf16 = 0; j.y = m->sh_out;
+        j.y_ld = H;
+        CK((hipError_t)whip_route_gemv(&rc, lg, m->d_bias, d_ids, d_w, m->pair_tok, m->pair_exp, m->pair_w,
+                                       m->tok_pairs, m->d_recs, m->pair_rec, m->err, &j, s));
+        m->sh_done = 1;
+        m->pair_rec_ok = 1;
+        return 0;
+    }
     CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, m->pair_tok, m->pair_exp,
                               m->pair_w, m->tok_pairs, m->err, s));
     if (T > 1)
@@ -507,6 +526,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     whip_vq_args a;
     memset(&a, 0, sizeof a);
     a.recs = m->d_recs; a.pair_exp = m->pair_exp; a.pair_src = m->pair_tok;
+    a.pair_rec = (T == 1 && m->pair_rec_ok) ? m->pair_rec : NULL;
     a.src = x; a.src_ld = H; a.src_bf16 = x_bf16; a.booksT = m->d_booksT; a.cb = m->cb;
     a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.kinds = 2; a.M = I; a.nv = m->nv_gu; a.P = P; a.rsplit = m->rsplit_gu;
@@ -527,7 +547,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     a.span = 0;
     CK((hipError_t)whip_vq_apply(&a, s));
     MARK(5);
-    if (m->has_shared)
+    if (m->has_shared && !m->sh_done)
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
     MARK(6);
     CK((hipError_t)whip_combine(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
@@ -608,6 +628,7 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *c
     a.cb = m->cb;
     a.n_books = m->n_books > 0 ? m->n_books : 65536 + 9;
     CK((hipError_t)whip_bind(m->d_recs, &a, m->err, (hipStream_t)stream));
+    m->pair_rec_ok = 0;
     for (int i = 0; i < n; i++) {
         const int e = a.expert[i];
         if (m->h_recs[e] && !a.rec[i]) m->bound--;
