@@ -300,6 +300,49 @@ __device__ __forceinline__ float chunk_dot(uint4 raw, const uint4 *xw)
     return a;
 }
 
+// Q4G chunk against bf16 x on the dot-product unit.  A byte of two nibbles
+// (n_lo, n_hi) becomes the bf16 pair (128 + n_lo, 128 + n_hi): the code is
+// the low mantissa bits under the exponent of 128, exact; one v_dot2 per
+// pair multiplies it into the raw bf16 x pair with fp32 accumulation, and
+// sum((128 + n) x) - 136 sum(x) = sum((n - 8) x).  sx136 = 136 * sum(x) of
+// the chunk, shared by the matrices that read it.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float chunk_dot_q4bf(uint4 raw, const uint4 *xw, float sx136)
+{
+    const uint32_t uw[4] = {raw.x, raw.y, raw.z, raw.w};
+    const uint32_t xd[16] = {xw[0].x, xw[0].y, xw[0].z, xw[0].w, xw[1].x, xw[1].y, xw[1].z, xw[1].w,
+                             xw[2].x, xw[2].y, xw[2].z, xw[2].w, xw[3].x, xw[3].y, xw[3].z, xw[3].w};
+    float a = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        const uint32_t t = uw[m] & 0x0F0F0F0Fu, u = (uw[m] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            // [t.byte j, 0, u.byte j, 0] | 128.0 in both halves
+            const uint32_t pr = __builtin_amdgcn_perm(u, t, 0x0C000C00u | ((4u + j) << 16) | (uint32_t)j) | 0x43004300u;
+            a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pr),
+                                               __builtin_bit_cast(bf16x2_t, xd[4 * m + j]), a, false);
+        }
+    }
+    return a - sx136;
+}
+
+__device__ __forceinline__ float chunk_sum136_bf(const uint4 *xw)
+{
+    const uint32_t one2 = 0x3F803F80u;                 // (1.0, 1.0) in bf16
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t w4[4] = {xw[i].x, xw[i].y, xw[i].z, xw[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w4[k]),
+                                               __builtin_bit_cast(bf16x2_t, one2), s, false);
+    }
+    return 136.0f * s;
+}
+
 template <int FMT, int RPW, bool XBF>
 __device__ __forceinline__ void run_job1(const gemv_job &J, int blk, float (*red)[4][2])
 {
@@ -350,6 +393,16 @@ __device__ __forceinline__ void run_job1(const gemv_job &J, int blk, float (*red
             const int k = k0 + u * stride;
             if (k >= nchunk) continue;                 // rows past the end are never written
             mask_xs<FMT, XBF>(J.cols, k, xw[u]);
+            if (FMT == 3 && XBF) {
+                const float sx = chunk_sum136_bf(xw[u]);
+#pragma unroll
+                for (int i = 0; i < RPW; i++) {
+                    a0[i] = __fmaf_rn(wh_f16_scale(s0[i][u]), chunk_dot_q4bf(w0[i][u], xw[u], sx), a0[i]);
+                    if (pair)
+                        a1[i] = __fmaf_rn(wh_f16_scale(s1[i][u]), chunk_dot_q4bf(w1[i][u], xw[u], sx), a1[i]);
+                }
+                continue;
+            }
 #pragma unroll
             for (int i = 0; i < RPW; i++) {
                 const float d0 = chunk_dot<FMT, XBF>(w0[i][u], xw[u]);
