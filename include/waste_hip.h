@@ -42,6 +42,9 @@ extern "C" {
 #define WASTE_HIP_EDEVICE   (-8)   /* a HIP runtime call failed          */
 #define WASTE_HIP_ERANGE    (-9)   /* an fp16 operand of the many-token
                                       path was out of range              */
+#define WASTE_HIP_ETIMEOUT  (-10)  /* a stage of the one-launch decode
+                                      waited too long for another (its
+                                      workgroups were not all resident)  */
 
 /* Library name and device check.  NULL when no usable gfx950 device. */
 const char *waste_hip_device_name(void);
@@ -140,6 +143,17 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T,
                           float *y, int32_t *ids, float *w, float *logits,
                           void *stream);
 
+/* How forward() runs T == 1: mode 0 (the default) as the staged kernels
+ * route()/experts() run; mode 1 as two launches, the router and the shared
+ * expert's gate/up, then every expert stage in one persistent launch whose
+ * stages wait for each other through counters in device memory.  Shapes
+ * mode 1 does not take (E > 256, K > 16, H or moe_inter not a multiple of
+ * 256, an F32 shared down projection) and profiled forwards run staged.
+ * Mode 1 holds every CU for the launch: forwards of one layer must not
+ * overlap, and other work that holds CUs delays it (past ~50 ms a stage
+ * gives up: WASTE_HIP_ETIMEOUT). */
+int waste_hip_moe_set_decode(waste_hip_moe *m, int mode);
+
 /* forward() in two halves, for a caller that must see the selection
  * before the experts run (an expert cache: moe_layer's hint and holds sit
  * between its router and its experts, src/model.c:5639-5700).
@@ -193,7 +207,7 @@ int waste_hip_moe_forward_cached(waste_hip_moe *m, waste_hip_ecache *c, int laye
 
 /* Waits for the layer's work and returns the sticky device error (0, or
  * WASTE_HIP_EROUTE / WASTE_HIP_ERECORD / WASTE_HIP_EUNBOUND /
- * WASTE_HIP_ERANGE), clearing it. */
+ * WASTE_HIP_ERANGE / WASTE_HIP_ETIMEOUT), clearing it. */
 int waste_hip_moe_status(waste_hip_moe *m, void *stream);
 
 /* Bytes the layer reads from HBM for one forward that touches `n_distinct`

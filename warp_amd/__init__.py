@@ -23,10 +23,10 @@ WQ_F32, WQ_Q8G, WQ_Q4G, WQ_VQ3R = 0, 2, 3, 4
 SCORE_SIGMOID, SCORE_SOFTMAX, SCORE_SQRTSOFTPLUS = 0, 1, 2
 
 ERRORS = {0: "ok", -1: "EINVAL", -2: "ENODEV", -3: "ENOMEM", -4: "ERECORD", -5: "ECRC",
-          -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE", -9: "ERANGE"}
+          -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE", -9: "ERANGE", -10: "ETIMEOUT"}
 
-OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE, ERANGE = \
-    0, -1, -2, -3, -4, -5, -6, -7, -8, -9
+OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE, ERANGE, ETIMEOUT = \
+    0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10
 
 # Every symbol include/waste_hip.h declares.
 EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_host_buffers",
@@ -37,7 +37,7 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_moe_profile", "waste_hip_moe_profile_read", "waste_hip_record_bytes",
            "waste_hip_synth_codebooks", "waste_hip_synth_records",
            "waste_hip_moe_route", "waste_hip_moe_experts", "waste_hip_moe_bind_table",
-           "waste_hip_moe_predict", "waste_hip_moe_forward_cached",
+           "waste_hip_moe_predict", "waste_hip_moe_forward_cached", "waste_hip_moe_set_decode",
            "waste_hip_ecache_create", "waste_hip_ecache_destroy", "waste_hip_ecache_set_source",
            "waste_hip_ecache_hint", "waste_hip_ecache_prefetch", "waste_hip_ecache_get",
            "waste_hip_ecache_hold", "waste_hip_ecache_release", "waste_hip_ecache_admit",
@@ -119,6 +119,7 @@ def lib():
         "waste_hip_moe_bind_table": (i, [vp, ip, C.POINTER(vp), i, i, vp]),
         "waste_hip_moe_predict": (i, [vp, vp, i, i, vp, vp]),
         "waste_hip_moe_forward_cached": (i, [vp, vp, i, vp, i, vp, i, vp, vp, vp, vp]),
+        "waste_hip_moe_set_decode": (i, [vp, i]),
         "waste_hip_ecache_create": (i, [C.c_size_t, C.c_size_t, i, i, i, C.POINTER(vp)]),
         "waste_hip_ecache_destroy": (None, [vp]),
         "waste_hip_ecache_set_source": (i, [vp, C.POINTER(vp), i, i]),
@@ -212,6 +213,10 @@ class MoeLayer:
                 stream=None):
         check(self.L.waste_hip_moe_forward(self.h, x_ptr, int(bf16), T, y_ptr, ids_ptr, w_ptr,
                                            logits_ptr, stream), "forward")
+
+    def set_decode(self, mode):
+        """1: one-launch decode for T == 1 (the default); 0: staged kernels."""
+        check(self.L.waste_hip_moe_set_decode(self.h, int(mode)), "set_decode")
 
     def status(self, stream=None):
         return self.L.waste_hip_moe_status(self.h, stream)

@@ -30,7 +30,8 @@ __constant__ const uint64_t wh_exp_tab[32] = {
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
 };
 
-WH_INLINE float wh_expf(float x)
+// tab: the 32 table entries (wh_exp_tab, or a copy of it in LDS)
+WH_INLINE float wh_expf_t(float x, const uint64_t *tab)
 {
     const uint32_t ux = __float_as_uint(x);
     const uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -50,7 +51,7 @@ WH_INLINE float wh_expf(float x)
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd = __dsub_rn(kd, shift);
     const double r = __fma_rn(inv, xd, -kd);
-    uint64_t t = wh_exp_tab[ki % 32];
+    uint64_t t = tab[ki % 32];
     t += ki << 47;
     const double s = __longlong_as_double((long long)t);
     const double p = __fma_rn(c0, r, c1);
@@ -60,6 +61,8 @@ WH_INLINE float wh_expf(float x)
     y = __dmul_rn(y, s);
     return (float)y;
 }
+
+WH_INLINE float wh_expf(float x) { return wh_expf_t(x, wh_exp_tab); }
 
 /* fp16 per-row / per-group scale: subnormals kept, exponent 31 read as a
  * normal exponent (the engine's waste_f16). */

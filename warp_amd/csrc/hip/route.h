@@ -78,25 +78,42 @@ __device__ __forceinline__ float wave_max_f32(float v)
 // selection keys, which picks exactly the expert the engine's pass picks.
 // Every wavefront that runs it for one token computes the same values and
 // writes them to the same places, so a workgroup of several wavefronts may
-// run it (its barriers then meet).
-template <int NPL>
+// run it (its barriers then meet).  lds: ROUTE_LDS_FLOATS(NPL) floats of
+// workgroup scratch.  COH: the logits were written by other workgroups of
+// the same launch, so they are read device-coherent (past the
+// non-coherent caches).  etab: expf's table (NULL: the constant one).
+#define ROUTE_LDS_FLOATS(NPL) (64 * (NPL) + 128)
+
+template <typename T> __device__ __forceinline__ T coh_ld(const T *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T> __device__ __forceinline__ void coh_st(T *p, T v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NPL, bool COH = false>
 __device__ __forceinline__ void
 route_body(const whip_route_cfg &c, const float *__restrict__ logits, const float *__restrict__ bias,
            int T, int t, int L, int32_t *__restrict__ ids, float *__restrict__ wout,
            int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp, float *__restrict__ pair_w,
            int32_t *__restrict__ tok_pairs, const uint8_t *const *__restrict__ recs,
-           const uint8_t **__restrict__ pair_rec, int *__restrict__ err)
+           const uint8_t **__restrict__ pair_rec, int *__restrict__ err, float *lds,
+           const uint64_t *etab = nullptr)
 {
-    __shared__ float s_v[64 * NPL];
-    __shared__ float s_g[64];
-    __shared__ int s_keep[64];
+    const uint64_t *et = etab ? etab : wh_exp_tab;
+    float *s_v = lds, *s_g = lds + 64 * NPL;
+    int *s_keep = (int *)(lds + 64 * NPL + 64);
     const int E = c.E, K = c.K;
     const float *lg = logits + (size_t)t * E;
     float sc[NPL], sel[NPL];
 #pragma unroll
     for (int j = 0; j < NPL; j++) {
         const int e = L * NPL + j;
-        sc[j] = e < E ? lg[e] : 0.0f;
+        const int ec = e < E ? e : 0;
+        const float l = COH ? coh_ld(lg + ec) : lg[ec];
+        sc[j] = e < E ? l : 0.0f;
     }
 
     if (c.score_func == 1) {
@@ -109,7 +126,7 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
 #pragma unroll
         for (int j = 0; j < NPL; j++) {
             const int e = L * NPL + j;
-            sc[j] = e < E ? wh_expf(__fsub_rn(sc[j], mx)) : 0.0f;
+            sc[j] = e < E ? wh_expf_t(__fsub_rn(sc[j], mx), et) : 0.0f;
             if (e < E) s_v[e] = sc[j];
         }
         __syncthreads();
@@ -121,12 +138,12 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
 #pragma unroll
         for (int j = 0; j < NPL; j++) {
             const float l = sc[j];
-            const float sp = l > 30.0f ? l : log1pf(wh_expf(l));
+            const float sp = l > 30.0f ? l : log1pf(wh_expf_t(l, et));
             sc[j] = __fsqrt_rn(sp);
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < NPL; j++) sc[j] = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf(-sc[j])));
+        for (int j = 0; j < NPL; j++) sc[j] = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf_t(-sc[j], et)));
     }
 #pragma unroll
     for (int j = 0; j < NPL; j++) {
@@ -247,4 +264,3 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         }
     }
 }
-

@@ -27,8 +27,9 @@ k_route(whip_route_cfg c, const float *__restrict__ logits, const float *__restr
         int32_t *__restrict__ pair_exp, float *__restrict__ pair_w, int32_t *__restrict__ tok_pairs,
         int *__restrict__ err)
 {
+    __shared__ float rl[ROUTE_LDS_FLOATS(NPL)];
     route_body<NPL>(c, logits, bias, T, blockIdx.x, threadIdx.x, ids, wout, pair_tok, pair_exp, pair_w,
-                    tok_pairs, nullptr, nullptr, err);
+                    tok_pairs, nullptr, nullptr, err, rl);
 }
 
 extern "C" int whip_route(const whip_route_cfg *c, const float *logits, const float *bias, int T,

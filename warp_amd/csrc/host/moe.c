@@ -62,6 +62,8 @@ struct waste_hip_moe {
     int sh_done;                 /* the route's launch ran the shared down  */
     int32_t *d_look;             /* the lookahead's ids                    */
     int prof_on;
+    int decode_mode;             /* 1: the persistent experts launch (T == 1) */
+    int *sync;                   /* its stage counters (zero between launches) */
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
     waste_hip_moe_prof prof;
 };
@@ -121,7 +123,8 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->logits, m->w, m->pair_w, m->part_gu, m->h, m->part_d, m->sh_a,
                      m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
                      m->tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
-                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->pair_rec };
+                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->pair_rec,
+                     m->sync };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0])
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -187,6 +190,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     m->rec_min = m->off_sc + 2 * (size_t)(2 * m->I + m->H);
     m->rec_bytes = (m->rec_min + 4095) / 4096 * 4096;
     m->cb = -1;
+    m->decode_mode = 0;
     const int P = m->T * m->K, Pd = m->Td * m->K;
     m->rsplit_gu = pick_rsplit(m->nch_gu * 2 * m->K, m->I / 64);
     m->rsplit_d = pick_rsplit(m->nch_d * m->K, m->H / 64);
@@ -210,6 +214,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->pw, 64 * 4);
     rc |= dmalloc((void **)&m->d_look, 64 * 4);
     rc |= dmalloc((void **)&m->pair_rec, 64 * sizeof(void *));
+    rc |= dmalloc((void **)&m->sync, whip_decode1_sync_ints(m->H) * 4);
     if (m->T > m->Td) {
         rc |= dmalloc((void **)&m->pair_pos, (size_t)P * 4);
         rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
@@ -220,7 +225,8 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     }
     if (rc || !m->h_recs) { waste_hip_moe_destroy(m); return WASTE_HIP_ENOMEM; }
     if (hipMemset(m->d_recs, 0, ((size_t)m->E + 1) * sizeof(void *)) != hipSuccess ||
-        hipMemset(m->err, 0, 64) != hipSuccess) {
+        hipMemset(m->err, 0, 64) != hipSuccess ||
+        hipMemset(m->sync, 0, whip_decode1_sync_ints(m->H) * 4) != hipSuccess) {
         waste_hip_moe_destroy(m);
         return WASTE_HIP_EDEVICE;
     }
@@ -592,12 +598,68 @@ int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     return T > m->Td ? experts_many(m, x, x_bf16, T, y, s) : experts_few(m, x, x_bf16, T, y, s);
 }
 
+/* T == 1 in two launches: the router and the shared expert's gate/up
+ * (gemv.hip), then every expert stage in one (decode.hip); 1 if it ran, 0
+ * if the shape is not one the second takes (the staged kernels then run),
+ * < 0 on a launch failure. */
+static int forward_one(waste_hip_moe *m, const void *x, int x_bf16, float *y, int32_t *ids, float *w,
+                       float *logits, hipStream_t s)
+{
+    if (!m->decode_mode || m->prof_on || (uintptr_t)x % 16) return 0;
+    whip_dec1_args a;
+    memset(&a, 0, sizeof a);
+    a.E = m->E; a.K = m->K; a.H = m->H; a.I = m->I; a.SI = m->SI;
+    a.rc.E = m->E; a.rc.K = m->K; a.rc.score_func = m->c.score_func; a.rc.renorm = m->c.renorm;
+    a.rc.routed_scale = m->c.routed_scale; a.rc.n_group = m->c.n_group; a.rc.topk_group = m->c.topk_group;
+    a.x = x; a.x_bf16 = x_bf16;
+    a.router = m->router; a.bias = m->d_bias;
+    a.has_shared = m->has_shared;
+    if (m->has_shared) { a.sh[0] = m->sh[0]; a.sh[1] = m->sh[1]; a.sh[2] = m->sh[2]; }
+    a.recs = m->d_recs; a.booksT = m->d_booksT; a.cb = m->cb;
+    a.off_gate = m->off_gate; a.off_up = m->off_up; a.off_down = m->off_down; a.off_sc = m->off_sc;
+    a.logits = logits ? logits : m->logits;
+    a.ids = ids ? ids : m->ids;
+    a.w = w ? w : m->w;
+    a.pair_tok = m->pair_tok; a.pair_exp = m->pair_exp; a.pair_w = m->pair_w; a.tok_pairs = m->tok_pairs;
+    a.pair_rec = m->pair_rec;
+    a.h_sh = m->h_sh; a.sh_out = m->sh_out; a.part_gu = m->part_gu; a.part_d = m->part_d; a.y = y;
+    a.err = m->err; a.sync = m->sync;
+    if (whip_decode1_check(&a)) return 0;
+    /* router logits and the shared expert's gate/up, then the experts */
+    whip_gemv_job r[2];
+    int nr = 0;
+    r[nr].A = m->router; r[nr].B = NULL; r[nr].x = x; r[nr].x_ld = m->H; r[nr].x_bf16 = x_bf16;
+    r[nr].y = a.logits; r[nr].y_ld = m->E; nr++;
+    if (m->has_shared) {
+        r[nr].A = m->sh[0]; r[nr].B = &m->sh[1]; r[nr].x = x; r[nr].x_ld = m->H; r[nr].x_bf16 = x_bf16;
+        r[nr].y = m->h_sh; r[nr].y_ld = m->SI; nr++;
+    }
+    CK((hipError_t)whip_gemv_multi(r, nr, 1, s));
+    if (whip_decode1(&a, s)) return WASTE_HIP_EDEVICE;
+    m->routed_T = 1;
+    m->pair_rec_ok = 1;
+    m->sh_done = 1;
+    return 1;
+}
+
+int waste_hip_moe_set_decode(waste_hip_moe *m, int mode)
+{
+    if (!m || mode < 0 || mode > 1) return WASTE_HIP_EINVAL;
+    m->decode_mode = mode;
+    return 0;
+}
+
 int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
                           int32_t *ids, float *w, float *logits, void *stream)
 {
     int rc = ready(m, x, T);
     if (rc) return rc;
     if (!y || m->cb < 0 || m->cb + 9 > m->n_books) return WASTE_HIP_EINVAL;
+    if (T == 1) {
+        m->routed_T = 0;
+        rc = forward_one(m, x, x_bf16, y, ids, w, logits, (hipStream_t)stream);
+        if (rc) return rc < 0 ? rc : 0;
+    }
     rc = waste_hip_moe_route(m, x, x_bf16, T, ids, w, logits, stream);
     return rc ? rc : waste_hip_moe_experts(m, x, x_bf16, T, y, stream);
 }
@@ -736,6 +798,7 @@ int waste_hip_moe_status(waste_hip_moe *m, void *stream)
     if (e & 8) return WASTE_HIP_ERECORD;
     if (e & 1) return WASTE_HIP_EUNBOUND;
     if (e & 4) return WASTE_HIP_ERANGE;
+    if (e & 16) return WASTE_HIP_ETIMEOUT;
     return 0;
 }
 
