@@ -80,6 +80,13 @@ typedef struct {
     float *part;
     int *err;
     const uint8_t *const *pair_rec;  /* [P] the pairs' records, or NULL     */
+    /* Down pass from the gate/up partials (positions-across-lanes kernel
+     * only, M of them = nv*8 rows): pair p's x is silu(scale_g * sum of its
+     * act_nch gate partials) * (scale_u * sum of its up partials), the
+     * record's gate|up row scales at act_sc_off; src is then unused. */
+    const float *act_part;
+    int act_nch;
+    uint32_t act_sc_off;
 } whip_vq_args;
 int whip_vq_apply(const whip_vq_args *a, hipStream_t s);
 int whip_vq_chunks(int nv);          /* nch for a given nv                  */

@@ -206,6 +206,7 @@ struct tile_map {
 // instead of branches): the hardware counts loads in issue order, and a
 // load on only one side of a branch leaves the compiler unsure how many are
 // in flight, so it would wait for all of them, the prefetched tiles too.
+template <bool ACT>
 __device__ __forceinline__ void
 vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, int shares)
 {
@@ -213,6 +214,7 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
     __shared__ float sbook[3 * 8 * 256];             // a kind's books, [stage][dim][code]
     __shared__ const uint8_t *s_rec[SPAN_MAX];       // records of pairs p_lo ..
     __shared__ int s_xr[SPAN_MAX];                   // and their source rows
+    __shared__ float s_h[256];                       // x of a class reduced from partials (act_part)
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int v = lane & 31, h = lane >> 5;
     tile_map tm;
@@ -273,23 +275,74 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
         const float *bk = a.booksT + (size_t)(a.cb + kind * 3) * 8 * 256;
 #pragma unroll
         for (int i = 0; i < 3 * 8 * 256 / LT; i++) bv[i] = bk[tid + i * LT];
+        if (ACT) return;                             // x comes from the partials (build)
         const size_t e0 = (size_t)xr * a.src_ld + (size_t)(chunk * PW + v) * 8;
         const uint8_t *xb = (const uint8_t *)a.src + e0 * (a.src_bf16 ? 2 : 4);
         xq0 = *(const uint4 *)xb;
         xq1 = *(const uint4 *)(xb + (a.src_bf16 ? 0 : 16));
     };
+    // act_part: x of class (pair p, chunk) is silu(g) * u for the 256
+    // rows chunk*256 .. of pair p, g and u the sums of its gate and up
+    // partials times the rows' scales (the SwiGLU the separate act kernel
+    // does).  Thread (row i, quarter q) sums a quarter of the chunks of both
+    // kinds; the quarters meet in LDS (the tables' space, rebuilt next).
+    auto act_x = [&](int p, int chunk) {
+        const int I = a.nv * 8, nc = a.act_nch;
+        const int i = tid & 255, q = tid >> 8, r = chunk * 256 + i;
+        const int ns = (nc + 3) / 4, c_lo = min(nc, q * ns), c_hi = min(nc, c_lo + ns);
+        const float *pg = a.act_part + (size_t)p * 2 * nc * I + r;
+        float sg = 0.0f, su = 0.0f;
+        for (int cb = c_lo; cb < c_hi; cb += 4) {
+            float gv[4], uv[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int c = cb + k < c_hi ? cb + k : c_lo;
+                gv[k] = pg[(size_t)c * I];
+                uv[k] = pg[(size_t)(nc + c) * I];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (cb + k < c_hi) { sg += gv[k]; su += uv[k]; }
+        }
+        const uint8_t *rec = s_rec[p - p_lo];
+        uint16_t hg = 0, hu = 0;
+        if (rec && tid < 256) {
+            g_u16 *sc = (g_u16 *)(as_global(rec) + a.act_sc_off);
+            hg = sc[r];
+            hu = sc[I + r];
+        }
+        __syncthreads();                             // the old tables' readers are done
+        smem[(q * 256 + i) * 2] = sg;
+        smem[(q * 256 + i) * 2 + 1] = su;
+        __syncthreads();
+        if (tid < 256) {
+            float gg = 0.0f, uu = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) { gg += smem[(k * 256 + i) * 2]; uu += smem[(k * 256 + i) * 2 + 1]; }
+            s_h[i] = rec ? wh_silu_mul(__fmul_rn(gg, wh_f16_scale(hg)), __fmul_rn(uu, wh_f16_scale(hu))) : 0.0f;
+        }
+        __syncthreads();
+    };
     // the tables: books to LDS, then 24 products of 32 codes x 32 positions
     // on the matrix cores (books[code][dim] x x[dim][position])
-    auto build = [&]() {
+    auto build = [&](int t) {
 #pragma unroll
         for (int i = 0; i < 3 * 8 * 256 / LT; i++) sbook[tid + i * LT] = bv[i];
         float xv[8];
-        const uint32_t w8[8] = {xq0.x, xq0.y, xq0.z, xq0.w, xq1.x, xq1.y, xq1.z, xq1.w};
+        if (ACT) {
+            int p, kind, chunk, rb;
+            tm.at(t, p, kind, chunk, rb);
+            act_x(p, chunk);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float lo16 = wh_bf16(w8[i] & 0xffff), hi16 = wh_bf16(w8[i] >> 16);
-            xv[2 * i] = a.src_bf16 ? lo16 : __uint_as_float(w8[2 * i]);
-            xv[2 * i + 1] = a.src_bf16 ? hi16 : __uint_as_float(w8[2 * i + 1]);
+            for (int k = 0; k < 8; k++) xv[k] = s_h[v * 8 + k];
+        } else {
+            const uint32_t w8[8] = {xq0.x, xq0.y, xq0.z, xq0.w, xq1.x, xq1.y, xq1.z, xq1.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float lo16 = wh_bf16(w8[i] & 0xffff), hi16 = wh_bf16(w8[i] >> 16);
+                xv[2 * i] = a.src_bf16 ? lo16 : __uint_as_float(w8[2 * i]);
+                xv[2 * i + 1] = a.src_bf16 ? hi16 : __uint_as_float(w8[2 * i + 1]);
+            }
         }
         __syncthreads();
         table_mfma(smem, sbook, xv, wv, v, h);
@@ -327,7 +380,7 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
     bool inA = true;                                 // the next tile is in A
     where(t, src, outA, liveA);
     load_tile(A, src, loff);
-    build();
+    build(t0);
 
     for (int lo = t0; lo < t1;) {
         int p, kind, chunk, rb;
@@ -358,7 +411,7 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
             tm.at(lo, pn, k_, c_, r_);
             build_loads(lo, s_xr[pn - p_lo]);
             __syncthreads();                         // the old tables are done with
-            build();
+            build(lo);
         }
     }
     if (unbound) atomicOr(a.err, 1);
@@ -369,13 +422,20 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
 __global__ void __launch_bounds__(LT)
 k_vq_gate_up(whip_vq_args a, int nch, int span, int tiles, int per_wg, int shares)
 {
-    vq_lanes_body(a, nch, span, tiles, per_wg, shares);
+    vq_lanes_body<false>(a, nch, span, tiles, per_wg, shares);
 }
 
 __global__ void __launch_bounds__(LT)
 k_vq_down(whip_vq_args a, int nch, int span, int tiles, int per_wg, int shares)
 {
-    vq_lanes_body(a, nch, span, tiles, per_wg, shares);
+    vq_lanes_body<false>(a, nch, span, tiles, per_wg, shares);
+}
+
+// The down pass with SwiGLU of the gate/up partials in its table build.
+__global__ void __launch_bounds__(LT)
+k_vq_act_down(whip_vq_args a, int nch, int span, int tiles, int per_wg, int shares)
+{
+    vq_lanes_body<true>(a, nch, span, tiles, per_wg, shares);
 }
 
 extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
@@ -388,6 +448,8 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
         a->P < 1 || a->rsplit < 1 || a->rsplit > rows || (span > 1 && (span != a->P || span > SPAN_MAX)))
         return (int)hipErrorInvalidValue;
     const int nch = whip_vq_chunks(a->nv);
+    if (a->act_part && (!(WH_LANES && a->nv % PW == 0) || a->act_nch < 1 || a->kinds != 1 || span > 1))
+        return (int)hipErrorInvalidValue;
     if (WH_LANES && a->nv % PW == 0) {
         // 16-byte aligned tiles (the kernel's 128-bit loads)
         if (a->idx_off[0] % 16 || a->idx_off[1] % 16) return (int)hipErrorInvalidValue;
@@ -422,6 +484,9 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
         }
         if (a->kinds == 2)
             hipLaunchKernelGGL(k_vq_gate_up, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
+                               (int)per_wg, (int)shares);
+        else if (a->act_part)
+            hipLaunchKernelGGL(k_vq_act_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
                                (int)per_wg, (int)shares);
         else
             hipLaunchKernelGGL(k_vq_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,

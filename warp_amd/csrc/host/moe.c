@@ -544,10 +544,15 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     }
     CK((hipError_t)whip_vq_apply(&a, s));
     MARK(3);
-    CK((hipError_t)whip_vq_act(m->d_recs, m->pair_exp, P, m->part_gu, m->nch_gu, I, m->off_sc,
-                               m->h, s));
+    /* the down kernel reduces the gate/up partials and applies SwiGLU in its
+     * table build when it runs positions across lanes; else a separate pass */
+    const int act_fused = m->nv_d % 32 == 0;
+    if (!act_fused)
+        CK((hipError_t)whip_vq_act(m->d_recs, m->pair_exp, P, m->part_gu, m->nch_gu, I, m->off_sc,
+                                   m->h, s));
     MARK(4);
     a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb + 6;
+    if (act_fused) { a.act_part = m->part_gu; a.act_nch = m->nch_gu; a.act_sc_off = m->off_sc; }
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
     a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
     a.span = 0;
