@@ -141,6 +141,7 @@ extern "C" int whip_sort_pairs(const int32_t *ids, const float *w, int T, int K,
 #define PF_THREADS 512
 #define PF_KC 64                     // k per LDS chunk
 #define PF_ALD (PF_KC + 8)           // A row stride in halves (144 B: rows fall on different banks)
+#define PF_BIG 64                    // expert segments this long take the register-tiled kernel
 
 enum { DEC_F32 = 0, DEC_Q8 = 2, DEC_Q4 = 3, DEC_VQ = 4 };
 
@@ -172,6 +173,7 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
     const int n_seg = a.seg_off ? a.seg_off[seg + 1] - s0 : a.rows;
     const int r0 = blockIdx.z * (MT * 32);           // this workgroup's rows of the segment
     if (r0 >= n_seg) return;
+    if (DEC == DEC_VQ && MT == 4 && a.seg_off && n_seg >= PF_BIG) return;   // long segments: k_pf_gemm4
     const int mrows = min(MT * 32, n_seg - r0);
     const int kind = EPI == 0 ? wave >> 2 : 0;
     const int ncol = blockIdx.x * (EPI == 0 ? 128 : 256) + (EPI == 0 ? (wave & 3) : wave) * 32 + (lane & 31);
@@ -386,6 +388,220 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
     if (bad) atomicOr(a.err, ERR_RANGE);
 }
 
+// Register-tiled variant for the routed experts' segments (VQ3R records,
+// 128-row M blocks): each wavefront holds NT 32-column N fragments over all
+// four 32-row M tiles, so an A fragment read from LDS feeds NT products.
+// EPI 0: a wavefront's fragments are the gate and up rows of the same
+// columns, so SwiGLU happens in registers; EPI 1: NT*32 columns of one
+// matrix.  Per product, LDS delivers 1/NT of an A fragment and a quarter of
+// a B decode (three codebook rows per lane per 16-wide k step, reused over
+// the four M tiles).  NT = 2: eight wavefronts, two per SIMD (about
+// 1.25 KB of LDS per product); NT = 4: four wavefronts (about 1 KB).
+#ifndef PF_NT
+#define PF_NT 2                      // N fragments per wavefront of the register-tiled kernel
+#endif
+template <int NT> struct pf4 { static constexpr int W = 16 / NT, THREADS = 64 * W; };
+
+template <int EPI, int NT>
+__global__ void __launch_bounds__(pf4<NT>::THREADS)
+k_pf_gemm4(whip_pf_args a)
+{
+    constexpr int MT = 4, W = pf4<NT>::W, THREADS = pf4<NT>::THREADS;
+    constexpr int FK = EPI == 0 ? NT / 2 : NT;                      // fragments per kind
+    constexpr int CW = 32 * FK;                                     // a wavefront's columns
+    constexpr int NBOOK = EPI == 0 ? 6 : 3;
+    constexpr int ABUF = MT * 32 * PF_ALD;                          // halves per A buffer
+    __shared__ uint4 cbk[NBOOK * 256];
+    __shared__ __attribute__((aligned(16))) _Float16 As[2 * ABUF];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int seg = a.order ? a.order[blockIdx.y] : (int)blockIdx.y;
+    const int s0 = a.seg_off ? a.seg_off[seg] : 0;
+    const int n_seg = a.seg_off ? a.seg_off[seg + 1] - s0 : a.rows;
+    const int r0 = blockIdx.z * (MT * 32);
+    if (r0 >= n_seg || (a.seg_off && n_seg < PF_BIG)) return;   // short segments: k_pf_gemm
+    const int mrows = min(MT * 32, n_seg - r0);
+
+    int ncol[NT], kj[NT];
+    bool nok[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+        kj[j] = EPI == 0 ? j / FK : 0;
+        ncol[j] = blockIdx.x * (W * CW) + wave * CW + (j % FK) * 32 + (lane & 31);
+        nok[j] = ncol[j] < a.N;
+    }
+    const uint8_t *rec = a.recs[seg];
+    if (rec == nullptr) {                            // unbound expert: zeros + flag
+        for (int m = 0; m < mrows; m++) {
+            const size_t row = (size_t)(s0 + r0 + m);
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                if (!nok[j] || (EPI == 0 && kj[j] != 0)) continue;
+                if (EPI == 0) ((_Float16 *)a.out)[row * a.out_ld + ncol[j]] = (_Float16)0.0f;
+                else ((float *)a.out)[row * a.out_ld + ncol[j]] = 0.0f;
+            }
+        }
+        if (tid == 0) atomicOr(a.err, 1);
+        return;
+    }
+    for (int i = tid; i < NBOOK * 256; i += THREADS)
+        cbk[i] = *(const uint4 *)(a.books16 + ((size_t)(a.cb + i / 256) * 256 + (i & 255)) * 8);
+    const int nv = a.Kd / 8;
+    const size_t rstride = (size_t)nv * 192;
+    g_u8 *ib[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+        const int nc = nok[j] ? ncol[j] : 0;
+        ib[j] = as_global(rec) + a.idx_off[kj[j]] + (size_t)(nc >> 6) * rstride + (nc & 63) * 3;
+    }
+    bool bad = false;
+
+    acc16 acc[NT][MT];
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[j][t][r] = 0.0f;
+
+    // the k loop: chunks kc+1 and kc+2's A rows and B indices are in flight
+    // while chunk kc's products run (two register slots, the loop unrolled by
+    // two so each slot is a fixed set of registers); A double buffered in LDS
+    const int nchunk = a.Kd / PF_KC;
+    constexpr int NITEM = MT * 32 * (PF_KC / 8);
+    constexpr int NA = NITEM / THREADS;
+    size_t abase[NA];
+    bool alive[NA];
+#pragma unroll
+    for (int q = 0; q < NA; q++) {
+        const int it = tid + q * THREADS, m = it >> 3;
+        alive[q] = m < mrows;
+        const int mm = alive[q] ? m : 0;
+        const int row = a.tok ? a.tok[s0 + r0 + mm] : s0 + r0 + mm;
+        abase[q] = (size_t)row * a.x_ld + (it & 7) * 8;
+    }
+    uint4 ra[2][NA][2];
+    uint32_t bw[2][4][NT];
+    auto load = [&](int kc, int sl) {                 // kc clamped: a valid repeat past the end
+        const int kk = kc < nchunk ? kc : nchunk - 1;
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            const size_t e0 = abase[q] + (size_t)kk * PF_KC;
+            if (a.x_mode == 0) {
+                ra[sl][q][0] = *(const uint4 *)((const float *)a.x + e0);
+                ra[sl][q][1] = *(const uint4 *)((const float *)a.x + e0 + 4);
+            } else {
+                ra[sl][q][0] = *(const uint4 *)((const uint16_t *)a.x + e0);
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int k = kk * PF_KC + st * 16 + 8 * (lane >> 5);
+#pragma unroll
+            for (int j = 0; j < NT; j++) bw[sl][st][j] = ld_u32_unaligned((const uint8_t *)(ib[j] + (size_t)(k >> 3) * 192));
+        }
+    };
+    auto chunk = [&](int kc, int sl) {
+        h8 av8[NA];
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            h8 v;
+            if (a.x_mode == 2) {
+                v = as_h8(ra[sl][q][0]);
+            } else if (a.x_mode == 1) {
+                const uint32_t uu[4] = {ra[sl][q][0].x, ra[sl][q][0].y, ra[sl][q][0].z, ra[sl][q][0].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    v[2 * i] = to_h(wh_bf16(uu[i] & 0xffff), bad);
+                    v[2 * i + 1] = to_h(wh_bf16(uu[i] >> 16), bad);
+                }
+            } else {
+                const float f[8] = {__uint_as_float(ra[sl][q][0].x), __uint_as_float(ra[sl][q][0].y),
+                                    __uint_as_float(ra[sl][q][0].z), __uint_as_float(ra[sl][q][0].w),
+                                    __uint_as_float(ra[sl][q][1].x), __uint_as_float(ra[sl][q][1].y),
+                                    __uint_as_float(ra[sl][q][1].z), __uint_as_float(ra[sl][q][1].w)};
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = to_h(f[i], bad);
+            }
+            if (!alive[q])
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = (_Float16)0.0f;
+            av8[q] = v;
+        }
+        uint32_t u[4][NT];
+#pragma unroll
+        for (int st = 0; st < 4; st++)
+#pragma unroll
+            for (int j = 0; j < NT; j++) u[st][j] = bw[sl][st][j];
+        // buffer kc&1 was last read two chunks ago; the barrier of the chunk
+        // between guarantees every wave is done with it
+        _Float16 *Ab = As + (kc & 1) * ABUF;
+#pragma unroll
+        for (int q = 0; q < NA; q++) {
+            const int it = tid + q * THREADS;
+            *(uint4 *)(Ab + (it >> 3) * PF_ALD + (it & 7) * 8) = as_u4(av8[q]);
+        }
+        __syncthreads();
+        load(kc + 2, sl);                             // this slot's next chunk flies now
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            h8 b[NT];
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                const uint4 *bk = cbk + kj[j] * 3 * 256;
+                const h8 c0 = as_h8(bk[u[st][j] & 255]);
+                const h8 c1 = as_h8(bk[256 + ((u[st][j] >> 8) & 255)]);
+                const h8 c2 = as_h8(bk[512 + ((u[st][j] >> 16) & 255)]);
+                b[j] = c0 + (c1 + c2);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                if (t * 32 >= mrows) continue;        // uniform
+                const h8 av = as_h8(*(const uint4 *)(Ab + (t * 32 + (lane & 31)) * PF_ALD + st * 16 + 8 * (lane >> 5)));
+#pragma unroll
+                for (int j = 0; j < NT; j++)
+                    acc[j][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b[j], acc[j][t], 0, 0, 0);
+            }
+        }
+    };
+    load(0, 0);
+    load(1, 1);
+    for (int kc = 0; kc < nchunk; kc += 2) {
+        chunk(kc, 0);
+        if (kc + 1 < nchunk) chunk(kc + 1, 1);        // uniform
+    }
+
+    // epilogue: lane l, register r of tile t holds row t*32 + (r/4)*8 + (l/32)*4 + r%4
+    float rsc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+        g_u16 *sc = (g_u16 *)(as_global(rec) + a.sc_off[kj[j]]);
+        rsc[j] = wh_f16_scale(sc[nok[j] ? ncol[j] : 0]);
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        if (t * 32 >= mrows) continue;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            if (m >= mrows) continue;
+            const size_t row = (size_t)(s0 + r0 + m);
+            if (EPI == 0) {
+#pragma unroll
+                for (int f = 0; f < FK; f++)
+                    if (nok[f]) {
+                        const float h = wh_silu_mul(acc[f][t][r] * rsc[f], acc[FK + f][t][r] * rsc[FK + f]);
+                        ((_Float16 *)a.out)[row * a.out_ld + ncol[f]] = to_h(h, bad);
+                    }
+            } else {
+#pragma unroll
+                for (int j = 0; j < NT; j++)
+                    if (nok[j]) ((float *)a.out)[row * a.out_ld + ncol[j]] = acc[j][t][r] * rsc[j];
+            }
+        }
+    }
+    if (bad) atomicOr(a.err, ERR_RANGE);
+}
+
 extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, int segs, int mblocks,
                             hipStream_t s)
 {
@@ -395,6 +611,16 @@ extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, in
     if (dec != DEC_VQ && a->rowbytes % 16) return (int)hipErrorInvalidValue;
     if (dec == DEC_VQ && a->N % 64) return (int)hipErrorInvalidValue;
     if (a->x_ld % 8) return (int)hipErrorInvalidValue;
+    if (dec == DEC_VQ && mt == 4) {
+        // expert segments of PF_BIG tokens or more: the register-tiled
+        // kernel; shorter ones below (each workgroup checks its segment)
+        const int ntile = pair ? 256 : 512;
+        dim3 grid((a->N + ntile - 1) / ntile, segs, mblocks);
+        if (pair) hipLaunchKernelGGL((k_pf_gemm4<0, PF_NT>), grid, dim3(pf4<PF_NT>::THREADS), 0, s, *a);
+        else hipLaunchKernelGGL((k_pf_gemm4<1, PF_NT>), grid, dim3(pf4<PF_NT>::THREADS), 0, s, *a);
+        const int e = (int)hipGetLastError();
+        if (e || !a->seg_off) return e;
+    }
     const int ntile = pair ? 128 : 256;
     dim3 grid((a->N + ntile - 1) / ntile, segs, mblocks);
 #define PF(D, E)                                                                                 \
