@@ -58,6 +58,7 @@ struct gemv_job {
     int y_ld;
     int wpr, blk0, nblk;
     int rpw;                   // rows per wavefront (one-token kernel)
+    int coh;                   // y read by other workgroups of the launch: device-coherent stores
 };
 struct gemv_pack {
     gemv_job j[3];
@@ -299,7 +300,11 @@ __device__ __forceinline__ void run_job1(const gemv_job &J, int blk, float (*red
     if (part == 0 && lane == 0)
 #pragma unroll
         for (int i = 0; i < RPW; i++)
-            if (r0 + i < J.rows) J.y[r0 + i] = pair ? wh_silu_mul(a0[i], a1[i]) : a0[i];
+            if (r0 + i < J.rows) {
+                const float v = pair ? wh_silu_mul(a0[i], a1[i]) : a0[i];
+                if (J.coh) __hip_atomic_store(J.y + r0 + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else J.y[r0 + i] = v;
+            }
 }
 
 template <int FMT, bool XBF>
@@ -319,7 +324,7 @@ __device__ __forceinline__ void gemv1_block(const gemv_pack &pk, int b, float (*
     J.W0 = SEL(W0); J.W1 = SEL(W1); J.S0 = SEL(S0); J.S1 = SEL(S1); J.rowbytes = SEL(rowbytes);
     J.fmt = SEL(fmt); J.rows = SEL(rows); J.cols = SEL(cols); J.group = SEL(group);
     J.x = SEL(x); J.x_ld = SEL(x_ld); J.x_bf16 = SEL(x_bf16); J.y = SEL(y); J.y_ld = SEL(y_ld);
-    J.wpr = SEL(wpr); J.blk0 = SEL(blk0); J.nblk = SEL(nblk); J.rpw = SEL(rpw);
+    J.wpr = SEL(wpr); J.blk0 = SEL(blk0); J.nblk = SEL(nblk); J.rpw = SEL(rpw); J.coh = SEL(coh);
 #undef SEL
     const int blk = b - J.blk0;
     if (J.fmt == 0) run_fmt1<0, XBF>(J, blk, red);
@@ -356,6 +361,45 @@ k_route_gemv1(whip_route_cfg c, const float *__restrict__ logits, const float *_
     gemv1_block<XBF>(pk, blockIdx.x - 1, red);
 }
 
+// The batch-1 launch with the router as job 0: when the last of the
+// router's blocks has written its logits, that block routes the token
+// (route.h, the pair list and the pairs' records for the expert kernels)
+// while the other jobs' blocks (the shared expert's gate/up) still run.
+// cnt: a device counter, zero between launches (the routing block resets
+// it).
+template <bool XBF, int NPL>
+__global__ void __launch_bounds__(256)
+k_gemv1_route(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, int32_t *__restrict__ ids,
+              float *__restrict__ wout, int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp,
+              float *__restrict__ pair_w, int32_t *__restrict__ tok_pairs,
+              const uint8_t *const *__restrict__ recs, const uint8_t **__restrict__ pair_rec,
+              int *__restrict__ err, int *__restrict__ cnt)
+{
+    __shared__ float red[4][4][2];
+    __shared__ float rl[ROUTE_LDS_FLOATS(NPL)];
+    __shared__ int s_last;
+    gemv1_block<XBF>(pk, blockIdx.x, red);
+    const int nrb = pk.j[0].nblk;                     // the router's blocks come first
+    if ((int)blockIdx.x >= nrb) return;               // uniform
+    // the logits went out device-coherent (through the per-XCD caches);
+    // once they are acknowledged the block counts itself, and the last one
+    // reads them all device-coherent: no cache flush or invalidate
+    __builtin_amdgcn_s_waitcnt(0x0F70);               // vmcnt(0): this thread's stores completed
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nrb - 1;
+    __syncthreads();
+    if (!s_last) return;
+    route_body<NPL, true>(c, pk.j[0].y, bias, 1, 0, threadIdx.x & 63, ids, wout, pair_tok, pair_exp, pair_w,
+                          tok_pairs, recs, pair_rec, err, rl);
+    if (threadIdx.x == 0) *cnt = 0;
+}
+
+extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
+                               int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
+                               int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
+                               int *err, int *cnt, hipStream_t s);
+
 // padded columns of a matrix (whole quantisation groups)
 static int padded_cols(const whip_mat *A)
 {
@@ -383,6 +427,7 @@ static int pack_gemv1(const whip_gemv_job *jobs, int n, gemv_pack &pk)
         J.x_ld = q->x_ld;
         J.rpw = rpw;
         J.wpr = wpr;
+        J.coh = 0;
         const int groups = (J.rows + rpw - 1) / rpw;
         J.nblk = (groups + 4 / wpr - 1) / (4 / wpr);
         J.blk0 = blk;
@@ -494,6 +539,46 @@ extern "C" int whip_route_gemv(const whip_route_cfg *c, const float *logits, con
 #define RG(N, XB) hipLaunchKernelGGL((k_route_gemv1<N, XB>), dim3(blk + 1), dim3(256), 0, s, *c, logits, bias, \
                                      ids, w, pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err, pk)
 #define RGX(N) do { if (job->x_bf16) RG(N, true); else RG(N, false); } while (0)
+    if (E <= 64) RGX(1);
+    else if (E <= 128) RGX(2);
+    else if (E <= 256) RGX(4);
+    else if (E <= 512) RGX(8);
+    else RGX(16);
+#undef RGX
+#undef RG
+    return (int)hipGetLastError();
+}
+
+// One token: router logits (job 0, writing logits[E]) and up to two more
+// batch-1 products in one launch, the token routed by the launch's last
+// router block.
+extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
+                               int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
+                               int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
+                               int *err, int *cnt, hipStream_t s)
+{
+    if (n < 1 || n > 3 || c->E > MAXE || c->E <= 0 || c->K <= 0 || c->K > 64 || c->K > c->E || !pair_exp || !cnt ||
+        jobs[0].A.rows != c->E)
+        return (int)hipErrorInvalidValue;
+    if (c->n_group > 1 && (c->n_group > 64 || c->E % c->n_group || c->topk_group < 1))
+        return (int)hipErrorInvalidValue;
+    for (int i = 0; i < n; i++) {
+        const whip_gemv_job *q = &jobs[i];
+        if (check_mat(&q->A) || (q->B && (q->B->fmt != q->A.fmt || q->B->rows != q->A.rows ||
+                                          q->B->cols != q->A.cols || q->B->group != q->A.group ||
+                                          q->B->rowbytes != q->A.rowbytes)))
+            return (int)hipErrorInvalidValue;
+        if (q->x_ld % 4 || (uintptr_t)q->x % 16 || (q->A.fmt != 0 && q->A.cols % 8) ||
+            q->x_bf16 != jobs[0].x_bf16)
+            return (int)hipErrorInvalidValue;
+    }
+    gemv_pack pk;
+    const int blk = pack_gemv1(jobs, n, pk);
+    pk.j[0].coh = 1;
+    const int E = c->E;
+#define RG(N, XB) hipLaunchKernelGGL((k_gemv1_route<XB, N>), dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w, \
+                                     pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err, cnt)
+#define RGX(N) do { if (jobs[0].x_bf16) RG(N, true); else RG(N, false); } while (0)
     if (E <= 64) RGX(1);
     else if (E <= 128) RGX(2);
     else if (E <= 256) RGX(4);

@@ -189,6 +189,24 @@ typedef struct {
 } whip_bind_args;
 int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err, hipStream_t s);
 
+/* One token: the router (job 0; its y = the logits, E rows) and up to two
+ * more batch-1 products (the shared expert's gate/up) in one launch; the
+ * last router block to finish routes the token as whip_route_gemv's
+ * routing does.  cnt: a device int, zero before the first launch; every
+ * launch leaves it zero. */
+int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
+                    int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
+                    int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
+                    int *err, int *cnt, hipStream_t s);
+
+/* whip_combine with the shared expert's down projection (shd . h_sh[t],
+ * F32/Q8G/Q4G rows) computed in each block for its rows. */
+int whip_combine_sh(const uint8_t *const *recs, const int32_t *pair_exp,
+                    const float *pair_w, const int32_t *tok_pairs, int T, int K,
+                    const float *part_d, int nch, int H, uint32_t sc_off_down,
+                    int skip_zero, const whip_mat *shd, const float *h_sh, float *y,
+                    hipStream_t s);
+
 /* One token's routing (as whip_route with T = 1, plus pair_rec[j] = the
  * selected expert's record) and a batch-1 product that does not depend on
  * it (job; no paired matrix), in one launch. */

@@ -28,6 +28,7 @@
 // token's eight experts fill 256 CUs.
 #include "common.h"
 #include "launch.h"
+#include "gemv_dev.h"
 
 #ifndef WH_VC
 #define WH_VC 8
@@ -653,6 +654,134 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
     r.z = __fadd_rn(o[2], shr ? shr[2] : 0.0f);
     r.w = __fadd_rn(o[3], shr ? shr[3] : 0.0f);
     *(float4 *)(y + (size_t)t * H + r0) = r;
+}
+
+// The combine with the shared expert's down projection computed in the
+// block: wavefront w takes rows w*8 .. w*8+7 of the block's 32, each lane a
+// 16-byte chunk of every row per step against the matching slice of h_sh
+// (fp32), then eight wave sums.
+template <int FMT>
+__device__ __forceinline__ void sh_rows8(const whip_mat &W, const float *x, int row0, int H, float *shs)
+{
+    constexpr int NE = chunk_of<FMT>::NE, NW = xw_of<FMT, false>::N;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int ng = FMT == 0 ? 1 : (W.cols + W.group - 1) / W.group;
+    const int C = (FMT == 0 ? W.cols : ng * W.group) / NE;
+    const uint8_t *Wq = (const uint8_t *)W.q;
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+    for (int k0 = 0; k0 < C; k0 += 64) {            // uniform
+        const int k = k0 + lane, kc = k < C ? k : 0;
+        uint4 xw[NW], wv[8];
+        uint16_t sv[8];
+        load_xs<FMT, false>(x, W.cols, kc, xw);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = min(row0 + w * 8 + i, H - 1);
+            wv[i] = *(const uint4 *)(Wq + (size_t)r * W.rowbytes + (size_t)kc * 16);
+            if (FMT != 0) sv[i] = W.qs[(size_t)r * ng + (size_t)kc * NE / W.group];
+        }
+        if (k < C) {
+            mask_xs<FMT, false>(W.cols, k, xw);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float d = chunk_dot<FMT, false>(wv[i], xw);
+                acc[i] = FMT == 0 ? acc[i] + d : __fmaf_rn(wh_f16_scale(sv[i]), d, acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = wave_sum(acc[i]);
+    if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < 8; i++) shs[w * 8 + i] = acc[i];
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(256)
+k_combine_sh(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
+             const float *__restrict__ pair_w, const int32_t *__restrict__ tok_pairs, int K,
+             const float *__restrict__ part_d, int nch, int H, uint32_t sc_off_down, int skip_zero,
+             whip_mat shd, const float *__restrict__ h_sh, float *__restrict__ y)
+{
+    extern __shared__ float4 cred[];
+    __shared__ float shs[CMB_ROWS];
+    constexpr int G = CMB_ROWS / 4;
+    float4 *csc = cred + K * CMB_SLICES * G;
+    float *cw = (float *)(csc + K * G);
+    int *cl = (int *)(cw + K);
+    const int t = blockIdx.y, tid = threadIdx.x;
+    const int g = tid % G;
+    const int r0 = blockIdx.x * CMB_ROWS + g * 4;
+    const int per = (nch + CMB_SLICES - 1) / CMB_SLICES;
+    sh_rows8<FMT>(shd, h_sh + (size_t)t * shd.cols, blockIdx.x * CMB_ROWS, H, shs);
+    for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G) {
+        const int j = it / CMB_SLICES, sl = it % CMB_SLICES;
+        const int p = tok_pairs[t * K + j];
+        const float wj = pair_w[p];
+        const uint8_t *rec = recs[pair_exp[p]];
+        const bool live = rec && !(skip_zero && wj == 0.0f);
+        uint16_t rs[4] = {0, 0, 0, 0};
+        if (sl == 0 && live && r0 < H) {
+            g_u16 *sc = (g_u16 *)(as_global(rec) + sc_off_down) + r0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) rs[q] = sc[q];
+        }
+        const int c0 = min(nch, sl * per), c1 = min(nch, c0 + per);
+        float4 v = make_float4(0, 0, 0, 0);
+        if (r0 < H && live) v = sum_chunks(part_d + (size_t)p * nch * H + r0, H, c0, c1);
+        cred[(j * CMB_SLICES + sl) * G + g] = v;
+        if (sl == 0) {
+            csc[j * G + g] = make_float4(wh_f16_scale(rs[0]), wh_f16_scale(rs[1]), wh_f16_scale(rs[2]),
+                                         wh_f16_scale(rs[3]));
+            if (g == 0) { cw[j] = wj; cl[j] = live; }
+        }
+    }
+    __syncthreads();
+    if (tid >= G || r0 >= H) return;
+    float o[4] = {0, 0, 0, 0};
+    for (int j = 0; j < K; j++) {                    // combine order
+        if (!cl[j]) continue;
+        const float wj = cw[j];
+        float sum[4] = {0, 0, 0, 0};
+        for (int sl = 0; sl < CMB_SLICES; sl++) {
+            const float4 a = cred[(j * CMB_SLICES + sl) * G + g];
+            sum[0] += a.x; sum[1] += a.y; sum[2] += a.z; sum[3] += a.w;
+        }
+        const float4 sc = csc[j * G + g];
+        o[0] = __fadd_rn(o[0], __fmul_rn(wj, __fmul_rn(sum[0], sc.x)));
+        o[1] = __fadd_rn(o[1], __fmul_rn(wj, __fmul_rn(sum[1], sc.y)));
+        o[2] = __fadd_rn(o[2], __fmul_rn(wj, __fmul_rn(sum[2], sc.z)));
+        o[3] = __fadd_rn(o[3], __fmul_rn(wj, __fmul_rn(sum[3], sc.w)));
+    }
+    float4 r;
+    r.x = __fadd_rn(o[0], shs[g * 4 + 0]);
+    r.y = __fadd_rn(o[1], shs[g * 4 + 1]);
+    r.z = __fadd_rn(o[2], shs[g * 4 + 2]);
+    r.w = __fadd_rn(o[3], shs[g * 4 + 3]);
+    *(float4 *)(y + (size_t)t * H + r0) = r;
+}
+
+extern "C" int whip_combine_sh(const uint8_t *const *recs, const int32_t *pair_exp,
+                               const float *pair_w, const int32_t *tok_pairs, int T, int K,
+                               const float *part_d, int nch, int H, uint32_t sc_off_down,
+                               int skip_zero, const whip_mat *shd, const float *h_sh, float *y,
+                               hipStream_t s)
+{
+    if (H % 4 || K < 1 || K > 64 || shd->rows != H || (uintptr_t)h_sh % 16 || shd->rowbytes % 16 ||
+        (shd->fmt != 0 && (shd->group % 32 || shd->cols % 8)) || (shd->fmt == 0 && shd->cols % 4) ||
+        (shd->fmt != 0 && shd->fmt != 2 && shd->fmt != 3))
+        return (int)hipErrorInvalidValue;
+    dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
+    const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
+#define CS(F) hipLaunchKernelGGL((k_combine_sh<F>), grid, dim3(256), lds, s, recs, pair_exp, pair_w, tok_pairs, K, \
+                                 part_d, nch, H, sc_off_down, skip_zero, *shd, h_sh, y)
+    if (shd->fmt == 3) CS(3);
+    else if (shd->fmt == 2) CS(2);
+    else CS(0);
+#undef CS
+    return (int)hipGetLastError();
 }
 
 extern "C" int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,

@@ -60,6 +60,8 @@ struct waste_hip_moe {
     const uint8_t **pair_rec;    /* [64] records of a T = 1 route's pairs   */
     int pair_rec_ok;             /* pair_rec matches the table (no bind since) */
     int sh_done;                 /* the route's launch ran the shared down  */
+    int sh_in_combine;           /* the combine runs the shared down        */
+    int *rcnt;                   /* the routing launch's block counter (0)  */
     int32_t *d_look;             /* the lookahead's ids                    */
     int prof_on;
     int decode_mode;             /* 1: the persistent experts launch (T == 1) */
@@ -124,7 +126,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
                      m->tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
                      m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->pair_rec,
-                     m->sync };
+                     m->sync, m->rcnt };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0])
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -215,6 +217,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->d_look, 64 * 4);
     rc |= dmalloc((void **)&m->pair_rec, 64 * sizeof(void *));
     rc |= dmalloc((void **)&m->sync, whip_decode1_sync_ints(m->H) * 4);
+    rc |= dmalloc((void **)&m->rcnt, 256);
     if (m->T > m->Td) {
         rc |= dmalloc((void **)&m->pair_pos, (size_t)P * 4);
         rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
@@ -226,7 +229,8 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     if (rc || !m->h_recs) { waste_hip_moe_destroy(m); return WASTE_HIP_ENOMEM; }
     if (hipMemset(m->d_recs, 0, ((size_t)m->E + 1) * sizeof(void *)) != hipSuccess ||
         hipMemset(m->err, 0, 64) != hipSuccess ||
-        hipMemset(m->sync, 0, whip_decode1_sync_ints(m->H) * 4) != hipSuccess) {
+        hipMemset(m->sync, 0, whip_decode1_sync_ints(m->H) * 4) != hipSuccess ||
+        hipMemset(m->rcnt, 0, 256) != hipSuccess) {
         waste_hip_moe_destroy(m);
         return WASTE_HIP_EDEVICE;
     }
@@ -499,12 +503,27 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
         r[nr].A = m->sh[0]; r[nr].B = &m->sh[1]; r[nr].x = x; r[nr].x_ld = H; r[nr].x_bf16 = x_bf16;
         r[nr].y = m->h_sh; r[nr].y_ld = m->SI; nr++;
     }
-    CK((hipError_t)whip_gemv_multi(r, nr, T, s));
-    MARK(1);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
     m->sh_done = 0;
+    m->sh_in_combine = 0;
     m->pair_rec_ok = 0;
+    if (T == 1) {
+        /* one launch: the last router block routes the token (with the pair
+         * list and the pairs' records) while the shared gate/up rows still
+         * stream; the shared down projection then runs in the combine */
+        const int rr = whip_gemv_route(r, nr, &rc, m->d_bias, d_ids, d_w, m->pair_tok, m->pair_exp, m->pair_w,
+                                       m->tok_pairs, m->d_recs, m->pair_rec, m->err, m->rcnt, s);
+        if (rr == 0) {
+            MARK(1);
+            m->pair_rec_ok = 1;
+            m->sh_in_combine = m->has_shared;
+            return 0;
+        }
+        if (rr != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
+    }
+    CK((hipError_t)whip_gemv_multi(r, nr, T, s));
+    MARK(1);
     if (T == 1 && m->has_shared) {
         /* routing and the shared expert's down projection in one launch;
          * the route also writes the pairs' records */
@@ -558,8 +577,21 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     a.span = 0;
     CK((hipError_t)whip_vq_apply(&a, s));
     MARK(5);
-    if (m->has_shared && !m->sh_done)
+    if (m->sh_in_combine) {
+        /* the shared down projection inside the combine's blocks */
+        MARK(6);
+        const int rc = whip_combine_sh(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
+                                       m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1, &m->sh[2], m->h_sh,
+                                       y, s);
+        if (rc == 0) {
+            MARK(7);
+            return prof_end(m);
+        }
+        if (rc != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
+    } else if (m->has_shared && !m->sh_done) {
+        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
+    }
     MARK(6);
     CK((hipError_t)whip_combine(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
                                 m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1,
