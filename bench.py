@@ -334,7 +334,7 @@ def measured_traffic(dom, config, batch):
     """HBM bytes per launch of the dominant kernel, as measured by the two
     rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE, each scaled by a copy of
     known size) whose summary is kept in profiles/; None without one."""
-    kernel = "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_down"
+    kernel = "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_act_down"
     path = os.path.join(ROOT, "profiles", f"{kernel}-{config}-decode-b{batch}-hbm-traffic.md")
     try:
         with open(path) as f:
@@ -438,8 +438,10 @@ def main():
     gbps = bytes_per_step / (ms_per_step * 1e-3) / 1e9
     us_per_token = ms_per_step * 1e3 / B
 
-    # live per-stage timing (HIP events on the forward's stream), a second
-    # pass over the same steps with profiling on
+    # live per-stage timing, a second pass over the same steps with profiling
+    # on: at batch 1 each stage's kernel carries its own start/stop events in
+    # its dispatch (kernel time only, no launch gaps); otherwise events on
+    # the forward's stream around each stage
     for m in layers:
         m.profile(True)
     for i in range(a.warmup, a.warmup + a.steps):
@@ -511,7 +513,7 @@ def main():
         "distinct_experts_per_step": round(u_mean, 2),
         "wall_ms_per_step": round(wall * 1e3 / a.steps, 5),
         "stage_us": {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
-        "roofline": {"bound": "hbm", "kernel": "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_down",
+        "roofline": {"bound": "hbm", "kernel": "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_act_down",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "launch_us": round(dom_ms * 1e3, 2), "algorithmic_bytes": int(dom_bytes)},

@@ -9,7 +9,20 @@
  */
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
+
+// A launch that honours whip_time_next (launch.h): with timing armed, the
+// dispatch records the armed events around the kernel.
+bool whip_take_timing(hipEvent_t *start, hipEvent_t *stop);
+#define WHIP_LAUNCH(K, GRID, BLOCK, LDS, S, ...)                                                 \
+    do {                                                                                       \
+        hipEvent_t e0_, e1_;                                                                   \
+        if (whip_take_timing(&e0_, &e1_))                                                      \
+            hipExtLaunchKernelGGL(K, GRID, BLOCK, LDS, S, e0_, e1_, 0, __VA_ARGS__);           \
+        else                                                                                   \
+            hipLaunchKernelGGL(K, GRID, BLOCK, LDS, S, __VA_ARGS__);                           \
+    } while (0)
 
 #define WH_INLINE __device__ __forceinline__
 

@@ -20,6 +20,23 @@
 #include "launch.h"
 #include "route.h"
 
+static thread_local hipEvent_t t_start = nullptr, t_stop = nullptr;
+
+extern "C" void whip_time_next(hipEvent_t start, hipEvent_t stop)
+{
+    t_start = start;
+    t_stop = stop;
+}
+
+bool whip_take_timing(hipEvent_t *start, hipEvent_t *stop)
+{
+    if (!t_start) return false;
+    *start = t_start;
+    *stop = t_stop;
+    t_start = t_stop = nullptr;
+    return true;
+}
+
 #define TB 4          // tokens sharing one pass over the weights
 #define UNROLL 4      // 16-byte chunks in flight per lane
 
@@ -442,8 +459,8 @@ static int launch_gemv1(const whip_gemv_job *jobs, int n, hipStream_t s)
 {
     gemv_pack pk;
     const int blk = pack_gemv1(jobs, n, pk);
-    if (jobs[0].x_bf16) hipLaunchKernelGGL(k_gemv1<true>, dim3(blk), dim3(256), 0, s, pk);
-    else hipLaunchKernelGGL(k_gemv1<false>, dim3(blk), dim3(256), 0, s, pk);
+    if (jobs[0].x_bf16) WHIP_LAUNCH(k_gemv1<true>, dim3(blk), dim3(256), 0, s, pk);
+    else WHIP_LAUNCH(k_gemv1<false>, dim3(blk), dim3(256), 0, s, pk);
     return (int)hipGetLastError();
 }
 
@@ -576,7 +593,7 @@ extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_rout
     const int blk = pack_gemv1(jobs, n, pk);
     pk.j[0].coh = 1;
     const int E = c->E;
-#define RG(N, XB) hipLaunchKernelGGL((k_gemv1_route<XB, N>), dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w, \
+#define RG(N, XB) WHIP_LAUNCH((k_gemv1_route<XB, N>), dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w, \
                                      pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err, cnt)
 #define RGX(N) do { if (jobs[0].x_bf16) RG(N, true); else RG(N, false); } while (0)
     if (E <= 64) RGX(1);

@@ -15,6 +15,12 @@
 extern "C" {
 #endif
 
+/* Arms kernel timing for the calling thread's next decode launch (the
+ * batch-1 GEMV, the VQ3R apply, the combine): its dispatch records start
+ * and stop (hipExtLaunchKernel's events, taken by the dispatch itself, so
+ * they bracket the kernel and nothing else). */
+void whip_time_next(hipEvent_t start, hipEvent_t stop);
+
 /* bf16 activations to fp32 (exact). */
 int whip_bf16_to_f32(const uint16_t *x, float *y, size_t n, hipStream_t s);
 

@@ -484,13 +484,13 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
             G = (tiles + per_wg - 1) / per_wg;
         }
         if (a->kinds == 2)
-            hipLaunchKernelGGL(k_vq_gate_up, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
+            WHIP_LAUNCH(k_vq_gate_up, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
                                (int)per_wg, (int)shares);
         else if (a->act_part)
-            hipLaunchKernelGGL(k_vq_act_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
+            WHIP_LAUNCH(k_vq_act_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
                                (int)per_wg, (int)shares);
         else
-            hipLaunchKernelGGL(k_vq_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
+            WHIP_LAUNCH(k_vq_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
                                (int)per_wg, (int)shares);
         return (int)hipGetLastError();
     }
@@ -775,7 +775,7 @@ extern "C" int whip_combine_sh(const uint8_t *const *recs, const int32_t *pair_e
         return (int)hipErrorInvalidValue;
     dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
     const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
-#define CS(F) hipLaunchKernelGGL((k_combine_sh<F>), grid, dim3(256), lds, s, recs, pair_exp, pair_w, tok_pairs, K, \
+#define CS(F) WHIP_LAUNCH((k_combine_sh<F>), grid, dim3(256), lds, s, recs, pair_exp, pair_w, tok_pairs, K, \
                                  part_d, nch, H, sc_off_down, skip_zero, *shd, h_sh, y)
     if (shd->fmt == 3) CS(3);
     else if (shd->fmt == 2) CS(2);
@@ -792,8 +792,8 @@ extern "C" int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
     if (H % 4 || K < 1 || K > 64) return (int)hipErrorInvalidValue;
     dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
     const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
-    hipLaunchKernelGGL(k_combine, grid, dim3(256), lds, s,
-                       recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, sh, y);
+    WHIP_LAUNCH(k_combine, grid, dim3(256), lds, s,
+                recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, sh, y);
     return (int)hipGetLastError();
 }
 

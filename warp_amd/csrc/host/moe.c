@@ -67,6 +67,8 @@ struct waste_hip_moe {
     int decode_mode;             /* 1: the persistent experts launch (T == 1) */
     int *sync;                   /* its stage counters (zero between launches) */
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
+    hipEvent_t kev[2 * WASTE_HIP_STAGES];   /* per-stage kernel start/stop   */
+    unsigned ktimed;             /* stages timed by their kernel this forward */
     waste_hip_moe_prof prof;
 };
 
@@ -128,8 +130,10 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->pair_rec,
                      m->sync, m->rcnt };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
-    if (m->ev[0])
+    if (m->ev[0]) {
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
+        for (int i = 0; i < 2 * WASTE_HIP_STAGES; i++) hipEventDestroy(m->kev[i]);
+    }
     if (m->h_sel) hipHostFree(m->h_sel);
     free(m->h_recs);
     free(m);
@@ -411,15 +415,24 @@ static int prof_end(waste_hip_moe *m)
     if (!m->prof_on) return 0;
     CK(hipEventSynchronize(m->ev[WASTE_HIP_STAGES]));
     for (int i = 0; i < WASTE_HIP_STAGES; i++) {
+        /* a stage's kernel, timed by its own dispatch; else the events
+         * around the stage (which also hold the launch gaps) */
         float ms = 0;
-        CK(hipEventElapsedTime(&ms, m->ev[i], m->ev[i + 1]));
+        if (m->ktimed) {
+            if (m->ktimed >> i & 1) CK(hipEventElapsedTime(&ms, m->kev[2 * i], m->kev[2 * i + 1]));
+        } else {
+            CK(hipEventElapsedTime(&ms, m->ev[i], m->ev[i + 1]));
+        }
         m->prof.ms[i] += ms;
     }
+    m->ktimed = 0;
     m->prof.forwards++;
     return 0;
 }
 
 #define MARK(i) do { if (m->prof_on) CK(hipEventRecord(m->ev[i], s)); } while (0)
+/* the next launch of stage i times itself */
+#define KT(i) do { if (m->prof_on) { whip_time_next(m->kev[2 * (i)], m->kev[2 * (i) + 1]); m->ktimed |= 1u << (i); } } while (0)
 
 /* T > Td: moe_chunk (src/model.c:7110-7285) as grouped products on the
  * matrix cores.  Stages as forward(): 0 router (+ shared gate/up), 1
@@ -512,8 +525,10 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
         /* one launch: the last router block routes the token (with the pair
          * list and the pairs' records) while the shared gate/up rows still
          * stream; the shared down projection then runs in the combine */
+        KT(0);
         const int rr = whip_gemv_route(r, nr, &rc, m->d_bias, d_ids, d_w, m->pair_tok, m->pair_exp, m->pair_w,
                                        m->tok_pairs, m->d_recs, m->pair_rec, m->err, m->rcnt, s);
+        if (rr) { whip_time_next(NULL, NULL); m->ktimed = 0; }
         if (rr == 0) {
             MARK(1);
             m->pair_rec_ok = 1;
@@ -561,6 +576,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
         a.span = P;
         a.rsplit = pick_span_split(m->nch_gu * 2, P * (I / 64));
     }
+    if (m->sh_in_combine || m->ktimed) KT(2);
     CK((hipError_t)whip_vq_apply(&a, s));
     MARK(3);
     /* the down kernel reduces the gate/up partials and applies SwiGLU in its
@@ -575,11 +591,13 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
     a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
     a.span = 0;
+    if (m->ktimed && act_fused) KT(4);
     CK((hipError_t)whip_vq_apply(&a, s));
     MARK(5);
     if (m->sh_in_combine) {
         /* the shared down projection inside the combine's blocks */
         MARK(6);
+        KT(6);
         const int rc = whip_combine_sh(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
                                        m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1, &m->sh[2], m->h_sh,
                                        y, s);
@@ -588,11 +606,14 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
             return prof_end(m);
         }
         if (rc != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
+        whip_time_next(NULL, NULL);
+        m->ktimed = 0;
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
     } else if (m->has_shared && !m->sh_done) {
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
     }
     MARK(6);
+    if (m->ktimed) KT(6);
     CK((hipError_t)whip_combine(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
                                 m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1,
                                 m->has_shared ? m->sh_out : NULL, y, s));
@@ -756,9 +777,11 @@ int waste_hip_moe_predict(waste_hip_moe *m, const void *x, int x_bf16, int n, in
 int waste_hip_moe_profile(waste_hip_moe *m, int on)
 {
     if (!m) return WASTE_HIP_EINVAL;
-    if (on && !m->ev[0])
-        for (int i = 0; i <= WASTE_HIP_STAGES; i++)
-            CK(hipEventCreate(&m->ev[i]));
+    if (on && !m->ev[0]) {
+        for (int i = 0; i <= WASTE_HIP_STAGES; i++) CK(hipEventCreate(&m->ev[i]));
+        for (int i = 0; i < 2 * WASTE_HIP_STAGES; i++) CK(hipEventCreate(&m->kev[i]));
+    }
+    m->ktimed = 0;
     memset(&m->prof, 0, sizeof m->prof);
     m->prof_on = on;
     return 0;
