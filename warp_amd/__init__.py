@@ -215,7 +215,9 @@ class MoeLayer:
                                            logits_ptr, stream), "forward")
 
     def set_decode(self, mode):
-        """1: one-launch decode for T == 1 (the default); 0: staged kernels."""
+        """How forward() runs T == 1: 0 the staged kernels (the default), 1 the
+        persistent experts launch, 2 the staged kernels with the shared expert
+        on a second stream beside the routed path."""
         check(self.L.waste_hip_moe_set_decode(self.h, int(mode)), "set_decode")
 
     def status(self, stream=None):

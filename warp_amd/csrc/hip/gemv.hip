@@ -41,6 +41,7 @@ bool whip_take_timing(hipEvent_t *start, hipEvent_t *stop)
 #define UNROLL 4      // 16-byte chunks in flight per lane
 
 #include "gemv_dev.h"
+#include "trace.h"
 
 // n activations starting at element e of token row xr (fp32 or bf16)
 template <int N>
@@ -382,8 +383,11 @@ k_route_gemv1(whip_route_cfg c, const float *__restrict__ logits, const float *_
 // router's blocks has written its logits, that block routes the token
 // (route.h, the pair list and the pairs' records for the expert kernels)
 // while the other jobs' blocks (the shared expert's gate/up) still run.
-// cnt: a device counter, zero between launches (the routing block resets
-// it).
+// Every router block loads what the routing reads besides the logits (the
+// bias, the record table, the exp table) beside its product's loads and
+// keeps it in LDS, so the block that turns out last routes with no other
+// memory round trip than the logits'.  cnt: a device counter, zero between
+// launches (the routing block resets it).
 template <bool XBF, int NPL>
 __global__ void __launch_bounds__(256)
 k_gemv1_route(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, int32_t *__restrict__ ids,
@@ -392,25 +396,62 @@ k_gemv1_route(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, in
               const uint8_t *const *__restrict__ recs, const uint8_t **__restrict__ pair_rec,
               int *__restrict__ err, int *__restrict__ cnt)
 {
+    constexpr int PER = (64 * NPL + 255) / 256;       // table entries per thread
     __shared__ float red[4][4][2];
     __shared__ float rl[ROUTE_LDS_FLOATS(NPL)];
+    __shared__ float s_bias[64 * NPL];
+    __shared__ const uint8_t *s_recs[64 * NPL];
+    __shared__ uint64_t s_etab[32];
     __shared__ int s_last;
-    gemv1_block<XBF>(pk, blockIdx.x, red);
+    WT_SPAN(0, 0);
+    WT_DECL;
+    WT_KEEP(0);
     const int nrb = pk.j[0].nblk;                     // the router's blocks come first
-    if ((int)blockIdx.x >= nrb) return;               // uniform
+    const bool router = (int)blockIdx.x < nrb;        // uniform
+    const int tid = threadIdx.x, E = c.E;
+    float bv[PER];
+    const uint8_t *rv[PER];
+    uint64_t ev = 0;
+    if (router) {
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int e = tid + 256 * i, ec = e < E ? e : 0;
+            bv[i] = bias ? bias[ec] : 0.0f;
+            rv[i] = recs[ec];
+        }
+        ev = wh_exp_tab[tid & 31];
+    }
+    gemv1_block<XBF>(pk, blockIdx.x, red);
+    WT_SPAN(0, 1);
+    WT_KEEP(1);
+    if (!router) return;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int e = tid + 256 * i;
+        if (e < E) { s_bias[e] = bv[i]; s_recs[e] = rv[i]; }
+    }
+    if (tid < 32) s_etab[tid] = ev;
     // the logits went out device-coherent (through the per-XCD caches);
     // once they are acknowledged the block counts itself, and the last one
     // reads them all device-coherent: no cache flush or invalidate
     __builtin_amdgcn_s_waitcnt(0x0F70);               // vmcnt(0): this thread's stores completed
     __syncthreads();
+    WT_KEEP(2);
     if (threadIdx.x == 0)
         s_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nrb - 1;
     __syncthreads();
+    WT_KEEP(3);
     if (!s_last) return;
-    route_body<NPL, true>(c, pk.j[0].y, bias, 1, 0, threadIdx.x & 63, ids, wout, pair_tok, pair_exp, pair_w,
-                          tok_pairs, recs, pair_rec, err, rl);
+    route_body<NPL, true>(c, pk.j[0].y, bias ? s_bias : nullptr, 1, 0, threadIdx.x & 63, ids, wout, pair_tok,
+                          pair_exp, pair_w, tok_pairs, s_recs, pair_rec, err, rl, s_etab);
     if (threadIdx.x == 0) *cnt = 0;
+    WT_KEEP(4);
+    if (threadIdx.x == 0)                             // the routing block's stages
+        for (int i = 0; i < 5; i++) WT_PUTAT(0, 1, i);
+    WT(0, 2);                                         // the routing block's end
 }
+
+WT_READER(whip_trace_gemv)
 
 extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
                                int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,

@@ -69,8 +69,8 @@ int whip_pairs(const int32_t *ids, const float *w, int T, int K, int E,
  *   part[((p*kinds + k)*nch + c)*M + r] = sum over chunk c's positions of
  *       L_k[v][0][i0] + L_k[v][1][i1] + L_k[v][2][i2]
  * with L_k built in LDS from src[pair_src[p]] and books cb + 3k.
- * span = P (<= 64) declares that every pair reads the same source row:
- * one table then serves all pairs, and rsplit divides the P*M/64 row
+ * span = P (<= 64) declares a one-token launch, every pair reading source
+ * row 0: one table then serves all pairs, and rsplit divides the P*M/64 row
  * blocks of all pairs; span <= 1 splits each pair's M/64 row blocks.
  * part holds P*kinds*nch*M floats plus 64 (a sink for dead stores). */
 typedef struct {
@@ -93,6 +93,12 @@ typedef struct {
     const float *act_part;
     int act_nch;
     uint32_t act_sc_off;
+    /* Gate/up pass of the positions-across-lanes kernel, shd_y set: extra
+     * workgroups of the launch compute shd_y = shd . shd_x (the shared
+     * expert's down projection, shd.rows outputs, fp32 x). */
+    whip_mat shd;
+    const float *shd_x;
+    float *shd_y;
 } whip_vq_args;
 int whip_vq_apply(const whip_vq_args *a, hipStream_t s);
 int whip_vq_chunks(int nv);          /* nch for a given nv                  */

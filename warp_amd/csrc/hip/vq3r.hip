@@ -29,6 +29,7 @@
 #include "common.h"
 #include "launch.h"
 #include "gemv_dev.h"
+#include "trace.h"
 
 #ifndef WH_VC
 #define WH_VC 8
@@ -45,8 +46,8 @@ typedef const uint3 WH_GLOBAL g_uint3;
 
 // Row blocks are numbered over the pairs a workgroup may span: vb = q*nb + rb
 // is row block rb of pair p0 + q.  With span 1 a workgroup owns (a share of)
-// one pair's rows; with span = P every pair reads the same source row (a
-// one-token decode's gate/up), so one table serves all of their rows and a
+// one pair's rows; with span = P every pair reads source row 0 (a one-token
+// decode's gate/up), so one table serves all of their rows and a
 // workgroup's share runs across experts.
 #define SPAN_MAX 64
 #define VQ_THREADS 512
@@ -190,6 +191,56 @@ VQ_KERNEL(k_vq_rows_down)
 
 #include "vq_tile.h"
 
+// The shared expert's down projection, eight rows r0 .. r0+7 per
+// wavefront: each lane a 16-byte chunk of every row per step against the
+// matching slice of x (fp32), then eight wave sums.  Used by the combine
+// (rows of its block) and by the gate/up launch's spare workgroups.
+template <int FMT>
+__device__ __forceinline__ void sh_rows8_acc(const whip_mat &W, const float *x, int r0, int H, int lane,
+                                             float (&acc)[8])
+{
+    constexpr int NE = chunk_of<FMT>::NE, NW = xw_of<FMT, false>::N;
+    const int ng = FMT == 0 ? 1 : (W.cols + W.group - 1) / W.group;
+    const int C = (FMT == 0 ? W.cols : ng * W.group) / NE;
+    const uint8_t *Wq = (const uint8_t *)W.q;
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+    for (int k0 = 0; k0 < C; k0 += 64) {            // uniform
+        const int k = k0 + lane, kc = k < C ? k : 0;
+        uint4 xw[NW], wv[8];
+        uint16_t sv[8];
+        load_xs<FMT, false>(x, W.cols, kc, xw);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = min(r0 + i, H - 1);
+            wv[i] = *(const uint4 *)(Wq + (size_t)r * W.rowbytes + (size_t)kc * 16);
+            if (FMT != 0) sv[i] = W.qs[(size_t)r * ng + (size_t)kc * NE / W.group];
+        }
+        if (k < C) {
+            mask_xs<FMT, false>(W.cols, k, xw);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float d = chunk_dot<FMT, false>(wv[i], xw);
+                acc[i] = FMT == 0 ? acc[i] + d : __fmaf_rn(wh_f16_scale(sv[i]), d, acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = wave_sum(acc[i]);
+}
+
+// rows row0 + 8w .. of the block's wavefront w into shs (LDS)
+template <int FMT>
+__device__ __forceinline__ void sh_rows8(const whip_mat &W, const float *x, int row0, int H, float *shs)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float acc[8];
+    sh_rows8_acc<FMT>(W, x, row0 + w * 8, H, lane, acc);
+    if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < 8; i++) shs[w * 8 + i] = acc[i];
+}
+
 // A workgroup's tiles in table order: t -> (pair, kind, chunk, row block).
 // span: classes (kind, chunk), each over every pair's row blocks; else
 // classes (pair, kind, chunk), each over one pair's row blocks.
@@ -207,9 +258,17 @@ struct tile_map {
 // instead of branches): the hardware counts loads in issue order, and a
 // load on only one side of a branch leaves the compiler unsure how many are
 // in flight, so it would wait for all of them, the prefetched tiles too.
-template <bool ACT>
+//
+// Issue order, so that no wait covers a load it does not need: the pairs'
+// records; then the first class's books and x (SPAN: every pair reads
+// source row 0) or, for ACT, its gate/up partials (summed as they arrive,
+// with the records); then the rows' scales (ACT) and the first two tiles of
+// every wavefront; then the build, which waits only for what came before
+// the tiles.  Two tiles stay in flight per wavefront from there on.
+#define ACT_PF 8                                     // partials per kind a thread prefetches
+template <bool ACT, bool SPAN>
 __device__ __forceinline__ void
-vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, int shares)
+vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
 {
     __shared__ float smem[2 * 256 * 64];             // table A | table B
     __shared__ float sbook[3 * 8 * 256];             // a kind's books, [stage][dim][code]
@@ -218,9 +277,12 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
     __shared__ float s_h[256];                       // x of a class reduced from partials (act_part)
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int v = lane & 31, h = lane >> 5;
+    const int wk = a.kinds == 2 ? 1 : 2;             // trace row of this pass
+    WT_DECL;
+    WT_KEEP(0);
     tile_map tm;
-    tm.span = span; tm.nch = nch; tm.kinds = a.kinds; tm.nb = a.M >> 6;
-    tm.tpc = span ? a.P * tm.nb : tm.nb;
+    tm.span = SPAN; tm.nch = nch; tm.kinds = a.kinds; tm.nb = a.M >> 6;
+    tm.tpc = SPAN ? a.P * tm.nb : tm.nb;
     // shares > 0: workgroup = (class, share), a share never leaves its class
     int t0, t1;
     if (shares > 0) {
@@ -243,12 +305,12 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
     const uint32_t lrow = 32 * h + rho;              // output row in a block
     g_u8 *dummy = as_global((const uint8_t *)a.booksT);
     float *sink = a.part + (size_t)a.P * a.kinds * nch * a.M;
-    int p_lo = 0, p_hi = a.P - 1, u0, u1, u2, p_first;
-    if (!span) {                                     // p_hi - p_lo < SPAN_MAX (host)
+    int p_lo = 0, p_hi = a.P - 1, u0, u1, u2, p_first, chunk_first;
+    if (!SPAN) {                                     // p_hi - p_lo < SPAN_MAX (host)
         tm.at(t0, p_lo, u0, u1, u2);
         tm.at(t1 - 1, p_hi, u0, u1, u2);
     }
-    tm.at(t0, p_first, u0, u1, u2);
+    tm.at(t0, p_first, u0, chunk_first, u2);
 
     auto uni = [](const void *q) -> const uint8_t * {
         const uint64_t u = (uint64_t)q;
@@ -256,9 +318,10 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
         const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
         return (const uint8_t *)(((uint64_t)hi << 32) | lo);
     };
-    // tile t -> uniform bases of its index bytes (or the dummy) and output block
-    auto where = [&](int t, g_u8 *&src, float *&out, bool &live) {
-        if (t >= t1) { src = dummy; out = sink; live = true; return; }
+    // tile t of a class ending at hi -> uniform bases of its index bytes
+    // (or the dummy, past the class) and output block
+    auto where = [&](int t, int hi, g_u8 *&src, float *&out, bool &live) {
+        if (t >= hi) { src = dummy; out = sink; live = true; return; }
         int p, kind, chunk, rb;
         tm.at(t, p, kind, chunk, rb);
         const uint8_t *rec = uni(s_rec[p - p_lo]);
@@ -267,7 +330,74 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
         out = a.part + (((size_t)p * a.kinds + kind) * nch + chunk) * (size_t)a.M + rb * 64;
     };
 
+    // act_part: x of class (pair p, chunk) is silu(g) * u for the 256
+    // rows chunk*256 .. of pair p, g and u the sums of its gate and up
+    // partials times the rows' scales (the SwiGLU the separate act kernel
+    // does).  Thread (row i, quarter q) sums a quarter of the chunks of both
+    // kinds, the first ACT_PF of them with the class's other loads (summed
+    // at once, before any tile is in flight); the quarters meet in LDS (the
+    // tables' space, rebuilt next).
+    // thread = (row a_i, quarter a_q): the quarter and the row's 64-row
+    // group are wavefront-uniform, so every partial address is a scalar
+    // base plus the lane's offset (few vector registers)
+    const int a_q = wv >> 2, a_g = (wv & 3) * 64, a_i = a_g + lane;
+    float sg0 = 0.0f, su0 = 0.0f;                    // sums of the prefetched partials
+    uint16_t hg = 0, hu = 0;
+    auto act_range = [&](int &c_lo, int &c_hi) {
+        const int nc = a.act_nch, ns = (nc + 3) / 4;
+        c_lo = min(nc, a_q * ns);
+        c_hi = min(nc, c_lo + ns);
+    };
+    auto act_loads = [&](int p, int chunk) {
+        const int I = a.nv * 8, nc = a.act_nch;
+        int c_lo, c_hi;
+        act_range(c_lo, c_hi);
+        const float *pgp = a.act_part + (size_t)p * 2 * nc * I + chunk * 256 + a_g;
+        float pg[ACT_PF], pu[ACT_PF];
+#pragma unroll
+        for (int k = 0; k < ACT_PF; k++) {
+            const int c = c_lo + k < c_hi ? c_lo + k : 0;
+            pg[k] = (pgp + (size_t)c * I)[lane];
+            pu[k] = (pgp + (size_t)(nc + c) * I)[lane];
+        }
+        sg0 = su0 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ACT_PF; k++)
+            if (c_lo + k < c_hi) { sg0 += pg[k]; su0 += pu[k]; }
+    };
+    auto act_scales = [&](int p, int chunk) {
+        const int I = a.nv * 8, r0 = wv < 4 ? chunk * 256 + a_g : 0;
+        const uint8_t *rec = uni(s_rec[p - p_lo]);
+        g_u16 *sc = (g_u16 *)(rec ? as_global(rec) + a.act_sc_off : dummy);
+        hg = (sc + (rec ? r0 : 0))[rec ? lane : 0];
+        hu = (sc + (rec ? I + r0 : 0))[rec ? lane : 0];
+    };
+    auto act_x = [&](int p, int chunk) {
+        const int I = a.nv * 8, nc = a.act_nch;
+        int c_lo, c_hi;
+        act_range(c_lo, c_hi);
+        const float *pgp = a.act_part + (size_t)p * 2 * nc * I + chunk * 256 + a_g;
+        float sg = sg0, su = su0;
+        for (int c = c_lo + ACT_PF; c < c_hi; c++) {  // past the prefetched ones (rare)
+            sg += (pgp + (size_t)c * I)[lane];
+            su += (pgp + (size_t)(nc + c) * I)[lane];
+        }
+        const bool live = s_rec[p - p_lo] != nullptr;
+        __syncthreads();                             // the old tables' readers are done
+        smem[(a_q * 256 + a_i) * 2] = sg;
+        smem[(a_q * 256 + a_i) * 2 + 1] = su;
+        __syncthreads();
+        if (wv < 4) {
+            float gg = 0.0f, uu = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; k++) { gg += smem[(k * 256 + a_i) * 2]; uu += smem[(k * 256 + a_i) * 2 + 1]; }
+            s_h[a_i] = live ? wh_silu_mul(__fmul_rn(gg, wh_f16_scale(hg)), __fmul_rn(uu, wh_f16_scale(hu))) : 0.0f;
+        }
+        __syncthreads();
+    };
+
     // the build's loads for the class of tile t: the kind's books and x
+    // (or, for ACT, the class's partials)
     float bv[3 * 8 * 256 / LT];
     uint4 xq0, xq1;
     auto build_loads = [&](int t, int xr) {
@@ -276,167 +406,185 @@ vq_lanes_body(const whip_vq_args &a, int nch, int span, int tiles, int per_wg, i
         const float *bk = a.booksT + (size_t)(a.cb + kind * 3) * 8 * 256;
 #pragma unroll
         for (int i = 0; i < 3 * 8 * 256 / LT; i++) bv[i] = bk[tid + i * LT];
-        if (ACT) return;                             // x comes from the partials (build)
+        if (ACT) {
+            act_loads(p, chunk);
+            return;
+        }
         const size_t e0 = (size_t)xr * a.src_ld + (size_t)(chunk * PW + v) * 8;
         const uint8_t *xb = (const uint8_t *)a.src + e0 * (a.src_bf16 ? 2 : 4);
         xq0 = *(const uint4 *)xb;
         xq1 = *(const uint4 *)(xb + (a.src_bf16 ? 0 : 16));
     };
-    // act_part: x of class (pair p, chunk) is silu(g) * u for the 256
-    // rows chunk*256 .. of pair p, g and u the sums of its gate and up
-    // partials times the rows' scales (the SwiGLU the separate act kernel
-    // does).  Thread (row i, quarter q) sums a quarter of the chunks of both
-    // kinds; the quarters meet in LDS (the tables' space, rebuilt next).
-    auto act_x = [&](int p, int chunk) {
-        const int I = a.nv * 8, nc = a.act_nch;
-        const int i = tid & 255, q = tid >> 8, r = chunk * 256 + i;
-        const int ns = (nc + 3) / 4, c_lo = min(nc, q * ns), c_hi = min(nc, c_lo + ns);
-        const float *pg = a.act_part + (size_t)p * 2 * nc * I + r;
-        float sg = 0.0f, su = 0.0f;
-        for (int cb = c_lo; cb < c_hi; cb += 4) {
-            float gv[4], uv[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int c = cb + k < c_hi ? cb + k : c_lo;
-                gv[k] = pg[(size_t)c * I];
-                uv[k] = pg[(size_t)(nc + c) * I];
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-                if (cb + k < c_hi) { sg += gv[k]; su += uv[k]; }
-        }
-        const uint8_t *rec = s_rec[p - p_lo];
-        uint16_t hg = 0, hu = 0;
-        if (rec && tid < 256) {
-            g_u16 *sc = (g_u16 *)(as_global(rec) + a.act_sc_off);
-            hg = sc[r];
-            hu = sc[I + r];
-        }
-        __syncthreads();                             // the old tables' readers are done
-        smem[(q * 256 + i) * 2] = sg;
-        smem[(q * 256 + i) * 2 + 1] = su;
-        __syncthreads();
-        if (tid < 256) {
-            float gg = 0.0f, uu = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 4; k++) { gg += smem[(k * 256 + i) * 2]; uu += smem[(k * 256 + i) * 2 + 1]; }
-            s_h[i] = rec ? wh_silu_mul(__fmul_rn(gg, wh_f16_scale(hg)), __fmul_rn(uu, wh_f16_scale(hu))) : 0.0f;
-        }
-        __syncthreads();
-    };
-    // the tables: books to LDS, then 24 products of 32 codes x 32 positions
-    // on the matrix cores (books[code][dim] x x[dim][position])
-    auto build = [&](int t) {
+    // The build in two steps.  stage: the books to LDS and the class's x
+    // (converted, or for ACT reduced from the partials) to s_h, both LDS
+    // writes, which the compiler cannot move past the barrier that follows,
+    // so the tiles' loads go out after the build's own have arrived.
+    // tables: 24 products of 32 codes x 32 positions on the matrix cores
+    // (books[code][dim] x x[dim][position]).
+    auto stage = [&](int t) {
 #pragma unroll
         for (int i = 0; i < 3 * 8 * 256 / LT; i++) sbook[tid + i * LT] = bv[i];
-        float xv[8];
         if (ACT) {
             int p, kind, chunk, rb;
             tm.at(t, p, kind, chunk, rb);
-            act_x(p, chunk);
-#pragma unroll
-            for (int k = 0; k < 8; k++) xv[k] = s_h[v * 8 + k];
+            act_x(p, chunk);                         // ends with a barrier
         } else {
             const uint32_t w8[8] = {xq0.x, xq0.y, xq0.z, xq0.w, xq1.x, xq1.y, xq1.z, xq1.w};
+            float xv[8];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float lo16 = wh_bf16(w8[i] & 0xffff), hi16 = wh_bf16(w8[i] >> 16);
                 xv[2 * i] = a.src_bf16 ? lo16 : __uint_as_float(w8[2 * i]);
                 xv[2 * i + 1] = a.src_bf16 ? hi16 : __uint_as_float(w8[2 * i + 1]);
             }
+            if (tid < 32) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) s_h[v * 8 + k] = xv[k];
+            }
+            __syncthreads();
         }
-        __syncthreads();
+    };
+    auto tables = [&]() {
+        float xv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) xv[k] = s_h[v * 8 + k];
         table_mfma(smem, sbook, xv, wv, v, h);
         __syncthreads();
     };
 
-    // prologue.  Round 1: each thread's pair (its expert and source row)
-    // and the first class's source row.  Round 2: the records, the first
-    // build's books and x.  Then the records to LDS, the first tile's
-    // index bytes, and the first build, whose loads were issued before the
-    // tile's and so are waited for without it.
+    // prologue: the records (one load each: the router wrote them, else
+    // through the pair's expert), then the first build's loads
     {
         const int q = p_lo + min(tid, p_hi - p_lo);
         const int32_t *psrc = a.pair_src ? a.pair_src : a.pair_exp;
         const uint8_t *myrec;
-        int xq, xf;
-        if (a.pair_rec) {                           // one load: the router wrote them
+        int xq, xf = 0;
+        if (a.pair_rec) {
             myrec = a.pair_rec[q];
-            xq = psrc[q]; xf = psrc[p_first];
+            xq = psrc[q];
+            if (!(ACT || SPAN)) xf = psrc[p_first];
         } else {
             const int e = a.pair_exp[q];
-            xq = psrc[q]; xf = psrc[p_first];
+            xq = psrc[q];
+            if (!(ACT || SPAN)) xf = psrc[p_first];
             myrec = a.recs[e];
         }
-        const int myxr = a.pair_src ? xq : q, xr0 = a.pair_src ? xf : p_first;
-        build_loads(t0, xr0);
+        const int myxr = a.pair_src ? xq : q;
+        build_loads(t0, (ACT || SPAN) ? 0 : (a.pair_src ? xf : p_first));
         if (tid <= p_hi - p_lo) { s_rec[tid] = myrec; s_xr[tid] = myxr; }
     }
     __syncthreads();
+    if (ACT) act_scales(p_first, chunk_first);
+    stage(t0);
+    WT_KEEP(1);
     int t = t0 + wv;
     tile_buf A, B;
     g_u8 *src;
     float *outA, *outB;
     bool liveA, liveB, unbound = false;
-    bool inA = true;                                 // the next tile is in A
-    where(t, src, outA, liveA);
-    load_tile(A, src, loff);
-    build(t0);
-
     for (int lo = t0; lo < t1;) {
-        int p, kind, chunk, rb;
-        tm.at(lo, p, kind, chunk, rb);
         const int hi = min(t1, (lo / tm.tpc + 1) * tm.tpc);
-        // this wavefront's tiles of the class, the next one always in flight
-        while (t < hi) {
-            float r;
-            if (inA) {
-                where(t + LW, src, outB, liveB);
-                load_tile(B, src, loff);
-                r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
-                outA[lrow] = liveA ? r : 0.0f;
-                unbound |= !liveA;
-            } else {
-                where(t + LW, src, outA, liveA);
-                load_tile(A, src, loff);
-                r = tile_sum(B, smem, bA0, bA1, bB, s0, s1, s2, lane);
-                outB[lrow] = liveB ? r : 0.0f;
-                unbound |= !liveB;
-            }
-            inA = !inA;
-            t += LW;
-        }
-        lo = hi;
-        if (lo < t1) {                               // uniform: the next class
+        if (lo > t0) {                               // uniform: the next class's build inputs
             int pn, k_, c_, r_;
             tm.at(lo, pn, k_, c_, r_);
             build_loads(lo, s_xr[pn - p_lo]);
-            __syncthreads();                         // the old tables are done with
-            build(lo);
+            if (ACT) act_scales(pn, c_);
+            __syncthreads();                         // the old tables and s_h are done with
+            stage(lo);
         }
+        // this wavefront's tiles of the class, two a round: A holds tile t,
+        // B tile t + LW, and after each the tile two ahead goes out into the
+        // buffer it freed (the dummy past the class).  The buffers never
+        // trade roles: that would be a register copy, which waits for the
+        // loads in flight.  The first two go out before the tables.
+#ifndef VQ_ORDER
+#define VQ_ORDER 0
+#endif
+        if (VQ_ORDER == 1) tables();
+        where(t, hi, src, outA, liveA);
+        load_tile(A, src, loff);
+        if (VQ_ORDER == 2) tables();
+        where(t + LW, hi, src, outB, liveB);
+        load_tile(B, src, loff);
+        if (VQ_ORDER == 0) tables();
+        if (lo == t0) WT_KEEP(2);
+        // A counted loop of pairs and an odd tile after it: an exit in the
+        // middle of a round leaves the compiler unsure which loads are in
+        // flight at the loop's head, and it then waits for all of them.
+        const int n = t < hi ? (hi - t + LW - 1) / LW : 0;
+        for (int i = 0; i + 1 < n; i += 2) {
+            float r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
+            outA[lrow] = liveA ? r : 0.0f;
+            unbound |= !liveA;
+            where(t + 2 * LW, hi, src, outA, liveA);
+            load_tile(A, src, loff);
+            r = tile_sum(B, smem, bA0, bA1, bB, s0, s1, s2, lane);
+            outB[lrow] = liveB ? r : 0.0f;
+            unbound |= !liveB;
+            where(t + 3 * LW, hi, src, outB, liveB);
+            load_tile(B, src, loff);
+            t += 2 * LW;
+        }
+        if (n & 1) {
+            const float r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
+            outA[lrow] = liveA ? r : 0.0f;
+            unbound |= !liveA;
+            t += LW;
+        }
+        lo = hi;
     }
+    WT(wk, 4 + wv);
+    if (wv == 0) { WT_PUT(wk, 0); WT_PUT(wk, 1); WT_PUT(wk, 2); }
     if (unbound) atomicOr(a.err, 1);
 }
 
-// Two symbols for one body, so that profiles tell the gate/up pass from the
-// down pass.
-__global__ void __launch_bounds__(LT)
-k_vq_gate_up(whip_vq_args a, int nch, int span, int tiles, int per_wg, int shares)
+// The gate/up launch's workgroups past its tile workgroups (g of NG) run
+// the shared expert's down projection, which needs only the launch before
+// (h_sh), on CUs the tiles leave idle: rows in groups of eight, one group
+// per wavefront at a time.
+template <int FMT>
+__device__ __forceinline__ void shd_role(const whip_vq_args &a, int g, int NG)
 {
-    vq_lanes_body<false>(a, nch, span, tiles, per_wg, shares);
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = a.shd.rows, ngr = (H + 7) / 8;
+    for (int rg = g * LW + wv; rg < ngr; rg += NG * LW) {   // wave-uniform
+        float acc[8];
+        sh_rows8_acc<FMT>(a.shd, a.shd_x, rg * 8, H, lane, acc);
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (rg * 8 + i < H) a.shd_y[rg * 8 + i] = acc[i];
+    }
+}
+
+// Separate symbols, so that profiles tell the gate/up pass from the down
+// pass.  SPAN: one token, every pair reads source row 0.  Workgroups from
+// g_vq on take the shared down projection (a.shd_y set).
+template <bool SPAN>
+__global__ void __launch_bounds__(LT)
+k_vq_gate_up(whip_vq_args a, int nch, int tiles, int per_wg, int shares, int g_vq)
+{
+    if ((int)blockIdx.x >= g_vq) {                   // uniform
+        const int g = blockIdx.x - g_vq, NG = gridDim.x - g_vq;
+        if (a.shd.fmt == 3) shd_role<3>(a, g, NG);
+        else if (a.shd.fmt == 2) shd_role<2>(a, g, NG);
+        else shd_role<0>(a, g, NG);
+        return;
+    }
+    vq_lanes_body<false, SPAN>(a, nch, tiles, per_wg, shares);
 }
 
 __global__ void __launch_bounds__(LT)
-k_vq_down(whip_vq_args a, int nch, int span, int tiles, int per_wg, int shares)
+k_vq_down(whip_vq_args a, int nch, int tiles, int per_wg, int shares)
 {
-    vq_lanes_body<false>(a, nch, span, tiles, per_wg, shares);
+    vq_lanes_body<false, false>(a, nch, tiles, per_wg, shares);
 }
 
 // The down pass with SwiGLU of the gate/up partials in its table build.
 __global__ void __launch_bounds__(LT)
-k_vq_act_down(whip_vq_args a, int nch, int span, int tiles, int per_wg, int shares)
+k_vq_act_down(whip_vq_args a, int nch, int tiles, int per_wg, int shares)
 {
-    vq_lanes_body<true>(a, nch, span, tiles, per_wg, shares);
+    vq_lanes_body<true, false>(a, nch, tiles, per_wg, shares);
 }
 
 extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
@@ -451,6 +599,14 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
     const int nch = whip_vq_chunks(a->nv);
     if (a->act_part && (!(WH_LANES && a->nv % PW == 0) || a->act_nch < 1 || a->kinds != 1 || span > 1))
         return (int)hipErrorInvalidValue;
+    if (a->shd_y) {
+        // the gate/up pass of the tile kernel only; whole 16-byte chunks
+        const whip_mat *d = &a->shd;
+        if (a->kinds != 2 || !(WH_LANES && a->nv % PW == 0) || !a->shd_x || (uintptr_t)a->shd_x % 16 ||
+            d->rows < 1 || d->rowbytes % 16 || (d->fmt != 0 && d->fmt != 2 && d->fmt != 3) ||
+            (d->fmt != 0 && (d->group % 32 || d->cols % 8)) || (d->fmt == 0 && d->cols % 4))
+            return (int)hipErrorInvalidValue;
+    }
     if (WH_LANES && a->nv % PW == 0) {
         // 16-byte aligned tiles (the kernel's 128-bit loads)
         if (a->idx_off[0] % 16 || a->idx_off[1] % 16) return (int)hipErrorInvalidValue;
@@ -483,15 +639,21 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
             per_wg = (long)(SPAN_MAX - 1) * tiles_per_pair;
             G = (tiles + per_wg - 1) / per_wg;
         }
-        if (a->kinds == 2)
-            WHIP_LAUNCH(k_vq_gate_up, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
-                               (int)per_wg, (int)shares);
+        // the shared down projection on the CUs the tiles leave (at least
+        // eight workgroups, which then run where tiles finish first)
+        const long roles = a->shd_y ? (n_cu - G > 8 ? n_cu - G : 8) : 0;
+        if (a->kinds == 2 && sp)
+            WHIP_LAUNCH(k_vq_gate_up<true>, dim3((unsigned)(G + roles)), dim3(LT), 0, s, *a, nch, (int)tiles,
+                        (int)per_wg, (int)shares, (int)G);
+        else if (a->kinds == 2)
+            WHIP_LAUNCH(k_vq_gate_up<false>, dim3((unsigned)(G + roles)), dim3(LT), 0, s, *a, nch, (int)tiles,
+                        (int)per_wg, (int)shares, (int)G);
         else if (a->act_part)
-            WHIP_LAUNCH(k_vq_act_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
-                               (int)per_wg, (int)shares);
+            WHIP_LAUNCH(k_vq_act_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, (int)tiles,
+                        (int)per_wg, (int)shares);
         else
-            WHIP_LAUNCH(k_vq_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, sp, (int)tiles,
-                               (int)per_wg, (int)shares);
+            WHIP_LAUNCH(k_vq_down, dim3((unsigned)G), dim3(LT), 0, s, *a, nch, (int)tiles,
+                        (int)per_wg, (int)shares);
         return (int)hipGetLastError();
     }
     dim3 grid(nch, a->kinds * a->rsplit, span > 1 ? 1 : a->P);
@@ -656,47 +818,6 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
     *(float4 *)(y + (size_t)t * H + r0) = r;
 }
 
-// The combine with the shared expert's down projection computed in the
-// block: wavefront w takes rows w*8 .. w*8+7 of the block's 32, each lane a
-// 16-byte chunk of every row per step against the matching slice of h_sh
-// (fp32), then eight wave sums.
-template <int FMT>
-__device__ __forceinline__ void sh_rows8(const whip_mat &W, const float *x, int row0, int H, float *shs)
-{
-    constexpr int NE = chunk_of<FMT>::NE, NW = xw_of<FMT, false>::N;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int ng = FMT == 0 ? 1 : (W.cols + W.group - 1) / W.group;
-    const int C = (FMT == 0 ? W.cols : ng * W.group) / NE;
-    const uint8_t *Wq = (const uint8_t *)W.q;
-    float acc[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-    for (int k0 = 0; k0 < C; k0 += 64) {            // uniform
-        const int k = k0 + lane, kc = k < C ? k : 0;
-        uint4 xw[NW], wv[8];
-        uint16_t sv[8];
-        load_xs<FMT, false>(x, W.cols, kc, xw);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int r = min(row0 + w * 8 + i, H - 1);
-            wv[i] = *(const uint4 *)(Wq + (size_t)r * W.rowbytes + (size_t)kc * 16);
-            if (FMT != 0) sv[i] = W.qs[(size_t)r * ng + (size_t)kc * NE / W.group];
-        }
-        if (k < C) {
-            mask_xs<FMT, false>(W.cols, k, xw);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float d = chunk_dot<FMT, false>(wv[i], xw);
-                acc[i] = FMT == 0 ? acc[i] + d : __fmaf_rn(wh_f16_scale(sv[i]), d, acc[i]);
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = wave_sum(acc[i]);
-    if (lane == 0)
-#pragma unroll
-        for (int i = 0; i < 8; i++) shs[w * 8 + i] = acc[i];
-}
 
 template <int FMT>
 __global__ void __launch_bounds__(256)
@@ -715,6 +836,7 @@ k_combine_sh(const uint8_t *const *__restrict__ recs, const int32_t *__restrict_
     const int g = tid % G;
     const int r0 = blockIdx.x * CMB_ROWS + g * 4;
     const int per = (nch + CMB_SLICES - 1) / CMB_SLICES;
+    WT_SPAN(3, 0);
     sh_rows8<FMT>(shd, h_sh + (size_t)t * shd.cols, blockIdx.x * CMB_ROWS, H, shs);
     for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G) {
         const int j = it / CMB_SLICES, sl = it % CMB_SLICES;
@@ -761,7 +883,10 @@ k_combine_sh(const uint8_t *const *__restrict__ recs, const int32_t *__restrict_
     r.z = __fadd_rn(o[2], shs[g * 4 + 2]);
     r.w = __fadd_rn(o[3], shs[g * 4 + 3]);
     *(float4 *)(y + (size_t)t * H + r0) = r;
+    WT_SPAN(3, 1);
 }
+
+WT_READER(whip_trace_vq)
 
 extern "C" int whip_combine_sh(const uint8_t *const *recs, const int32_t *pair_exp,
                                const float *pair_w, const int32_t *tok_pairs, int T, int K,
