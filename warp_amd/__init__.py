@@ -216,8 +216,7 @@ class MoeLayer:
 
     def set_decode(self, mode):
         """How forward() runs T == 1: 0 the staged kernels (the default), 1 the
-        persistent experts launch, 2 the staged kernels with the shared expert
-        on a second stream beside the routed path."""
+        persistent experts launch."""
         check(self.L.waste_hip_moe_set_decode(self.h, int(mode)), "set_decode")
 
     def status(self, stream=None):

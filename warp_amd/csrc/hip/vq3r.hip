@@ -497,16 +497,11 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         // buffer it freed (the dummy past the class).  The buffers never
         // trade roles: that would be a register copy, which waits for the
         // loads in flight.  The first two go out before the tables.
-#ifndef VQ_ORDER
-#define VQ_ORDER 0
-#endif
-        if (VQ_ORDER == 1) tables();
         where(t, hi, src, outA, liveA);
         load_tile(A, src, loff);
-        if (VQ_ORDER == 2) tables();
         where(t + LW, hi, src, outB, liveB);
         load_tile(B, src, loff);
-        if (VQ_ORDER == 0) tables();
+        tables();
         if (lo == t0) WT_KEEP(2);
         // A counted loop of pairs and an odd tile after it: an exit in the
         // middle of a round leaves the compiler unsure which loads are in

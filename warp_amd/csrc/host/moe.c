@@ -65,12 +65,6 @@ struct waste_hip_moe {
     int32_t *d_look;             /* the lookahead's ids                    */
     int prof_on;
     int decode_mode;             /* 1: the persistent experts launch (T == 1) */
-    /* decode mode 2: a T == 1 forward runs the shared expert on its own
-     * stream beside the routed path; ev_x orders it after the caller's
-     * work, ev_sh the combine after it */
-    hipStream_t s2;
-    hipEvent_t ev_x, ev_sh;
-    int sh_async;                /* this forward's shared expert is on s2   */
     int *sync;                   /* its stage counters (zero between launches) */
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
     hipEvent_t kev[2 * WASTE_HIP_STAGES];   /* per-stage kernel start/stop   */
@@ -140,9 +134,6 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
         for (int i = 0; i < 2 * WASTE_HIP_STAGES; i++) hipEventDestroy(m->kev[i]);
     }
-    if (m->ev_x) hipEventDestroy(m->ev_x);
-    if (m->ev_sh) hipEventDestroy(m->ev_sh);
-    if (m->s2) hipStreamDestroy(m->s2);
     if (m->h_sel) hipHostFree(m->h_sel);
     free(m->h_recs);
     free(m);
@@ -530,19 +521,6 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
     m->sh_done = 0;
     m->sh_in_combine = 0;
     m->pair_rec_ok = 0;
-    m->sh_async = 0;
-    if (T == 1 && m->has_shared && m->decode_mode == 2 && m->s2 && !m->prof_on) {
-        /* the shared expert's gate/up and down on the second stream, after
-         * what the caller queued before this forward; the router launch
-         * then holds only the router */
-        CK(hipEventRecord(m->ev_x, s));
-        CK(hipStreamWaitEvent(m->s2, m->ev_x, 0));
-        CK((hipError_t)whip_gemv_multi(&r[1], 1, 1, m->s2));
-        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, 1, m->sh_out, NULL, H, m->s2));
-        CK(hipEventRecord(m->ev_sh, m->s2));
-        m->sh_async = 1;
-        nr = 1;
-    }
     if (T == 1) {
         /* one launch: the last router block routes the token (with the pair
          * list and the pairs' records) while the shared gate/up rows still
@@ -554,14 +532,14 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
         if (rr == 0) {
             MARK(1);
             m->pair_rec_ok = 1;
-            m->sh_in_combine = m->has_shared && !m->sh_async;
+            m->sh_in_combine = m->has_shared;
             return 0;
         }
         if (rr != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
     }
     CK((hipError_t)whip_gemv_multi(r, nr, T, s));
     MARK(1);
-    if (T == 1 && m->has_shared && !m->sh_async) {
+    if (T == 1 && m->has_shared) {
         /* routing and the shared expert's down projection in one launch;
          * the route also writes the pairs' records */
         whip_gemv_job j;
@@ -645,8 +623,6 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
         whip_time_next(NULL, NULL);
         m->ktimed = 0;
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
-    } else if (m->sh_async) {
-        CK(hipStreamWaitEvent(s, m->ev_sh, 0));      /* sh_out from the second stream */
     } else if (m->has_shared && !m->sh_done && !sh_in_gu) {
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
     }
@@ -701,7 +677,7 @@ int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
 static int forward_one(waste_hip_moe *m, const void *x, int x_bf16, float *y, int32_t *ids, float *w,
                        float *logits, hipStream_t s)
 {
-    if (m->decode_mode != 1 || m->prof_on || (uintptr_t)x % 16) return 0;
+    if (!m->decode_mode || m->prof_on || (uintptr_t)x % 16) return 0;
     whip_dec1_args a;
     memset(&a, 0, sizeof a);
     a.E = m->E; a.K = m->K; a.H = m->H; a.I = m->I; a.SI = m->SI;
@@ -740,19 +716,7 @@ static int forward_one(waste_hip_moe *m, const void *x, int x_bf16, float *y, in
 
 int waste_hip_moe_set_decode(waste_hip_moe *m, int mode)
 {
-    if (!m || mode < 0 || mode > 2) return WASTE_HIP_EINVAL;
-    if (mode == 2 && !m->s2) {
-        /* default priority, like every stream of this library */
-        if (hipStreamCreateWithFlags(&m->s2, hipStreamNonBlocking) != hipSuccess) {
-            m->s2 = NULL;
-            return WASTE_HIP_EDEVICE;
-        }
-        /* device-scope release: the two streams only exchange device memory */
-        const unsigned fl = hipEventDisableTiming | hipEventReleaseToDevice;
-        if (hipEventCreateWithFlags(&m->ev_x, fl) != hipSuccess ||
-            hipEventCreateWithFlags(&m->ev_sh, fl) != hipSuccess)
-            return WASTE_HIP_EDEVICE;
-    }
+    if (!m || mode < 0 || mode > 1) return WASTE_HIP_EINVAL;
     m->decode_mode = mode;
     return 0;
 }
