@@ -267,165 +267,6 @@ __device__ __forceinline__ int padded_cols_d(const whip_mat &A)
     return A.fmt == 0 ? A.cols : (A.cols + A.group - 1) / A.group * A.group;
 }
 
-// ---- routing by the whole workgroup ----------------------------------------------
-// One token's selection with the engine's semantics (route.h: the same
-// scores, group limit and keys), computed without its K dependent passes:
-// the keys are distinct (the expert id is in the low word), so the expert
-// the engine's pass p picks is the one with exactly p keys above it.  Each
-// expert's rank is counted by DT/E threads over slices of the keys in LDS.
-// The weights are summed for the renormalisation in selection order, as
-// the passes add them.  Every thread calls it; results in s_ids/s_w/s_rec
-// (K entries; ids -1, weights 0, records NULL and err bit 2 when fewer than
-// K experts are candidates).
-struct route_lds {
-    float *sc, *sel;           // [E] scores, biased scores (may share storage)
-    uint64_t *key;             // [E]
-    int *rank;                 // [E]
-    float *g;                  // [64] group scores
-    int *keep;                 // [64]
-    float *wraw;               // [64]
-};
-
-__device__ __forceinline__ void route_wg(const whip_route_cfg &c, float l, float bias_e,
-                                         const uint8_t *const *s_recs, const uint64_t *etab,
-                                         const route_lds &R, int32_t *s_ids, float *s_w,
-                                         const uint8_t **s_rec, int *err)
-{
-    const int tid = threadIdx.x, E = c.E, K = c.K;
-    float sc = 0.0f;
-    if (tid < E) {
-        if (c.score_func == 2) {
-            const float sp = l > 30.0f ? l : log1pf(wh_expf_t(l, etab));
-            sc = __fsqrt_rn(sp);
-        } else if (c.score_func == 0) {
-            sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf_t(-l, etab)));
-        } else {
-            sc = l;
-        }
-        R.sc[tid] = sc;
-    }
-    if (c.score_func == 1) {                          // softmax: max, then the sum in expert order
-        __syncthreads();
-        if (tid < 64) {
-            float mx = -1e30f;
-            for (int e = tid; e < E; e += 64) mx = R.sc[e] > mx ? R.sc[e] : mx;
-            mx = wave_max_f32(mx);
-            if (tid == 0) R.g[0] = mx;
-        }
-        __syncthreads();
-        if (tid < E) {
-            sc = wh_expf_t(__fsub_rn(sc, R.g[0]), etab);
-            R.sc[tid] = sc;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float sum = 0.0f;
-            for (int e = 0; e < E; e++) sum = __fadd_rn(sum, R.sc[e]);
-            R.g[1] = sum;
-        }
-        __syncthreads();
-        if (tid < E) {
-            sc = __fdiv_rn(sc, R.g[1]);
-            R.sc[tid] = sc;
-        }
-    }
-    const float selv = tid < E ? __fadd_rn(sc, bias_e) : NEG_INF;
-    if (tid < E) R.sel[tid] = selv;
-    const int G = c.n_group > 1 ? c.n_group : 1, gs = E / G;
-    if (G > 1 && gs <= 64 && (gs & (gs - 1)) == 0) {
-        // a group's score: the sum of its two largest values above -inf,
-        // merged across the group's lanes (values only)
-        float a = selv, b = NEG_INF;
-        for (int o = 1; o < gs; o <<= 1) {
-            const float pa = __shfl_xor(a, o, 64), pb = __shfl_xor(b, o, 64);
-            const float hi = fmaxf(a, pa), lo = fminf(a, pa);
-            b = fmaxf(lo, fmaxf(b, pb));
-            a = hi;
-        }
-        if (tid < E && tid % gs == 0) R.g[tid / gs] = __fadd_rn(a, gs > 1 ? b : 0.0f);
-    }
-    __syncthreads();
-    TR(13);
-    if (G > 1) {
-        if (!(gs <= 64 && (gs & (gs - 1)) == 0)) {
-            if (tid < G) {
-                float a = NEG_INF, b = NEG_INF;
-                for (int k = tid * gs; k < (tid + 1) * gs; k++) {
-                    const float v = R.sel[k];
-                    if (v > a) { b = a; a = v; }
-                    else if (v > b) b = v;
-                }
-                R.g[tid] = __fadd_rn(a, gs > 1 ? b : 0.0f);
-            }
-            __syncthreads();
-        }
-        if (tid < G) {
-            const float mine = R.g[tid];
-            int rk = 0;
-            for (int k = 0; k < G; k++) {
-                const float o = R.g[k];
-                rk += (o > NEG_INF) && before(o, k, mine, tid);
-            }
-            R.keep[tid] = mine > NEG_INF && rk < c.topk_group;
-        }
-        __syncthreads();
-    }
-    uint64_t key = 0;
-    if (tid < E) {
-        const bool kept = G > 1 ? R.keep[tid / gs] != 0 : true;
-        key = sel_key(kept ? selv : NEG_INF, tid);
-        R.key[tid] = key;
-        R.rank[tid] = 0;
-    }
-    const int nvalid = __syncthreads_count(key != 0);
-    {
-        // DT/E threads per expert, each over a slice of the keys, eight
-        // loads in flight at a time; the lanes of a wavefront hold
-        // consecutive experts and read the same key (one LDS broadcast)
-        const int Q = DT / E, part = tid / E, e = tid % E;   // a wavefront reads one key at a time
-        const int per = (E + Q - 1) / Q, lo = part * per, hi = min(E, lo + per);
-        if (e < E) {
-            const uint64_t mine = R.key[e];
-            int n = 0;
-            int k = lo;
-            for (; k + 8 <= hi; k += 8) {
-                uint64_t q[8];
-#pragma unroll
-                for (int j = 0; j < 8; j++) q[j] = R.key[k + j];
-#pragma unroll
-                for (int j = 0; j < 8; j++) n += q[j] > mine;
-            }
-            for (; k < hi; k++) n += R.key[k] > mine;
-            if (mine && n) atomicAdd(R.rank + e, n);
-        }
-    }
-    __syncthreads();
-    TR(14);
-    if (tid < E && R.key[tid] && R.rank[tid] < K) {
-        const int r = R.rank[tid];
-        s_ids[r] = tid;
-        R.wraw[r] = sc;
-        s_rec[r] = s_recs[tid];
-    }
-    __syncthreads();
-    if (tid < K) {
-        const bool ok = nvalid >= K;
-        float wsum = 0.0f;
-        for (int p = 0; p < K; p++) wsum = __fadd_rn(wsum, R.wraw[p]);
-        float myw = R.wraw[tid];
-        if (ok) {
-            if (c.renorm && K > 1) myw = __fdiv_rn(myw, __fadd_rn(wsum, 1e-20f));
-            myw = __fmul_rn(myw, c.routed_scale);
-        } else {
-            myw = 0.0f;
-            s_ids[tid] = -1;
-            s_rec[tid] = nullptr;
-            if (tid == 0) atomicOr(err, 2);
-        }
-        s_w[tid] = myw;
-    }
-    __syncthreads();
-}
 
 // ---- the launch ----------------------------------------------------------------
 // A stage's tiles split over the workgroups: whole classes of tpc tiles
@@ -625,7 +466,7 @@ __global__ void __launch_bounds__(DT) k_moe_decode1(whip_dec1_args a)
         route_lds R;
         R.sc = s_h; R.sel = s_h; R.key = s_rkey; R.rank = s_rrank;
         R.g = s_rg; R.keep = s_rkeep; R.wraw = s_rwraw;
-        route_wg(a.rc, l, be, s_recs, s_etab, R, s_ids, s_w, s_rec, a.err);
+        route_wg<DT>(a.rc, l, be, s_recs, s_etab, R, s_ids, s_w, s_rec, a.err);
         TR(1);
     };
     if (a.has_shared) {

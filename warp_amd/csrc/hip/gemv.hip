@@ -77,6 +77,8 @@ struct gemv_job {
     int wpr, blk0, nblk;
     int rpw;                   // rows per wavefront (one-token kernel)
     int coh;                   // y read by other workgroups of the launch: device-coherent stores
+    uint64_t *xchg;            // also (epoch << 32 | bits) of y[r] at xchg[r], device-coherent
+    uint32_t epoch;
 };
 struct gemv_pack {
     gemv_job j[3];
@@ -322,6 +324,9 @@ __device__ __forceinline__ void run_job1(const gemv_job &J, int blk, float (*red
                 const float v = pair ? wh_silu_mul(a0[i], a1[i]) : a0[i];
                 if (J.coh) __hip_atomic_store(J.y + r0 + i, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 else J.y[r0 + i] = v;
+                if (J.xchg)
+                    __hip_atomic_store(J.xchg + r0 + i, ((uint64_t)J.epoch << 32) | __float_as_uint(v),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
 }
 
@@ -343,6 +348,7 @@ __device__ __forceinline__ void gemv1_block(const gemv_pack &pk, int b, float (*
     J.fmt = SEL(fmt); J.rows = SEL(rows); J.cols = SEL(cols); J.group = SEL(group);
     J.x = SEL(x); J.x_ld = SEL(x_ld); J.x_bf16 = SEL(x_bf16); J.y = SEL(y); J.y_ld = SEL(y_ld);
     J.wpr = SEL(wpr); J.blk0 = SEL(blk0); J.nblk = SEL(nblk); J.rpw = SEL(rpw); J.coh = SEL(coh);
+    J.xchg = SEL(xchg); J.epoch = SEL(epoch);
 #undef SEL
     const int blk = b - J.blk0;
     if (J.fmt == 0) run_fmt1<0, XBF>(J, blk, red);
@@ -451,12 +457,111 @@ k_gemv1_route(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, in
     WT(0, 2);                                         // the routing block's end
 }
 
+// E <= 256: the same launch without a counter.  Every router block tags
+// its logits with the launch's epoch in xchg (device-coherent); the last
+// router block, which the dispatcher starts after all the others, waits
+// for the E tagged words (each thread its expert's, a bounded wait) and
+// selects with all 256 threads (route_wg's two-level ranks instead of K
+// dependent passes).  A logit that never arrives sets the status's time-out bit and
+// selects nothing.
+#define XWAIT_TICKS 5000000ull         // 50 ms of the 100 MHz constant clock
+template <bool XBF>
+__global__ void __launch_bounds__(256)
+k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, int32_t *__restrict__ ids,
+               float *__restrict__ wout, int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp,
+               float *__restrict__ pair_w, int32_t *__restrict__ tok_pairs,
+               const uint8_t *const *__restrict__ recs, const uint8_t **__restrict__ pair_rec,
+               int *__restrict__ err)
+{
+    __shared__ float red[4][4][2];
+    __shared__ float s_sc[256], s_sel[256];
+    __shared__ uint64_t s_key[256], s_cand[64];
+    __shared__ int s_rank[256];
+    __shared__ float s_g[64], s_wraw[64], s_w[64];
+    __shared__ int s_keep[64];
+    __shared__ int32_t s_ids[64];
+    __shared__ const uint8_t *s_recs[256];
+    __shared__ const uint8_t *s_rec[64];
+    __shared__ uint64_t s_etab[32];
+    WT_SPAN(0, 0);
+    WT_DECL;
+    WT_KEEP(0);
+    const int nrb = pk.j[0].nblk, tid = threadIdx.x, E = c.E, K = c.K;
+    const bool routing = (int)blockIdx.x == nrb - 1;  // uniform
+    // the routing's other inputs, loaded beside the product's
+    float be = 0.0f;
+    const uint8_t *rv = nullptr;
+    uint64_t ev = 0;
+    if (routing) {
+        const int ec = tid < E ? tid : 0;
+        be = bias ? bias[ec] : 0.0f;
+        rv = recs[ec];
+        ev = wh_exp_tab[tid & 31];
+    }
+    gemv1_block<XBF>(pk, blockIdx.x, red);
+    WT_SPAN(0, 1);
+    WT_KEEP(1);
+    if (!routing) return;
+    if (tid < E) s_recs[tid] = rv;
+    if (tid < 32) s_etab[tid] = ev;
+    const uint32_t epoch = pk.j[0].epoch;
+    float l = 0.0f;
+    int late = 0;
+    if (tid < E) {
+        const uint64_t *q = pk.j[0].xchg + tid;
+        uint64_t v = coh_ld(q);
+        if ((uint32_t)(v >> 32) != epoch) {
+            const uint64_t t0 = wall_clock64();
+            do {
+                __builtin_amdgcn_s_sleep(2);
+                v = coh_ld(q);
+            } while ((uint32_t)(v >> 32) != epoch && wall_clock64() - t0 < XWAIT_TICKS);
+            late = (uint32_t)(v >> 32) != epoch;
+        }
+        l = __uint_as_float((uint32_t)v);
+    }
+    if (__syncthreads_or(late)) {
+        if (tid == 0) atomicOr(err, 16);
+        if (tid < K) {
+            ids[tid] = -1; wout[tid] = 0.0f;
+            pair_tok[tid] = 0; pair_exp[tid] = E; pair_w[tid] = 0.0f; tok_pairs[tid] = tid;
+            pair_rec[tid] = nullptr;
+        }
+        return;
+    }
+    WT_KEEP(2);
+#ifdef WH_TRACE
+    wt_keep_[5] = clock64();
+#endif
+    route_lds R;
+    R.sc = s_sc; R.sel = s_sel; R.key = s_key; R.rank = s_rank; R.g = s_g; R.keep = s_keep; R.wraw = s_wraw;
+    R.cand = s_cand;
+    route_wg<256, true>(c, l, be, s_recs, s_etab, R, s_ids, s_w, s_rec, err);
+    WT_KEEP(3);
+#ifdef WH_TRACE
+    wt_keep_[6] = clock64();
+#endif
+    if (tid < K) {
+        const int e = s_ids[tid];
+        ids[tid] = e;
+        wout[tid] = s_w[tid];
+        pair_tok[tid] = 0;
+        pair_exp[tid] = e < 0 ? E : e;               // E: the table's NULL sentinel
+        pair_w[tid] = s_w[tid];
+        tok_pairs[tid] = tid;
+        pair_rec[tid] = s_rec[tid];
+    }
+    WT_KEEP(4);
+    if (tid == 0)
+        for (int i = 0; i < 7; i++) WT_PUTAT(0, 1, i);
+}
+
 WT_READER(whip_trace_gemv)
 
 extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
                                int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
                                int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
-                               int *err, int *cnt, hipStream_t s);
+                               int *err, int *cnt, uint64_t *xchg, uint32_t epoch, hipStream_t s);
 
 // padded columns of a matrix (whole quantisation groups)
 static int padded_cols(const whip_mat *A)
@@ -486,6 +591,8 @@ static int pack_gemv1(const whip_gemv_job *jobs, int n, gemv_pack &pk)
         J.rpw = rpw;
         J.wpr = wpr;
         J.coh = 0;
+        J.xchg = nullptr;
+        J.epoch = 0;
         const int groups = (J.rows + rpw - 1) / rpw;
         J.nblk = (groups + 4 / wpr - 1) / (4 / wpr);
         J.blk0 = blk;
@@ -544,6 +651,9 @@ extern "C" int whip_gemv_multi(const whip_gemv_job *jobs, int n, int T, hipStrea
         J.y = q->y; J.y_ld = q->y_ld;
         J.wpr = waves_per_row(&q->A);
         J.rpw = 1;
+        J.coh = 0;
+        J.xchg = nullptr;
+        J.epoch = 0;
         J.blk0 = blk;
         J.nblk = (J.rows + (4 / J.wpr) - 1) / (4 / J.wpr);
         blk += J.nblk;
@@ -613,10 +723,10 @@ extern "C" int whip_route_gemv(const whip_route_cfg *c, const float *logits, con
 extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
                                int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
                                int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
-                               int *err, int *cnt, hipStream_t s)
+                               int *err, int *cnt, uint64_t *xchg, uint32_t epoch, hipStream_t s)
 {
-    if (n < 1 || n > 3 || c->E > MAXE || c->E <= 0 || c->K <= 0 || c->K > 64 || c->K > c->E || !pair_exp || !cnt ||
-        jobs[0].A.rows != c->E)
+    if (n < 1 || n > 3 || c->E > MAXE || c->E <= 0 || c->K <= 0 || c->K > 64 || c->K > c->E || !pair_exp ||
+        (!cnt && !xchg) || jobs[0].A.rows != c->E)
         return (int)hipErrorInvalidValue;
     if (c->n_group > 1 && (c->n_group > 64 || c->E % c->n_group || c->topk_group < 1))
         return (int)hipErrorInvalidValue;
@@ -632,8 +742,18 @@ extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_rout
     }
     gemv_pack pk;
     const int blk = pack_gemv1(jobs, n, pk);
-    pk.j[0].coh = 1;
     const int E = c->E;
+    if (xchg && epoch && E <= 256 && pair_rec) {
+        pk.j[0].xchg = xchg;
+        pk.j[0].epoch = epoch;
+        if (jobs[0].x_bf16) WHIP_LAUNCH(k_gemv1_xroute<true>, dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w,
+                                        pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err);
+        else WHIP_LAUNCH(k_gemv1_xroute<false>, dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w,
+                         pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err);
+        return (int)hipGetLastError();
+    }
+    if (!cnt) return (int)hipErrorInvalidValue;
+    pk.j[0].coh = 1;
 #define RG(N, XB) WHIP_LAUNCH((k_gemv1_route<XB, N>), dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w, \
                                      pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err, cnt)
 #define RGX(N) do { if (jobs[0].x_bf16) RG(N, true); else RG(N, false); } while (0)

@@ -202,14 +202,17 @@ typedef struct {
 int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err, hipStream_t s);
 
 /* One token: the router (job 0; its y = the logits, E rows) and up to two
- * more batch-1 products (the shared expert's gate/up) in one launch; the
- * last router block to finish routes the token as whip_route_gemv's
- * routing does.  cnt: a device int, zero before the first launch; every
- * launch leaves it zero. */
+ * more batch-1 products (the shared expert's gate/up) in one launch, and
+ * the token routed as whip_route_gemv's routing does.  E <= 256 with xchg
+ * and epoch != 0: the router blocks tag their logits with epoch in xchg
+ * (E 64-bit words, device memory; no other launch may use the same epoch
+ * on it) and the last router block routes once all are tagged.  Otherwise
+ * the last router block to finish routes; cnt: a device int, zero before
+ * the first launch; every launch leaves it zero. */
 int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
                     int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
                     int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
-                    int *err, int *cnt, hipStream_t s);
+                    int *err, int *cnt, uint64_t *xchg, uint32_t epoch, hipStream_t s);
 
 /* whip_combine with the shared expert's down projection (shd . h_sh[t],
  * F32/Q8G/Q4G rows) computed in each block for its rows. */

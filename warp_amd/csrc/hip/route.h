@@ -6,6 +6,7 @@
 #pragma once
 #include "common.h"
 #include "launch.h"
+#include "trace.h"
 
 #define MAXE 1024
 
@@ -116,6 +117,7 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         sc[j] = e < E ? l : 0.0f;
     }
 
+    WT(0, 8);
     if (c.score_func == 1) {
         // max (order-free), then the engine's sum in expert order
         float mx = -1e30f;
@@ -151,6 +153,7 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         sel[j] = e < E ? __fadd_rn(sc[j], bias ? bias[e] : 0.0f) : NEG_INF;
     }
 
+    WT(0, 9);
     if (c.n_group > 1) {
         // a group's score: the sum of its two largest values above -inf
         // (-inf when it has fewer); keep the topk_group groups that come
@@ -218,6 +221,7 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         }
     }
 
+    WT(0, 10);
     uint64_t key[NPL];
 #pragma unroll
     for (int j = 0; j < NPL; j++) key[j] = L * NPL + j < E ? sel_key(sel[j], L * NPL + j) : 0;
@@ -243,6 +247,7 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         wsum = __fadd_rn(wsum, wf);
         if (L == p) { myid = e; myw = wf; }
     }
+    WT(0, 11);
     if (ok) {
         if (c.renorm && K > 1) myw = __fdiv_rn(myw, __fadd_rn(wsum, 1e-20f));
         myw = __fmul_rn(myw, c.routed_scale);
@@ -263,4 +268,244 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
             if (pair_rec) pair_rec[L] = myid < 0 ? nullptr : recs[myid];
         }
     }
+}
+
+// ---- routing by the whole workgroup ----------------------------------------------
+// One token's selection with the engine's semantics (route.h: the same
+// scores, group limit and keys), computed without its K dependent passes:
+// the keys are distinct (the expert id is in the low word), so the expert
+// the engine's pass p picks is the one with exactly p keys above it.  Each
+// expert's rank is counted by NT/E threads over slices of the keys in LDS
+// (NT: the workgroup's threads, at least E).
+// The weights are summed for the renormalisation in selection order, as
+// the passes add them.  Every thread calls it; results in s_ids/s_w/s_rec
+// (K entries; ids -1, weights 0, records NULL and err bit 2 when fewer than
+// K experts are candidates).
+struct route_lds {
+    float *sc, *sel;           // [E] scores, biased scores (may share storage unless TWO)
+    uint64_t *key;             // [E]
+    int *rank;                 // [E]
+    float *g;                  // [64] group scores
+    int *keep;                 // [64]
+    float *wraw;               // [64]
+    uint64_t *cand;            // [64] (TWO only)
+};
+
+// Keys above `key` among the lanes of this lane's segment of the wavefront
+// (seg 1 .. 64 lanes, a power of two, aligned): the segment's keys come to
+// every lane by row rotations (DPP) of its own row of 16 and, for
+// segments past one row, of the rows the lane-swaps bring; the rotations
+// are independent of each other, so they issue back to back.
+template <int R> __device__ __forceinline__ void cnt_rot(uint32_t slo, uint32_t shi, uint64_t key, int i, int seg,
+                                                        bool self, int &n)
+{
+    const uint32_t olo = R ? dpp32<0x120 + R>(slo) : slo, ohi = R ? dpp32<0x120 + R>(shi) : shi;
+    const uint64_t o = ((uint64_t)ohi << 32) | olo;
+    const int j = (i - R) & 15;                      // the source lane's place in its row
+    n += (o > key) & !(self && R == 0) & (seg >= 16 || (j ^ i) < seg);
+}
+__device__ __forceinline__ int seg_rank(uint64_t key, int seg)
+{
+    const int lane = threadIdx.x & 63, i = lane & 15;
+    const bool odd16 = (lane >> 4) & 1, hi32 = lane >= 32;
+    int n = 0;
+    auto row = [&](uint32_t slo, uint32_t shi, bool self) {
+        cnt_rot<0>(slo, shi, key, i, seg, self, n);   cnt_rot<1>(slo, shi, key, i, seg, self, n);
+        cnt_rot<2>(slo, shi, key, i, seg, self, n);   cnt_rot<3>(slo, shi, key, i, seg, self, n);
+        cnt_rot<4>(slo, shi, key, i, seg, self, n);   cnt_rot<5>(slo, shi, key, i, seg, self, n);
+        cnt_rot<6>(slo, shi, key, i, seg, self, n);   cnt_rot<7>(slo, shi, key, i, seg, self, n);
+        cnt_rot<8>(slo, shi, key, i, seg, self, n);   cnt_rot<9>(slo, shi, key, i, seg, self, n);
+        cnt_rot<10>(slo, shi, key, i, seg, self, n);  cnt_rot<11>(slo, shi, key, i, seg, self, n);
+        cnt_rot<12>(slo, shi, key, i, seg, self, n);  cnt_rot<13>(slo, shi, key, i, seg, self, n);
+        cnt_rot<14>(slo, shi, key, i, seg, self, n);  cnt_rot<15>(slo, shi, key, i, seg, self, n);
+    };
+    auto p16 = [&](uint32_t v) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return odd16 ? r[0] : r[1];                  // the same place in the other row of the pair
+    };
+    auto p32 = [&](uint32_t v) {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return hi32 ? r[0] : r[1];                   // the same place in the other half
+    };
+    const uint32_t lo = (uint32_t)key, hi = (uint32_t)(key >> 32);
+    row(lo, hi, true);
+    if (seg >= 32) row(p16(lo), p16(hi), false);     // uniform
+    if (seg >= 64) {
+        const uint32_t lo2 = p32(lo), hi2 = p32(hi);
+        row(lo2, hi2, false);
+        row(p16(lo2), p16(hi2), false);
+    }
+    return n;
+}
+
+// TWO: the ranks in two levels where they fit, for a workgroup too small
+// to split every expert's count over several threads.  Level one: each
+// lane's rank among the lanes of its segment (its group when groups are a
+// power of two of at most 64 experts, else its wavefront), by moving the
+// segment's keys across lanes (seg_rank); a segment's experts of rank
+// below K are the only ones that can be selected.  Level two: one wavefront ranks
+// those candidates (at most 64) the same way.  A key's rank is the number
+// of keys above it either way, so the selection is the same.
+template <int NT, bool TWO = false>
+__device__ __forceinline__ void route_wg(const whip_route_cfg &c, float l, float bias_e,
+                                         const uint8_t *const *s_recs, const uint64_t *etab,
+                                         const route_lds &R, int32_t *s_ids, float *s_w,
+                                         const uint8_t **s_rec, int *err)
+{
+    const int tid = threadIdx.x, E = c.E, K = c.K;
+    float sc = 0.0f;
+    if (tid < E) {
+        if (c.score_func == 2) {
+            const float sp = l > 30.0f ? l : log1pf(wh_expf_t(l, etab));
+            sc = __fsqrt_rn(sp);
+        } else if (c.score_func == 0) {
+            sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf_t(-l, etab)));
+        } else {
+            sc = l;
+        }
+        R.sc[tid] = sc;
+    }
+    if (c.score_func == 1) {                          // softmax: max, then the sum in expert order
+        __syncthreads();
+        if (tid < 64) {
+            float mx = -1e30f;
+            for (int e = tid; e < E; e += 64) mx = R.sc[e] > mx ? R.sc[e] : mx;
+            mx = wave_max_f32(mx);
+            if (tid == 0) R.g[0] = mx;
+        }
+        __syncthreads();
+        if (tid < E) {
+            sc = wh_expf_t(__fsub_rn(sc, R.g[0]), etab);
+            R.sc[tid] = sc;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float sum = 0.0f;
+            for (int e = 0; e < E; e++) sum = __fadd_rn(sum, R.sc[e]);
+            R.g[1] = sum;
+        }
+        __syncthreads();
+        if (tid < E) {
+            sc = __fdiv_rn(sc, R.g[1]);
+            R.sc[tid] = sc;
+        }
+    }
+    WT(0, 12);
+    const float selv = tid < E ? __fadd_rn(sc, bias_e) : NEG_INF;
+    if (tid < E) R.sel[tid] = selv;
+    const int G = c.n_group > 1 ? c.n_group : 1, gs = E / G;
+    if (G > 1 && gs <= 64 && (gs & (gs - 1)) == 0) {
+        // a group's score: the sum of its two largest values above -inf,
+        // merged across the group's lanes (values only)
+        float a = selv, b = NEG_INF;
+        for (int o = 1; o < gs; o <<= 1) {
+            const float pa = __shfl_xor(a, o, 64), pb = __shfl_xor(b, o, 64);
+            const float hi = fmaxf(a, pa), lo = fminf(a, pa);
+            b = fmaxf(lo, fmaxf(b, pb));
+            a = hi;
+        }
+        if (tid < E && tid % gs == 0) R.g[tid / gs] = __fadd_rn(a, gs > 1 ? b : 0.0f);
+    }
+    __syncthreads();
+    if (G > 1) {
+        if (!(gs <= 64 && (gs & (gs - 1)) == 0)) {
+            if (tid < G) {
+                float a = NEG_INF, b = NEG_INF;
+                for (int k = tid * gs; k < (tid + 1) * gs; k++) {
+                    const float v = R.sel[k];
+                    if (v > a) { b = a; a = v; }
+                    else if (v > b) b = v;
+                }
+                R.g[tid] = __fadd_rn(a, gs > 1 ? b : 0.0f);
+            }
+            __syncthreads();
+        }
+        if (tid < G) {
+            const float mine = R.g[tid];
+            int rk = 0;
+            for (int k = 0; k < G; k++) {
+                const float o = R.g[k];
+                rk += (o > NEG_INF) && before(o, k, mine, tid);
+            }
+            R.keep[tid] = mine > NEG_INF && rk < c.topk_group;
+        }
+        __syncthreads();
+    }
+    WT(0, 13);
+    uint64_t key = 0;
+    if (tid < E) {
+        const bool kept = G > 1 ? R.keep[tid / gs] != 0 : true;
+        key = sel_key(kept ? selv : NEG_INF, tid);
+        R.key[tid] = key;
+        R.rank[tid] = 0;
+    }
+    const int seg = (G > 1 && gs <= 64 && (gs & (gs - 1)) == 0) ? gs : 64;
+    const int kc = K < seg ? K : seg, ns = (E + seg - 1) / seg * kc;
+    const bool two = TWO && ns <= 64;                 // uniform
+    if (two && tid < 64) R.cand[tid] = 0;
+    const int nvalid = __syncthreads_count(key != 0);
+    WT(0, 14);
+    if (two) {
+        const int r1 = seg_rank(key, seg);
+        if (tid < E && key && r1 < kc) R.cand[(tid / seg) * kc + r1] = key;
+        __syncthreads();
+        if (tid < 64) {
+            const uint64_t cv = tid < ns ? R.cand[tid] : 0;
+            const uint32_t clo = (uint32_t)cv;
+            const int r2 = seg_rank(cv, 64);
+            if (cv && r2 < K) {
+                const int e = (int)~clo;                 // the key's low word
+                s_ids[r2] = e;
+                R.wraw[r2] = R.sc[e];
+                s_rec[r2] = s_recs[e];
+            }
+        }
+        __syncthreads();
+    } else {
+        // NT/E threads per expert, each over a slice of the keys, eight
+        // loads in flight at a time; the lanes of a wavefront hold
+        // consecutive experts and read the same key (one LDS broadcast)
+        const int Q = NT / E, part = tid / E, e = tid % E;   // a wavefront reads one key at a time
+        const int per = (E + Q - 1) / Q, lo = part * per, hi = min(E, lo + per);
+        if (e < E) {
+            const uint64_t mine = R.key[e];
+            int n = 0;
+            int k = lo;
+            for (; k + 8 <= hi; k += 8) {
+                uint64_t q[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) q[j] = R.key[k + j];
+#pragma unroll
+                for (int j = 0; j < 8; j++) n += q[j] > mine;
+            }
+            for (; k < hi; k++) n += R.key[k] > mine;
+            if (mine && n) atomicAdd(R.rank + e, n);
+        }
+        __syncthreads();
+        if (tid < E && R.key[tid] && R.rank[tid] < K) {
+            const int r = R.rank[tid];
+            s_ids[r] = tid;
+            R.wraw[r] = sc;
+            s_rec[r] = s_recs[tid];
+        }
+        __syncthreads();
+    }
+    WT(0, 15);
+    if (tid < K) {
+        const bool ok = nvalid >= K;
+        float wsum = 0.0f;
+        for (int p = 0; p < K; p++) wsum = __fadd_rn(wsum, R.wraw[p]);
+        float myw = R.wraw[tid];
+        if (ok) {
+            if (c.renorm && K > 1) myw = __fdiv_rn(myw, __fadd_rn(wsum, 1e-20f));
+            myw = __fmul_rn(myw, c.routed_scale);
+        } else {
+            myw = 0.0f;
+            s_ids[tid] = -1;
+            s_rec[tid] = nullptr;
+            if (tid == 0) atomicOr(err, 2);
+        }
+        s_w[tid] = myw;
+    }
+    __syncthreads();
 }

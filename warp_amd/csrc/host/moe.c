@@ -62,6 +62,8 @@ struct waste_hip_moe {
     int sh_done;                 /* the route's launch ran the shared down  */
     int sh_in_combine;           /* the combine runs the shared down        */
     int *rcnt;                   /* the routing launch's block counter (0)  */
+    uint64_t *xchg;              /* [E] its tagged logits (E <= 256)        */
+    uint32_t epoch;              /* the last routing launch's tag            */
     int32_t *d_look;             /* the lookahead's ids                    */
     int prof_on;
     int decode_mode;             /* 1: the persistent experts launch (T == 1) */
@@ -128,7 +130,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
                      m->tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
                      m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->pair_rec,
-                     m->sync, m->rcnt };
+                     m->sync, m->rcnt, m->xchg };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0]) {
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -222,6 +224,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->pair_rec, 64 * sizeof(void *));
     rc |= dmalloc((void **)&m->sync, whip_decode1_sync_ints(m->H) * 4);
     rc |= dmalloc((void **)&m->rcnt, 256);
+    rc |= dmalloc((void **)&m->xchg, (size_t)m->E * 8);
     if (m->T > m->Td) {
         rc |= dmalloc((void **)&m->pair_pos, (size_t)P * 4);
         rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
@@ -234,7 +237,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     if (hipMemset(m->d_recs, 0, ((size_t)m->E + 1) * sizeof(void *)) != hipSuccess ||
         hipMemset(m->err, 0, 64) != hipSuccess ||
         hipMemset(m->sync, 0, whip_decode1_sync_ints(m->H) * 4) != hipSuccess ||
-        hipMemset(m->rcnt, 0, 256) != hipSuccess) {
+        hipMemset(m->rcnt, 0, 256) != hipSuccess || hipMemset(m->xchg, 0, (size_t)m->E * 8) != hipSuccess) {
         waste_hip_moe_destroy(m);
         return WASTE_HIP_EDEVICE;
     }
@@ -526,8 +529,10 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
          * list and the pairs' records) while the shared gate/up rows still
          * stream; the shared down projection then runs in the combine */
         KT(0);
+        if (++m->epoch == 0) m->epoch = 1;           /* 0 is the exchange's initial tag */
         const int rr = whip_gemv_route(r, nr, &rc, m->d_bias, d_ids, d_w, m->pair_tok, m->pair_exp, m->pair_w,
-                                       m->tok_pairs, m->d_recs, m->pair_rec, m->err, m->rcnt, s);
+                                       m->tok_pairs, m->d_recs, m->pair_rec, m->err, m->rcnt, m->xchg,
+                                       m->epoch, s);
         if (rr) { whip_time_next(NULL, NULL); m->ktimed = 0; }
         if (rr == 0) {
             MARK(1);
