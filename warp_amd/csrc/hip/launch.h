@@ -87,12 +87,15 @@ typedef struct {
     int *err;
     const uint8_t *const *pair_rec;  /* [P] the pairs' records, or NULL     */
     /* Down pass from the gate/up partials (positions-across-lanes kernel
-     * only, M of them = nv*8 rows): pair p's x is silu(scale_g * sum of its
-     * act_nch gate partials) * (scale_u * sum of its up partials), the
-     * record's gate|up row scales at act_sc_off; src is then unused. */
+     * only, M of them = nv*8 rows): pair p's x is silu(sum of its act_nch
+     * gate partials) * (sum of its up partials), partials a gate/up launch
+     * with out_sc_off wrote (already scaled); src is then unused. */
     const float *act_part;
     int act_nch;
-    uint32_t act_sc_off;
+    /* Positions-across-lanes kernel, nonzero: every partial of row r of
+     * kind k is multiplied by the record's f16 scale at byte out_sc_off +
+     * 2*(k*M + r) (the gate|up row scales). */
+    uint32_t out_sc_off;
     /* Gate/up pass of the positions-across-lanes kernel, shd_y set: extra
      * workgroups of the launch compute shd_y = shd . shd_x (the shared
      * expert's down projection, shd.rows outputs, fp32 x). */

@@ -320,7 +320,9 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     };
     // tile t of a class ending at hi -> uniform bases of its index bytes
     // (or the dummy, past the class) and output block
-    auto where = [&](int t, int hi, g_u8 *&src, float *&out, bool &live) {
+    // (out_sc_off: and the f16 scales of its 64 rows, else the dummy)
+    auto where = [&](int t, int hi, g_u8 *&src, float *&out, bool &live, g_u16 *&scb) {
+        scb = (g_u16 *)dummy;
         if (t >= hi) { src = dummy; out = sink; live = true; return; }
         int p, kind, chunk, rb;
         tm.at(t, p, kind, chunk, rb);
@@ -328,12 +330,13 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         live = rec != nullptr;
         src = rec ? as_global(rec) + a.idx_off[kind] + (size_t)rb * rstride + (size_t)chunk * PW * 192 : dummy;
         out = a.part + (((size_t)p * a.kinds + kind) * nch + chunk) * (size_t)a.M + rb * 64;
+        if (a.out_sc_off && rec) scb = (g_u16 *)(as_global(rec) + a.out_sc_off) + (size_t)kind * a.M + rb * 64;
     };
 
     // act_part: x of class (pair p, chunk) is silu(g) * u for the 256
     // rows chunk*256 .. of pair p, g and u the sums of its gate and up
-    // partials times the rows' scales (the SwiGLU the separate act kernel
-    // does).  Thread (row i, quarter q) sums a quarter of the chunks of both
+    // partials, which the gate/up launch scaled by their rows' scales (the
+    // SwiGLU the separate act kernel does).  Thread (row i, quarter q) sums a quarter of the chunks of both
     // kinds, the first ACT_PF of them with the class's other loads (summed
     // at once, before any tile is in flight); the quarters meet in LDS (the
     // tables' space, rebuilt next).
@@ -342,7 +345,6 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     // base plus the lane's offset (few vector registers)
     const int a_q = wv >> 2, a_g = (wv & 3) * 64, a_i = a_g + lane;
     float sg0 = 0.0f, su0 = 0.0f;                    // sums of the prefetched partials
-    uint16_t hg = 0, hu = 0;
     auto act_range = [&](int &c_lo, int &c_hi) {
         const int nc = a.act_nch, ns = (nc + 3) / 4;
         c_lo = min(nc, a_q * ns);
@@ -365,13 +367,6 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         for (int k = 0; k < ACT_PF; k++)
             if (c_lo + k < c_hi) { sg0 += pg[k]; su0 += pu[k]; }
     };
-    auto act_scales = [&](int p, int chunk) {
-        const int I = a.nv * 8, r0 = wv < 4 ? chunk * 256 + a_g : 0;
-        const uint8_t *rec = uni(s_rec[p - p_lo]);
-        g_u16 *sc = (g_u16 *)(rec ? as_global(rec) + a.act_sc_off : dummy);
-        hg = (sc + (rec ? r0 : 0))[rec ? lane : 0];
-        hu = (sc + (rec ? I + r0 : 0))[rec ? lane : 0];
-    };
     auto act_x = [&](int p, int chunk) {
         const int I = a.nv * 8, nc = a.act_nch;
         int c_lo, c_hi;
@@ -391,7 +386,7 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             float gg = 0.0f, uu = 0.0f;
 #pragma unroll
             for (int k = 0; k < 4; k++) { gg += smem[(k * 256 + a_i) * 2]; uu += smem[(k * 256 + a_i) * 2 + 1]; }
-            s_h[a_i] = live ? wh_silu_mul(__fmul_rn(gg, wh_f16_scale(hg)), __fmul_rn(uu, wh_f16_scale(hu))) : 0.0f;
+            s_h[a_i] = live ? wh_silu_mul(gg, uu) : 0.0f;
         }
         __syncthreads();
     };
@@ -474,21 +469,22 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         if (tid <= p_hi - p_lo) { s_rec[tid] = myrec; s_xr[tid] = myxr; }
     }
     __syncthreads();
-    if (ACT) act_scales(p_first, chunk_first);
     stage(t0);
     WT_KEEP(1);
     int t = t0 + wv;
     tile_buf A, B;
     g_u8 *src;
+    g_u16 *scb;
     float *outA, *outB;
+    uint16_t scA, scB;                               // the lane's row scale of each tile
     bool liveA, liveB, unbound = false;
+    const bool presc = a.out_sc_off != 0;            // uniform
     for (int lo = t0; lo < t1;) {
         const int hi = min(t1, (lo / tm.tpc + 1) * tm.tpc);
         if (lo > t0) {                               // uniform: the next class's build inputs
             int pn, k_, c_, r_;
             tm.at(lo, pn, k_, c_, r_);
             build_loads(lo, s_xr[pn - p_lo]);
-            if (ACT) act_scales(pn, c_);
             __syncthreads();                         // the old tables and s_h are done with
             stage(lo);
         }
@@ -496,40 +492,49 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         // B tile t + LW, and after each the tile two ahead goes out into the
         // buffer it freed (the dummy past the class).  The buffers never
         // trade roles: that would be a register copy, which waits for the
-        // loads in flight.  The first two go out before the tables.
-        where(t, hi, src, outA, liveA);
+        // loads in flight.  The first two go out before the tables (the
+        // earlier the loads go out the better: measured).
+        where(t, hi, src, outA, liveA, scb);
         load_tile(A, src, loff);
-        where(t + LW, hi, src, outB, liveB);
+        scA = scb[presc ? lrow : 0];
+        where(t + LW, hi, src, outB, liveB, scb);
         load_tile(B, src, loff);
-        tables();
+        scB = scb[presc ? lrow : 0];
         if (lo == t0) WT_KEEP(2);
+        tables();
+        if (lo == t0) WT_KEEP(3);
         // A counted loop of pairs and an odd tile after it: an exit in the
         // middle of a round leaves the compiler unsure which loads are in
         // flight at the loop's head, and it then waits for all of them.
         const int n = t < hi ? (hi - t + LW - 1) / LW : 0;
         for (int i = 0; i + 1 < n; i += 2) {
             float r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
-            outA[lrow] = liveA ? r : 0.0f;
+            r = presc ? __fmul_rn(r, wh_f16_scale(scA)) : r;
+            __builtin_nontemporal_store(liveA ? r : 0.0f, outA + lrow);
             unbound |= !liveA;
-            where(t + 2 * LW, hi, src, outA, liveA);
+            where(t + 2 * LW, hi, src, outA, liveA, scb);
             load_tile(A, src, loff);
+            scA = scb[presc ? lrow : 0];
             r = tile_sum(B, smem, bA0, bA1, bB, s0, s1, s2, lane);
-            outB[lrow] = liveB ? r : 0.0f;
+            r = presc ? __fmul_rn(r, wh_f16_scale(scB)) : r;
+            __builtin_nontemporal_store(liveB ? r : 0.0f, outB + lrow);
             unbound |= !liveB;
-            where(t + 3 * LW, hi, src, outB, liveB);
+            where(t + 3 * LW, hi, src, outB, liveB, scb);
             load_tile(B, src, loff);
+            scB = scb[presc ? lrow : 0];
             t += 2 * LW;
         }
         if (n & 1) {
-            const float r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
-            outA[lrow] = liveA ? r : 0.0f;
+            float r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
+            r = presc ? __fmul_rn(r, wh_f16_scale(scA)) : r;
+            __builtin_nontemporal_store(liveA ? r : 0.0f, outA + lrow);
             unbound |= !liveA;
             t += LW;
         }
         lo = hi;
     }
     WT(wk, 4 + wv);
-    if (wv == 0) { WT_PUT(wk, 0); WT_PUT(wk, 1); WT_PUT(wk, 2); }
+    if (wv == 0) { WT_PUT(wk, 0); WT_PUT(wk, 1); WT_PUT(wk, 2); WT_PUT(wk, 3); }
     if (unbound) atomicOr(a.err, 1);
 }
 
@@ -593,6 +598,8 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
         return (int)hipErrorInvalidValue;
     const int nch = whip_vq_chunks(a->nv);
     if (a->act_part && (!(WH_LANES && a->nv % PW == 0) || a->act_nch < 1 || a->kinds != 1 || span > 1))
+        return (int)hipErrorInvalidValue;
+    if (a->out_sc_off && (!(WH_LANES && a->nv % PW == 0) || a->out_sc_off % 2 || a->act_part))
         return (int)hipErrorInvalidValue;
     if (a->shd_y) {
         // the gate/up pass of the tile kernel only; whole 16-byte chunks

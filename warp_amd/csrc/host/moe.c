@@ -576,6 +576,12 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.kinds = 2; a.M = I; a.nv = m->nv_gu; a.P = P; a.rsplit = m->rsplit_gu;
     a.part = m->part_gu; a.err = m->err;
+    /* the down kernel reduces the gate/up partials and applies SwiGLU in its
+     * table build when both passes run positions across lanes (the gate/up
+     * partials then leave scaled by their rows' scales); else a separate
+     * pass */
+    const int act_fused = m->nv_d % 32 == 0 && m->nv_gu % 32 == 0;
+    a.out_sc_off = act_fused ? m->off_sc : 0;
     if (T == 1 && P <= 64) {
         /* one token: every pair's gate/up table is the same */
         a.span = P;
@@ -598,15 +604,13 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     CK((hipError_t)arc);
     a.shd_x = NULL; a.shd_y = NULL;
     MARK(3);
-    /* the down kernel reduces the gate/up partials and applies SwiGLU in its
-     * table build when it runs positions across lanes; else a separate pass */
-    const int act_fused = m->nv_d % 32 == 0;
+    a.out_sc_off = 0;
     if (!act_fused)
         CK((hipError_t)whip_vq_act(m->d_recs, m->pair_exp, P, m->part_gu, m->nch_gu, I, m->off_sc,
                                    m->h, s));
     MARK(4);
     a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb + 6;
-    if (act_fused) { a.act_part = m->part_gu; a.act_nch = m->nch_gu; a.act_sc_off = m->off_sc; }
+    if (act_fused) { a.act_part = m->part_gu; a.act_nch = m->nch_gu; }
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
     a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
     a.span = 0;
