@@ -42,9 +42,10 @@ extern "C" {
 #define WASTE_HIP_EDEVICE   (-8)   /* a HIP runtime call failed          */
 #define WASTE_HIP_ERANGE    (-9)   /* an fp16 operand of the many-token
                                       path was out of range              */
-#define WASTE_HIP_ETIMEOUT  (-10)  /* a stage of the one-launch decode
-                                      waited too long for another (its
-                                      workgroups were not all resident)  */
+#define WASTE_HIP_ETIMEOUT  (-10)  /* a device-side wait gave up (~50 ms):
+                                      the router launch's wait for the
+                                      logits, or a stage of the one-launch
+                                      decode (mode 1) */
 
 /* Library name and device check.  NULL when no usable gfx950 device. */
 const char *waste_hip_device_name(void);
