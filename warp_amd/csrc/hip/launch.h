@@ -113,7 +113,9 @@ int whip_vq_act(const uint8_t *const *recs, const int32_t *pair_exp, int P,
                 hipStream_t s);
 
 /* y[t*H + i] = sum over token t's pairs (combine order) of
- *   w * (scale_d[i] * sum_c part_d) + sh[t*H + i] (sh may be NULL). */
+ *   w * (scale_d[i] * sum_c part_d) + sh[t*H + i] (sh may be NULL).
+ * sc_off_down 0: part_d is already scaled (a down launch with out_sc_off).
+ * T == 1: the token's pairs are pairs 0 .. K-1 (tok_pairs is not read). */
 int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                  const float *pair_w, const int32_t *tok_pairs, int T, int K,
                  const float *part_d, int nch, int H, uint32_t sc_off_down,

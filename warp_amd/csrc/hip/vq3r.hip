@@ -262,9 +262,11 @@ struct tile_map {
 // Issue order, so that no wait covers a load it does not need: the pairs'
 // records; then the first class's books and x (SPAN: every pair reads
 // source row 0) or, for ACT, its gate/up partials (summed as they arrive,
-// with the records); then the rows' scales (ACT) and the first two tiles of
-// every wavefront; then the build, which waits only for what came before
-// the tiles.  Two tiles stay in flight per wavefront from there on.
+// with the records); then the first two tiles of every wavefront; then the
+// build, which waits only for what came before the tiles.  Two tiles stay
+// in flight per wavefront from there on.  (The small loads the build needs
+// are waited for before the tiles go out: sent together, they queue behind
+// the launch-wide burst of tile loads, which measured slower.)
 #define ACT_PF 8                                     // partials per kind a thread prefetches
 template <bool ACT, bool SPAN>
 __device__ __forceinline__ void
@@ -344,12 +346,12 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     // group are wavefront-uniform, so every partial address is a scalar
     // base plus the lane's offset (few vector registers)
     const int a_q = wv >> 2, a_g = (wv & 3) * 64, a_i = a_g + lane;
-    float sg0 = 0.0f, su0 = 0.0f;                    // sums of the prefetched partials
     auto act_range = [&](int &c_lo, int &c_hi) {
         const int nc = a.act_nch, ns = (nc + 3) / 4;
         c_lo = min(nc, a_q * ns);
         c_hi = min(nc, c_lo + ns);
     };
+    float sg0 = 0.0f, su0 = 0.0f;                    // sums of the prefetched partials
     auto act_loads = [&](int p, int chunk) {
         const int I = a.nv * 8, nc = a.act_nch;
         int c_lo, c_hi;
@@ -599,7 +601,7 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
     const int nch = whip_vq_chunks(a->nv);
     if (a->act_part && (!(WH_LANES && a->nv % PW == 0) || a->act_nch < 1 || a->kinds != 1 || span > 1))
         return (int)hipErrorInvalidValue;
-    if (a->out_sc_off && (!(WH_LANES && a->nv % PW == 0) || a->out_sc_off % 2 || a->act_part))
+    if (a->out_sc_off && (!(WH_LANES && a->nv % PW == 0) || a->out_sc_off % 2))
         return (int)hipErrorInvalidValue;
     if (a->shd_y) {
         // the gate/up pass of the tile kernel only; whole 16-byte chunks
@@ -756,6 +758,47 @@ extern "C" int whip_vq_act(const uint8_t *const *recs, const int32_t *pair_exp, 
 #define CMB_ROWS 32
 #define CMB_SLICES 4
 
+// One (pair j, chunk slice sl) of a combine block: the slice's partial sums
+// of four rows, the rows' scales, the pair's weight and whether it counts.
+// One token (T == 1): pair j is the token's j-th pair (the routing's order),
+// so no load stands before the weight's and the partials'.  sc_off_down 0:
+// the down launch scaled its partials already (no record or scale loads;
+// an unbound expert's partials are zeros).  The loads do not wait for the
+// record: every address is valid.
+__device__ __forceinline__ void
+cmb_gather(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
+           const float *__restrict__ pair_w, const int32_t *__restrict__ tok_pairs, int K,
+           const float *__restrict__ part_d, int nch, int H, uint32_t sc_off_down, int skip_zero, int t, int it,
+           int g, int r0, int per, float4 *cred, float4 *csc, float *cw, int *cl)
+{
+    constexpr int G = CMB_ROWS / 4;
+    const int j = it / CMB_SLICES, sl = it % CMB_SLICES;
+    const int p = gridDim.y == 1 ? j : tok_pairs[t * K + j];
+    const float wj = pair_w[p];
+    const int rr = r0 < H ? r0 : 0;
+    const int c0 = min(nch, sl * per), c1 = min(nch, c0 + per);
+    float4 v = sum_chunks(part_d + (size_t)p * nch * H + rr, H, c0, c1);
+    bool live = !(skip_zero && wj == 0.0f);          // else the pair adds nothing
+    float4 scv = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    if (sc_off_down) {                               // uniform
+        const uint8_t *rec = recs[pair_exp[p]];
+        live = live && rec;
+        uint16_t rs[4] = {0, 0, 0, 0};
+        if (sl == 0 && rec) {
+            g_u16 *sc = (g_u16 *)(as_global(rec) + sc_off_down) + rr;
+#pragma unroll
+            for (int q = 0; q < 4; q++) rs[q] = sc[q];
+        }
+        scv = make_float4(wh_f16_scale(rs[0]), wh_f16_scale(rs[1]), wh_f16_scale(rs[2]), wh_f16_scale(rs[3]));
+    }
+    if (!live || r0 >= H) v = make_float4(0, 0, 0, 0);
+    cred[(j * CMB_SLICES + sl) * G + g] = v;
+    if (sl == 0) {
+        csc[j * G + g] = scv;
+        if (g == 0) { cw[j] = wj; cl[j] = live; }
+    }
+}
+
 __global__ void __launch_bounds__(256)
 k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
           const float *__restrict__ pair_w, const int32_t *__restrict__ tok_pairs, int K,
@@ -772,28 +815,9 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
     const int g = tid % G;
     const int r0 = blockIdx.x * CMB_ROWS + g * 4;
     const int per = (nch + CMB_SLICES - 1) / CMB_SLICES;
-    for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G) {
-        const int j = it / CMB_SLICES, sl = it % CMB_SLICES;
-        const int p = tok_pairs[t * K + j];
-        const float wj = pair_w[p];
-        const uint8_t *rec = recs[pair_exp[p]];
-        const bool live = rec && !(skip_zero && wj == 0.0f);   // else the pair adds nothing
-        uint16_t rs[4] = {0, 0, 0, 0};
-        if (sl == 0 && live && r0 < H) {
-            g_u16 *sc = (g_u16 *)(as_global(rec) + sc_off_down) + r0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) rs[q] = sc[q];
-        }
-        const int c0 = min(nch, sl * per), c1 = min(nch, c0 + per);
-        float4 v = make_float4(0, 0, 0, 0);
-        if (r0 < H && live) v = sum_chunks(part_d + (size_t)p * nch * H + r0, H, c0, c1);
-        cred[(j * CMB_SLICES + sl) * G + g] = v;
-        if (sl == 0) {
-            csc[j * G + g] = make_float4(wh_f16_scale(rs[0]), wh_f16_scale(rs[1]), wh_f16_scale(rs[2]),
-                                         wh_f16_scale(rs[3]));
-            if (g == 0) { cw[j] = wj; cl[j] = live; }
-        }
-    }
+    for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G)
+        cmb_gather(recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, t, it, g, r0,
+                   per, cred, csc, cw, cl);
     __syncthreads();
     if (tid >= G || r0 >= H) return;
     float o[4] = {0, 0, 0, 0};
@@ -840,28 +864,9 @@ k_combine_sh(const uint8_t *const *__restrict__ recs, const int32_t *__restrict_
     const int per = (nch + CMB_SLICES - 1) / CMB_SLICES;
     WT_SPAN(3, 0);
     sh_rows8<FMT>(shd, h_sh + (size_t)t * shd.cols, blockIdx.x * CMB_ROWS, H, shs);
-    for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G) {
-        const int j = it / CMB_SLICES, sl = it % CMB_SLICES;
-        const int p = tok_pairs[t * K + j];
-        const float wj = pair_w[p];
-        const uint8_t *rec = recs[pair_exp[p]];
-        const bool live = rec && !(skip_zero && wj == 0.0f);
-        uint16_t rs[4] = {0, 0, 0, 0};
-        if (sl == 0 && live && r0 < H) {
-            g_u16 *sc = (g_u16 *)(as_global(rec) + sc_off_down) + r0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) rs[q] = sc[q];
-        }
-        const int c0 = min(nch, sl * per), c1 = min(nch, c0 + per);
-        float4 v = make_float4(0, 0, 0, 0);
-        if (r0 < H && live) v = sum_chunks(part_d + (size_t)p * nch * H + r0, H, c0, c1);
-        cred[(j * CMB_SLICES + sl) * G + g] = v;
-        if (sl == 0) {
-            csc[j * G + g] = make_float4(wh_f16_scale(rs[0]), wh_f16_scale(rs[1]), wh_f16_scale(rs[2]),
-                                         wh_f16_scale(rs[3]));
-            if (g == 0) { cw[j] = wj; cl[j] = live; }
-        }
-    }
+    for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G)
+        cmb_gather(recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, t, it, g, r0,
+                   per, cred, csc, cw, cl);
     __syncthreads();
     if (tid >= G || r0 >= H) return;
     float o[4] = {0, 0, 0, 0};

@@ -610,7 +610,11 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
                                    m->h, s));
     MARK(4);
     a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb + 6;
-    if (act_fused) { a.act_part = m->part_gu; a.act_nch = m->nch_gu; }
+    if (act_fused) {
+        a.act_part = m->part_gu; a.act_nch = m->nch_gu;
+        a.out_sc_off = m->off_sc + 4u * (uint32_t)I;  /* the down partials leave scaled too */
+    }
+    const uint32_t cmb_sc = act_fused ? 0u : m->off_sc + 4u * (uint32_t)I;
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
     a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
     a.span = 0;
@@ -622,8 +626,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
         MARK(6);
         KT(6);
         const int rc = whip_combine_sh(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
-                                       m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1, &m->sh[2], m->h_sh,
-                                       y, s);
+                                       m->nch_d, H, cmb_sc, T > 1, &m->sh[2], m->h_sh, y, s);
         if (rc == 0) {
             MARK(7);
             return prof_end(m);
@@ -638,7 +641,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     MARK(6);
     if (m->ktimed) KT(6);
     CK((hipError_t)whip_combine(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
-                                m->nch_d, H, m->off_sc + 4u * (uint32_t)I, T > 1,
+                                m->nch_d, H, cmb_sc, T > 1,
                                 m->has_shared ? m->sh_out : NULL, y, s));
     MARK(7);
     return prof_end(m);
