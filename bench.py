@@ -71,6 +71,20 @@ def build_layers(torch, warp_amd, synth, cfg, n_layers, max_tokens, seed=0):
     return layers, slab, books, rb, (router, bias, sh)
 
 
+def host_cpu():
+    """The host's CPU model and logical CPU count (from /proc/cpuinfo)."""
+    model, n = "unknown", 0
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                n += line.startswith("processor")
+    except OSError:
+        pass
+    return f"{model}, {n} logical CPUs"
+
+
 def cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, budget_s, nthreads):
     """The reference's CPU decode path (the oracle's AVX-512-order C
     restatement, threaded) on the same layer, timed on a bounded sample of
@@ -98,23 +112,28 @@ def cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, budget_s, nthreads):
     out = np.zeros(H, np.float32)
     idx = np.zeros(K, np.int32)
     w = np.zeros(K, np.float32)
-    n, t_used = 0, 0.0
-    first = True
-    for i in range(1 << 20):                   # the sample's tokens, cycled until the budget is spent
-        x = np.ascontiguousarray(xs[i % len(xs)], np.float32)
-        t0 = time.perf_counter()
-        orc.lib.orc_moe_layer_mt(C.byref(m), ptr(x, fp), ptr(out, fp), idx.ctypes.data_as(C.POINTER(C.c_int)),
-                                 ptr(w, fp), nthreads)
-        dt = time.perf_counter() - t0
-        if first:                   # warm caches and the thread pool; not timed
-            first = False
-            continue
-        n += 1
-        t_used += dt
-        if t_used >= budget_s and n >= 3:
-            break
+
+    def timed(threads, budget):
+        n, t_used = 0, 0.0
+        first = True
+        for i in range(1 << 20):               # the sample's tokens, cycled until the budget is spent
+            x = np.ascontiguousarray(xs[i % len(xs)], np.float32)
+            t0 = time.perf_counter()
+            orc.lib.orc_moe_layer_mt(C.byref(m), ptr(x, fp), ptr(out, fp), idx.ctypes.data_as(C.POINTER(C.c_int)),
+                                     ptr(w, fp), threads)
+            dt = time.perf_counter() - t0
+            if first:               # warm caches and the thread pool; not timed
+                first = False
+                continue
+            n += 1
+            t_used += dt
+            if t_used >= budget and n >= 3:
+                break
+        return n, t_used
+    n, t_used = timed(nthreads, budget_s)
+    n1, t1 = timed(1, budget_s / 4)            # one thread, a quarter of the budget
     isa = {2: "AVX-512", 0: "portable C"}[orc.lib.orc_cpu_isa()]
-    return n, t_used, isa
+    return n, t_used, isa, n1, t1
 
 
 def bench_prefill(torch, warp_amd, synth, cfg, slab, books, rb, trunk, T, reps, hot=False):
@@ -488,11 +507,13 @@ def main():
     if not a.no_cpu and B == 1:
         nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
         xs = x_all[a.warmup:].to(torch.float32).numpy()
-        n, t_used, isa = cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, a.cpu_seconds, nthreads)
+        n, t_used, isa, n1, t1 = cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, a.cpu_seconds, nthreads)
         cpu = {"value": round(t_used / n * 1e6, 1), "unit": "us/token", "cores": nthreads,
                "kind": "port",
                "sample": f"{n} tokens ({t_used:.1f} s) of the same {a.config} batch-1 layer, the timed "
-                         f"steps' {len(xs)} tokens cycled, {isa} kernels, after one untimed warm-up token"}
+                         f"steps' {len(xs)} tokens cycled, {isa} kernels, after one untimed warm-up token",
+               "single_thread_value": round(t1 / n1 * 1e6, 1), "single_thread_sample": f"{n1} tokens ({t1:.1f} s)",
+               "host": host_cpu()}
 
     out = {
         "metric": METRIC,

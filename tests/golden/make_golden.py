@@ -16,8 +16,9 @@ from), and the reference's outputs:
   chunk_out{o}, chunk_ids{o}, chunk_w{o}   moe_chunk over all tokens
   act           waste_act_pair_range on seeded vectors
   exp_x, exp_y  glibc expf on 65,536 seeded inputs and the special values
+  ssp_x, ssp_y  router_scores, sqrt-softplus, on special and seeded logits
 
-  python tests/golden/make_golden.py
+  python tests/golden/make_golden.py [scalars]
 """
 import hashlib
 import os
@@ -64,6 +65,9 @@ def input_digest(L, X):
 
 def main():
     orc, ref = Oracle(), Ref()
+    if sys.argv[1:] == ["scalars"]:                 # only scalars.npz
+        write_scalars(ref)
+        return
     if ref.isa != 2:
         print("warning: this host does not run the reference's AVX-512 kernels; order 1 = portable")
     for name in CASES:
@@ -92,6 +96,10 @@ def main():
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **out)
         print(name, "written")
 
+    write_scalars(ref)
+
+
+def write_scalars(ref):
     # activation and expf
     r = np.random.default_rng(5)
     g = (r.standard_normal(4096) * 4).astype(np.float32)
@@ -101,8 +109,15 @@ def main():
                          float.fromhex("-0x1.f8cbb2p+5")], np.float32)
     ex = np.concatenate([specials, (r.standard_normal(65536) * 20).astype(np.float32)])
     ey = np.array([ref.lib.ref_expf(float(v)) for v in ex], np.float32)
+    # sqrt-softplus router scores (score_func 2): the branch at 30, the
+    # log1pf of tiny and huge arguments, and a seeded spread of logits
+    sspec = np.array([0.0, -0.0, 1e-8, -1e-8, 1e-3, -1e-3, 0.5, -0.5, 29.999998, 30.0, 30.000002, -30.0,
+                      -80.0, -87.0, -103.0, -104.0, 88.0, 100.0, np.inf, -np.inf], np.float32)
+    sx = np.concatenate([sspec, (r.standard_normal(16384) * 8).astype(np.float32),
+                         r.uniform(-110, 110, 16384).astype(np.float32)])
+    sy = ref.router_scores(2, sx)
     np.savez_compressed(os.path.join(HERE, "scalars.npz"), act_g=g, act_u=u,
-                        act=ref.act_pair(g, u), exp_x=ex, exp_y=ey)
+                        act=ref.act_pair(g, u), exp_x=ex, exp_y=ey, ssp_x=sx, ssp_y=sy)
     print("scalars written")
 
 

@@ -174,7 +174,8 @@ def _planted_layer(E, K, sf, bias, ng, tg, seed):
 @pytest.mark.parametrize("E,K,sf,bias,ng,tg", [
     (64, 8, 0, False, 1, 1), (64, 64, 0, True, 1, 1), (64, 8, 1, False, 1, 1),
     (128, 6, 0, True, 16, 5), (256, 8, 0, True, 8, 4), (256, 8, 1, True, 8, 4),
-    (256, 8, 0, True, 64, 8), (512, 8, 0, True, 1, 1), (1024, 16, 0, True, 16, 3)])
+    (256, 8, 0, True, 64, 8), (512, 8, 0, True, 1, 1), (1024, 16, 0, True, 16, 3),
+    (64, 8, 2, False, 1, 1), (256, 8, 2, True, 8, 4)])
 def test_route_planted(orc, E, K, sf, bias, ng, tg):
     """Top-k over planted logits: few distinct values (so most experts tie
     with several others), +-0, and +-40 (sigmoid saturates to exactly 0 and
@@ -190,6 +191,24 @@ def test_route_planted(orc, E, K, sf, bias, ng, tg):
     m.close()
     assert st == 0
     assert np.array_equal(lg.view(np.uint32) & 0x7fffffff, X.view(np.uint32) & 0x7fffffff)
+    check_routing(orc, L, lg, ids, w)
+
+
+@pytest.mark.parametrize("E,K,bias,ng,tg,T", [(64, 8, False, 1, 1, 1), (256, 8, True, 8, 4, 1),
+                                               (256, 8, True, 8, 4, 16)])
+def test_route_sqrt_softplus(orc, E, K, bias, ng, tg, T):
+    """sqrt-softplus scores (score_func 2) on spread logits (every token a
+    different set of values, through the log1pf branch at 30 and below):
+    ids and weights bit-exact against the oracle, whose log1pf is the host
+    libm's; at T = 1 through the router launch's own routing."""
+    say("test_route_sqrt_softplus", E, K, T)
+    L, r = _planted_layer(E, K, 2, bias, ng, tg, seed=E + 7 * T)
+    X = np.concatenate([r.standard_normal((T, E // 2)) * 6, r.uniform(-40, 40, (T, E - E // 2))],
+                       1).astype(np.float32)
+    m = gpu_layer(L, max_tokens=T)
+    st, y, ids, w, lg = run_forward(torch, m, L, X)
+    m.close()
+    assert st == 0
     check_routing(orc, L, lg, ids, w)
 
 

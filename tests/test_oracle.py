@@ -81,6 +81,24 @@ def test_golden_scalars(orc):
     assert eq_bits(ey, g["exp_y"])
 
 
+def test_golden_sqrt_softplus(orc):
+    """score_func 2 (model.c:5478-5484) against the compiled reference's own
+    router_scores on special and seeded logits, bit for bit; and the
+    formula: sqrt(log1p(exp(l))) in fp64 within 2 ulp below the branch, and
+    sqrt(l) exactly above it."""
+    g = np.load(os.path.join(GOLD, "scalars.npz"))
+    x, y = g["ssp_x"], g["ssp_y"]
+    got = orc.router_scores(2, x)
+    assert eq_bits(got, y)
+    fin = np.isfinite(x)
+    hi = fin & (x > 30.0)
+    assert eq_bits(got[hi], np.sqrt(x[hi]).astype(np.float32))
+    lo = fin & (x <= 30.0) & (x > -80.0)
+    want = np.sqrt(np.log1p(np.exp(x[lo].astype(np.float64))))
+    ulp = np.abs(np.spacing(want.astype(np.float32))).astype(np.float64)
+    assert np.all(np.abs(got[lo].astype(np.float64) - want) <= 2 * ulp)
+
+
 def test_expf_against_host_libm(orc):
     """On glibc 2.35 (this image) the restatement is glibc's expf bit for bit
     (exhaustively: oracle/expf_check).  Here: 2^20 spread inputs."""
@@ -337,3 +355,15 @@ def test_expf_exhaustive():
     subprocess.check_call(["make", "-C", os.path.join(root, "oracle"), "expf_check"])
     out = subprocess.check_output([os.path.join(root, "oracle", "expf_check")]).decode()
     assert "mismatches 0" in out
+
+
+def test_device_log1pf_sampled():
+    """The device's log1pf (warp_amd/csrc/hip/log1pf.h, compiled for the
+    host) against the host libm, bit for bit, on every 4099th float (about
+    a million inputs); WARP_SLOW=1 runs all of them."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    subprocess.check_call(["make", "-s", "-C", os.path.join(root, "oracle"), "log1pf_check"])
+    stride = "1" if os.environ.get("WARP_SLOW") else "4099"
+    out = subprocess.check_output([os.path.join(root, "oracle", "log1pf_check"), stride]).decode()
+    assert " 0 differ" in out, out

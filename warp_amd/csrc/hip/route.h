@@ -7,6 +7,7 @@
 #include "common.h"
 #include "launch.h"
 #include "trace.h"
+#include "log1pf.h"
 
 #define MAXE 1024
 
@@ -140,8 +141,8 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
 #pragma unroll
         for (int j = 0; j < NPL; j++) {
             const float l = sc[j];
-            const float sp = l > 30.0f ? l : log1pf(wh_expf_t(l, et));
-            sc[j] = __fsqrt_rn(sp);
+            const float sp = l > 30.0f ? l : wh_log1pf(wh_expf_t(l, et));
+            sc[j] = sqrtf(sp);              // correctly rounded (HIP's __fsqrt_rn is the native approximation)
         }
     } else {
 #pragma unroll
@@ -356,8 +357,8 @@ __device__ __forceinline__ void route_wg(const whip_route_cfg &c, float l, float
     float sc = 0.0f;
     if (tid < E) {
         if (c.score_func == 2) {
-            const float sp = l > 30.0f ? l : log1pf(wh_expf_t(l, etab));
-            sc = __fsqrt_rn(sp);
+            const float sp = l > 30.0f ? l : wh_log1pf(wh_expf_t(l, etab));
+            sc = sqrtf(sp);
         } else if (c.score_func == 0) {
             sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf_t(-l, etab)));
         } else {

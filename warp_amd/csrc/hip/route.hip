@@ -5,8 +5,8 @@
 // Bit-exact with the engine's CPU path on identical logits
 // (src/model.c:5466-5553):
 //   scores    sigmoid 1/(1+expf(-l)); softmax expf(l-max)/sum with the sum
-//             taken sequentially in expert order; sqrt-softplus (its log1pf
-//             is the device's, not restated);
+//             taken sequentially in expert order; sqrt-softplus with the
+//             host libm's log1pf restated (log1pf.h);
 //   select    K passes, each the first expert (ascending id) whose value
 //             score+bias is strictly greater than every earlier one and
 //             than -1e30, skipping taken ids.  A pass is one wave max of a
