@@ -80,3 +80,23 @@ int main(void){
         subprocess.check_call(["gcc", "-I" + inc, str(f), "-o", str(exe)])
         out.append(subprocess.check_output([str(exe)]).decode())
     assert out[0] == out[1], out
+
+
+def test_empty_and_invalid_calls_fail_before_any_device_work():
+    """An empty batch is an error, as in the engine's accelerator entry
+    (src/metal.m:353: n <= 0 returns -1; the caller at model.c:5734 then
+    falls through to its serial loop, model.c:5788-5790); a missing layer or
+    T <= 0 is WASTE_HIP_EINVAL.  These
+    checks come before any HIP call, so they run without a GPU."""
+    lib = ctypes.CDLL(LIB)
+    lib.waste_hip_vq3r.restype = ctypes.c_int
+    lib.waste_hip_vq3r.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    assert lib.waste_hip_vq3r(None, 0) == -1
+    assert lib.waste_hip_vq3r(None, -3) == -1
+    f = lib.waste_hip_moe_forward
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    x = (ctypes.c_float * 8)()
+    assert f(None, x, 0, 1, x, None, None, None, None) == -1
+    assert f(None, x, 0, 0, x, None, None, None, None) == -1
