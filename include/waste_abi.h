@@ -148,6 +148,7 @@ WASTE_ABI_ASSERT(sizeof(lutb_arg) == 40, "lutb_arg layout");
 WASTE_ABI_ASSERT(sizeof(vqp_arg) == 48, "vqp_arg layout");
 WASTE_ABI_ASSERT(offsetof(waste_kernels, mvq_rows_f32) == 24, "slot offset");
 WASTE_ABI_ASSERT(offsetof(waste_kernels, on_device) == 56, "on_device");
+WASTE_ABI_ASSERT(offsetof(waste_kernels, mvq_rows_cpu) == 64, "mvq_rows_cpu");
 WASTE_ABI_ASSERT(sizeof(waste_kernels) == 80, "waste_kernels layout");
 WASTE_ABI_ASSERT(sizeof(waste_vq_job) == 72, "waste_vq_job layout");
 #undef WASTE_ABI_ASSERT

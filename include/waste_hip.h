@@ -247,8 +247,10 @@ int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W,
  * Pointers get/hold return are device addresses.  The caller's stream is
  * made to wait for the slot's fill; the caller enqueues its readers and
  * then calls release(stream), after which a refill of the slot waits for
- * them.  A get() pointer is good until the next get/hold; a hold()
- * pointer until release.  Releases go on one stream.
+ * them.  A get() pointer is good until the next get/hold (work already
+ * enqueued on its stream by then still reads the old record: a refill of
+ * the slot waits for it); a hold() pointer until release.  Releases go on
+ * one stream.
  *
  * dry = 1: the policy alone, no device (slot pointers are tokens, nothing
  * is copied) — for replaying a routing trace.

@@ -167,7 +167,7 @@ class Oracle:
 
     def mvq_rows(self, t, x, order):
         y = np.zeros(t.rows, np.float32)
-        bits = {2: 8, 3: 4}[t.fmt]
+        bits = {2: 8, 3: 4, 7: 3}[t.fmt]
         self.lib.orc_mvq_rows(ptr(y, fp), ptr(t.q, i8p), ptr(t.qs, u16p), ptr(np.ascontiguousarray(x, np.float32), fp),
                               0, t.rows, t.cols, t.group, bits, t.rowbytes, order)
         return y
@@ -328,7 +328,7 @@ class Ref:
 
     def mvq_rows(self, t, x):
         y = np.zeros(t.rows, np.float32)
-        bits = {2: 8, 3: 4}[t.fmt]
+        bits = {2: 8, 3: 4, 7: 3}[t.fmt]
         self.lib.ref_mvq_rows(ptr(y, fp), ptr(t.q, i8p), ptr(t.qs, u16p), ptr(np.ascontiguousarray(x, np.float32), fp),
                               t.rows, t.cols, t.group, bits, t.rowbytes)
         return y

@@ -116,3 +116,29 @@ class Layer:
     def inputs(self, T, seed=1):
         r = np.random.default_rng(seed)
         return r.standard_normal((T, self.H)).astype(np.float32)
+
+
+def quant_q3g(W, group=128):
+    """Q3G rows (tools/convert.py:854-892): codes round(w/scale) in [-4, 3]
+    biased by +4, LSB-first at bit 3i of the row, each row padded to
+    (n*3+7)/8 bytes plus one guard byte; scale = amax/3 per group, f16.
+    Returns (packed uint8 [rows][rowbytes], f16 scale bits [rows][ng],
+    rowbytes)."""
+    rows, N = W.shape
+    ng = (N + group - 1) // group
+    n = ng * group
+    Wp = np.zeros((rows, n), np.float32)
+    Wp[:, :N] = W
+    g = Wp.reshape(rows, ng, group)
+    sc = np.maximum(np.abs(g).max(-1, keepdims=True), np.float32(1e-8)) / np.float32(3.0)
+    sc16 = sc.astype(np.float16)
+    u = (np.clip(np.rint(g / sc), -4, 3).astype(np.int32) + 4).reshape(rows, n)
+    rowbytes = (n * 3 + 7) // 8 + 1
+    buf = np.zeros((rows, rowbytes), np.int32)
+    off = np.arange(n) * 3
+    byte, shift = off // 8, off % 8
+    for i in range(n):
+        buf[:, byte[i]] += (u[:, i] << shift[i]) & 0xFF
+        if shift[i] > 5:
+            buf[:, byte[i] + 1] += (u[:, i] >> (8 - shift[i])) & 0xFF
+    return buf.astype(np.uint8), sc16.view(np.uint16).reshape(rows, ng), rowbytes

@@ -305,3 +305,53 @@ def test_forward_cached(orc, n_slots, look):
     for m in ms:
         m.close()
     cache.close()
+
+
+def test_get_slot_refill_waits_for_readers(orc):
+    """A slot handed out by get() and let go by the policy before a release
+    (the next two gets make it the victim) is refilled only after the work
+    already enqueued on its stream: the layer reading it still sees the old
+    record, bit for bit."""
+    say("test_get_slot_refill_waits_for_readers")
+    dev = torch.device("cuda:0")
+    L = dsv3_layer(0, 500)
+    rec = L.rec_bytes
+    host = torch.empty((L.E, rec), dtype=torch.uint8, pin_memory=True)
+    host[:] = torch.from_numpy(np.frombuffer(L.bank(), np.uint8).reshape(L.E, rec).copy())
+    ref = gpu_layer(L)
+    X = bf16_inputs(L, 1, 77)
+    xd = torch.from_numpy(X).to(dev).to(torch.bfloat16)
+    y0 = torch.empty((1, L.H), device=dev)
+    ids0 = torch.empty((1, L.K), dtype=torch.int32, device=dev)
+    ref.forward(xd.data_ptr(), 1, y0.data_ptr(), ids0.data_ptr(), None, None, bf16=True, stream=stream())
+    assert ref.status(stream()) == 0
+    ids = ids0.cpu().numpy()[0].tolist()
+    # 9 slots: the 8 routed records, then one more get and a refill of the
+    # first one's slot while the layer that reads it may still be queued
+    cache = warp_amd.ExpertCache(rec, 9 * rec, policy=1, depth=0)
+    cache.set_source([host.data_ptr() + e * rec for e in range(L.E)], 1, L.E)
+    m = gpu_layer(L, records=False)
+    s = torch.cuda.Stream()
+    outs = []
+    with torch.cuda.stream(s):
+        sp = s.cuda_stream
+        ptrs = [cache.get(0, e, sp) for e in ids]
+        assert all(ptrs)
+        assert m.bind_table(ids, ptrs, codebook_id=L.cb_base, stream=sp) == 0
+        for _ in range(6):                           # a queue of readers
+            y = torch.empty((1, L.H), device=dev)
+            m.forward(xd.data_ptr(), 1, y.data_ptr(), None, None, None, bf16=True, stream=sp)
+            outs.append(y)
+        others = [e for e in range(L.E) if e not in ids][:2]
+        for e in others:                             # LRU: the first slot goes
+            assert cache.get(0, e, sp)
+        assert any(cache.slot(0, e) < 0 for e in ids), "no routed record's slot was reused"
+    torch.cuda.synchronize()
+    assert m.status(stream()) == 0
+    want = bits(y0.cpu().numpy())
+    for y in outs:
+        assert np.array_equal(bits(y.cpu().numpy()), want)
+    cache.release(stream())
+    m.close()
+    ref.close()
+    cache.close()

@@ -18,7 +18,7 @@ import pytest
 
 from gpu_util import LAYER_RTOL, LOGIT_RTOL, gpu_layer, rel_err, run_forward
 from oracle_lib import Oracle
-from records import FMT_F32, FMT_Q4G, FMT_Q8G, Layer, Tensor
+from records import FMT_F32, FMT_Q4G, FMT_Q8G, Layer, Tensor, quant_q3g
 
 pytestmark = pytest.mark.gpu
 
@@ -293,6 +293,8 @@ def test_register_slot(orc):
         _fields_ = [("y", C.c_void_p), ("W", C.c_void_p), ("ws", C.c_void_p), ("xq", C.c_void_p),
                     ("xs", C.c_void_p), ("in_", C.c_int), ("ng", C.c_int), ("group", C.c_int),
                     ("bits", C.c_int), ("rowbytes", C.c_size_t)]
+    # The device sums each row in its own order: rows within 1e-5 of the
+    # engine's AVX-512 order (not bit-exact).
     for fmt in (FMT_Q8G, FMT_Q4G):
         L = Layer(1024, 512, 2, 1, n_shared=1, shared_fmt=fmt, seed=500 + fmt)
         t = L.sh[0]
@@ -303,4 +305,65 @@ def test_register_slot(orc):
         SLOT(0, t.rows, C.addressof(a))
         ref = orc.mvq_rows(t, x, 1)
         assert rel_err(y, ref) <= 1e-5
+    # Q3G rows (3-bit codes plus a guard byte per row, tools/convert.py:854-892):
+    # decoded on the host into int8 rows, only the decoded bytes copied
+    rng = np.random.default_rng(77)
+    for cols in (1024, 1000):
+        W = (rng.standard_normal((384, cols)) * 0.02).astype(np.float32)
+        q, qs, rb = quant_q3g(W)
+        t = Tensor(7, 384, cols, 128, q.view(np.int8), qs, rb)
+        x = rng.standard_normal(cols).astype(np.float32)
+        y = np.zeros(t.rows, np.float32)
+        a = MvqArg(y.ctypes.data, q.ctypes.data, qs.ctypes.data, None, x.ctypes.data, cols,
+                   qs.shape[1], 128, 3, rb)
+        SLOT(0, t.rows, C.addressof(a))
+        ref = orc.mvq_rows(t, x, 1)
+        assert rel_err(y, ref) <= 1e-5, cols
+    warp_amd.lib().waste_hip_release_host_buffers()
+
+
+def test_register_slot_cpu_fallback(orc):
+    """A range the device declines (here a group of 16, which its kernels
+    do not take) goes to the CPU kernel the table held when the backend
+    registered (mvq_rows_cpu, src/model.c:805-812), not to NaN."""
+    say("test_register_slot_cpu_fallback")
+
+    class MvqArg(C.Structure):
+        _fields_ = [("y", C.c_void_p), ("W", C.c_void_p), ("ws", C.c_void_p), ("xq", C.c_void_p),
+                    ("xs", C.c_void_p), ("in_", C.c_int), ("ng", C.c_int), ("group", C.c_int),
+                    ("bits", C.c_int), ("rowbytes", C.c_size_t)]
+    rows, cols, g = 96, 256, 16
+    rng = np.random.default_rng(5)
+    W = np.clip(np.rint(rng.standard_normal((rows, cols)) * 40), -127, 127).astype(np.int8)
+    ws = (rng.random((rows, cols // g)) * 0.01 + 0.001).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(cols).astype(np.float32)
+    calls = []
+
+    def cpu_rows(b, e, p):
+        a = C.cast(p, C.POINTER(MvqArg)).contents
+        calls.append((b, e))
+        out = (C.c_float * rows).from_address(a.y)
+        t = Tensor(FMT_Q8G, rows, cols, g, W, ws, cols)
+        ref = orc.mvq_rows(t, x, 1)
+        for r in range(b, e):
+            out[r] = float(ref[r])
+
+    CB = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_void_p)
+    cb = CB(cpu_rows)
+    tab = (C.c_uint8 * 80)()
+    C.c_void_p.from_address(C.addressof(tab) + 64).value = C.cast(cb, C.c_void_p).value  # mvq_rows_cpu
+    name = warp_amd.lib().waste_register_hip(C.cast(tab, C.c_void_p))
+    assert name
+    fnp = C.cast(C.addressof(tab) + 24, C.POINTER(C.c_void_p)).contents.value
+    SLOT = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_void_p)(fnp)
+    y = np.full(rows, np.nan, np.float32)
+    a = MvqArg(y.ctypes.data, W.ctypes.data, ws.ctypes.data, None, x.ctypes.data, cols, cols // g, g, 8,
+               cols)
+    SLOT(0, rows, C.addressof(a))
+    assert calls == [(0, rows)]
+    ref = orc.mvq_rows(Tensor(FMT_Q8G, rows, cols, g, W, ws, cols), x, 1)
+    assert np.array_equal(bits(y), bits(ref))
+    # registering again with an empty table leaves no CPU kernel behind
+    tab2 = (C.c_uint8 * 80)()
+    assert warp_amd.lib().waste_register_hip(C.cast(tab2, C.c_void_p))
     warp_amd.lib().waste_hip_release_host_buffers()

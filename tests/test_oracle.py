@@ -336,6 +336,36 @@ def test_record_check(orc):
     assert orc.lib.orc_crc32((C.c_uint8 * len(payload)).from_buffer_copy(payload), len(payload)) == zlib.crc32(payload)
 
 
+@pytest.mark.parametrize("name", list(CASES) + ["grouped"])
+def test_apply_equals_layer_and_chunk(orc, name):
+    """orc_moe_apply, the function every GPU layer test compares against,
+    is moe_layer's expert half (chunk 0) and moe_chunk's (chunk 1) bit for
+    bit when given their own routing; both of those are pinned to the
+    compiled reference's golden outputs above."""
+    if name == "grouped":
+        L = Layer(512, 128, 64, 8, score_func=0, renorm=1, routed_scale=2.5, bias=True, n_group=8,
+                  topk_group=4, n_shared=1, shared_fmt=3, seed=44)
+        X = L.inputs(5, seed=45)
+    else:
+        L, X = case_layer(name)
+    for o in (0, 1):
+        ol = orc.moe(L, o)
+        for t in range(X.shape[0]):
+            rc, out, idx, w, _ = ol.layer(X[t])
+            assert rc == 0
+            rc, out2 = ol.apply(X[t:t + 1], idx[None], w[None], chunk=0)
+            assert rc == 0 and eq_bits(out2[0], out), (name, o, t)
+        rc, co, ci, cw = ol.chunk(X)
+        assert rc == 0
+        rc, co2 = ol.apply(X, ci, cw, chunk=1)
+        assert rc == 0 and eq_bits(co2, co), (name, o)
+        # a planted wrong weight is seen (the comparison is not vacuous)
+        cw_bad = cw.copy()
+        cw_bad[0, 0] = np.nextafter(cw_bad[0, 0], np.float32(1))
+        rc, co3 = ol.apply(X, ci, cw_bad, chunk=1)
+        assert not eq_bits(co3, co)
+
+
 def test_cpu_baseline_same_bits(orc):
     L = Layer(512, 256, 16, 4, score_func=0, renorm=1, routed_scale=2.5, bias=True, n_shared=1,
               shared_fmt=3, seed=40)

@@ -36,34 +36,53 @@ static pthread_mutex_t g_mu = PTHREAD_MUTEX_INITIALIZER;
 static struct { const void *key; size_t bytes; void *dev; } g_mirror[MIRRORS];
 static int g_ready;              /* 1 registered, -1 declined              */
 static hipStream_t g_stream;
+static void (*g_cpu_rows)(int b, int e, void *arg);  /* the engine's CPU kernel */
 static void *g_io;               /* staging: x in, y out                   */
 static size_t g_io_cap;
 static void *g_job;              /* staging for the vq3r batch             */
 static size_t g_job_cap;
 
-static void *mirror(const void *host, size_t bytes)
+/* The device copy of a host tensor keyed by (host, bytes), NULL when there
+ * is none.  A key whose copy is too small is dropped. */
+static void *mirror_find(const void *key, size_t bytes)
 {
-    int free_slot = -1;
     for (int i = 0; i < MIRRORS; i++) {
-        if (g_mirror[i].key == host && g_mirror[i].bytes >= bytes) return g_mirror[i].dev;
-        if (g_mirror[i].key == host) {                /* grew: replace      */
-            hipFree(g_mirror[i].dev);
-            g_mirror[i].key = NULL;
-        }
-        if (!g_mirror[i].key && free_slot < 0) free_slot = i;
+        if (g_mirror[i].key != key) continue;
+        if (g_mirror[i].bytes >= bytes) return g_mirror[i].dev;
+        hipFree(g_mirror[i].dev);                     /* grew: replace      */
+        g_mirror[i].key = NULL;
+        g_mirror[i].dev = NULL;
+        g_mirror[i].bytes = 0;
     }
-    if (free_slot < 0) {                               /* evict the first    */
+    return NULL;
+}
+
+/* A new device copy under `key` of `bytes` bytes read from `src` (a host
+ * buffer of at least that size); NULL when the allocation or the copy
+ * failed (nothing is then registered). */
+static void *mirror_add(const void *key, const void *src, size_t bytes)
+{
+    int slot = -1;
+    for (int i = 0; i < MIRRORS && slot < 0; i++)
+        if (!g_mirror[i].key) slot = i;
+    if (slot < 0) {                                   /* evict the first    */
         hipFree(g_mirror[0].dev);
         g_mirror[0].key = NULL;
-        free_slot = 0;
+        slot = 0;
     }
     void *d = NULL;
     if (hipMalloc(&d, bytes) != hipSuccess) return NULL;
-    if (hipMemcpy(d, host, bytes, hipMemcpyHostToDevice) != hipSuccess) { hipFree(d); return NULL; }
-    g_mirror[free_slot].key = host;
-    g_mirror[free_slot].bytes = bytes;
-    g_mirror[free_slot].dev = d;
+    if (hipMemcpy(d, src, bytes, hipMemcpyHostToDevice) != hipSuccess) { hipFree(d); return NULL; }
+    g_mirror[slot].key = key;
+    g_mirror[slot].bytes = bytes;
+    g_mirror[slot].dev = d;
     return d;
+}
+
+static void *mirror(const void *host, size_t bytes)
+{
+    void *d = mirror_find(host, bytes);
+    return d ? d : mirror_add(host, host, bytes);
 }
 
 static void *staging(void **buf, size_t *cap, size_t bytes)
@@ -78,31 +97,33 @@ static void *staging(void **buf, size_t *cap, size_t bytes)
 }
 
 /* Q3G rows (3-bit codes at bit 3i, minus 4; waste_q3_at, src/simd.h:101-106)
- * are decoded on the host into Q8G-shaped int8 rows once, then mirrored. */
+ * are decoded on the host into Q8G-shaped int8 rows once, then mirrored.
+ * A Q3G row holds ng*group codes in rowbytes bytes (the packed tensor is
+ * rows*rowbytes, src/model.c:1377); only the decoded rows are copied. */
 static void *mirror_q3(const mvq_arg *a, int rows, size_t *rowbytes_out)
 {
     const size_t rb8 = (size_t)a->ng * a->group;
     const size_t bytes = (size_t)rows * rb8;
-    for (int i = 0; i < MIRRORS; i++)
-        if (g_mirror[i].key == (const void *)((const uint8_t *)a->W + 1) && g_mirror[i].bytes >= bytes) {
-            *rowbytes_out = rb8;
-            return g_mirror[i].dev;
-        }
+    /* keyed one byte past the packed tensor so it cannot alias its mirror */
+    const void *key = (const uint8_t *)a->W + 1;
+    *rowbytes_out = rb8;
+    void *d = mirror_find(key, bytes);
+    if (d) return d;
+    if ((rb8 * 3 + 7) / 8 > a->rowbytes) return NULL;  /* codes past the row */
     int8_t *tmp = (int8_t *)malloc(bytes);
     if (!tmp) return NULL;
     for (int r = 0; r < rows; r++) {
         const uint8_t *p = (const uint8_t *)a->W + (size_t)r * a->rowbytes;
         for (size_t i = 0; i < rb8; i++) {
-            const long off = (long)i * 3;
-            const int v = (p[off >> 3] >> (off & 7)) | (p[(off >> 3) + 1] << (8 - (off & 7)));
+            const size_t off = i * 3;
+            /* the second byte only when the code straddles it */
+            const int hi = (off & 7) > 5 ? p[(off >> 3) + 1] << (8 - (off & 7)) : 0;
+            const int v = (p[off >> 3] >> (off & 7)) | hi;
             tmp[(size_t)r * rb8 + i] = (int8_t)((v & 7) - 4);
         }
     }
-    /* keyed one byte past the packed tensor so it cannot alias its mirror */
-    void *d = mirror((const uint8_t *)a->W + 1, bytes);
-    if (d) hipMemcpy(d, tmp, bytes, hipMemcpyHostToDevice);
+    d = mirror_add(key, tmp, bytes);
     free(tmp);
-    *rowbytes_out = rb8;
     return d;
 }
 
@@ -132,8 +153,15 @@ static void mvq_rows_hip(int b, int e, void *p)
     if (ok) ok = hipStreamSynchronize(g_stream) == hipSuccess;
     pthread_mutex_unlock(&g_mu);
     if (!ok) {
-        /* The slot has no error channel (src/waste_backend.h:69-107): a row
-         * range the device could not compute is NaN, never stale data. */
+        /* The slot has no error channel (src/waste_backend.h:69-107).  A
+         * row range the device declined or failed goes to the CPU kernel
+         * the table held before this backend registered (mvq_rows_cpu, the
+         * one run_rows uses below device_min_bytes, src/model.c:805-812);
+         * without one it is NaN, never stale data. */
+        if (g_cpu_rows) {
+            g_cpu_rows(b, e, p);
+            return;
+        }
         const float nan = __builtin_nanf("");
         for (int r = b; r < e; r++) a->y[r] = nan;
     }
@@ -149,6 +177,11 @@ const char *waste_register_hip(waste_kernels *t)
     const int ok = g_ready > 0;
     pthread_mutex_unlock(&g_mu);
     if (!ok) return NULL;
+    /* the engine snapshots its best CPU kernel before accelerators register
+     * (src/backend.c:198-202); without the snapshot the slot itself still
+     * holds it */
+    if (t->mvq_rows_f32 != mvq_rows_hip)
+        g_cpu_rows = t->mvq_rows_cpu ? t->mvq_rows_cpu : t->mvq_rows_f32;
     t->mvq_rows_f32 = mvq_rows_hip;
     t->on_device = 1;
     /* A synchronous dispatch with two PCIe copies costs tens of us; below

@@ -11,7 +11,9 @@
  * A slot is refilled only after the work that last read it.  release(s)
  * records an event on the caller's stream after its kernels; a later fill
  * into any slot handed out before that release waits for the event on the
- * fill stream.  Releases are expected on one stream (or on streams the
+ * fill stream.  A slot refilled while still handed out (a get() pointer
+ * the policy lets go before the release) waits for the work enqueued so
+ * far on the stream it was last handed to.  Releases are expected on one stream (or on streams the
  * caller orders), since an event slot of the ring is reused after RING
  * releases and then stands for a later point of the same stream.
  *
@@ -47,6 +49,7 @@ typedef struct {
     int has_fill;
     int has_waiter;                  /* `waited` is ordered after the fill */
     void *waited;                    /* (the null stream is a value too)   */
+    void *out_stream;                /* the stream it was last handed to   */
 } slot_t;
 
 struct waste_hip_ecache {
@@ -58,6 +61,7 @@ struct waste_hip_ecache {
     uint8_t *slab;
     hipStream_t fill;
     hipEvent_t ring[RING];
+    hipEvent_t evict;                /* a handed-out slot's readers so far */
     uint64_t n_release;
     int *out_list, n_out;            /* handed out since the last release  */
     int *inflight, n_inflight;
@@ -165,6 +169,13 @@ static int start_fill(waste_hip_ecache *c, int si, int layer, int expert)
     slot_t *q = &c->slot[si];
     if (!src) goto fail;
     if (q->use && hipStreamWaitEvent(c->fill, c->ring[q->use % RING], 0) != hipSuccess) goto fail;
+    /* A slot handed out by get() and not released yet can be the victim
+     * of a later demand (the policy pins only the last one handed out and
+     * the held ones).  Its readers are whatever the caller enqueued on the
+     * stream it went to before this call: the fill waits for them. */
+    if (q->out && (hipEventRecord(c->evict, (hipStream_t)q->out_stream) != hipSuccess ||
+                   hipStreamWaitEvent(c->fill, c->evict, 0) != hipSuccess))
+        goto fail;
     if (hipMemcpyAsync(c->slab + (size_t)si * c->rec_bytes, src, c->rec_bytes, hipMemcpyHostToDevice,
                        c->fill) != hipSuccess)
         goto fail;
@@ -271,6 +282,7 @@ int waste_hip_ecache_create(size_t rec_bytes, size_t budget_bytes, int policy, i
         int bad = hipStreamCreateWithFlags(&c->fill, hipStreamNonBlocking) != hipSuccess;
         for (int i = 0; !bad && i < RING; i++)
             bad = hipEventCreateWithFlags(&c->ring[i], hipEventDisableTiming) != hipSuccess;
+        if (!bad) bad = hipEventCreateWithFlags(&c->evict, hipEventDisableTiming) != hipSuccess;
         for (int i = 0; !bad && i < c->n_slots; i++)
             bad = hipEventCreateWithFlags(&c->slot[i].filled, hipEventDisableTiming) != hipSuccess;
         if (bad) {
@@ -291,6 +303,7 @@ void waste_hip_ecache_destroy(waste_hip_ecache *c)
             if (c->slot[i].filled) hipEventDestroy(c->slot[i].filled);
     for (int i = 0; i < RING; i++)
         if (c->ring[i]) hipEventDestroy(c->ring[i]);
+    if (c->evict) hipEventDestroy(c->evict);
     if (c->fill) hipStreamDestroy(c->fill);
     if (c->slab) hipFree(c->slab);
     free(c->slot);
@@ -351,6 +364,7 @@ static const void *hand_out(waste_hip_ecache *c, int si, void *stream)
         q->out = 1;
         c->out_list[c->n_out++] = si;
     }
+    q->out_stream = stream;
     if (c->dry) return (const void *)(uintptr_t)(((size_t)si + 1) * c->rec_bytes);
     if (q->has_fill && !(q->has_waiter && q->waited == stream)) {
         if (hipStreamWaitEvent((hipStream_t)stream, q->filled, 0) != hipSuccess) return NULL;
