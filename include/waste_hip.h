@@ -46,6 +46,9 @@ extern "C" {
                                       the router launch's wait for the
                                       logits, or a stage of the one-launch
                                       decode (mode 1) */
+#define WASTE_HIP_ESCRATCH  (-11)  /* the call needs more device memory than
+                                      the library's static scratch area
+                                      (16 MiB per GPU) holds             */
 
 /* Library name and device check.  NULL when no usable gfx950 device. */
 const char *waste_hip_device_name(void);
@@ -143,6 +146,28 @@ int waste_hip_moe_bind_expert(waste_hip_moe *m, int expert,
 int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T,
                           float *y, int32_t *ids, float *w, float *logits,
                           void *stream);
+
+/* forward() for a caller that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  The same staged kernels as forward()
+ * for T <= prefill_min_tokens, with every per-forward buffer
+ * (logits, selection and pair lists, expert partials, the shared expert's
+ * activations, the routing exchange) in one static area of 16 MiB per GPU
+ * instead of the layer's own; the call itself allocates nothing (the layer
+ * and its weights are set up beforehand as usual).  A shape needing more
+ * than the area holds (waste_hip_moe_static_bytes: DeepSeek-V3's layer
+ * takes about 5.6 MB per token) or more tokens fails with
+ * WASTE_HIP_ESCRATCH before anything is enqueued.  Every layer on a GPU
+ * shares that GPU's area, which keeps the last call's contents: calls
+ * that overlap on one GPU (other streams, other threads) race; calls
+ * ordered on one stream do not.  ids/w/logits as in forward(); NULL
+ * leaves them in the area, good until the next call on the GPU. */
+int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, int T,
+                                 float *y, int32_t *ids, float *w, float *logits,
+                                 void *stream);
+/* Bytes of the static area a call of T tokens would use (its head
+ * included); more than 16 MiB means WASTE_HIP_ESCRATCH. */
+size_t waste_hip_moe_static_bytes(const waste_hip_moe *m, int T);
 
 /* How forward() runs T == 1: mode 0 (the default) as the staged kernels
  * route()/experts() run; mode 1 as two launches, the router and the shared

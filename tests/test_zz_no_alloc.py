@@ -1,0 +1,97 @@
+# SPDX-License-Identifier: Apache-2.0
+"""waste_hip_moe_forward_static, the forward that allocates nothing (its
+buffers in the library's static scratch area), through the C ABI against
+waste_hip_moe_forward on the same inputs.
+
+Bar: bit-identical outputs, ids and weights (the same kernels in the same
+order; only the buffers' addresses differ), on two calls in a row, the
+second with fewer tokens, and with two layers of different widths sharing
+the area in turn.  Shapes that need more than the area are refused with
+WASTE_HIP_ESCRATCH before anything runs.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+import warp_amd  # noqa: E402
+from test_gpu_fullsize import FullLayer, bits  # noqa: E402
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+
+
+def run(L, x, static):
+    T = x.shape[0]
+    dev = torch.device("cuda:0")
+    xd = x.to(dev)
+    y = torch.full((T, L.H), float("nan"), device=dev)
+    ids = torch.empty((T, L.K), dtype=torch.int32, device=dev)
+    w = torch.empty((T, L.K), dtype=torch.float32, device=dev)
+    lg = torch.empty((T, L.E), dtype=torch.float32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    f = warp_amd.lib().waste_hip_moe_forward_static if static else warp_amd.lib().waste_hip_moe_forward
+    rc = f(L.m.h, xd.data_ptr(), int(L.cfg["bf16"]), T, y.data_ptr(), ids.data_ptr(), w.data_ptr(),
+           lg.data_ptr(), s)
+    assert rc == 0, rc
+    assert L.m.status(s) == 0
+    return y.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy(), lg.cpu().numpy()
+
+
+def same(a, b):
+    for u, v in zip(a, b):
+        if u.dtype == np.float32:
+            assert np.array_equal(bits(u), bits(v))
+        else:
+            assert np.array_equal(u, v)
+
+
+def test_forward_static_matches_forward():
+    say("test_forward_static_matches_forward")
+    lib = warp_amd.lib()
+    ds = FullLayer("dsv3", 8)
+    ki = FullLayer("kimi", 8)
+    try:
+        need = {T: lib.waste_hip_moe_static_bytes(ds.m.h, T) for T in (1, 2, 8)}
+        say(f"  dsv3 static bytes per call: {need}")
+        assert need[2] <= 16 << 20 < need[8]
+        # two calls in a row, the second with fewer tokens, each against forward()
+        for L, Ts in ((ds, (2, 1)), (ki, (6, 3)), (ds, (1,)), (ki, (1,))):
+            for T in Ts:
+                x = L.tokens(T, seed=50 + T)
+                a = run(L, x, static=True)
+                b = run(L, x, static=False)
+                same(a, b)
+                say(f"  {L.cfg['hidden']}x{L.E} T={T}: bit-identical to forward()")
+        # the routing exchange is shared by both layers: interleaved single
+        # tokens still route on their own logits
+        for i in range(4):
+            for L in (ds, ki):
+                x = L.tokens(1, seed=90 + i)
+                same(run(L, x, static=True), run(L, x, static=False))
+        # too many tokens for the area: refused before anything is enqueued
+        x = ds.tokens(8, seed=3).to("cuda:0")
+        y = torch.full((8, ds.H), 7.0, device="cuda:0")
+        rc = lib.waste_hip_moe_forward_static(ds.m.h, x.data_ptr(), 1, 8, y.data_ptr(), None, None, None,
+                                              torch.cuda.current_stream().cuda_stream)
+        assert rc == warp_amd.ESCRATCH
+        torch.cuda.synchronize()
+        assert bool((y == 7.0).all())
+        # and the layer's own forward still works after the static calls
+        x = ds.tokens(1, seed=5)
+        a = run(ds, x, static=False)
+        b = run(ds, x, static=True)
+        same(a, b)
+    finally:
+        ds.close()
+        ki.close()

@@ -23,10 +23,11 @@ WQ_F32, WQ_Q8G, WQ_Q4G, WQ_VQ3R = 0, 2, 3, 4
 SCORE_SIGMOID, SCORE_SOFTMAX, SCORE_SQRTSOFTPLUS = 0, 1, 2
 
 ERRORS = {0: "ok", -1: "EINVAL", -2: "ENODEV", -3: "ENOMEM", -4: "ERECORD", -5: "ECRC",
-          -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE", -9: "ERANGE", -10: "ETIMEOUT"}
+          -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE", -9: "ERANGE", -10: "ETIMEOUT",
+          -11: "ESCRATCH"}
 
-OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE, ERANGE, ETIMEOUT = \
-    0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10
+OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE, ERANGE, ETIMEOUT, ESCRATCH = \
+    0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11
 
 # Every symbol include/waste_hip.h declares.
 EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_host_buffers",
@@ -38,6 +39,7 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_synth_codebooks", "waste_hip_synth_records",
            "waste_hip_moe_route", "waste_hip_moe_experts", "waste_hip_moe_bind_table",
            "waste_hip_moe_predict", "waste_hip_moe_forward_cached", "waste_hip_moe_set_decode",
+           "waste_hip_moe_forward_static", "waste_hip_moe_static_bytes",
            "waste_hip_ecache_create", "waste_hip_ecache_destroy", "waste_hip_ecache_set_source",
            "waste_hip_ecache_hint", "waste_hip_ecache_prefetch", "waste_hip_ecache_get",
            "waste_hip_ecache_hold", "waste_hip_ecache_release", "waste_hip_ecache_admit",
@@ -120,6 +122,8 @@ def lib():
         "waste_hip_moe_predict": (i, [vp, vp, i, i, vp, vp]),
         "waste_hip_moe_forward_cached": (i, [vp, vp, i, vp, i, vp, i, vp, vp, vp, vp]),
         "waste_hip_moe_set_decode": (i, [vp, i]),
+        "waste_hip_moe_forward_static": (i, [vp, vp, i, i, vp, vp, vp, vp, vp]),
+        "waste_hip_moe_static_bytes": (C.c_size_t, [vp, i]),
         "waste_hip_ecache_create": (i, [C.c_size_t, C.c_size_t, i, i, i, C.POINTER(vp)]),
         "waste_hip_ecache_destroy": (None, [vp]),
         "waste_hip_ecache_set_source": (i, [vp, C.POINTER(vp), i, i]),

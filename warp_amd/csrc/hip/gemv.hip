@@ -339,7 +339,7 @@ __device__ __forceinline__ void run_fmt1(const gemv_job &J, int blk, float (*red
 
 // block b of a batch-1 launch; every job of one launch reads x of one type
 template <bool XBF>
-__device__ __forceinline__ void gemv1_block(const gemv_pack &pk, int b, float (*red)[4][2])
+__device__ __forceinline__ void gemv1_block(const gemv_pack &pk, int b, float (*red)[4][2], uint32_t epoch = 0)
 {
     const int ji = (pk.n > 2 && b >= pk.j[2].blk0) ? 2 : (pk.n > 1 && b >= pk.j[1].blk0) ? 1 : 0;
 #define SEL(f) (ji == 2 ? pk.j[2].f : ji == 1 ? pk.j[1].f : pk.j[0].f)
@@ -348,7 +348,7 @@ __device__ __forceinline__ void gemv1_block(const gemv_pack &pk, int b, float (*
     J.fmt = SEL(fmt); J.rows = SEL(rows); J.cols = SEL(cols); J.group = SEL(group);
     J.x = SEL(x); J.x_ld = SEL(x_ld); J.x_bf16 = SEL(x_bf16); J.y = SEL(y); J.y_ld = SEL(y_ld);
     J.wpr = SEL(wpr); J.blk0 = SEL(blk0); J.nblk = SEL(nblk); J.rpw = SEL(rpw); J.coh = SEL(coh);
-    J.xchg = SEL(xchg); J.epoch = SEL(epoch);
+    J.xchg = SEL(xchg); J.epoch = epoch;
 #undef SEL
     const int blk = b - J.blk0;
     if (J.fmt == 0) run_fmt1<0, XBF>(J, blk, red);
@@ -488,6 +488,17 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
     WT_KEEP(0);
     const int nrb = pk.j[0].nblk, tid = threadIdx.x, E = c.E, K = c.K;
     const bool routing = (int)blockIdx.x == nrb - 1;  // uniform
+    // This launch's tag: one past the last launch's, kept in the word before
+    // the exchange (the routing block advances it once every router block
+    // has tagged its logits, so every router block has read it by then).
+    // A launch replayed from a graph, or another layer sharing the buffer,
+    // therefore never meets a word carrying its own tag before it is written.
+    uint64_t *const ew = pk.j[0].xchg - 1;
+    uint32_t epoch = 0;
+    if ((int)blockIdx.x < nrb) {                      // uniform
+        epoch = (uint32_t)coh_ld(ew) + 1u;
+        epoch = epoch ? epoch : 1u;                   // 0 is the buffer's initial tag
+    }
     // the routing's other inputs, loaded beside the product's
     float be = 0.0f;
     const uint8_t *rv = nullptr;
@@ -498,13 +509,12 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
         rv = recs[ec];
         ev = wh_exp_tab[tid & 31];
     }
-    gemv1_block<XBF>(pk, blockIdx.x, red);
+    gemv1_block<XBF>(pk, blockIdx.x, red, epoch);
     WT_SPAN(0, 1);
     WT_KEEP(1);
     if (!routing) return;
     if (tid < E) s_recs[tid] = rv;
     if (tid < 32) s_etab[tid] = ev;
-    const uint32_t epoch = pk.j[0].epoch;
     float l = 0.0f;
     int late = 0;
     if (tid < E) {
@@ -520,7 +530,9 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
         }
         l = __uint_as_float((uint32_t)v);
     }
-    if (__syncthreads_or(late)) {
+    const int any_late = __syncthreads_or(late);
+    if (tid == 0) coh_st(ew, (uint64_t)epoch);       // the next launch's tag follows this one
+    if (any_late) {
         if (tid == 0) atomicOr(err, 16);
         if (tid < K) {
             ids[tid] = -1; wout[tid] = 0.0f;
@@ -561,7 +573,7 @@ WT_READER(whip_trace_gemv)
 extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
                                int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
                                int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
-                               int *err, int *cnt, uint64_t *xchg, uint32_t epoch, hipStream_t s);
+                               int *err, int *cnt, uint64_t *xchg, hipStream_t s);
 
 // padded columns of a matrix (whole quantisation groups)
 static int padded_cols(const whip_mat *A)
@@ -723,7 +735,7 @@ extern "C" int whip_route_gemv(const whip_route_cfg *c, const float *logits, con
 extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
                                int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
                                int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
-                               int *err, int *cnt, uint64_t *xchg, uint32_t epoch, hipStream_t s)
+                               int *err, int *cnt, uint64_t *xchg, hipStream_t s)
 {
     if (n < 1 || n > 3 || c->E > MAXE || c->E <= 0 || c->K <= 0 || c->K > 64 || c->K > c->E || !pair_exp ||
         (!cnt && !xchg) || jobs[0].A.rows != c->E)
@@ -743,9 +755,8 @@ extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_rout
     gemv_pack pk;
     const int blk = pack_gemv1(jobs, n, pk);
     const int E = c->E;
-    if (xchg && epoch && E <= 256 && pair_rec) {
-        pk.j[0].xchg = xchg;
-        pk.j[0].epoch = epoch;
+    if (xchg && E <= 256 && pair_rec) {
+        pk.j[0].xchg = xchg + 1;                      // word 0: the last launch's tag
         if (jobs[0].x_bf16) WHIP_LAUNCH(k_gemv1_xroute<true>, dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w,
                                         pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err);
         else WHIP_LAUNCH(k_gemv1_xroute<false>, dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w,

@@ -208,16 +208,18 @@ int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err, hipStream
 
 /* One token: the router (job 0; its y = the logits, E rows) and up to two
  * more batch-1 products (the shared expert's gate/up) in one launch, and
- * the token routed as whip_route_gemv's routing does.  E <= 256 with xchg
- * and epoch != 0: the router blocks tag their logits with epoch in xchg
- * (E 64-bit words, device memory; no other launch may use the same epoch
- * on it) and the last router block routes once all are tagged.  Otherwise
- * the last router block to finish routes; cnt: a device int, zero before
- * the first launch; every launch leaves it zero. */
+ * the token routed as whip_route_gemv's routing does.  E <= 256 with xchg:
+ * the router blocks tag their logits in xchg (1 + E 64-bit words of device
+ * memory, zero before the first launch; word 0 holds the last launch's tag,
+ * which each launch advances, words 1 .. E the tagged logits) and the last
+ * router block routes once all carry this launch's tag.  Layers of any E
+ * may share one exchange: tags only grow.  Otherwise the last router block to finish
+ * routes; cnt: a device int, zero before the first launch; every launch
+ * leaves it zero.  Launches that share xchg or cnt must not overlap. */
 int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_route_cfg *c, const float *bias,
                     int32_t *ids, float *w, int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
                     int32_t *tok_pairs, const uint8_t *const *recs, const uint8_t **pair_rec,
-                    int *err, int *cnt, uint64_t *xchg, uint32_t epoch, hipStream_t s);
+                    int *err, int *cnt, uint64_t *xchg, hipStream_t s);
 
 /* whip_combine with the shared expert's down projection (shd . h_sh[t],
  * F32/Q8G/Q4G rows) computed in each block for its rows. */
@@ -270,6 +272,23 @@ typedef struct {
 size_t whip_decode1_sync_ints(int H);
 int whip_decode1_check(const whip_dec1_args *a);
 int whip_decode1(const whip_dec1_args *a, hipStream_t s);
+
+/* ---- the static scratch area (scratch.hip) ---- */
+
+/* Bytes of the area, and of its head: state that must start at zero (the
+ * routing exchange, 1 + 1024 tagged words, and a block counter). */
+#define WHIP_SCRATCH_BYTES (16u << 20)
+#define WHIP_SCRATCH_HEAD  8704u
+#define WHIP_SCRATCH_XCHG  0u                /* 1 + E 64-bit words, E <= 1024 */
+#define WHIP_SCRATCH_RCNT  8448u             /* one int, zero between launches */
+/* The current device's address of the area (hipGetSymbolAddress, once per
+ * device). */
+int whip_scratch(void **ptr);
+/* Zeroes the head of the area ptr (the current device's), the first time
+ * it is called on that device, with a fill kernel on s. */
+int whip_scratch_clear_once(void *ptr, hipStream_t s);
+/* Zeroes `bytes` (a multiple of 4) at p with a fill kernel on s. */
+int whip_zero(void *p, size_t bytes, hipStream_t s);
 
 #ifdef __cplusplus
 }

@@ -27,6 +27,25 @@
 
 #define CK(call) do { if ((call) != hipSuccess) return WASTE_HIP_EDEVICE; } while (0)
 
+/* The device buffers one forward writes and reads back: logits, the
+ * selection and its pair lists, the expert partials, the shared expert's
+ * activations, the routing launch's exchange.  A layer owns one set
+ * (allocated at create); waste_hip_moe_forward_static points them into the
+ * library's static scratch area for one call instead. */
+typedef struct {
+    float *logits;               /* [T][E]                                  */
+    float *w, *pair_w;           /* [P]                                     */
+    int32_t *ids, *pair_tok, *pair_exp, *tok_pairs;   /* [P]                */
+    float *part_gu;              /* [P][2][nch_gu][I] + 64 (a sink)         */
+    float *h;                    /* [P][I] (widths the fused SwiGLU misses) */
+    float *part_d;               /* [P][nch_d][H] + 64                      */
+    float *h_sh;                 /* [T][SI] the shared expert's SwiGLU      */
+    float *sh_out;               /* [T][H] its down projection              */
+    const uint8_t **pair_rec;    /* [64] records of a T = 1 route's pairs   */
+    int *rcnt;                   /* the routing launch's block counter (0)  */
+    uint64_t *xchg;              /* [E + 1] its tagged logits, last tag     */
+} fwd_bufs;
+
 struct waste_hip_moe {
     waste_hip_moe_cfg c;
     int E, K, H, I, SI, T;
@@ -47,8 +66,7 @@ struct waste_hip_moe {
     void *router_mem, *sh_mem[3];
     float *d_bias;
     int has_router, has_shared;
-    float *xf, *logits, *w, *pair_w, *part_gu, *h, *part_d, *sh_a, *sh_b, *h_sh, *sh_out;
-    int32_t *ids, *pair_tok, *pair_exp, *tok_pairs;
+    fwd_bufs b;                  /* the forward's buffers (see fwd_bufs)    */
     /* many-token path (T > Td) */
     int32_t *pair_pos, *seg_off, *order;
     uint16_t *h16, *sh_h16;      /* fp16 [P][I], [T][SI]                   */
@@ -57,13 +75,9 @@ struct waste_hip_moe {
     float *plogits, *pw;         /* the lookahead's logits and weights      */
     int routed_T;                /* T of the last route(), 0 none          */
     int32_t *h_sel;              /* pinned: selection [0,64), lookahead [64,128) */
-    const uint8_t **pair_rec;    /* [64] records of a T = 1 route's pairs   */
     int pair_rec_ok;             /* pair_rec matches the table (no bind since) */
     int sh_done;                 /* the route's launch ran the shared down  */
     int sh_in_combine;           /* the combine runs the shared down        */
-    int *rcnt;                   /* the routing launch's block counter (0)  */
-    uint64_t *xchg;              /* [E] its tagged logits (E <= 256)        */
-    uint32_t epoch;              /* the last routing launch's tag            */
     int32_t *d_look;             /* the lookahead's ids                    */
     int prof_on;
     int decode_mode;             /* 1: the persistent experts launch (T == 1) */
@@ -125,12 +139,12 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
 {
     if (!m) return;
     void *bufs[] = { m->d_recs, m->slab, m->d_books, m->d_booksT, m->router_mem,
-                     m->sh_mem[0], m->sh_mem[1], m->sh_mem[2], m->d_bias, m->xf,
-                     m->logits, m->w, m->pair_w, m->part_gu, m->h, m->part_d, m->sh_a,
-                     m->sh_b, m->h_sh, m->sh_out, m->ids, m->pair_tok, m->pair_exp,
-                     m->tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
-                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->pair_rec,
-                     m->sync, m->rcnt, m->xchg };
+                     m->sh_mem[0], m->sh_mem[1], m->sh_mem[2], m->d_bias,
+                     m->b.logits, m->b.w, m->b.pair_w, m->b.part_gu, m->b.h, m->b.part_d,
+                     m->b.h_sh, m->b.sh_out, m->b.ids, m->b.pair_tok, m->b.pair_exp,
+                     m->b.tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
+                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->b.pair_rec,
+                     m->sync, m->b.rcnt, m->b.xchg };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0]) {
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -205,26 +219,25 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     m->h_recs = (const uint8_t **)calloc((size_t)m->E + 1, sizeof(void *));
     int rc = 0;
     rc |= dmalloc((void **)&m->d_recs, ((size_t)m->E + 1) * sizeof(void *));
-    rc |= dmalloc((void **)&m->xf, (size_t)m->T * m->H * 4);
-    rc |= dmalloc((void **)&m->logits, (size_t)m->T * m->E * 4);
-    rc |= dmalloc((void **)&m->ids, (size_t)P * 4);
-    rc |= dmalloc((void **)&m->w, (size_t)P * 4);
-    rc |= dmalloc((void **)&m->pair_tok, (size_t)P * 4);
-    rc |= dmalloc((void **)&m->pair_exp, (size_t)P * 4);
-    rc |= dmalloc((void **)&m->pair_w, (size_t)P * 4);
-    rc |= dmalloc((void **)&m->tok_pairs, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->b.logits, (size_t)m->T * m->E * 4);
+    rc |= dmalloc((void **)&m->b.ids, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->b.w, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->b.pair_tok, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->b.pair_exp, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->b.pair_w, (size_t)P * 4);
+    rc |= dmalloc((void **)&m->b.tok_pairs, (size_t)P * 4);
     /* + 64 floats: the apply kernels' sink for rows past a split's end */
-    rc |= dmalloc((void **)&m->part_gu, ((size_t)Pd * 2 * m->nch_gu * m->I + 64) * 4);
-    rc |= dmalloc((void **)&m->h, (size_t)Pd * m->I * 4);
-    rc |= dmalloc((void **)&m->part_d, ((size_t)Pd * m->nch_d * m->H + 64) * 4);
+    rc |= dmalloc((void **)&m->b.part_gu, ((size_t)Pd * 2 * m->nch_gu * m->I + 64) * 4);
+    rc |= dmalloc((void **)&m->b.h, (size_t)Pd * m->I * 4);
+    rc |= dmalloc((void **)&m->b.part_d, ((size_t)Pd * m->nch_d * m->H + 64) * 4);
     rc |= dmalloc((void **)&m->err, 64);
     rc |= dmalloc((void **)&m->plogits, (size_t)m->E * 4);
     rc |= dmalloc((void **)&m->pw, 64 * 4);
     rc |= dmalloc((void **)&m->d_look, 64 * 4);
-    rc |= dmalloc((void **)&m->pair_rec, 64 * sizeof(void *));
+    rc |= dmalloc((void **)&m->b.pair_rec, 64 * sizeof(void *));
     rc |= dmalloc((void **)&m->sync, whip_decode1_sync_ints(m->H) * 4);
-    rc |= dmalloc((void **)&m->rcnt, 256);
-    rc |= dmalloc((void **)&m->xchg, (size_t)m->E * 8);
+    rc |= dmalloc((void **)&m->b.rcnt, 256);
+    rc |= dmalloc((void **)&m->b.xchg, ((size_t)m->E + 1) * 8);
     if (m->T > m->Td) {
         rc |= dmalloc((void **)&m->pair_pos, (size_t)P * 4);
         rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
@@ -237,7 +250,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     if (hipMemset(m->d_recs, 0, ((size_t)m->E + 1) * sizeof(void *)) != hipSuccess ||
         hipMemset(m->err, 0, 64) != hipSuccess ||
         hipMemset(m->sync, 0, whip_decode1_sync_ints(m->H) * 4) != hipSuccess ||
-        hipMemset(m->rcnt, 0, 256) != hipSuccess || hipMemset(m->xchg, 0, (size_t)m->E * 8) != hipSuccess) {
+        hipMemset(m->b.rcnt, 0, 256) != hipSuccess || hipMemset(m->b.xchg, 0, ((size_t)m->E + 1) * 8) != hipSuccess) {
         waste_hip_moe_destroy(m);
         return WASTE_HIP_EDEVICE;
     }
@@ -296,11 +309,9 @@ int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
     if (!rc) rc = upload_tensor(down, m->H, m->SI, &m->sh[2], &m->sh_mem[2]);
     if (rc) return rc;
     if (gate->fmt != up->fmt || gate->group != up->group) return WASTE_HIP_EINVAL;
-    if (!m->sh_a) {
-        rc |= dmalloc((void **)&m->sh_a, (size_t)m->Td * m->SI * 4);
-        rc |= dmalloc((void **)&m->sh_b, (size_t)m->Td * m->SI * 4);
-        rc |= dmalloc((void **)&m->h_sh, (size_t)m->Td * m->SI * 4);
-        rc |= dmalloc((void **)&m->sh_out, (size_t)m->T * m->H * 4);
+    if (!m->b.h_sh) {
+        rc |= dmalloc((void **)&m->b.h_sh, (size_t)m->Td * m->SI * 4);
+        rc |= dmalloc((void **)&m->b.sh_out, (size_t)m->T * m->H * 4);
         if (m->T > m->Td) rc |= dmalloc((void **)&m->sh_h16, (size_t)m->T * m->SI * 2);
         if (rc) return WASTE_HIP_ENOMEM;
     }
@@ -461,8 +472,8 @@ static int route_many(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
     CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, NULL, NULL, NULL, NULL, m->err, s));
-    CK((hipError_t)whip_sort_pairs(d_ids, d_w, T, K, E, m->pair_tok, m->pair_exp, m->pair_w,
-                                   m->tok_pairs, m->pair_pos, m->seg_off, m->order, s));
+    CK((hipError_t)whip_sort_pairs(d_ids, d_w, T, K, E, m->b.pair_tok, m->b.pair_exp, m->b.pair_w,
+                                   m->b.tok_pairs, m->pair_pos, m->seg_off, m->order, s));
     return 0;
 }
 
@@ -476,7 +487,7 @@ static int experts_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
     a.recs = m->d_recs; a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.sc_off[0] = m->off_sc; a.sc_off[1] = m->off_sc + 2u * (uint32_t)I;
     a.books16 = m->d_books16; a.cb = m->cb;
-    a.N = I; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H; a.tok = m->pair_tok;
+    a.N = I; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H; a.tok = m->b.pair_tok;
     a.seg_off = m->seg_off; a.order = m->order; a.out = m->h16; a.out_ld = I; a.err = m->err;
     CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 1, 4, E, mb, s));
     MARK(3);
@@ -491,12 +502,12 @@ static int experts_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
         memset(&a, 0, sizeof a);
         a.W0 = (const uint8_t *)m->sh[2].q; a.S0 = m->sh[2].qs; a.rowbytes = m->sh[2].rowbytes;
         a.group = m->sh[2].group; a.N = H; a.Kd = m->SI; a.x = m->sh_h16; a.x_mode = 2;
-        a.x_ld = m->SI; a.rows = T; a.out = m->sh_out; a.out_ld = H; a.err = m->err;
+        a.x_ld = m->SI; a.rows = T; a.out = m->b.sh_out; a.out_ld = H; a.err = m->err;
         CK((hipError_t)whip_pf_gemm(&a, m->sh[2].fmt, 0, 1, 1, (T + 31) / 32, s));
     }
     MARK(6);
-    CK((hipError_t)whip_pf_combine(m->tok_pairs, m->pair_exp, m->pair_w, m->d_recs, T, K, E, m->ypair, H,
-                                   m->has_shared ? m->sh_out : NULL, y, s));
+    CK((hipError_t)whip_pf_combine(m->b.tok_pairs, m->b.pair_exp, m->b.pair_w, m->d_recs, T, K, E, m->ypair, H,
+                                   m->has_shared ? m->b.sh_out : NULL, y, s));
     MARK(7);
     return prof_end(m);
 }
@@ -517,7 +528,7 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
     r[nr].y = lg; r[nr].y_ld = E; nr++;
     if (m->has_shared) {
         r[nr].A = m->sh[0]; r[nr].B = &m->sh[1]; r[nr].x = x; r[nr].x_ld = H; r[nr].x_bf16 = x_bf16;
-        r[nr].y = m->h_sh; r[nr].y_ld = m->SI; nr++;
+        r[nr].y = m->b.h_sh; r[nr].y_ld = m->SI; nr++;
     }
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
                           m->c.n_group, m->c.topk_group };
@@ -529,10 +540,8 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
          * list and the pairs' records) while the shared gate/up rows still
          * stream; the shared down projection then runs in the combine */
         KT(0);
-        if (++m->epoch == 0) m->epoch = 1;           /* 0 is the exchange's initial tag */
-        const int rr = whip_gemv_route(r, nr, &rc, m->d_bias, d_ids, d_w, m->pair_tok, m->pair_exp, m->pair_w,
-                                       m->tok_pairs, m->d_recs, m->pair_rec, m->err, m->rcnt, m->xchg,
-                                       m->epoch, s);
+        const int rr = whip_gemv_route(r, nr, &rc, m->d_bias, d_ids, d_w, m->b.pair_tok, m->b.pair_exp, m->b.pair_w,
+                                       m->b.tok_pairs, m->d_recs, m->b.pair_rec, m->err, m->b.rcnt, m->b.xchg, s);
         if (rr) { whip_time_next(NULL, NULL); m->ktimed = 0; }
         if (rr == 0) {
             MARK(1);
@@ -548,19 +557,19 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
         /* routing and the shared expert's down projection in one launch;
          * the route also writes the pairs' records */
         whip_gemv_job j;
-        j.A = m->sh[2]; j.B = NULL; j.x = m->h_sh; j.x_ld = m->SI; j.x_bf16 = 0; j.y = m->sh_out;
+        j.A = m->sh[2]; j.B = NULL; j.x = m->b.h_sh; j.x_ld = m->SI; j.x_bf16 = 0; j.y = m->b.sh_out;
         j.y_ld = H;
-        CK((hipError_t)whip_route_gemv(&rc, lg, m->d_bias, d_ids, d_w, m->pair_tok, m->pair_exp, m->pair_w,
-                                       m->tok_pairs, m->d_recs, m->pair_rec, m->err, &j, s));
+        CK((hipError_t)whip_route_gemv(&rc, lg, m->d_bias, d_ids, d_w, m->b.pair_tok, m->b.pair_exp, m->b.pair_w,
+                                       m->b.tok_pairs, m->d_recs, m->b.pair_rec, m->err, &j, s));
         m->sh_done = 1;
         m->pair_rec_ok = 1;
         return 0;
     }
-    CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, m->pair_tok, m->pair_exp,
-                              m->pair_w, m->tok_pairs, m->err, s));
+    CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, m->b.pair_tok, m->b.pair_exp,
+                              m->b.pair_w, m->b.tok_pairs, m->err, s));
     if (T > 1)
-        CK((hipError_t)whip_pairs(d_ids, d_w, T, K, E, m->pair_tok, m->pair_exp, m->pair_w,
-                                  m->tok_pairs, s));
+        CK((hipError_t)whip_pairs(d_ids, d_w, T, K, E, m->b.pair_tok, m->b.pair_exp, m->b.pair_w,
+                                  m->b.tok_pairs, s));
     return 0;
 }
 
@@ -570,12 +579,12 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     MARK(2);
     whip_vq_args a;
     memset(&a, 0, sizeof a);
-    a.recs = m->d_recs; a.pair_exp = m->pair_exp; a.pair_src = m->pair_tok;
-    a.pair_rec = (T == 1 && m->pair_rec_ok) ? m->pair_rec : NULL;
+    a.recs = m->d_recs; a.pair_exp = m->b.pair_exp; a.pair_src = m->b.pair_tok;
+    a.pair_rec = (T == 1 && m->pair_rec_ok) ? m->b.pair_rec : NULL;
     a.src = x; a.src_ld = H; a.src_bf16 = x_bf16; a.booksT = m->d_booksT; a.cb = m->cb;
     a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.kinds = 2; a.M = I; a.nv = m->nv_gu; a.P = P; a.rsplit = m->rsplit_gu;
-    a.part = m->part_gu; a.err = m->err;
+    a.part = m->b.part_gu; a.err = m->err;
     /* the down kernel reduces the gate/up partials and applies SwiGLU in its
      * table build when both passes run positions across lanes (the gate/up
      * partials then leave scaled by their rows' scales); else a separate
@@ -591,7 +600,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
      * launch's spare workgroups take it (it needs only h_sh) */
     int sh_in_gu = 0;
     if (m->sh_in_combine && a.span) {
-        a.shd = m->sh[2]; a.shd_x = m->h_sh; a.shd_y = m->sh_out;
+        a.shd = m->sh[2]; a.shd_x = m->b.h_sh; a.shd_y = m->b.sh_out;
         sh_in_gu = 1;
     }
     if (m->sh_in_combine || m->ktimed) KT(2);
@@ -606,17 +615,17 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     MARK(3);
     a.out_sc_off = 0;
     if (!act_fused)
-        CK((hipError_t)whip_vq_act(m->d_recs, m->pair_exp, P, m->part_gu, m->nch_gu, I, m->off_sc,
-                                   m->h, s));
+        CK((hipError_t)whip_vq_act(m->d_recs, m->b.pair_exp, P, m->b.part_gu, m->nch_gu, I, m->off_sc,
+                                   m->b.h, s));
     MARK(4);
-    a.pair_src = NULL; a.src = m->h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb + 6;
+    a.pair_src = NULL; a.src = m->b.h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb + 6;
     if (act_fused) {
-        a.act_part = m->part_gu; a.act_nch = m->nch_gu;
+        a.act_part = m->b.part_gu; a.act_nch = m->nch_gu;
         a.out_sc_off = m->off_sc + 4u * (uint32_t)I;  /* the down partials leave scaled too */
     }
     const uint32_t cmb_sc = act_fused ? 0u : m->off_sc + 4u * (uint32_t)I;
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
-    a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->part_d;
+    a.kinds = 1; a.M = H; a.nv = m->nv_d; a.rsplit = m->rsplit_d; a.part = m->b.part_d;
     a.span = 0;
     if (m->ktimed && act_fused) KT(4);
     CK((hipError_t)whip_vq_apply(&a, s));
@@ -625,8 +634,8 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
         /* the shared down projection inside the combine's blocks */
         MARK(6);
         KT(6);
-        const int rc = whip_combine_sh(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
-                                       m->nch_d, H, cmb_sc, T > 1, &m->sh[2], m->h_sh, y, s);
+        const int rc = whip_combine_sh(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->b.part_d,
+                                       m->nch_d, H, cmb_sc, T > 1, &m->sh[2], m->b.h_sh, y, s);
         if (rc == 0) {
             MARK(7);
             return prof_end(m);
@@ -634,15 +643,15 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
         if (rc != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
         whip_time_next(NULL, NULL);
         m->ktimed = 0;
-        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
+        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->b.h_sh, m->SI, T, m->b.sh_out, NULL, H, s));
     } else if (m->has_shared && !m->sh_done && !sh_in_gu) {
-        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->h_sh, m->SI, T, m->sh_out, NULL, H, s));
+        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->b.h_sh, m->SI, T, m->b.sh_out, NULL, H, s));
     }
     MARK(6);
     if (m->ktimed) KT(6);
-    CK((hipError_t)whip_combine(m->d_recs, m->pair_exp, m->pair_w, m->tok_pairs, T, K, m->part_d,
+    CK((hipError_t)whip_combine(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->b.part_d,
                                 m->nch_d, H, cmb_sc, T > 1,
-                                m->has_shared ? m->sh_out : NULL, y, s));
+                                m->has_shared ? m->b.sh_out : NULL, y, s));
     MARK(7);
     return prof_end(m);
 }
@@ -661,9 +670,9 @@ int waste_hip_moe_route(waste_hip_moe *m, const void *x, int x_bf16, int T, int3
     const int rc = ready(m, x, T);
     if (rc) return rc;
     hipStream_t s = (hipStream_t)stream;
-    int32_t *d_ids = ids ? ids : m->ids;
-    float *d_w = w ? w : m->w;
-    float *lg = logits ? logits : m->logits;
+    int32_t *d_ids = ids ? ids : m->b.ids;
+    float *d_w = w ? w : m->b.w;
+    float *lg = logits ? logits : m->b.logits;
     m->routed_T = 0;
     const int r = T > m->Td ? route_many(m, x, x_bf16, T, d_ids, d_w, lg, s)
                             : route_few(m, x, x_bf16, T, d_ids, d_w, lg, s);
@@ -701,12 +710,12 @@ static int forward_one(waste_hip_moe *m, const void *x, int x_bf16, float *y, in
     if (m->has_shared) { a.sh[0] = m->sh[0]; a.sh[1] = m->sh[1]; a.sh[2] = m->sh[2]; }
     a.recs = m->d_recs; a.booksT = m->d_booksT; a.cb = m->cb;
     a.off_gate = m->off_gate; a.off_up = m->off_up; a.off_down = m->off_down; a.off_sc = m->off_sc;
-    a.logits = logits ? logits : m->logits;
-    a.ids = ids ? ids : m->ids;
-    a.w = w ? w : m->w;
-    a.pair_tok = m->pair_tok; a.pair_exp = m->pair_exp; a.pair_w = m->pair_w; a.tok_pairs = m->tok_pairs;
-    a.pair_rec = m->pair_rec;
-    a.h_sh = m->h_sh; a.sh_out = m->sh_out; a.part_gu = m->part_gu; a.part_d = m->part_d; a.y = y;
+    a.logits = logits ? logits : m->b.logits;
+    a.ids = ids ? ids : m->b.ids;
+    a.w = w ? w : m->b.w;
+    a.pair_tok = m->b.pair_tok; a.pair_exp = m->b.pair_exp; a.pair_w = m->b.pair_w; a.tok_pairs = m->b.tok_pairs;
+    a.pair_rec = m->b.pair_rec;
+    a.h_sh = m->b.h_sh; a.sh_out = m->b.sh_out; a.part_gu = m->b.part_gu; a.part_d = m->b.part_d; a.y = y;
     a.err = m->err; a.sync = m->sync;
     if (whip_decode1_check(&a)) return 0;
     /* router logits and the shared expert's gate/up, then the experts */
@@ -716,7 +725,7 @@ static int forward_one(waste_hip_moe *m, const void *x, int x_bf16, float *y, in
     r[nr].y = a.logits; r[nr].y_ld = m->E; nr++;
     if (m->has_shared) {
         r[nr].A = m->sh[0]; r[nr].B = &m->sh[1]; r[nr].x = x; r[nr].x_ld = m->H; r[nr].x_bf16 = x_bf16;
-        r[nr].y = m->h_sh; r[nr].y_ld = m->SI; nr++;
+        r[nr].y = m->b.h_sh; r[nr].y_ld = m->SI; nr++;
     }
     CK((hipError_t)whip_gemv_multi(r, nr, 1, s));
     if (whip_decode1(&a, s)) return WASTE_HIP_EDEVICE;
@@ -746,6 +755,79 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     }
     rc = waste_hip_moe_route(m, x, x_bf16, T, ids, w, logits, stream);
     return rc ? rc : waste_hip_moe_experts(m, x, x_bf16, T, y, stream);
+}
+
+/* Bytes of the static area one allocation-free forward of T tokens uses
+ * beyond its head, with the regions' offsets when b is set. */
+static size_t static_layout(const waste_hip_moe *m, int T, uint8_t *base, fwd_bufs *b)
+{
+    const size_t P = (size_t)T * m->K;
+    const int act_fused = m->nv_d % 32 == 0 && m->nv_gu % 32 == 0;
+    size_t off = WHIP_SCRATCH_HEAD;
+#define TAKE(field, type, bytes)                                               \
+    do {                                                                       \
+        if (b) b->field = (type)(base + off);                                  \
+        off += ((size_t)(bytes) + 255) / 256 * 256;                            \
+    } while (0)
+    TAKE(logits, float *, (size_t)T * m->E * 4);
+    TAKE(ids, int32_t *, P * 4);
+    TAKE(w, float *, P * 4);
+    TAKE(pair_tok, int32_t *, P * 4);
+    TAKE(pair_exp, int32_t *, P * 4);
+    TAKE(pair_w, float *, P * 4);
+    TAKE(tok_pairs, int32_t *, P * 4);
+    TAKE(pair_rec, const uint8_t **, 64 * sizeof(void *));
+    TAKE(part_gu, float *, (P * 2 * m->nch_gu * m->I + 64) * 4);
+    TAKE(part_d, float *, (P * m->nch_d * m->H + 64) * 4);
+    if (!act_fused) TAKE(h, float *, P * m->I * 4);
+    else if (b) b->h = NULL;
+    if (m->has_shared) {
+        TAKE(h_sh, float *, (size_t)T * m->SI * 4);
+        TAKE(sh_out, float *, (size_t)T * m->H * 4);
+    } else if (b) {
+        b->h_sh = b->sh_out = NULL;
+    }
+#undef TAKE
+    if (b) {
+        b->xchg = (uint64_t *)(base + WHIP_SCRATCH_XCHG);
+        b->rcnt = (int *)(base + WHIP_SCRATCH_RCNT);
+    }
+    return off;
+}
+
+size_t waste_hip_moe_static_bytes(const waste_hip_moe *m, int T)
+{
+    if (!m || T <= 0) return 0;
+    return static_layout(m, T, NULL, NULL);
+}
+
+int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
+                                 int32_t *ids, float *w, float *logits, void *stream)
+{
+    int rc = ready(m, x, T);
+    if (rc) return rc;
+    if (!y || m->cb < 0 || m->cb + 9 > m->n_books) return WASTE_HIP_EINVAL;
+    if (T > m->Td || static_layout(m, T, NULL, NULL) > WHIP_SCRATCH_BYTES)
+        return WASTE_HIP_ESCRATCH;
+    hipStream_t s = (hipStream_t)stream;
+    void *base = NULL;
+    if (whip_scratch(&base) || whip_scratch_clear_once(base, s)) return WASTE_HIP_EDEVICE;
+    fwd_bufs sb;
+    static_layout(m, T, (uint8_t *)base, &sb);
+    /* the staged kernels on the static buffers; the layer's own come back
+     * afterwards, and nothing of this call's routing is left for experts() */
+    const fwd_bufs own = m->b;
+    const int mode = m->decode_mode;
+    m->b = sb;
+    m->decode_mode = 0;
+    m->routed_T = 0;
+    rc = waste_hip_moe_route(m, x, x_bf16, T, ids, w, logits, stream);
+    if (!rc) rc = waste_hip_moe_experts(m, x, x_bf16, T, y, stream);
+    m->b = own;
+    m->decode_mode = mode;
+    m->routed_T = 0;
+    m->pair_rec_ok = 0;
+    return rc;
 }
 
 int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *const *dev_records, int n,
@@ -836,8 +918,8 @@ int waste_hip_moe_forward_cached(waste_hip_moe *m, waste_hip_ecache *c, int laye
         m->h_sel = NULL;
         return WASTE_HIP_ENOMEM;
     }
-    int32_t *d_ids = ids ? ids : m->ids;
-    float *d_w = w ? w : m->w;
+    int32_t *d_ids = ids ? ids : m->b.ids;
+    float *d_w = w ? w : m->b.w;
     int rc = waste_hip_moe_route(m, x, x_bf16, 1, d_ids, d_w, NULL, stream);
     if (rc) return rc;
     int nl = next && lookahead > 0 ? (lookahead < next->E ? lookahead : next->E) : 0;
