@@ -457,6 +457,155 @@ k_gemv1_route(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, in
     WT(0, 2);                                         // the routing block's end
 }
 
+// ---- one token, x staged in LDS --------------------------------------------
+// The batch-1 launch that carries the router.  A block first copies x (the
+// one activation row every job of the launch reads) into LDS: those loads
+// go out before the block's weight loads, so they come back first.  Each
+// lane then has all its weight chunks in flight at once (GX_U per matrix,
+// a row split over wpr wavefronts so that they cover it) and reads x from
+// LDS beside them.  Keeping x once per block instead of per lane leaves the
+// launch about 80 VGPRs, so all of its blocks are resident from the start
+// and the whole launch's traffic is requested at once.
+//
+// LDS layout of x: chunk k's slice (NE elements) at 16-byte word k*(NW+1)
+// when a slice is NW >= 2 words (a spare word after each slice spreads
+// consecutive lanes' 128-bit reads over all banks), else packed.
+template <int FMT, bool PAIR> struct gx_u { static constexpr int U = FMT == 0 && !PAIR ? 8 : 4; };
+
+template <int FMT, bool XBF> struct gx_lay {
+    static constexpr int NW = xw_of<FMT, XBF>::N;     // 16-byte words per chunk slice
+    static constexpr bool PAD = NW >= 2 && chunk_of<FMT>::NE * (XBF ? 2 : 4) >= 32;
+    __device__ static int word(int i) { return PAD ? i + i / NW : i; }   // x word i -> LDS word
+};
+
+template <int NXL>
+__device__ __forceinline__ void gx_x_issue(const void *x, int xbytes, uint4 (&xr)[NXL])
+{
+#pragma unroll
+    for (int i = 0; i < NXL; i++) {
+        const int o = (threadIdx.x + 256 * i) * 16;
+        xr[i] = *(const uint4 *)((const uint8_t *)x + (o < xbytes ? o : 0));
+    }
+}
+
+template <int FMT, bool XBF, int NXL, bool PAIR>
+__device__ __forceinline__ void gx_rows(const gemv_job &J, int blk, const uint4 (&xr)[NXL], int xbytes,
+                                        int xl_bytes, uint4 *xs, float (*red)[2], uint32_t epoch)
+{
+    constexpr int NE = chunk_of<FMT>::NE, NW = gx_lay<FMT, XBF>::NW, U = gx_u<FMT, PAIR>::U;
+    constexpr bool pair = PAIR;
+    constexpr int XS = gx_lay<FMT, XBF>::PAD ? NW + 1 : NW;      // LDS words per slice
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wpr = J.wpr, part = wave % wpr;
+    const int r = blk * (4 / wpr) + wave / wpr;
+    const int rc = r < J.rows ? r : J.rows - 1;
+    const int ng = FMT == 0 ? 1 : (J.cols + J.group - 1) / J.group;
+    const int nchunk = (FMT == 0 ? J.cols : ng * J.group) / NE;
+    const int stride = 64 * wpr;
+    const uint8_t *row0 = J.W0 + (size_t)rc * J.rowbytes;
+    const uint8_t *row1 = pair ? J.W1 + (size_t)rc * J.rowbytes : row0;
+    const uint16_t *sr0 = FMT == 0 ? nullptr : J.S0 + (size_t)rc * ng;
+    const uint16_t *sr1 = FMT == 0 ? nullptr : (pair ? J.S1 : J.S0) + (size_t)rc * ng;
+    uint4 w0[U], w1[PAIR ? U : 1];
+    uint16_t s0[U], s1[PAIR ? U : 1];
+    auto issue = [&](int k0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = k0 + u * stride, kc = k < nchunk ? k : 0;
+            w0[u] = *(const uint4 *)(row0 + (size_t)kc * 16);
+            if (FMT != 0) s0[u] = sr0[(size_t)kc * NE / J.group];
+        }
+        if (PAIR)
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int k = k0 + u * stride, kc = k < nchunk ? k : 0;
+                w1[PAIR ? u : 0] = *(const uint4 *)(row1 + (size_t)kc * 16);
+                if (FMT != 0) s1[PAIR ? u : 0] = sr1[(size_t)kc * NE / J.group];
+            }
+    };
+    int k0 = part * 64 + lane;
+    issue(k0);
+    // x to LDS (its loads were issued before the weights'), zero past the
+    // last column up to the whole groups the rows are padded to
+#pragma unroll
+    for (int i = 0; i < NXL; i++) {
+        const int w = threadIdx.x + 256 * i;
+        if (w * 16 < xl_bytes) xs[gx_lay<FMT, XBF>::word(w)] = w * 16 < xbytes ? xr[i] : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    float a0 = 0.0f, a1 = 0.0f;
+    for (;;) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = k0 + u * stride;
+            if (k >= nchunk) continue;
+            // x slices are read as they are needed, not hoisted for all chunks
+            __builtin_amdgcn_sched_barrier(0);
+            uint4 xw[NW > 0 ? NW : 1];
+            if (NE * (XBF ? 2 : 4) < 16) {             // F32 rows, bf16 x: 8 bytes
+                const uint2 v = *((const uint2 *)xs + k);
+                xw[0] = make_uint4(v.x, v.y, 0, 0);
+            } else {
+#pragma unroll
+                for (int j = 0; j < NW; j++) xw[j] = xs[k * XS + j];
+            }
+            if (FMT == 3 && XBF) {
+                const float sx = chunk_sum136_bf(xw);
+                a0 = __fmaf_rn(wh_f16_scale(s0[u]), chunk_dot_q4bf(w0[u], xw, sx), a0);
+                if (PAIR) a1 = __fmaf_rn(wh_f16_scale(s1[PAIR ? u : 0]), chunk_dot_q4bf(w1[PAIR ? u : 0], xw, sx), a1);
+                continue;
+            }
+            const float d0 = chunk_dot<FMT, XBF>(w0[u], xw);
+            a0 = FMT == 0 ? a0 + d0 : __fmaf_rn(wh_f16_scale(s0[u]), d0, a0);
+            if (PAIR) {
+                const float d1 = chunk_dot<FMT, XBF>(w1[PAIR ? u : 0], xw);
+                a1 = FMT == 0 ? a1 + d1 : __fmaf_rn(wh_f16_scale(s1[PAIR ? u : 0]), d1, a1);
+            }
+        }
+        k0 += stride * U;
+        if (k0 - lane >= nchunk) break;                // uniform
+        issue(k0);
+    }
+    a0 = wave_sum(a0);
+    if (pair) a1 = wave_sum(a1);
+    if (wpr > 1) {                                     // uniform
+        if (lane == 0) { red[wave][0] = a0; red[wave][1] = a1; }
+        __syncthreads();
+        if (part == 0 && lane == 0)
+            for (int q = 1; q < wpr; q++) { a0 += red[wave + q][0]; a1 += red[wave + q][1]; }
+    }
+    if (part == 0 && lane == 0 && r < J.rows) {
+        const float v = pair ? wh_silu_mul(a0, a1) : a0;
+        J.y[r] = v;
+        if (J.xchg)
+            __hip_atomic_store(J.xchg + r, ((uint64_t)epoch << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// block b of the launch (jobs as gemv_pack; all read pk.j[0].x)
+template <bool XBF, int NXL>
+__device__ __forceinline__ void gx_block(const gemv_pack &pk, int b, int xbytes, int xl_bytes, uint4 *xs,
+                                         float (*red)[2], uint32_t epoch)
+{
+    uint4 xr[NXL];
+    gx_x_issue<NXL>(pk.j[0].x, xbytes, xr);
+    const int ji = (pk.n > 2 && b >= pk.j[2].blk0) ? 2 : (pk.n > 1 && b >= pk.j[1].blk0) ? 1 : 0;
+#define SEL(f) (ji == 2 ? pk.j[2].f : ji == 1 ? pk.j[1].f : pk.j[0].f)
+    gemv_job J;
+    J.W0 = SEL(W0); J.W1 = SEL(W1); J.S0 = SEL(S0); J.S1 = SEL(S1); J.rowbytes = SEL(rowbytes);
+    J.fmt = SEL(fmt); J.rows = SEL(rows); J.cols = SEL(cols); J.group = SEL(group);
+    J.y = SEL(y); J.wpr = SEL(wpr); J.blk0 = SEL(blk0); J.xchg = SEL(xchg);
+#undef SEL
+    const int blk = b - J.blk0;
+    const bool pair = J.W1 != nullptr;               // uniform
+#define GR(F, P) gx_rows<F, XBF, NXL, P>(J, blk, xr, xbytes, xl_bytes, xs, red, epoch)
+    if (J.fmt == 0) { if (pair) GR(0, true); else GR(0, false); }
+    else if (J.fmt == 2) { if (pair) GR(2, true); else GR(2, false); }
+    else { if (pair) GR(3, true); else GR(3, false); }
+#undef GR
+}
+
 // E <= 256: the same launch without a counter.  Every router block tags
 // its logits with the launch's epoch in xchg (device-coherent); the last
 // router block, which the dispatcher starts after all the others, waits
@@ -465,16 +614,18 @@ k_gemv1_route(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, in
 // dependent passes).  A logit that never arrives sets the status's time-out bit and
 // selects nothing.
 #define XWAIT_TICKS 5000000ull         // 50 ms of the 100 MHz constant clock
-template <bool XBF>
+template <bool XBF, int NXL>
 __global__ void __launch_bounds__(256)
 k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, int32_t *__restrict__ ids,
                float *__restrict__ wout, int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp,
                float *__restrict__ pair_w, int32_t *__restrict__ tok_pairs,
                const uint8_t *const *__restrict__ recs, const uint8_t **__restrict__ pair_rec,
-               int *__restrict__ err)
+               int *__restrict__ err, int xbytes, int xl_bytes)
 {
-    __shared__ float red[4][4][2];
-    __shared__ float s_sc[256], s_sel[256];
+    extern __shared__ uint4 xs[];                     // x, as gx_lay lays it out
+    __shared__ float red[4][2];
+    __shared__ __align__(16) float s_sc[ROUTE_FAST_FLOATS(256) > 256 ? ROUTE_FAST_FLOATS(256) : 256];
+    __shared__ float s_sel[256];
     __shared__ uint64_t s_key[256], s_cand[64];
     __shared__ int s_rank[256];
     __shared__ float s_g[64], s_wraw[64], s_w[64];
@@ -509,7 +660,7 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
         rv = recs[ec];
         ev = wh_exp_tab[tid & 31];
     }
-    gemv1_block<XBF>(pk, blockIdx.x, red, epoch);
+    gx_block<XBF, NXL>(pk, blockIdx.x, xbytes, xl_bytes, xs, red, epoch);
     WT_SPAN(0, 1);
     WT_KEEP(1);
     if (!routing) return;
@@ -545,10 +696,14 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
 #ifdef WH_TRACE
     wt_keep_[5] = clock64();
 #endif
-    route_lds R;
-    R.sc = s_sc; R.sel = s_sel; R.key = s_key; R.rank = s_rank; R.g = s_g; R.keep = s_keep; R.wraw = s_wraw;
-    R.cand = s_cand;
-    route_wg<256, true>(c, l, be, s_recs, s_etab, R, s_ids, s_w, s_rec, err);
+    if (((E + 63) >> 6) * K <= 64) {                  // uniform
+        route_fast<256>(c, l, be, s_recs, s_etab, s_sc, s_ids, s_w, s_rec, err);
+    } else {
+        route_lds R;
+        R.sc = s_sc; R.sel = s_sel; R.key = s_key; R.rank = s_rank; R.g = s_g; R.keep = s_keep; R.wraw = s_wraw;
+        R.cand = s_cand;
+        route_wg<256, true>(c, l, be, s_recs, s_etab, R, s_ids, s_w, s_rec, err);
+    }
     WT_KEEP(3);
 #ifdef WH_TRACE
     wt_keep_[6] = clock64();
@@ -609,6 +764,49 @@ static int pack_gemv1(const whip_gemv_job *jobs, int n, gemv_pack &pk)
         J.nblk = (groups + 4 / wpr - 1) / (4 / wpr);
         J.blk0 = blk;
         blk += J.nblk;
+    }
+    pk.n = n;
+    pk.T = 1;
+    return blk;
+}
+
+// the x-in-LDS launch's job table: rows split over wpr wavefronts so that a
+// lane's chunks fit gx_u; returns the block count, and the bytes of x
+// (xbytes), of its padded columns (xl_bytes) and of its LDS layout (lds)
+static int pack_gx(const whip_gemv_job *jobs, int n, gemv_pack &pk, int &xbytes, int &xl_bytes, int &lds)
+{
+    int blk = 0;
+    const int esz = jobs[0].x_bf16 ? 2 : 4;
+    xbytes = jobs[0].A.cols * esz;
+    xl_bytes = 0;
+    lds = 0;
+    for (int i = 0; i < n; i++) {
+        const whip_gemv_job *q = &jobs[i];
+        const int fmt = q->A.fmt;
+        const int ne = fmt == 0 ? 4 : fmt == 2 ? 16 : 32;
+        const int nchunk = padded_cols(&q->A) / ne;
+        const int U = fmt == 0 && !q->B ? 8 : 4;
+        gemv_job &J = pk.j[i];
+        J.W0 = (const uint8_t *)q->A.q; J.S0 = q->A.qs;
+        J.W1 = q->B ? (const uint8_t *)q->B->q : nullptr; J.S1 = q->B ? q->B->qs : nullptr;
+        J.rowbytes = q->A.rowbytes; J.fmt = fmt; J.rows = q->A.rows; J.cols = q->A.cols;
+        J.group = q->A.group; J.x = q->x; J.x_bf16 = q->x_bf16; J.y = q->y; J.y_ld = q->y_ld;
+        J.x_ld = q->x_ld;
+        J.wpr = nchunk <= 64 * U ? 1 : nchunk <= 128 * U ? 2 : 4;
+        J.rpw = 1;
+        J.coh = 0;
+        J.xchg = nullptr;
+        J.epoch = 0;
+        const int rpb = 4 / J.wpr;
+        J.nblk = (J.rows + rpb - 1) / rpb;
+        J.blk0 = blk;
+        blk += J.nblk;
+        const int xl = padded_cols(&q->A) * esz;
+        const int nw = (ne * esz + 15) / 16;
+        const bool pad = nw >= 2 && ne * esz >= 32;
+        const int l = pad ? xl / 16 / nw * (nw + 1) * 16 : xl;
+        if (xl > xl_bytes) xl_bytes = xl;
+        if (l > lds) lds = l;
     }
     pk.n = n;
     pk.T = 1;
@@ -755,13 +953,26 @@ extern "C" int whip_gemv_route(const whip_gemv_job *jobs, int n, const whip_rout
     gemv_pack pk;
     const int blk = pack_gemv1(jobs, n, pk);
     const int E = c->E;
-    if (xchg && E <= 256 && pair_rec) {
-        pk.j[0].xchg = xchg + 1;                      // word 0: the last launch's tag
-        if (jobs[0].x_bf16) WHIP_LAUNCH(k_gemv1_xroute<true>, dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w,
-                                        pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err);
-        else WHIP_LAUNCH(k_gemv1_xroute<false>, dim3(blk), dim3(256), 0, s, pk, *c, bias, ids, w,
-                         pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err);
-        return (int)hipGetLastError();
+    bool one_x = true;                                // every job reads the router's x
+    for (int i = 1; i < n; i++) one_x = one_x && jobs[i].x == jobs[0].x && jobs[i].A.cols == jobs[0].A.cols;
+    if (xchg && E <= 256 && pair_rec && one_x) {
+        gemv_pack gp;
+        int xbytes, xl_bytes, lds;
+        const int gblk = pack_gx(jobs, n, gp, xbytes, xl_bytes, lds);
+        gp.j[0].xchg = xchg + 1;                      // word 0: the last launch's tag
+        const int nxl = (xl_bytes + 4095) / 4096;     // 16-byte x loads per thread
+        if (nxl <= 16 && lds <= 48 * 1024) {
+#define XR(XB, NX) WHIP_LAUNCH((k_gemv1_xroute<XB, NX>), dim3(gblk), dim3(256), (size_t)lds, s, gp, *c, bias, ids, \
+                               w, pair_tok, pair_exp, pair_w, tok_pairs, recs, pair_rec, err, xbytes, xl_bytes)
+#define XRB(NX) do { if (jobs[0].x_bf16) XR(true, NX); else XR(false, NX); } while (0)
+            if (nxl <= 2) XRB(2);
+            else if (nxl <= 4) XRB(4);
+            else if (nxl <= 8) XRB(8);
+            else XRB(16);
+#undef XRB
+#undef XR
+            return (int)hipGetLastError();
+        }
     }
     if (!cnt) return (int)hipErrorInvalidValue;
     pk.j[0].coh = 1;

@@ -510,3 +510,209 @@ __device__ __forceinline__ void route_wg(const whip_route_cfg &c, float l, float
     }
     __syncthreads();
 }
+
+
+// ---- routing by the whole workgroup, sorted in registers -----------------------
+// The same selection as route_wg (scores, group limit, keys, selection order,
+// weights summed in selection order) with far fewer instructions, for a
+// workgroup of NT threads (a multiple of 64, >= E) whose thread e holds
+// expert e's logit:
+//  - group scores: each group's top two merged across its lanes by DPP and
+//    lane swaps (groups of a power of two experts, at most 64, so a group
+//    lies inside one wavefront), else as route_wg does;
+//  - top K: each wavefront holding experts sorts its 64 keys (one per
+//    lane) with a bitonic network on lane moves; the wavefronts' first K
+//    are then sorted once more by wavefront 0.  Keys are distinct, so the
+//    order of the sorted keys is the engine's selection order.
+// LDS: ROUTE_FAST_FLOATS(E) floats at lds (8-byte aligned).  E <= 64 * 64 / K
+// (the candidates fit one wavefront).  Results in s_ids/s_w/s_rec (K <= 64
+// entries; ids -1, weights 0, records NULL and err bit 2 when fewer than K
+// experts are candidates).  Every thread calls it.
+#define ROUTE_FAST_FLOATS(E) (2 * (E) + 2 * (E) + 128 + 128 + 64 + 8)
+
+__device__ __forceinline__ void top2_merge(float &a, float &b, float pa, float pb)
+{
+    const float hi = fmaxf(a, pa), lo = fminf(a, pa);
+    b = fmaxf(lo, fmaxf(b, pb));
+    a = hi;
+}
+
+// the key of lane i ^ (2^s - 1) (FLIP) or i ^ d (otherwise), a whole wave
+template <bool FLIP, int D> __device__ __forceinline__ uint32_t lane_partner(uint32_t v, int lane)
+{
+    const bool odd16 = (lane >> 4) & 1, hi32 = lane >= 32;
+    auto p16 = [&](uint32_t x) { const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false); return odd16 ? r[0] : r[1]; };
+    auto p32 = [&](uint32_t x) { const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false); return hi32 ? r[0] : r[1]; };
+    if (FLIP) {                                      // D = 2^s: mirror inside blocks of D lanes
+        if (D == 2) return dpp32<0xB1>(v);           // i ^ 1
+        if (D == 4) return dpp32<0x1B>(v);           // quad_perm [3,2,1,0]: i ^ 3
+        if (D == 8) return dpp32<0x141>(v);          // row_half_mirror: i ^ 7
+        if (D == 16) return dpp32<0x140>(v);         // row_mirror: i ^ 15
+        if (D == 32) return p16(dpp32<0x140>(v));    // i ^ 31
+        return p32(p16(dpp32<0x140>(v)));            // i ^ 63
+    }
+    if (D == 1) return dpp32<0xB1>(v);
+    if (D == 2) return dpp32<0x4E>(v);               // quad_perm [2,3,0,1]
+    if (D == 4) return dpp32<0x1B>(dpp32<0x141>(v)); // (i ^ 7) ^ 3
+    if (D == 8) return dpp32<0x128>(v);              // row_ror:8 is i ^ 8 in a row of 16
+    if (D == 16) return p16(v);
+    return p32(v);                                   // D == 32
+}
+
+// one comparator layer: the lower lane of each pair keeps the larger key
+template <bool FLIP, int D> __device__ __forceinline__ uint64_t cmp_layer(uint64_t v, int lane)
+{
+    const uint32_t lo = lane_partner<FLIP, D>((uint32_t)v, lane);
+    const uint32_t hi = lane_partner<FLIP, D>((uint32_t)(v >> 32), lane);
+    const uint64_t o = ((uint64_t)hi << 32) | lo;
+    const bool upper = FLIP ? (lane & (D >> 1)) != 0 : (lane & D) != 0;
+    return (o > v) != upper ? o : v;
+}
+
+// the wave's 64 keys sorted, largest at lane 0
+__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t v, int lane)
+{
+    v = cmp_layer<true, 2>(v, lane);
+    v = cmp_layer<true, 4>(v, lane);  v = cmp_layer<false, 1>(v, lane);
+    v = cmp_layer<true, 8>(v, lane);  v = cmp_layer<false, 2>(v, lane);  v = cmp_layer<false, 1>(v, lane);
+    v = cmp_layer<true, 16>(v, lane); v = cmp_layer<false, 4>(v, lane);  v = cmp_layer<false, 2>(v, lane);
+    v = cmp_layer<false, 1>(v, lane);
+    v = cmp_layer<true, 32>(v, lane); v = cmp_layer<false, 8>(v, lane);  v = cmp_layer<false, 4>(v, lane);
+    v = cmp_layer<false, 2>(v, lane); v = cmp_layer<false, 1>(v, lane);
+    v = cmp_layer<true, 64>(v, lane); v = cmp_layer<false, 16>(v, lane); v = cmp_layer<false, 8>(v, lane);
+    v = cmp_layer<false, 4>(v, lane); v = cmp_layer<false, 2>(v, lane);  v = cmp_layer<false, 1>(v, lane);
+    return v;
+}
+
+template <int NT>
+__device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, float bias_e,
+                                           const uint8_t *const *s_tab, const uint64_t *etab, float *lds,
+                                           int32_t *s_ids, float *s_w, const uint8_t **s_rec, int *err)
+{
+    constexpr int NWV = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, E = c.E, K = c.K;
+    const int ewv = (E + 63) >> 6;                           // wavefronts holding experts
+    uint64_t *s_cand = (uint64_t *)lds;                      // [64] the wavefronts' first K
+    float *s_sc = lds + 128;                                 // [E]
+    float *s_sel = s_sc + E;                                 // [E] (group scan fallback)
+    float *s_g = s_sel + E;                                  // [64] group scores
+    float *s_part = s_g + 64;                                // [NWV + 1] softmax
+    float *s_wraw = s_part + 64;                             // [64]
+    // scores
+    float sc = 0.0f;
+    if (tid < E) {
+        if (c.score_func == 2) {
+            const float sp = l > 30.0f ? l : wh_log1pf(wh_expf_t(l, etab));
+            sc = sqrtf(sp);
+        } else if (c.score_func == 0) {
+            sc = __fdiv_rn(1.0f, __fadd_rn(1.0f, wh_expf_t(-l, etab)));
+        }
+    }
+    if (c.score_func == 1) {                                 // softmax: max, then the sum in expert order
+        if (wv < ewv) {
+            const float mx_w = wave_max_f32(tid < E ? l : -1e30f);
+            if (lane == 0) s_part[wv] = mx_w;
+        }
+        __syncthreads();
+        float mx = -1e30f;
+        for (int w = 0; w < ewv; w++) mx = s_part[w] > mx ? s_part[w] : mx;
+        if (tid < E) {
+            sc = wh_expf_t(__fsub_rn(l, mx), etab);
+            s_sc[tid] = sc;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float sum = 0.0f;
+            for (int e = 0; e < E; e++) sum = __fadd_rn(sum, s_sc[e]);
+            s_part[NWV] = sum;
+        }
+        __syncthreads();
+        if (tid < E) sc = __fdiv_rn(sc, s_part[NWV]);
+    }
+    if (tid < E) s_sc[tid] = sc;
+    const float selv = tid < E ? __fadd_rn(sc, bias_e) : NEG_INF;
+    // group limit
+    const int G = c.n_group > 1 ? c.n_group : 1;
+    const int gsh = G > 1 ? __builtin_ctz((unsigned)(E / G)) : 0, gs = E / G;
+    bool kept = true;
+    if (G > 1) {
+        if (gs <= 64 && (gs & (gs - 1)) == 0) {
+            if (wv < ewv) {                                  // uniform
+                float a = selv, b = NEG_INF;
+                auto step = [&](uint32_t pa, uint32_t pb) {
+                    top2_merge(a, b, __uint_as_float(pa), __uint_as_float(pb));
+                };
+                if (gs > 1) step(dpp32<0xB1>(__float_as_uint(a)), dpp32<0xB1>(__float_as_uint(b)));
+                if (gs > 2) step(dpp32<0x4E>(__float_as_uint(a)), dpp32<0x4E>(__float_as_uint(b)));
+                if (gs > 4) step(dpp32<0x141>(__float_as_uint(a)), dpp32<0x141>(__float_as_uint(b)));
+                if (gs > 8) step(dpp32<0x140>(__float_as_uint(a)), dpp32<0x140>(__float_as_uint(b)));
+                if (gs > 16)
+                    step(lane_partner<false, 16>(__float_as_uint(a), lane),
+                         lane_partner<false, 16>(__float_as_uint(b), lane));
+                if (gs > 32)
+                    step(lane_partner<false, 32>(__float_as_uint(a), lane),
+                         lane_partner<false, 32>(__float_as_uint(b), lane));
+                if (tid < E && (tid & (gs - 1)) == 0) s_g[tid >> gsh] = __fadd_rn(a, gs > 1 ? b : 0.0f);
+            }
+        } else {
+            if (tid < E) s_sel[tid] = selv;
+            __syncthreads();
+            if (tid < G) {
+                float a = NEG_INF, b = NEG_INF;
+                for (int k = tid * gs; k < (tid + 1) * gs; k++) {
+                    const float v = s_sel[k];
+                    if (v > a) { b = a; a = v; }
+                    else if (v > b) b = v;
+                }
+                s_g[tid] = __fadd_rn(a, gs > 1 ? b : 0.0f);
+            }
+        }
+        __syncthreads();
+        if (tid < E) {
+            const int g = (gs & (gs - 1)) == 0 ? tid >> gsh : tid / gs;
+            const float mine = s_g[g];
+            int rk = 0;
+            for (int k = 0; k < G; k++) {
+                const float o = s_g[k];
+                rk += (o > NEG_INF) && before(o, k, mine, g);
+            }
+            kept = mine > NEG_INF && rk < c.topk_group;
+        }
+    }
+    // each wavefront's keys sorted; its first K are the candidates
+    if (wv < ewv) {                                          // uniform
+        const uint64_t key = tid < E ? sel_key(kept ? selv : NEG_INF, tid) : 0;
+        const uint64_t srt = ewv == 1 ? key : wave_sort_desc(key, lane);
+        if (ewv > 1 && lane < K) s_cand[wv * K + lane] = srt;
+        if (ewv == 1) s_cand[lane] = key;
+    }
+    __syncthreads();
+    if (wv == 0) {
+        const uint64_t cv = lane < (ewv > 1 ? ewv * K : 64) ? s_cand[lane] : 0;
+        const uint64_t srt = wave_sort_desc(cv, lane);
+        if (lane < K) {
+            const int e = srt ? (int)~(uint32_t)srt : -1;    // the key's low word is ~id
+            s_ids[lane] = e;
+            s_wraw[lane] = e >= 0 ? s_sc[e] : 0.0f;
+            s_rec[lane] = e >= 0 ? s_tab[e] : nullptr;
+        }
+    }
+    __syncthreads();
+    if (tid < K) {
+        const bool ok = s_ids[K - 1] >= 0;                   // K candidates
+        float wsum = 0.0f;
+        for (int p = 0; p < K; p++) wsum = __fadd_rn(wsum, s_wraw[p]);
+        float myw = s_wraw[tid];
+        if (ok) {
+            if (c.renorm && K > 1) myw = __fdiv_rn(myw, __fadd_rn(wsum, 1e-20f));
+            myw = __fmul_rn(myw, c.routed_scale);
+        } else {
+            myw = 0.0f;
+            s_ids[tid] = -1;
+            s_rec[tid] = nullptr;
+            if (tid == 0) atomicOr(err, 2);
+        }
+        s_w[tid] = myw;
+    }
+    __syncthreads();
+}

@@ -29,6 +29,7 @@
 #include "common.h"
 #include "launch.h"
 #include "gemv_dev.h"
+#include "route.h"
 #include "trace.h"
 
 #ifndef WH_VC
@@ -535,7 +536,7 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         }
         lo = hi;
     }
-    WT(wk, 4 + wv);
+    WT(wk, 6 + wv);
     if (wv == 0) { WT_PUT(wk, 0); WT_PUT(wk, 1); WT_PUT(wk, 2); WT_PUT(wk, 3); }
     if (unbound) atomicOr(a.err, 1);
 }
@@ -815,10 +816,12 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
     const int g = tid % G;
     const int r0 = blockIdx.x * CMB_ROWS + g * 4;
     const int per = (nch + CMB_SLICES - 1) / CMB_SLICES;
+    WT_SPAN(3, 0);
     for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G)
         cmb_gather(recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, t, it, g, r0,
                    per, cred, csc, cw, cl);
     __syncthreads();
+    WT_SPAN(3, 1);
     if (tid >= G || r0 >= H) return;
     float o[4] = {0, 0, 0, 0};
     for (int j = 0; j < K; j++) {                    // combine order
