@@ -49,6 +49,11 @@ extern "C" {
 #define WASTE_HIP_ESCRATCH  (-11)  /* the call needs more device memory than
                                       the library's static scratch area
                                       (16 MiB per GPU) holds             */
+#define WASTE_HIP_EFORMAT   (-12)  /* a container's manifest or file layout
+                                      is out of range or not understood
+                                      (the engine's WASTE_E_FORMAT)      */
+#define WASTE_HIP_EIO       (-13)  /* a container file is missing or a read
+                                      came back short                    */
 
 /* Library name and device check.  NULL when no usable gfx950 device. */
 const char *waste_hip_device_name(void);
@@ -121,6 +126,11 @@ int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
  * loader does (subnormals flushed; src/model.c:2906-2941). */
 int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16,
                                 int n_books);
+/* The same for books [first, first + n_books) of a container's table only
+ * (a layer's nine, starting at its bank's codebook_base): record codebook
+ * ids keep their container-wide meaning and must fall inside the window. */
+int waste_hip_moe_set_codebooks_at(waste_hip_moe *m, const uint16_t *f16,
+                                   int first, int n_books);
 /* One expert record (host memory), checked as record_check does
  * (src/model.c:3645-3692) and copied into the layer's HBM slab. */
 int waste_hip_moe_set_expert(waste_hip_moe *m, int expert,
@@ -313,6 +323,98 @@ int  waste_hip_ecache_slot(const waste_hip_ecache *c, int layer, int expert);
 int  waste_hip_ecache_n_slots(const waste_hip_ecache *c);
 /* waits for every fill issued so far */
 int  waste_hip_ecache_sync(waste_hip_ecache *c);
+/* The learned hotlist, usage.waste: save writes a 16-byte header (magic
+ * "WUSG", version 1, `tokens`) and one 16-byte entry (layer, expert, hits,
+ * last use, 0) per resident record, slot order; 0 or WASTE_HIP_EIO (the
+ * file is removed).  warm reads one, sorts it by hits (ties by layer, then
+ * expert) and loads the first min(entries, slots) of that order from the
+ * source into victims: entries already resident or missing from the
+ * source are skipped and still use up their place.
+ * Returns how many records it loaded, or WASTE_HIP_EIO / WASTE_HIP_EFORMAT
+ * (bad magic).  Counters are untouched, as the engine's are.
+ * Replaces: waste_ecache_save_usage, waste_ecache_warm,
+ * src/ecache.c:827-913. */
+int  waste_hip_ecache_save_usage(const waste_hip_ecache *c, const char *path, uint64_t tokens);
+int  waste_hip_ecache_warm(waste_hip_ecache *c, const char *path);
+
+/* ---- 5. container reader ---------------------------------------------- */
+
+/* A WARP container directory (manifest.json, trunk.bin, codebooks.bin,
+ * experts-L<n>.bin) opened read-only, with the engine's checks: the
+ * manifest's format_version (0), the MoE half of cfg_sane, expert_quant's
+ * ranges, every bank's size arithmetic and codebook base, and each record's
+ * header (record_check) as it is read, its crc32 too when `verify` is set.
+ * Trunk tensors are read on first request, not at open.  Reads of records
+ * are positional (pread): several threads may read one container.
+ * Replaces: the container half of waste_model_open, src/model.c:2640-2741,
+ * 2906-3060; load_trunk, src/model.c:1286-1420; bank_fetch and
+ * record_check, src/model.c:3645-3748. */
+typedef struct waste_hip_container waste_hip_container;
+
+typedef struct {
+    int n_layers, hidden, vocab;
+    int n_experts, top_k, moe_inter;
+    int n_shared;             /* num_shared_experts as written (0: one of width I) */
+    int first_dense;          /* first_k_dense_replace                        */
+    int latent_dim;           /* routed_expert_hidden_size (0: none)          */
+    int score_func, renorm;
+    float routed_scale;
+    int n_group, topk_group;  /* the config's group limit (1, 1 when absent)  */
+    int stages, vec_dim, entries, index_bits, index_block;
+    int n_books, n_tensors;
+    char prefix[64];          /* tensor_prefix                                */
+} waste_hip_container_cfg;
+
+int  waste_hip_container_open(const char *dir, int verify, waste_hip_container **out);
+void waste_hip_container_close(waste_hip_container *c);
+int  waste_hip_container_config(const waste_hip_container *c, waste_hip_container_cfg *out);
+/* Layer `layer`'s expert bank: 0, or WASTE_HIP_EINVAL when it has none. */
+int  waste_hip_container_bank(const waste_hip_container *c, int layer, int *n_experts,
+                              int *codebook_base, size_t *rec_bytes);
+/* codebooks.bin's payloads, fp16 [n_books][entries][vec_dim], as stored
+ * (subnormals are flushed by whoever converts them). */
+const uint16_t *waste_hip_container_codebooks(const waste_hip_container *c, int *n_books);
+/* One record read into dst (dst_bytes >= the bank's rec_bytes) and
+ * checked: 0, WASTE_HIP_EIO (short read), WASTE_HIP_ERECORD (header),
+ * WASTE_HIP_ECRC (payload, with verify), WASTE_HIP_EINVAL (no such
+ * record).  Replaces: bank_fetch, src/model.c:3712-3748. */
+int  waste_hip_container_read_expert(waste_hip_container *c, int layer, int expert,
+                                     void *dst, size_t dst_bytes);
+/* Every record of the layer, [n_experts][rec_bytes], each checked. */
+int  waste_hip_container_read_bank(waste_hip_container *c, int layer, void *dst,
+                                   size_t dst_bytes);
+/* The first failed read since open: its code (0 when none), layer and
+ * expert.  Replaces: waste_error_detail's record report, src/model.c:3700-3710. */
+int  waste_hip_container_error(const waste_hip_container *c, int *layer, int *expert);
+/* A trunk tensor by name, as waste_hip_tensor (host memory the container
+ * owns until close; F32 rows in q, Q8G/Q4G/Q3G rows in q and f16 group
+ * scales in qs), with its manifest shape (ndim, shape may be NULL).
+ * WASTE_HIP_EFORMAT when the manifest has no such tensor or its extent
+ * does not fit trunk.bin. */
+int  waste_hip_container_tensor(waste_hip_container *c, const char *name, waste_hip_tensor *out,
+                                int *ndim, int shape[4]);
+
+/* A device MoE layer for container layer `layer`: the config's routing
+ * (scoring_func, moe_renormalize, routed_scaling_factor), the router
+ * <prefix>model.layers.<L>.block_sparse_moe.gate.weight and its
+ * e_score_correction_bias (when present), the shared expert
+ * (.shared_experts.{gate,up,down}_proj.weight, width moe_inter times
+ * num_shared_experts or 1), the layer's nine codebooks.  Flags:
+ * WASTE_HIP_CT_RECORDS copies every record of the bank into the layer's
+ * slab (otherwise records are bound later, e.g. from an expert cache);
+ * WASTE_HIP_CT_GROUP_LIMIT routes with the config's n_group/topk_group
+ * (the engine's moe_layer has no group limit, so parity with it wants the
+ * flag off).  VQ3R containers without a latent projection only
+ * (WASTE_HIP_EINVAL otherwise).  Replaces: the tensor lookups of
+ * moe_layer, src/model.c:5494-5497, 5932-5936. */
+#define WASTE_HIP_CT_RECORDS     1
+#define WASTE_HIP_CT_GROUP_LIMIT 2
+int  waste_hip_container_moe(waste_hip_container *c, int layer, int max_tokens,
+                             int prefill_min_tokens, int flags, waste_hip_moe **out);
+
+/* zlib's crc32 (running value `crc`, 0 to start): the record checksum.
+ * Replaces: waste_crc32, src/crc32.h:22. */
+uint32_t waste_hip_crc32(uint32_t crc, const void *data, size_t n);
 
 #ifdef __cplusplus
 }

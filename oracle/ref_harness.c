@@ -251,6 +251,20 @@ static int ref_slot_of(const waste_ecache *c, const uint8_t *p)
     return -2;
 }
 
+/* Usage files for the next ref_ecache_run: warm from `warm` after init,
+ * save to `save` (tokens = the cache's clock) after the script; NULL for
+ * neither.  ref_ecache_warmed() is the last warm's return. */
+static char ref_warm_path[4096], ref_save_path[4096];
+static int ref_warm_n;
+
+void ref_ecache_usage(const char *warm, const char *save)
+{
+    snprintf(ref_warm_path, sizeof ref_warm_path, "%s", warm ? warm : "");
+    snprintf(ref_save_path, sizeof ref_save_path, "%s", save ? save : "");
+}
+
+int ref_ecache_warmed(void) { return ref_warm_n; }
+
 int ref_ecache_run(int n_slots, int depth, int policy, const int *ops, int n_words, int *out,
                    uint64_t stats[6])
 {
@@ -261,6 +275,7 @@ int ref_ecache_run(int n_slots, int depth, int policy, const int *ops, int n_wor
     ref_main = pthread_self();
     __atomic_store_n(&ref_gate, 0, __ATOMIC_RELEASE);
     if (depth > 0) waste_ecache_io_start(&c, ref_fetch, NULL, 2, depth);
+    ref_warm_n = ref_warm_path[0] ? waste_ecache_warm(&c, ref_warm_path, ref_fetch, NULL) : 0;
     int n_out = 0, bad = 0;
     for (int w = 0; w < n_words && !bad;) {
         const int op = ops[w];
@@ -290,6 +305,7 @@ int ref_ecache_run(int n_slots, int depth, int policy, const int *ops, int n_wor
         }
     }
     ref_quiesce(&c);
+    if (ref_save_path[0] && waste_ecache_save_usage(&c, ref_save_path, c.clock)) bad = 1;
     stats[0] = c.hits; stats[1] = c.misses; stats[2] = c.evictions;
     stats[3] = c.prefetched; stats[4] = c.spec_issued; stats[5] = c.bytes_read / rec;
     waste_ecache_io_stop(&c);

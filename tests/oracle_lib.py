@@ -297,19 +297,28 @@ class Ref:
                                      rt, fp, rt, rt, rt, fp, C.c_int, u8p, C.c_size_t, fp, C.c_int, fp, i32p, fp])
         _sig(L, "ref_ecache_run", C.c_int, [C.c_int, C.c_int, C.c_int, i32p, C.c_int, i32p,
                                             C.POINTER(C.c_uint64)])
+        _sig(L, "ref_ecache_usage", None, [C.c_char_p, C.c_char_p])
+        _sig(L, "ref_ecache_warmed", C.c_int, [])
         self.isa = L.ref_init()
 
-    def ecache_run(self, ops, n_slots, depth, policy):
+    def ecache_run(self, ops, n_slots, depth, policy, warm=None, save=None):
         """The engine's own src/ecache.c on a cache script, reads landing by
         the next demand get: (outputs, [hits, misses, evictions,
-        prefetched, spec_issued, reads])."""
+        prefetched, spec_issued, reads]).  warm / save: usage files read
+        after init / written after the script (ecache_warmed() then says
+        how many the warm loaded)."""
+        self.lib.ref_ecache_usage(os.fsencode(warm) if warm else None, os.fsencode(save) if save else None)
         a = np.ascontiguousarray(ops, np.int32)
         out = np.zeros(max(len(ops), 1), np.int32)
         st = (C.c_uint64 * 6)()
         k = self.lib.ref_ecache_run(n_slots, depth, policy, ptr(a, i32p), len(ops), ptr(out, i32p), st)
+        self.lib.ref_ecache_usage(None, None)
         if k < 0:
             raise RuntimeError("ref_ecache_run failed")
         return [int(v) for v in out[:k]], list(st)
+
+    def ecache_warmed(self):
+        return self.lib.ref_ecache_warmed()
 
     def set_order(self, order):
         self.lib.ref_set_order(order)

@@ -231,3 +231,91 @@ def test_product_rejects_bad_arguments():
         warp_amd.ExpertCache(REC, 10 * REC, policy=2, dry=True)
     with pytest.raises(warp_amd.HipError):
         warp_amd.ExpertCache(REC, 10 * REC, depth=-1, dry=True)
+
+
+# ---- the learned hotlist (usage.waste) ----------------------------------
+
+def _usage(path, entries, magic=0x47535557, tokens=7):
+    import struct
+    with open(path, "wb") as f:
+        f.write(struct.pack("<IIQ", magic, 1, tokens))
+        for layer, e, hits, last in entries:
+            f.write(struct.pack("<HHIII", layer, e, hits, last, 0))
+
+
+@pytest.mark.parametrize("trace", ["trace_olmoe_299", "trace_kimi_300"])
+@pytest.mark.parametrize("n_slots,depth,policy", [(100, 0, 0), (201, 2, 0), (402, 2, 1), (25, 2, 0)])
+def test_usage_save_and_warm_equal_engine(ref, traces, tmp_path, trace, n_slots, depth, policy):
+    """save_usage writes the engine's file byte for byte after the same
+    script; a cache warmed from it then decides as the engine's warmed
+    cache does, slot for slot (src/ecache.c:827-913)."""
+    tr = traces[trace]
+    kw = dict(hold=True, hint=depth > 0, lookahead=6 if depth else 0)
+    a, b = str(tmp_path / "engine.waste"), str(tmp_path / "product.waste")
+    ref.ecache_run(es.layer_calls(tr[:40], **kw), n_slots, depth, policy, save=a)
+    c = product(n_slots, depth, policy)
+    es.run_product(c, es.layer_calls(tr[:40], **kw))
+    raw = open(a, "rb").read()
+    tokens = int(np.frombuffer(raw[8:16], np.uint64)[0])
+    assert c.save_usage(b, tokens) == 0
+    assert open(b, "rb").read() == raw
+    assert (len(raw) - 16) // 16 > 0
+    ops2 = es.layer_calls(tr[40:90], **kw)
+    r_out, r_st = ref.ecache_run(ops2, n_slots, depth, policy, warm=a)
+    r_warm = ref.ecache_warmed()
+    c2 = product(n_slots, depth, policy)
+    assert c2.warm(a) == r_warm == min(n_slots, (len(raw) - 16) // 16)
+    p_out, p_st = es.run_product(c2, ops2)
+    assert p_st == r_st
+    assert p_out == r_out
+
+
+def test_warm_order_and_limits(tmp_path):
+    """Hottest first, ties by (layer, expert); the engine walks the first
+    min(entries, slots) entries of the sorted file, so a duplicate or a
+    resident record uses up a place (src/ecache.c:890-910)."""
+    path = str(tmp_path / "u.waste")
+    ents = [(0, 5, 3, 1), (1, 2, 9, 2), (0, 1, 9, 3), (2, 7, 1, 4), (0, 1, 9, 5), (1, 0, 3, 6)]
+    _usage(path, ents)
+    c = product(3, 0, 0)
+    # sorted: (0,1) (0,1) (1,2) | (0,5) (1,0) (2,7); three places, one a duplicate
+    assert c.warm(path) == 2
+    assert [c.slot(0, 1), c.slot(1, 2)] == [0, 1]
+    assert c.slot(0, 5) == -1 and c.slot(1, 0) == -1
+    assert c.stats()["reads"] == 0 and c.stats()["misses"] == 0
+    # a warmed record is a hit on its first demand
+    c.get(0, 1)
+    assert c.stats()["hits"] == 1
+    four = product(4, 0, 0)
+    assert four.warm(path) == 3 and four.slot(0, 5) == 2 and four.slot(1, 0) == -1
+    big = product(10, 0, 0)
+    assert big.warm(path) == 5
+    assert big.warm(path) == 0                       # all resident already
+
+
+def test_warm_skips_records_the_source_lacks(tmp_path):
+    path = str(tmp_path / "u.waste")
+    _usage(path, [(0, 1, 5, 1), (3, 0, 4, 2), (1, 9, 3, 3), (1, 2, 2, 4)])
+    c = product(8, 0, 0)
+    c.set_source([4096 * (k + 1) for k in range(2 * 4)], 2, 4)     # layers 0-1, experts 0-3
+    assert c.warm(path) == 2
+    assert c.slot(0, 1) == 0 and c.slot(1, 2) == 1
+    assert c.slot(3, 0) == -1 and c.slot(1, 9) == -1
+
+
+def test_warm_refusals(tmp_path):
+    import warp_amd
+    c = product(4, 0, 0)
+    assert c.warm(str(tmp_path / "missing.waste")) == warp_amd.EIO
+    bad = str(tmp_path / "bad.waste")
+    _usage(bad, [(0, 1, 1, 1)], magic=0x12345678)
+    assert c.warm(bad) == warp_amd.EFORMAT
+    empty = str(tmp_path / "empty.waste")
+    _usage(empty, [])
+    assert c.warm(empty) == 0
+    with open(empty, "ab") as f:
+        f.write(b"\0" * 7)                         # a partial entry is ignored
+    assert c.warm(empty) == 0
+    assert c.save_usage(str(tmp_path / "no_dir" / "u.waste"), 0) == warp_amd.EIO
+    z = product(0, 0, 0)
+    assert z.warm(bad) == 0                         # no slots: nothing to do

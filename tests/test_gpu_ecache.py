@@ -355,3 +355,125 @@ def test_get_slot_refill_waits_for_readers(orc):
     m.close()
     ref.close()
     cache.close()
+
+
+def _pinned_bank(Ls):
+    rec = Ls[0].rec_bytes
+    host = torch.empty((len(Ls) * Ls[0].E, rec), dtype=torch.uint8, pin_memory=True)
+    for l, L in enumerate(Ls):
+        host[l * L.E:(l + 1) * L.E] = torch.from_numpy(np.frombuffer(L.bank(), np.uint8).reshape(L.E, rec).copy())
+    return host
+
+
+def _run_cached(Ls, host, tokens, n_slots, depth, look, warm=None, save=None):
+    """Every token through every layer by forward_cached: [(y, ids, w)]."""
+    dev = torch.device("cuda:0")
+    rec, E = Ls[0].rec_bytes, Ls[0].E
+    cache = warp_amd.ExpertCache(rec, n_slots * rec, policy=0, depth=depth)
+    cache.set_source([host.data_ptr() + i * rec for i in range(len(Ls) * E)], len(Ls), E)
+    warmed = cache.warm(warm) if warm else 0
+    ms = [gpu_layer(L, records=False) for L in Ls]
+    for m, L in zip(ms, Ls):
+        assert m.bind_table([], [], codebook_id=L.cb_base) == 0
+    s = stream()
+    outs = []
+    for t in range(tokens):
+        for l, (L, m) in enumerate(zip(Ls, ms)):
+            xd = torch.from_numpy(bf16_inputs(L, 1, 7000 * t + l)).to(dev).to(torch.bfloat16)
+            y = torch.full((1, L.H), float("nan"), device=dev)
+            ids = torch.empty((1, L.K), dtype=torch.int32, device=dev)
+            w = torch.empty((1, L.K), device=dev)
+            nxt = ms[l + 1] if l + 1 < len(Ls) else None
+            m.forward_cached(cache, l, xd.data_ptr(), y.data_ptr(), nxt=nxt, lookahead=look if nxt else 0,
+                             ids_ptr=ids.data_ptr(), w_ptr=w.data_ptr(), bf16=True, stream=s)
+            assert m.status(s) == 0, (t, l)
+            outs.append((y.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy()))
+    cache.sync()
+    st = cache.stats()
+    if save:
+        assert cache.save_usage(save, tokens) == 0
+    for m in ms:
+        m.close()
+    cache.close()
+    return outs, st, warmed
+
+
+def test_cache_configs_bit_identical(orc, tmp_path):
+    """Placement decides speed, never the numbers: the same tokens through
+    layers holding their own records and through caches of every shape
+    (everything resident, tight, read-ahead depth 0 and 2, lookahead 0
+    and 6, warmed from a usage file) give bit-identical outputs, ids and
+    weights."""
+    say("test_cache_configs_bit_identical")
+    n_layers, tokens = 3, 5
+    Ls = [dsv3_layer(l, 800 + l) for l in range(n_layers)]
+    dev = torch.device("cuda:0")
+    base = []
+    ms = [gpu_layer(L) for L in Ls]
+    for t in range(tokens):
+        for l, (L, m) in enumerate(zip(Ls, ms)):
+            xd = torch.from_numpy(bf16_inputs(L, 1, 7000 * t + l)).to(dev).to(torch.bfloat16)
+            y = torch.full((1, L.H), float("nan"), device=dev)
+            ids = torch.empty((1, L.K), dtype=torch.int32, device=dev)
+            w = torch.empty((1, L.K), device=dev)
+            m.forward(xd.data_ptr(), 1, y.data_ptr(), ids.data_ptr(), w.data_ptr(), None, bf16=True, stream=stream())
+            assert m.status(stream()) == 0
+            base.append((y.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy()))
+    for m in ms:
+        m.close()
+    host = _pinned_bank(Ls)
+    usage = str(tmp_path / "usage.waste")
+    configs = [(n_layers * 64, 0, 0, None, usage), (24, 2, 6, None, None), (16, 0, 0, None, None),
+               (16, 2, 6, None, None), (24, 2, 0, None, None), (24, 2, 6, usage, None)]
+    for n_slots, depth, look, warm, save in configs:
+        outs, st, warmed = _run_cached(Ls, host, tokens, n_slots, depth, look, warm=warm, save=save)
+        say(f"  slots {n_slots} depth {depth} look {look} warm {warmed}: hits {st['hits']} misses {st['misses']}")
+        if warm:
+            assert warmed == 24
+        for k, (a, b) in enumerate(zip(base, outs)):
+            assert np.array_equal(a[1], b[1]), (n_slots, depth, look, k)
+            assert np.array_equal(bits(a[0]), bits(b[0])) and np.array_equal(bits(a[2]), bits(b[2])), \
+                (n_slots, depth, look, k)
+
+
+def test_warm_fills_slots(orc, tmp_path):
+    """A warmed cache's slots hold the records the usage file names before
+    any demand: each slot, bound to a layer, passes the device header
+    check and dequantises bit-exactly to the record's matrices."""
+    say("test_warm_fills_slots")
+    import struct
+    Ls = [dsv3_layer(l, 820 + l) for l in range(2)]
+    host = _pinned_bank(Ls)
+    rec, E = Ls[0].rec_bytes, Ls[0].E
+    path = str(tmp_path / "u.waste")
+    picks = [(1, 5, 40), (0, 3, 30), (1, 63, 20), (0, 0, 10), (5, 1, 5)]     # (5, 1): not in the source
+    with open(path, "wb") as f:
+        f.write(struct.pack("<IIQ", 0x47535557, 1, 9))
+        for layer, e, hits in picks:
+            f.write(struct.pack("<HHIII", layer, e, hits, 1, 0))
+    cache = warp_amd.ExpertCache(rec, 8 * rec, policy=0, depth=0)
+    cache.set_source([host.data_ptr() + i * rec for i in range(2 * E)], 2, E)
+    assert cache.warm(path) == 4
+    ms = [gpu_layer(L, records=False) for L in Ls]
+    dev = torch.device("cuda:0")
+    s = stream()
+    for i, (layer, e, _) in enumerate(picks[:4]):
+        assert cache.slot(layer, e) == i
+        L, m = Ls[layer], ms[layer]
+        p = cache.get(layer, e, s)
+        assert p
+        assert m.bind_table([e], [p], codebook_id=L.cb_base, stream=s) == 0
+        books = orc.books(L.books_f16)[0]
+        for kind, (M, N) in enumerate(L.shapes):
+            W = torch.empty((M, N), device=dev)
+            assert m.dequant(e, kind, W.data_ptr(), s) == 0
+            off = [48, 48 + L.I * L.H * 3 // 8, 48 + 2 * L.I * L.H * 3 // 8][kind]
+            want = orc.dequant(L.records[e][off:], L.scales[e][kind], books, 3 * kind, M, N)
+            assert np.array_equal(bits(W.cpu().numpy()), bits(want)), (layer, e, kind)
+        assert m.status(s) == 0
+        cache.release(s)
+    st = cache.stats()
+    assert st["hits"] == 4 and st["misses"] == 0 and st["reads"] == 0
+    for m in ms:
+        m.close()
+    cache.close()

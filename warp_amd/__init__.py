@@ -24,10 +24,12 @@ SCORE_SIGMOID, SCORE_SOFTMAX, SCORE_SQRTSOFTPLUS = 0, 1, 2
 
 ERRORS = {0: "ok", -1: "EINVAL", -2: "ENODEV", -3: "ENOMEM", -4: "ERECORD", -5: "ECRC",
           -6: "EUNBOUND", -7: "EROUTE", -8: "EDEVICE", -9: "ERANGE", -10: "ETIMEOUT",
-          -11: "ESCRATCH"}
+          -11: "ESCRATCH", -12: "EFORMAT", -13: "EIO"}
 
 OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE, ERANGE, ETIMEOUT, ESCRATCH = \
     0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11
+EFORMAT, EIO = -12, -13
+CT_RECORDS, CT_GROUP_LIMIT = 1, 2
 
 # Every symbol include/waste_hip.h declares.
 EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_host_buffers",
@@ -45,7 +47,12 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_ecache_hold", "waste_hip_ecache_release", "waste_hip_ecache_admit",
            "waste_hip_ecache_resident_mask", "waste_hip_ecache_resident_all",
            "waste_hip_ecache_stats", "waste_hip_ecache_slot", "waste_hip_ecache_n_slots",
-           "waste_hip_ecache_sync"]
+           "waste_hip_ecache_sync", "waste_hip_moe_set_codebooks_at",
+           "waste_hip_container_open", "waste_hip_container_close", "waste_hip_container_config",
+           "waste_hip_container_bank", "waste_hip_container_codebooks", "waste_hip_container_read_expert",
+           "waste_hip_container_read_bank", "waste_hip_container_error", "waste_hip_container_tensor",
+           "waste_hip_container_moe", "waste_hip_crc32", "waste_hip_ecache_save_usage",
+           "waste_hip_ecache_warm"]
 
 STAGES = ["router_shared_gate_up", "route", "routed_gate_up", "swiglu", "routed_down",
           "shared_down", "combine"]
@@ -76,6 +83,15 @@ class EcacheCounts(C.Structure):
     _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("evictions", C.c_uint64),
                 ("prefetched", C.c_uint64), ("spec_issued", C.c_uint64), ("reads", C.c_uint64),
                 ("bytes_read", C.c_uint64)]
+
+
+class ContainerCfg(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layers", "hidden", "vocab", "n_experts", "top_k", "moe_inter",
+                                       "n_shared", "first_dense", "latent_dim", "score_func", "renorm")] + \
+               [("routed_scale", C.c_float)] + \
+               [(n, C.c_int) for n in ("n_group", "topk_group", "stages", "vec_dim", "entries", "index_bits",
+                                       "index_block", "n_books", "n_tensors")] + \
+               [("prefix", C.c_char * 64)]
 
 
 class VqJob(C.Structure):
@@ -139,6 +155,20 @@ def lib():
         "waste_hip_ecache_slot": (i, [vp, i, i]),
         "waste_hip_ecache_n_slots": (i, [vp]),
         "waste_hip_ecache_sync": (i, [vp]),
+        "waste_hip_moe_set_codebooks_at": (i, [vp, vp, i, i]),
+        "waste_hip_container_open": (i, [C.c_char_p, i, C.POINTER(vp)]),
+        "waste_hip_container_close": (None, [vp]),
+        "waste_hip_container_config": (i, [vp, C.POINTER(ContainerCfg)]),
+        "waste_hip_container_bank": (i, [vp, i, ip, ip, C.POINTER(C.c_size_t)]),
+        "waste_hip_container_codebooks": (vp, [vp, ip]),
+        "waste_hip_container_read_expert": (i, [vp, i, i, vp, C.c_size_t]),
+        "waste_hip_container_read_bank": (i, [vp, i, vp, C.c_size_t]),
+        "waste_hip_container_error": (i, [vp, ip, ip]),
+        "waste_hip_container_tensor": (i, [vp, C.c_char_p, C.POINTER(HipTensor), ip, ip]),
+        "waste_hip_container_moe": (i, [vp, i, i, i, i, C.POINTER(vp)]),
+        "waste_hip_crc32": (C.c_uint32, [C.c_uint32, vp, C.c_size_t]),
+        "waste_hip_ecache_save_usage": (i, [vp, C.c_char_p, C.c_uint64]),
+        "waste_hip_ecache_warm": (i, [vp, C.c_char_p]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -202,9 +232,17 @@ class MoeLayer:
         a, b, c = _tensor(g), _tensor(u), _tensor(d)
         check(self.L.waste_hip_moe_set_shared(self.h, C.byref(a), C.byref(b), C.byref(c)), "set_shared")
 
-    def set_codebooks(self, books_f16):
+    @classmethod
+    def _adopt(cls, h):
+        """Owns a handle another call created (Container.moe)."""
+        self = cls.__new__(cls)
+        self.L, self.h, self.cfg = lib(), h, None
+        return self
+
+    def set_codebooks(self, books_f16, first=0):
         b = np.ascontiguousarray(books_f16, np.uint16)
-        check(self.L.waste_hip_moe_set_codebooks(self.h, b.ctypes.data, b.shape[0]), "set_codebooks")
+        check(self.L.waste_hip_moe_set_codebooks_at(self.h, b.ctypes.data, first, b.shape[0]),
+              "set_codebooks")
 
     def set_expert(self, e, record):
         buf = np.frombuffer(record, np.uint8)
@@ -343,3 +381,117 @@ class ExpertCache:
 
     def sync(self):
         check(self.L.waste_hip_ecache_sync(self.h), "sync")
+
+    def save_usage(self, path, tokens):
+        return self.L.waste_hip_ecache_save_usage(self.h, os.fsencode(path), tokens)
+
+    def warm(self, path):
+        """Records loaded from a usage file (>= 0), or a negative code."""
+        return self.L.waste_hip_ecache_warm(self.h, os.fsencode(path))
+
+
+def crc32(data, crc=0):
+    """zlib's crc32 as the library computes it."""
+    b = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data)
+    return int(lib().waste_hip_crc32(crc, b.ctypes.data if b.size else None, b.nbytes))
+
+
+class TrunkTensor:
+    """A trunk tensor read from a container (copies of its payloads)."""
+
+    def __init__(self, ht, ndim, shape):
+        self.fmt, self.rows, self.cols, self.group = ht.fmt, ht.rows, ht.cols, ht.group
+        self.rowbytes = ht.rowbytes
+        self.shape = tuple(shape[:ndim])
+        if ht.fmt == WQ_F32:
+            self.q = np.ctypeslib.as_array(C.cast(ht.q, C.POINTER(C.c_float)),
+                                           (ht.rows * ht.cols,)).copy().reshape(ht.rows, ht.cols)
+            self.qs = None
+        else:
+            ng = (ht.cols + ht.group - 1) // ht.group
+            self.q = np.ctypeslib.as_array(C.cast(ht.q, C.POINTER(C.c_uint8)),
+                                           (ht.rows * ht.rowbytes,)).copy().reshape(ht.rows, ht.rowbytes)
+            self.qs = np.ctypeslib.as_array(C.cast(ht.qs, C.POINTER(C.c_uint16)),
+                                            (ht.rows * ng,)).copy().reshape(ht.rows, ng)
+
+
+class Container:
+    """A WARP container directory opened read-only (waste_hip_container)."""
+
+    def __init__(self, path, verify=False):
+        self.L = lib()
+        h = C.c_void_p()
+        check(self.L.waste_hip_container_open(os.fsencode(path), int(verify), C.byref(h)),
+              "waste_hip_container_open")
+        self.h = h
+
+    def close(self):
+        if self.h:
+            self.L.waste_hip_container_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def config(self):
+        c = ContainerCfg()
+        check(self.L.waste_hip_container_config(self.h, C.byref(c)), "config")
+        out = {k: getattr(c, k) for k, _ in ContainerCfg._fields_}
+        out["prefix"] = c.prefix.decode()
+        return out
+
+    def bank(self, layer):
+        """(n_experts, codebook_base, rec_bytes), or None without a bank."""
+        n, cb, rb = C.c_int(), C.c_int(), C.c_size_t()
+        if self.L.waste_hip_container_bank(self.h, layer, C.byref(n), C.byref(cb), C.byref(rb)):
+            return None
+        return n.value, cb.value, rb.value
+
+    def codebooks(self):
+        n = C.c_int()
+        p = self.L.waste_hip_container_codebooks(self.h, C.byref(n))
+        c = self.config()
+        per = c["entries"] * c["vec_dim"]
+        if not n.value:
+            return np.zeros((0, c["entries"], c["vec_dim"]), np.uint16)
+        a = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), (n.value * per,))
+        return a.copy().reshape(n.value, c["entries"], c["vec_dim"])
+
+    def read_expert(self, layer, expert, dst=None):
+        """(rc, record bytes as uint8)."""
+        b = self.bank(layer)
+        rb = b[2] if b else 4096
+        buf = np.zeros(rb, np.uint8) if dst is None else dst
+        rc = self.L.waste_hip_container_read_expert(self.h, layer, expert, buf.ctypes.data, buf.nbytes)
+        return rc, buf
+
+    def read_bank(self, layer, dst):
+        """Every record of the layer into dst (an object with .ctypes/.nbytes,
+        or an integer address and size as (addr, nbytes))."""
+        if isinstance(dst, tuple):
+            return self.L.waste_hip_container_read_bank(self.h, layer, dst[0], dst[1])
+        return self.L.waste_hip_container_read_bank(self.h, layer, dst.ctypes.data, dst.nbytes)
+
+    def error(self):
+        lay, exp = C.c_int(), C.c_int()
+        rc = self.L.waste_hip_container_error(self.h, C.byref(lay), C.byref(exp))
+        return rc, lay.value, exp.value
+
+    def tensor(self, name):
+        ht = HipTensor()
+        nd = C.c_int()
+        sh = (C.c_int * 4)()
+        check(self.L.waste_hip_container_tensor(self.h, name.encode(), C.byref(ht), C.byref(nd), sh),
+              f"tensor {name}")
+        return TrunkTensor(ht, nd.value, list(sh))
+
+    def moe(self, layer, *, max_tokens=1, prefill_min_tokens=0, records=True, group_limit=False):
+        """A MoeLayer for container layer `layer`."""
+        h = C.c_void_p()
+        flags = (CT_RECORDS if records else 0) | (CT_GROUP_LIMIT if group_limit else 0)
+        check(self.L.waste_hip_container_moe(self.h, layer, max_tokens, prefill_min_tokens, flags,
+                                             C.byref(h)), "waste_hip_container_moe")
+        return MoeLayer._adopt(h)

@@ -202,7 +202,7 @@ typedef struct {
     const uint8_t *rec[WHIP_BIND_MAX];
     uint32_t layer, rec_4k_blocks, off_up, off_down, off_sc;
     int cb;                        /* required codebook id, -1 any          */
-    int n_books;
+    int book0, n_books;            /* ids the layer holds: [book0, n_books - 9] */
 } whip_bind_args;
 int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err, hipStream_t s);
 

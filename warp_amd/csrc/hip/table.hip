@@ -35,7 +35,8 @@ k_bind(const uint8_t **__restrict__ recs, whip_bind_args a, int *__restrict__ er
     const bool ok = magic == WASTE_MAGIC_EXPERT && layer == a.layer && eid == (uint32_t)e &&
                     fmt == WQ_VQ3R && lowrank == 0 && q1.x == a.rec_4k_blocks && q1.y == 48u &&
                     q1.z == a.off_up && q1.w == a.off_down && q2.x == a.off_sc &&
-                    (a.cb < 0 || cb == (uint32_t)a.cb) && (long)cb + 9L <= (long)a.n_books;
+                    (a.cb < 0 || cb == (uint32_t)a.cb) && (long)cb >= (long)a.book0 &&
+                    (long)cb + 9L <= (long)a.n_books;
     recs[e] = ok ? r : nullptr;
     if (!ok) atomicOr(err, 8);
 }

@@ -31,6 +31,7 @@
 #include "waste_hip.h"
 
 #include <hip/hip_runtime_api.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -157,15 +158,19 @@ static int victim(waste_hip_ecache *c)
     return best;
 }
 
-/* Copy (layer, expert) into slot si after the slot's last reader. */
-static int start_fill(waste_hip_ecache *c, int si, int layer, int expert)
+/* The host copy of (layer, expert), or NULL when the source has none. */
+static const void *source_of(const waste_hip_ecache *c, int layer, int expert)
 {
-    c->st.reads++;
-    c->st.bytes_read += c->rec_bytes;
-    if (c->dry) return 0;
-    const void *src = NULL;
     if (c->src && layer >= 0 && layer < c->src_layers && expert >= 0 && expert < c->src_experts)
-        src = c->src[(size_t)layer * c->src_experts + expert];
+        return c->src[(size_t)layer * c->src_experts + expert];
+    return NULL;
+}
+
+/* Copy (layer, expert) into slot si after the slot's last reader. */
+static int copy_in(waste_hip_ecache *c, int si, int layer, int expert)
+{
+    if (c->dry) return 0;
+    const void *src = source_of(c, layer, expert);
     slot_t *q = &c->slot[si];
     if (!src) goto fail;
     if (q->use && hipStreamWaitEvent(c->fill, c->ring[q->use % RING], 0) != hipSuccess) goto fail;
@@ -186,6 +191,13 @@ static int start_fill(waste_hip_ecache *c, int si, int layer, int expert)
 fail:
     c->failed = 1;
     return -1;
+}
+
+static int start_fill(waste_hip_ecache *c, int si, int layer, int expert)
+{
+    c->st.reads++;
+    c->st.bytes_read += c->rec_bytes;
+    return copy_in(c, si, layer, expert);
 }
 
 /* Give slot si to key: the engine's claim (hits 1, last = now). */
@@ -513,4 +525,124 @@ int waste_hip_ecache_sync(waste_hip_ecache *c)
     if (c->failed) return WASTE_HIP_EDEVICE;
     if (c->dry || !c->fill) return WASTE_HIP_OK;
     return hipStreamSynchronize(c->fill) == hipSuccess ? WASTE_HIP_OK : WASTE_HIP_EDEVICE;
+}
+
+/* ---- the learned hotlist (src/ecache.c:825-913) --------------------------
+ *
+ * usage.waste: a 16-byte header (magic "WUSG", version 1, tokens) and one
+ * 16-byte entry per resident record (layer, expert, hits, last use, a
+ * coupling field written as 0; src/waste_format.h:169-187). */
+
+typedef struct {
+    uint32_t magic, version;
+    uint64_t tokens;
+} usage_hdr;
+
+typedef struct {
+    uint16_t layer, expert;
+    uint32_t hits, last, next_top;
+} usage_ent;
+
+#define MAGIC_USAGE 0x47535557u
+#define USAGE_MAX_ENTRIES (1u << 26)
+
+int waste_hip_ecache_save_usage(const waste_hip_ecache *c, const char *path, uint64_t tokens)
+{
+    if (!c || !path) return WASTE_HIP_EINVAL;
+    if (c->n_slots <= 0) return WASTE_HIP_OK;
+    FILE *f = fopen(path, "wb");
+    if (!f) return WASTE_HIP_EIO;
+    const usage_hdr h = { MAGIC_USAGE, 1, tokens };
+    int bad = fwrite(&h, sizeof h, 1, f) != 1;
+    for (int i = 0; i < c->n_slots && !bad; i++) {
+        const slot_t *q = &c->slot[i];
+        if (q->key < 0 || q->state != S_READY) continue;
+        usage_ent e;
+        e.layer = (uint16_t)((uint32_t)q->key >> 16);
+        e.expert = (uint16_t)(q->key & 0xFFFF);
+        e.hits = q->hits;
+        e.last = (uint32_t)q->last;
+        e.next_top = 0;
+        bad = fwrite(&e, sizeof e, 1, f) != 1;
+    }
+    if (fclose(f) != 0) bad = 1;
+    if (bad) {
+        remove(path);
+        return WASTE_HIP_EIO;
+    }
+    return WASTE_HIP_OK;
+}
+
+/* hits descending, then (layer, expert): a file warms the same way every
+ * run (src/ecache.c:852-862) */
+static int hotter(const void *a, const void *b)
+{
+    const usage_ent *x = (const usage_ent *)a, *y = (const usage_ent *)b;
+    if (x->hits != y->hits) return x->hits > y->hits ? -1 : 1;
+    if (x->layer != y->layer) return x->layer < y->layer ? -1 : 1;
+    if (x->expert != y->expert) return x->expert < y->expert ? -1 : 1;
+    return 0;
+}
+
+int waste_hip_ecache_warm(waste_hip_ecache *c, const char *path)
+{
+    if (!c || !path) return WASTE_HIP_EINVAL;
+    if (c->n_slots <= 0) return 0;
+    FILE *f = fopen(path, "rb");
+    if (!f) return WASTE_HIP_EIO;
+    usage_hdr h;
+    if (fread(&h, sizeof h, 1, f) != 1 || h.magic != MAGIC_USAGE) {
+        fclose(f);
+        return WASTE_HIP_EFORMAT;
+    }
+    long n = 0;
+    if (fseek(f, 0, SEEK_END) == 0) {
+        const long end = ftell(f);
+        n = end > (long)sizeof h ? (end - (long)sizeof h) / (long)sizeof(usage_ent) : 0;
+    }
+    if (n <= 0) {
+        fclose(f);
+        return 0;
+    }
+    if ((unsigned long)n > USAGE_MAX_ENTRIES) {
+        fclose(f);
+        return WASTE_HIP_EFORMAT;
+    }
+    usage_ent *ent = (usage_ent *)malloc((size_t)n * sizeof *ent);
+    if (!ent || fseek(f, (long)sizeof h, SEEK_SET) != 0 || fread(ent, sizeof *ent, (size_t)n, f) != (size_t)n) {
+        free(ent);
+        fclose(f);
+        return ent ? WASTE_HIP_EIO : WASTE_HIP_ENOMEM;
+    }
+    fclose(f);
+    qsort(ent, (size_t)n, sizeof *ent, hotter);
+    const int want = n < c->n_slots ? (int)n : c->n_slots;
+    int loaded = 0;
+    for (int i = 0; i < want; i++) {
+        const int32_t key = key_of(ent[i].layer, ent[i].expert);
+        if (lookup(c, key) >= 0) continue;
+        const int vi = victim(c);
+        if (vi < 0) break;
+        /* a record the source does not have is stale, not an error: skipped
+         * before its slot is touched, as a failed fetch is */
+        if (c->src && !source_of(c, ent[i].layer, ent[i].expert)) continue;
+        if (!c->dry && !c->src) continue;
+        slot_t *q = &c->slot[vi];
+        if (q->key >= 0) h_erase(c, q->key);
+        if (vi >= c->n_used) c->n_used = vi + 1;
+        q->key = key;
+        h_insert(c, key, vi);
+        q->state = S_READY;
+        q->fresh = 0;
+        q->pin = 0;
+        q->hits = ent[i].hits;
+        q->last = ++c->clock;
+        if (copy_in(c, vi, ent[i].layer, ent[i].expert)) {
+            free(ent);
+            return WASTE_HIP_EDEVICE;
+        }
+        loaded++;
+    }
+    free(ent);
+    return loaded;
 }

@@ -61,7 +61,8 @@ struct waste_hip_moe {
     uint8_t *slab;               /* owned records, E x rec_bytes (lazy)    */
     float *d_books, *d_booksT;
     uint16_t *d_books16;         /* fp16, subnormals flushed (prefill)     */
-    int n_books;
+    int n_books;                 /* books held, ids [book0, book0 + n_books) */
+    int book0;
     whip_mat router, sh[3];
     void *router_mem, *sh_mem[3];
     float *d_bias;
@@ -98,21 +99,10 @@ static float f16_book(uint16_t h)
     return f;
 }
 
-static uint32_t crc32_z(const uint8_t *p, size_t n)
+/* The layer's codebook id is known and its nine books are on the device. */
+static int books_ok(const waste_hip_moe *m)
 {
-    static uint32_t tab[256];
-    static int ready = 0;
-    if (!ready) {
-        for (uint32_t i = 0; i < 256; i++) {
-            uint32_t c = i;
-            for (int k = 0; k < 8; k++) c = (c & 1) ? 0xEDB88320u ^ (c >> 1) : c >> 1;
-            tab[i] = c;
-        }
-        ready = 1;
-    }
-    uint32_t c = 0xFFFFFFFFu;
-    for (size_t i = 0; i < n; i++) c = tab[(c ^ p[i]) & 0xff] ^ (c >> 8);
-    return c ^ 0xFFFFFFFFu;
+    return m->cb >= m->book0 && m->cb + 9 <= m->book0 + m->n_books;
 }
 
 static int dmalloc(void **p, size_t n)
@@ -321,7 +311,13 @@ int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
 
 int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16, int n_books)
 {
-    if (!m || !f16 || n_books < 9) return WASTE_HIP_EINVAL;
+    return waste_hip_moe_set_codebooks_at(m, f16, 0, n_books);
+}
+
+int waste_hip_moe_set_codebooks_at(waste_hip_moe *m, const uint16_t *f16, int first, int n_books)
+{
+    if (!m || !f16 || n_books < 9 || first < 0 || first > 65535 || n_books > 65536 + 9) return WASTE_HIP_EINVAL;
+    if (m->cb >= 0 && (m->cb < first || m->cb + 9 > first + n_books)) return WASTE_HIP_ERECORD;
     const size_t per = 256 * 8;
     float *b = (float *)malloc((size_t)n_books * per * 4);
     float *bt = (float *)malloc((size_t)n_books * per * 4);
@@ -350,6 +346,7 @@ int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16, int n_boo
     free(b); free(bt); free(h16);
     if (rc) return rc;
     m->n_books = n_books;
+    m->book0 = first;
     return 0;
 }
 
@@ -365,7 +362,8 @@ static int check_record(const waste_hip_moe *m, int expert, const uint8_t *rec, 
     if (h.layer != (uint16_t)m->c.layer || h.expert_id != (uint16_t)expert) return WASTE_HIP_ERECORD;
     if ((size_t)h.rec_4k_blocks * WASTE_ALIGN != rec_bytes) return WASTE_HIP_ERECORD;
     if (h.fmt != WQ_VQ3R || h.lowrank_id != 0) return WASTE_HIP_ERECORD;
-    if (m->n_books && (long)h.codebook_id + 9L > m->n_books) return WASTE_HIP_ERECORD;
+    if (m->n_books && (h.codebook_id < m->book0 || (long)h.codebook_id + 9L > (long)m->book0 + m->n_books))
+        return WASTE_HIP_ERECORD;
     if (!(h.gate_off == 48 && h.gate_off < h.up_off && h.up_off < h.down_off &&
           h.down_off < h.chan_corr_off && h.chan_corr_off <= rec_bytes))
         return WASTE_HIP_ERECORD;
@@ -377,7 +375,7 @@ static int check_record(const waste_hip_moe *m, int expert, const uint8_t *rec, 
     if (m->cb >= 0 && h.codebook_id != m->cb) return WASTE_HIP_ERECORD;
     if (verify) {
         const size_t payload = (size_t)h.chan_corr_off + scales - sizeof h;
-        if (crc32_z(rec + sizeof h, payload) != h.crc32) return WASTE_HIP_ECRC;
+        if (waste_hip_crc32(0, rec + sizeof h, payload) != h.crc32) return WASTE_HIP_ECRC;
     }
     return 0;
 }
@@ -486,14 +484,14 @@ static int experts_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
     memset(&a, 0, sizeof a);
     a.recs = m->d_recs; a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.sc_off[0] = m->off_sc; a.sc_off[1] = m->off_sc + 2u * (uint32_t)I;
-    a.books16 = m->d_books16; a.cb = m->cb;
+    a.books16 = m->d_books16; a.cb = m->cb - m->book0;
     a.N = I; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H; a.tok = m->b.pair_tok;
     a.seg_off = m->seg_off; a.order = m->order; a.out = m->h16; a.out_ld = I; a.err = m->err;
     CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 1, 4, E, mb, s));
     MARK(3);
     MARK(4);
     a.idx_off[0] = m->off_down; a.idx_off[1] = 0;
-    a.sc_off[0] = m->off_sc + 4u * (uint32_t)I; a.sc_off[1] = 0; a.cb = m->cb + 6;
+    a.sc_off[0] = m->off_sc + 4u * (uint32_t)I; a.sc_off[1] = 0; a.cb = m->cb - m->book0 + 6;
     a.N = H; a.Kd = I; a.x = m->h16; a.x_mode = 2; a.x_ld = I; a.tok = NULL;
     a.out = m->ypair; a.out_ld = H;
     CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 0, 4, E, mb, s));
@@ -581,7 +579,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     memset(&a, 0, sizeof a);
     a.recs = m->d_recs; a.pair_exp = m->b.pair_exp; a.pair_src = m->b.pair_tok;
     a.pair_rec = (T == 1 && m->pair_rec_ok) ? m->b.pair_rec : NULL;
-    a.src = x; a.src_ld = H; a.src_bf16 = x_bf16; a.booksT = m->d_booksT; a.cb = m->cb;
+    a.src = x; a.src_ld = H; a.src_bf16 = x_bf16; a.booksT = m->d_booksT; a.cb = m->cb - m->book0;
     a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.kinds = 2; a.M = I; a.nv = m->nv_gu; a.P = P; a.rsplit = m->rsplit_gu;
     a.part = m->b.part_gu; a.err = m->err;
@@ -618,7 +616,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
         CK((hipError_t)whip_vq_act(m->d_recs, m->b.pair_exp, P, m->b.part_gu, m->nch_gu, I, m->off_sc,
                                    m->b.h, s));
     MARK(4);
-    a.pair_src = NULL; a.src = m->b.h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb + 6;
+    a.pair_src = NULL; a.src = m->b.h; a.src_ld = I; a.src_bf16 = 0; a.cb = m->cb - m->book0 + 6;
     if (act_fused) {
         a.act_part = m->b.part_gu; a.act_nch = m->nch_gu;
         a.out_sc_off = m->off_sc + 4u * (uint32_t)I;  /* the down partials leave scaled too */
@@ -686,7 +684,7 @@ int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     const int rc = ready(m, x, T);
     if (rc) return rc;
     if (!y || T != m->routed_T) return WASTE_HIP_EINVAL;
-    if (m->cb < 0 || m->cb + 9 > m->n_books) return WASTE_HIP_EINVAL;
+    if (!books_ok(m)) return WASTE_HIP_EINVAL;
     hipStream_t s = (hipStream_t)stream;
     return T > m->Td ? experts_many(m, x, x_bf16, T, y, s) : experts_few(m, x, x_bf16, T, y, s);
 }
@@ -708,7 +706,7 @@ static int forward_one(waste_hip_moe *m, const void *x, int x_bf16, float *y, in
     a.router = m->router; a.bias = m->d_bias;
     a.has_shared = m->has_shared;
     if (m->has_shared) { a.sh[0] = m->sh[0]; a.sh[1] = m->sh[1]; a.sh[2] = m->sh[2]; }
-    a.recs = m->d_recs; a.booksT = m->d_booksT; a.cb = m->cb;
+    a.recs = m->d_recs; a.booksT = m->d_booksT; a.cb = m->cb - m->book0;
     a.off_gate = m->off_gate; a.off_up = m->off_up; a.off_down = m->off_down; a.off_sc = m->off_sc;
     a.logits = logits ? logits : m->b.logits;
     a.ids = ids ? ids : m->b.ids;
@@ -747,7 +745,7 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
 {
     int rc = ready(m, x, T);
     if (rc) return rc;
-    if (!y || m->cb < 0 || m->cb + 9 > m->n_books) return WASTE_HIP_EINVAL;
+    if (!y || !books_ok(m)) return WASTE_HIP_EINVAL;
     if (T == 1) {
         m->routed_T = 0;
         rc = forward_one(m, x, x_bf16, y, ids, w, logits, (hipStream_t)stream);
@@ -806,7 +804,7 @@ int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, in
 {
     int rc = ready(m, x, T);
     if (rc) return rc;
-    if (!y || m->cb < 0 || m->cb + 9 > m->n_books) return WASTE_HIP_EINVAL;
+    if (!y || !books_ok(m)) return WASTE_HIP_EINVAL;
     if (T > m->Td || static_layout(m, T, NULL, NULL) > WHIP_SCRATCH_BYTES)
         return WASTE_HIP_ESCRATCH;
     hipStream_t s = (hipStream_t)stream;
@@ -847,6 +845,8 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *c
     }
     if (codebook_id >= 0) {
         if (m->cb >= 0 && m->cb != codebook_id) return WASTE_HIP_ERECORD;
+        if (m->n_books && (codebook_id < m->book0 || codebook_id + 9 > m->book0 + m->n_books))
+            return WASTE_HIP_ERECORD;
         m->cb = codebook_id;
     }
     a.n = n;
@@ -854,7 +854,8 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *c
     a.rec_4k_blocks = (uint32_t)(m->rec_bytes / 4096);
     a.off_up = m->off_up; a.off_down = m->off_down; a.off_sc = m->off_sc;
     a.cb = m->cb;
-    a.n_books = m->n_books > 0 ? m->n_books : 65536 + 9;
+    a.book0 = m->n_books > 0 ? m->book0 : 0;
+    a.n_books = m->n_books > 0 ? m->book0 + m->n_books : 65536 + 9;
     CK((hipError_t)whip_bind(m->d_recs, &a, m->err, (hipStream_t)stream));
     m->pair_rec_ok = 0;
     for (int i = 0; i < n; i++) {
@@ -911,7 +912,7 @@ int waste_hip_moe_forward_cached(waste_hip_moe *m, waste_hip_ecache *c, int laye
 {
     if (!m || !c || !x || !y || layer < 0 || layer > 32767 || lookahead < 0 || lookahead > 64)
         return WASTE_HIP_EINVAL;
-    if (m->cb < 0) return WASTE_HIP_EINVAL;
+    if (!books_ok(m)) return WASTE_HIP_EINVAL;
     hipStream_t s = (hipStream_t)stream;
     const int K = m->K;
     if (!m->h_sel && hipHostMalloc((void **)&m->h_sel, 128 * sizeof(int32_t), hipHostMallocDefault) != hipSuccess) {
@@ -994,14 +995,14 @@ size_t waste_hip_moe_bytes(const waste_hip_moe *m, int T, int n_distinct)
 int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W, void *stream)
 {
     if (!m || expert < 0 || expert >= m->E || kind < 0 || kind > 2 || !W || !m->d_books ||
-        m->cb < 0 || m->cb + 9 > m->n_books)
+        !books_ok(m))
         return WASTE_HIP_EINVAL;
     const uint8_t *rec = m->h_recs[expert];
     if (!rec) return WASTE_HIP_EUNBOUND;
     const int M = kind == 2 ? m->H : m->I, N = kind == 2 ? m->I : m->H;
     const uint32_t off = kind == 0 ? m->off_gate : kind == 1 ? m->off_up : m->off_down;
     const uint16_t *sc = (const uint16_t *)(rec + m->off_sc) + (kind == 0 ? 0 : kind == 1 ? m->I : 2 * m->I);
-    CK((hipError_t)whip_dequant(rec + off, sc, m->d_books, m->cb + 3 * kind, M, N, W,
+    CK((hipError_t)whip_dequant(rec + off, sc, m->d_books, m->cb - m->book0 + 3 * kind, M, N, W,
                                 (hipStream_t)stream));
     return 0;
 }
