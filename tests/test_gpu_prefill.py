@@ -114,3 +114,21 @@ def test_prefill_unbound_expert(orc):
     rc, ref = ol.apply(X, ids, w_masked, chunk=1)
     assert rc == 0
     assert rel_err(y2, ref) <= LAYER_RTOL
+
+
+def test_prefill_out_of_fp16_range(orc):
+    """Tokens whose activations (2^17 x N(0,1): beyond 65504) or SwiGLU
+    outputs (2^11 x N(0,1) inputs) leave fp16's range: the chunk runs again
+    on the fp32 decode kernels with the routing it has, so the status is
+    clean and every output matches the oracle's moe_chunk."""
+    say("test_prefill_out_of_fp16_range")
+    L, X, bf16 = make_case("dsv3_small", 64)
+    X = X.copy()
+    X[[3, 40]] *= np.float32(2.0 ** 11)
+    X[17] *= np.float32(2.0 ** 17)
+    m = gpu_layer(L, max_tokens=64, prefill_min=16)
+    st, y, ids, w, lg = run_forward(torch, m, L, X, bf16)
+    m.close()
+    assert st == 0, warp_amd.ERRORS.get(st, st)
+    assert float(np.abs(X).max()) > 65504.0
+    check_layer(orc, L, X, bf16, y, ids, w, lg, "dsv3_small T=64, tokens out of fp16 range")

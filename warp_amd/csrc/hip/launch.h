@@ -205,6 +205,8 @@ typedef struct {
     int book0, n_books;            /* ids the layer holds: [book0, n_books - 9] */
 } whip_bind_args;
 int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err, hipStream_t s);
+/* err &= ~mask, in stream order. */
+int whip_err_clear(int *err, int mask, hipStream_t s);
 
 /* One token: the router (job 0; its y = the logits, E rows) and up to two
  * more batch-1 products (the shared expert's gate/up) in one launch, and

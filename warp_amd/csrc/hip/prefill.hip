@@ -18,7 +18,8 @@
 // (row, position) vector of the container, which the lane decodes itself —
 // VQ3R: C0[i0] + (C1[i1] + C2[i2]) from the fp16 codebooks in LDS (the
 // container stores them in fp16, subnormals flushed as the engine's loader
-// does); Q4G / Q8G: the integer times its group scale.  Row scales of VQ3R
+// does), summed in fp32 and rounded once; Q4G / Q8G: the integer times its
+// group scale.  Row scales of VQ3R
 // apply in the epilogue, exactly, in fp32.  A (activations) is staged in LDS
 // per 64-wide k chunk, converted to fp16; a value outside fp16's range
 // raises the sticky range error instead of turning into inf.
@@ -153,6 +154,27 @@ WH_INLINE _Float16 to_h(float v, bool &bad)
 
 WH_INLINE h8 as_h8(uint4 u) { return __builtin_bit_cast(h8, u); }
 WH_INLINE uint4 as_u4(h8 h) { return __builtin_bit_cast(uint4, h); }
+
+// One VQ3R weight vector from its three fp16 codebook rows: C0 + (C1 + C2)
+// summed in fp32 (exact for the books' magnitudes) and rounded to fp16 once,
+// the nearest fp16 to the container's fp32 weight/scale (docs/FORMAT.md:
+// 204-214).  Two fp16 additions would round twice, which doubled the
+// products' error.  Each element is two mixed-precision fmas (fp16 sources
+// read in place, fp32 arithmetic, the second rounding straight to fp16): the
+// 1.0 they multiply by is opaque to the compiler, which would otherwise
+// rewrite them as conversions and adds (five instructions an element).
+WH_INLINE h8 vq_sum3(h8 c0, h8 c1, h8 c2)
+{
+    float one;
+    asm volatile("v_mov_b32 %0, 1.0" : "=v"(one));
+    h8 w;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float t = __builtin_fmaf((float)c1[i], one, (float)c2[i]);
+        w[i] = (_Float16)__builtin_fmaf((float)c0[i], one, t);
+    }
+    return w;
+}
 
 template <int DEC, int EPI, int MT>
 __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
@@ -323,7 +345,7 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
                 const h8 c0 = as_h8(bk[u & 255]);
                 const h8 c1 = as_h8(bk[256 + ((u >> 8) & 255)]);
                 const h8 c2 = as_h8(bk[512 + ((u >> 16) & 255)]);
-                b = c0 + (c1 + c2);
+                b = vq_sum3(c0, c1, c2);
             } else if (DEC == DEC_Q4) {
                 const _Float16 sc = __builtin_bit_cast(_Float16, bs[st]);
                 const uint32_t u = bw[st][0];
@@ -551,7 +573,7 @@ k_pf_gemm4(whip_pf_args a)
                 const h8 c0 = as_h8(bk[u[st][j] & 255]);
                 const h8 c1 = as_h8(bk[256 + ((u[st][j] >> 8) & 255)]);
                 const h8 c2 = as_h8(bk[512 + ((u[st][j] >> 16) & 255)]);
-                b[j] = c0 + (c1 + c2);
+                b[j] = vq_sum3(c0, c1, c2);
             }
 #pragma unroll
             for (int t = 0; t < MT; t++) {

@@ -48,3 +48,17 @@ extern "C" int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err
     hipLaunchKernelGGL(k_bind, dim3(1), dim3(64), 0, s, recs, *a, err);
     return (int)hipGetLastError();
 }
+
+// Clears bits of the layer's error word in stream order (after the
+// kernels that may have raised them, before the ones that may raise them
+// again), so a host that reads the word and retries needs no copy.
+__global__ void __launch_bounds__(64) k_err_clear(int *__restrict__ err, int mask)
+{
+    if (threadIdx.x == 0) atomicAnd(err, ~mask);
+}
+
+extern "C" int whip_err_clear(int *err, int mask, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_err_clear, dim3(1), dim3(64), 0, s, err, mask);
+    return (int)hipGetLastError();
+}

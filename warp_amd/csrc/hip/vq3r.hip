@@ -255,6 +255,31 @@ struct tile_map {
     }
 };
 
+// A wavefront's position in the tile order, advanced without division: the
+// tile index t and its (pair, kind, chunk, row block).  Divisions by values
+// known only at run time cost tens of scalar instructions each, and the
+// sixteen wavefronts of a workgroup share one scalar unit, so decoding every
+// tile from its index serialised the wavefronts' first loads (measured: the
+// last wavefront's tiles went out 5 us after the first's).  A cursor starts
+// from one decode, done by a lane of the first wavefront in the prologue.
+struct tile_cur {
+    int t, p, kind, chunk, rb;
+    __device__ __forceinline__ void step(const tile_map &tm, int P, int n)
+    {
+        t += n;
+        rb += n;
+        while (rb >= tm.nb) {                        // uniform
+            rb -= tm.nb;
+            if (tm.span) {
+                if (++p == P) { p = 0; if (++chunk == tm.nch) { chunk = 0; ++kind; } }
+            } else if (++chunk == tm.nch) {
+                chunk = 0;
+                if (++kind == tm.kinds) { kind = 0; ++p; }
+            }
+        }
+    }
+};
+
 // Every global load below is unconditional (clamped addresses, selects
 // instead of branches): the hardware counts loads in issue order, and a
 // load on only one side of a branch leaves the compiler unsure how many are
@@ -278,6 +303,7 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     __shared__ const uint8_t *s_rec[SPAN_MAX];       // records of pairs p_lo ..
     __shared__ int s_xr[SPAN_MAX];                   // and their source rows
     __shared__ float s_h[256];                       // x of a class reduced from partials (act_part)
+    __shared__ int4 s_cur[2 * LW];                   // tiles t0 + i decoded: (p, kind, chunk, rb)
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int v = lane & 31, h = lane >> 5;
     const int wk = a.kinds == 2 ? 1 : 2;             // trace row of this pass
@@ -324,11 +350,10 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     // tile t of a class ending at hi -> uniform bases of its index bytes
     // (or the dummy, past the class) and output block
     // (out_sc_off: and the f16 scales of its 64 rows, else the dummy)
-    auto where = [&](int t, int hi, g_u8 *&src, float *&out, bool &live, g_u16 *&scb) {
+    auto where = [&](const tile_cur &c, int hi, g_u8 *&src, float *&out, bool &live, g_u16 *&scb) {
         scb = (g_u16 *)dummy;
-        if (t >= hi) { src = dummy; out = sink; live = true; return; }
-        int p, kind, chunk, rb;
-        tm.at(t, p, kind, chunk, rb);
+        if (c.t >= hi) { src = dummy; out = sink; live = true; return; }
+        const int p = c.p, kind = c.kind, chunk = c.chunk, rb = c.rb;
         const uint8_t *rec = uni(s_rec[p - p_lo]);
         live = rec != nullptr;
         src = rec ? as_global(rec) + a.idx_off[kind] + (size_t)rb * rstride + (size_t)chunk * PW * 192 : dummy;
@@ -470,11 +495,24 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         const int myxr = a.pair_src ? xq : q;
         build_loads(t0, (ACT || SPAN) ? 0 : (a.pair_src ? xf : p_first));
         if (tid <= p_hi - p_lo) { s_rec[tid] = myrec; s_xr[tid] = myxr; }
+        if (tid < 2 * LW) {                          // each wavefront's first two tiles
+            int cp, ck, cc, cr;
+            tm.at(t0 + tid, cp, ck, cc, cr);
+            s_cur[tid] = make_int4(cp, ck, cc, cr);
+        }
     }
     __syncthreads();
     stage(t0);
     WT_KEEP(1);
     int t = t0 + wv;
+    tile_cur cA, cB;                                 // the tiles buffers A and B hold
+    {
+        const int4 qa = s_cur[wv], qb = s_cur[wv + LW];
+        cA.t = t; cA.p = __builtin_amdgcn_readfirstlane(qa.x); cA.kind = __builtin_amdgcn_readfirstlane(qa.y);
+        cA.chunk = __builtin_amdgcn_readfirstlane(qa.z); cA.rb = __builtin_amdgcn_readfirstlane(qa.w);
+        cB.t = t + LW; cB.p = __builtin_amdgcn_readfirstlane(qb.x); cB.kind = __builtin_amdgcn_readfirstlane(qb.y);
+        cB.chunk = __builtin_amdgcn_readfirstlane(qb.z); cB.rb = __builtin_amdgcn_readfirstlane(qb.w);
+    }
     tile_buf A, B;
     g_u8 *src;
     g_u16 *scb;
@@ -497,10 +535,10 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         // trade roles: that would be a register copy, which waits for the
         // loads in flight.  The first two go out before the tables (the
         // earlier the loads go out the better: measured).
-        where(t, hi, src, outA, liveA, scb);
+        where(cA, hi, src, outA, liveA, scb);
         load_tile(A, src, loff);
         scA = scb[presc ? lrow : 0];
-        where(t + LW, hi, src, outB, liveB, scb);
+        where(cB, hi, src, outB, liveB, scb);
         load_tile(B, src, loff);
         scB = scb[presc ? lrow : 0];
         if (lo == t0) WT_KEEP(2);
@@ -515,14 +553,16 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             r = presc ? __fmul_rn(r, wh_f16_scale(scA)) : r;
             __builtin_nontemporal_store(liveA ? r : 0.0f, outA + lrow);
             unbound |= !liveA;
-            where(t + 2 * LW, hi, src, outA, liveA, scb);
+            cA.step(tm, a.P, 2 * LW);
+            where(cA, hi, src, outA, liveA, scb);
             load_tile(A, src, loff);
             scA = scb[presc ? lrow : 0];
             r = tile_sum(B, smem, bA0, bA1, bB, s0, s1, s2, lane);
             r = presc ? __fmul_rn(r, wh_f16_scale(scB)) : r;
             __builtin_nontemporal_store(liveB ? r : 0.0f, outB + lrow);
             unbound |= !liveB;
-            where(t + 3 * LW, hi, src, outB, liveB, scb);
+            cB.step(tm, a.P, 2 * LW);
+            where(cB, hi, src, outB, liveB, scb);
             load_tile(B, src, loff);
             scB = scb[presc ? lrow : 0];
             t += 2 * LW;
@@ -533,6 +573,11 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             __builtin_nontemporal_store(liveA ? r : 0.0f, outA + lrow);
             unbound |= !liveA;
             t += LW;
+            // the next tile of this wavefront is the one B holds; A's next, past it
+            const tile_cur c = cB;
+            cB = cA;
+            cB.step(tm, a.P, 2 * LW);
+            cA = c;
         }
         lo = hi;
     }

@@ -76,6 +76,9 @@ struct waste_hip_moe {
     float *plogits, *pw;         /* the lookahead's logits and weights      */
     int routed_T;                /* T of the last route(), 0 none          */
     int32_t *h_sel;              /* pinned: selection [0,64), lookahead [64,128) */
+    int *h_err;                  /* pinned: the error word, read after a chunk */
+    int32_t *r_ids;              /* the last route's ids and weights (device) */
+    float *r_w;
     int pair_rec_ok;             /* pair_rec matches the table (no bind since) */
     int sh_done;                 /* the route's launch ran the shared down  */
     int sh_in_combine;           /* the combine runs the shared down        */
@@ -141,6 +144,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
         for (int i = 0; i < 2 * WASTE_HIP_STAGES; i++) hipEventDestroy(m->kev[i]);
     }
     if (m->h_sel) hipHostFree(m->h_sel);
+    if (m->h_err) hipHostFree(m->h_err);
     free(m->h_recs);
     free(m);
 }
@@ -676,7 +680,56 @@ int waste_hip_moe_route(waste_hip_moe *m, const void *x, int x_bf16, int T, int3
                             : route_few(m, x, x_bf16, T, d_ids, d_w, lg, s);
     if (r) return r;
     m->routed_T = T;
+    m->r_ids = d_ids;
+    m->r_w = d_w;
     return 0;
+}
+
+/* A chunk whose fp16 operands left fp16's range (an activation or a SwiGLU
+ * output beyond 65504: the matrix-core kernels raise bit 4 and their
+ * outputs are not to be used) runs again on the fp32 decode kernels, Td
+ * tokens at a time, with the routing it already has: the shared expert's
+ * gate/up (fp32), the sub-chunk's pair lists, then the experts, their
+ * combine and the shared down projection.  The host reads the error word
+ * after the chunk for this; a stream being captured into a graph cannot
+ * wait, so there the bit stays raised for waste_hip_moe_status. */
+static int range_fallback(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return 0;
+    if (!m->h_err && hipHostMalloc((void **)&m->h_err, sizeof(int), hipHostMallocDefault) != hipSuccess) {
+        m->h_err = NULL;
+        return WASTE_HIP_ENOMEM;
+    }
+    CK(hipMemcpyAsync(m->h_err, m->err, sizeof(int), hipMemcpyDeviceToHost, s));
+    CK(hipStreamSynchronize(s));
+    if (!(*m->h_err & 4)) return 0;
+    CK((hipError_t)whip_err_clear(m->err, 4, s));
+    const int K = m->K, H = m->H, Td = m->Td, prof = m->prof_on;
+    const size_t esz = x_bf16 ? 2 : 4;
+    m->prof_on = 0;
+    int rc = 0;
+    for (int t0 = 0; t0 < T && !rc; t0 += Td) {
+        const int n = T - t0 < Td ? T - t0 : Td;
+        const void *xs = (const uint8_t *)x + (size_t)t0 * H * esz;
+        if (m->has_shared) {
+            whip_gemv_job j;
+            j.A = m->sh[0]; j.B = &m->sh[1]; j.x = xs; j.x_ld = H; j.x_bf16 = x_bf16;
+            j.y = m->b.h_sh; j.y_ld = m->SI;
+            if (whip_gemv_multi(&j, 1, n, s)) { rc = WASTE_HIP_EDEVICE; break; }
+        }
+        if (whip_pairs(m->r_ids + (size_t)t0 * K, m->r_w + (size_t)t0 * K, n, K, m->E, m->b.pair_tok,
+                       m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, s)) {
+            rc = WASTE_HIP_EDEVICE;
+            break;
+        }
+        m->sh_done = 0;
+        m->sh_in_combine = 0;
+        m->pair_rec_ok = 0;
+        rc = experts_few(m, xs, x_bf16, n, y + (size_t)t0 * H, s);
+    }
+    m->prof_on = prof;
+    return rc;
 }
 
 int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, void *stream)
@@ -686,7 +739,9 @@ int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     if (!y || T != m->routed_T) return WASTE_HIP_EINVAL;
     if (!books_ok(m)) return WASTE_HIP_EINVAL;
     hipStream_t s = (hipStream_t)stream;
-    return T > m->Td ? experts_many(m, x, x_bf16, T, y, s) : experts_few(m, x, x_bf16, T, y, s);
+    if (T <= m->Td) return experts_few(m, x, x_bf16, T, y, s);
+    const int r = experts_many(m, x, x_bf16, T, y, s);
+    return r ? r : range_fallback(m, x, x_bf16, T, y, s);
 }
 
 /* T == 1 in two launches: the router and the shared expert's gate/up
