@@ -201,6 +201,70 @@ void orc_vq_rows(float *y, const uint8_t *idx, const uint16_t *scale,
     }
 }
 
+/* VQ4P's int8 table, src/model.c:3979-4074 (vq_quant_range's scalar
+ * loop; its NEON loop is documented there as value-for-value equal): per
+ * block of ORC_VQ_LUT_BLK positions, scale = max|lut| / 127 and
+ * q = lrintf(lut * (127 / max)) clamped to [-127, 127] (0 for an all-zero
+ * block); lrintf rounds half to even in the default mode. */
+void orc_vq_quant_lut(const float *lut, int nv, int stages, int entries,
+                      int8_t *q, float *scale)
+{
+    const int st = stages, en = entries;
+    for (int blk = 0; blk < (nv + ORC_VQ_LUT_BLK - 1) / ORC_VQ_LUT_BLK; blk++) {
+        const int v0 = blk * ORC_VQ_LUT_BLK;
+        const int v1 = v0 + ORC_VQ_LUT_BLK < nv ? v0 + ORC_VQ_LUT_BLK : nv;
+        const size_t n = (size_t)(v1 - v0) * st * en;
+        const float *src = lut + (size_t)v0 * st * en;
+        int8_t *dst = q + (size_t)v0 * st * en;
+        float mx = 0;
+        for (size_t i = 0; i < n; i++) {
+            const float f = fabsf(src[i]);
+            if (f > mx) mx = f;
+        }
+        scale[blk] = mx / 127.0f;
+        const float inv = mx > 0 ? 127.0f / mx : 0.0f;
+        for (size_t i = 0; i < n; i++) {
+            int t = (int)lrintf(src[i] * inv);
+            if (t > 127) t = 127;
+            else if (t < -127) t = -127;
+            dst[i] = (int8_t)t;
+        }
+    }
+}
+
+/* VQ4P rows, src/model.c:4076-4114 (waste_vq_rows_p6, ORC_PORTABLE) and
+ * src/simd_avx512.c:129-236 (vq_rows_p6_avx512, ORC_AVX512): four 6-bit
+ * codes per (row, position) packed in three bytes (src/simd.h:73-76), the
+ * stages' int8 entries summed exactly per block of ORC_VQ_LUT_BLK
+ * positions (at most 4 * 32 * 127, so int16 holds it), then
+ * acc += lscale[blk] * sum in block order: a product and a sum in the
+ * portable C kernel, one fused multiply-add where the compiler contracts it
+ * (the AVX-512 file, built with FMA available); y = acc * f16(scale). */
+void orc_vq_rows_p6(float *y, const uint8_t *idx, const uint16_t *scale,
+                    const int8_t *lut8, const float *lscale, int r_lo,
+                    int r_hi, int nv, int order)
+{
+    const int en = 64;
+    for (int r = r_lo; r < r_hi; r++) {
+        float acc = 0.0f;
+        const uint8_t *base = idx + (size_t)(r / 64) * nv * 64 * 3 + (size_t)(r % 64) * 3;
+        for (int v0 = 0; v0 < nv; v0 += ORC_VQ_LUT_BLK) {
+            const int v1 = v0 + ORC_VQ_LUT_BLK < nv ? v0 + ORC_VQ_LUT_BLK : nv;
+            int16_t sum = 0;
+            for (int v = v0; v < v1; v++) {
+                const uint8_t *ix = base + (size_t)v * 64 * 3;
+                const unsigned b0 = ix[0], b1 = ix[1], b2 = ix[2];
+                const int8_t *T = lut8 + (size_t)v * 4 * en;
+                sum = (int16_t)(sum + T[b0 & 0x3f] + T[en + (((b0 >> 6) | (b1 << 2)) & 0x3f)] +
+                                T[2 * en + (((b1 >> 4) | (b2 << 4)) & 0x3f)] + T[3 * en + ((b2 >> 2) & 0x3f)]);
+            }
+            const float ls = lscale[v0 / ORC_VQ_LUT_BLK];
+            acc = order == ORC_AVX512 ? fmaf(ls, (float)sum, acc) : acc + ls * (float)sum;
+        }
+        y[r] = acc * orc_f16_scale(scale[r]);
+    }
+}
+
 /* The dequantised matrix in closed form (docs/FORMAT.md:204-214; the
  * Python oracle's Container.expert, tools/kimi_ref.py:240-273):
  *   W[r][8v+d] = (((0 + C0[i0][d]) + C1[i1][d]) + C2[i2][d]) * f16(scale[r])

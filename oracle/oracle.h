@@ -57,6 +57,14 @@ void orc_vq_rows(float *y, const uint8_t *idx, const uint16_t *scale,
 void orc_dequant(float *W, const uint8_t *idx, const uint16_t *scale,
                  const float *books, int cb_base, int M, int N, int stages,
                  int entries, int vec_dim);
+/* VQ4P (6-bit indices, 4 stages of 64 entries): the int8 shadow of a LUT,
+ * one fp32 scale per ORC_VQ_LUT_BLK positions, and the rows through it. */
+#define ORC_VQ_LUT_BLK 32
+void orc_vq_quant_lut(const float *lut, int nv, int stages, int entries,
+                      int8_t *q, float *scale);
+void orc_vq_rows_p6(float *y, const uint8_t *idx, const uint16_t *scale,
+                    const int8_t *lut8, const float *lscale, int r_lo,
+                    int r_hi, int nv, int order);
 void orc_mvq_rows(float *y, const int8_t *W, const uint16_t *ws,
                   const float *x, int r_lo, int r_hi, int in, int group,
                   int bits, size_t rowbytes, int order);

@@ -35,6 +35,7 @@ int ref_init(void)
     ref_portable = waste_k;
     ref_portable.mvq_rows_f32 = waste_mvq_rows_f32;
     ref_portable.lutb_range = waste_lutb_range;
+    ref_portable.vq_rows_p6 = waste_vq_rows_p6;
     ref_ready = (waste_k.lutb_range != waste_lutb_range) ? 2 : 1;
     return ref_ready;   /* 2: this host runs the AVX-512 kernels */
 }
@@ -52,6 +53,28 @@ void ref_vq_rows(float *y, const uint8_t *idx, const uint16_t *scale,
 {
     vq_arg a = { y, idx, scale, lut, nv, stages, entries };
     vq_rows(0, M, &a);
+}
+
+/* VQ4P: the engine's LUT quantisation (static in model.c) and its
+ * vq_rows_p6 slot as installed for the order (the portable C kernel, or the
+ * AVX-512 VBMI one on a host that has it). */
+void ref_vq_quant_lut(const float *lut, int nv, int st, int en, int8_t *q, float *scale)
+{
+    vq_quant_lut(lut, nv, st, en, q, scale);
+}
+
+void ref_vq_rows_p6(float *y, const uint8_t *idx, const uint16_t *scale, const int8_t *lut8,
+                    const float *lscale, int M, int nv)
+{
+    vqp_arg a = { y, idx, scale, lut8, lscale, nv };
+    waste_k.vq_rows_p6(0, M, &a);
+}
+
+/* 1 when this host's engine runs the AVX-512 VBMI VQ4P kernel */
+int ref_vq_p6_fast(void)
+{
+    ref_init();
+    return ref_avx512.vq_rows_p6 != waste_vq_rows_p6;
 }
 
 void ref_lutb(float *lut, const float *booksT, const float *x, int cb_base,

@@ -95,30 +95,24 @@ template <typename T> __device__ __forceinline__ void coh_st(T *p, T v)
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int NPL, bool COH = false>
+// One token's selection by one wavefront from its logits in registers:
+// lane L holds experts L*NPL .. L*NPL+NPL-1 (sc: their logits; entries past
+// E are ignored).  Lane p < K returns the p-th selected expert (myid, -1
+// when fewer than K experts are candidates: err bit 2) and its weight.
+// Every wavefront that runs it for one token computes the same values, so a
+// workgroup of several wavefronts may run it (its barriers then meet).
+template <int NPL>
 __device__ __forceinline__ void
-route_body(const whip_route_cfg &c, const float *__restrict__ logits, const float *__restrict__ bias,
-           int T, int t, int L, int32_t *__restrict__ ids, float *__restrict__ wout,
-           int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp, float *__restrict__ pair_w,
-           int32_t *__restrict__ tok_pairs, const uint8_t *const *__restrict__ recs,
-           const uint8_t **__restrict__ pair_rec, int *__restrict__ err, float *lds,
-           const uint64_t *etab = nullptr)
+route_wave(const whip_route_cfg &c, float (&sc)[NPL], const float *__restrict__ bias, int L,
+           int *__restrict__ err, float *lds, const uint64_t *et, int &myid, float &myw)
 {
-    const uint64_t *et = etab ? etab : wh_exp_tab;
     float *s_v = lds, *s_g = lds + 64 * NPL;
     int *s_keep = (int *)(lds + 64 * NPL + 64);
     const int E = c.E, K = c.K;
-    const float *lg = logits + (size_t)t * E;
-    float sc[NPL], sel[NPL];
+    float sel[NPL];
 #pragma unroll
-    for (int j = 0; j < NPL; j++) {
-        const int e = L * NPL + j;
-        const int ec = e < E ? e : 0;
-        const float l = COH ? coh_ld(lg + ec) : lg[ec];
-        sc[j] = e < E ? l : 0.0f;
-    }
+    for (int j = 0; j < NPL; j++) sc[j] = L * NPL + j < E ? sc[j] : 0.0f;
 
-    WT(0, 8);
     if (c.score_func == 1) {
         // max (order-free), then the engine's sum in expert order
         float mx = -1e30f;
@@ -154,7 +148,6 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         sel[j] = e < E ? __fadd_rn(sc[j], bias ? bias[e] : 0.0f) : NEG_INF;
     }
 
-    WT(0, 9);
     if (c.n_group > 1) {
         // a group's score: the sum of its two largest values above -inf
         // (-inf when it has fewer); keep the topk_group groups that come
@@ -222,13 +215,14 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         }
     }
 
-    WT(0, 10);
     uint64_t key[NPL];
 #pragma unroll
     for (int j = 0; j < NPL; j++) key[j] = L * NPL + j < E ? sel_key(sel[j], L * NPL + j) : 0;
 
-    float wsum = 0.0f, myw = 0.0f;
-    int myid = -1, ok = 1;
+    float wsum = 0.0f;
+    int ok = 1;
+    myw = 0.0f;
+    myid = -1;
     for (int p = 0; p < K; p++) {
         uint64_t best = key[0];
 #pragma unroll
@@ -248,7 +242,6 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         wsum = __fadd_rn(wsum, wf);
         if (L == p) { myid = e; myw = wf; }
     }
-    WT(0, 11);
     if (ok) {
         if (c.renorm && K > 1) myw = __fdiv_rn(myw, __fadd_rn(wsum, 1e-20f));
         myw = __fmul_rn(myw, c.routed_scale);
@@ -257,6 +250,31 @@ route_body(const whip_route_cfg &c, const float *__restrict__ logits, const floa
         myw = 0.0f;
         if (L == 0) atomicOr(err, 2);
     }
+}
+
+template <int NPL, bool COH = false>
+__device__ __forceinline__ void
+route_body(const whip_route_cfg &c, const float *__restrict__ logits, const float *__restrict__ bias,
+           int T, int t, int L, int32_t *__restrict__ ids, float *__restrict__ wout,
+           int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp, float *__restrict__ pair_w,
+           int32_t *__restrict__ tok_pairs, const uint8_t *const *__restrict__ recs,
+           const uint8_t **__restrict__ pair_rec, int *__restrict__ err, float *lds,
+           const uint64_t *etab = nullptr)
+{
+    const uint64_t *et = etab ? etab : wh_exp_tab;
+    const int E = c.E, K = c.K;
+    const float *lg = logits + (size_t)t * E;
+    float sc[NPL];
+#pragma unroll
+    for (int j = 0; j < NPL; j++) {
+        const int e = L * NPL + j;
+        const int ec = e < E ? e : 0;
+        const float l = COH ? coh_ld(lg + ec) : lg[ec];
+        sc[j] = e < E ? l : 0.0f;
+    }
+    int myid;
+    float myw;
+    route_wave<NPL>(c, sc, bias, L, err, lds, et, myid, myw);
     if (L < K) {
         ids[(size_t)t * K + L] = myid;
         wout[(size_t)t * K + L] = myw;
@@ -524,7 +542,7 @@ __device__ __forceinline__ void route_wg(const whip_route_cfg &c, float l, float
 //    lane) with a bitonic network on lane moves; the wavefronts' first K
 //    are then sorted once more by wavefront 0.  Keys are distinct, so the
 //    order of the sorted keys is the engine's selection order.
-// LDS: ROUTE_FAST_FLOATS(E) floats at lds (8-byte aligned).  E <= 64 * 64 / K
+// LDS: ROUTE_FAST_FLOATS(E) floats at lds (16-byte aligned).  E <= 64 * 64 / K
 // (the candidates fit one wavefront).  Results in s_ids/s_w/s_rec (K <= 64
 // entries; ids -1, weights 0, records NULL and err bit 2 when fewer than K
 // experts are candidates).  Every thread calls it.
@@ -593,11 +611,10 @@ __device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, flo
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, E = c.E, K = c.K;
     const int ewv = (E + 63) >> 6;                           // wavefronts holding experts
     uint64_t *s_cand = (uint64_t *)lds;                      // [64] the wavefronts' first K
-    float *s_sc = lds + 128;                                 // [E]
-    float *s_sel = s_sc + E;                                 // [E] (group scan fallback)
-    float *s_g = s_sel + E;                                  // [64] group scores
+    float *s_g = lds + 128;                                  // [64] group scores (16-byte aligned)
     float *s_part = s_g + 64;                                // [NWV + 1] softmax
-    float *s_wraw = s_part + 64;                             // [64]
+    float *s_sc = s_part + 64;                               // [E]
+    float *s_sel = s_sc + E;                                 // [E] (group scan fallback)
     // scores
     float sc = 0.0f;
     if (tid < E) {
@@ -669,12 +686,17 @@ __device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, flo
         }
         __syncthreads();
         if (tid < E) {
+            // every group's score, four to a 16-byte read (s_g has 64
+            // entries; those past G are not compared)
             const int g = (gs & (gs - 1)) == 0 ? tid >> gsh : tid / gs;
             const float mine = s_g[g];
             int rk = 0;
-            for (int k = 0; k < G; k++) {
-                const float o = s_g[k];
-                rk += (o > NEG_INF) && before(o, k, mine, g);
+            for (int k0 = 0; k0 < G; k0 += 8) {
+                const float4 q0 = *(const float4 *)(s_g + k0), q1 = *(const float4 *)(s_g + k0 + 4);
+                const float o[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    rk += (k0 + i < G) && (o[i] > NEG_INF) && before(o[i], k0 + i, mine, g);
             }
             kept = mine > NEG_INF && rk < c.topk_group;
         }
@@ -690,29 +712,27 @@ __device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, flo
     if (wv == 0) {
         const uint64_t cv = lane < (ewv > 1 ? ewv * K : 64) ? s_cand[lane] : 0;
         const uint64_t srt = wave_sort_desc(cv, lane);
-        if (lane < K) {
-            const int e = srt ? (int)~(uint32_t)srt : -1;    // the key's low word is ~id
-            s_ids[lane] = e;
-            s_wraw[lane] = e >= 0 ? s_sc[e] : 0.0f;
-            s_rec[lane] = e >= 0 ? s_tab[e] : nullptr;
-        }
-    }
-    __syncthreads();
-    if (tid < K) {
-        const bool ok = s_ids[K - 1] >= 0;                   // K candidates
+        // lane p < K: the p-th selection; its weight the unbiased score.
+        // The renormalising sum runs in selection order, the engine's, as a
+        // chain over the lanes' values (no LDS round trip per term).
+        const int e = srt ? (int)~(uint32_t)srt : -1;       // the key's low word is ~id
+        const float wr = lane < K && e >= 0 ? s_sc[e] : 0.0f;
+        const bool ok = __builtin_amdgcn_readlane(e, K - 1) >= 0;   // K candidates
         float wsum = 0.0f;
-        for (int p = 0; p < K; p++) wsum = __fadd_rn(wsum, s_wraw[p]);
-        float myw = s_wraw[tid];
+        for (int p = 0; p < K; p++) wsum = __fadd_rn(wsum, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wr), p)));
+        float myw = wr;
         if (ok) {
             if (c.renorm && K > 1) myw = __fdiv_rn(myw, __fadd_rn(wsum, 1e-20f));
             myw = __fmul_rn(myw, c.routed_scale);
         } else {
             myw = 0.0f;
-            s_ids[tid] = -1;
-            s_rec[tid] = nullptr;
-            if (tid == 0) atomicOr(err, 2);
+            if (lane == 0) atomicOr(err, 2);
         }
-        s_w[tid] = myw;
+        if (lane < K) {
+            s_ids[lane] = ok ? e : -1;
+            s_rec[lane] = ok && e >= 0 ? s_tab[e] : nullptr;
+            s_w[lane] = myw;
+        }
     }
     __syncthreads();
 }

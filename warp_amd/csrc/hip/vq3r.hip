@@ -242,44 +242,6 @@ __device__ __forceinline__ void sh_rows8(const whip_mat &W, const float *x, int 
         for (int i = 0; i < 8; i++) shs[w * 8 + i] = acc[i];
 }
 
-// A workgroup's tiles in table order: t -> (pair, kind, chunk, row block).
-// span: classes (kind, chunk), each over every pair's row blocks; else
-// classes (pair, kind, chunk), each over one pair's row blocks.
-struct tile_map {
-    int span, nch, kinds, nb, tpc;
-    __device__ __forceinline__ void at(int t, int &p, int &kind, int &chunk, int &rb) const
-    {
-        const int cls = t / tpc, within = t - cls * tpc;
-        if (span) { kind = cls / nch; chunk = cls - kind * nch; p = within / nb; rb = within - p * nb; }
-        else { p = cls / (kinds * nch); const int r = cls - p * kinds * nch; kind = r / nch; chunk = r - kind * nch; rb = within; }
-    }
-};
-
-// A wavefront's position in the tile order, advanced without division: the
-// tile index t and its (pair, kind, chunk, row block).  Divisions by values
-// known only at run time cost tens of scalar instructions each, and the
-// sixteen wavefronts of a workgroup share one scalar unit, so decoding every
-// tile from its index serialised the wavefronts' first loads (measured: the
-// last wavefront's tiles went out 5 us after the first's).  A cursor starts
-// from one decode, done by a lane of the first wavefront in the prologue.
-struct tile_cur {
-    int t, p, kind, chunk, rb;
-    __device__ __forceinline__ void step(const tile_map &tm, int P, int n)
-    {
-        t += n;
-        rb += n;
-        while (rb >= tm.nb) {                        // uniform
-            rb -= tm.nb;
-            if (tm.span) {
-                if (++p == P) { p = 0; if (++chunk == tm.nch) { chunk = 0; ++kind; } }
-            } else if (++chunk == tm.nch) {
-                chunk = 0;
-                if (++kind == tm.kinds) { kind = 0; ++p; }
-            }
-        }
-    }
-};
-
 // Every global load below is unconditional (clamped addresses, selects
 // instead of branches): the hardware counts loads in issue order, and a
 // load on only one side of a branch leaves the compiler unsure how many are
@@ -350,15 +312,18 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     // tile t of a class ending at hi -> uniform bases of its index bytes
     // (or the dummy, past the class) and output block
     // (out_sc_off: and the f16 scales of its 64 rows, else the dummy)
-    auto where = [&](const tile_cur &c, int hi, g_u8 *&src, float *&out, bool &live, g_u16 *&scb) {
+    auto where_rec = [&](const tile_cur &c, int hi, const uint8_t *rec, g_u8 *&src, float *&out, bool &live,
+                         g_u16 *&scb) {
         scb = (g_u16 *)dummy;
         if (c.t >= hi) { src = dummy; out = sink; live = true; return; }
         const int p = c.p, kind = c.kind, chunk = c.chunk, rb = c.rb;
-        const uint8_t *rec = uni(s_rec[p - p_lo]);
         live = rec != nullptr;
         src = rec ? as_global(rec) + a.idx_off[kind] + (size_t)rb * rstride + (size_t)chunk * PW * 192 : dummy;
         out = a.part + (((size_t)p * a.kinds + kind) * nch + chunk) * (size_t)a.M + rb * 64;
         if (a.out_sc_off && rec) scb = (g_u16 *)(as_global(rec) + a.out_sc_off) + (size_t)kind * a.M + rb * 64;
+    };
+    auto where = [&](const tile_cur &c, int hi, g_u8 *&src, float *&out, bool &live, g_u16 *&scb) {
+        where_rec(c, hi, c.t < hi ? uni(s_rec[c.p - p_lo]) : nullptr, src, out, live, scb);
     };
 
     // act_part: x of class (pair p, chunk) is silu(g) * u for the 256
@@ -475,6 +440,29 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         __syncthreads();
     };
 
+    // With the routing's record list at hand (one token), each wavefront's
+    // first tile goes out first: its record is one scalar load, and the
+    // tile's loads then fly while the build's inputs arrive and the tables
+    // are built (the build's loads go out right behind them: every one of
+    // them is an L2 hit but the partials of a down pass).
+    const bool early = a.pair_rec != nullptr;        // uniform
+    tile_buf A, B;
+    g_u8 *src;
+    g_u16 *scb;
+    float *outA, *outB;
+    uint16_t scA, scB;                               // the lane's row scale of each tile
+    bool liveA, liveB, unbound = false;
+    const bool presc = a.out_sc_off != 0;            // uniform
+    tile_cur cA, cB;                                 // the tiles buffers A and B hold
+    const int hi0 = min(t1, (t0 / tm.tpc + 1) * tm.tpc);
+    if (early) {
+        cA.t = t0 + wv;
+        tm.at(cA.t, cA.p, cA.kind, cA.chunk, cA.rb);
+        const int pc = cA.t < hi0 ? cA.p : p_lo;
+        where_rec(cA, hi0, uni(a.pair_rec[pc]), src, outA, liveA, scb);
+        load_tile(A, src, loff);
+        scA = scb[presc ? lrow : 0];
+    }
     // prologue: the records (one load each: the router wrote them, else
     // through the pair's expert), then the first build's loads
     {
@@ -505,7 +493,6 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     stage(t0);
     WT_KEEP(1);
     int t = t0 + wv;
-    tile_cur cA, cB;                                 // the tiles buffers A and B hold
     {
         const int4 qa = s_cur[wv], qb = s_cur[wv + LW];
         cA.t = t; cA.p = __builtin_amdgcn_readfirstlane(qa.x); cA.kind = __builtin_amdgcn_readfirstlane(qa.y);
@@ -513,13 +500,6 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         cB.t = t + LW; cB.p = __builtin_amdgcn_readfirstlane(qb.x); cB.kind = __builtin_amdgcn_readfirstlane(qb.y);
         cB.chunk = __builtin_amdgcn_readfirstlane(qb.z); cB.rb = __builtin_amdgcn_readfirstlane(qb.w);
     }
-    tile_buf A, B;
-    g_u8 *src;
-    g_u16 *scb;
-    float *outA, *outB;
-    uint16_t scA, scB;                               // the lane's row scale of each tile
-    bool liveA, liveB, unbound = false;
-    const bool presc = a.out_sc_off != 0;            // uniform
     for (int lo = t0; lo < t1;) {
         const int hi = min(t1, (lo / tm.tpc + 1) * tm.tpc);
         if (lo > t0) {                               // uniform: the next class's build inputs
@@ -535,9 +515,11 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         // trade roles: that would be a register copy, which waits for the
         // loads in flight.  The first two go out before the tables (the
         // earlier the loads go out the better: measured).
-        where(cA, hi, src, outA, liveA, scb);
-        load_tile(A, src, loff);
-        scA = scb[presc ? lrow : 0];
+        if (lo > t0 || !early) {                     // uniform: else already in flight
+            where(cA, hi, src, outA, liveA, scb);
+            load_tile(A, src, loff);
+            scA = scb[presc ? lrow : 0];
+        }
         where(cB, hi, src, outB, liveB, scb);
         load_tile(B, src, loff);
         scB = scb[presc ? lrow : 0];

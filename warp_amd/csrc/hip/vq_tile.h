@@ -136,3 +136,40 @@ __device__ __forceinline__ void table_mfma(float *smem, const float *sbook, cons
         }
     }
 }
+
+// A workgroup's tiles in table order: t -> (pair, kind, chunk, row block).
+// span: classes (kind, chunk), each over every pair's row blocks; else
+// classes (pair, kind, chunk), each over one pair's row blocks.
+struct tile_map {
+    int span, nch, kinds, nb, tpc;
+    __device__ __forceinline__ void at(int t, int &p, int &kind, int &chunk, int &rb) const
+    {
+        const int cls = t / tpc, within = t - cls * tpc;
+        if (span) { kind = cls / nch; chunk = cls - kind * nch; p = within / nb; rb = within - p * nb; }
+        else { p = cls / (kinds * nch); const int r = cls - p * kinds * nch; kind = r / nch; chunk = r - kind * nch; rb = within; }
+    }
+};
+
+// A wavefront's position in the tile order, advanced without division: the
+// tile index t and its (pair, kind, chunk, row block).  A division by a value
+// known only at run time is tens of scalar instructions, and the sixteen
+// wavefronts of a workgroup share one scalar unit; a cursor starts from one
+// decode, done by a lane of the first wavefront in the prologue, and then
+// only adds and compares.
+struct tile_cur {
+    int t, p, kind, chunk, rb;
+    __device__ __forceinline__ void step(const tile_map &tm, int P, int n)
+    {
+        t += n;
+        rb += n;
+        while (rb >= tm.nb) {                        // uniform
+            rb -= tm.nb;
+            if (tm.span) {
+                if (++p == P) { p = 0; if (++chunk == tm.nch) { chunk = 0; ++kind; } }
+            } else if (++chunk == tm.nch) {
+                chunk = 0;
+                if (++kind == tm.kinds) { kind = 0; ++p; }
+            }
+        }
+    }
+};
