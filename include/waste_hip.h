@@ -61,8 +61,11 @@ const char *waste_hip_device_name(void);
 /* ---- 1. kernel-table registration ------------------------------------- */
 
 /* Fills t->mvq_rows_f32 with a device implementation (whole range in one
- * call: t->on_device = 1) and t->device_min_bytes; leaves every other slot
- * as it was.  Returns "HIP (gfx950)" or NULL to decline (no device).
+ * call: t->on_device = 1) and t->device_min_bytes, and t->vq_rows_p6 (the
+ * VQ4P apply through the engine's int8 LUT, vqp_arg) with one whose rows
+ * are bit-identical to the CPU kernel it replaces; leaves every other slot
+ * as it was.  A range the device declines or fails goes to that CPU
+ * kernel.  Returns "HIP (gfx950)" or NULL to decline (no device).
  * Replaces: the accelerator registration of src/backend.c:206-216. */
 const char *waste_register_hip(waste_kernels *t);
 
@@ -79,6 +82,35 @@ void waste_hip_release_host_buffers(void);
  * was written and the caller must do them itself.
  * Replaces: waste_metal_vq3r, src/waste_metal.h:31-44. */
 int waste_hip_vq3r(const waste_vq_job *jobs, int n);
+
+/* ---- 2b. VQ4P on device pointers ---------------------------------------- */
+
+/* The int8 shadow of an fp32 LUT [nv][stages][entries] (device pointers):
+ * per block of 32 positions, scale[blk] = max|lut| / 127 and each entry
+ * rint(lut * (127 / max)) clamped to [-127, 127].  Bit-identical to the
+ * engine's quantisation.  q: nv*stages*entries bytes, scale: ceil(nv/32).
+ * Replaces: vq_quant_lut, src/model.c:3979-4074. */
+int waste_hip_vq_quant_lut(const float *lut, int nv, int stages, int entries, int8_t *q,
+                           float *scale, void *stream);
+
+/* Rows [r_lo, r_hi) of a VQ4P matrix (6-bit codes, three bytes per row and
+ * position, 64-row blocks; idx, scale and y indexed from row 0) through
+ * the int8 LUT of nv positions (4 stages x 64 entries each; lut8 16-byte
+ * aligned), device pointers.  order WASTE_HIP_ORDER_PORTABLE folds the
+ * blocks as the portable C kernel does, WASTE_HIP_ORDER_FMA as the AVX-512
+ * and NEON kernels do; either is bit-identical to that kernel.  r_lo a
+ * multiple of 64.
+ * Replaces: the vq_rows_p6 slot, src/model.c:4076-4114,
+ * src/simd_avx512.c:129-236, src/kda_neon.c:100-190. */
+#define WASTE_HIP_ORDER_PORTABLE 0
+#define WASTE_HIP_ORDER_FMA      1
+int waste_hip_vq_rows_p6(const uint8_t *idx, const uint16_t *scale, const int8_t *lut8,
+                         const float *lscale, int r_lo, int r_hi, int nv, int order, float *y,
+                         void *stream);
+
+/* The fold order the vq_rows_p6 slot uses on this host: the one of the CPU
+ * kernel the engine would install (FMA on an AVX-512 VBMI or AArch64 host). */
+int waste_hip_vq_p6_order(void);
 
 /* ---- 3. device MoE layer ------------------------------------------------ */
 

@@ -18,7 +18,14 @@ from), and the reference's outputs:
   exp_x, exp_y  glibc expf on 65,536 seeded inputs and the special values
   ssp_x, ssp_y  router_scores, sqrt-softplus, on special and seeded logits
 
-  python tests/golden/make_golden.py [scalars]
+vq4p.npz (VQ4P, 6-bit codes through the engine's int8 LUT):
+  lut{o}        LUT of x against four 64-entry books, order o
+  q{o}, qs{o}   vq_quant_lut of lut{o}
+  rows{o}       the vq_rows_p6 slot of order o on q{o}/qs{o}
+  qlut, qq, qsc vq_quant_lut of a planted table (an all-zero block, exact
+                halves under a unit inverse, a lone extreme)
+
+  python tests/golden/make_golden.py [scalars|vq4p]
 """
 import hashlib
 import os
@@ -68,6 +75,9 @@ def main():
     if sys.argv[1:] == ["scalars"]:                 # only scalars.npz
         write_scalars(ref)
         return
+    if sys.argv[1:] == ["vq4p"]:                    # only vq4p.npz
+        write_vq4p(orc, ref)
+        return
     if ref.isa != 2:
         print("warning: this host does not run the reference's AVX-512 kernels; order 1 = portable")
     for name in CASES:
@@ -97,6 +107,48 @@ def main():
         print(name, "written")
 
     write_scalars(ref)
+    write_vq4p(orc, ref)
+
+
+def vq4p_inputs(seed=21, M=192, nv=80):
+    """A seeded VQ4P matrix: four 64-entry books of 8 dims (fp16 values,
+    normal), codes as random bytes (every byte triple is four 6-bit codes),
+    f16 row scales, x ~ N(0,1); plus a planted table for the quantiser."""
+    r = np.random.default_rng(seed)
+    books16 = (r.standard_normal((4, 64, 8)) * [[[0.5]], [[0.2]], [[0.08]], [[0.03]]]).astype(np.float16)
+    booksT = np.ascontiguousarray(books16.astype(np.float32).transpose(0, 2, 1)).reshape(-1)
+    x = r.standard_normal(nv * 8).astype(np.float32)
+    idx = r.integers(0, 256, (M // 64) * nv * 192, dtype=np.uint8)
+    scale = (np.abs(r.standard_normal(M)) * 0.02 + 0.005).astype(np.float16).view(np.uint16)
+    # planted quantiser blocks (64 positions x 256 entries): block 0 all
+    # zeros; block 1 holds +-127 once (inverse exactly 1) and halves
+    # (ties to even); the rest seeded
+    qlut = (r.standard_normal((64, 256)) * 3).astype(np.float32)
+    qlut[:32] = 0.0
+    halves = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5], np.float32)
+    qlut[32:64] = r.uniform(-120, 120, (32, 256)).astype(np.float32)
+    qlut[32, :8] = halves
+    qlut[33, 0] = 127.0
+    qlut[40, 5] = -127.0
+    return books16, booksT, x, idx, scale, qlut.reshape(-1), M, nv
+
+
+def write_vq4p(orc, ref):
+    books16, booksT, x, idx, scale, qlut, M, nv = vq4p_inputs()
+    h = hashlib.sha256()
+    for a in (books16, x, idx, scale, qlut):
+        h.update(a.tobytes())
+    out = {"digest": np.array(h.hexdigest()), "isa": np.array(ref.isa), "p6_fast": np.array(ref.lib.ref_vq_p6_fast())}
+    for o in (0, 1):
+        ref.set_order(o)
+        lut = ref.lutb(booksT, x, 0, stages=4, entries=64)
+        q, qs = ref.vq_quant_lut(lut, nv)
+        out[f"lut{o}"], out[f"q{o}"], out[f"qs{o}"] = lut, q, qs
+        out[f"rows{o}"] = ref.vq_rows_p6(idx, scale, q, qs, M, nv)
+    out["qlut"] = qlut
+    out["qq"], out["qsc"] = ref.vq_quant_lut(qlut, 64, 4, 64)
+    np.savez_compressed(os.path.join(HERE, "vq4p.npz"), **out)
+    print("vq4p written")
 
 
 def write_scalars(ref):

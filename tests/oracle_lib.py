@@ -70,6 +70,8 @@ class Oracle:
         _sig(L, "orc_books_load", None, [u16p, C.c_int, C.c_int, C.c_int, fp, fp])
         _sig(L, "orc_lutb", None, [fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int])
         _sig(L, "orc_vq_rows", None, [fp, u8p, u16p, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int])
+        _sig(L, "orc_vq_quant_lut", None, [fp, C.c_int, C.c_int, C.c_int, i8p, fp])
+        _sig(L, "orc_vq_rows_p6", None, [fp, u8p, u16p, i8p, fp, C.c_int, C.c_int, C.c_int, C.c_int])
         _sig(L, "orc_dequant", None, [fp, u8p, u16p, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int])
         _sig(L, "orc_mvq_rows", None, [fp, i8p, u16p, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_size_t, C.c_int])
         _sig(L, "orc_matvec_f32", None, [fp, fp, fp, C.c_int, C.c_int])
@@ -93,6 +95,25 @@ class Oracle:
         _sig(L, "orc_ecache_resident_mask", None, [C.c_void_p, C.c_int, C.c_int, u8p])
         _sig(L, "orc_ecache_stats", None, [C.c_void_p, C.POINTER(C.c_uint64)])
         _sig(L, "orc_predict_next", C.c_int, [C.c_int, C.c_int, fp, fp, C.c_int, i32p])
+
+    def vq_quant_lut(self, lut, nv, stages=4, entries=64):
+        """VQ4P's int8 table and per-32-position scales (src/model.c:3979-4074)."""
+        lut = np.ascontiguousarray(lut, np.float32)
+        q = np.zeros(nv * stages * entries, np.int8)
+        sc = np.zeros((nv + 31) // 32, np.float32)
+        self.lib.orc_vq_quant_lut(ptr(lut, fp), nv, stages, entries, ptr(q, i8p), ptr(sc, fp))
+        return q, sc
+
+    def vq_rows_p6(self, idx, scale, lut8, lscale, M, nv, order, r_lo=0):
+        """VQ4P rows [r_lo, M) through the int8 table (src/model.c:4076-4114)."""
+        idx = np.ascontiguousarray(idx, np.uint8)
+        scale = np.ascontiguousarray(scale, np.uint16)
+        lut8 = np.ascontiguousarray(lut8, np.int8)
+        lscale = np.ascontiguousarray(lscale, np.float32)
+        y = np.zeros(M, np.float32)
+        self.lib.orc_vq_rows_p6(ptr(y, fp), ptr(idx, u8p), ptr(scale, u16p), ptr(lut8, i8p), ptr(lscale, fp),
+                                r_lo, M, nv, order)
+        return y
 
     def ecache_run(self, ops, n_slots, depth, policy, masks=None):
         """Runs a cache script (tests/ecache_script.py) through the
@@ -287,6 +308,9 @@ class Ref:
         _sig(L, "ref_set_order", None, [C.c_int])
         _sig(L, "ref_vq_rows", None, [fp, u8p, u16p, fp, C.c_int, C.c_int, C.c_int, C.c_int])
         _sig(L, "ref_lutb", None, [fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int])
+        _sig(L, "ref_vq_quant_lut", None, [fp, C.c_int, C.c_int, C.c_int, i8p, fp])
+        _sig(L, "ref_vq_rows_p6", None, [fp, u8p, u16p, i8p, fp, C.c_int, C.c_int])
+        _sig(L, "ref_vq_p6_fast", C.c_int, [])
         _sig(L, "ref_mvq_rows", None, [fp, i8p, u16p, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_size_t])
         _sig(L, "ref_matvec_f32", None, [fp, fp, fp, C.c_int, C.c_int])
         _sig(L, "ref_router_scores", None, [C.c_int, fp, fp, C.c_int])
@@ -300,6 +324,23 @@ class Ref:
         _sig(L, "ref_ecache_usage", None, [C.c_char_p, C.c_char_p])
         _sig(L, "ref_ecache_warmed", C.c_int, [])
         self.isa = L.ref_init()
+
+    def vq_quant_lut(self, lut, nv, stages=4, entries=64):
+        lut = np.ascontiguousarray(lut, np.float32)
+        q = np.zeros(nv * stages * entries, np.int8)
+        sc = np.zeros((nv + 31) // 32, np.float32)
+        self.lib.ref_vq_quant_lut(ptr(lut, fp), nv, stages, entries, ptr(q, i8p), ptr(sc, fp))
+        return q, sc
+
+    def vq_rows_p6(self, idx, scale, lut8, lscale, M, nv):
+        """The engine's vq_rows_p6 slot for the current order."""
+        idx = np.ascontiguousarray(idx, np.uint8)
+        scale = np.ascontiguousarray(scale, np.uint16)
+        lut8 = np.ascontiguousarray(lut8, np.int8)
+        lscale = np.ascontiguousarray(lscale, np.float32)
+        y = np.zeros(M, np.float32)
+        self.lib.ref_vq_rows_p6(ptr(y, fp), ptr(idx, u8p), ptr(scale, u16p), ptr(lut8, i8p), ptr(lscale, fp), M, nv)
+        return y
 
     def ecache_run(self, ops, n_slots, depth, policy, warm=None, save=None):
         """The engine's own src/ecache.c on a cache script, reads landing by
@@ -323,10 +364,11 @@ class Ref:
     def set_order(self, order):
         self.lib.ref_set_order(order)
 
-    def lutb(self, booksT, x, cb_base):
+    def lutb(self, booksT, x, cb_base, stages=3, entries=256):
         nv = x.size // 8
-        lut = np.zeros((nv, 3, 256), np.float32)
-        self.lib.ref_lutb(ptr(lut, fp), ptr(booksT, fp), ptr(np.ascontiguousarray(x, np.float32), fp), cb_base, 3, 256, 8, nv)
+        lut = np.zeros((nv, stages, entries), np.float32)
+        self.lib.ref_lutb(ptr(lut, fp), ptr(np.ascontiguousarray(booksT, np.float32), fp),
+                          ptr(np.ascontiguousarray(x, np.float32), fp), cb_base, stages, entries, 8, nv)
         return lut
 
     def vq_rows(self, idx_bytes, scale, lut, M, nv):

@@ -52,7 +52,8 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_container_bank", "waste_hip_container_codebooks", "waste_hip_container_read_expert",
            "waste_hip_container_read_bank", "waste_hip_container_error", "waste_hip_container_tensor",
            "waste_hip_container_moe", "waste_hip_crc32", "waste_hip_ecache_save_usage",
-           "waste_hip_ecache_warm"]
+           "waste_hip_ecache_warm", "waste_hip_vq_quant_lut", "waste_hip_vq_rows_p6",
+           "waste_hip_vq_p6_order"]
 
 STAGES = ["router_shared_gate_up", "route", "routed_gate_up", "swiglu", "routed_down",
           "shared_down", "combine"]

@@ -121,6 +121,21 @@ int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                  const float *part_d, int nch, int H, uint32_t sc_off_down,
                  int skip_zero, const float *sh, float *y, hipStream_t s);
 
+/* ---- VQ4P through the int8 LUT (vq4p.hip) ---- */
+
+/* The int8 shadow of an fp32 LUT [nv][stages][entries]: per block of 32
+ * positions, scale[blk] = max|lut| / 127 and q = rint(lut * (127 / max))
+ * clamped to [-127, 127] (src/model.c:3979-4074). */
+int whip_vq_quant_lut(const float *lut, int nv, int stages, int entries, int8_t *q,
+                      float *scale, hipStream_t s);
+/* Rows [r_lo, r_hi) (r_lo % 64 == 0) of a VQ4P matrix through lut8/lscale
+ * (src/model.c:4076-4114); fma: fold the blocks with one fused
+ * multiply-add (the AVX-512 and NEON kernels) instead of a product and a
+ * sum (the portable C kernel).  lut8 16-byte aligned. */
+int whip_vq_rows_p6(const uint8_t *idx, const uint16_t *scale, const int8_t *lut8,
+                    const float *lscale, int r_lo, int r_hi, int nv, int fma, float *y,
+                    hipStream_t s);
+
 /* ---- many tokens (prefill.hip) ---- */
 
 /* Stable sort of the T*K pairs by expert (id -1 after the last expert);

@@ -2,13 +2,15 @@
 /*
  * backend.c — the engine-facing registration and the VQ3R batch entry.
  *
- * waste_register_hip fills the waste_kernels slot a device backend is
- * meant to fill (the trunk matvec, mvq_rows_f32), marks it on_device so
- * the engine hands it whole row ranges (src/model.c:805-812), and sets
- * device_min_bytes below which the engine keeps the CPU kernel.  It does
- * not touch lutb_range: a host-in/host-out LUT build would spend more on
- * moving the table than the build costs, so that slot stays on the CPU,
- * as it does under the Metal backend (src/metal.m:503-516).
+ * waste_register_hip fills the waste_kernels slots a device backend can
+ * take: the trunk matvec mvq_rows_f32, marked on_device so the engine
+ * hands it whole row ranges (src/model.c:805-812), with device_min_bytes
+ * below which the engine keeps the CPU kernel; and vq_rows_p6, the VQ4P
+ * apply through the engine's int8 LUT, bit-identical to the CPU kernel it
+ * replaces.  It does not touch lutb_range: a host-in/host-out LUT build
+ * would spend more on moving the table than the build costs, so that slot
+ * stays on the CPU, as it does under the Metal backend
+ * (src/metal.m:503-516).
  *
  * Host weights are immutable trunk tensors, so the slot keeps an HBM copy
  * of each one it has seen, keyed by host address and size; the engine
@@ -41,6 +43,9 @@ static void *g_io;               /* staging: x in, y out                   */
 static size_t g_io_cap;
 static void *g_job;              /* staging for the vq3r batch             */
 static size_t g_job_cap;
+static void (*g_cpu_p6)(int b, int e, void *arg);    /* the engine's VQ4P kernel */
+static void *g_p6;               /* staging for the VQ4P slot              */
+static size_t g_p6_cap;
 
 /* The device copy of a host tensor keyed by (host, bytes), NULL when there
  * is none.  A key whose copy is too small is dropped. */
@@ -167,6 +172,84 @@ static void mvq_rows_hip(int b, int e, void *p)
     }
 }
 
+/* The fold order of the CPU VQ4P kernel the engine installs on this host:
+ * its AVX-512 VBMI kernel (x86 hosts with VBMI) and its NEON kernel are
+ * built where the compiler contracts the fold into a fused multiply-add;
+ * the portable C kernel is built without FMA. */
+int waste_hip_vq_p6_order(void)
+{
+#if defined(__x86_64__)
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512vbmi") ? WASTE_HIP_ORDER_FMA : WASTE_HIP_ORDER_PORTABLE;
+#elif defined(__aarch64__)
+    return WASTE_HIP_ORDER_FMA;
+#else
+    return WASTE_HIP_ORDER_PORTABLE;
+#endif
+}
+
+/* The vq_rows_p6 slot: rows [b, e) of a VQ4P matrix through the engine's
+ * int8 LUT (vqp_arg, src/simd.h:57-61).  The engine calls it from its pool
+ * with block-aligned row ranges (src/model.c:4152-4166); each call stages
+ * the ranges' 64-row index blocks, their scales and the table, and copies
+ * the rows back. */
+static void vq_rows_p6_hip(int b, int e, void *p)
+{
+    vqp_arg *a = (vqp_arg *)p;
+    if (e <= b) return;
+    const int nv = a->nv;
+    const int b0 = b & ~63, nblk64 = (e - b0 + 63) / 64, nsb = (nv + 31) / 32;
+    /* the last block may be partial: the engine addresses its rows at the
+     * full block stride but holds no bytes past its last row's codes */
+    const size_t idx_bytes = ((size_t)nblk64 * nv - 1) * 192 + (size_t)(e - b0 - (nblk64 - 1) * 64) * 3;
+    const size_t sc_off = (idx_bytes + 255) / 256 * 256;
+    const size_t lut_off = sc_off + ((size_t)(e - b0) * 2 + 255) / 256 * 256;
+    const size_t ls_off = lut_off + ((size_t)nv * 256 + 255) / 256 * 256;
+    const size_t y_off = ls_off + ((size_t)nsb * 4 + 255) / 256 * 256;
+    const size_t total = y_off + (size_t)(e - b0) * 4;
+    pthread_mutex_lock(&g_mu);
+    uint8_t *d = (uint8_t *)staging(&g_p6, &g_p6_cap, total);
+    int ok = d != NULL;
+    if (ok) ok = hipMemcpyAsync(d, a->idx + (size_t)(b0 / 64) * nv * 192, idx_bytes, hipMemcpyHostToDevice,
+                                g_stream) == hipSuccess;
+    if (ok) ok = hipMemcpyAsync(d + sc_off, a->scale + b0, (size_t)(e - b0) * 2, hipMemcpyHostToDevice,
+                                g_stream) == hipSuccess;
+    if (ok) ok = hipMemcpyAsync(d + lut_off, a->lut8, (size_t)nv * 256, hipMemcpyHostToDevice, g_stream) == hipSuccess;
+    if (ok) ok = hipMemcpyAsync(d + ls_off, a->lscale, (size_t)nsb * 4, hipMemcpyHostToDevice, g_stream) == hipSuccess;
+    if (ok) ok = whip_vq_rows_p6(d, (const uint16_t *)(d + sc_off), (const int8_t *)(d + lut_off),
+                                 (const float *)(d + ls_off), 0, e - b0, nv, waste_hip_vq_p6_order(),
+                                 (float *)(d + y_off), g_stream) == 0;
+    if (ok) ok = hipMemcpyAsync(a->y + b, d + y_off + (size_t)(b - b0) * 4, (size_t)(e - b) * 4,
+                                hipMemcpyDeviceToHost, g_stream) == hipSuccess;
+    if (ok) ok = hipStreamSynchronize(g_stream) == hipSuccess;
+    pthread_mutex_unlock(&g_mu);
+    if (!ok) {
+        if (g_cpu_p6) {
+            g_cpu_p6(b, e, p);
+            return;
+        }
+        const float nan = __builtin_nanf("");
+        for (int r = b; r < e; r++) a->y[r] = nan;
+    }
+}
+
+int waste_hip_vq_quant_lut(const float *lut, int nv, int stages, int entries, int8_t *q, float *scale,
+                           void *stream)
+{
+    if (!lut || !q || !scale || nv <= 0 || stages <= 0 || entries <= 0) return WASTE_HIP_EINVAL;
+    return whip_vq_quant_lut(lut, nv, stages, entries, q, scale, (hipStream_t)stream) ? WASTE_HIP_EDEVICE : 0;
+}
+
+int waste_hip_vq_rows_p6(const uint8_t *idx, const uint16_t *scale, const int8_t *lut8, const float *lscale,
+                         int r_lo, int r_hi, int nv, int order, float *y, void *stream)
+{
+    if (!idx || !scale || !lut8 || !lscale || !y || r_lo < 0 || r_lo % 64 || r_hi <= r_lo || nv <= 0 ||
+        (uintptr_t)lut8 % 16 || (order != WASTE_HIP_ORDER_PORTABLE && order != WASTE_HIP_ORDER_FMA))
+        return WASTE_HIP_EINVAL;
+    return whip_vq_rows_p6(idx, scale, lut8, lscale, r_lo, r_hi, nv, order, y, (hipStream_t)stream)
+               ? WASTE_HIP_EDEVICE : 0;
+}
+
 const char *waste_register_hip(waste_kernels *t)
 {
     pthread_mutex_lock(&g_mu);
@@ -183,6 +266,8 @@ const char *waste_register_hip(waste_kernels *t)
     if (t->mvq_rows_f32 != mvq_rows_hip)
         g_cpu_rows = t->mvq_rows_cpu ? t->mvq_rows_cpu : t->mvq_rows_f32;
     t->mvq_rows_f32 = mvq_rows_hip;
+    if (t->vq_rows_p6 != vq_rows_p6_hip) g_cpu_p6 = t->vq_rows_p6;
+    t->vq_rows_p6 = vq_rows_p6_hip;
     t->on_device = 1;
     /* A synchronous dispatch with two PCIe copies costs tens of us; below
      * a megabyte of weights the CPU pool finishes first. */
