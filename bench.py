@@ -380,8 +380,6 @@ def main():
     ap.add_argument("--stack-tokens", type=int, default=200,
                     help="tokens the 58-layer stack decodes through the HBM expert cache (0: skip)")
     ap.add_argument("--stack-budget-gb", type=float, default=64.0)
-    ap.add_argument("--decode-mode", type=int, default=-1,
-                    help="waste_hip_moe_set_decode mode for the layers (-1: the library default)")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device (a plain copy kernel of known "
                          "size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -400,9 +398,6 @@ def main():
     H, E, K, I = cfg["hidden"], cfg["n_experts"], cfg["top_k"], cfg["moe_inter"]
     B = a.batch
     layers, slab, books, rb, trunk = build_layers(torch, warp_amd, synth, cfg, a.layers, B)
-    if a.decode_mode >= 0:
-        for m in layers:
-            m.set_decode(a.decode_mode)
     if a.copy_calibrate:
         n = a.copy_calibrate << 20
         src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")

@@ -211,17 +211,6 @@ int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, in
  * included); more than 16 MiB means WASTE_HIP_ESCRATCH. */
 size_t waste_hip_moe_static_bytes(const waste_hip_moe *m, int T);
 
-/* How forward() runs T == 1: mode 0 (the default) as the staged kernels
- * route()/experts() run; mode 1 as two launches, the router and the shared
- * expert's gate/up, then every expert stage in one persistent launch whose
- * stages wait for each other through counters in device memory.  Shapes
- * mode 1 does not take (E > 256, K > 16, H or moe_inter not a multiple of
- * 256, an F32 shared down projection) and profiled forwards run staged.
- * Mode 1 holds every CU for the launch: forwards of one layer must not
- * overlap, and other work that holds CUs delays it (past ~50 ms a stage
- * gives up: WASTE_HIP_ETIMEOUT). */
-int waste_hip_moe_set_decode(waste_hip_moe *m, int mode);
-
 /* forward() in two halves, for a caller that must see the selection
  * before the experts run (an expert cache: moe_layer's hint and holds sit
  * between its router and its experts, src/model.c:5639-5700).

@@ -40,7 +40,7 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_moe_profile", "waste_hip_moe_profile_read", "waste_hip_record_bytes",
            "waste_hip_synth_codebooks", "waste_hip_synth_records",
            "waste_hip_moe_route", "waste_hip_moe_experts", "waste_hip_moe_bind_table",
-           "waste_hip_moe_predict", "waste_hip_moe_forward_cached", "waste_hip_moe_set_decode",
+           "waste_hip_moe_predict", "waste_hip_moe_forward_cached",
            "waste_hip_moe_forward_static", "waste_hip_moe_static_bytes",
            "waste_hip_ecache_create", "waste_hip_ecache_destroy", "waste_hip_ecache_set_source",
            "waste_hip_ecache_hint", "waste_hip_ecache_prefetch", "waste_hip_ecache_get",
@@ -138,7 +138,6 @@ def lib():
         "waste_hip_moe_bind_table": (i, [vp, ip, C.POINTER(vp), i, i, vp]),
         "waste_hip_moe_predict": (i, [vp, vp, i, i, vp, vp]),
         "waste_hip_moe_forward_cached": (i, [vp, vp, i, vp, i, vp, i, vp, vp, vp, vp]),
-        "waste_hip_moe_set_decode": (i, [vp, i]),
         "waste_hip_moe_forward_static": (i, [vp, vp, i, i, vp, vp, vp, vp, vp]),
         "waste_hip_moe_static_bytes": (C.c_size_t, [vp, i]),
         "waste_hip_ecache_create": (i, [C.c_size_t, C.c_size_t, i, i, i, C.POINTER(vp)]),
@@ -256,11 +255,6 @@ class MoeLayer:
                 stream=None):
         check(self.L.waste_hip_moe_forward(self.h, x_ptr, int(bf16), T, y_ptr, ids_ptr, w_ptr,
                                            logits_ptr, stream), "forward")
-
-    def set_decode(self, mode):
-        """How forward() runs T == 1: 0 the staged kernels (the default), 1 the
-        persistent experts launch."""
-        check(self.L.waste_hip_moe_set_decode(self.h, int(mode)), "set_decode")
 
     def status(self, stream=None):
         return self.L.waste_hip_moe_status(self.h, stream)

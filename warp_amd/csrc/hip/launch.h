@@ -255,41 +255,6 @@ int whip_route_gemv(const whip_route_cfg *c, const float *logits, const float *b
                     const uint8_t **pair_rec, int *err, const whip_gemv_job *job,
                     hipStream_t s);
 
-/* One token's experts in one launch (decode.hip), after the router logits
- * and the shared expert's silu(gate.x)*(up.x) (h_sh) are written: routing,
- * routed gate/up, SwiGLU, down, the shared down projection and the
- * combine, with the stages ordered by counters in `sync`
- * (whip_decode1_sync_ints(H) ints, zero before the first launch; each
- * launch leaves them zero).  Outputs as the staged kernels write them: ids/w
- * and the pair arrays, pair_rec, sh_out, the partials, y.  err bit 16: a
- * wait timed out.  whip_decode1_check: 0 if the launch takes the shape. */
-typedef struct {
-    int E, K, H, I, SI;
-    whip_route_cfg rc;
-    const void *x;
-    int x_bf16;
-    whip_mat router;
-    const float *bias;
-    int has_shared;
-    whip_mat sh[3];
-    const uint8_t *const *recs;
-    const float *booksT;
-    int cb;
-    uint32_t off_gate, off_up, off_down, off_sc;
-    float *logits;
-    int32_t *ids;
-    float *w;
-    int32_t *pair_tok, *pair_exp;
-    float *pair_w;
-    int32_t *tok_pairs;
-    const uint8_t **pair_rec;
-    float *h_sh, *sh_out, *part_gu, *part_d, *y;
-    int *err, *sync;
-} whip_dec1_args;
-size_t whip_decode1_sync_ints(int H);
-int whip_decode1_check(const whip_dec1_args *a);
-int whip_decode1(const whip_dec1_args *a, hipStream_t s);
-
 /* ---- the static scratch area (scratch.hip) ---- */
 
 /* Bytes of the area, and of its head: state that must start at zero (the

@@ -84,8 +84,6 @@ struct waste_hip_moe {
     int sh_in_combine;           /* the combine runs the shared down        */
     int32_t *d_look;             /* the lookahead's ids                    */
     int prof_on;
-    int decode_mode;             /* 1: the persistent experts launch (T == 1) */
-    int *sync;                   /* its stage counters (zero between launches) */
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
     hipEvent_t kev[2 * WASTE_HIP_STAGES];   /* per-stage kernel start/stop   */
     unsigned ktimed;             /* stages timed by their kernel this forward */
@@ -137,7 +135,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->b.h_sh, m->b.sh_out, m->b.ids, m->b.pair_tok, m->b.pair_exp,
                      m->b.tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
                      m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->b.pair_rec,
-                     m->sync, m->b.rcnt, m->b.xchg };
+                     m->b.rcnt, m->b.xchg };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0]) {
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -206,7 +204,6 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     m->rec_min = m->off_sc + 2 * (size_t)(2 * m->I + m->H);
     m->rec_bytes = (m->rec_min + 4095) / 4096 * 4096;
     m->cb = -1;
-    m->decode_mode = 0;
     const int P = m->T * m->K, Pd = m->Td * m->K;
     m->rsplit_gu = pick_rsplit(m->nch_gu * 2 * m->K, m->I / 64);
     m->rsplit_d = pick_rsplit(m->nch_d * m->K, m->H / 64);
@@ -229,7 +226,6 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->pw, 64 * 4);
     rc |= dmalloc((void **)&m->d_look, 64 * 4);
     rc |= dmalloc((void **)&m->b.pair_rec, 64 * sizeof(void *));
-    rc |= dmalloc((void **)&m->sync, whip_decode1_sync_ints(m->H) * 4);
     rc |= dmalloc((void **)&m->b.rcnt, 256);
     rc |= dmalloc((void **)&m->b.xchg, ((size_t)m->E + 1) * 8);
     if (m->T > m->Td) {
@@ -243,7 +239,6 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     if (rc || !m->h_recs) { waste_hip_moe_destroy(m); return WASTE_HIP_ENOMEM; }
     if (hipMemset(m->d_recs, 0, ((size_t)m->E + 1) * sizeof(void *)) != hipSuccess ||
         hipMemset(m->err, 0, 64) != hipSuccess ||
-        hipMemset(m->sync, 0, whip_decode1_sync_ints(m->H) * 4) != hipSuccess ||
         hipMemset(m->b.rcnt, 0, 256) != hipSuccess || hipMemset(m->b.xchg, 0, ((size_t)m->E + 1) * 8) != hipSuccess) {
         waste_hip_moe_destroy(m);
         return WASTE_HIP_EDEVICE;
@@ -744,68 +739,12 @@ int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     return r ? r : range_fallback(m, x, x_bf16, T, y, s);
 }
 
-/* T == 1 in two launches: the router and the shared expert's gate/up
- * (gemv.hip), then every expert stage in one (decode.hip); 1 if it ran, 0
- * if the shape is not one the second takes (the staged kernels then run),
- * < 0 on a launch failure. */
-static int forward_one(waste_hip_moe *m, const void *x, int x_bf16, float *y, int32_t *ids, float *w,
-                       float *logits, hipStream_t s)
-{
-    if (!m->decode_mode || m->prof_on || (uintptr_t)x % 16) return 0;
-    whip_dec1_args a;
-    memset(&a, 0, sizeof a);
-    a.E = m->E; a.K = m->K; a.H = m->H; a.I = m->I; a.SI = m->SI;
-    a.rc.E = m->E; a.rc.K = m->K; a.rc.score_func = m->c.score_func; a.rc.renorm = m->c.renorm;
-    a.rc.routed_scale = m->c.routed_scale; a.rc.n_group = m->c.n_group; a.rc.topk_group = m->c.topk_group;
-    a.x = x; a.x_bf16 = x_bf16;
-    a.router = m->router; a.bias = m->d_bias;
-    a.has_shared = m->has_shared;
-    if (m->has_shared) { a.sh[0] = m->sh[0]; a.sh[1] = m->sh[1]; a.sh[2] = m->sh[2]; }
-    a.recs = m->d_recs; a.booksT = m->d_booksT; a.cb = m->cb - m->book0;
-    a.off_gate = m->off_gate; a.off_up = m->off_up; a.off_down = m->off_down; a.off_sc = m->off_sc;
-    a.logits = logits ? logits : m->b.logits;
-    a.ids = ids ? ids : m->b.ids;
-    a.w = w ? w : m->b.w;
-    a.pair_tok = m->b.pair_tok; a.pair_exp = m->b.pair_exp; a.pair_w = m->b.pair_w; a.tok_pairs = m->b.tok_pairs;
-    a.pair_rec = m->b.pair_rec;
-    a.h_sh = m->b.h_sh; a.sh_out = m->b.sh_out; a.part_gu = m->b.part_gu; a.part_d = m->b.part_d; a.y = y;
-    a.err = m->err; a.sync = m->sync;
-    if (whip_decode1_check(&a)) return 0;
-    /* router logits and the shared expert's gate/up, then the experts */
-    whip_gemv_job r[2];
-    int nr = 0;
-    r[nr].A = m->router; r[nr].B = NULL; r[nr].x = x; r[nr].x_ld = m->H; r[nr].x_bf16 = x_bf16;
-    r[nr].y = a.logits; r[nr].y_ld = m->E; nr++;
-    if (m->has_shared) {
-        r[nr].A = m->sh[0]; r[nr].B = &m->sh[1]; r[nr].x = x; r[nr].x_ld = m->H; r[nr].x_bf16 = x_bf16;
-        r[nr].y = m->b.h_sh; r[nr].y_ld = m->SI; nr++;
-    }
-    CK((hipError_t)whip_gemv_multi(r, nr, 1, s));
-    if (whip_decode1(&a, s)) return WASTE_HIP_EDEVICE;
-    m->routed_T = 1;
-    m->pair_rec_ok = 1;
-    m->sh_done = 1;
-    return 1;
-}
-
-int waste_hip_moe_set_decode(waste_hip_moe *m, int mode)
-{
-    if (!m || mode < 0 || mode > 1) return WASTE_HIP_EINVAL;
-    m->decode_mode = mode;
-    return 0;
-}
-
 int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y,
                           int32_t *ids, float *w, float *logits, void *stream)
 {
     int rc = ready(m, x, T);
     if (rc) return rc;
     if (!y || !books_ok(m)) return WASTE_HIP_EINVAL;
-    if (T == 1) {
-        m->routed_T = 0;
-        rc = forward_one(m, x, x_bf16, y, ids, w, logits, (hipStream_t)stream);
-        if (rc) return rc < 0 ? rc : 0;
-    }
     rc = waste_hip_moe_route(m, x, x_bf16, T, ids, w, logits, stream);
     return rc ? rc : waste_hip_moe_experts(m, x, x_bf16, T, y, stream);
 }
@@ -870,14 +809,11 @@ int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, in
     /* the staged kernels on the static buffers; the layer's own come back
      * afterwards, and nothing of this call's routing is left for experts() */
     const fwd_bufs own = m->b;
-    const int mode = m->decode_mode;
     m->b = sb;
-    m->decode_mode = 0;
     m->routed_T = 0;
     rc = waste_hip_moe_route(m, x, x_bf16, T, ids, w, logits, stream);
     if (!rc) rc = waste_hip_moe_experts(m, x, x_bf16, T, y, stream);
     m->b = own;
-    m->decode_mode = mode;
     m->routed_T = 0;
     m->pair_rec_ok = 0;
     return rc;
