@@ -41,15 +41,31 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def build_layers(torch, warp_amd, synth, cfg, n_layers, max_tokens, seed=0):
+def build_layers(torch, warp_amd, synth, cfg, n_layers, max_tokens, seed=0, slab=None, books=None,
+                 own_slabs=False):
+    """n_layers layer objects of one shape.  They share one expert slab
+    (slab/books given, or generated here), or with own_slabs each holds its
+    own records (seed + layer), for shapes whose slab would fit the 256 MB
+    Infinity Cache and so not be read from HBM on every visit."""
     H, E, I = cfg["hidden"], cfg["n_experts"], cfg["moe_inter"]
     t0 = time.time()
-    books = synth.codebooks(seed, H, I)
+    if books is None:
+        books = synth.codebooks(seed, H, I)
     rb = synth.record_bytes(H, I)
-    slab = torch.empty(E * rb, dtype=torch.uint8, device="cuda:0")
-    synth.records(seed, 0, H, I, books, 0, E, slab.data_ptr())
+    slabs = []
+    if own_slabs:
+        for li in range(n_layers):
+            sl = torch.empty(E * rb, dtype=torch.uint8, device="cuda:0")
+            synth.records(seed + li, 0, H, I, books, 0, E, sl.data_ptr())
+            slabs.append(sl)
+    else:
+        if slab is None:
+            slab = torch.empty(E * rb, dtype=torch.uint8, device="cuda:0")
+            synth.records(seed, 0, H, I, books, 0, E, slab.data_ptr())
+        slabs = [slab] * n_layers
     torch.cuda.synchronize()
-    log(f"[bench] {E} expert records ({E * rb / 1e9:.2f} GB) generated in {time.time() - t0:.1f}s")
+    log(f"[bench] {len(set(map(id, slabs)))} x {E} expert records ({E * rb / 1e9:.2f} GB each) ready "
+        f"in {time.time() - t0:.1f}s")
     router, bias, sh = synth.trunk(cfg, seed + 1)
     layers = []
     for li in range(n_layers):
@@ -63,26 +79,133 @@ def build_layers(torch, warp_amd, synth, cfg, n_layers, max_tokens, seed=0):
         if sh:
             m.set_shared(*sh)
         for e in range(E):
-            rc = m.bind_expert(e, slab.data_ptr() + e * rb, rb)
+            rc = m.bind_expert(e, slabs[li].data_ptr() + e * rb, rb)
             if rc != 0:
                 raise RuntimeError(f"bind_expert {e}: {rc}")
         layers.append(m)
     log(f"[bench] {n_layers} layer objects ready in {time.time() - t0:.1f}s")
-    return layers, slab, books, rb, (router, bias, sh)
+    return layers, slabs[0] if not own_slabs else slabs, books, rb, (router, bias, sh)
+
+
+def run_decode(torch, cfg, layers, B, steps, warmup, seed=0):
+    """Decode steps at batch B: each step one forward of a fresh batch of
+    tokens through the next layer object (the objects cycled).  Returns the
+    timing record (event-timed over the steps, then a second pass with the
+    per-stage profile on) and the tokens."""
+    H, K, I = cfg["hidden"], cfg["top_k"], cfg["moe_inter"]
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    x_all = torch.randn(((warmup + steps + 8) * B, H), generator=gen, dtype=torch.float32)
+    if cfg["bf16"]:
+        x_all = x_all.to(torch.bfloat16)
+    xd = x_all.to("cuda:0")
+    esz = xd.element_size()
+    y = torch.empty((B, H), dtype=torch.float32, device="cuda:0")
+    ids = torch.empty((warmup + steps, B, K), dtype=torch.int32, device="cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def step(i, rec_ids=True):
+        m = layers[i % len(layers)]
+        m.forward(xd.data_ptr() + i * B * H * esz, B, y.data_ptr(),
+                  ids[i].data_ptr() if rec_ids else None, None, None, bf16=cfg["bf16"], stream=sp)
+
+    def status():
+        for m in layers:
+            st = m.status(sp)
+            if st != 0:
+                raise RuntimeError(f"device error {st}")
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    status()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(warmup, warmup + steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = ev0.elapsed_time(ev1) / steps
+    status()
+
+    # algorithmic bytes: distinct experts per step from the routed ids
+    ids_h = ids[warmup:].cpu().numpy()
+    distinct = [len(np.unique(ids_h[s].reshape(-1))) for s in range(steps)]
+    bytes_per_step = float(np.mean([layers[0].bytes(B, u) for u in distinct]))
+    gbps = bytes_per_step / (ms_per_step * 1e-3) / 1e9
+
+    # live per-stage timing, a second pass over the same steps with profiling
+    # on: at batch 1 each stage's kernel carries its own start/stop events in
+    # its dispatch (kernel time only, no launch gaps); otherwise events on
+    # the forward's stream around each stage
+    for m in layers:
+        m.profile(True)
+    for i in range(warmup, warmup + steps):
+        step(i, rec_ids=False)
+    torch.cuda.synchronize()
+    tot, nfw = {}, 0
+    for m in layers:
+        n, st = m.profile_read()
+        nfw += n
+        for k, v in st.items():
+            tot[k] = tot.get(k, 0.0) + v
+        m.profile(False)
+    stage_ms = {k: v / nfw for k, v in tot.items()}
+    dom = max(("routed_gate_up", "routed_down"), key=lambda k: stage_ms[k])
+    u_mean = float(np.mean(distinct))
+    # per-launch algorithmic bytes of the dominant kernel: the index streams
+    # it reads (gate+up of every routed expert, or down)
+    idx_gu = I * (H // 8) * 3
+    idx_d = H * (I // 8) * 3
+    dom_bytes = (2 * idx_gu if dom == "routed_gate_up" else idx_d) * u_mean
+    rec = {"us_per_token": round(ms_per_step * 1e3 / B, 2), "ms_per_step": round(ms_per_step, 5),
+           "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+           "bytes_per_step": int(bytes_per_step), "distinct_experts_per_step": round(u_mean, 2),
+           "wall_ms_per_step": round(wall * 1e3 / steps, 5),
+           "stage_us": {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
+           "dominant": {"stage": dom, "kernel": "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_act_down",
+                        "launch_us": round(stage_ms[dom] * 1e3, 2), "algorithmic_bytes": int(dom_bytes),
+                        "achieved_gbps": round(dom_bytes / (stage_ms[dom] * 1e-3) / 1e9, 1)}}
+    return rec, x_all
 
 
 def host_cpu():
-    """The host's CPU model and logical CPU count (from /proc/cpuinfo)."""
-    model, n = "unknown", 0
+    """The host's CPU as lscpu states it (model, sockets x cores x threads),
+    with the CPUs this process may run on and the physical cores among them
+    (distinct (package, core) pairs in sysfs)."""
+    import subprocess
+    info = {}
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name") and model == "unknown":
-                    model = line.split(":", 1)[1].strip()
-                n += line.startswith("processor")
-    except OSError:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return f"{model}, {n} logical CPUs"
+
+    def num(k):
+        try:
+            return int(info[k])
+        except (KeyError, ValueError):
+            return None
+    aff = sorted(os.sched_getaffinity(0))
+    cores = set()
+    for c in aff:
+        try:
+            base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                cores.add((pkg, f.read().strip()))
+        except OSError:
+            cores = None
+            break
+    return {"model": info.get("Model name", "unknown"), "sockets": num("Socket(s)"),
+            "cores_per_socket": num("Core(s) per socket"), "threads_per_core": num("Thread(s) per core"),
+            "logical_cpus": num("CPU(s)"), "affinity_cpus": len(aff),
+            "physical_cores_in_affinity": len(cores) if cores is not None else None}
 
 
 def cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, budget_s, nthreads):
@@ -214,42 +337,95 @@ def bench_prefill(torch, warp_amd, synth, cfg, slab, books, rb, trunk, T, reps, 
     }
 
 
-def stack_inputs(torch, T, n_layers, H, rho, gamma, seed):
-    """A synthetic residual stream, bf16 [T][n_layers][H] on the device.
+def sticky_gumbel(rng, T, E, keep):
+    """[T][E] Gumbel noise whose entries each carry over from the row before
+    with probability keep (else a fresh draw): every row is Gumbel, and
+    consecutive rows share about `keep` of their values."""
+    g = np.empty((T, E))
+    g[0] = rng.gumbel(size=E)
+    for t in range(1, T):
+        g[t] = np.where(rng.random(E) < keep, g[t - 1], rng.gumbel(size=E))
+    return g
 
-    Layer L's input is gamma * (layer L-1's input) + sqrt(1-gamma^2) * z_L,
-    and each z_L is an AR(1) over tokens with coefficient rho; every input
-    is N(0,1) per coordinate.  rho sets how much of a layer's selection the
-    next token reuses, gamma how well the next layer's router applied to
-    this layer's input predicts the next layer's selection (the lookahead).
-    """
-    g = torch.Generator(device="cuda:0").manual_seed(seed)
-    c = (1.0 - gamma * gamma) ** 0.5
-    A = torch.zeros((n_layers, n_layers), device="cuda:0")
+
+def stack_inputs(torch, routers, T, zipf_s, reuse_keep, look_keep, scale, seed, device="cuda:0"):
+    """Tokens whose routing follows the stated workload, bf16 [T][L][H] on
+    the device, and each layer's popularity ranks.
+
+    Layer L's router logits for token t are planted as
+    scale * (log p_L + g[t]) (less their expected mean): p_L ~ rank^-zipf_s over a seeded permutation of
+    the experts, g sticky Gumbel noise (sticky_gumbel, reuse_keep).  With
+    Gumbel noise the router's top-k is a draw without replacement from p_L
+    (the Gumbel-max form), and the carried-over noise is what makes
+    consecutive tokens reuse experts.  The next layer's router applied to
+    the same token sees its own planted logits with only look_keep of the
+    noise values in common, so the lookahead guesses as well as that
+    overlap allows.  The token is the minimum-norm solution of both
+    routers' equations (x = M^T (M M^T)^-1 [l_L; l_L+1~], M the two routers
+    stacked) plus N(0,1) noise orthogonal to their rows, so every coordinate
+    still looks like N(0,1) noise."""
+    rng = np.random.default_rng(seed)
+    n_layers = len(routers)
+    E, H = routers[0].shape
+    ranks = []
     for L in range(n_layers):
-        for j in range(L + 1):
-            A[L, j] = gamma ** (L - j) * (1.0 if j == 0 else c)
-    X = torch.empty((T, n_layers, H), dtype=torch.bfloat16, device="cuda:0")
-    z = torch.randn((n_layers, H), generator=g, device="cuda:0")
-    r = (1.0 - rho * rho) ** 0.5
-    for t in range(T):
-        if t:
-            z = rho * z + r * torch.randn((n_layers, H), generator=g, device="cuda:0")
-        X[t] = (A @ z).to(torch.bfloat16)
-    return X
+        rank = np.empty(E, np.int64)
+        rank[rng.permutation(E)] = np.arange(E)
+        ranks.append(rank)
+    # log-popularity and the noise, both centred: a constant added to every
+    # logit of a token changes no selection, and centred logits keep the
+    # planted part of the token small
+    lp = [-zipf_s * np.log(r + 1.0) for r in ranks]
+    lp = [v - v.mean() - np.euler_gamma for v in lp]
+    g = [sticky_gumbel(rng, T, E, reuse_keep) for _ in range(n_layers)]
+    X = torch.empty((T, n_layers, H), dtype=torch.bfloat16, device=device)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    for L in range(n_layers):
+        own = scale * (lp[L] + g[L])                                     # [T][E]
+        rows = [torch.from_numpy(routers[L]).to(device, torch.float64)]
+        tg = [own]
+        if L + 1 < n_layers:
+            mix = np.where(rng.random((T, E)) < look_keep, g[L + 1], rng.gumbel(size=(T, E)))
+            tg.append(scale * (lp[L + 1] + mix))
+            rows.append(torch.from_numpy(routers[L + 1]).to(device, torch.float64))
+        M = torch.cat(rows)                                              # [nE][H]
+        Gm = M @ M.T
+        tgt = torch.from_numpy(np.concatenate(tg, 1)).to(device, torch.float64)   # [T][nE]
+        x = torch.linalg.solve(Gm, tgt.T).T @ M
+        z = torch.randn((T, H), generator=gen, device=device, dtype=torch.float64)
+        z -= torch.linalg.solve(Gm, (z @ M.T).T).T @ M
+        X[:, L] = (x + z).to(torch.bfloat16)
+    if torch.device(device).type == "cuda":
+        torch.cuda.synchronize()
+    return X, ranks
+
+
+def zipf_mle(counts_by_rank):
+    """Maximum-likelihood Zipf exponent of counts indexed by rank (rank 1
+    first), over every rank."""
+    n = np.asarray(counts_by_rank, np.float64)
+    r = np.arange(1, n.size + 1, dtype=np.float64)
+    ss = np.arange(0.3, 2.5, 0.001)
+    ll = [-s * float((n * np.log(r)).sum()) - n.sum() * np.log(float((r ** -s).sum())) for s in ss]
+    return float(ss[int(np.argmax(ll))])
 
 
 def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_gb=64.0,
-                lookahead=6, depth=2, seed=0, rho=0.80, gamma=0.96, zipf_s=1.1, beta=0.125):
+                lookahead=6, depth=2, seed=0, zipf_s=1.1, reuse_keep=0.63, look_keep=0.88, scale=0.5):
     """58 DeepSeek-V3-shaped MoE layers decoding `tokens` tokens at batch 1
     through the HBM expert cache (64 GB of slots), the expert records in
     pinned host memory, misses filled by hipMemcpyAsync on the cache's
     stream, the lookahead's guesses (the next layer's router on this
     layer's input, 6 ids) read after each layer's experts.
 
-    Popularity: each layer's e_score_correction_bias is beta * log of a
-    Zipf(1.1) rank over a seeded permutation of the experts; reuse and
-    lookahead precision come from the residual stream (stack_inputs).
+    Routing (stack_inputs): each layer's experts drawn without replacement
+    from Zipf(zipf_s) popularity over a seeded permutation, consecutive
+    tokens sharing reuse_keep of the draw's noise (0.63: 0.6 of a token's
+    experts reused by the next), the next layer's router on this layer's
+    input sharing look_keep of it (0.88: about 81% of the top-6 guesses
+    land and 92% of the first, the precision the engine measured on a real
+    model, docs/LEARNED.md:1866-1868).  The e_score_correction_bias is
+    present and zero.
 
     The host bank: one set of 256 records (4.2 GB pinned); layer L's expert
     e is a byte copy of record e, so every layer object carries layer id 0
@@ -266,12 +442,11 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
     torch.cuda.synchronize()
     _, _, sh = synth.trunk(cfg, seed + 1)
     rng = np.random.default_rng(seed + 7)
-    layers = []
+    layers, routers = [], []
     for L in range(n_layers):
         W = (rng.standard_normal((E, H), np.float32) * 0.02).astype(np.float32)
-        b = np.zeros(E, np.float64)
-        b[rng.permutation(E)] = -zipf_s * np.log(np.arange(1, E + 1))
-        b = (beta * (b - b.mean())).astype(np.float32)
+        routers.append(W)
+        b = np.zeros(E, np.float32)
         m = warp_amd.MoeLayer(hidden=H, n_experts=E, top_k=K, moe_inter=I,
                               n_shared=cfg["n_shared"], score_func=cfg["score_func"],
                               renorm=cfg["renorm"], routed_scale=cfg["routed_scale"],
@@ -286,7 +461,7 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
     budget = int(budget_gb * 1e9)
     cache = warp_amd.ExpertCache(rb, budget, policy=0, depth=depth)
     cache.set_source([host.data_ptr() + e * rb for _ in range(n_layers) for e in range(E)], n_layers, E)
-    X = stack_inputs(torch, tokens, n_layers, H, rho, gamma, seed + 11)
+    X, ranks = stack_inputs(torch, routers, tokens, zipf_s, reuse_keep, look_keep, scale, seed + 11)
     y = torch.empty((1, H), dtype=torch.float32, device="cuda:0")
     ids = torch.empty((tokens, n_layers, K), dtype=torch.int32, device="cuda:0")
     torch.cuda.synchronize()
@@ -322,11 +497,26 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
     reuse = float(np.mean([len(set(ih[t, L]) & set(ih[t - 1, L])) / K
                            for t in range(1, tokens) for L in range(n_layers)]))
     cnt = np.zeros((n_layers, E))
+    by_rank, fresh_by_rank = np.zeros(E), np.zeros(E)
     for L in range(n_layers):
         np.add.at(cnt[L], ih[:, L].reshape(-1), 1)
-    f = np.sort(cnt, axis=1)[:, ::-1].mean(0)
-    r = np.arange(1, 65)
-    slope = float(np.polyfit(np.log(r), np.log(f[:64] + 1e-9), 1)[0])
+        np.add.at(by_rank, ranks[L][ih[:, L].reshape(-1)], 1)
+        for t in range(tokens):
+            new = [e for e in ih[t, L] if t == 0 or e not in ih[t - 1, L]]
+            np.add.at(fresh_by_rank, ranks[L][np.array(new, np.int64)], 1)
+    # the lookahead's guesses: the next layer's router on this layer's
+    # input, its top 6 by score (the bias is zero), against what the next
+    # layer then selected
+    hits6 = hits1 = n_guess = 0
+    for L in range(n_layers - 1):
+        Wn = torch.from_numpy(routers[L + 1]).to("cuda:0")
+        sc = torch.sigmoid(X[:, L].float() @ Wn.T).cpu().numpy()
+        for t in range(tokens):
+            g = np.argsort(-sc[t], kind="stable")[:lookahead]
+            nxt_sel = set(ih[t, L + 1].tolist())
+            hits6 += len(nxt_sel & set(g.tolist()))
+            hits1 += int(g[0] in nxt_sel)
+            n_guess += 1
     out = {
         "workload": f"{n_layers}-layer dsv3 MoE stack, batch-1 decode of {tokens} tokens through the "
                     f"HBM expert cache", "layers": n_layers, "tokens": tokens,
@@ -338,9 +528,16 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
         "tok_s": round(tokens / wall, 3), "ms_per_token": round(wall * 1e3 / tokens, 2),
         "tok_s_second_half": round(steady, 3) if steady else None,
         "host_to_device_gbps": round(st["bytes_read"] / wall / 1e9, 2),
-        "routing": {"token_to_token_reuse": round(reuse, 3), "zipf_slope_top64": round(slope, 3),
-                    "distinct_experts_per_layer": round(float((cnt > 0).sum(1).mean()), 1),
-                    "rho": rho, "gamma": gamma, "bias_scale": beta},
+        "routing": {"distinct_experts_per_layer": round(float((cnt > 0).sum(1).mean()), 1),
+                    "token_to_token_reuse": round(reuse, 3),
+                    "fresh_selections_per_layer": round(float(fresh_by_rank.sum()) / n_layers, 1),
+                    "zipf_mle_all_ranks": round(zipf_mle(by_rank), 3),
+                    "zipf_mle_fresh_all_ranks": round(zipf_mle(fresh_by_rank), 3),
+                    "lookahead_precision_top6": round(hits6 / max(1, n_guess * lookahead), 3),
+                    "lookahead_precision_rank1": round(hits1 / max(1, n_guess), 3),
+                    "generator": {"popularity": f"Zipf({zipf_s}) over a seeded permutation per layer, "
+                                                f"drawn without replacement (Gumbel top-k)",
+                                  "reuse_keep": reuse_keep, "look_keep": look_keep, "logit_scale": scale}},
     }
     for m in layers:
         m.close()
@@ -380,6 +577,8 @@ def main():
     ap.add_argument("--stack-tokens", type=int, default=200,
                     help="tokens the 58-layer stack decodes through the HBM expert cache (0: skip)")
     ap.add_argument("--stack-budget-gb", type=float, default=64.0)
+    ap.add_argument("--no-extra-configs", dest="extra_configs", action="store_false",
+                    help="skip the other decode configurations (olmoe B=1, kimi B=1/4/16, dsv3 B=8/32)")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device (a plain copy kernel of known "
                          "size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -408,82 +607,40 @@ def main():
         log(f"[bench] copied {a.copy_calibrate} MiB device to device 3 times (counter scale)")
         del src, dst
 
-    gen = torch.Generator(device="cpu").manual_seed(0)
-    n_tok = (a.warmup + a.steps + 8) * B
-    x_all = torch.randn((n_tok, H), generator=gen, dtype=torch.float32)
-    if cfg["bf16"]:
-        x_all = x_all.to(torch.bfloat16)
-    xd = x_all.to("cuda:0")
-    esz = xd.element_size()
-    y = torch.empty((B, H), dtype=torch.float32, device="cuda:0")
-    ids = torch.empty((a.warmup + a.steps, B, K), dtype=torch.int32, device="cuda:0")
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
+    dec, x_all = run_decode(torch, cfg, layers, B, a.steps, a.warmup)
+    ms_per_step = dec["ms_per_step"]
+    us_per_token = dec["us_per_token"]
+    dom = dec["dominant"]
+    achieved = dom["achieved_gbps"]
+    traffic = measured_traffic(dom["stage"], a.config, B)
 
-    def step(i, rec_ids=True):
-        m = layers[i % len(layers)]
-        m.forward(xd.data_ptr() + i * B * H * esz, B, y.data_ptr(),
-                  ids[i].data_ptr() if rec_ids else None, None, None, bf16=cfg["bf16"], stream=sp)
-
-    for i in range(a.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    for m in layers:
-        st = m.status(sp)
-        if st != 0:
-            raise RuntimeError(f"device error {st}")
-
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for i in range(a.warmup, a.warmup + a.steps):
-        step(i)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = ev0.elapsed_time(ev1)
-    ms_per_step = gpu_ms / a.steps
-    for m in layers:
-        st = m.status(sp)
-        if st != 0:
-            raise RuntimeError(f"device error {st}")
-
-    # algorithmic bytes: distinct experts per step from the routed ids
-    ids_h = ids[a.warmup:].cpu().numpy()
-    distinct = [len(np.unique(ids_h[s].reshape(-1))) for s in range(a.steps)]
-    bytes_steps = [layers[0].bytes(B, u) for u in distinct]
-    bytes_per_step = float(np.mean(bytes_steps))
-    gbps = bytes_per_step / (ms_per_step * 1e-3) / 1e9
-    us_per_token = ms_per_step * 1e3 / B
-
-    # live per-stage timing, a second pass over the same steps with profiling
-    # on: at batch 1 each stage's kernel carries its own start/stop events in
-    # its dispatch (kernel time only, no launch gaps); otherwise events on
-    # the forward's stream around each stage
-    for m in layers:
-        m.profile(True)
-    for i in range(a.warmup, a.warmup + a.steps):
-        step(i, rec_ids=False)
-    torch.cuda.synchronize()
-    tot, nfw = {}, 0
-    for m in layers:
-        n, st = m.profile_read()
-        nfw += n
-        for k, v in st.items():
-            tot[k] = tot.get(k, 0.0) + v
-        m.profile(False)
-    stage_ms = {k: v / nfw for k, v in tot.items()}
-    dom = max(("routed_gate_up", "routed_down"), key=lambda k: stage_ms[k])
-    idx_gu = I * (H // 8) * 3
-    idx_d = H * (I // 8) * 3
-    u_mean = float(np.mean(distinct))
-    # per-launch algorithmic bytes of the dominant kernel: the index streams
-    # it reads (gate+up of every routed (token, expert) pair, or down)
-    dom_bytes = (2 * idx_gu if dom == "routed_gate_up" else idx_d) * u_mean
-    dom_ms = stage_ms[dom]
-    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    traffic = measured_traffic(dom, a.config, B)
+    # the other decode configurations, each on its own layer objects: the
+    # small shapes with a slab per object so the cycled records do not fit
+    # the Infinity Cache
+    per_config = None
+    if a.extra_configs and B == 1 and a.config == "dsv3":
+        per_config = []
+        big = build_layers(torch, warp_amd, synth, cfg, a.layers, 32, slab=slab, books=books)[0]
+        for bb in (8, 32):
+            r, _ = run_decode(torch, cfg, big, bb, a.steps, a.warmup, seed=bb)
+            per_config.append(dict(config="C3", workload=f"dsv3 MoE layer decode, batch {bb}", batch=bb, **r))
+            log(f"[bench] C3 B={bb}: {r['us_per_token']} us/token, {r['hbm_frac']:.3f} of HBM peak")
+        for m in big:
+            m.close()
+        del big
+        for name, tag, batches in (("olmoe", "C1", (1,)), ("kimi", "C2", (1, 4, 16))):
+            c2 = synth.CONFIGS[name]
+            ls, slabs, _, _, _ = build_layers(torch, warp_amd, synth, c2, a.layers, max(batches),
+                                              own_slabs=True)
+            for bb in batches:
+                r, _ = run_decode(torch, c2, ls, bb, a.steps, a.warmup, seed=bb)
+                per_config.append(dict(config=tag, workload=f"{name} MoE layer decode, batch {bb}", batch=bb, **r))
+                log(f"[bench] {tag} B={bb}: {r['us_per_token']} us/token, {r['hbm_frac']:.3f} of HBM peak")
+            for m in ls:
+                m.close()
+            del ls, slabs
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
 
     prefill = None
     if a.prefill_tokens and B == 1:
@@ -500,7 +657,11 @@ def main():
 
     cpu = None
     if not a.no_cpu and B == 1:
-        nthreads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+        host = host_cpu()
+        # every physical core this process may use, within the host's share
+        # of CPUs (OMP_NUM_THREADS where set; 16 otherwise)
+        share = int(os.environ.get("OMP_NUM_THREADS", "0")) or 16
+        nthreads = max(1, min(share, host["physical_cores_in_affinity"] or host["affinity_cpus"]))
         xs = x_all[a.warmup:].to(torch.float32).numpy()
         n, t_used, isa, n1, t1 = cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, a.cpu_seconds, nthreads)
         cpu = {"value": round(t_used / n * 1e6, 1), "unit": "us/token", "cores": nthreads,
@@ -508,16 +669,26 @@ def main():
                "sample": f"{n} tokens ({t_used:.1f} s) of the same {a.config} batch-1 layer, the timed "
                          f"steps' {len(xs)} tokens cycled, {isa} kernels, after one untimed warm-up token",
                "single_thread_value": round(t1 / n1 * 1e6, 1), "single_thread_sample": f"{n1} tokens ({t1:.1f} s)",
-               "host": host_cpu()}
+               "host": host}
+        try:
+            with open(os.path.join(ROOT, "tests", "golden", "cpu_calibration.json")) as f:
+                cal = json.load(f)
+            cpu["calibration"] = {
+                "what": "restatement time / the reference engine's moe_layer compiled from its sources, "
+                        "same layer, tokens and threads, outputs bit-exact",
+                "host": cal["host"]["model"],
+                "ratio_by_threads": {k: v["restatement_over_reference"] for k, v in cal["threads"].items()}}
+        except (OSError, KeyError, ValueError):
+            pass
 
     out = {
         "metric": METRIC,
-        "value": round(us_per_token, 2),
+        "value": us_per_token,
         "unit": "us/token",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "ms_per_step": ms_per_step,
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -528,16 +699,17 @@ def main():
         "config": {"workload": f"{a.config} MoE layer decode, batch {B}", "hidden": H,
                    "experts": E, "top_k": K, "moe_inter": I, "batch": B,
                    "layers_cycled": a.layers},
-        "hbm_gbps": round(gbps, 1),
-        "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-        "bytes_per_step": int(bytes_per_step),
-        "distinct_experts_per_step": round(u_mean, 2),
-        "wall_ms_per_step": round(wall * 1e3 / a.steps, 5),
-        "stage_us": {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
-        "roofline": {"bound": "hbm", "kernel": "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_act_down",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+        "hbm_gbps": dec["hbm_gbps"],
+        "hbm_frac": dec["hbm_frac"],
+        "bytes_per_step": dec["bytes_per_step"],
+        "distinct_experts_per_step": dec["distinct_experts_per_step"],
+        "wall_ms_per_step": dec["wall_ms_per_step"],
+        "stage_us": dec["stage_us"],
+        "roofline": {"bound": "hbm", "kernel": dom["kernel"],
+                     "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "launch_us": round(dom_ms * 1e3, 2), "algorithmic_bytes": int(dom_bytes)},
+                     "launch_us": dom["launch_us"], "algorithmic_bytes": dom["algorithmic_bytes"]},
+        "decode_configs": per_config,
         "cpu_baseline": cpu,
         "prefill": prefill,
         "expert_cache": stack,

@@ -113,14 +113,19 @@ static void vq_rows_fast(float *y, const uint8_t *idx, const uint16_t *scale,
                     uint32_t w0, w1, w2, w3, w4, w5;
                     memcpy(&w0, ix, 4); memcpy(&w1, ix + 4, 4); memcpy(&w2, ix + 8, 4);
                     memcpy(&w3, ix + 12, 4); memcpy(&w4, ix + 16, 4); memcpy(&w5, ix + 20, 4);
-                    ac[r + 0] += b0[w0 & 0xff] + b1[(w0 >> 8) & 0xff] + b2[(w0 >> 16) & 0xff];
-                    ac[r + 1] += b0[w0 >> 24] + b1[w1 & 0xff] + b2[(w1 >> 8) & 0xff];
-                    ac[r + 2] += b0[(w1 >> 16) & 0xff] + b1[w1 >> 24] + b2[w2 & 0xff];
-                    ac[r + 3] += b0[(w2 >> 8) & 0xff] + b1[(w2 >> 16) & 0xff] + b2[w2 >> 24];
-                    ac[r + 4] += b0[w3 & 0xff] + b1[(w3 >> 8) & 0xff] + b2[(w3 >> 16) & 0xff];
-                    ac[r + 5] += b0[w3 >> 24] + b1[w4 & 0xff] + b2[(w4 >> 8) & 0xff];
-                    ac[r + 6] += b0[(w4 >> 16) & 0xff] + b1[w4 >> 24] + b2[w5 & 0xff];
-                    ac[r + 7] += b0[(w5 >> 8) & 0xff] + b1[(w5 >> 16) & 0xff] + b2[w5 >> 24];
+                    /* all eight gathers before the first store: a store
+                     * to acc may alias the tables for the compiler, and
+                     * would otherwise hold back the next row's loads */
+                    const float t0 = b0[w0 & 0xff] + b1[(w0 >> 8) & 0xff] + b2[(w0 >> 16) & 0xff];
+                    const float t1 = b0[w0 >> 24] + b1[w1 & 0xff] + b2[(w1 >> 8) & 0xff];
+                    const float t2 = b0[(w1 >> 16) & 0xff] + b1[w1 >> 24] + b2[w2 & 0xff];
+                    const float t3 = b0[(w2 >> 8) & 0xff] + b1[(w2 >> 16) & 0xff] + b2[w2 >> 24];
+                    const float t4 = b0[w3 & 0xff] + b1[(w3 >> 8) & 0xff] + b2[(w3 >> 16) & 0xff];
+                    const float t5 = b0[w3 >> 24] + b1[w4 & 0xff] + b2[(w4 >> 8) & 0xff];
+                    const float t6 = b0[(w4 >> 16) & 0xff] + b1[w4 >> 24] + b2[w5 & 0xff];
+                    const float t7 = b0[(w5 >> 8) & 0xff] + b1[(w5 >> 16) & 0xff] + b2[w5 >> 24];
+                    ac[r] += t0; ac[r + 1] += t1; ac[r + 2] += t2; ac[r + 3] += t3;
+                    ac[r + 4] += t4; ac[r + 5] += t5; ac[r + 6] += t6; ac[r + 7] += t7;
                 }
                 for (; r < nr; r++, ix += 3) ac[r] += b0[ix[0]] + b1[ix[1]] + b2[ix[2]];
             }
@@ -143,10 +148,16 @@ AVX512_FN static void mvq_avx512(float *y, const int8_t *W, const uint16_t *ws,
             for (int k = 0; k < ng; k++) {
                 const int8_t *w;
                 if (bits == 4) {
+                    /* element 2i is byte i's low nibble, 2i + 1 its high
+                     * one: sixteen bytes unpack to 32 elements in order */
                     const uint8_t *p4 = (const uint8_t *)row + (size_t)k * g / 2;
-                    for (int i = 0; i < g / 2; i++) {
-                        unp[2 * i] = (int8_t)((p4[i] & 0x0F) - 8);
-                        unp[2 * i + 1] = (int8_t)((p4[i] >> 4) - 8);
+                    const __m128i m4 = _mm_set1_epi8(0x0F), b8 = _mm_set1_epi8(8);
+                    for (int i = 0; i < g / 2; i += 16) {
+                        const __m128i b = _mm_loadu_si128((const __m128i *)(p4 + i));
+                        const __m128i lo = _mm_sub_epi8(_mm_and_si128(b, m4), b8);
+                        const __m128i hi = _mm_sub_epi8(_mm_and_si128(_mm_srli_epi16(b, 4), m4), b8);
+                        _mm_storeu_si128((__m128i *)(unp + 2 * i), _mm_unpacklo_epi8(lo, hi));
+                        _mm_storeu_si128((__m128i *)(unp + 2 * i + 16), _mm_unpackhi_epi8(lo, hi));
                     }
                     w = unp;
                 } else {

@@ -17,7 +17,9 @@
  * engine's own bank_fetch/record_check, and the scratch buffers
  * waste_model_load would size.  No expert cache, no lookahead, no
  * read-ahead: the serial paths of moe_layer (model.c:5876-5910) and
- * moe_chunk (model.c:7203-7251).
+ * moe_chunk (model.c:7203-7251).  ref_moe_time() times moe_layer on the
+ * same model with the engine's pool and an expert cache that holds the
+ * bank, to calibrate the CPU baseline's restatement against it.
  */
 #define _GNU_SOURCE
 #include "model.c"
@@ -136,18 +138,17 @@ static void put_tensor(waste_tensor *t, const char *name, const ref_tensor *s)
     t->rowbytes = s->rowbytes;
 }
 
-/* Runs moe_layer (T == 1) or moe_chunk (T > 1) over `bank`, E records of
- * rec_bytes each, layer 0.  route/rw receive the chunk's routing (T > 1)
- * or the decode ids (T == 1, rw untouched).  Returns the model's read
- * error (0 when every record passed record_check). */
-int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
-            int score_func, int renorm, float routed_scale,
-            const ref_tensor *router, const float *bias,
-            const ref_tensor *sh_gate, const ref_tensor *sh_up,
-            const ref_tensor *sh_down,
-            const float *booksT, int n_books,
-            const uint8_t *bank, size_t rec_bytes,
-            const float *x, int T, float *out, int *route, float *rw)
+/* The smallest waste_model moe_layer and moe_chunk read: the config, a
+ * tensor table holding the router, bias and shared expert, the codebook
+ * table, one expert bank served from a memfd through the engine's own
+ * bank_fetch/record_check, and the scratch buffers waste_model_load would
+ * size.  NULL on failure. */
+static waste_model *ref_model(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
+                              int score_func, int renorm, float routed_scale,
+                              const ref_tensor *router, const float *bias,
+                              const ref_tensor *sh_gate, const ref_tensor *sh_up,
+                              const ref_tensor *sh_down, const float *booksT, int n_books,
+                              const uint8_t *bank, size_t rec_bytes)
 {
     ref_init();
     waste_model *m = (waste_model *)calloc(1, sizeof *m);
@@ -156,7 +157,7 @@ int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
     c->top_k = top_k; c->moe_inter = moe_inter; c->n_shared = n_shared;
     c->score_func = score_func; c->renorm = renorm;
     c->routed_scale = routed_scale;
-    const int H = hidden, I = moe_inter, E = n_experts, K = top_k;
+    const int H = hidden, I = moe_inter, E = n_experts;
     const int SI = I * (n_shared ? n_shared : 1);
 
     m->t = (waste_tensor *)calloc(5, sizeof(waste_tensor));
@@ -182,7 +183,18 @@ int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
 
     const int fd = memfd_create("bank", 0);
     const size_t bank_bytes = rec_bytes * (size_t)E;
-    if (fd < 0 || write(fd, bank, bank_bytes) != (ssize_t)bank_bytes) return -100;
+    size_t done = 0;
+    while (fd >= 0 && done < bank_bytes) {
+        const ssize_t w = write(fd, bank + done, bank_bytes - done);
+        if (w <= 0) break;
+        done += (size_t)w;
+    }
+    if (fd < 0 || done != bank_bytes) {
+        if (fd >= 0) close(fd);
+        free(m->t);
+        free(m);
+        return NULL;
+    }
     m->bank[0].fd[0] = fd; m->bank[0].n_shards = 1;
     m->bank[0].rec_bytes = (int64_t)rec_bytes; m->bank[0].n_experts = E;
     m->miss_buf = (uint8_t *)aligned_alloc(4096, rec_bytes);
@@ -196,7 +208,38 @@ int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
     m->h = (float *)calloc((size_t)H, sizeof(float));
     m->lut = (float *)calloc(3 * lut_sz, sizeof(float));
     m->lut_bytes = 3 * lut_sz * sizeof(float);
+    return m;
+}
 
+static void ref_model_free(waste_model *m)
+{
+    close(m->bank[0].fd[0]);
+    free(m->miss_buf); free(m->att); free(m->ff); free(m->e_gate);
+    free(m->ares); free(m->h); free(m->lut); free(m->t);
+    pthread_mutex_destroy(&m->fetch_mu);
+    free(m);
+}
+
+/* Runs moe_layer (T == 1) or moe_chunk (T > 1) over `bank`, E records of
+ * rec_bytes each, layer 0.  route/rw receive the chunk's routing (T > 1)
+ * or the decode ids (T == 1, rw untouched).  Returns the model's read
+ * error (0 when every record passed record_check). */
+int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
+            int score_func, int renorm, float routed_scale,
+            const ref_tensor *router, const float *bias,
+            const ref_tensor *sh_gate, const ref_tensor *sh_up,
+            const ref_tensor *sh_down,
+            const float *booksT, int n_books,
+            const uint8_t *bank, size_t rec_bytes,
+            const float *x, int T, float *out, int *route, float *rw)
+{
+    waste_model *m = ref_model(hidden, n_experts, top_k, moe_inter, n_shared, score_func, renorm,
+                               routed_scale, router, bias, sh_gate, sh_up, sh_down, booksT, n_books,
+                               bank, rec_bytes);
+    if (!m) return -100;
+    const int H = hidden, I = moe_inter, E = n_experts, K = top_k;
+    const int SI = I * (n_shared ? n_shared : 1);
+    const size_t lut_sz = (size_t)((H > I ? H : I) / 8) * 3 * 256;
     if (T == 1) {
         moe_layer(m, 0, x, out, route);
     } else {
@@ -215,12 +258,48 @@ int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
         free(m->cq); free(m->cff); free(m->ckv);
     }
     const int err = m->read_error;
-    close(fd);
-    free(m->miss_buf); free(m->att); free(m->ff); free(m->e_gate);
-    free(m->ares); free(m->h); free(m->lut); free(m->t);
-    pthread_mutex_destroy(&m->fetch_mu);
-    free(m);
+    ref_model_free(m);
     return err;
+}
+
+/* Seconds moe_layer takes over ntok tokens (xs[ntok][hidden]) with the
+ * engine's pool at nthreads and an expert cache that holds every record,
+ * after one untimed pass over the same tokens has made each routed record
+ * resident: the timed pass is the decode path's arithmetic (the per-expert
+ * loop, model.c:5876-5910, each matrix's rows split over the pool,
+ * src/threads.h:325-341) with no bank reads.  The pool is shut down again
+ * afterwards, so the other entry points stay serial.  out: the last
+ * token's output.  < 0 on failure. */
+double ref_moe_time(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
+                    int score_func, int renorm, float routed_scale,
+                    const ref_tensor *router, const float *bias,
+                    const ref_tensor *sh_gate, const ref_tensor *sh_up,
+                    const ref_tensor *sh_down,
+                    const float *booksT, int n_books,
+                    const uint8_t *bank, size_t rec_bytes,
+                    const float *xs, int ntok, int nthreads, float *out)
+{
+    if (ntok <= 0 || top_k > 64) return -1.0;
+    waste_model *m = ref_model(hidden, n_experts, top_k, moe_inter, n_shared, score_func, renorm,
+                               routed_scale, router, bias, sh_gate, sh_up, sh_down, booksT, n_books,
+                               bank, rec_bytes);
+    if (!m) return -1.0;
+    waste_pool_shutdown();
+    waste_pool_init(nthreads, NULL);
+    double r = -2.0;
+    if (waste_ecache_init(&m->cache, (size_t)n_experts * rec_bytes, rec_bytes, 0) == 0) {
+        int route[64];
+        for (int t = 0; t < ntok; t++) moe_layer(m, 0, xs + (size_t)t * hidden, out, route);
+        struct timespec a, b;
+        clock_gettime(CLOCK_MONOTONIC, &a);
+        for (int t = 0; t < ntok; t++) moe_layer(m, 0, xs + (size_t)t * hidden, out, route);
+        clock_gettime(CLOCK_MONOTONIC, &b);
+        r = m->read_error ? -3.0 : (double)(b.tv_sec - a.tv_sec) + 1e-9 * (double)(b.tv_nsec - a.tv_nsec);
+        waste_ecache_free(&m->cache);
+    }
+    waste_pool_shutdown();
+    ref_model_free(m);
+    return r;
 }
 
 /* ---- the engine's expert cache, scripted --------------------------------

@@ -319,6 +319,9 @@ class Ref:
         rt = C.POINTER(RefTensor)
         _sig(L, "ref_moe", C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                      rt, fp, rt, rt, rt, fp, C.c_int, u8p, C.c_size_t, fp, C.c_int, fp, i32p, fp])
+        _sig(L, "ref_moe_time", C.c_double, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                             C.c_float, rt, fp, rt, rt, rt, fp, C.c_int, u8p, C.c_size_t, fp,
+                                             C.c_int, C.c_int, fp])
         _sig(L, "ref_ecache_run", C.c_int, [C.c_int, C.c_int, C.c_int, i32p, C.c_int, i32p,
                                             C.POINTER(C.c_uint64)])
         _sig(L, "ref_ecache_usage", None, [C.c_char_p, C.c_char_p])
@@ -401,14 +404,30 @@ class Ref:
         self.lib.ref_act_pair(ptr(g, fp), ptr(np.ascontiguousarray(u, np.float32), fp), g.size)
         return g
 
+    @staticmethod
+    def _rt(t):
+        if t.rows == 0:
+            return None
+        return C.byref(RefTensor(t.fmt, t.rows, t.cols, t.group, t.q.ctypes.data_as(C.c_void_p),
+                                 ptr(t.qs, u16p) if t.qs is not None else None, t.rowbytes))
+
+    def moe_time(self, L, X, booksT, nthreads, bank=None):
+        """Seconds the engine's moe_layer takes over the tokens X with its
+        pool at nthreads and every routed record resident (one untimed pass
+        first); and the last token's output."""
+        rt = self._rt
+        bank = np.frombuffer(L.bank(), np.uint8) if bank is None else bank
+        X = np.ascontiguousarray(X, np.float32)
+        out = np.zeros(L.H, np.float32)
+        sec = self.lib.ref_moe_time(L.H, L.E, L.K, L.I, L.n_shared, L.score_func, L.renorm, L.routed_scale,
+                                    rt(L.router), ptr(L.bias, fp) if L.bias is not None else None,
+                                    rt(L.sh[0]), rt(L.sh[1]), rt(L.sh[2]), ptr(booksT, fp), L.n_books,
+                                    ptr(bank, u8p), L.rec_bytes, ptr(X, fp), X.shape[0], nthreads, ptr(out, fp))
+        return sec, out
+
     def moe(self, L, X, booksT):
         T = X.shape[0]
-
-        def rt(t):
-            if t.rows == 0:
-                return None
-            return C.byref(RefTensor(t.fmt, t.rows, t.cols, t.group, t.q.ctypes.data_as(C.c_void_p),
-                                     ptr(t.qs, u16p) if t.qs is not None else None, t.rowbytes))
+        rt = self._rt
         bank = np.frombuffer(L.bank(), np.uint8)
         out = np.zeros((T, L.H), np.float32)
         route = np.zeros((T, L.K), np.int32)
