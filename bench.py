@@ -259,6 +259,48 @@ def cpu_baseline(torch, cfg, slab, books, rb, trunk, xs, budget_s, nthreads):
     return n, t_used, isa, n1, t1
 
 
+def bench_vq4p(torch, warp_amd, reps=64):
+    """VQ4P rows through the int8 LUT (the vq_rows_p6 slot's kernel on device
+    pointers) on the C3 shapes: gate/up (2048 rows x 896 positions) and down
+    (7168 x 256).  Random codes (any byte triple is four 6-bit codes), a
+    quantised random table; each launch reads its own matrix of `reps`, so
+    the 256 MB Infinity Cache holds none of them from the launch before.
+    Algorithmic bytes: the codes, 3 per (row, position), plus the f16 row
+    scales and the int8 table."""
+    L = warp_amd.lib()
+    dev = "cuda:0"
+    s = torch.cuda.current_stream()
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(5)
+    for name, M, nv in (("gate_up", 2048, 896), ("down", 7168, 256)):
+        idx = torch.randint(0, 256, (reps, M * nv * 3), dtype=torch.uint8, device=dev, generator=g)
+        sc = (torch.rand((M,), device=dev, generator=g) * 0.02 + 0.005).half()
+        lut = torch.randn((nv * 256,), device=dev, generator=g)
+        q = torch.empty((nv * 256,), dtype=torch.int8, device=dev)
+        qs = torch.empty(((nv + 31) // 32,), dtype=torch.float32, device=dev)
+        warp_amd.check(L.waste_hip_vq_quant_lut(lut.data_ptr(), nv, 4, 64, q.data_ptr(), qs.data_ptr(), s.cuda_stream),
+                       "vq_quant_lut")
+        y = torch.empty((M,), dtype=torch.float32, device=dev)
+
+        def one(r):
+            warp_amd.check(L.waste_hip_vq_rows_p6(idx[r].data_ptr(), sc.data_ptr(), q.data_ptr(), qs.data_ptr(), 0, M,
+                                                  nv, 1, y.data_ptr(), s.cuda_stream), "vq_rows_p6")
+        for r in range(reps):
+            one(r)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for r in range(reps):
+            one(r)
+        e1.record(s)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = M * nv * 3 + M * 2 + nv * 256 + ((nv + 31) // 32) * 4
+        out[name] = {"rows": M, "positions": nv, "us": round(us, 2), "bytes": nbytes,
+                     "gbps": round(nbytes / (us * 1e-6) / 1e9, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 8e12, 4)}
+        del idx
+    return out
+
+
 def bench_prefill(torch, warp_amd, synth, cfg, slab, books, rb, trunk, T, reps, hot=False):
     """One T-token chunk of the layer (moe_chunk on the matrix cores).  Tokens
     are planted so per-expert counts follow Zipf(1.1) (synth.zipf_tokens), or
@@ -649,6 +691,11 @@ def main():
                                                 a.prefill_tokens, 5, hot=True)["routed_grouped_gemm"]
         log(f"[bench] prefill {prefill['tokens_per_s']} tok/s")
 
+    vq4p = None
+    if a.extra_configs and B == 1:
+        vq4p = bench_vq4p(torch, warp_amd)
+        log(f"[bench] vq4p rows: {vq4p}")
+
     stack = None
     if a.stack_tokens and B == 1 and a.config == "dsv3":
         stack = bench_stack(torch, warp_amd, synth, cfg, books, a.stack_tokens,
@@ -712,6 +759,7 @@ def main():
         "decode_configs": per_config,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "vq4p_rows": vq4p,
         "expert_cache": stack,
     }
     print(json.dumps(out))

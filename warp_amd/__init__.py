@@ -169,6 +169,9 @@ def lib():
         "waste_hip_crc32": (C.c_uint32, [C.c_uint32, vp, C.c_size_t]),
         "waste_hip_ecache_save_usage": (i, [vp, C.c_char_p, C.c_uint64]),
         "waste_hip_ecache_warm": (i, [vp, C.c_char_p]),
+        "waste_hip_vq_quant_lut": (i, [vp, i, i, i, vp, vp, vp]),
+        "waste_hip_vq_rows_p6": (i, [vp, vp, vp, vp, i, i, i, i, vp, vp]),
+        "waste_hip_vq_p6_order": (i, []),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)

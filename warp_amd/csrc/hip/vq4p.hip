@@ -19,7 +19,7 @@
 #define P6_BLK 32                      // positions per int8 scale block
 #define P6_EN 64                       // entries per stage (the 6-bit codes)
 #define QL_THREADS 1024
-#define P6_THREADS 256                 // four 64-row blocks a workgroup
+#define P6_THREADS 1024                // sixteen wavefronts on one 64-row block
 
 // ---- the int8 table, one scale block per workgroup ---------------------------
 __global__ void __launch_bounds__(QL_THREADS)
@@ -66,49 +66,96 @@ extern "C" int whip_vq_quant_lut(const float *lut, int nv, int stages, int entri
 }
 
 // ---- rows through the int8 table ---------------------------------------------
-// Wavefront w of a workgroup owns the 64-row block blockIdx.x * 4 + w, a
-// lane one row.  Per scale block the workgroup stages the block's table
-// (32 positions x 4 stages x 64 entries, 8 KB) in LDS; each lane then reads
-// its row's three code bytes per position (a block's 64 rows are 192
-// contiguous bytes, so the wavefront's reads coalesce) and adds the four
-// stages' entries into an exact integer sum.
+// One 1,024-thread workgroup per 64-row block, a lane per row.  The sixteen
+// wavefronts split the block's 32-position scale blocks between them: for
+// each, a wavefront stages that block's table (32 positions x 4 stages x 64
+// entries, 8 KB) in its own LDS area, reads its rows' three code bytes per
+// position (a position's 64 rows are 192 contiguous bytes, so the loads
+// coalesce) and adds the four stages' entries into the block's exact integer
+// sum.  A stage's table is 64 bytes, sixteen dwords in sixteen banks, so two
+// lanes that meet in a bank read the same dword: the lookups never conflict.
+// The sums wait in LDS until wavefront 0 folds them into fp32 in block order,
+// the engine's order.
+#define P6_WAVES (P6_THREADS / 64)
+#define P6_GROUP 64                    // scale blocks folded per round
+
+// the three code bytes at p (any alignment) from the aligned words that hold
+// them: no read reaches past the aligned word holding the last code byte
+__device__ __forceinline__ uint32_t p6_codes(const uint8_t *p)
+{
+    const uintptr_t a = (uintptr_t)p & ~(uintptr_t)3;
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t w0 = *(const uint32_t *)a;
+    const uint32_t w1 = *(const uint32_t *)(a + (sh > 1 ? 4 : 0));
+    return (uint32_t)((((uint64_t)w1 << 32) | w0) >> (8 * sh));
+}
+
 template <bool FMA>
 __global__ void __launch_bounds__(P6_THREADS)
 k_vq_rows_p6(const uint8_t *__restrict__ idx, const uint16_t *__restrict__ scale,
              const int8_t *__restrict__ lut8, const float *__restrict__ lscale, int r_lo, int r_hi, int nv,
              float *__restrict__ y)
 {
-    __shared__ __align__(16) int8_t s_t[P6_BLK * 4 * P6_EN];
+    __shared__ __align__(16) int8_t s_t[P6_WAVES][P6_BLK * 4 * P6_EN];
+    __shared__ int s_sum[P6_GROUP][64];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int rb = r_lo / 64 + blockIdx.x * (P6_THREADS / 64) + wv;   // 64-row block
+    const int rb = r_lo / 64 + blockIdx.x;                             // 64-row block
     const int r = rb * 64 + lane;
-    const bool live = r >= r_lo && r < r_hi;
+    const bool live = r < r_hi;
     const uint8_t *base = idx + (size_t)rb * nv * 192 + lane * 3;
+    const int nb = (nv + P6_BLK - 1) / P6_BLK;
+    int8_t *T = s_t[wv];
     float acc = 0.0f;
-    for (int v0 = 0; v0 < nv; v0 += P6_BLK) {
-        const int nb = min(P6_BLK, nv - v0);
-        __syncthreads();                             // the last block's table is done with
-        {
-            const uint4 *src = (const uint4 *)(lut8 + (size_t)v0 * 4 * P6_EN);
-            uint4 *dst = (uint4 *)s_t;
-            for (int i = tid; i < nb * 4 * P6_EN / 16; i += P6_THREADS) dst[i] = src[i];
+    for (int g0 = 0; g0 < nb; g0 += P6_GROUP) {
+        const int gn = min(P6_GROUP, nb - g0);
+        for (int jj = wv; jj < gn; jj += P6_WAVES) {                  // uniform per wavefront
+            const int v0 = (g0 + jj) * P6_BLK, n = min(P6_BLK, nv - v0);
+            {
+                const uint4 *src = (const uint4 *)(lut8 + (size_t)v0 * 4 * P6_EN);
+                for (int i = lane; i < n * 16; i += 64) ((uint4 *)T)[i] = src[i];
+            }
+            // the table's writes before any lane's lookups (one wavefront:
+            // its LDS operations complete in order)
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            int sum = 0;
+            if (live) {
+                const uint8_t *ix = base + (size_t)v0 * 192;
+                auto add = [&](int v, uint32_t c) {
+                    const unsigned b0 = c & 0xff, b1 = (c >> 8) & 0xff, b2 = (c >> 16) & 0xff;
+                    const int8_t *Tv = T + v * 4 * P6_EN;
+                    sum += Tv[b0 & 0x3f] + Tv[P6_EN + (((b0 >> 6) | (b1 << 2)) & 0x3f)] +
+                           Tv[2 * P6_EN + (((b1 >> 4) | (b2 << 4)) & 0x3f)] + Tv[3 * P6_EN + ((b2 >> 2) & 0x3f)];
+                };
+                if (n == P6_BLK) {
+                    // every position's codes in flight at once, then the lookups
+                    uint32_t c[P6_BLK];
+#pragma unroll
+                    for (int v = 0; v < P6_BLK; v++) c[v] = p6_codes(ix + (size_t)v * 192);
+#pragma unroll
+                    for (int v = 0; v < P6_BLK; v++) add(v, c[v]);
+                } else {
+                    for (int v = 0; v < n; v++) add(v, p6_codes(ix + (size_t)v * 192));
+                }
+            }
+            // at most 4 * 32 * 127 in magnitude: the engine's int16 sum, exactly
+            s_sum[jj][lane] = sum;
+            // the next block's table overwrites this one: every lane's
+            // lookups first
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
         __syncthreads();
-        int sum = 0;
-        if (live) {
-            for (int v = 0; v < nb; v++) {
-                const uint8_t *ix = base + (size_t)(v0 + v) * 192;
-                const unsigned b0 = ix[0], b1 = ix[1], b2 = ix[2];
-                const int8_t *T = s_t + v * 4 * P6_EN;
-                sum += T[b0 & 0x3f] + T[P6_EN + (((b0 >> 6) | (b1 << 2)) & 0x3f)] +
-                       T[2 * P6_EN + (((b1 >> 4) | (b2 << 4)) & 0x3f)] + T[3 * P6_EN + ((b2 >> 2) & 0x3f)];
+        if (wv == 0)
+            for (int jj = 0; jj < gn; jj++) {
+                const float ls = lscale[g0 + jj], sm = (float)s_sum[jj][lane];
+                acc = FMA ? __fmaf_rn(ls, sm, acc) : __fadd_rn(acc, __fmul_rn(ls, sm));
             }
-        }
-        // at most 4 * 32 * 127 in magnitude: the engine's int16 sum, exactly
-        const float ls = lscale[v0 / P6_BLK];
-        acc = FMA ? __fmaf_rn(ls, (float)sum, acc) : __fadd_rn(acc, __fmul_rn(ls, (float)sum));
+        __syncthreads();
     }
-    if (live) y[r] = __fmul_rn(acc, wh_f16_scale(scale[r]));
+    if (wv == 0 && live) y[r] = __fmul_rn(acc, wh_f16_scale(scale[r]));
 }
 
 // Rows [r_lo, r_hi) (r_lo a multiple of 64); idx, scale and y are indexed
@@ -118,8 +165,7 @@ extern "C" int whip_vq_rows_p6(const uint8_t *idx, const uint16_t *scale, const 
                                hipStream_t s)
 {
     if (r_lo < 0 || r_lo % 64 || r_hi <= r_lo || nv <= 0 || (uintptr_t)lut8 % 16) return (int)hipErrorInvalidValue;
-    const int blocks = (r_hi - r_lo + 63) / 64;
-    const dim3 grid((blocks + P6_THREADS / 64 - 1) / (P6_THREADS / 64));
+    const dim3 grid((r_hi - r_lo + 63) / 64);
     if (fma) hipLaunchKernelGGL(k_vq_rows_p6<true>, grid, dim3(P6_THREADS), 0, s, idx, scale, lut8, lscale, r_lo, r_hi, nv, y);
     else hipLaunchKernelGGL(k_vq_rows_p6<false>, grid, dim3(P6_THREADS), 0, s, idx, scale, lut8, lscale, r_lo, r_hi, nv, y);
     return (int)hipGetLastError();
