@@ -178,6 +178,10 @@ typedef struct {
 } whip_pf_args;
 int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, int segs, int mblocks, hipStream_t s);
 
+/* n activations (fp32, or bf16 when bf16) to fp16 for the products' A
+ * operand; a value outside fp16's range sets err bit 4. */
+int whip_pf_to_f16(const void *x, int bf16, size_t n, uint16_t *y, int *err, hipStream_t s);
+
 /* Router logits for T tokens on the matrix cores (fp32 products), through
  * part[whip_pf_router_part_floats(T, E)]. */
 size_t whip_pf_router_part_floats(int T, int E);

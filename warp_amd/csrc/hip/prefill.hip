@@ -142,7 +142,7 @@ extern "C" int whip_sort_pairs(const int32_t *ids, const float *w, int T, int K,
 #define PF_THREADS 512
 #define PF_KC 64                     // k per LDS chunk
 #define PF_ALD (PF_KC + 8)           // A row stride in halves (144 B: rows fall on different banks)
-#define PF_BIG 64                    // expert segments this long take the register-tiled kernel
+#define PF_BIG 64                    // expert segments this long take the 256 x 256 tile kernel
 
 enum { DEC_F32 = 0, DEC_Q8 = 2, DEC_Q4 = 3, DEC_VQ = 4 };
 
@@ -195,7 +195,7 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
     const int n_seg = a.seg_off ? a.seg_off[seg + 1] - s0 : a.rows;
     const int r0 = blockIdx.z * (MT * 32);           // this workgroup's rows of the segment
     if (r0 >= n_seg) return;
-    if (DEC == DEC_VQ && MT == 4 && a.seg_off && n_seg >= PF_BIG) return;   // long segments: k_pf_gemm4
+    if (DEC == DEC_VQ && MT == 4 && a.seg_off && n_seg >= PF_BIG) return;   // long segments: k_pf_gemm8
     const int mrows = min(MT * 32, n_seg - r0);
     const int kind = EPI == 0 ? wave >> 2 : 0;
     const int ncol = blockIdx.x * (EPI == 0 ? 128 : 256) + (EPI == 0 ? (wave & 3) : wave) * 32 + (lane & 31);
@@ -410,214 +410,237 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
     if (bad) atomicOr(a.err, ERR_RANGE);
 }
 
-// Register-tiled variant for the routed experts' segments (VQ3R records,
-// 128-row M blocks): each wavefront holds NT 32-column N fragments over all
-// four 32-row M tiles, so an A fragment read from LDS feeds NT products.
-// EPI 0: a wavefront's fragments are the gate and up rows of the same
-// columns, so SwiGLU happens in registers; EPI 1: NT*32 columns of one
-// matrix.  Per product, LDS delivers 1/NT of an A fragment and a quarter of
-// a B decode (three codebook rows per lane per 16-wide k step, reused over
-// the four M tiles).  NT = 2: eight wavefronts, two per SIMD (about
-// 1.25 KB of LDS per product); NT = 4: four wavefronts (about 1 KB).
-#ifndef PF_NT
-#define PF_NT 2                      // N fragments per wavefront of the register-tiled kernel
-#endif
-template <int NT> struct pf4 { static constexpr int W = 16 / NT, THREADS = 64 * W; };
+// ---- 256 x 256 tiles for long segments ---------------------------------------
+// Segments of PF_BIG tokens or more: a workgroup takes 256 tokens and 256 B
+// columns (VQ3R rows: 128 gate + 128 up for EPI 0, 256 of one matrix for
+// EPI 1), and decodes its B tile once per 64-wide k chunk into LDS, where
+// all eight wavefronts read it as they read A.  In k_pf_gemm each wavefront
+// decodes the B fragments it multiplies, for up to four 32-token M tiles;
+// here a decoded fragment feeds eight (the M tiles of the four wavefronts
+// that share its columns), so the codebook gathers per product halve, and a
+// wavefront's k step is 8 products from 2 A and 4 B fragment reads.  Rows
+// past a segment's end are zeros in the A tile: every product runs, and the
+// epilogue drops their rows.
+// Both tiles are [256][8] slots of 8 halves (one VQ vector, or 8 k of a
+// token) with the slot index XOR-swizzled by (row >> 1) & 7: every 16-lane
+// pass of a 128-bit read or write, operand reads included, touches sixteen
+// different bank groups.  The tiles are double buffered: chunk kc's products
+// read one pair while chunk kc+1 is staged and decoded into the other, one
+// barrier per chunk.  Wavefront w owns rows (w & 3) * 64 and columns
+// (w >> 2) * 64 (EPI 0: gate and up of the same 64, SwiGLU in registers) or
+// (w >> 2) * 128 (EPI 1).
+#define PF8_M 256
+#define PF8_N 256                    // B columns a workgroup decodes
+#define PF8_THREADS 512
 
-template <int EPI, int NT>
-__global__ void __launch_bounds__(pf4<NT>::THREADS)
-k_pf_gemm4(whip_pf_args a)
+WH_INLINE int pf8_slot(int r, int g) { return r * 8 + (g ^ ((r >> 1) & 7)); }
+
+// XM: the activations' format (0 fp32, 1 bf16, 2 fp16), fixed per launch
+template <int EPI, int XM>
+__global__ void __launch_bounds__(PF8_THREADS) k_pf_gemm8(whip_pf_args a)
 {
-    constexpr int MT = 4, W = pf4<NT>::W, THREADS = pf4<NT>::THREADS;
-    constexpr int FK = EPI == 0 ? NT / 2 : NT;                      // fragments per kind
-    constexpr int CW = 32 * FK;                                     // a wavefront's columns
     constexpr int NBOOK = EPI == 0 ? 6 : 3;
-    constexpr int ABUF = MT * 32 * PF_ALD;                          // halves per A buffer
+    constexpr int OUTN = EPI == 0 ? PF8_N / 2 : PF8_N;                // output columns per workgroup
     __shared__ uint4 cbk[NBOOK * 256];
-    __shared__ __attribute__((aligned(16))) _Float16 As[2 * ABUF];
+    __shared__ uint4 sA[2][PF8_M * 8];
+    __shared__ uint4 sB[2][PF8_N * 8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int mw = wave & 3, nw = wave >> 2;
     const int seg = a.order ? a.order[blockIdx.y] : (int)blockIdx.y;
-    const int s0 = a.seg_off ? a.seg_off[seg] : 0;
-    const int n_seg = a.seg_off ? a.seg_off[seg + 1] - s0 : a.rows;
-    const int r0 = blockIdx.z * (MT * 32);
-    if (r0 >= n_seg || (a.seg_off && n_seg < PF_BIG)) return;   // short segments: k_pf_gemm
-    const int mrows = min(MT * 32, n_seg - r0);
-
-    int ncol[NT], kj[NT];
-    bool nok[NT];
-#pragma unroll
-    for (int j = 0; j < NT; j++) {
-        kj[j] = EPI == 0 ? j / FK : 0;
-        ncol[j] = blockIdx.x * (W * CW) + wave * CW + (j % FK) * 32 + (lane & 31);
-        nok[j] = ncol[j] < a.N;
-    }
+    const int s0 = a.seg_off[seg];
+    const int n_seg = a.seg_off[seg + 1] - s0;
+    const int r0 = blockIdx.z * PF8_M;
+    if (r0 >= n_seg || n_seg < PF_BIG) return;       // shorter segments: k_pf_gemm
+    const int mrows = min(PF8_M, n_seg - r0);
     const uint8_t *rec = a.recs[seg];
-    if (rec == nullptr) {                            // unbound expert: zeros + flag
-        for (int m = 0; m < mrows; m++) {
-            const size_t row = (size_t)(s0 + r0 + m);
+
+    // this thread's B column to decode (4 of its 8 positions per chunk)
+    const int dc = tid & (PF8_N - 1), dv0 = tid >> 8;
+    const int dkind = EPI == 0 ? dc >> 7 : 0;
+    const int dwr = blockIdx.x * OUTN + (EPI == 0 ? (dc & 127) : dc);
+    // the wavefront's four B fragments: columns in the tile, W rows, kinds
+    int bcol[4], wrow[4], bkind[4];
+    bool nok[4];
 #pragma unroll
-            for (int j = 0; j < NT; j++) {
-                if (!nok[j] || (EPI == 0 && kj[j] != 0)) continue;
-                if (EPI == 0) ((_Float16 *)a.out)[row * a.out_ld + ncol[j]] = (_Float16)0.0f;
-                else ((float *)a.out)[row * a.out_ld + ncol[j]] = 0.0f;
-            }
+    for (int j = 0; j < 4; j++) {
+        if (EPI == 0) {
+            bkind[j] = j >> 1;
+            bcol[j] = bkind[j] * 128 + nw * 64 + (j & 1) * 32;
+            wrow[j] = blockIdx.x * OUTN + nw * 64 + (j & 1) * 32 + (lane & 31);
+        } else {
+            bkind[j] = 0;
+            bcol[j] = nw * 128 + j * 32;
+            wrow[j] = blockIdx.x * OUTN + nw * 128 + j * 32 + (lane & 31);
         }
+        nok[j] = wrow[j] < a.N;
+    }
+    if (rec == nullptr) {                            // unbound expert: zeros + flag
+        if (mw == 0)                                 // one wavefront per column half
+            for (int m = 0; m < mrows; m++) {
+                const size_t row = (size_t)(s0 + r0 + m);
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if (!nok[j] || (EPI == 0 && bkind[j] != 0)) continue;
+                    if (EPI == 0) ((_Float16 *)a.out)[row * a.out_ld + wrow[j]] = (_Float16)0.0f;
+                    else ((float *)a.out)[row * a.out_ld + wrow[j]] = 0.0f;
+                }
+            }
         if (tid == 0) atomicOr(a.err, 1);
         return;
     }
-    for (int i = tid; i < NBOOK * 256; i += THREADS)
+    for (int i = tid; i < NBOOK * 256; i += PF8_THREADS)
         cbk[i] = *(const uint4 *)(a.books16 + ((size_t)(a.cb + i / 256) * 256 + (i & 255)) * 8);
     const int nv = a.Kd / 8;
     const size_t rstride = (size_t)nv * 192;
-    g_u8 *ib[NT];
-#pragma unroll
-    for (int j = 0; j < NT; j++) {
-        const int nc = nok[j] ? ncol[j] : 0;
-        ib[j] = as_global(rec) + a.idx_off[kj[j]] + (size_t)(nc >> 6) * rstride + (nc & 63) * 3;
-    }
+    g_u8 *dib = as_global(rec) + a.idx_off[dkind] + (size_t)((dwr < a.N ? dwr : 0) >> 6) * rstride +
+                ((dwr < a.N ? dwr : 0) & 63) * 3;
     bool bad = false;
 
-    acc16 acc[NT][MT];
+    // A items: it = tid + 512 q -> token row it >> 3, k group it & 7
+    size_t abase[4];
+    bool alive[4];
 #pragma unroll
-    for (int j = 0; j < NT; j++)
-#pragma unroll
-        for (int t = 0; t < MT; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[j][t][r] = 0.0f;
-
-    // the k loop: chunks kc+1 and kc+2's A rows and B indices are in flight
-    // while chunk kc's products run (two register slots, the loop unrolled by
-    // two so each slot is a fixed set of registers); A double buffered in LDS
-    const int nchunk = a.Kd / PF_KC;
-    constexpr int NITEM = MT * 32 * (PF_KC / 8);
-    constexpr int NA = NITEM / THREADS;
-    size_t abase[NA];
-    bool alive[NA];
-#pragma unroll
-    for (int q = 0; q < NA; q++) {
-        const int it = tid + q * THREADS, m = it >> 3;
+    for (int q = 0; q < 4; q++) {
+        const int it = tid + q * PF8_THREADS, m = it >> 3;
         alive[q] = m < mrows;
         const int mm = alive[q] ? m : 0;
         const int row = a.tok ? a.tok[s0 + r0 + mm] : s0 + r0 + mm;
         abase[q] = (size_t)row * a.x_ld + (it & 7) * 8;
     }
-    uint4 ra[2][NA][2];
-    uint32_t bw[2][4][NT];
-    auto load = [&](int kc, int sl) {                 // kc clamped: a valid repeat past the end
-        const int kk = kc < nchunk ? kc : nchunk - 1;
+    const int nchunk = a.Kd / PF_KC;
+    uint4 ra[4][2];
+    uint32_t bw[4];
+    auto load = [&](int kc) {
 #pragma unroll
-        for (int q = 0; q < NA; q++) {
-            const size_t e0 = abase[q] + (size_t)kk * PF_KC;
-            if (a.x_mode == 0) {
-                ra[sl][q][0] = *(const uint4 *)((const float *)a.x + e0);
-                ra[sl][q][1] = *(const uint4 *)((const float *)a.x + e0 + 4);
+        for (int q = 0; q < 4; q++) {
+            const size_t e0 = abase[q] + (size_t)kc * PF_KC;
+            if (XM == 0) {
+                ra[q][0] = *(const uint4 *)((const float *)a.x + e0);
+                ra[q][1] = *(const uint4 *)((const float *)a.x + e0 + 4);
             } else {
-                ra[sl][q][0] = *(const uint4 *)((const uint16_t *)a.x + e0);
+                ra[q][0] = *(const uint4 *)((const uint16_t *)a.x + e0);
             }
         }
 #pragma unroll
-        for (int st = 0; st < 4; st++) {
-            const int k = kk * PF_KC + st * 16 + 8 * (lane >> 5);
-#pragma unroll
-            for (int j = 0; j < NT; j++) bw[sl][st][j] = ld_u32_unaligned((const uint8_t *)(ib[j] + (size_t)(k >> 3) * 192));
-        }
+        for (int q = 0; q < 4; q++)
+            bw[q] = ld_u32_unaligned((const uint8_t *)(dib + (size_t)(kc * 8 + dv0 + 2 * q) * 192));
     };
-    auto chunk = [&](int kc, int sl) {
-        h8 av8[NA];
+    auto stage_a = [&](int buf) {
 #pragma unroll
-        for (int q = 0; q < NA; q++) {
+        for (int q = 0; q < 4; q++) {
             h8 v;
-            if (a.x_mode == 2) {
-                v = as_h8(ra[sl][q][0]);
-            } else if (a.x_mode == 1) {
-                const uint32_t uu[4] = {ra[sl][q][0].x, ra[sl][q][0].y, ra[sl][q][0].z, ra[sl][q][0].w};
+            if (XM == 2) {
+                v = as_h8(ra[q][0]);
+            } else if (XM == 1) {
+                const uint32_t uu[4] = {ra[q][0].x, ra[q][0].y, ra[q][0].z, ra[q][0].w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     v[2 * i] = to_h(wh_bf16(uu[i] & 0xffff), bad);
                     v[2 * i + 1] = to_h(wh_bf16(uu[i] >> 16), bad);
                 }
             } else {
-                const float f[8] = {__uint_as_float(ra[sl][q][0].x), __uint_as_float(ra[sl][q][0].y),
-                                    __uint_as_float(ra[sl][q][0].z), __uint_as_float(ra[sl][q][0].w),
-                                    __uint_as_float(ra[sl][q][1].x), __uint_as_float(ra[sl][q][1].y),
-                                    __uint_as_float(ra[sl][q][1].z), __uint_as_float(ra[sl][q][1].w)};
+                const float f[8] = {__uint_as_float(ra[q][0].x), __uint_as_float(ra[q][0].y),
+                                    __uint_as_float(ra[q][0].z), __uint_as_float(ra[q][0].w),
+                                    __uint_as_float(ra[q][1].x), __uint_as_float(ra[q][1].y),
+                                    __uint_as_float(ra[q][1].z), __uint_as_float(ra[q][1].w)};
 #pragma unroll
                 for (int i = 0; i < 8; i++) v[i] = to_h(f[i], bad);
             }
             if (!alive[q])
 #pragma unroll
                 for (int i = 0; i < 8; i++) v[i] = (_Float16)0.0f;
-            av8[q] = v;
-        }
-        uint32_t u[4][NT];
-#pragma unroll
-        for (int st = 0; st < 4; st++)
-#pragma unroll
-            for (int j = 0; j < NT; j++) u[st][j] = bw[sl][st][j];
-        // buffer kc&1 was last read two chunks ago; the barrier of the chunk
-        // between guarantees every wave is done with it
-        _Float16 *Ab = As + (kc & 1) * ABUF;
-#pragma unroll
-        for (int q = 0; q < NA; q++) {
-            const int it = tid + q * THREADS;
-            *(uint4 *)(Ab + (it >> 3) * PF_ALD + (it & 7) * 8) = as_u4(av8[q]);
-        }
-        __syncthreads();
-        load(kc + 2, sl);                             // this slot's next chunk flies now
-#pragma unroll
-        for (int st = 0; st < 4; st++) {
-            h8 b[NT];
-#pragma unroll
-            for (int j = 0; j < NT; j++) {
-                const uint4 *bk = cbk + kj[j] * 3 * 256;
-                const h8 c0 = as_h8(bk[u[st][j] & 255]);
-                const h8 c1 = as_h8(bk[256 + ((u[st][j] >> 8) & 255)]);
-                const h8 c2 = as_h8(bk[512 + ((u[st][j] >> 16) & 255)]);
-                b[j] = vq_sum3(c0, c1, c2);
-            }
-#pragma unroll
-            for (int t = 0; t < MT; t++) {
-                if (t * 32 >= mrows) continue;        // uniform
-                const h8 av = as_h8(*(const uint4 *)(Ab + (t * 32 + (lane & 31)) * PF_ALD + st * 16 + 8 * (lane >> 5)));
-#pragma unroll
-                for (int j = 0; j < NT; j++)
-                    acc[j][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b[j], acc[j][t], 0, 0, 0);
-            }
+            const int it = tid + q * PF8_THREADS;
+            sA[buf][pf8_slot(it >> 3, it & 7)] = as_u4(v);
         }
     };
-    load(0, 0);
-    load(1, 1);
-    for (int kc = 0; kc < nchunk; kc += 2) {
-        chunk(kc, 0);
-        if (kc + 1 < nchunk) chunk(kc + 1, 1);        // uniform
+    const uint4 *bk = cbk + dkind * 3 * 256;
+    auto decode = [&](int buf, int q) {
+        const uint32_t u = bw[q];
+        const h8 w = vq_sum3(as_h8(bk[u & 255]), as_h8(bk[256 + ((u >> 8) & 255)]), as_h8(bk[512 + ((u >> 16) & 255)]));
+        sB[buf][pf8_slot(dc, dv0 + 2 * q)] = as_u4(w);
+    };
+
+    acc16 acc[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[t][j][r] = 0.0f;
+    bool tlive[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++) tlive[t] = mw * 64 + t * 32 < mrows;
+
+    load(0);
+    __syncthreads();                                 // the books
+    stage_a(0);
+#pragma unroll
+    for (int q = 0; q < 4; q++) decode(0, q);
+    if (nchunk > 1) load(1);
+    __syncthreads();
+    // operands of k step st: 2 A and 4 B fragments
+    auto read_ops = [&](int buf, int st, h8 (&av)[2], h8 (&bv)[4]) {
+        const int g = 2 * st + (lane >> 5);
+#pragma unroll
+        for (int t = 0; t < 2; t++) av[t] = as_h8(sA[buf][pf8_slot(mw * 64 + t * 32 + (lane & 31), g)]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) bv[j] = as_h8(sB[buf][pf8_slot(bcol[j] + (lane & 31), g)]);
+    };
+    for (int kc = 0; kc < nchunk; kc++) {
+        const int buf = kc & 1;
+        const bool more = kc + 1 < nchunk;           // uniform
+        if (more) stage_a(buf ^ 1);
+        h8 av[2], bv[4];
+        read_ops(buf, 0, av, bv);
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            // the next step's operands are read before this step's products
+            // go out; rows past the segment are zeros, so every tile runs
+            h8 avn[2], bvn[4];
+            if (st < 3) read_ops(buf, st + 1, avn, bvn);
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[t], bv[j], acc[t][j], 0, 0, 0);
+            if (more) decode(buf ^ 1, st);           // chunk kc+1's B, one vector per k step
+            if (st < 3) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) av[t] = avn[t];
+#pragma unroll
+                for (int j = 0; j < 4; j++) bv[j] = bvn[j];
+            }
+        }
+        if (kc + 2 < nchunk) load(kc + 2);
+        __syncthreads();
     }
 
-    // epilogue: lane l, register r of tile t holds row t*32 + (r/4)*8 + (l/32)*4 + r%4
-    float rsc[NT];
+    // epilogue: lane l, register r of tile t holds row mw*64 + t*32 + (r/4)*8 + (l/32)*4 + r%4
+    float rsc[4];
 #pragma unroll
-    for (int j = 0; j < NT; j++) {
-        g_u16 *sc = (g_u16 *)(as_global(rec) + a.sc_off[kj[j]]);
-        rsc[j] = wh_f16_scale(sc[nok[j] ? ncol[j] : 0]);
+    for (int j = 0; j < 4; j++) {
+        g_u16 *sc = (g_u16 *)(as_global(rec) + a.sc_off[bkind[j]]);
+        rsc[j] = wh_f16_scale(sc[nok[j] ? wrow[j] : 0]);
     }
 #pragma unroll
-    for (int t = 0; t < MT; t++) {
-        if (t * 32 >= mrows) continue;
+    for (int t = 0; t < 2; t++) {
+        if (!tlive[t]) continue;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const int m = t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+            const int m = mw * 64 + t * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
             if (m >= mrows) continue;
             const size_t row = (size_t)(s0 + r0 + m);
             if (EPI == 0) {
 #pragma unroll
-                for (int f = 0; f < FK; f++)
+                for (int f = 0; f < 2; f++)
                     if (nok[f]) {
-                        const float h = wh_silu_mul(acc[f][t][r] * rsc[f], acc[FK + f][t][r] * rsc[FK + f]);
-                        ((_Float16 *)a.out)[row * a.out_ld + ncol[f]] = to_h(h, bad);
+                        const float h = wh_silu_mul(acc[t][f][r] * rsc[f], acc[t][f + 2][r] * rsc[f + 2]);
+                        ((_Float16 *)a.out)[row * a.out_ld + wrow[f]] = to_h(h, bad);
                     }
             } else {
 #pragma unroll
-                for (int j = 0; j < NT; j++)
-                    if (nok[j]) ((float *)a.out)[row * a.out_ld + ncol[j]] = acc[j][t][r] * rsc[j];
+                for (int j = 0; j < 4; j++)
+                    if (nok[j]) ((float *)a.out)[row * a.out_ld + wrow[j]] = acc[t][j][r] * rsc[j];
             }
         }
     }
@@ -633,15 +656,19 @@ extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, in
     if (dec != DEC_VQ && a->rowbytes % 16) return (int)hipErrorInvalidValue;
     if (dec == DEC_VQ && a->N % 64) return (int)hipErrorInvalidValue;
     if (a->x_ld % 8) return (int)hipErrorInvalidValue;
-    if (dec == DEC_VQ && mt == 4) {
-        // expert segments of PF_BIG tokens or more: the register-tiled
-        // kernel; shorter ones below (each workgroup checks its segment)
-        const int ntile = pair ? 256 : 512;
-        dim3 grid((a->N + ntile - 1) / ntile, segs, mblocks);
-        if (pair) hipLaunchKernelGGL((k_pf_gemm4<0, PF_NT>), grid, dim3(pf4<PF_NT>::THREADS), 0, s, *a);
-        else hipLaunchKernelGGL((k_pf_gemm4<1, PF_NT>), grid, dim3(pf4<PF_NT>::THREADS), 0, s, *a);
+    if (dec == DEC_VQ && mt == 4 && a->seg_off) {
+        // expert segments of PF_BIG tokens or more: 256 x 256 tiles; shorter
+        // ones below (each workgroup checks its segment)
+        const int n8 = pair ? PF8_N / 2 : PF8_N;
+        dim3 grid8((a->N + n8 - 1) / n8, segs, (mblocks + 1) / 2);
+        if (pair && a->x_mode == 2) hipLaunchKernelGGL((k_pf_gemm8<0, 2>), grid8, dim3(PF8_THREADS), 0, s, *a);
+        else if (pair && a->x_mode == 1) hipLaunchKernelGGL((k_pf_gemm8<0, 1>), grid8, dim3(PF8_THREADS), 0, s, *a);
+        else if (pair) hipLaunchKernelGGL((k_pf_gemm8<0, 0>), grid8, dim3(PF8_THREADS), 0, s, *a);
+        else if (a->x_mode == 2) hipLaunchKernelGGL((k_pf_gemm8<1, 2>), grid8, dim3(PF8_THREADS), 0, s, *a);
+        else if (a->x_mode == 1) hipLaunchKernelGGL((k_pf_gemm8<1, 1>), grid8, dim3(PF8_THREADS), 0, s, *a);
+        else hipLaunchKernelGGL((k_pf_gemm8<1, 0>), grid8, dim3(PF8_THREADS), 0, s, *a);
         const int e = (int)hipGetLastError();
-        if (e || !a->seg_off) return e;
+        if (e) return e;
     }
     const int ntile = pair ? 128 : 256;
     dim3 grid((a->N + ntile - 1) / ntile, segs, mblocks);
@@ -656,6 +683,43 @@ extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, in
     else if (dec == DEC_F32) { if (pair) PF(DEC_F32, 0); else PF(DEC_F32, 1); }
     else return (int)hipErrorInvalidValue;
 #undef PF
+    return (int)hipGetLastError();
+}
+
+// ---- activations to fp16, once per chunk ---------------------------------------
+// The products' A operand: each token row is staged by every column block
+// of every expert it is routed to, so its conversion (and range check) is
+// done once here.  n8: elements / 8; x 16-byte aligned.
+__global__ void __launch_bounds__(256)
+k_pf_to_f16(const void *__restrict__ x, int bf16, size_t n8, uint4 *__restrict__ y, int *err)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    bool bad = false;
+    h8 v;
+    if (bf16) {
+        const uint4 u = ((const uint4 *)x)[i];
+        const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            v[2 * k] = to_h(wh_bf16(uu[k] & 0xffff), bad);
+            v[2 * k + 1] = to_h(wh_bf16(uu[k] >> 16), bad);
+        }
+    } else {
+        const float4 f0 = ((const float4 *)x)[2 * i], f1 = ((const float4 *)x)[2 * i + 1];
+        v[0] = to_h(f0.x, bad); v[1] = to_h(f0.y, bad); v[2] = to_h(f0.z, bad); v[3] = to_h(f0.w, bad);
+        v[4] = to_h(f1.x, bad); v[5] = to_h(f1.y, bad); v[6] = to_h(f1.z, bad); v[7] = to_h(f1.w, bad);
+    }
+    y[i] = as_u4(v);
+    if (bad) atomicOr(err, ERR_RANGE);
+}
+
+extern "C" int whip_pf_to_f16(const void *x, int bf16, size_t n, uint16_t *y, int *err, hipStream_t s)
+{
+    if (n % 8 || (uintptr_t)x % 16 || (uintptr_t)y % 16) return (int)hipErrorInvalidValue;
+    const size_t n8 = n / 8;
+    if (!n8) return 0;
+    hipLaunchKernelGGL(k_pf_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, x, bf16, n8, (uint4 *)y, err);
     return (int)hipGetLastError();
 }
 

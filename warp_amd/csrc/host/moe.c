@@ -71,6 +71,7 @@ struct waste_hip_moe {
     /* many-token path (T > Td) */
     int32_t *pair_pos, *seg_off, *order;
     uint16_t *h16, *sh_h16;      /* fp16 [P][I], [T][SI]                   */
+    uint16_t *x16;               /* the chunk's activations, fp16 [T][H]    */
     float *ypair, *rpart;        /* [P][H]; router partial sums            */
     int *err;                    /* [0] status bits; [4] the lookahead's    */
     float *plogits, *pw;         /* the lookahead's logits and weights      */
@@ -134,7 +135,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->b.logits, m->b.w, m->b.pair_w, m->b.part_gu, m->b.h, m->b.part_d,
                      m->b.h_sh, m->b.sh_out, m->b.ids, m->b.pair_tok, m->b.pair_exp,
                      m->b.tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
-                     m->sh_h16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->b.pair_rec,
+                     m->sh_h16, m->x16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->b.pair_rec,
                      m->b.rcnt, m->b.xchg };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0]) {
@@ -233,6 +234,7 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
         rc |= dmalloc((void **)&m->seg_off, ((size_t)m->E + 2) * 4);
         rc |= dmalloc((void **)&m->order, (size_t)m->E * 4);
         rc |= dmalloc((void **)&m->h16, (size_t)P * m->I * 2);
+        rc |= dmalloc((void **)&m->x16, (size_t)m->T * m->H * 2);
         rc |= dmalloc((void **)&m->ypair, (size_t)P * m->H * 4);
         rc |= dmalloc((void **)&m->rpart, whip_pf_router_part_floats(m->T, m->E) * 4);
     }
@@ -456,12 +458,14 @@ static int route_many(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_
     if ((uintptr_t)x % 16) return WASTE_HIP_EINVAL;
     MARK(0);
     CK((hipError_t)whip_pf_router(&m->router, x, x_bf16, T, m->rpart, lg, s));
+    /* the products' A operand, converted once (experts() reads it too) */
+    CK((hipError_t)whip_pf_to_f16(x, x_bf16, (size_t)T * H, m->x16, m->err, s));
     if (m->has_shared) {
         whip_pf_args a;
         memset(&a, 0, sizeof a);
         a.W0 = (const uint8_t *)m->sh[0].q; a.W1 = (const uint8_t *)m->sh[1].q;
         a.S0 = m->sh[0].qs; a.S1 = m->sh[1].qs; a.rowbytes = m->sh[0].rowbytes; a.group = m->sh[0].group;
-        a.N = m->SI; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H;
+        a.N = m->SI; a.Kd = H; a.x = m->x16; a.x_mode = 2; a.x_ld = H;
         a.rows = T; a.out = m->sh_h16; a.out_ld = m->SI; a.err = m->err;
         CK((hipError_t)whip_pf_gemm(&a, m->sh[0].fmt, 1, 1, 1, (T + 31) / 32, s));
     }
@@ -476,6 +480,7 @@ static int route_many(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_
 
 static int experts_many(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
 {
+    (void)x; (void)x_bf16;       /* the products read route()'s fp16 copy of x */
     const int E = m->E, K = m->K, H = m->H, I = m->I;
     const int mb = (T + 127) / 128;
     MARK(2);
@@ -484,7 +489,7 @@ static int experts_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
     a.recs = m->d_recs; a.idx_off[0] = m->off_gate; a.idx_off[1] = m->off_up;
     a.sc_off[0] = m->off_sc; a.sc_off[1] = m->off_sc + 2u * (uint32_t)I;
     a.books16 = m->d_books16; a.cb = m->cb - m->book0;
-    a.N = I; a.Kd = H; a.x = x; a.x_mode = x_bf16 ? 1 : 0; a.x_ld = H; a.tok = m->b.pair_tok;
+    a.N = I; a.Kd = H; a.x = m->x16; a.x_mode = 2; a.x_ld = H; a.tok = m->b.pair_tok;   /* route()'s fp16 copy */
     a.seg_off = m->seg_off; a.order = m->order; a.out = m->h16; a.out_ld = I; a.err = m->err;
     CK((hipError_t)whip_pf_gemm(&a, WQ_VQ3R, 1, 4, E, mb, s));
     MARK(3);
