@@ -113,13 +113,39 @@ int whip_vq_act(const uint8_t *const *recs, const int32_t *pair_exp, int P,
                 hipStream_t s);
 
 /* y[t*H + i] = sum over token t's pairs (combine order) of
- *   w * (scale_d[i] * sum_c part_d) + sh[t*H + i] (sh may be NULL).
+ *   w * (scale_d[i] * sum_c part_d) + sh_t[i] (sh may be NULL), where
+ * sh_t[i] = sum over q < sh_n, in order, of sh[q*sh_stride + t*H + i]
+ * (the slices of a split product; sh_n 1: sh[t*H + i] itself).
  * sc_off_down 0: part_d is already scaled (a down launch with out_sc_off).
  * T == 1: the token's pairs are pairs 0 .. K-1 (tok_pairs is not read). */
 int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                  const float *pair_w, const int32_t *tok_pairs, int T, int K,
                  const float *part_d, int nch, int H, uint32_t sc_off_down,
-                 int skip_zero, const float *sh, float *y, hipStream_t s);
+                 int skip_zero, const float *sh, int sh_n, size_t sh_stride,
+                 float *y, hipStream_t s);
+
+/* ---- products of a few tokens on the matrix cores (skinny.hip) ---- */
+
+/* part[q][t][r] (q < nsl, t < T, r < A.rows) = the partial sum of A[r] . x[t]
+ * over column slice q; the slices' sum is the product.  x is fp32 or bf16
+ * (x_bf16), rows x_ld elements apart (x_ld % 8 == 0, x 16-byte aligned); all
+ * jobs of one launch read the same kind of x.  nsl must be
+ * whip_sk_slices(&A); whip_sk_ok says whether A's shape is taken (columns a
+ * multiple of 128, F32 or Q8G/Q4G with groups a multiple of 128). */
+typedef struct {
+    whip_mat A;
+    const void *x;
+    int x_ld, x_bf16;
+    float *part;
+    int nsl;
+} whip_sk_job;
+int whip_sk_ok(const whip_mat *A);
+int whip_sk_slices(const whip_mat *A);
+int whip_sk_run(const whip_sk_job *jobs, int n, int T, hipStream_t s);
+/* logits[t*E + e] = sum over q < nsl_r of pr[q][t][e], in order; with pg
+ * set, also h[t*SI + i] = silu(sum of pg[q][t][i]) * (sum of pu[q][t][i]). */
+int whip_sk_finish(const float *pr, int nsl_r, int E, float *logits, const float *pg,
+                   const float *pu, int nsl_g, int SI, float *h, int T, hipStream_t s);
 
 /* ---- VQ4P through the int8 LUT (vq4p.hip) ---- */
 

@@ -56,23 +56,37 @@ extern "C" int whip_route(const whip_route_cfg *c, const float *logits, const fl
 // experts in (src/model.c:7193-7197) — and each token's pairs in ascending
 // expert order, its combine order (src/model.c:7230-7250).  Keys carry the
 // selection slot as the last tie-break so every position is written once.
+// The pairs' experts are staged in LDS first (at most PAIRS_LDS of them;
+// beyond that they are read from global memory): a pair's position is a
+// count over all pairs, and one global round trip per comparison made this
+// launch cost more than the routing at 64 and more pairs.
+#define PAIRS_LDS 4096
 __global__ void __launch_bounds__(256)
 k_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T, int K, int E,
         int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp, float *__restrict__ pair_w,
         int32_t *__restrict__ tok_pairs)
 {
+    __shared__ int se[PAIRS_LDS];
     const int P = T * K;
+    const bool staged = P <= PAIRS_LDS;
+    if (staged) {
+        for (int q = threadIdx.x; q < P; q += blockDim.x) se[q] = ids[q] < 0 ? E : ids[q];
+        __syncthreads();
+    }
+    auto exp_of = [&](int q) { return staged ? se[q] : (ids[q] < 0 ? E : ids[q]); };
     for (int q = threadIdx.x; q < P; q += blockDim.x) {
         const int t = q / K, j = q % K;
-        const int e = ids[q] < 0 ? E : ids[q];
+        const int e = exp_of(q);
+        // pairs before q: a lower expert, or the same expert at an earlier
+        // (token, slot), i.e. an earlier flat index
         int pos = 0;
         for (int q2 = 0; q2 < P; q2++) {
-            const int e2 = ids[q2] < 0 ? E : ids[q2], t2 = q2 / K, j2 = q2 % K;
-            pos += (e2 < e) || (e2 == e && (t2 < t || (t2 == t && j2 < j)));
+            const int e2 = exp_of(q2);
+            pos += (e2 < e) || (e2 == e && q2 < q);
         }
         int rk = 0;
         for (int j2 = 0; j2 < K; j2++) {
-            const int e2 = ids[t * K + j2] < 0 ? E : ids[t * K + j2];
+            const int e2 = exp_of(t * K + j2);
             rk += (e2 < e) || (e2 == e && j2 < j);
         }
         pair_tok[pos] = t;

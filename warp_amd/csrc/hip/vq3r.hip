@@ -831,7 +831,7 @@ __global__ void __launch_bounds__(256)
 k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
           const float *__restrict__ pair_w, const int32_t *__restrict__ tok_pairs, int K,
           const float *__restrict__ part_d, int nch, int H, uint32_t sc_off_down,
-          int skip_zero, const float *__restrict__ sh, float *__restrict__ y)
+          int skip_zero, const float *__restrict__ sh, int sh_n, size_t sh_stride, float *__restrict__ y)
 {
     // [K][CMB_SLICES][G] slice sums, [K][G] row scales, [K] weights, [K] live
     extern __shared__ float4 cred[];
@@ -844,6 +844,18 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
     const int r0 = blockIdx.x * CMB_ROWS + g * 4;
     const int per = (nch + CMB_SLICES - 1) / CMB_SLICES;
     WT_SPAN(3, 0);
+    // the shared expert's slices, summed in order while the gathers fly
+    float4 shv = make_float4(0, 0, 0, 0);
+    const bool has_sh = sh != nullptr;
+    if (has_sh && tid < G && r0 < H) {
+        const float *shr = sh + (size_t)t * H + r0;
+        shv = *(const float4 *)shr;
+        for (int q = 1; q < sh_n; q++) {
+            const float4 v = *(const float4 *)(shr + (size_t)q * sh_stride);
+            shv.x = __fadd_rn(shv.x, v.x); shv.y = __fadd_rn(shv.y, v.y);
+            shv.z = __fadd_rn(shv.z, v.z); shv.w = __fadd_rn(shv.w, v.w);
+        }
+    }
     for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G)
         cmb_gather(recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, t, it, g, r0,
                    per, cred, csc, cw, cl);
@@ -866,11 +878,10 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
         o[3] = __fadd_rn(o[3], __fmul_rn(wj, __fmul_rn(sum[3], sc.w)));
     }
     float4 r;
-    const float *shr = sh ? sh + (size_t)t * H + r0 : nullptr;
-    r.x = __fadd_rn(o[0], shr ? shr[0] : 0.0f);
-    r.y = __fadd_rn(o[1], shr ? shr[1] : 0.0f);
-    r.z = __fadd_rn(o[2], shr ? shr[2] : 0.0f);
-    r.w = __fadd_rn(o[3], shr ? shr[3] : 0.0f);
+    r.x = __fadd_rn(o[0], shv.x);
+    r.y = __fadd_rn(o[1], shv.y);
+    r.z = __fadd_rn(o[2], shv.z);
+    r.w = __fadd_rn(o[3], shv.w);
     *(float4 *)(y + (size_t)t * H + r0) = r;
 }
 
@@ -949,13 +960,16 @@ extern "C" int whip_combine_sh(const uint8_t *const *recs, const int32_t *pair_e
 extern "C" int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                             const float *pair_w, const int32_t *tok_pairs, int T, int K,
                             const float *part_d, int nch, int H, uint32_t sc_off_down,
-                            int skip_zero, const float *sh, float *y, hipStream_t s)
+                            int skip_zero, const float *sh, int sh_n, size_t sh_stride, float *y,
+                            hipStream_t s)
 {
-    if (H % 4 || K < 1 || K > 64) return (int)hipErrorInvalidValue;
+    if (H % 4 || K < 1 || K > 64 || (sh && (sh_n < 1 || sh_stride % 4 || (uintptr_t)sh % 16)))
+        return (int)hipErrorInvalidValue;
     dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
     const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
     WHIP_LAUNCH(k_combine, grid, dim3(256), lds, s,
-                recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, sh, y);
+                recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, sh, sh_n,
+                sh_stride, y);
     return (int)hipGetLastError();
 }
 

@@ -44,6 +44,8 @@ typedef struct {
     const uint8_t **pair_rec;    /* [64] records of a T = 1 route's pairs   */
     int *rcnt;                   /* the routing launch's block counter (0)  */
     uint64_t *xchg;              /* [E + 1] its tagged logits, last tag     */
+    float *sk_part;              /* column-slice partials of the few-token
+                                    products (NULL: the GEMV kernels)       */
 } fwd_bufs;
 
 struct waste_hip_moe {
@@ -84,6 +86,12 @@ struct waste_hip_moe {
     int sh_done;                 /* the route's launch ran the shared down  */
     int sh_in_combine;           /* the combine runs the shared down        */
     int32_t *d_look;             /* the lookahead's ids                    */
+    /* few-token products on the matrix cores (skinny.hip): column slices of
+     * the router, the shared gate/up and the shared down (0: not taken),
+     * and the partials' buffer, Td tokens' worth */
+    int sk_r, sk_g, sk_d;
+    float *sk_mem;
+    size_t sk_cap;
     int prof_on;
     hipEvent_t ev[WASTE_HIP_STAGES + 1];
     hipEvent_t kev[2 * WASTE_HIP_STAGES];   /* per-stage kernel start/stop   */
@@ -136,7 +144,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->b.h_sh, m->b.sh_out, m->b.ids, m->b.pair_tok, m->b.pair_exp,
                      m->b.tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
                      m->sh_h16, m->x16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->b.pair_rec,
-                     m->b.rcnt, m->b.xchg };
+                     m->b.rcnt, m->b.xchg, m->sk_mem };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0]) {
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -276,6 +284,34 @@ static int upload_tensor(const waste_hip_tensor *t, int rows, int cols, whip_mat
     return 0;
 }
 
+/* The few-token products' column slices for the trunk tensors held now, and
+ * a partials buffer for Td tokens of the larger of the two launches (the
+ * router with the shared gate/up; the shared down).  Without a router, or
+ * with a shape the matrix-core kernel does not take, the GEMV kernels run. */
+static int sk_setup(waste_hip_moe *m)
+{
+    m->sk_r = m->has_router && m->Td > 1 ? whip_sk_slices(&m->router) : 0;
+    m->sk_g = m->sk_r && m->has_shared ? whip_sk_slices(&m->sh[0]) : 0;
+    m->sk_d = m->sk_r && m->has_shared ? whip_sk_slices(&m->sh[2]) : 0;
+    if (m->has_shared && (!m->sk_g || !m->sk_d)) m->sk_r = m->sk_g = m->sk_d = 0;
+    m->b.sk_part = NULL;
+    if (!m->sk_r) return 0;
+    const size_t a = (size_t)m->sk_r * m->E + 2 * (size_t)m->sk_g * m->SI;
+    const size_t d = (size_t)m->sk_d * m->H;
+    const size_t need = (size_t)m->Td * (a > d ? a : d) * 4;
+    if (need > m->sk_cap) {
+        if (m->sk_mem) hipFree(m->sk_mem);
+        m->sk_cap = 0;
+        if (dmalloc((void **)&m->sk_mem, need)) {
+            m->sk_r = m->sk_g = m->sk_d = 0;
+            return WASTE_HIP_ENOMEM;
+        }
+        m->sk_cap = need;
+    }
+    m->b.sk_part = m->sk_mem;
+    return 0;
+}
+
 int waste_hip_moe_set_router(waste_hip_moe *m, const waste_hip_tensor *gate, const float *bias)
 {
     if (!m) return WASTE_HIP_EINVAL;
@@ -287,14 +323,14 @@ int waste_hip_moe_set_router(waste_hip_moe *m, const waste_hip_tensor *gate, con
         CK(hipMemcpy(m->d_bias, bias, (size_t)m->E * 4, hipMemcpyHostToDevice));
     }
     m->has_router = 1;
-    return 0;
+    return sk_setup(m);
 }
 
 int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
                              const waste_hip_tensor *up, const waste_hip_tensor *down)
 {
     if (!m) return WASTE_HIP_EINVAL;
-    if (!gate && !up && !down) { m->has_shared = 0; return 0; }
+    if (!gate && !up && !down) { m->has_shared = 0; return sk_setup(m); }
     int rc = upload_tensor(gate, m->SI, m->H, &m->sh[0], &m->sh_mem[0]);
     if (!rc) rc = upload_tensor(up, m->SI, m->H, &m->sh[1], &m->sh_mem[1]);
     if (!rc) rc = upload_tensor(down, m->H, m->SI, &m->sh[2], &m->sh_mem[2]);
@@ -307,7 +343,7 @@ int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
         if (rc) return WASTE_HIP_ENOMEM;
     }
     m->has_shared = 1;
-    return 0;
+    return sk_setup(m);
 }
 
 int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16, int n_books)
@@ -553,7 +589,27 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
         }
         if (rr != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
     }
-    CK((hipError_t)whip_gemv_multi(r, nr, T, s));
+    if (T > 1 && m->b.sk_part && (uintptr_t)x % 16 == 0 && H % 8 == 0) {
+        /* a few tokens: the router and the shared gate/up on the matrix
+         * cores, column-sliced, then the slices' sums (and the SwiGLU) */
+        float *pr = m->b.sk_part, *pg = NULL, *pu = NULL;
+        whip_sk_job j[3];
+        int nj = 0;
+        j[nj].A = m->router; j[nj].x = x; j[nj].x_ld = H; j[nj].x_bf16 = x_bf16; j[nj].part = pr;
+        j[nj].nsl = m->sk_r; nj++;
+        if (m->has_shared) {
+            pg = pr + (size_t)m->sk_r * T * E;
+            pu = pg + (size_t)m->sk_g * T * m->SI;
+            for (int q = 0; q < 2; q++) {
+                j[nj].A = m->sh[q]; j[nj].x = x; j[nj].x_ld = H; j[nj].x_bf16 = x_bf16;
+                j[nj].part = q ? pu : pg; j[nj].nsl = m->sk_g; nj++;
+            }
+        }
+        CK((hipError_t)whip_sk_run(j, nj, T, s));
+        CK((hipError_t)whip_sk_finish(pr, m->sk_r, E, lg, pg, pu, m->sk_g, m->SI, m->b.h_sh, T, s));
+    } else {
+        CK((hipError_t)whip_gemv_multi(r, nr, T, s));
+    }
     MARK(1);
     if (T == 1 && m->has_shared) {
         /* routing and the shared expert's down projection in one launch;
@@ -646,14 +702,26 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
         whip_time_next(NULL, NULL);
         m->ktimed = 0;
         CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->b.h_sh, m->SI, T, m->b.sh_out, NULL, H, s));
-    } else if (m->has_shared && !m->sh_done && !sh_in_gu) {
-        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->b.h_sh, m->SI, T, m->b.sh_out, NULL, H, s));
+    }
+    const float *shp = m->has_shared ? m->b.sh_out : NULL;
+    int sh_n = 1;
+    if (m->has_shared && !m->sh_done && !sh_in_gu && !m->sh_in_combine) {
+        if (T > 1 && m->b.sk_part) {
+            /* column slices on the matrix cores; the combine adds them */
+            whip_sk_job j;
+            j.A = m->sh[2]; j.x = m->b.h_sh; j.x_ld = m->SI; j.x_bf16 = 0; j.part = m->b.sk_part;
+            j.nsl = m->sk_d;
+            CK((hipError_t)whip_sk_run(&j, 1, T, s));
+            shp = m->b.sk_part;
+            sh_n = m->sk_d;
+        } else {
+            CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->b.h_sh, m->SI, T, m->b.sh_out, NULL, H, s));
+        }
     }
     MARK(6);
     if (m->ktimed) KT(6);
     CK((hipError_t)whip_combine(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->b.part_d,
-                                m->nch_d, H, cmb_sc, T > 1,
-                                m->has_shared ? m->b.sh_out : NULL, y, s));
+                                m->nch_d, H, cmb_sc, T > 1, shp, sh_n, (size_t)T * H, y, s));
     MARK(7);
     return prof_end(m);
 }
@@ -783,6 +851,14 @@ static size_t static_layout(const waste_hip_moe *m, int T, uint8_t *base, fwd_bu
         TAKE(sh_out, float *, (size_t)T * m->H * 4);
     } else if (b) {
         b->h_sh = b->sh_out = NULL;
+    }
+    /* the few-token products' slice partials, as forward() has them */
+    if (T > 1 && m->sk_r && m->sk_mem) {
+        const size_t a = (size_t)m->sk_r * m->E + 2 * (size_t)m->sk_g * m->SI;
+        const size_t d = (size_t)m->sk_d * m->H;
+        TAKE(sk_part, float *, (size_t)T * (a > d ? a : d) * 4);
+    } else if (b) {
+        b->sk_part = NULL;
     }
 #undef TAKE
     if (b) {
