@@ -203,6 +203,11 @@ typedef struct {
     int *err;
 } whip_pf_args;
 int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, int segs, int mblocks, hipStream_t s);
+/* One dense Q4G/Q8G product of a.rows tokens (the shared expert): fp16 A
+ * (x_mode 2) against the rows W0 (and W1 with pair: SwiGLU to fp16 out),
+ * groups a multiple of 128 columns summed exactly and scaled in fp32.
+ * hipErrorInvalidValue for a shape it does not take (then whip_pf_gemm). */
+int whip_pf_dense(const whip_pf_args *a, int dec, int pair, hipStream_t s);
 
 /* n activations (fp32, or bf16 when bf16) to fp16 for the products' A
  * operand; a value outside fp16's range sets err bit 4. */

@@ -723,6 +723,196 @@ extern "C" int whip_pf_to_f16(const void *x, int bf16, size_t n, uint16_t *y, in
     return (int)hipGetLastError();
 }
 
+// ---- the shared expert over many tokens --------------------------------------
+// Q4G / Q8G rows (model.c:484-492) against the chunk's fp16 activations on
+// v_mfma_f32_32x32x16_f16.  Each 128-column group's integer products are
+// summed in fp32 and then multiplied by the group's f16 scale, in fp32 (the
+// engine's order: the group's dot product, then its scale); no weight is
+// rounded.  A weight enters as the fp16 of its integer: 0x6400 | code is
+// 1024 + code, and one packed fp16 subtraction of 1032 (4-bit: code = q + 8)
+// or 1152 (8-bit: code = q + 128) leaves q exactly, two weights per
+// instruction.  The pairs come out interleaved (codes j and j + 4 of a
+// word, or bytes j and j + 2), and the A fragments are staged in LDS in the
+// same interleaved column order, so every product still pairs each weight
+// with its own activation.
+//
+// A workgroup: 64 tokens x 128 weight rows, a wavefront per 32 rows, the k
+// loop in 128-column chunks (one scale group); A double-buffered in LDS in
+// the operand's order, B one chunk ahead in registers.
+//   EPI 0: 64 gate rows (waves 0-1) and the same 64 up rows (waves 2-3);
+//          h = silu(gate) * up leaves as fp16 (range-checked).
+//   EPI 1: 128 rows of one matrix, fp32 out.
+#define DN_KC 128
+typedef _Float16 dn_h2 __attribute__((ext_vector_type(2)));
+
+template <int FMT>
+WH_INLINE h8 dn_frag(const uint4 *w, int s)
+{
+    uint32_t o[4];
+    if constexpr (FMT == DEC_Q4) {
+        const uint4 q = w[s >> 2];
+        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+        const uint32_t d = wd[s & 3];
+#pragma unroll
+        for (int j = 0; j < 4; j++) o[j] = ((d >> (4 * j)) & 0x000f000fu) | 0x64006400u;
+    } else {
+        const uint4 q = w[(s >> 1) & 3];
+        const uint32_t d0 = ((s & 1) ? q.z : q.x) ^ 0x80808080u, d1 = ((s & 1) ? q.w : q.y) ^ 0x80808080u;
+        o[0] = (d0 & 0x00ff00ffu) | 0x64006400u;
+        o[1] = ((d0 >> 8) & 0x00ff00ffu) | 0x64006400u;
+        o[2] = (d1 & 0x00ff00ffu) | 0x64006400u;
+        o[3] = ((d1 >> 8) & 0x00ff00ffu) | 0x64006400u;
+    }
+    const _Float16 c = FMT == DEC_Q4 ? (_Float16)-1032.0f : (_Float16)-1152.0f;
+    const dn_h2 off = {c, c};
+#pragma unroll
+    for (int j = 0; j < 4; j++) o[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(dn_h2, o[j]) + off);
+    return as_h8(make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+// eight fp16 activations (words [x0 x1][x2 x3][x4 x5][x6 x7]) in dn_frag's
+// column order
+template <int FMT>
+WH_INLINE uint4 dn_order(uint4 v)
+{
+    if constexpr (FMT == DEC_Q4)                     // x0 x4 x1 x5 x2 x6 x3 x7
+        return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                          __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+    return make_uint4(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u),
+                      __builtin_amdgcn_perm(v.w, v.z, 0x05040100u), __builtin_amdgcn_perm(v.w, v.z, 0x07060302u));
+}
+
+template <int FMT, int EPI>
+__global__ void __launch_bounds__(256) k_pf_dense(whip_pf_args a)
+{
+    __shared__ uint4 Af[2][2][8][64];                // [buffer][M fragment][product][lane]
+    constexpr int NW = FMT == DEC_Q4 ? 2 : 4;        // 16-byte words of a lane's chunk
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.y * 64;
+    const int kind = EPI == 0 ? (w >> 1) : 0;
+    const int row = EPI == 0 ? blockIdx.x * 64 + (w & 1) * 32 + n : blockIdx.x * 128 + w * 32 + n;
+    const bool row_ok = row < a.N;
+    const int rc = row_ok ? row : a.N - 1;
+    const int ng = a.Kd / a.group;
+    const uint8_t *Wr = (kind ? a.W1 : a.W0) + (size_t)rc * a.rowbytes;
+    const uint16_t *Sr = (kind ? a.S1 : a.S0) + (size_t)rc * ng;
+    // staging: thread -> token sm of the tile, columns 32sj .. 32sj+31 of the
+    // chunk: half sj/2, products 4(sj&1) .. +3.  Tokens past the chunk read
+    // its last token again (their outputs are never stored).
+    const int sm = tid >> 2, sj = tid & 3;
+    const int tok = min(t0 + sm, a.rows - 1);
+    const uint16_t *xr = (const uint16_t *)a.x + (size_t)tok * a.x_ld + 32 * sj;
+    const int mf = sm >> 5, slot = (sj >> 1) * 32 + (sm & 31), s_base = 4 * (sj & 1);
+    uint4 ra[4], wn[NW], wc[NW];
+    uint16_t scn, scc;
+    auto load = [&](int c) {
+        const int k0 = c * DN_KC;
+#pragma unroll
+        for (int i = 0; i < 4; i++) ra[i] = *(const uint4 *)(xr + k0 + 8 * i);
+        const int kk = k0 + 64 * h;
+        const uint8_t *p = Wr + (FMT == DEC_Q4 ? kk / 2 : kk);
+#pragma unroll
+        for (int i = 0; i < NW; i++) wn[i] = *(const uint4 *)(p + 16 * i);
+        scn = Sr[k0 / a.group];
+    };
+    auto stage = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) Af[b][mf][s_base + i][slot] = dn_order<FMT>(ra[i]);
+    };
+    const int nch = a.Kd / DN_KC;
+    acc16 acc[2];
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[f][r] = 0.0f;
+    load(0);
+    stage(0);
+#pragma unroll
+    for (int i = 0; i < NW; i++) wc[i] = wn[i];
+    scc = scn;
+    __syncthreads();
+    for (int c = 0; c < nch; c++) {
+        load(min(c + 1, nch - 1));                   // unconditional: the last chunk again at the end
+        acc16 ag[2];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const h8 b = dn_frag<FMT>(wc, s);
+#pragma unroll
+            for (int f = 0; f < 2; f++) {
+                const h8 av = as_h8(Af[c & 1][f][s][lane]);
+                if (s == 0) {
+                    acc16 z;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) z[r] = 0.0f;
+                    ag[f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b, z, 0, 0, 0);
+                } else {
+                    ag[f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, b, ag[f], 0, 0, 0);
+                }
+            }
+        }
+        const float g = wh_f16_scale(scc);
+#pragma unroll
+        for (int f = 0; f < 2; f++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[f][r] = __fmaf_rn(g, ag[f][r], acc[f][r]);
+        stage((c + 1) & 1);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NW; i++) wc[i] = wn[i];
+        scc = scn;
+    }
+    // lane (n, h), register r of M fragment f: token t0 + 32f + 8(r/4) + 4h + r%4
+    if (EPI == 1) {
+        if (!row_ok) return;
+#pragma unroll
+        for (int f = 0; f < 2; f++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int t = t0 + 32 * f + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (t < a.rows) ((float *)a.out)[(size_t)t * a.out_ld + row] = acc[f][r];
+            }
+        return;
+    }
+    float *ex = (float *)Af;                         // [gate wave][f][16][64]
+    if (w < 2)
+#pragma unroll
+        for (int f = 0; f < 2; f++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) ex[((w * 2 + f) * 16 + r) * 64 + lane] = acc[f][r];
+    __syncthreads();
+    if (w < 2 || !row_ok) return;
+    bool bad = false;
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int t = t0 + 32 * f + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (t < a.rows) {
+                const float v = wh_silu_mul(ex[(((w - 2) * 2 + f) * 16 + r) * 64 + lane], acc[f][r]);
+                ((_Float16 *)a.out)[(size_t)t * a.out_ld + row] = to_h(v, bad);
+            }
+        }
+    if (bad) atomicOr(a.err, ERR_RANGE);
+}
+
+extern "C" int whip_pf_dense(const whip_pf_args *a, int dec, int pair, hipStream_t s)
+{
+    if ((dec != DEC_Q4 && dec != DEC_Q8) || a->x_mode != 2 || a->rows < 1 || a->N < 1 || a->Kd < DN_KC ||
+        a->Kd % DN_KC || a->group < DN_KC || a->group % DN_KC || a->Kd % a->group || a->rowbytes % 16 ||
+        a->x_ld % 8 || (uintptr_t)a->x % 16 || !a->S0 || (pair && (!a->W1 || !a->S1)))
+        return (int)hipErrorInvalidValue;
+    const dim3 grid(pair ? (a->N + 63) / 64 : (a->N + 127) / 128, (a->rows + 63) / 64);
+    if (dec == DEC_Q4) {
+        if (pair) WHIP_LAUNCH((k_pf_dense<DEC_Q4, 0>), grid, dim3(256), 0, s, *a);
+        else WHIP_LAUNCH((k_pf_dense<DEC_Q4, 1>), grid, dim3(256), 0, s, *a);
+    } else {
+        if (pair) WHIP_LAUNCH((k_pf_dense<DEC_Q8, 0>), grid, dim3(256), 0, s, *a);
+        else WHIP_LAUNCH((k_pf_dense<DEC_Q8, 1>), grid, dim3(256), 0, s, *a);
+    }
+    return (int)hipGetLastError();
+}
+
 // ---- router on the matrix cores (fp32) -------------------------------------
 // logits[t][e] = W[e] . x[t] with fp32 products (v_mfma_f32_32x32x2_f32),
 // split over k into RT_KS ranges whose partial sums are then added in

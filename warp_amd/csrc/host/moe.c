@@ -503,7 +503,11 @@ static int route_many(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_
         a.S0 = m->sh[0].qs; a.S1 = m->sh[1].qs; a.rowbytes = m->sh[0].rowbytes; a.group = m->sh[0].group;
         a.N = m->SI; a.Kd = H; a.x = m->x16; a.x_mode = 2; a.x_ld = H;
         a.rows = T; a.out = m->sh_h16; a.out_ld = m->SI; a.err = m->err;
-        CK((hipError_t)whip_pf_gemm(&a, m->sh[0].fmt, 1, 1, 1, (T + 31) / 32, s));
+        const int rc = whip_pf_dense(&a, m->sh[0].fmt, 1, s);
+        if (rc == (int)hipErrorInvalidValue)
+            CK((hipError_t)whip_pf_gemm(&a, m->sh[0].fmt, 1, 1, 1, (T + 31) / 32, s));
+        else
+            CK((hipError_t)rc);
     }
     MARK(1);
     whip_route_cfg rc = { E, K, m->c.score_func, m->c.renorm, m->c.routed_scale,
@@ -541,7 +545,11 @@ static int experts_many(waste_hip_moe *m, const void *x, int x_bf16, int T, floa
         a.W0 = (const uint8_t *)m->sh[2].q; a.S0 = m->sh[2].qs; a.rowbytes = m->sh[2].rowbytes;
         a.group = m->sh[2].group; a.N = H; a.Kd = m->SI; a.x = m->sh_h16; a.x_mode = 2;
         a.x_ld = m->SI; a.rows = T; a.out = m->b.sh_out; a.out_ld = H; a.err = m->err;
-        CK((hipError_t)whip_pf_gemm(&a, m->sh[2].fmt, 0, 1, 1, (T + 31) / 32, s));
+        const int rc = whip_pf_dense(&a, m->sh[2].fmt, 0, s);
+        if (rc == (int)hipErrorInvalidValue)
+            CK((hipError_t)whip_pf_gemm(&a, m->sh[2].fmt, 0, 1, 1, (T + 31) / 32, s));
+        else
+            CK((hipError_t)rc);
     }
     MARK(6);
     CK((hipError_t)whip_pf_combine(m->b.tok_pairs, m->b.pair_exp, m->b.pair_w, m->d_recs, T, K, E, m->ypair, H,
