@@ -146,6 +146,11 @@ int whip_sk_run(const whip_sk_job *jobs, int n, int T, hipStream_t s);
  * set, also h[t*SI + i] = silu(sum of pg[q][t][i]) * (sum of pu[q][t][i]). */
 int whip_sk_finish(const float *pr, int nsl_r, int E, float *logits, const float *pg,
                    const float *pu, int nsl_g, int SI, float *h, int T, hipStream_t s);
+/* whip_sk_finish and whip_route (ids, w; no pair lists) in one launch, for
+ * E <= 256 with ceil(E/64)*K <= 64; hipErrorInvalidValue otherwise. */
+int whip_sk_route(const whip_route_cfg *c, const float *pr, int nsl_r, float *logits, const float *bias,
+                  int T, int32_t *ids, float *w, int *err, const float *pg, const float *pu, int nsl_g,
+                  int SI, float *h, hipStream_t s);
 
 /* ---- VQ4P through the int8 LUT (vq4p.hip) ---- */
 

@@ -59,18 +59,22 @@ extern "C" int whip_route(const whip_route_cfg *c, const float *logits, const fl
 // The pairs' experts are staged in LDS first (at most PAIRS_LDS of them;
 // beyond that they are read from global memory): a pair's position is a
 // count over all pairs, and one global round trip per comparison made this
-// launch cost more than the routing at 64 and more pairs.
+// launch cost more than the routing at 64 and more pairs.  The count reads
+// four experts per LDS access, several accesses in flight (a loop that
+// waits on each read took 19 us at 256 pairs); the staged list is padded to
+// a multiple of four with a value no expert id reaches.
 #define PAIRS_LDS 4096
 __global__ void __launch_bounds__(256)
 k_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T, int K, int E,
         int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp, float *__restrict__ pair_w,
         int32_t *__restrict__ tok_pairs)
 {
-    __shared__ int se[PAIRS_LDS];
+    __shared__ __attribute__((aligned(16))) int se[PAIRS_LDS + 4];
     const int P = T * K;
     const bool staged = P <= PAIRS_LDS;
     if (staged) {
         for (int q = threadIdx.x; q < P; q += blockDim.x) se[q] = ids[q] < 0 ? E : ids[q];
+        if (threadIdx.x < 4) se[P + threadIdx.x] = 0x7fffffff;
         __syncthreads();
     }
     auto exp_of = [&](int q) { return staged ? se[q] : (ids[q] < 0 ? E : ids[q]); };
@@ -80,9 +84,23 @@ k_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T, int
         // pairs before q: a lower expert, or the same expert at an earlier
         // (token, slot), i.e. an earlier flat index
         int pos = 0;
-        for (int q2 = 0; q2 < P; q2++) {
-            const int e2 = exp_of(q2);
-            pos += (e2 < e) || (e2 == e && q2 < q);
+        if (staged) {
+            const int4 *s4 = (const int4 *)se;
+            const int n4 = (P + 3) >> 2;
+#pragma unroll 4
+            for (int i = 0; i < n4; i++) {
+                const int4 v = s4[i];
+                const int b = 4 * i;
+                pos += (v.x < e) | ((v.x == e) & (b < q));
+                pos += (v.y < e) | ((v.y == e) & (b + 1 < q));
+                pos += (v.z < e) | ((v.z == e) & (b + 2 < q));
+                pos += (v.w < e) | ((v.w == e) & (b + 3 < q));
+            }
+        } else {
+            for (int q2 = 0; q2 < P; q2++) {
+                const int e2 = exp_of(q2);
+                pos += (e2 < e) || (e2 == e && q2 < q);
+            }
         }
         int rk = 0;
         for (int j2 = 0; j2 < K; j2++) {

@@ -42,6 +42,7 @@
 // A operand's order, one 16-byte read per lane per product.
 #include "common.h"
 #include "launch.h"
+#include "route.h"
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float acc16 __attribute__((ext_vector_type(16)));
@@ -349,6 +350,61 @@ k_sk_finish(const float *__restrict__ pr, int nsl_r, int E, float *__restrict__ 
     const float g = sum_slices(pg + j, nsl_g, (size_t)nh);
     const float u = sum_slices(pu + j, nsl_g, (size_t)nh);
     h[j] = wh_silu_mul(g, u);
+}
+
+// The same sums and the routing in one launch: block t < T sums token t's
+// router slices into its logits (written out) and selects its experts with
+// the batch-1 router launch's workgroup selection (route_fast: the engine's
+// scores, group limit, tie rule and selection-order weights); blocks from T
+// on sum the shared gate/up slices and apply the SwiGLU.
+__global__ void __launch_bounds__(256)
+k_sk_route(whip_route_cfg c, const float *__restrict__ pr, int nsl_r, float *__restrict__ logits,
+           const float *__restrict__ bias, int T, int32_t *__restrict__ ids, float *__restrict__ wout,
+           int *__restrict__ err, const float *__restrict__ pg, const float *__restrict__ pu, int nsl_g,
+           int SI, float *__restrict__ h)
+{
+    __shared__ __align__(16) float s_lds[ROUTE_FAST_FLOATS(256)];
+    __shared__ int32_t s_ids[64];
+    __shared__ float s_w[64];
+    __shared__ const uint8_t *s_tab[256];
+    __shared__ const uint8_t *s_rec[64];
+    __shared__ uint64_t s_etab[32];
+    const int tid = threadIdx.x, E = c.E, K = c.K;
+    if ((int)blockIdx.x >= T) {                      // uniform
+        const int j = ((int)blockIdx.x - T) * 256 + tid, nh = T * SI;
+        if (j < nh) h[j] = wh_silu_mul(sum_slices(pg + j, nsl_g, (size_t)nh), sum_slices(pu + j, nsl_g, (size_t)nh));
+        return;
+    }
+    const int t = blockIdx.x;
+    float l = 0.0f, be = 0.0f;
+    if (tid < E) {
+        l = sum_slices(pr + (size_t)t * E + tid, nsl_r, (size_t)T * E);
+        logits[(size_t)t * E + tid] = l;
+        be = bias ? bias[tid] : 0.0f;
+    }
+    s_tab[tid] = nullptr;                            // no records wanted: pairs come after
+    if (tid < 32) s_etab[tid] = wh_exp_tab[tid];
+    __syncthreads();
+    route_fast<256>(c, l, be, s_tab, s_etab, s_lds, s_ids, s_w, s_rec, err);
+    if (tid < K) {
+        ids[(size_t)t * K + tid] = s_ids[tid];
+        wout[(size_t)t * K + tid] = s_w[tid];
+    }
+}
+
+extern "C" int whip_sk_route(const whip_route_cfg *c, const float *pr, int nsl_r, float *logits, const float *bias,
+                             int T, int32_t *ids, float *w, int *err, const float *pg, const float *pu, int nsl_g,
+                             int SI, float *h, hipStream_t s)
+{
+    // route_fast's shapes: every expert a thread, the candidates one wavefront
+    if (T < 1 || c->E < 1 || c->E > 256 || c->K < 1 || ((c->E + 63) >> 6) * c->K > 64 || nsl_r < 1 ||
+        (c->n_group > 1 && (c->n_group > 64 || c->E % c->n_group || c->topk_group < 1)) ||
+        (pg && (!pu || !h || nsl_g < 1 || SI < 1)))
+        return (int)hipErrorInvalidValue;
+    const int nb = T + (pg ? (T * SI + 255) / 256 : 0);
+    WHIP_LAUNCH(k_sk_route, dim3(nb), dim3(256), 0, s, *c, pr, nsl_r, logits, bias, T, ids, w, err, pg, pu, nsl_g,
+                SI, h);
+    return (int)hipGetLastError();
 }
 
 extern "C" int whip_sk_ok(const whip_mat *A)

@@ -597,9 +597,11 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
         }
         if (rr != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
     }
+    int routed = 0;
     if (T > 1 && m->b.sk_part && (uintptr_t)x % 16 == 0 && H % 8 == 0) {
         /* a few tokens: the router and the shared gate/up on the matrix
-         * cores, column-sliced, then the slices' sums (and the SwiGLU) */
+         * cores, column-sliced, then the slices' sums (and the SwiGLU) with
+         * the routing in the same launch where its shape allows */
         float *pr = m->b.sk_part, *pg = NULL, *pu = NULL;
         whip_sk_job j[3];
         int nj = 0;
@@ -614,7 +616,11 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
             }
         }
         CK((hipError_t)whip_sk_run(j, nj, T, s));
-        CK((hipError_t)whip_sk_finish(pr, m->sk_r, E, lg, pg, pu, m->sk_g, m->SI, m->b.h_sh, T, s));
+        const int rr = whip_sk_route(&rc, pr, m->sk_r, lg, m->d_bias, T, d_ids, d_w, m->err, pg, pu, m->sk_g,
+                                     m->SI, m->b.h_sh, s);
+        if (rr == 0) routed = 1;
+        else if (rr != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
+        else CK((hipError_t)whip_sk_finish(pr, m->sk_r, E, lg, pg, pu, m->sk_g, m->SI, m->b.h_sh, T, s));
     } else {
         CK((hipError_t)whip_gemv_multi(r, nr, T, s));
     }
@@ -631,8 +637,9 @@ static int route_few(waste_hip_moe *m, const void *x, int x_bf16, int T, int32_t
         m->pair_rec_ok = 1;
         return 0;
     }
-    CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, m->b.pair_tok, m->b.pair_exp,
-                              m->b.pair_w, m->b.tok_pairs, m->err, s));
+    if (!routed)
+        CK((hipError_t)whip_route(&rc, lg, m->d_bias, T, d_ids, d_w, m->b.pair_tok, m->b.pair_exp,
+                                  m->b.pair_w, m->b.tok_pairs, m->err, s));
     if (T > 1)
         CK((hipError_t)whip_pairs(d_ids, d_w, T, K, E, m->b.pair_tok, m->b.pair_exp, m->b.pair_w,
                                   m->b.tok_pairs, s));
