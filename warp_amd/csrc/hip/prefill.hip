@@ -29,6 +29,7 @@
 // meaning), split over k with the partial sums added in a fixed order.
 #include "common.h"
 #include "launch.h"
+#include "bf16_split.h"
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float acc16 __attribute__((ext_vector_type(16)));
@@ -106,10 +107,14 @@ k_sort_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T
     }
     for (int q = tid; q < P; q += SORT_THREADS) {
         const int t = q / K, j = q - t * K;
-        const int e = ids[q] < 0 ? E : ids[q];
+        // the token's experts from LDS when staged (a global read per
+        // comparison, waited for one at a time, made this loop most of the
+        // launch)
+        const int e = staged ? eid[q] : (ids[q] < 0 ? E : ids[q]);
         int rk = 0;
         for (int j2 = 0; j2 < K; j2++) {
-            const int e2 = ids[t * K + j2] < 0 ? E : ids[t * K + j2];
+            const int q2 = t * K + j2;
+            const int e2 = staged ? eid[q2] : (ids[q2] < 0 ? E : ids[q2]);
             rk += e2 < e || (e2 == e && j2 < j);
         }
         tok_pairs[t * K + rk] = staged ? pos[q] : pair_pos[q];
@@ -1012,6 +1017,109 @@ k_pf_router(whip_mat W, const void *__restrict__ x, int x_bf16, int T, float *__
         }
 }
 
+// The same logits for F32 router rows on the bf16 matrix cores: each weight
+// split exactly into three bf16 pieces, bf16 activations used as they are
+// (fp32 ones split the same way, XS = 3), so every product is exact and
+// only the fp32 accumulation rounds (bf16_split.h); three or six bf16
+// products cost a fifth of the fp32 ones.  A workgroup: 32 tokens x 128
+// rows (a wavefront per 32 rows) x one of RT_KS column ranges, 128-column
+// chunks, the A fragments staged in LDS in the operand's order (double
+// buffered), a lane's 64 floats of the next chunk in flight during this one.
+// Partial sums in the k_pf_router layout, added by k_pf_router_sum.
+template <int XS>
+__global__ void __launch_bounds__(256) k_pf_router16(whip_mat W, const void *__restrict__ x, int T,
+                                                     float *__restrict__ part)
+{
+    __shared__ uint4 frag[2][XS][8][64];
+    const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.y * 32, ks = blockIdx.z, H = W.cols;
+    const int nck = H / DN_KC, per = (nck + RT_KS - 1) / RT_KS;
+    const int c_lo = ks * per, nc = max(0, min(nck, c_lo + per) - c_lo);
+    const int row = blockIdx.x * 128 + w * 32 + n;
+    const uint8_t *wr = (const uint8_t *)W.q + (size_t)min(row, W.rows - 1) * W.rowbytes;
+    // staging: thread -> token sm, 16 columns at 64*shh + 16*sq (products
+    // 2sq and 2sq + 1 of lane half shh); tokens past T read token 0 again
+    const int sm = tid >> 3, sj = tid & 7, shh = sj >> 2, sq = sj & 3;
+    const uint8_t *xrow = (const uint8_t *)x + (size_t)(t0 + sm < T ? t0 + sm : 0) * H * (XS == 1 ? 2 : 4);
+    constexpr int XW = XS == 1 ? 2 : 4;
+    uint4 xr[XW], wc[16], wn[16];
+    auto load = [&](int c) {                         // chunk c's activations and weights (into wn)
+        const int k0 = (c_lo + c) * DN_KC;
+        const int e = k0 + 64 * shh + 16 * sq;
+#pragma unroll
+        for (int i = 0; i < XW; i++) xr[i] = *(const uint4 *)(xrow + (size_t)e * (XS == 1 ? 2 : 4) + 16 * i);
+        const uint8_t *p = wr + (size_t)(k0 + 64 * h) * 4;
+#pragma unroll
+        for (int i = 0; i < 16; i++) wn[i] = *(const uint4 *)(p + 16 * i);
+    };
+    auto stage = [&](int b) {
+        const int slot = shh * 32 + sm;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++) {
+            if (XS == 1) {
+                frag[b][0][2 * sq + s2][slot] = xr[s2];
+            } else {
+                const float f[8] = {__uint_as_float(xr[2 * s2].x), __uint_as_float(xr[2 * s2].y),
+                                    __uint_as_float(xr[2 * s2].z), __uint_as_float(xr[2 * s2].w),
+                                    __uint_as_float(xr[2 * s2 + 1].x), __uint_as_float(xr[2 * s2 + 1].y),
+                                    __uint_as_float(xr[2 * s2 + 1].z), __uint_as_float(xr[2 * s2 + 1].w)};
+                uint4 p0, p1, p2;
+                split3(f, p0, p1, p2);
+                frag[b][0][2 * sq + s2][slot] = p0;
+                frag[b][XS > 1 ? 1 : 0][2 * sq + s2][slot] = p1;
+                frag[b][XS > 2 ? 2 : 0][2 * sq + s2][slot] = p2;
+            }
+        }
+    };
+    acc16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    if (nc > 0) {                                    // uniform
+        load(0);
+        stage(0);
+#pragma unroll
+        for (int i = 0; i < 16; i++) wc[i] = wn[i];
+        __syncthreads();
+        for (int c = 0; c < nc; c++) {
+            load(min(c + 1, nc - 1));                // unconditional: the last chunk again at the end
+#pragma unroll
+            for (int s = 0; s < 8; s++) {
+                bf16x8 a[XS];
+#pragma unroll
+                for (int p = 0; p < XS; p++) a[p] = as_b8(frag[c & 1][p][s][lane]);
+                const float f[8] = {__uint_as_float(wc[2 * s].x), __uint_as_float(wc[2 * s].y),
+                                    __uint_as_float(wc[2 * s].z), __uint_as_float(wc[2 * s].w),
+                                    __uint_as_float(wc[2 * s + 1].x), __uint_as_float(wc[2 * s + 1].y),
+                                    __uint_as_float(wc[2 * s + 1].z), __uint_as_float(wc[2 * s + 1].w)};
+                uint4 bh, bm, bl;
+                split3(f, bh, bm, bl);
+                // smallest terms first; for fp32 x the three below 2^-24 of
+                // the product are left out
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], as_b8(bl), acc, 0, 0, 0);
+                if (XS == 3) {
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[XS > 2 ? 2 : 0], as_b8(bh), acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[XS > 1 ? 1 : 0], as_b8(bm), acc, 0, 0, 0);
+                }
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], as_b8(bm), acc, 0, 0, 0);
+                if (XS == 3) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[XS > 1 ? 1 : 0], as_b8(bh), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], as_b8(bh), acc, 0, 0, 0);
+            }
+            stage((c + 1) & 1);
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 16; i++) wc[i] = wn[i];
+        }
+    }
+    if (row >= W.rows) return;
+    // lane (n, h), register r: token t0 + 8(r/4) + 4h + r%4
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int t = t0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (t < T) part[((size_t)ks * T + t) * W.rows + row] = acc[r];
+    }
+}
+
 __global__ void __launch_bounds__(256)
 k_pf_router_sum(const float *__restrict__ part, int n, float *__restrict__ logits)
 {
@@ -1031,7 +1139,11 @@ extern "C" int whip_pf_router(const whip_mat *W, const void *x, int x_bf16, int 
     if (W->cols % RT_KC || (W->fmt != 0 && (W->group % 32 || (W->fmt != 2 && W->fmt != 3))))
         return (int)hipErrorInvalidValue;
     dim3 grid((W->rows + 127) / 128, (T + 31) / 32, RT_KS);
-    if (W->fmt == 0) hipLaunchKernelGGL(k_pf_router<0>, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
+    const bool split = W->fmt == 0 && W->cols % DN_KC == 0 && W->rowbytes % 16 == 0 && (uintptr_t)x % 16 == 0 &&
+                       W->cols % 8 == 0;
+    if (split && x_bf16) hipLaunchKernelGGL(k_pf_router16<1>, grid, dim3(256), 0, s, *W, x, T, part);
+    else if (split) hipLaunchKernelGGL(k_pf_router16<3>, grid, dim3(256), 0, s, *W, x, T, part);
+    else if (W->fmt == 0) hipLaunchKernelGGL(k_pf_router<0>, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
     else if (W->fmt == 2) hipLaunchKernelGGL(k_pf_router<2>, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
     else hipLaunchKernelGGL(k_pf_router<3>, grid, dim3(256), 0, s, *W, x, x_bf16, T, part);
     const int n = T * W->rows;

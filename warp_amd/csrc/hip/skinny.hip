@@ -43,8 +43,8 @@
 #include "common.h"
 #include "launch.h"
 #include "route.h"
+#include "bf16_split.h"
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float acc16 __attribute__((ext_vector_type(16)));
 
 #define SK_WAVES 4
@@ -72,35 +72,6 @@ struct sk_pack {
     sk_job j[3];
     int n, T;
 };
-
-WH_INLINE bf16x8 as_b8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
-
-// bf16 pieces of 8 floats: hi, mid, lo with hi + mid + lo == f exactly
-WH_INLINE void split3(const float *f, uint4 &p0, uint4 &p1, uint4 &p2)
-{
-    uint32_t w0[4], w1[4], w2[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        uint32_t a[2], b[2], c[2];
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const float v = f[2 * i + j];
-            const uint32_t hi = __float_as_uint(v) & 0xffff0000u;
-            const float r1 = __fsub_rn(v, __uint_as_float(hi));
-            const uint32_t mid = __float_as_uint(r1) & 0xffff0000u;
-            const float r2 = __fsub_rn(r1, __uint_as_float(mid));
-            a[j] = hi >> 16;
-            b[j] = mid >> 16;
-            c[j] = __float_as_uint(r2) >> 16;
-        }
-        w0[i] = a[0] | (a[1] << 16);
-        w1[i] = b[0] | (b[1] << 16);
-        w2[i] = c[0] | (c[1] << 16);
-    }
-    p0 = make_uint4(w0[0], w0[1], w0[2], w0[3]);
-    p1 = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-    p2 = make_uint4(w2[0], w2[1], w2[2], w2[3]);
-}
 
 // eight nibbles (low first) as bf16(n + 128): 0x4300 | n, exact
 WH_INLINE uint4 q4_frag(uint32_t d)
