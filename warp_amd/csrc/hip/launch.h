@@ -104,7 +104,7 @@ typedef struct {
     float *shd_y;
 } whip_vq_args;
 int whip_vq_apply(const whip_vq_args *a, hipStream_t s);
-int whip_vq_chunks(int nv);          /* nch for a given nv                  */
+int whip_vq_chunks(int nv, int M);   /* nch for nv positions, M rows        */
 
 /* h[p*I + r] = silu(scale_g[r]*sum_c gpart) * (scale_u[r]*sum_c upart)
  * for the routed pairs. */

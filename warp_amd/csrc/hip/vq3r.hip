@@ -41,7 +41,10 @@
 #endif
 #define LUT_PER_V (3 * 256)
 
-extern "C" int whip_vq_chunks(int nv) { return (WH_LANES && nv % 32 == 0) ? nv / 32 : (nv + VC - 1) / VC; }
+// The tile kernels take whole 32-position chunks and pairs of 64-row blocks.
+#define LANES_OK(nv, M) (WH_LANES && (nv) % 32 == 0 && (M) % 128 == 0)
+
+extern "C" int whip_vq_chunks(int nv, int M) { return LANES_OK(nv, M) ? nv / 32 : (nv + VC - 1) / VC; }
 
 typedef const uint3 WH_GLOBAL g_uint3;
 
@@ -430,6 +433,11 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
                 for (int k = 0; k < 8; k++) s_h[v * 8 + k] = xv[k];
             }
             __syncthreads();
+            // The other wavefronts never read their x loads; without this
+            // wait the compiler keeps those registers pending into the tile
+            // loop and waits for every load at its head.  (Every earlier
+            // load, the prefetched tiles included, has landed by then.)
+            __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
         }
     };
     auto tables = [&]() {
@@ -454,12 +462,18 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     bool liveA, liveB, unbound = false;
     const bool presc = a.out_sc_off != 0;            // uniform
     tile_cur cA, cB;                                 // the tiles buffers A and B hold
-    const int hi0 = min(t1, (t0 / tm.tpc + 1) * tm.tpc);
+    // A run inside one class (shares > 0) is walked interleaved: wavefront
+    // wv takes tiles t0 + wv + LW j.  A run across classes is walked in
+    // pairs of adjacent row blocks (t, t + 1), t = t0 + 2 wv + 2 LW k: its
+    // classes and its length are even (host), so no pair straddles two
+    // classes and A and B stay in step across the classes.
+    const bool paired = shares == 0;                 // uniform
+    const int d1 = paired ? 2 : 1, d2 = paired ? 1 : LW;
     if (early) {
-        cA.t = t0 + wv;
+        cA.t = t0 + d1 * wv;
         tm.at(cA.t, cA.p, cA.kind, cA.chunk, cA.rb);
-        const int pc = cA.t < hi0 ? cA.p : p_lo;
-        where_rec(cA, hi0, uni(a.pair_rec[pc]), src, outA, liveA, scb);
+        const int pc = cA.t < t1 ? cA.p : p_lo;
+        where_rec(cA, t1, uni(a.pair_rec[pc]), src, outA, liveA, scb);
         load_tile(A, src, loff);
         scA = scb[presc ? lrow : 0];
     }
@@ -492,14 +506,30 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     __syncthreads();
     stage(t0);
     WT_KEEP(1);
-    int t = t0 + wv;
+    int t = t0 + d1 * wv;
     {
-        const int4 qa = s_cur[wv], qb = s_cur[wv + LW];
+        const int4 qa = s_cur[d1 * wv], qb = s_cur[d1 * wv + d2];
         cA.t = t; cA.p = __builtin_amdgcn_readfirstlane(qa.x); cA.kind = __builtin_amdgcn_readfirstlane(qa.y);
         cA.chunk = __builtin_amdgcn_readfirstlane(qa.z); cA.rb = __builtin_amdgcn_readfirstlane(qa.w);
-        cB.t = t + LW; cB.p = __builtin_amdgcn_readfirstlane(qb.x); cB.kind = __builtin_amdgcn_readfirstlane(qb.y);
+        cB.t = t + d2; cB.p = __builtin_amdgcn_readfirstlane(qb.x); cB.kind = __builtin_amdgcn_readfirstlane(qb.y);
         cB.chunk = __builtin_amdgcn_readfirstlane(qb.z); cB.rb = __builtin_amdgcn_readfirstlane(qb.w);
     }
+    // A holds the wavefront's next tile, B the one after.  After each tile,
+    // the tile two ahead goes out into the buffer it freed (the dummy past
+    // the run): across classes, a class's first pair is in flight while its
+    // tables are built.  The first two go out before the first tables (the
+    // earlier the loads go out the better: measured).  The buffers never
+    // trade contents: that would be a register copy, which waits for the
+    // loads in flight.
+    if (!early) {                                    // uniform: else already in flight
+        where(cA, t1, src, outA, liveA, scb);
+        load_tile(A, src, loff);
+        scA = scb[presc ? lrow : 0];
+    }
+    where(cB, t1, src, outB, liveB, scb);
+    load_tile(B, src, loff);
+    scB = scb[presc ? lrow : 0];
+    WT_KEEP(2);
     for (int lo = t0; lo < t1;) {
         const int hi = min(t1, (lo / tm.tpc + 1) * tm.tpc);
         if (lo > t0) {                               // uniform: the next class's build inputs
@@ -509,58 +539,40 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             __syncthreads();                         // the old tables and s_h are done with
             stage(lo);
         }
-        // this wavefront's tiles of the class, two a round: A holds tile t,
-        // B tile t + LW, and after each the tile two ahead goes out into the
-        // buffer it freed (the dummy past the class).  The buffers never
-        // trade roles: that would be a register copy, which waits for the
-        // loads in flight.  The first two go out before the tables (the
-        // earlier the loads go out the better: measured).
-        if (lo > t0 || !early) {                     // uniform: else already in flight
-            where(cA, hi, src, outA, liveA, scb);
-            load_tile(A, src, loff);
-            scA = scb[presc ? lrow : 0];
-        }
-        where(cB, hi, src, outB, liveB, scb);
-        load_tile(B, src, loff);
-        scB = scb[presc ? lrow : 0];
-        if (lo == t0) WT_KEEP(2);
         tables();
         if (lo == t0) WT_KEEP(3);
         // A counted loop of pairs and an odd tile after it: an exit in the
         // middle of a round leaves the compiler unsure which loads are in
         // flight at the loop's head, and it then waits for all of them.
-        const int n = t < hi ? (hi - t + LW - 1) / LW : 0;
+        // Only a single-class run has an odd count (its last class).
+        const int n = t >= hi ? 0 : paired ? 2 * ((hi - t + 2 * LW - 1) / (2 * LW)) : (hi - t + LW - 1) / LW;
         for (int i = 0; i + 1 < n; i += 2) {
             float r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
             r = presc ? __fmul_rn(r, wh_f16_scale(scA)) : r;
             __builtin_nontemporal_store(liveA ? r : 0.0f, outA + lrow);
             unbound |= !liveA;
             cA.step(tm, a.P, 2 * LW);
-            where(cA, hi, src, outA, liveA, scb);
+            where(cA, t1, src, outA, liveA, scb);
             load_tile(A, src, loff);
             scA = scb[presc ? lrow : 0];
+            __builtin_amdgcn_sched_barrier(0);       // the reload goes out before B's tile is read
             r = tile_sum(B, smem, bA0, bA1, bB, s0, s1, s2, lane);
             r = presc ? __fmul_rn(r, wh_f16_scale(scB)) : r;
             __builtin_nontemporal_store(liveB ? r : 0.0f, outB + lrow);
             unbound |= !liveB;
             cB.step(tm, a.P, 2 * LW);
-            where(cB, hi, src, outB, liveB, scb);
+            where(cB, t1, src, outB, liveB, scb);
             load_tile(B, src, loff);
             scB = scb[presc ? lrow : 0];
-            t += 2 * LW;
+            __builtin_amdgcn_sched_barrier(0);
         }
         if (n & 1) {
             float r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
             r = presc ? __fmul_rn(r, wh_f16_scale(scA)) : r;
             __builtin_nontemporal_store(liveA ? r : 0.0f, outA + lrow);
             unbound |= !liveA;
-            t += LW;
-            // the next tile of this wavefront is the one B holds; A's next, past it
-            const tile_cur c = cB;
-            cB = cA;
-            cB.step(tm, a.P, 2 * LW);
-            cA = c;
         }
+        t += n * LW;
         lo = hi;
     }
     WT(wk, 6 + wv);
@@ -626,20 +638,20 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
     if (a->M <= 0 || a->M % 64 || a->nv <= 0 || a->nv % VC || a->idx_off[0] % 4 || a->idx_off[1] % 4 ||
         a->P < 1 || a->rsplit < 1 || a->rsplit > rows || (span > 1 && (span != a->P || span > SPAN_MAX)))
         return (int)hipErrorInvalidValue;
-    const int nch = whip_vq_chunks(a->nv);
-    if (a->act_part && (!(WH_LANES && a->nv % PW == 0) || a->act_nch < 1 || a->kinds != 1 || span > 1))
+    const int nch = whip_vq_chunks(a->nv, a->M);
+    if (a->act_part && (!(LANES_OK(a->nv, a->M)) || a->act_nch < 1 || a->kinds != 1 || span > 1))
         return (int)hipErrorInvalidValue;
-    if (a->out_sc_off && (!(WH_LANES && a->nv % PW == 0) || a->out_sc_off % 2))
+    if (a->out_sc_off && (!(LANES_OK(a->nv, a->M)) || a->out_sc_off % 2))
         return (int)hipErrorInvalidValue;
     if (a->shd_y) {
         // the gate/up pass of the tile kernel only; whole 16-byte chunks
         const whip_mat *d = &a->shd;
-        if (a->kinds != 2 || !(WH_LANES && a->nv % PW == 0) || !a->shd_x || (uintptr_t)a->shd_x % 16 ||
+        if (a->kinds != 2 || !(LANES_OK(a->nv, a->M)) || !a->shd_x || (uintptr_t)a->shd_x % 16 ||
             d->rows < 1 || d->rowbytes % 16 || (d->fmt != 0 && d->fmt != 2 && d->fmt != 3) ||
             (d->fmt != 0 && (d->group % 32 || d->cols % 8)) || (d->fmt == 0 && d->cols % 4))
             return (int)hipErrorInvalidValue;
     }
-    if (WH_LANES && a->nv % PW == 0) {
+    if (LANES_OK(a->nv, a->M)) {
         // 16-byte aligned tiles (the kernel's 128-bit loads)
         if (a->idx_off[0] % 16 || a->idx_off[1] % 16) return (int)hipErrorInvalidValue;
         static int n_cu = 0;
@@ -662,8 +674,11 @@ extern "C" int whip_vq_apply(const whip_vq_args *a, hipStream_t s)
             shares = (tpc + per_wg - 1) / per_wg;
             G = classes * shares;
         } else {
-            G = n_cu;
-            per_wg = (tiles + G - 1) / G;
+            // runs across classes: an even number of tiles (the kernel's
+            // tile pairs; every class is even, M % 128 == 0)
+            per_wg = (tiles + n_cu - 1) / n_cu;
+            per_wg += per_wg & 1;
+            G = (tiles + per_wg - 1) / per_wg;
         }
         // a workgroup's records fit its table (at most SPAN_MAX pairs)
         const long tiles_per_pair = sp ? tiles : (long)a->kinds * nch * nb;

@@ -200,8 +200,8 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
         m->Td = m->T < pm ? m->T : pm;
     }
     m->nv_gu = m->H / 8; m->nv_d = m->I / 8;
-    m->nch_gu = whip_vq_chunks(m->nv_gu);
-    m->nch_d = whip_vq_chunks(m->nv_d);
+    m->nch_gu = whip_vq_chunks(m->nv_gu, m->I);
+    m->nch_d = whip_vq_chunks(m->nv_d, m->H);
     /* canonical record layout (tools/convert.py:942-977): 48 B header,
      * gate, up, down index streams, then f16 scales gate|up|down */
     m->idx_gu = (size_t)m->I * m->nv_gu * 3;
