@@ -130,11 +130,13 @@ def test_dsv3_prefill_512_hot(orc):
     _prefill_case(orc, hot=True)
 
 
-@pytest.mark.parametrize("H,I,T", [(2048, 1408, 1), (2048, 1408, 4), (1088, 512, 1), (1088, 512, 6)])
+@pytest.mark.parametrize("H,I,T", [(2048, 1408, 1), (2048, 1408, 4), (1088, 512, 1), (1088, 512, 6),
+                                   (1024, 448, 1), (1024, 448, 12)])
 def test_row_lane_widths(orc, H, I, T):
-    """Widths whose position count (H/8 or I/8) is not a multiple of 32 run
-    the row-lane apply kernels, the separate SwiGLU pass and the scales in
-    the combine."""
+    """Widths whose position count (H/8 or I/8) is not a multiple of 32, or
+    whose row count (I for gate/up, H for down) is an odd number of 64-row
+    blocks, run the row-lane apply kernels, the separate SwiGLU pass and the
+    scales in the combine."""
     say("test_row_lane_widths", H, I, T)
     L = Layer(H, I, 16, 4, score_func=0, renorm=1, routed_scale=2.5, bias=True, n_shared=1,
               shared_fmt=FMT_Q8G, router_fmt=FMT_F32, seed=600 + I + T)
