@@ -61,10 +61,12 @@ extern "C" int whip_route(const whip_route_cfg *c, const float *logits, const fl
 // count over all pairs, and one global round trip per comparison made this
 // launch cost more than the routing at 64 and more pairs.  The count reads
 // four experts per LDS access, several accesses in flight (a loop that
-// waits on each read took 19 us at 256 pairs); the staged list is padded to
-// a multiple of four with a value no expert id reaches.
+// waits on each read took 19 us at 256 pairs), and four threads share each
+// pair's count; the staged list is padded to a multiple of four with a
+// value no expert id reaches.
 #define PAIRS_LDS 4096
-__global__ void __launch_bounds__(256)
+#define PAIRS_THREADS 1024
+__global__ void __launch_bounds__(PAIRS_THREADS)
 k_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T, int K, int E,
         int32_t *__restrict__ pair_tok, int32_t *__restrict__ pair_exp, float *__restrict__ pair_w,
         int32_t *__restrict__ tok_pairs)
@@ -78,9 +80,14 @@ k_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T, int
         __syncthreads();
     }
     auto exp_of = [&](int q) { return staged ? se[q] : (ids[q] < 0 ? E : ids[q]); };
-    for (int q = threadIdx.x; q < P; q += blockDim.x) {
-        const int t = q / K, j = q % K;
-        const int e = exp_of(q);
+    // four threads per pair (part 0-3 of four adjacent lanes), each counting
+    // every fourth group of four entries; the parts meet by two shuffles
+    const int part = threadIdx.x & 3;
+    for (int q0 = 0; q0 < P; q0 += PAIRS_THREADS / 4) {   // uniform
+        const int q = q0 + (int)(threadIdx.x >> 2);
+        const bool live = q < P;
+        const int qc = live ? q : 0;
+        const int e = exp_of(qc);
         // pairs before q: a lower expert, or the same expert at an earlier
         // (token, slot), i.e. an earlier flat index
         int pos = 0;
@@ -88,29 +95,34 @@ k_pairs(const int32_t *__restrict__ ids, const float *__restrict__ w, int T, int
             const int4 *s4 = (const int4 *)se;
             const int n4 = (P + 3) >> 2;
 #pragma unroll 4
-            for (int i = 0; i < n4; i++) {
+            for (int i = part; i < n4; i += 4) {
                 const int4 v = s4[i];
                 const int b = 4 * i;
-                pos += (v.x < e) | ((v.x == e) & (b < q));
-                pos += (v.y < e) | ((v.y == e) & (b + 1 < q));
-                pos += (v.z < e) | ((v.z == e) & (b + 2 < q));
-                pos += (v.w < e) | ((v.w == e) & (b + 3 < q));
+                pos += (v.x < e) | ((v.x == e) & (b < qc));
+                pos += (v.y < e) | ((v.y == e) & (b + 1 < qc));
+                pos += (v.z < e) | ((v.z == e) & (b + 2 < qc));
+                pos += (v.w < e) | ((v.w == e) & (b + 3 < qc));
             }
         } else {
-            for (int q2 = 0; q2 < P; q2++) {
+            for (int q2 = part; q2 < P; q2 += 4) {
                 const int e2 = exp_of(q2);
-                pos += (e2 < e) || (e2 == e && q2 < q);
+                pos += (e2 < e) || (e2 == e && q2 < qc);
             }
         }
-        int rk = 0;
-        for (int j2 = 0; j2 < K; j2++) {
-            const int e2 = exp_of(t * K + j2);
-            rk += (e2 < e) || (e2 == e && j2 < j);
+        pos += __shfl_xor(pos, 1, 4);
+        pos += __shfl_xor(pos, 2, 4);
+        if (live && part == 0) {
+            const int t = q / K, j = q % K;
+            int rk = 0;
+            for (int j2 = 0; j2 < K; j2++) {
+                const int e2 = exp_of(t * K + j2);
+                rk += (e2 < e) || (e2 == e && j2 < j);
+            }
+            pair_tok[pos] = t;
+            pair_exp[pos] = e;
+            pair_w[pos] = w[q];
+            tok_pairs[t * K + rk] = pos;
         }
-        pair_tok[pos] = t;
-        pair_exp[pos] = e;
-        pair_w[pos] = w[q];
-        tok_pairs[t * K + rk] = pos;
     }
 }
 
@@ -118,7 +130,7 @@ extern "C" int whip_pairs(const int32_t *ids, const float *w, int T, int K, int 
                             int32_t *pair_tok, int32_t *pair_exp, float *pair_w,
                             int32_t *tok_pairs, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_pairs, dim3(1), dim3(256), 0, s, ids, w, T, K, E, pair_tok, pair_exp,
+    hipLaunchKernelGGL(k_pairs, dim3(1), dim3(PAIRS_THREADS), 0, s, ids, w, T, K, E, pair_tok, pair_exp,
                        pair_w, tok_pairs);
     return (int)hipGetLastError();
 }
