@@ -533,6 +533,7 @@ __device__ __forceinline__ void gx_rows(const gemv_job &J, int blk, const uint4 
         if (w * 16 < xl_bytes) xs[gx_lay<FMT, XBF>::word(w)] = w * 16 < xbytes ? xr[i] : make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
+    WT_L(8);
     float a0 = 0.0f, a1 = 0.0f;
     for (;;) {
 #pragma unroll
@@ -663,6 +664,13 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
     gx_block<XBF, NXL>(pk, blockIdx.x, xbytes, xl_bytes, xs, red, epoch);
     WT_SPAN(0, 1);
     WT_KEEP(1);
+#ifdef WH_TRACE
+    if (threadIdx.x == 0 && blockIdx.x < 1024) {
+        wt_buf[blockIdx.x * WT_SLOTS + 16] = wt_keep_[0];
+        wt_buf[blockIdx.x * WT_SLOTS + 17] = wt_lds_[8];
+        wt_buf[blockIdx.x * WT_SLOTS + 18] = wt_keep_[1];
+    }
+#endif
     if (!routing) return;
     if (tid < E) s_recs[tid] = rv;
     if (tid < 32) s_etab[tid] = ev;
@@ -696,6 +704,7 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
 #ifdef WH_TRACE
     wt_keep_[5] = clock64();
 #endif
+    WT_L(0);
     if (((E + 63) >> 6) * K <= 64) {                  // uniform
         route_fast<256>(c, l, be, s_recs, s_etab, s_sc, s_ids, s_w, s_rec, err);
     } else {
@@ -705,6 +714,7 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
         route_wg<256, true>(c, l, be, s_recs, s_etab, R, s_ids, s_w, s_rec, err);
     }
     WT_KEEP(3);
+    WT_L(6);
 #ifdef WH_TRACE
     wt_keep_[6] = clock64();
 #endif
@@ -721,6 +731,7 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
     WT_KEEP(4);
     if (tid == 0)
         for (int i = 0; i < 7; i++) WT_PUTAT(0, 1, i);
+    WT_LPUT(0, 2);
 }
 
 WT_READER(whip_trace_gemv)

@@ -647,6 +647,7 @@ __device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, flo
         if (tid < E) sc = __fdiv_rn(sc, s_part[NWV]);
     }
     if (tid < E) s_sc[tid] = sc;
+    WT_L(1);
     const float selv = tid < E ? __fadd_rn(sc, bias_e) : NEG_INF;
     // group limit
     const int G = c.n_group > 1 ? c.n_group : 1;
@@ -685,6 +686,7 @@ __device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, flo
             }
         }
         __syncthreads();
+        WT_L(2);
         if (tid < E) {
             // every group's score, four to a 16-byte read (s_g has 64
             // entries; those past G are not compared)
@@ -701,6 +703,7 @@ __device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, flo
             kept = mine > NEG_INF && rk < c.topk_group;
         }
     }
+    WT_L(3);
     // each wavefront's keys sorted; its first K are the candidates
     if (wv < ewv) {                                          // uniform
         const uint64_t key = tid < E ? sel_key(kept ? selv : NEG_INF, tid) : 0;
@@ -709,9 +712,11 @@ __device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, flo
         if (ewv == 1) s_cand[lane] = key;
     }
     __syncthreads();
+    WT_L(4);
     if (wv == 0) {
         const uint64_t cv = lane < (ewv > 1 ? ewv * K : 64) ? s_cand[lane] : 0;
         const uint64_t srt = wave_sort_desc(cv, lane);
+        WT_L(5);
         // lane p < K: the p-th selection; its weight the unbiased score.
         // The renormalising sum runs in selection order, the engine's, as a
         // chain over the lanes' values (no LDS round trip per term).

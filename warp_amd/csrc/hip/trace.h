@@ -35,6 +35,15 @@ __device__ uint64_t wt_buf[WT_ROWS * WT_SLOTS];
         if ((threadIdx.x & 63) == 0) wt_buf[((k) * 256 + (blockIdx.x & 255)) * WT_SLOTS + (i)] = wt_keep_[(i)]; \
     } while (0)
 #define WT_PUTAT(k, row, i) (wt_buf[((k) * 256 + (row)) * WT_SLOTS + (i)] = wt_keep_[(i)])
+// WT_L(i): thread 0 keeps a stamp in LDS (no memory counter touched);
+// WT_LPUT(k, row) stores the kept stamps to row `row` of kernel k
+__shared__ uint64_t wt_lds_[16];
+#define WT_L(i) do { if (threadIdx.x == 0) wt_lds_[(i)] = wall_clock64(); } while (0)
+#define WT_LPUT(k, row)                                                                                \
+    do {                                                                                               \
+        if (threadIdx.x == 0)                                                                          \
+            for (int q_ = 0; q_ < 16; q_++) wt_buf[((k) * 256 + (row)) * WT_SLOTS + q_] = wt_lds_[q_]; \
+    } while (0)
 #define WT_READER(name)                                                                                \
     extern "C" int name(uint64_t *host)                                                                \
     {                                                                                                  \
@@ -50,5 +59,7 @@ __device__ uint64_t wt_buf[WT_ROWS * WT_SLOTS];
 #define WT_KEEP(i) do { } while (0)
 #define WT_PUT(k, i) do { } while (0)
 #define WT_PUTAT(k, row, i) do { } while (0)
+#define WT_L(i) do { } while (0)
+#define WT_LPUT(k, row) do { } while (0)
 #define WT_READER(name)
 #endif

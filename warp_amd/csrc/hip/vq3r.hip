@@ -253,11 +253,11 @@ __device__ __forceinline__ void sh_rows8(const whip_mat &W, const float *x, int 
 // Issue order, so that no wait covers a load it does not need: the pairs'
 // records; then the first class's books and x (SPAN: every pair reads
 // source row 0) or, for ACT, its gate/up partials (summed as they arrive,
-// with the records); then the first two tiles of every wavefront; then the
-// build, which waits only for what came before the tiles.  Two tiles stay
+// with the records), staged in LDS; then each wavefront's first tile, which
+// flies while the first tables are built; then its second.  Two tiles stay
 // in flight per wavefront from there on.  (The small loads the build needs
-// are waited for before the tiles go out: sent together, they queue behind
-// the launch-wide burst of tile loads, which measured slower.)
+// are waited for before any tile goes out: sent together, they queue
+// behind the launch-wide burst of tile loads, which measured slower.)
 #define ACT_PF 8                                     // partials per kind a thread prefetches
 template <bool ACT, bool SPAN>
 __device__ __forceinline__ void
@@ -435,8 +435,9 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             __syncthreads();
             // The other wavefronts never read their x loads; without this
             // wait the compiler keeps those registers pending into the tile
-            // loop and waits for every load at its head.  (Every earlier
-            // load, the prefetched tiles included, has landed by then.)
+            // loop and waits for every load at its head.  (For the first
+            // class no tile is in flight yet; for a later one the tiles in
+            // flight went out before its build loads, so they have landed.)
             __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
         }
     };
@@ -445,15 +446,10 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
 #pragma unroll
         for (int k = 0; k < 8; k++) xv[k] = s_h[v * 8 + k];
         table_mfma(smem, sbook, xv, wv, v, h);
+        WT_KEEP(4);
         __syncthreads();
     };
 
-    // With the routing's record list at hand (one token), each wavefront's
-    // first tile goes out first: its record is one scalar load, and the
-    // tile's loads then fly while the build's inputs arrive and the tables
-    // are built (the build's loads go out right behind them: every one of
-    // them is an L2 hit but the partials of a down pass).
-    const bool early = a.pair_rec != nullptr;        // uniform
     tile_buf A, B;
     g_u8 *src;
     g_u16 *scb;
@@ -469,14 +465,6 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     // classes and A and B stay in step across the classes.
     const bool paired = shares == 0;                 // uniform
     const int d1 = paired ? 2 : 1, d2 = paired ? 1 : LW;
-    if (early) {
-        cA.t = t0 + d1 * wv;
-        tm.at(cA.t, cA.p, cA.kind, cA.chunk, cA.rb);
-        const int pc = cA.t < t1 ? cA.p : p_lo;
-        where_rec(cA, t1, uni(a.pair_rec[pc]), src, outA, liveA, scb);
-        load_tile(A, src, loff);
-        scA = scb[presc ? lrow : 0];
-    }
     // prologue: the records (one load each: the router wrote them, else
     // through the pair's expert), then the first build's loads
     {
@@ -503,6 +491,7 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             s_cur[tid] = make_int4(cp, ck, cc, cr);
         }
     }
+    WT_KEEP(5);
     __syncthreads();
     stage(t0);
     WT_KEEP(1);
@@ -517,15 +506,23 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     // A holds the wavefront's next tile, B the one after.  After each tile,
     // the tile two ahead goes out into the buffer it freed (the dummy past
     // the run): across classes, a class's first pair is in flight while its
-    // tables are built.  The first two go out before the first tables (the
-    // earlier the loads go out the better: measured).  The buffers never
-    // trade contents: that would be a register copy, which waits for the
-    // loads in flight.
-    if (!early) {                                    // uniform: else already in flight
-        where(cA, t1, src, outA, liveA, scb);
-        load_tile(A, src, loff);
-        scA = scb[presc ? lrow : 0];
-    }
+    // tables are built.  The buffers never trade contents: that would be a
+    // register copy, which waits for the loads in flight.
+    //
+    // Order at the start, measured on the batch-1 launch timelines: the
+    // build's inputs go out first and are staged (a tile sent ahead of them
+    // delays them by the whole launch's first burst: every wavefront's
+    // loads come back in issue order, and the first tiles of 224 workgroups
+    // fill the memory system); then the first tile goes out, the first
+    // tables are built while it flies, and only then the second tile.  With
+    // both tiles sent before the build, wavefronts stall issuing the second
+    // tile's loads and the barrier after the build waits for them: tables
+    // ready 9.3 us into the gate/up launch instead of 5.5.
+    where(cA, t1, src, outA, liveA, scb);
+    load_tile(A, src, loff);
+    scA = scb[presc ? lrow : 0];
+    tables();                                        // the first class's
+    WT_KEEP(3);
     where(cB, t1, src, outB, liveB, scb);
     load_tile(B, src, loff);
     scB = scb[presc ? lrow : 0];
@@ -538,9 +535,8 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             build_loads(lo, s_xr[pn - p_lo]);
             __syncthreads();                         // the old tables and s_h are done with
             stage(lo);
+            tables();
         }
-        tables();
-        if (lo == t0) WT_KEEP(3);
         // A counted loop of pairs and an odd tile after it: an exit in the
         // middle of a round leaves the compiler unsure which loads are in
         // flight at the loop's head, and it then waits for all of them.
@@ -548,6 +544,9 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         const int n = t >= hi ? 0 : paired ? 2 * ((hi - t + 2 * LW - 1) / (2 * LW)) : (hi - t + LW - 1) / LW;
         for (int i = 0; i + 1 < n; i += 2) {
             float r = tile_sum(A, smem, bA0, bA1, bB, s0, s1, s2, lane);
+#ifdef WH_TRACE
+            if (lo == t0 && i == 0) WT_KEEP(6);
+#endif
             r = presc ? __fmul_rn(r, wh_f16_scale(scA)) : r;
             __builtin_nontemporal_store(liveA ? r : 0.0f, outA + lrow);
             unbound |= !liveA;
@@ -576,7 +575,10 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         lo = hi;
     }
     WT(wk, 6 + wv);
-    if (wv == 0) { WT_PUT(wk, 0); WT_PUT(wk, 1); WT_PUT(wk, 2); WT_PUT(wk, 3); }
+    if (wv == 0) { WT_PUT(wk, 0); WT_PUT(wk, 1); WT_PUT(wk, 2); WT_PUT(wk, 3); WT_PUT(wk, 4); WT_PUT(wk, 5); }
+#ifdef WH_TRACE
+    if (wv == 0 && lane == 0) wt_buf[(wk * 256 + (blockIdx.x & 255)) * WT_SLOTS + 22] = wt_keep_[6];
+#endif
     if (unbound) atomicOr(a.err, 1);
 }
 
