@@ -441,11 +441,16 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
         }
     };
+    // x of this lane's position as bf16 pieces: bf16 activations are one
+    // exact piece; fp32 ones (and the down pass's SwiGLU) three
+    const bool x3 = ACT || !a.src_bf16;
     auto tables = [&]() {
         float xv[8];
 #pragma unroll
         for (int k = 0; k < 8; k++) xv[k] = s_h[v * 8 + k];
-        table_mfma(smem, sbook, xv, wv, v, h);
+        uint4 xb[3];
+        split3(xv, xb[0], xb[1], xb[2]);
+        table_mfma(smem, sbook, xb[0], xb[1], xb[2], x3, wv, lane);
         WT_KEEP(4);
         __syncthreads();
     };

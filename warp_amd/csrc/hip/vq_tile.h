@@ -5,6 +5,7 @@
 // on the matrix cores.  Shared by the apply kernels and the one-launch decode.
 #pragma once
 #include "common.h"
+#include "bf16_split.h"
 
 // ---- positions across lanes ------------------------------------------------
 // The same products with the lanes laid across positions instead of rows.
@@ -106,34 +107,57 @@ __device__ __forceinline__ float tile_sum(tile_buf &b, const float *smem, uint32
     return keep + __uint_as_float(dpp32<0x4E>(__float_as_uint(send)));
 }
 
-// A chunk's tables from one kind's three books (sbook: [stage][dim][code] in
-// LDS, visible to the workgroup) and x at this lane's position v (xv[8]):
-// 24 products of 32 codes x 32 positions on the matrix cores
-// (books[code][dim] x x[dim][position]), fp32 throughout.  Table A holds
-// stage 0 in slots 0-31 and stage 1 in slots 32-63, table B stage 2 twice;
-// a lane's slot is its position.  The caller synchronises after.
-__device__ __forceinline__ void table_mfma(float *smem, const float *sbook, const float *xv, int wv, int v, int h)
+// A chunk's tables from one kind's three books (sbook: [stage][dim][code]
+// fp32 in LDS, visible to the workgroup) and x at this lane's position
+// (x0, and x1, x2 when three: its 8 values as bf16 pieces), on the bf16
+// matrix cores.  A book value is an fp16 (11 significant bits), so
+// hi = its top 8 bits and lo = the rest (at most 3 bits) are exact bf16
+// values with hi + lo == value; x is one exact bf16 piece (bf16
+// activations) or three (fp32, bf16_split.h).  One
+// v_mfma_f32_32x32x16_bf16 takes K = 16 as (hi of dims 0-7 | lo of dims
+// 0-7) against (the x piece's dims 0-7, twice): every product is exact in
+// fp32 and only the fp32 sums round, as in an fp32 dot product.
+//
+// A product is 32 rows x 32 positions.  Its rows are chosen so that the two
+// half-waves of the output write the two slot halves of the same codes:
+// table A products take row m = (stage (m/4)%2, code c0 + 4(m/8) + m%4), so
+// output register r of lane (v, h) is stage h of code c0 + r at position v,
+// slot 32h + v; table B products take stage 2 in both halves (its two
+// copies).  Every LDS write of a wavefront then covers 64 consecutive
+// words, one per bank.  16 products of 16 codes for each table.  The caller
+// synchronises after.
+__device__ __forceinline__ void table_mfma(float *smem, const float *sbook, uint4 x0, uint4 x1, uint4 x2, bool three,
+                                           int wv, int lane)
 {
-    float xb[4];                                     // B operand: x[position v][dim 2i + h]
+    const int m = lane & 31, h = lane >> 5;
+    for (int tile = wv; tile < 32; tile += LW) {     // uniform per wavefront
+        const bool tb = tile >= 16;
+        const int c0 = (tile & 15) * 16;
+        const int st = tb ? 2 : (m >> 2) & 1, code = c0 + (m >> 3) * 4 + (m & 3);
+        uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) xb[i] = h ? xv[2 * i + 1] : xv[2 * i];
-    for (int tile = wv; tile < 24; tile += LW) {     // uniform per wavefront
-        const int st = tile >> 3, c0 = (tile & 7) * 32;
+        for (int i = 0; i < 4; i++) {
+            uint32_t q[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const float f = sbook[(st * 8 + 2 * i + j) * 256 + code];
+                const uint32_t hi = __float_as_uint(f) & 0xffff0000u;
+                q[j] = h ? __float_as_uint(__fsub_rn(f, __uint_as_float(hi))) >> 16 : hi >> 16;
+            }
+            w[i] = q[0] | (q[1] << 16);
+        }
+        const bf16x8 A = as_b8(make_uint4(w[0], w[1], w[2], w[3]));
         acc16 acc;
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float av = sbook[(st * 8 + 2 * i + h) * 256 + c0 + v];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, xb[i], acc, 0, 0, 0);
+        if (three) {                                 // uniform; the smallest pieces first
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, as_b8(x2), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, as_b8(x1), acc, 0, 0, 0);
         }
-        // acc[r]: code c0 + 8(r/4) + 4h + r%4, position v
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, as_b8(x0), acc, 0, 0, 0);
+        float *row = smem + (tb ? LUT_B : 0) + c0 * 64 + 32 * h + m;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int c = c0 + (r >> 2) * 8 + 4 * h + (r & 3);
-            if (st < 2) smem[c * 64 + 32 * st + v] = acc[r];
-            else { smem[LUT_B + c * 64 + v] = acc[r]; smem[LUT_B + c * 64 + 32 + v] = acc[r]; }
-        }
+        for (int r = 0; r < 16; r++) row[r * 64] = acc[r];
     }
 }
 
