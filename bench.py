@@ -452,29 +452,13 @@ def zipf_mle(counts_by_rank):
     return float(ss[int(np.argmax(ll))])
 
 
-def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_gb=64.0,
-                lookahead=6, depth=2, seed=0, zipf_s=1.1, reuse_keep=0.63, look_keep=0.88, scale=0.5):
-    """58 DeepSeek-V3-shaped MoE layers decoding `tokens` tokens at batch 1
-    through the HBM expert cache (64 GB of slots), the expert records in
-    pinned host memory, misses filled by hipMemcpyAsync on the cache's
-    stream, the lookahead's guesses (the next layer's router on this
-    layer's input, 6 ids) read after each layer's experts.
-
-    Routing (stack_inputs): each layer's experts drawn without replacement
-    from Zipf(zipf_s) popularity over a seeded permutation, consecutive
-    tokens sharing reuse_keep of the draw's noise (0.63: 0.6 of a token's
-    experts reused by the next), the next layer's router on this layer's
-    input sharing look_keep of it (0.88: about 81% of the top-6 guesses
-    land and 92% of the first, the precision the engine measured on a real
-    model, docs/LEARNED.md:1866-1868).  The e_score_correction_bias is
-    present and zero.
-
-    The host bank: one set of 256 records (4.2 GB pinned); layer L's expert
-    e is a byte copy of record e, so every layer object carries layer id 0
-    (the records' header) while the cache keys are (L, e): each miss still
-    moves its own 16.5 MB over PCIe into its own slot."""
+def stack_setup(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_gb=64.0, depth=2, seed=0,
+                zipf_s=1.1, reuse_keep=0.63, look_keep=0.88, scale=0.5):
+    """The stack bench_stack runs (see there): the host bank in pinned
+    memory, n_layers layer objects with their own routers and the shared
+    expert, the HBM expert cache over the bank, and the tokens.  Returns
+    (layers, routers, cache, host, X [T][L][H] bf16, ranks, rec_bytes)."""
     H, E, I, K = cfg["hidden"], cfg["n_experts"], cfg["moe_inter"], cfg["top_k"]
-    t0 = time.time()
     rb = synth.record_bytes(H, I)
     dev = torch.empty(E * rb, dtype=torch.uint8, device="cuda:0")
     synth.records(seed, 0, H, I, books, 0, E, dev.data_ptr())
@@ -500,10 +484,38 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
             m.set_shared(*sh)
         warp_amd.check(m.bind_table([], [], codebook_id=0), "bind_table")
         layers.append(m)
-    budget = int(budget_gb * 1e9)
-    cache = warp_amd.ExpertCache(rb, budget, policy=0, depth=depth)
+    cache = warp_amd.ExpertCache(rb, int(budget_gb * 1e9), policy=0, depth=depth)
     cache.set_source([host.data_ptr() + e * rb for _ in range(n_layers) for e in range(E)], n_layers, E)
     X, ranks = stack_inputs(torch, routers, tokens, zipf_s, reuse_keep, look_keep, scale, seed + 11)
+    return layers, routers, cache, host, X, ranks, rb
+
+
+def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_gb=64.0,
+                lookahead=6, depth=2, seed=0, zipf_s=1.1, reuse_keep=0.63, look_keep=0.88, scale=0.5):
+    """58 DeepSeek-V3-shaped MoE layers decoding `tokens` tokens at batch 1
+    through the HBM expert cache (64 GB of slots), the expert records in
+    pinned host memory, misses filled by hipMemcpyAsync on the cache's
+    stream, the lookahead's guesses (the next layer's router on this
+    layer's input, 6 ids) read after each layer's experts.
+
+    Routing (stack_inputs): each layer's experts drawn without replacement
+    from Zipf(zipf_s) popularity over a seeded permutation, consecutive
+    tokens sharing reuse_keep of the draw's noise (0.63: 0.6 of a token's
+    experts reused by the next), the next layer's router on this layer's
+    input sharing look_keep of it (0.88: about 81% of the top-6 guesses
+    land and 92% of the first, the precision the engine measured on a real
+    model, docs/LEARNED.md:1866-1868).  The e_score_correction_bias is
+    present and zero.
+
+    The host bank: one set of 256 records (4.2 GB pinned); layer L's expert
+    e is a byte copy of record e, so every layer object carries layer id 0
+    (the records' header) while the cache keys are (L, e): each miss still
+    moves its own 16.5 MB over PCIe into its own slot."""
+    H, E, I, K = cfg["hidden"], cfg["n_experts"], cfg["moe_inter"], cfg["top_k"]
+    t0 = time.time()
+    layers, routers, cache, host, X, ranks, rb = stack_setup(torch, warp_amd, synth, cfg, books, tokens, n_layers,
+                                                             budget_gb, depth, seed, zipf_s, reuse_keep, look_keep,
+                                                             scale)
     y = torch.empty((1, H), dtype=torch.float32, device="cuda:0")
     ids = torch.empty((tokens, n_layers, K), dtype=torch.int32, device="cuda:0")
     torch.cuda.synchronize()

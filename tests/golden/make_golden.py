@@ -25,7 +25,11 @@ vq4p.npz (VQ4P, 6-bit codes through the engine's int8 LUT):
   qlut, qq, qsc vq_quant_lut of a planted table (an all-zero block, exact
                 halves under a unit inverse, a lone extreme)
 
-  python tests/golden/make_golden.py [scalars|vq4p]
+q3g.npz (Q3G trunk rows, 3-bit codes plus a guard byte, tools/convert.py:854-892):
+  rows{o}_{cols}  mvq_rows of order o on the seeded rows of each width
+  digest_{cols}   sha256 of the case's packed rows, scales and x
+
+  python tests/golden/make_golden.py [scalars|vq4p|q3g]
 """
 import hashlib
 import os
@@ -35,6 +39,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 from records import FMT_F32, FMT_Q4G, FMT_Q8G, Layer  # noqa: E402
 from oracle_lib import Oracle, Ref  # noqa: E402
 
@@ -78,6 +83,9 @@ def main():
     if sys.argv[1:] == ["vq4p"]:                    # only vq4p.npz
         write_vq4p(orc, ref)
         return
+    if sys.argv[1:] == ["q3g"]:                     # only q3g.npz
+        write_q3g(ref)
+        return
     if ref.isa != 2:
         print("warning: this host does not run the reference's AVX-512 kernels; order 1 = portable")
     for name in CASES:
@@ -108,6 +116,41 @@ def main():
 
     write_scalars(ref)
     write_vq4p(orc, ref)
+    write_q3g(ref)
+
+
+Q3G_WIDTHS = (1024, 1000, 640)
+
+
+def q3g_inputs(cols, seed=31, rows=96):
+    """Seeded Q3G rows of one width (a partial last group when cols is not
+    a multiple of 128) and x ~ N(0,1)."""
+    from records import Tensor, quant_q3g
+    r = np.random.default_rng(seed + cols)
+    W = (r.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+    q, qs, rb = quant_q3g(W)
+    x = r.standard_normal(cols).astype(np.float32)
+    return Tensor(7, rows, cols, 128, q.view(np.int8), qs, rb), x
+
+
+def q3g_digest(t, x):
+    h = hashlib.sha256()
+    h.update(t.q.tobytes())
+    h.update(t.qs.tobytes())
+    h.update(x.tobytes())
+    return h.hexdigest()
+
+
+def write_q3g(ref):
+    out = {"isa": np.array(ref.isa)}
+    for cols in Q3G_WIDTHS:
+        t, x = q3g_inputs(cols)
+        out[f"digest_{cols}"] = np.array(q3g_digest(t, x))
+        for o in (0, 1):
+            ref.set_order(o)
+            out[f"rows{o}_{cols}"] = ref.mvq_rows(t, x)
+    np.savez_compressed(os.path.join(HERE, "q3g.npz"), **out)
+    print("q3g written")
 
 
 def vq4p_inputs(seed=21, M=192, nv=80):

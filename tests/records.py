@@ -118,12 +118,12 @@ class Layer:
         return r.standard_normal((T, self.H)).astype(np.float32)
 
 
-def quant_q3g(W, group=128):
+def quant_q3g(W, group=128, codes=False):
     """Q3G rows (tools/convert.py:854-892): codes round(w/scale) in [-4, 3]
     biased by +4, LSB-first at bit 3i of the row, each row padded to
     (n*3+7)/8 bytes plus one guard byte; scale = amax/3 per group, f16.
     Returns (packed uint8 [rows][rowbytes], f16 scale bits [rows][ng],
-    rowbytes)."""
+    rowbytes), and with codes=True also the signed codes [rows][n]."""
     rows, N = W.shape
     ng = (N + group - 1) // group
     n = ng * group
@@ -141,4 +141,5 @@ def quant_q3g(W, group=128):
         buf[:, byte[i]] += (u[:, i] << shift[i]) & 0xFF
         if shift[i] > 5:
             buf[:, byte[i] + 1] += (u[:, i] >> (8 - shift[i])) & 0xFF
-    return buf.astype(np.uint8), sc16.view(np.uint16).reshape(rows, ng), rowbytes
+    out = (buf.astype(np.uint8), sc16.view(np.uint16).reshape(rows, ng), rowbytes)
+    return out + (u - 4,) if codes else out

@@ -9,6 +9,7 @@ waste_model_open and record_check (src/model.c:2640-2741, 2957-3100,
 field of a container that otherwise opens.
 """
 import copy
+import ctypes
 import json
 import os
 import struct
@@ -429,3 +430,94 @@ def test_oracle_from_container(tmp_path, group_limit):
             assert np.array_equal(ia, ib) and np.array_equal(wa.view(np.uint32), wb.view(np.uint32))
             assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
             assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32))
+
+
+# ---- a container the reference's own tool wrote -------------------------
+
+def ref_container(tmp_path):
+    """tests/golden/ref_container.npz (tests/golden/make_ref_container.py:
+    the reference's tools/make_test_container.py, seed 0) unpacked into a
+    directory."""
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ref_container.npz"))
+    d = tmp_path / "ref"
+    d.mkdir()
+    for name in g.files:
+        (d / name).write_bytes(g[name].tobytes())
+    return str(d), {name: g[name].tobytes() for name in g.files}
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return Oracle()
+
+
+def test_reference_written_container(tmp_path, orc):
+    """The reader on a container written by the reference's tooling: the
+    config against the manifest's JSON, every record crc-checked and equal
+    to its slice of the bank file, the codebooks against the file's
+    per-book layout (a 16-byte waste_codebook_hdr, then 256 x 8 f16,
+    src/waste_format.h:139-150), the MoE trunk tensors against their
+    manifest offsets, and the oracle's layer on what the reader returned."""
+    path, raw = ref_container(tmp_path)
+    man = json.loads(raw["manifest.json"])
+    jc = man["config"]
+    c = warp_amd.Container(path, verify=True)
+    cfg = c.config()
+    assert (cfg["n_layers"], cfg["hidden"], cfg["n_experts"], cfg["top_k"], cfg["moe_inter"]) == (
+        jc["num_hidden_layers"], jc["hidden_size"], jc["num_experts"], jc["num_experts_per_token"],
+        jc["moe_intermediate_size"])
+    assert (cfg["n_shared"], cfg["first_dense"], cfg["score_func"], cfg["renorm"]) == (
+        jc["num_shared_experts"], jc["first_k_dense_replace"], 0, 1)
+    assert cfg["routed_scale"] == np.float32(jc["routed_scaling_factor"])
+    eq = man["expert_quant"]
+    assert (cfg["stages"], cfg["vec_dim"], cfg["entries"], cfg["index_block"]) == (
+        eq["stages"], eq["vec_dim"], eq["entries"], eq["index_block"])
+    # codebooks: book i at i * (16 + 256*8*2) + 16
+    books = c.codebooks()
+    cbf = raw["codebooks.bin"]
+    per = 16 + 256 * 8 * 2
+    assert books.shape[0] * per == len(cbf)
+    for i in range(books.shape[0]):
+        want = np.frombuffer(cbf[i * per + 16:(i + 1) * per], np.uint16).reshape(256, 8)
+        assert np.array_equal(books[i], want), i
+    # banks and records
+    trunk = raw["trunk.bin"]
+    tmap = {t["name"]: t for t in man["trunk"]}
+    for ls, lay in man["layers"].items():
+        L = int(ls)
+        n, cb, rb = c.bank(L)
+        assert (n, cb, rb * n) == (lay["experts"], lay["codebook_base"], lay["bytes"])
+        bank = raw[lay["file"]]
+        for e in range(n):
+            rc, rec = c.read_expert(L, e)
+            assert rc == 0 and rec.tobytes() == bank[e * rb:(e + 1) * rb], (L, e)
+            buf = np.ascontiguousarray(rec, np.uint8)
+            assert orc.lib.orc_record_check(buf.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)), rb, L, e,
+                                            cfg["moe_inter"], cfg["hidden"], 3, books.shape[0], 1) == 0, (L, e)
+        dst = np.zeros((n, rb), np.uint8)
+        assert c.read_bank(L, dst) == 0 and dst.tobytes() == bank
+        p = f"model.layers.{L}.block_sparse_moe."
+        for name in ("gate.weight", "gate.e_score_correction_bias", "shared_experts.gate_proj.weight",
+                     "shared_experts.up_proj.weight", "shared_experts.down_proj.weight"):
+            ent = tmap[p + name]
+            t = c.tensor(p + name)
+            assert t.fmt == ent["fmt"], name
+            if ent["fmt"] == 0:
+                want = np.frombuffer(trunk[ent["off"]:ent["off"] + ent["bytes"]], np.float32)
+                assert np.array_equal(np.asarray(t.q).reshape(-1), want), name
+            else:
+                rows, cols = ent["shape"]
+                q = np.asarray(t.q).view(np.uint8)
+                assert q.size == rows * t.rowbytes, name
+                assert q.tobytes() == trunk[ent["off"]:ent["off"] + rows * t.rowbytes], name
+                ng = (cols + ent["group"] - 1) // ent["group"]
+                so = ent["scale_off"]
+                assert np.array_equal(np.asarray(t.qs).reshape(-1),
+                                      np.frombuffer(trunk[so:so + rows * ng * 2], np.uint16)), name
+        # the oracle's moe_layer on the reader's view of the layer
+        view = oracle_view(c, L, group_limit=False)
+        x = np.random.default_rng(L).standard_normal(cfg["hidden"]).astype(np.float32)
+        rc, out, idx, w, _ = orc.moe(view, 1).layer(x)
+        assert rc == 0 and np.all(np.isfinite(out)) and len(set(idx.tolist())) == cfg["top_k"], L
+    assert c.error() == (0, 0, 0)
+    c.close()

@@ -144,3 +144,38 @@ def test_container_layer_through_cache(orc, ctr):
         m.close()
     cache.close()
     c.close()
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_reference_written_container_layers(orc, tmp_path, T):
+    """The three MoE layers of the container the reference's own tool
+    wrote (tests/golden/ref_container.npz, hidden 128, 8 experts, top-2,
+    sigmoid with a bias, a Q4G router and shared expert) as device layers
+    through the reader: ids and weights bit-exact on the device logits,
+    outputs within 1e-3 of the oracle built from the reader's view."""
+    from test_container import ref_container
+    say("test_reference_written_container_layers", T)
+    path, _ = ref_container(tmp_path)
+    c = warp_amd.Container(path, verify=True)
+    for layer in (1, 2, 3):
+        ref = oracle_view(c, layer, False)
+        X = np.random.default_rng(700 + layer + T).standard_normal((T, ref.H)).astype(np.float32)
+        X = torch.from_numpy(X).to(torch.bfloat16).to(torch.float32).numpy()
+        m = c.moe(layer, max_tokens=T)
+        st, y, ids, w, lg = run_forward(torch, m, ref, X, bf16=True)
+        assert st == 0
+        ol = orc.moe(ref, 1)
+        assert rel_err(lg, ol.logits(X)) <= LOGIT_RTOL
+        for t in range(T):
+            rc, oi, ow, _ = orc.route(lg[t], ref.bias, ref.E, ref.K, ref.score_func, ref.renorm,
+                                      ref.routed_scale, ref.n_group, ref.topk_group)
+            assert rc == ref.K
+            assert np.array_equal(oi, ids[t]) and np.array_equal(bits(ow), bits(w[t])), (layer, t)
+        rc, yref = ol.apply(X, ids, w, chunk=0 if T == 1 else 1)
+        assert rc == 0
+        e = rel_err(y, yref)
+        say(f"  layer {layer} T={T}: rel err {e:.3e}")
+        assert e <= LAYER_RTOL
+        m.close()
+    assert c.error()[0] == 0
+    c.close()

@@ -9,7 +9,8 @@ Pins, per oracle function (oracle/oracle.c):
   orc_lutb          golden (both orders) + fp64 closed form
   orc_vq_rows       golden + fp64 materialised-W bound
   orc_dequant       closed form recomputed in numpy from the raw indices
-  orc_mvq_rows      golden (both orders) + fp64 dequantised matvec bound
+  orc_mvq_rows      golden (both orders) + fp64 dequantised matvec bound,
+                    Q8G/Q4G (layer goldens) and Q3G (q3g.npz, three widths)
   orc_router_scores golden + numpy formula in fp64
   orc_route         golden ids/weights + brute force tie rule, permutation
                     at K=E, renorm sum, group-limited brute force and its
@@ -26,9 +27,9 @@ import zlib
 import numpy as np
 import pytest
 
-from golden.make_golden import CASES, case_layer, input_digest
+from golden.make_golden import CASES, Q3G_WIDTHS, case_layer, input_digest, q3g_digest, q3g_inputs
 from oracle_lib import Oracle
-from records import FMT_F32, Layer, unblock_indices
+from records import FMT_F32, Layer, Tensor, quant_q3g, unblock_indices
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -172,6 +173,44 @@ def test_dequant_and_apply_closed_form(orc):
         exact = W.astype(np.float64) @ x.astype(np.float64)
         bound = 1e-5 * np.abs(W).astype(np.float64) @ np.abs(x).astype(np.float64)
         assert np.all(np.abs(y - exact) <= bound)
+
+
+def test_q3g_golden(orc):
+    """orc_mvq_rows' Q3G branch (3-bit codes at bit 3i, minus 4,
+    src/simd.h:101-106) bit for bit against the reference compiled from its
+    sources, both fold orders, at three widths (one with a partial last
+    group); the inputs are regenerated and checked against the fixture's
+    digests first."""
+    g = np.load(os.path.join(GOLD, "q3g.npz"))
+    for cols in Q3G_WIDTHS:
+        t, x = q3g_inputs(cols)
+        assert q3g_digest(t, x) == str(g[f"digest_{cols}"]), cols
+        for o in (0, 1):
+            if o == 1 and int(g["isa"]) != 2:
+                continue
+            assert eq_bits(orc.mvq_rows(t, x, o), g[f"rows{o}_{cols}"]), (cols, o)
+
+
+def test_q3g_closed_form(orc):
+    """Q3G rows against the quantiser's own signed codes times the f16
+    group scales, in fp64: pins the unpacking (bit offsets across byte
+    boundaries, the -4 bias) and the scale per 128-column group."""
+    rng = np.random.default_rng(41)
+    for cols in (1024, 1000):
+        W = (rng.standard_normal((64, cols)) * 0.02).astype(np.float32)
+        q, qs, rb, codes = quant_q3g(W, codes=True)
+        t = Tensor(7, 64, cols, 128, q.view(np.int8), qs, rb)
+        x = rng.standard_normal(cols).astype(np.float32)
+        ng = qs.shape[1]
+        sc = qs.view(np.float16).astype(np.float64).reshape(64, ng, 1)
+        Wd = (codes.reshape(64, ng, 128).astype(np.float64) * sc).reshape(64, ng * 128)[:, :cols]
+        exact = Wd @ x.astype(np.float64)
+        for o in (0, 1):
+            y = orc.mvq_rows(t, x, o)
+            assert np.all(np.abs(y - exact) <= 1e-5 * (np.abs(Wd) @ np.abs(x))), (cols, o)
+        # a planted wrong bias (codes read as unsigned) is caught
+        bad = ((codes + 4).reshape(64, ng, 128).astype(np.float64) * sc).reshape(64, ng * 128)[:, :cols] @ x
+        assert not np.all(np.abs(orc.mvq_rows(t, x, 1) - bad) <= 1e-5 * (np.abs(Wd) @ np.abs(x)))
 
 
 def test_mvq_closed_form(orc):

@@ -164,13 +164,25 @@ def test_device_quant_and_rows_bit_exact(orc, gold):
 @pytest.mark.gpu
 def test_slot_rows_bit_exact(orc, gold):
     """waste_register_hip's vq_rows_p6 slot (waste_kernels offset 40,
-    src/waste_backend.h:85) on host buffers, over the ranges the engine's
-    pool hands it, against the CPU kernel of this host's fold order."""
+    src/waste_backend.h:85), installed only with WASTE_HIP_P6=1, on host
+    buffers, over the ranges the engine's pool hands it, against the CPU
+    kernel of this host's fold order."""
     torch, lib = _gpu()
     _, _, _, idx, scale, _, M, nv = vq4p_inputs()
-    tab = (C.c_uint8 * 80)()
     lib.waste_register_hip.restype = C.c_char_p
+    sentinel = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_void_p)(lambda b, e, p: None)
+    tab = (C.c_uint8 * 80)()
+    C.cast(C.addressof(tab) + 40, C.POINTER(C.c_void_p))[0] = C.cast(sentinel, C.c_void_p).value
+    os.environ.pop("WASTE_HIP_P6", None)
     assert lib.waste_register_hip(C.cast(tab, C.c_void_p))
+    # not asked for: the CPU kernel the table held stays in the slot
+    assert C.cast(C.addressof(tab) + 40, C.POINTER(C.c_void_p)).contents.value == C.cast(sentinel, C.c_void_p).value
+    tab = (C.c_uint8 * 80)()
+    os.environ["WASTE_HIP_P6"] = "1"
+    try:
+        assert lib.waste_register_hip(C.cast(tab, C.c_void_p))
+    finally:
+        os.environ.pop("WASTE_HIP_P6", None)
     fnp = C.cast(C.addressof(tab) + 40, C.POINTER(C.c_void_p)).contents.value
     assert fnp
     slot = C.CFUNCTYPE(None, C.c_int, C.c_int, C.c_void_p)(fnp)

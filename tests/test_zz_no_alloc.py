@@ -95,3 +95,59 @@ def test_forward_static_matches_forward():
     finally:
         ds.close()
         ki.close()
+
+
+def test_forward_static_under_graph_capture():
+    """The claim itself: forward_static runs where allocation is refused.
+    A one-token call is captured into a HIP graph (torch's capture: a
+    hipMalloc or a stream synchronisation inside it fails the capture) and
+    the graph is replayed three times, with new tokens copied into its input
+    and eager forward() calls and synchronisations between the replays;
+    every replay is bit-identical to forward() on the same token.  Repeated
+    eager static calls leave the device's free memory unchanged."""
+    say("test_forward_static_under_graph_capture")
+    lib = warp_amd.lib()
+    ds = FullLayer("dsv3", 8)
+    dev = torch.device("cuda:0")
+    try:
+        x = ds.tokens(1, seed=200).to(dev)
+        y = torch.full((1, ds.H), float("nan"), device=dev)
+        ids = torch.empty((1, ds.K), dtype=torch.int32, device=dev)
+        w = torch.empty((1, ds.K), dtype=torch.float32, device=dev)
+        lg = torch.empty((1, ds.E), dtype=torch.float32, device=dev)
+
+        def static_call():
+            rc = lib.waste_hip_moe_forward_static(ds.m.h, x.data_ptr(), int(ds.cfg["bf16"]), 1, y.data_ptr(),
+                                                  ids.data_ptr(), w.data_ptr(), lg.data_ptr(),
+                                                  torch.cuda.current_stream().cuda_stream)
+            assert rc == 0, rc
+
+        static_call()                                # warm: the static area's address is looked up
+        torch.cuda.synchronize()
+        free0 = torch.cuda.mem_get_info()[0]
+        for _ in range(5):
+            static_call()
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free0
+        say("  five static calls: device free memory unchanged")
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s, capture_error_mode="thread_local"):
+                static_call()
+        torch.cuda.synchronize()
+        for i in range(3):
+            tok = ds.tokens(1, seed=300 + i)
+            x.copy_(tok.to(dev))
+            y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = (y.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy(), lg.cpu().numpy())
+            assert ds.m.status(torch.cuda.current_stream().cuda_stream) == 0
+            same(got, run(ds, tok, static=False))    # eager forward() between the replays
+            say(f"  replay {i}: bit-identical to forward()")
+        del g
+    finally:
+        ds.close()

@@ -298,7 +298,9 @@ int whip_route_gemv(const whip_route_cfg *c, const float *logits, const float *b
 /* ---- the static scratch area (scratch.hip) ---- */
 
 /* Bytes of the area, and of its head: state that must start at zero (the
- * routing exchange, 1 + 1024 tagged words, and a block counter). */
+ * routing exchange, 1 + 1024 tagged words, and a block counter).  The area
+ * is zero when the code object loads, and every launch leaves the head as
+ * valid for the next (the counter back at zero, the tags only growing). */
 #define WHIP_SCRATCH_BYTES (16u << 20)
 #define WHIP_SCRATCH_HEAD  8704u
 #define WHIP_SCRATCH_XCHG  0u                /* 1 + E 64-bit words, E <= 1024 */
@@ -306,9 +308,6 @@ int whip_route_gemv(const whip_route_cfg *c, const float *logits, const float *b
 /* The current device's address of the area (hipGetSymbolAddress, once per
  * device). */
 int whip_scratch(void **ptr);
-/* Zeroes the head of the area ptr (the current device's), the first time
- * it is called on that device, with a fill kernel on s. */
-int whip_scratch_clear_once(void *ptr, hipStream_t s);
 /* Zeroes `bytes` (a multiple of 4) at p with a fill kernel on s. */
 int whip_zero(void *p, size_t bytes, hipStream_t s);
 

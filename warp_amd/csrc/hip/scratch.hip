@@ -12,8 +12,11 @@
 // The area keeps what the last call left in it.  Its first
 // WHIP_SCRATCH_HEAD bytes hold state that must start at zero (the routing
 // exchange's tag word and tagged logits, the routing launch's block
-// counter); whip_scratch_clear_once zeroes them, once per device, with a
-// fill kernel on the caller's stream.
+// counter).  A device variable without an initializer is zero-filled when
+// the code object loads, and every launch leaves that state as valid for
+// the next (the counter back at zero, the tags only growing), so no call
+// clears it: a first call captured into a graph, or made on any stream,
+// needs nothing done before it.
 #include <hip/hip_runtime.h>
 #include <mutex>
 
@@ -24,7 +27,6 @@ static __device__ __align__(256) unsigned char scratch[WHIP_SCRATCH_BYTES];
 #define SCRATCH_DEVS 64
 static std::mutex g_mu;
 static void *g_ptr[SCRATCH_DEVS];
-static bool g_clear[SCRATCH_DEVS];
 
 extern "C" int whip_scratch(void **ptr)
 {
@@ -58,18 +60,4 @@ extern "C" int whip_zero(void *p, size_t bytes, hipStream_t s)
     const unsigned blocks = (unsigned)((n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024);
     hipLaunchKernelGGL(k_zero_words, dim3(blocks), dim3(256), 0, s, (uint32_t *)p, n);
     return (int)hipGetLastError();
-}
-
-extern "C" int whip_scratch_clear_once(void *ptr, hipStream_t s)
-{
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return (int)e;
-    if (dev < 0 || dev >= SCRATCH_DEVS) return (int)hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (ptr != g_ptr[dev]) return (int)hipErrorInvalidValue;
-    if (g_clear[dev]) return 0;
-    const int rc = whip_zero(ptr, WHIP_SCRATCH_HEAD, s);
-    if (rc == 0) g_clear[dev] = true;
-    return rc;
 }

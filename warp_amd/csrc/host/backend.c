@@ -173,14 +173,22 @@ static void mvq_rows_hip(int b, int e, void *p)
 }
 
 /* The fold order of the CPU VQ4P kernel the engine installs on this host:
- * its AVX-512 VBMI kernel (x86 hosts with VBMI) and its NEON kernel are
- * built where the compiler contracts the fold into a fused multiply-add;
- * the portable C kernel is built without FMA. */
+ * its AVX-512 VBMI kernel and its NEON kernel are built where the compiler
+ * contracts the fold into a fused multiply-add; the portable C kernel is
+ * built without FMA.  The engine installs the VBMI kernel only with its
+ * AVX-512 backend, which needs AVX512F and AVX512BW with the OS saving the
+ * zmm state (src/backend.c:191, the XCR0 test of waste_cpu_features), and
+ * then only with VBMI as well (src/simd_avx512.c:239-242); GCC's
+ * __builtin_cpu_supports reports the AVX-512 features only when XCR0 shows
+ * that state saved. */
 int waste_hip_vq_p6_order(void)
 {
 #if defined(__x86_64__)
     __builtin_cpu_init();
-    return __builtin_cpu_supports("avx512vbmi") ? WASTE_HIP_ORDER_FMA : WASTE_HIP_ORDER_PORTABLE;
+    return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+                   __builtin_cpu_supports("avx512vbmi")
+               ? WASTE_HIP_ORDER_FMA
+               : WASTE_HIP_ORDER_PORTABLE;
 #elif defined(__aarch64__)
     return WASTE_HIP_ORDER_FMA;
 #else
@@ -266,8 +274,21 @@ const char *waste_register_hip(waste_kernels *t)
     if (t->mvq_rows_f32 != mvq_rows_hip)
         g_cpu_rows = t->mvq_rows_cpu ? t->mvq_rows_cpu : t->mvq_rows_f32;
     t->mvq_rows_f32 = mvq_rows_hip;
-    if (t->vq_rows_p6 != vq_rows_p6_hip) g_cpu_p6 = t->vq_rows_p6;
-    t->vq_rows_p6 = vq_rows_p6_hip;
+    /* The VQ4P slot only when asked for (WASTE_HIP_P6=1): the engine calls
+     * it once per pool range (pf_wide, src/model.c:4157-4159), and each call
+     * is a synchronous round trip over PCIe.  Measured on an MI355X host
+     * against the engine's own VBMI kernel on one thread: a Kimi-Linear
+     * gate/up matrix (1024 x 288 positions) in one call 86-106 us against
+     * 44 us, in the pool's 1024-row ranges 196 us (down, 2304 x 128) against
+     * 44 us; a DeepSeek-V3 matrix breaks even only when handed whole.  The
+     * device-resident layer is where VQ4P belongs on the GPU. */
+    const char *p6 = getenv("WASTE_HIP_P6");
+    if (p6 && *p6 == '1') {
+        if (t->vq_rows_p6 != vq_rows_p6_hip) g_cpu_p6 = t->vq_rows_p6;
+        t->vq_rows_p6 = vq_rows_p6_hip;
+    } else if (t->vq_rows_p6 == vq_rows_p6_hip) {
+        t->vq_rows_p6 = g_cpu_p6;                    /* a registration before this one installed it */
+    }
     t->on_device = 1;
     /* A synchronous dispatch with two PCIe copies costs tens of us; below
      * a megabyte of weights the CPU pool finishes first. */

@@ -899,7 +899,7 @@ int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, in
         return WASTE_HIP_ESCRATCH;
     hipStream_t s = (hipStream_t)stream;
     void *base = NULL;
-    if (whip_scratch(&base) || whip_scratch_clear_once(base, s)) return WASTE_HIP_EDEVICE;
+    if (whip_scratch(&base)) return WASTE_HIP_EDEVICE;
     fwd_bufs sb;
     static_layout(m, T, (uint8_t *)base, &sb);
     /* the staged kernels on the static buffers; the layer's own come back
