@@ -490,13 +490,27 @@ def stack_setup(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
     return layers, routers, cache, host, X, ranks, rb
 
 
+def group_top(sc, n, n_group, topk_group):
+    """The n best of scores sc [E] within the topk_group groups of the
+    largest top-2 sums (the routing's group limit), best first."""
+    g = sc.reshape(n_group, -1)
+    keep = np.argsort(-np.sort(g, 1)[:, -2:].sum(1), kind="stable")[:topk_group]
+    m = np.full(sc.shape, -np.inf)
+    for k in keep:
+        m[k * g.shape[1]:(k + 1) * g.shape[1]] = g[k]
+    return np.argsort(-m, kind="stable")[:n]
+
+
 def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_gb=64.0,
-                lookahead=6, depth=2, seed=0, zipf_s=1.1, reuse_keep=0.63, look_keep=0.88, scale=0.5):
+                lookahead=6, depth=2, seed=0, zipf_s=1.1, reuse_keep=0.63, look_keep=0.88, scale=0.5,
+                grouped=False):
     """58 DeepSeek-V3-shaped MoE layers decoding `tokens` tokens at batch 1
     through the HBM expert cache (64 GB of slots), the expert records in
     pinned host memory, misses filled by hipMemcpyAsync on the cache's
     stream, the lookahead's guesses (the next layer's router on this
-    layer's input, 6 ids) read after each layer's experts.
+    layer's input, 6 ids) read after each layer's experts.  grouped: the
+    guesses within the next layer's own group limit (8 groups, 4 kept)
+    rather than the engine's rule (the top 6 over all experts).
 
     Routing (stack_inputs): each layer's experts drawn without replacement
     from Zipf(zipf_s) popularity over a seeded permutation, consecutive
@@ -516,6 +530,8 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
     layers, routers, cache, host, X, ranks, rb = stack_setup(torch, warp_amd, synth, cfg, books, tokens, n_layers,
                                                              budget_gb, depth, seed, zipf_s, reuse_keep, look_keep,
                                                              scale)
+    for m in layers:
+        m.set_lookahead_groups(grouped)
     y = torch.empty((1, H), dtype=torch.float32, device="cuda:0")
     ids = torch.empty((tokens, n_layers, K), dtype=torch.int32, device="cuda:0")
     torch.cuda.synchronize()
@@ -559,14 +575,15 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
             new = [e for e in ih[t, L] if t == 0 or e not in ih[t - 1, L]]
             np.add.at(fresh_by_rank, ranks[L][np.array(new, np.int64)], 1)
     # the lookahead's guesses: the next layer's router on this layer's
-    # input, its top 6 by score (the bias is zero), against what the next
-    # layer then selected
+    # input, its top 6 by score (the bias is zero; grouped: within the
+    # group limit), against what the next layer then selected
     hits6 = hits1 = n_guess = 0
     for L in range(n_layers - 1):
         Wn = torch.from_numpy(routers[L + 1]).to("cuda:0")
         sc = torch.sigmoid(X[:, L].float() @ Wn.T).cpu().numpy()
         for t in range(tokens):
-            g = np.argsort(-sc[t], kind="stable")[:lookahead]
+            g = (group_top(sc[t], lookahead, cfg["n_group"], cfg["topk_group"]) if grouped
+                 else np.argsort(-sc[t], kind="stable")[:lookahead])
             nxt_sel = set(ih[t, L + 1].tolist())
             hits6 += len(nxt_sel & set(g.tolist()))
             hits1 += int(g[0] in nxt_sel)
@@ -576,9 +593,15 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
                     f"HBM expert cache", "layers": n_layers, "tokens": tokens,
         "budget_gb": budget_gb, "slots": cache.n_slots, "records": n_layers * E, "rec_bytes": rb,
         "policy": "lfru", "readahead_depth": depth, "lookahead": lookahead,
+        "lookahead_rule": "within the group limit" if grouped else "top n over all experts (predict_next_moe)",
         "hit_rate": round(hit, 4), "hits": st["hits"], "misses": st["misses"],
         "evictions": st["evictions"], "hint_reads": st["prefetched"],
-        "lookahead_reads": st["spec_issued"], "gb_read": round(st["bytes_read"] / 1e9, 2),
+        "lookahead_reads": st["spec_issued"],
+        # what became of them: demanded while resident, evicted unread, or
+        # still resident and unread when the run ended
+        "lookahead_reads_used": st["spec_used"], "lookahead_reads_wasted": st["spec_wasted"],
+        "lookahead_reads_unresolved": st["spec_issued"] - st["spec_used"] - st["spec_wasted"],
+        "gb_read": round(st["bytes_read"] / 1e9, 2), "gb_read_per_token": round(st["bytes_read"] / 1e9 / tokens, 3),
         "tok_s": round(tokens / wall, 3), "ms_per_token": round(wall * 1e3 / tokens, 2),
         "tok_s_second_half": round(steady, 3) if steady else None,
         "host_to_device_gbps": round(st["bytes_read"] / wall / 1e9, 2),
@@ -631,6 +654,8 @@ def main():
     ap.add_argument("--stack-tokens", type=int, default=200,
                     help="tokens the 58-layer stack decodes through the HBM expert cache (0: skip)")
     ap.add_argument("--stack-budget-gb", type=float, default=64.0)
+    ap.add_argument("--no-stack-grouped", dest="stack_grouped", action="store_false",
+                    help="skip the second stack run, whose lookahead guesses lie within the group limit")
     ap.add_argument("--no-extra-configs", dest="extra_configs", action="store_false",
                     help="skip the other decode configurations (olmoe B=1, kimi B=1/4/16, dsv3 B=8/32)")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MB",
@@ -713,6 +738,19 @@ def main():
         stack = bench_stack(torch, warp_amd, synth, cfg, books, a.stack_tokens,
                             budget_gb=a.stack_budget_gb)
         log(f"[bench] stack {stack['tok_s']} tok/s, hit rate {stack['hit_rate']}")
+        # the same stack and tokens with the lookahead's guesses inside the
+        # next layer's group limit: a guess in a group the routing drops is
+        # never selected, so its read is wasted
+        if a.stack_grouped:
+            v = bench_stack(torch, warp_amd, synth, cfg, books, a.stack_tokens, budget_gb=a.stack_budget_gb,
+                            grouped=True)
+            stack["lookahead_grouped"] = {k: v[k] for k in (
+                "lookahead", "lookahead_rule", "hit_rate", "misses", "lookahead_reads", "lookahead_reads_used",
+                "lookahead_reads_wasted", "gb_read", "gb_read_per_token", "tok_s", "ms_per_token",
+                "tok_s_second_half", "host_to_device_gbps")}
+            stack["lookahead_grouped"]["lookahead_precision_top6"] = v["routing"]["lookahead_precision_top6"]
+            log(f"[bench] stack, grouped lookahead: {v['tok_s']} tok/s, hit rate {v['hit_rate']}, "
+                f"{v['gb_read_per_token']} GB/token")
 
     cpu = None
     if not a.no_cpu and B == 1:

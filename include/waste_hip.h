@@ -246,6 +246,16 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts,
 int waste_hip_moe_predict(waste_hip_moe *m, const void *x, int x_bf16, int n,
                           int32_t *ids, void *stream);
 
+/* on = 1: this layer's predict (and so the lookahead forward_cached makes
+ * with it as `next`) applies the layer's own group limit, as its routing
+ * does: the n best of score + bias within the topk_group groups it keeps
+ * (n capped at those groups' experts; ids past the cap untouched).  0 (the
+ * default): predict_next_moe's rule above.  No counterpart in the
+ * reference: predict_next_moe ignores the group limit, so on a model with
+ * n_group > 1 some of its guesses lie in groups the routing then drops,
+ * and those reads are wasted.  No effect when n_group <= 1. */
+int waste_hip_moe_set_lookahead_groups(waste_hip_moe *m, int on);
+
 /* Forward declaration; the cache is section 4. */
 typedef struct waste_hip_ecache waste_hip_ecache;
 
@@ -317,6 +327,9 @@ typedef struct {
     uint64_t prefetched;     /* misses the hint's read-ahead issued        */
     uint64_t spec_issued;    /* lookahead reads (not misses)               */
     uint64_t reads, bytes_read;
+    /* what became of the lookahead reads (counters only: no decision reads
+     * them): demanded while still resident, or evicted first */
+    uint64_t spec_used, spec_wasted;
 } waste_hip_ecache_counts;
 
 /* policy 0 LFRU, 1 LRU; depth 0 = no read-ahead (the engine's synchronous

@@ -88,3 +88,17 @@ def test_full_overlap_is_full_reuse():
     s1 = select(orc, Xf[:, 1] @ W[1].T)
     look = select(orc, Xf[:, 0] @ W[1].T)
     assert np.mean([len(a & b) for a, b in zip(s1, look)]) > 7.5
+
+
+def test_group_top_is_the_group_limited_route():
+    """bench.group_top: the oracle's group-limited route (8 groups, 4 kept,
+    no bias) on the same sigmoid scores, in its order."""
+    orc = Oracle()
+    rng = np.random.default_rng(5)
+    for _ in range(50):
+        lg = rng.standard_normal(256).astype(np.float32)
+        sc = orc.router_scores(0, lg)
+        for n in (1, 6, 8, 64):
+            rc, want, _, _ = orc.route(lg, None, 256, n, 0, 0, 1.0, 8, 4)
+            assert rc == n
+            assert list(bench.group_top(sc.astype(np.float64), n, 8, 4)) == list(want)

@@ -319,3 +319,23 @@ def test_warm_refusals(tmp_path):
     assert c.save_usage(str(tmp_path / "no_dir" / "u.waste"), 0) == warp_amd.EIO
     z = product(0, 0, 0)
     assert z.warm(bad) == 0                         # no slots: nothing to do
+
+
+def test_lookahead_use_and_waste_counted():
+    """What became of the lookahead reads: demanded while resident (used)
+    or evicted first (wasted); counters only, the decisions unchanged (a
+    dry cache of 4 slots)."""
+    import warp_amd
+    rb = 4096
+    c = warp_amd.ExpertCache(rb, 4 * rb, policy=0, depth=2, dry=True)
+    c.prefetch(1, [4, 5])                      # two lookahead reads
+    assert c.get(1, 4)                         # one demanded: used
+    st = c.stats()
+    assert (st["spec_issued"], st["spec_used"], st["spec_wasted"]) == (2, 1, 0)
+    assert c.get(1, 4)                         # a second demand counts once
+    for e in (10, 11, 12, 13, 14, 15):         # misses push every older record out
+        assert c.get(2, e)
+    st = c.stats()
+    assert (st["spec_used"], st["spec_wasted"]) == (1, 1)   # expert 5 left unread
+    assert st["spec_issued"] == 2 and st["hits"] == 2 and st["misses"] == 6
+    c.close()

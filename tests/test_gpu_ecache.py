@@ -160,6 +160,42 @@ def test_predict_matches_oracle(orc, name, n):
     m.close()
 
 
+@pytest.mark.parametrize("name,n", [("dsv3_small", 6), ("dsv3_small", 64), ("olmoe_small", 5)])
+def test_predict_grouped_matches_oracle(orc, name, n):
+    """With the lookahead in the layer's own group limit: the oracle's
+    group-limited route of n (no renorm, scale 1) on the device logits, in
+    its order; n capped at the kept groups' experts (dsv3_small: 4 of 8
+    groups of 8, so 32), ids past the cap untouched.  A layer without
+    groups keeps predict_next_moe's rule."""
+    say("test_predict_grouped_matches_oracle", name, n)
+    L, X, bf16 = make_case(name, 4)
+    m = gpu_layer(L)
+    m.set_lookahead_groups(True)
+    dev = torch.device("cuda:0")
+    for t in range(X.shape[0]):
+        xd = torch.from_numpy(X[t:t + 1]).to(dev)
+        if bf16:
+            xd = xd.to(torch.bfloat16)
+        lg = torch.empty((1, L.E), device=dev)
+        y = torch.empty((1, L.H), device=dev)
+        m.forward(xd.data_ptr(), 1, y.data_ptr(), None, None, lg.data_ptr(), bf16=bf16, stream=stream())
+        ids = torch.full((64,), -5, dtype=torch.int32, device=dev)
+        m.predict(xd.data_ptr(), n, ids.data_ptr(), bf16=bf16, stream=stream())
+        assert m.status(stream()) == 0
+        got = ids.cpu().numpy()
+        logits = lg.cpu().numpy()[0]
+        if L.n_group > 1:
+            k = min(n, L.topk_group * (L.E // L.n_group))
+            rc, want, _, _ = orc.route(logits, L.bias, L.E, k, L.score_func, 0, 1.0, L.n_group, L.topk_group)
+            assert rc == k
+        else:
+            k = min(n, L.E)
+            want = orc.predict_next(L.score_func, logits, L.bias, n)
+        assert np.array_equal(got[:k], want), (t, got[:k], want)
+        assert np.all(got[k:] == -5)
+    m.close()
+
+
 @pytest.mark.parametrize("n_slots,depth,look,own", [(20, 2, 6, False), (72, 2, 6, True),
                                                    (200, 2, 0, False), (24, 4, 16, True)])
 def test_cache_fed_layers(orc, n_slots, depth, look, own):

@@ -40,7 +40,7 @@ EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_hos
            "waste_hip_moe_profile", "waste_hip_moe_profile_read", "waste_hip_record_bytes",
            "waste_hip_synth_codebooks", "waste_hip_synth_records",
            "waste_hip_moe_route", "waste_hip_moe_experts", "waste_hip_moe_bind_table",
-           "waste_hip_moe_predict", "waste_hip_moe_forward_cached",
+           "waste_hip_moe_predict", "waste_hip_moe_set_lookahead_groups", "waste_hip_moe_forward_cached",
            "waste_hip_moe_forward_static", "waste_hip_moe_static_bytes",
            "waste_hip_ecache_create", "waste_hip_ecache_destroy", "waste_hip_ecache_set_source",
            "waste_hip_ecache_hint", "waste_hip_ecache_prefetch", "waste_hip_ecache_get",
@@ -83,7 +83,7 @@ class MoeProf(C.Structure):
 class EcacheCounts(C.Structure):
     _fields_ = [("hits", C.c_uint64), ("misses", C.c_uint64), ("evictions", C.c_uint64),
                 ("prefetched", C.c_uint64), ("spec_issued", C.c_uint64), ("reads", C.c_uint64),
-                ("bytes_read", C.c_uint64)]
+                ("bytes_read", C.c_uint64), ("spec_used", C.c_uint64), ("spec_wasted", C.c_uint64)]
 
 
 class ContainerCfg(C.Structure):
@@ -137,6 +137,7 @@ def lib():
         "waste_hip_moe_experts": (i, [vp, vp, i, i, vp, vp]),
         "waste_hip_moe_bind_table": (i, [vp, ip, C.POINTER(vp), i, i, vp]),
         "waste_hip_moe_predict": (i, [vp, vp, i, i, vp, vp]),
+        "waste_hip_moe_set_lookahead_groups": (i, [vp, i]),
         "waste_hip_moe_forward_cached": (i, [vp, vp, i, vp, i, vp, i, vp, vp, vp, vp]),
         "waste_hip_moe_forward_static": (i, [vp, vp, i, i, vp, vp, vp, vp, vp]),
         "waste_hip_moe_static_bytes": (C.c_size_t, [vp, i]),
@@ -291,6 +292,11 @@ class MoeLayer:
 
     def predict(self, x_ptr, n, ids_ptr, bf16=False, stream=None):
         check(self.L.waste_hip_moe_predict(self.h, x_ptr, int(bf16), n, ids_ptr, stream), "predict")
+
+    def set_lookahead_groups(self, on):
+        """predict() within the layer's own group limit (True) or by the
+        engine's rule, top n of score + bias over every expert (False)."""
+        check(self.L.waste_hip_moe_set_lookahead_groups(self.h, int(bool(on))), "set_lookahead_groups")
 
     def forward_cached(self, cache, layer, x_ptr, y_ptr, nxt=None, lookahead=0, ids_ptr=None,
                        w_ptr=None, bf16=False, stream=None):

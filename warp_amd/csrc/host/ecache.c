@@ -43,6 +43,7 @@ enum { S_EMPTY = 0, S_READY, S_INFLIGHT };
 typedef struct {
     int32_t key;                     /* (layer << 16) | expert, -1 empty   */
     uint8_t state, fresh, out;
+    uint8_t spec;                    /* a lookahead read not demanded yet  */
     uint32_t hits;
     uint64_t last, pin;
     uint64_t use;                    /* release that last covered a reader */
@@ -207,7 +208,9 @@ static void claim(waste_hip_ecache *c, int si, int32_t key, uint8_t state)
     if (q->key >= 0) {
         h_erase(c, q->key);
         c->st.evictions++;
+        if (q->spec) c->st.spec_wasted++;           /* read ahead, never demanded */
     }
+    q->spec = 0;
     if (si >= c->n_used) c->n_used = si + 1;
     q->key = key;
     h_insert(c, key, si);
@@ -363,6 +366,7 @@ int waste_hip_ecache_prefetch(waste_hip_ecache *c, int layer, const int *ids, in
         claim(c, vi, key, S_INFLIGHT);
         c->slot[vi].fresh = 0;
         c->slot[vi].pin = 0;
+        c->slot[vi].spec = 1;
         c->st.spec_issued++;
         start_fill(c, vi, layer, ids[i]);
     }
@@ -404,6 +408,10 @@ static int demand(waste_hip_ecache *c, int layer, int expert)
     int si = lookup(c, key);
     if (si >= 0) {
         slot_t *q = &c->slot[si];
+        if (q->spec) {                               /* a lookahead read that landed */
+            q->spec = 0;
+            c->st.spec_used++;
+        }
         if (q->fresh) q->fresh = 0;
         else {
             c->st.hits++;

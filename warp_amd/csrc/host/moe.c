@@ -86,6 +86,7 @@ struct waste_hip_moe {
     int sh_done;                 /* the route's launch ran the shared down  */
     int sh_in_combine;           /* the combine runs the shared down        */
     int32_t *d_look;             /* the lookahead's ids                    */
+    int look_groups;             /* predict applies the group limit        */
     /* few-token products on the matrix cores (skinny.hip): column slices of
      * the router, the shared gate/up and the shared down (0: not taken),
      * and the partials' buffer, Td tokens' worth */
@@ -954,17 +955,38 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *c
     return 0;
 }
 
+/* The lookahead's guesses a predict() of n on m writes: at most E, and
+ * with the group limit at most the experts of the groups it keeps. */
+static int look_count(const waste_hip_moe *m, int n)
+{
+    if (n > m->E) n = m->E;
+    if (m->look_groups && m->c.n_group > 1) {
+        const int kept = m->c.topk_group * (m->E / m->c.n_group);
+        if (n > kept) n = kept;
+    }
+    return n;
+}
+
+int waste_hip_moe_set_lookahead_groups(waste_hip_moe *m, int on)
+{
+    if (!m || (on != 0 && on != 1)) return WASTE_HIP_EINVAL;
+    m->look_groups = on;
+    return 0;
+}
+
 int waste_hip_moe_predict(waste_hip_moe *m, const void *x, int x_bf16, int n, int32_t *ids, void *stream)
 {
     if (!m || !x || !ids || n <= 0 || n > 64 || !m->has_router) return WASTE_HIP_EINVAL;
-    if (n > m->E) n = m->E;
+    n = look_count(m, n);
     hipStream_t s = (hipStream_t)stream;
     whip_gemv_job j;
     j.A = m->router; j.B = NULL; j.x = x; j.x_ld = m->H; j.x_bf16 = x_bf16; j.y = m->plogits;
     j.y_ld = m->E;
     CK((hipError_t)whip_gemv_multi(&j, 1, 1, s));
-    /* selection order only: no group limit, weights unused */
-    whip_route_cfg rc = { m->E, n, m->c.score_func, 0, 1.0f, 0, 0 };
+    /* selection order only, weights unused; the group limit when asked */
+    const int grouped = m->look_groups && m->c.n_group > 1;
+    whip_route_cfg rc = { m->E, n, m->c.score_func, 0, 1.0f, grouped ? m->c.n_group : 0,
+                          grouped ? m->c.topk_group : 0 };
     CK((hipError_t)whip_route(&rc, m->plogits, m->d_bias, 1, ids, m->pw, NULL, NULL, NULL, NULL,
                               m->err + 4, s));
     return 0;
@@ -1010,7 +1032,7 @@ int waste_hip_moe_forward_cached(waste_hip_moe *m, waste_hip_ecache *c, int laye
     float *d_w = w ? w : m->b.w;
     int rc = waste_hip_moe_route(m, x, x_bf16, 1, d_ids, d_w, NULL, stream);
     if (rc) return rc;
-    int nl = next && lookahead > 0 ? (lookahead < next->E ? lookahead : next->E) : 0;
+    const int nl = next && lookahead > 0 ? look_count(next, lookahead) : 0;
     if (nl && (rc = waste_hip_moe_predict(next, x, x_bf16, nl, m->d_look, stream))) return rc;
     CK(hipMemcpyAsync(m->h_sel, d_ids, (size_t)K * sizeof(int32_t), hipMemcpyDeviceToHost, s));
     if (nl) CK(hipMemcpyAsync(m->h_sel + 64, m->d_look, (size_t)nl * sizeof(int32_t), hipMemcpyDeviceToHost, s));
