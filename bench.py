@@ -675,7 +675,11 @@ def main():
     cfg = synth.CONFIGS[a.config]
     H, E, K, I = cfg["hidden"], cfg["n_experts"], cfg["top_k"], cfg["moe_inter"]
     B = a.batch
-    layers, slab, books, rb, trunk = build_layers(torch, warp_amd, synth, cfg, a.layers, B)
+    # a slab per layer object for the small shapes (as in the other
+    # configurations below): one shared slab of theirs fits the Infinity Cache
+    own = a.config != "dsv3"
+    layers, slab, books, rb, trunk = build_layers(torch, warp_amd, synth, cfg, a.layers, B, own_slabs=own)
+    slabs_own, slab = (slab, slab[0]) if own else (None, slab)
     if a.copy_calibrate:
         n = a.copy_calibrate << 20
         src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda:0")

@@ -284,7 +284,18 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
         t0 = cls * tm.tpc + j * per_wg;
         t1 = min(t0 + per_wg, (cls + 1) * tm.tpc);
     } else {
-        t0 = blockIdx.x * per_wg;
+        // runs in tile order.  Without SPAN a run is about one pair's
+        // classes, and pairs of one expert are neighbours in the pair order:
+        // they read the same index tiles in the same order.  Workgroup w
+        // runs on XCD w % 8, so consecutive runs go to one XCD (a bijection
+        // of [0, G)); those workgroups start together and the expert's
+        // second read is served by that XCD's L2.
+        int w = blockIdx.x;
+        if (!SPAN) {
+            const int G = (tiles + per_wg - 1) / per_wg, x = w & 7;
+            w = x * (G >> 3) + min(x, G & 7) + (w >> 3);
+        }
+        t0 = w * per_wg;
         t1 = min(tiles, t0 + per_wg);
     }
     if (t0 >= t1) return;                            // whole workgroup
@@ -401,10 +412,12 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             act_loads(p, chunk);
             return;
         }
-        const size_t e0 = (size_t)xr * a.src_ld + (size_t)(chunk * PW + v) * 8;
-        const uint8_t *xb = (const uint8_t *)a.src + e0 * (a.src_bf16 ? 2 : 4);
-        xq0 = *(const uint4 *)xb;
-        xq1 = *(const uint4 *)(xb + (a.src_bf16 ? 0 : 16));
+        if (wv == 0) {                               // uniform: the wavefront that stages x
+            const size_t e0 = (size_t)xr * a.src_ld + (size_t)(chunk * PW + v) * 8;
+            const uint8_t *xb = (const uint8_t *)a.src + e0 * (a.src_bf16 ? 2 : 4);
+            xq0 = *(const uint4 *)xb;
+            xq1 = *(const uint4 *)(xb + (a.src_bf16 ? 0 : 16));
+        }
     };
     // The build in two steps.  stage: the books to LDS and the class's x
     // (converted, or for ACT reduced from the partials) to s_h, both LDS
@@ -420,25 +433,21 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
             tm.at(t, p, kind, chunk, rb);
             act_x(p, chunk);                         // ends with a barrier
         } else {
-            const uint32_t w8[8] = {xq0.x, xq0.y, xq0.z, xq0.w, xq1.x, xq1.y, xq1.z, xq1.w};
-            float xv[8];
+            if (wv == 0) {                           // uniform: only wavefront 0 loaded x
+                const uint32_t w8[8] = {xq0.x, xq0.y, xq0.z, xq0.w, xq1.x, xq1.y, xq1.z, xq1.w};
+                float xv[8];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float lo16 = wh_bf16(w8[i] & 0xffff), hi16 = wh_bf16(w8[i] >> 16);
-                xv[2 * i] = a.src_bf16 ? lo16 : __uint_as_float(w8[2 * i]);
-                xv[2 * i + 1] = a.src_bf16 ? hi16 : __uint_as_float(w8[2 * i + 1]);
-            }
-            if (tid < 32) {
+                for (int i = 0; i < 4; i++) {
+                    const float lo16 = wh_bf16(w8[i] & 0xffff), hi16 = wh_bf16(w8[i] >> 16);
+                    xv[2 * i] = a.src_bf16 ? lo16 : __uint_as_float(w8[2 * i]);
+                    xv[2 * i + 1] = a.src_bf16 ? hi16 : __uint_as_float(w8[2 * i + 1]);
+                }
+                if (lane < 32) {
 #pragma unroll
-                for (int k = 0; k < 8; k++) s_h[v * 8 + k] = xv[k];
+                    for (int k = 0; k < 8; k++) s_h[v * 8 + k] = xv[k];
+                }
             }
             __syncthreads();
-            // The other wavefronts never read their x loads; without this
-            // wait the compiler keeps those registers pending into the tile
-            // loop and waits for every load at its head.  (For the first
-            // class no tile is in flight yet; for a later one the tiles in
-            // flight went out before its build loads, so they have landed.)
-            __builtin_amdgcn_s_waitcnt(0x0F70);      // vmcnt(0)
         }
     };
     // x of this lane's position as bf16 pieces: bf16 activations are one
@@ -532,15 +541,27 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     load_tile(B, src, loff);
     scB = scb[presc ? lrow : 0];
     WT_KEEP(2);
+    // A run across classes: the next class's build inputs go out at the
+    // start of a class, ahead of the reloads that bring the next class's
+    // tiles, so at the class boundary they have landed and the build waits
+    // for nothing in flight.  (ACT: at the boundary; its inputs are summed
+    // as they arrive.)
     for (int lo = t0; lo < t1;) {
         const int hi = min(t1, (lo / tm.tpc + 1) * tm.tpc);
-        if (lo > t0) {                               // uniform: the next class's build inputs
-            int pn, k_, c_, r_;
-            tm.at(lo, pn, k_, c_, r_);
-            build_loads(lo, s_xr[pn - p_lo]);
+        if (lo > t0) {                               // uniform
+            if (ACT) {
+                int pn, k_, c_, r_;
+                tm.at(lo, pn, k_, c_, r_);
+                build_loads(lo, s_xr[pn - p_lo]);
+            }
             __syncthreads();                         // the old tables and s_h are done with
             stage(lo);
             tables();
+        }
+        if (!ACT && hi < t1) {                       // uniform
+            int pn, k_, c_, r_;
+            tm.at(hi, pn, k_, c_, r_);
+            build_loads(hi, s_xr[pn - p_lo]);
         }
         // A counted loop of pairs and an odd tile after it: an exit in the
         // middle of a round leaves the compiler unsure which loads are in
