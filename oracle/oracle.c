@@ -20,6 +20,7 @@
 #define WQ_Q4G 3
 #define WQ_Q3G 7
 #define WQ_VQ3R 4
+#define WQ_VQ4P 8
 #define MAGIC_EXPERT 0x50584557u
 
 /* ---- expf ----------------------------------------------------------------
@@ -553,7 +554,9 @@ int orc_record_check(const uint8_t *rec, size_t rec_bytes, int layer,
     if (magic != MAGIC_EXPERT) return 1;
     if (lay != (uint16_t)layer || eid != (uint16_t)expert) return 1;
     if ((size_t)rec4k * 4096u != rec_bytes) return 1;
-    if (fmt != WQ_VQ3R) return 1;
+    /* index_bits 6 (four stages of 64 entries) is VQ4P, else VQ3R
+     * (src/model.c:3660-3666) */
+    if (fmt != (stages == 4 ? WQ_VQ4P : WQ_VQ3R)) return 1;
     if (lr != 0) return 1;
     if ((long)cbid + 3L * stages > n_books) return 1;
     if (!(go == 48 && go < uo && uo < dof && dof < co && co <= rec_bytes)) return 1;
@@ -576,6 +579,37 @@ static rec_view view(const uint8_t *rec)
     memcpy(&v.go, rec + 20, 4); memcpy(&v.uo, rec + 24, 4);
     memcpy(&v.dof, rec + 28, 4); memcpy(&v.co, rec + 32, 4);
     return v;
+}
+
+/* One matrix's table (vq_build_lut, src/model.c:3864-3880): the fp32 LUT,
+ * and for VQ4P its int8 shadow with one scale per block of ORC_VQ_LUT_BLK
+ * positions; the rows through it (vq_apply, src/model.c:4152-4171): VQ4P
+ * through the int8 table, VQ3R through the fp32 one.  VQ4P is the engine's
+ * index_bits == 6, the one geometry of four stages of 64 entries. */
+static int is_p6(const orc_moe *m) { return m->stages == 4 && m->entries == 64; }
+
+typedef struct { float *lut; int8_t *q; float *qs; } orc_tab;
+
+static void tab_alloc(orc_tab *t, size_t lut_sz)
+{
+    t->lut = (float *)malloc(lut_sz * sizeof(float));
+    t->q = (int8_t *)malloc(lut_sz);
+    t->qs = (float *)malloc((lut_sz / ORC_VQ_LUT_BLK + 2) * sizeof(float));
+}
+
+static void tab_free(orc_tab *t) { free(t->lut); free(t->q); free(t->qs); }
+
+static void tab_build(const orc_moe *m, orc_tab *t, const float *x, int cb, int nv)
+{
+    orc_lutb(t->lut, m->booksT, x, cb, m->stages, m->entries, m->vec_dim, 0, nv, m->order);
+    if (is_p6(m)) orc_vq_quant_lut(t->lut, nv, m->stages, m->entries, t->q, t->qs);
+}
+
+static void tab_rows(const orc_moe *m, float *y, const uint8_t *idx, const uint16_t *sc,
+                     const orc_tab *t, int M, int nv)
+{
+    if (is_p6(m)) orc_vq_rows_p6(y, idx, sc, t->q, t->qs, 0, M, nv, m->order);
+    else orc_vq_rows(y, idx, sc, t->lut, 0, M, nv, m->stages, m->entries);
 }
 
 /* matvec_t for one token (src/model.c:939-999 on the default trunk kernel):
@@ -625,9 +659,8 @@ int orc_moe_layer(const orc_moe *m, const float *x, float *out, int *idx_o,
 
     memset(out, 0, (size_t)H * sizeof(float));
     const size_t lut_sz = (size_t)((H > I ? H : I) / vd) * st * en;
-    float *lut_g = (float *)malloc(lut_sz * sizeof(float));
-    float *lut_u = (float *)malloc(lut_sz * sizeof(float));
-    float *lut_d = (float *)malloc(lut_sz * sizeof(float));
+    orc_tab tg, tu, td;
+    tab_alloc(&tg, lut_sz); tab_alloc(&tu, lut_sz); tab_alloc(&td, lut_sz);
     float *ga = (float *)malloc((size_t)I * sizeof(float));
     float *ub = (float *)malloc((size_t)I * sizeof(float));
     float *acc = (float *)malloc((size_t)H * sizeof(float));
@@ -638,15 +671,15 @@ int orc_moe_layer(const orc_moe *m, const float *x, float *out, int *idx_o,
         const rec_view h = view(rec);
         const uint16_t *sc = (const uint16_t *)(rec + h.co);
         if (!lut_ready) {
-            orc_lutb(lut_g, m->booksT, x, h.cbid + 0 * st, st, en, vd, 0, H / vd, m->order);
-            orc_lutb(lut_u, m->booksT, x, h.cbid + 1 * st, st, en, vd, 0, H / vd, m->order);
+            tab_build(m, &tg, x, h.cbid + 0 * st, H / vd);
+            tab_build(m, &tu, x, h.cbid + 1 * st, H / vd);
             lut_ready = 1;
         }
-        orc_vq_rows(ga, rec + h.go, sc, lut_g, 0, I, H / vd, st, en);
-        orc_vq_rows(ub, rec + h.uo, sc + I, lut_u, 0, I, H / vd, st, en);
+        tab_rows(m, ga, rec + h.go, sc, &tg, I, H / vd);
+        tab_rows(m, ub, rec + h.uo, sc + I, &tu, I, H / vd);
         orc_act_pair(ga, ub, I);
-        orc_lutb(lut_d, m->booksT, ga, h.cbid + 2 * st, st, en, vd, 0, I / vd, m->order);
-        orc_vq_rows(acc, rec + h.dof, sc + 2 * I, lut_d, 0, H, I / vd, st, en);
+        tab_build(m, &td, ga, h.cbid + 2 * st, I / vd);
+        tab_rows(m, acc, rec + h.dof, sc + 2 * I, &td, H, I / vd);
         const float wj = w[j];
         for (int i = 0; i < H; i++) out[i] += wj * acc[i];
     }
@@ -661,7 +694,7 @@ int orc_moe_layer(const orc_moe *m, const float *x, float *out, int *idx_o,
     tensor_mv(&m->sh_down, a, tmp, m->order);
     for (int i = 0; i < H; i++) out[i] += tmp[i];
     free(a); free(b); free(tmp);
-    free(lut_g); free(lut_u); free(lut_d); free(ga); free(ub); free(acc); free(logit);
+    tab_free(&tg); tab_free(&tu); tab_free(&td); free(ga); free(ub); free(acc); free(logit);
     return nsel < 0 ? -1 : rcode;
 }
 
@@ -689,8 +722,9 @@ int orc_moe_chunk(const orc_moe *m, const float *x, int T, float *out,
     memset(out, 0, (size_t)T * H * sizeof(float));
 
     const size_t lut_sz = (size_t)((H > I ? H : I) / vd) * st * en;
-    float *lut_gu = (float *)malloc((size_t)T * 2 * lut_sz * sizeof(float));
-    float *lut_d = (float *)malloc(lut_sz * sizeof(float));
+    orc_tab *tgu = (orc_tab *)malloc((size_t)T * 2 * sizeof(orc_tab)), td;
+    for (int q = 0; q < 2 * T; q++) tab_alloc(&tgu[q], lut_sz);
+    tab_alloc(&td, lut_sz);
     float *ga = (float *)malloc((size_t)I * sizeof(float));
     float *ub = (float *)malloc((size_t)I * sizeof(float));
     float *acc = (float *)malloc((size_t)H * sizeof(float));
@@ -705,10 +739,8 @@ int orc_moe_chunk(const orc_moe *m, const float *x, int T, float *out,
         const uint16_t *s16 = (const uint16_t *)(rec + h.co);
         if (!lut_ready) {
             for (int t = 0; t < T; t++) {
-                orc_lutb(lut_gu + (size_t)(2 * t) * lut_sz, m->booksT, x + (size_t)t * H,
-                         h.cbid + 0 * st, st, en, vd, 0, H / vd, m->order);
-                orc_lutb(lut_gu + (size_t)(2 * t + 1) * lut_sz, m->booksT, x + (size_t)t * H,
-                         h.cbid + 1 * st, st, en, vd, 0, H / vd, m->order);
+                tab_build(m, &tgu[2 * t], x + (size_t)t * H, h.cbid + 0 * st, H / vd);
+                tab_build(m, &tgu[2 * t + 1], x + (size_t)t * H, h.cbid + 1 * st, H / vd);
             }
             lut_ready = 1;
         }
@@ -717,11 +749,11 @@ int orc_moe_chunk(const orc_moe *m, const float *x, int T, float *out,
             for (int j = 0; j < K; j++)
                 if (route[(size_t)t * K + j] == e) { wj = rw[(size_t)t * K + j]; break; }
             if (wj == 0.0f) continue;
-            orc_vq_rows(ga, rec + h.go, s16, lut_gu + (size_t)(2 * t) * lut_sz, 0, I, H / vd, st, en);
-            orc_vq_rows(ub, rec + h.uo, s16 + I, lut_gu + (size_t)(2 * t + 1) * lut_sz, 0, I, H / vd, st, en);
+            tab_rows(m, ga, rec + h.go, s16, &tgu[2 * t], I, H / vd);
+            tab_rows(m, ub, rec + h.uo, s16 + I, &tgu[2 * t + 1], I, H / vd);
             orc_act_pair(ga, ub, I);
-            orc_lutb(lut_d, m->booksT, ga, h.cbid + 2 * st, st, en, vd, 0, I / vd, m->order);
-            orc_vq_rows(acc, rec + h.dof, s16 + 2 * I, lut_d, 0, H, I / vd, st, en);
+            tab_build(m, &td, ga, h.cbid + 2 * st, I / vd);
+            tab_rows(m, acc, rec + h.dof, s16 + 2 * I, &td, H, I / vd);
             float *dst = out + (size_t)t * H;
             for (int i = 0; i < H; i++) dst[i] += wj * acc[i];
         }
@@ -736,7 +768,9 @@ int orc_moe_chunk(const orc_moe *m, const float *x, int T, float *out,
     tensor_mm(&m->sh_down, sa, sh, T);
     for (size_t i = 0; i < (size_t)T * H; i++) out[i] += sh[i];
     free(sa); free(sb); free(sh);
-    free(lut_gu); free(lut_d); free(ga); free(ub); free(acc); free(logit); free(route); free(rw);
+    for (int q = 0; q < 2 * T; q++) tab_free(&tgu[q]);
+    free(tgu); tab_free(&td);
+    free(ga); free(ub); free(acc); free(logit); free(route); free(rw);
     return rcode;
 }
 
@@ -752,9 +786,8 @@ int orc_moe_apply(const orc_moe *m, const float *x, int T, const int *idx,
     const int K = m->top_k, H = m->hidden, I = m->moe_inter;
     const int st = m->stages, en = m->entries, vd = m->vec_dim, E = m->n_experts;
     const size_t lut_sz = (size_t)((H > I ? H : I) / vd) * st * en;
-    float *lut_g = (float *)malloc(lut_sz * sizeof(float));
-    float *lut_u = (float *)malloc(lut_sz * sizeof(float));
-    float *lut_d = (float *)malloc(lut_sz * sizeof(float));
+    orc_tab tg, tu, td;
+    tab_alloc(&tg, lut_sz); tab_alloc(&tu, lut_sz); tab_alloc(&td, lut_sz);
     float *ga = (float *)malloc((size_t)I * sizeof(float));
     float *ub = (float *)malloc((size_t)I * sizeof(float));
     float *acc = (float *)malloc((size_t)H * sizeof(float));
@@ -779,15 +812,15 @@ int orc_moe_apply(const orc_moe *m, const float *x, int T, const int *idx,
             const rec_view h = view(rec);
             const uint16_t *sc = (const uint16_t *)(rec + h.co);
             if (!lut_ready) {
-                orc_lutb(lut_g, m->booksT, xt, h.cbid, st, en, vd, 0, H / vd, m->order);
-                orc_lutb(lut_u, m->booksT, xt, h.cbid + st, st, en, vd, 0, H / vd, m->order);
+                tab_build(m, &tg, xt, h.cbid, H / vd);
+                tab_build(m, &tu, xt, h.cbid + st, H / vd);
                 lut_ready = 1;
             }
-            orc_vq_rows(ga, rec + h.go, sc, lut_g, 0, I, H / vd, st, en);
-            orc_vq_rows(ub, rec + h.uo, sc + I, lut_u, 0, I, H / vd, st, en);
+            tab_rows(m, ga, rec + h.go, sc, &tg, I, H / vd);
+            tab_rows(m, ub, rec + h.uo, sc + I, &tu, I, H / vd);
             orc_act_pair(ga, ub, I);
-            orc_lutb(lut_d, m->booksT, ga, h.cbid + 2 * st, st, en, vd, 0, I / vd, m->order);
-            orc_vq_rows(acc, rec + h.dof, sc + 2 * I, lut_d, 0, H, I / vd, st, en);
+            tab_build(m, &td, ga, h.cbid + 2 * st, I / vd);
+            tab_rows(m, acc, rec + h.dof, sc + 2 * I, &td, H, I / vd);
             float *dst = out + (size_t)t * H;
             for (int i = 0; i < H; i++) dst[i] += wj * acc[i];
         }
@@ -811,7 +844,7 @@ int orc_moe_apply(const orc_moe *m, const float *x, int T, const int *idx,
     }
     for (size_t i = 0; i < (size_t)T * H; i++) out[i] += sh[i];
     free(a); free(b); free(sh);
-    free(lut_g); free(lut_u); free(lut_d); free(ga); free(ub); free(acc);
+    tab_free(&tg); tab_free(&tu); tab_free(&td); free(ga); free(ub); free(acc);
     return rc;
 }
 

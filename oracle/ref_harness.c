@@ -143,6 +143,13 @@ static void put_tensor(waste_tensor *t, const char *name, const ref_tensor *s)
  * table, one expert bank served from a memfd through the engine's own
  * bank_fetch/record_check, and the scratch buffers waste_model_load would
  * size.  NULL on failure. */
+/* The container geometry ref_model builds: 8 (VQ3R, three stages of 256
+ * entries) or 6 (VQ4P, four stages of 64, with the int8 table shadows
+ * waste_model_load allocates for it, src/model.c:3340-3356). */
+static int ref_ib = 8;
+
+void ref_set_index_bits(int ib) { ref_ib = ib == 6 ? 6 : 8; }
+
 static waste_model *ref_model(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
                               int score_func, int renorm, float routed_scale,
                               const ref_tensor *router, const float *bias,
@@ -176,8 +183,10 @@ static waste_model *ref_model(int hidden, int n_experts, int top_k, int moe_inte
     m->n_tensors = nt;
 
     m->codebooksT = (float *)booksT;
-    m->n_books = n_books; m->vec_dim = 8; m->cb_entries = 256; m->stages = 3;
-    m->index_bits = 8;
+    m->n_books = n_books; m->vec_dim = 8;
+    m->index_bits = ref_ib;
+    m->stages = ref_ib == 6 ? 4 : 3;
+    m->cb_entries = ref_ib == 6 ? 64 : 256;
     m->expert_m[0] = m->expert_m[1] = I; m->expert_m[2] = H;
     m->expert_n[0] = m->expert_n[1] = H; m->expert_n[2] = I;
 
@@ -208,6 +217,11 @@ static waste_model *ref_model(int hidden, int n_experts, int top_k, int moe_inte
     m->h = (float *)calloc((size_t)H, sizeof(float));
     m->lut = (float *)calloc(3 * lut_sz, sizeof(float));
     m->lut_bytes = 3 * lut_sz * sizeof(float);
+    if (ref_ib == 6) {
+        const size_t nvmax = (size_t)((H > I ? H : I) / 8);
+        m->lut8 = (int8_t *)calloc(3 * nvmax * 4 * 64, 1);
+        m->lut8_scale = (float *)calloc(3 * (nvmax / WASTE_VQ_LUT_BLK + 2), sizeof(float));
+    }
     return m;
 }
 
@@ -216,6 +230,7 @@ static void ref_model_free(waste_model *m)
     close(m->bank[0].fd[0]);
     free(m->miss_buf); free(m->att); free(m->ff); free(m->e_gate);
     free(m->ares); free(m->h); free(m->lut); free(m->t);
+    free(m->lut8); free(m->lut8_scale);
     pthread_mutex_destroy(&m->fetch_mu);
     free(m);
 }
@@ -248,6 +263,12 @@ int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
         m->cused = (int *)calloc((size_t)E, sizeof(int));
         m->clat = (float *)calloc(2 * (size_t)T * H, sizeof(float));
         m->cq = (float *)calloc(((size_t)2 * T + 1) * lut_sz, sizeof(float));
+        if (ref_ib == 6) {      /* moe_chunk's int8 shadows, src/model.c:7052-7065 */
+            const size_t nvmax = (size_t)((H > I ? H : I) / 8);
+            m->cq8 = (int8_t *)calloc(((size_t)2 * T + 1) * nvmax * 4 * 64 + 64, 1);
+            m->cq8_scale = (float *)calloc(((size_t)2 * T + 1) * (nvmax / WASTE_VQ_LUT_BLK + 2) + 64,
+                                           sizeof(float));
+        }
         m->cff = (float *)calloc(2 * (size_t)I + H, sizeof(float));
         m->ckv = (float *)calloc(2 * (size_t)T * SI + (size_t)T * H, sizeof(float));
         m->chunk_cap = T;
@@ -256,6 +277,8 @@ int ref_moe(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
         if (rw) memcpy(rw, m->crw, (size_t)T * K * sizeof(float));
         free(m->croute); free(m->crw); free(m->cused); free(m->clat);
         free(m->cq); free(m->cff); free(m->ckv);
+        free(m->cq8); free(m->cq8_scale);
+        m->cq8 = NULL; m->cq8_scale = NULL;
     }
     const int err = m->read_error;
     ref_model_free(m);

@@ -25,11 +25,16 @@ vq4p.npz (VQ4P, 6-bit codes through the engine's int8 LUT):
   qlut, qq, qsc vq_quant_lut of a planted table (an all-zero block, exact
                 halves under a unit inverse, a lone extreme)
 
+vq4p_layer.npz (whole VQ4P layers: moe_layer and moe_chunk with index_bits 6,
+the tables quantised to int8 and the rows through vq_rows_p6):
+  {case}_digest, {case}_layer_out{o}, {case}_layer_ids{o},
+  {case}_chunk_out{o}, {case}_chunk_ids{o}, {case}_chunk_w{o}
+
 q3g.npz (Q3G trunk rows, 3-bit codes plus a guard byte, tools/convert.py:854-892):
   rows{o}_{cols}  mvq_rows of order o on the seeded rows of each width
   digest_{cols}   sha256 of the case's packed rows, scales and x
 
-  python tests/golden/make_golden.py [scalars|vq4p|q3g]
+  python tests/golden/make_golden.py [scalars|vq4p|vq4p_layer|q3g]
 """
 import hashlib
 import os
@@ -86,6 +91,9 @@ def main():
     if sys.argv[1:] == ["q3g"]:                     # only q3g.npz
         write_q3g(ref)
         return
+    if sys.argv[1:] == ["vq4p_layer"]:              # only vq4p_layer.npz
+        write_vq4p_layer(orc, ref)
+        return
     if ref.isa != 2:
         print("warning: this host does not run the reference's AVX-512 kernels; order 1 = portable")
     for name in CASES:
@@ -116,7 +124,42 @@ def main():
 
     write_scalars(ref)
     write_vq4p(orc, ref)
+    write_vq4p_layer(orc, ref)
     write_q3g(ref)
+
+
+# VQ4P layers: name -> (H, I, E, K, kwargs, T)
+VQ4P_CASES = {
+    "p6_softmax": (256, 128, 16, 4, dict(score_func=1, seed=41, index_bits=6), 3),
+    "p6_sigmoid_q8g": (256, 128, 16, 4, dict(score_func=0, renorm=1, routed_scale=2.5, bias=True,
+                                             n_shared=1, shared_fmt=FMT_Q8G, seed=42, index_bits=6), 4),
+}
+
+
+def vq4p_case(name):
+    H, I, E, K, kw, T = VQ4P_CASES[name]
+    L = Layer(H, I, E, K, **kw)
+    return L, L.inputs(T, seed=kw["seed"] + 100)
+
+
+def write_vq4p_layer(orc, ref):
+    out = {}
+    for name in VQ4P_CASES:
+        L, X = vq4p_case(name)
+        _, bT = orc.books(L.books_f16)
+        out[f"{name}_digest"] = np.array(input_digest(L, X))
+        for o in (0, 1):
+            ref.set_order(o)
+            rc, lo, lr, _ = ref.moe(L, X[:1], bT)
+            assert rc == 0, rc
+            out[f"{name}_layer_out{o}"], out[f"{name}_layer_ids{o}"] = lo[0], lr[0]
+            rc, co, cr, cw = ref.moe(L, X, bT)
+            assert rc == 0, rc
+            out[f"{name}_chunk_out{o}"], out[f"{name}_chunk_ids{o}"], out[f"{name}_chunk_w{o}"] = co, cr, cw
+    ref.lib.ref_set_index_bits(8)
+    out["isa"] = np.array(ref.isa)
+    np.savez_compressed(os.path.join(HERE, "vq4p_layer.npz"), **out)
+    print("vq4p_layer written")
 
 
 Q3G_WIDTHS = (1024, 1000, 640)

@@ -159,10 +159,10 @@ class Oracle:
         return self.lib.orc_expf(float(x))
 
     def books(self, books_f16):
-        nb = books_f16.shape[0]
-        b = np.zeros((nb, 256, 8), np.float32)
-        bt = np.zeros((nb, 8, 256), np.float32)
-        self.lib.orc_books_load(ptr(np.ascontiguousarray(books_f16), u16p), nb, 256, 8, ptr(b, fp), ptr(bt, fp))
+        nb, en = books_f16.shape[0], books_f16.shape[1]
+        b = np.zeros((nb, en, 8), np.float32)
+        bt = np.zeros((nb, 8, en), np.float32)
+        self.lib.orc_books_load(ptr(np.ascontiguousarray(books_f16), u16p), nb, en, 8, ptr(b, fp), ptr(bt, fp))
         return b, bt
 
     def lutb(self, booksT, x, cb_base, order, stages=3, entries=256, vec_dim=8):
@@ -240,7 +240,8 @@ class _OrcLayer:
         self.rec_ptrs = (u8p * L.E)(*[ptr(b, u8p) for b in self.rec_bufs])
         self.bias = L.bias
         self.m = OrcMoe(L.H, L.E, L.K, L.I, L.n_shared, L.score_func, L.renorm, L.routed_scale,
-                        L.n_group, L.topk_group, 3, 256, 8, order, _tensor(L.router),
+                        L.n_group, L.topk_group, getattr(L, "stages", 3), getattr(L, "entries", 256), 8,
+                        order, _tensor(L.router),
                         ptr(L.bias, fp) if L.bias is not None else None,
                         _tensor(L.sh[0]), _tensor(L.sh[1]), _tensor(L.sh[2]),
                         ptr(self.booksT, fp), L.n_books, self.rec_ptrs, L.rec_bytes)
@@ -306,6 +307,7 @@ class Ref:
         L = self.lib = C.CDLL(path)
         _sig(L, "ref_init", C.c_int, [])
         _sig(L, "ref_set_order", None, [C.c_int])
+        _sig(L, "ref_set_index_bits", None, [C.c_int])
         _sig(L, "ref_vq_rows", None, [fp, u8p, u16p, fp, C.c_int, C.c_int, C.c_int, C.c_int])
         _sig(L, "ref_lutb", None, [fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int])
         _sig(L, "ref_vq_quant_lut", None, [fp, C.c_int, C.c_int, C.c_int, i8p, fp])
@@ -428,6 +430,7 @@ class Ref:
     def moe(self, L, X, booksT):
         T = X.shape[0]
         rt = self._rt
+        self.lib.ref_set_index_bits(getattr(L, "index_bits", 8))
         bank = np.frombuffer(L.bank(), np.uint8)
         out = np.zeros((T, L.H), np.float32)
         route = np.zeros((T, L.K), np.int32)

@@ -16,18 +16,29 @@ import numpy as np
 
 MAGIC_EXPERT = 0x50584557
 MAGIC_CODEBOOK = 0x4B424357
-FMT_F32, FMT_Q8G, FMT_Q4G, FMT_VQ3R = 0, 2, 3, 4
+FMT_F32, FMT_Q8G, FMT_Q4G, FMT_VQ3R, FMT_VQ4P = 0, 2, 3, 4, 8
 STAGES, ENTRIES, VEC_DIM, BLOCK = 3, 256, 8, 64
 
 
 def block_indices(idx, M, N):
-    """idx [M][N/8][stages] u8 -> [ceil(M/64)][N/8][64][stages], zero-padded
-    rows (tools/convert.py:777-792)."""
+    """idx [M][N/8][b] u8 (b = 3 bytes a (row, position) in both VQ3R and
+    VQ4P) -> [ceil(M/64)][N/8][64][b], zero-padded rows
+    (tools/convert.py:777-792)."""
     nv = N // VEC_DIM
     nb = (M + BLOCK - 1) // BLOCK
-    pad = np.zeros((nb * BLOCK, nv, STAGES), np.uint8)
+    b = idx.shape[2]
+    pad = np.zeros((nb * BLOCK, nv, b), np.uint8)
     pad[:M] = idx
-    return pad.reshape(nb, BLOCK, nv, STAGES).transpose(0, 2, 1, 3).copy()
+    return pad.reshape(nb, BLOCK, nv, b).transpose(0, 2, 1, 3).copy()
+
+
+def pack_p6(codes):
+    """VQ4P: four 6-bit codes [..][4] -> three bytes [..][3], code s at bit
+    6s of the little-endian 24-bit word (the inverse of the engine's
+    P6_J0..P6_J3, src/simd.h:73-76)."""
+    c = codes.astype(np.uint32)
+    w = c[..., 0] | (c[..., 1] << 6) | (c[..., 2] << 12) | (c[..., 3] << 18)
+    return np.stack([w & 0xFF, (w >> 8) & 0xFF, (w >> 16) & 0xFF], -1).astype(np.uint8)
 
 
 def unblock_indices(raw, M, N):
@@ -37,9 +48,10 @@ def unblock_indices(raw, M, N):
     return t.reshape(nb, nv, BLOCK, STAGES).transpose(0, 2, 1, 3).reshape(nb * BLOCK, nv, STAGES)[:M]
 
 
-def make_record(layer, eid, cb_base, shapes, idx_list, scale_list):
+def make_record(layer, eid, cb_base, shapes, idx_list, scale_list, fmt=FMT_VQ3R):
     """One WEXP record.  shapes = [(I,H),(I,H),(H,I)]; idx_list[k] is
-    [M][N/8][3] u8; scale_list[k] is [M] f16 bits (u16)."""
+    [M][N/8][3] u8 (VQ3R codes, or VQ4P's packed bytes); scale_list[k] is
+    [M] f16 bits (u16)."""
     body = bytearray()
     offs = []
     off = 48
@@ -53,7 +65,7 @@ def make_record(layer, eid, cb_base, shapes, idx_list, scale_list):
         body += np.asarray(s, np.uint16).tobytes()
     total = 48 + len(body)
     blocks = (total + 4095) // 4096
-    hdr = struct.pack("<IHHBBHHHIIIIIIII", MAGIC_EXPERT, layer, eid, FMT_VQ3R, 0,
+    hdr = struct.pack("<IHHBBHHHIIIIIIII", MAGIC_EXPERT, layer, eid, fmt, 0,
                       cb_base, 0, 0, blocks, offs[0], offs[1], offs[2], corr,
                       zlib.crc32(bytes(body)) & 0xFFFFFFFF, 0, 0)
     rec = bytearray(blocks * 4096)
@@ -66,20 +78,24 @@ from warp_amd.synth import Tensor, f16_bits, quant_q4g, quant_q8g  # noqa: E402,
 
 
 class Layer:
-    """One synthetic MoE layer."""
+    """One synthetic MoE layer.  index_bits 8: VQ3R experts (three stages
+    of 256 entries); 6: VQ4P (four stages of 64, the codes packed in three
+    bytes); idx then holds the unpacked codes [M][N/8][4]."""
 
     def __init__(self, H, I, E, K, *, score_func=0, renorm=0, routed_scale=1.0,
                  n_group=1, topk_group=1, n_shared=0, router_fmt=FMT_F32,
                  shared_fmt=FMT_Q8G, bias=False, seed=0, cb_base=0,
-                 book_scale=0.3, subnormal_books=0, layer=0):
+                 book_scale=0.3, subnormal_books=0, layer=0, index_bits=8):
         rng = np.random.default_rng(seed)
         self.H, self.I, self.E, self.K = H, I, E, K
         self.score_func, self.renorm, self.routed_scale = score_func, renorm, routed_scale
         self.n_group, self.topk_group, self.n_shared = n_group, topk_group, n_shared
         self.cb_base = cb_base
         self.layer = layer
-        self.n_books = cb_base + 3 * STAGES
-        books = (rng.standard_normal((self.n_books, ENTRIES, VEC_DIM)) * book_scale).astype(np.float32)
+        self.index_bits = index_bits
+        self.stages, self.entries = (4, 64) if index_bits == 6 else (STAGES, ENTRIES)
+        self.n_books = cb_base + 3 * self.stages
+        books = (rng.standard_normal((self.n_books, self.entries, VEC_DIM)) * book_scale).astype(np.float32)
         self.books_f16 = f16_bits(books)
         if subnormal_books:
             # plant fp16 subnormals: the loader flushes them to signed zero
@@ -93,11 +109,16 @@ class Layer:
         self.idx = []
         self.scales = []
         for e in range(E):
-            il = [rng.integers(0, ENTRIES, (M, N // VEC_DIM, STAGES), dtype=np.uint8) for M, N in shapes]
+            il = [rng.integers(0, self.entries, (M, N // VEC_DIM, self.stages), dtype=np.uint8)
+                  for M, N in shapes]
             sl = [f16_bits(rng.uniform(0.01, 0.05, M)) for M, _ in shapes]
             self.idx.append(il)
             self.scales.append(sl)
-            self.records.append(make_record(layer, e, cb_base, shapes, il, sl))
+            if index_bits == 6:
+                self.records.append(make_record(layer, e, cb_base, shapes, [pack_p6(c) for c in il], sl,
+                                                FMT_VQ4P))
+            else:
+                self.records.append(make_record(layer, e, cb_base, shapes, il, sl))
         self.rec_bytes = len(self.records[0])
         self.router = Tensor.make(router_fmt, (rng.standard_normal((E, H)) * 0.02).astype(np.float32))
         self.bias = (rng.standard_normal(E) * 0.02).astype(np.float32) if bias else None

@@ -16,7 +16,9 @@ Pins, per oracle function (oracle/oracle.c):
                     at K=E, renorm sum, group-limited brute force and its
                     n_group=1 reduction
   orc_act_pair      golden
-  orc_moe_layer / orc_moe_chunk   golden (both orders) + fp64 layer bound
+  orc_moe_layer / orc_moe_chunk   golden (both orders) + fp64 layer bound;
+                    VQ4P experts (int8 tables, vq_rows_p6) golden in both
+                    orders (vq4p_layer.npz)
   orc_record_check  valid/damaged records, crc32 against zlib
 """
 import ctypes
@@ -27,8 +29,9 @@ import zlib
 import numpy as np
 import pytest
 
-from golden.make_golden import CASES, Q3G_WIDTHS, case_layer, input_digest, q3g_digest, q3g_inputs
-from oracle_lib import Oracle
+from golden.make_golden import (CASES, Q3G_WIDTHS, VQ4P_CASES, case_layer, input_digest, q3g_digest, q3g_inputs,
+                                vq4p_case)
+from oracle_lib import Oracle, fp, i32p, ptr
 from records import FMT_F32, Layer, Tensor, quant_q3g, unblock_indices
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -436,3 +439,32 @@ def test_device_log1pf_sampled():
     stride = "1" if os.environ.get("WARP_SLOW") else "4099"
     out = subprocess.check_output([os.path.join(root, "oracle", "log1pf_check"), stride]).decode()
     assert " 0 differ" in out, out
+
+
+@pytest.mark.parametrize("name", list(VQ4P_CASES))
+def test_vq4p_layer_golden(orc, name):
+    """orc_moe_layer and orc_moe_chunk on VQ4P experts (index_bits 6: the
+    gate/up/down tables quantised to int8 per 32 positions, the rows
+    through vq_rows_p6) against the compiled reference's moe_layer and
+    moe_chunk, bit for bit in both orders."""
+    g = np.load(os.path.join(GOLD, "vq4p_layer.npz"))
+    L, X = vq4p_case(name)
+    assert input_digest(L, X) == str(g[f"{name}_digest"])
+    for o in (0, 1):
+        if o == 1 and int(g["isa"]) != 2:
+            continue
+        om = orc.moe(L, o)
+        rc, out, idx, w, lg = om.layer(X[0])
+        assert rc == 0
+        assert np.array_equal(idx, g[f"{name}_layer_ids{o}"])
+        assert np.array_equal(out.view(np.uint32), g[f"{name}_layer_out{o}"].view(np.uint32)), (name, o)
+        T = X.shape[0]
+        oc = np.zeros((T, L.H), np.float32)
+        ids = np.zeros((T, L.K), np.int32)
+        ww = np.zeros((T, L.K), np.float32)
+        rc = orc.lib.orc_moe_chunk(ctypes.byref(om.m), ptr(np.ascontiguousarray(X), fp), T, ptr(oc, fp),
+                                   ptr(ids, i32p), ptr(ww, fp))
+        assert rc == 0
+        assert np.array_equal(ids, g[f"{name}_chunk_ids{o}"])
+        assert np.array_equal(ww.view(np.uint32), g[f"{name}_chunk_w{o}"].view(np.uint32))
+        assert np.array_equal(oc.view(np.uint32), g[f"{name}_chunk_out{o}"].view(np.uint32)), (name, o)
