@@ -132,6 +132,14 @@ typedef struct {
     int verify_records;  /* check each record's crc32 when it is loaded     */
     int prefill_min_tokens; /* T above this runs the grouped matrix-core
                             path (0: 32); T up to it the decode kernels   */
+    int index_bits;      /* the container's (0 = 8): 8 VQ3R experts; 6 VQ4P
+                            (four stages of 64 entries, twelve books a
+                            record), every T on the decode path through
+                            the engine's int8 tables (vq_rows_p6)         */
+    int p6_order;        /* VQ4P: WASTE_HIP_ORDER_PORTABLE or _FMA, the
+                            arithmetic of the engine's table build and
+                            fold on a host without / with its AVX-512
+                            kernels (waste_hip_vq_p6_order(): this host's) */
 } waste_hip_moe_cfg;
 
 /* A trunk tensor as the engine holds it (waste_tensor, src/model.h:32-50):
@@ -154,7 +162,8 @@ int waste_hip_moe_set_router(waste_hip_moe *m, const waste_hip_tensor *gate,
 int waste_hip_moe_set_shared(waste_hip_moe *m, const waste_hip_tensor *gate,
                              const waste_hip_tensor *up,
                              const waste_hip_tensor *down);
-/* codebooks.bin payloads, fp16 [n_books][256][8], converted as the engine's
+/* codebooks.bin payloads, fp16 [n_books][entries][8] (256 entries, or 64
+ * for a VQ4P layer), converted as the engine's
  * loader does (subnormals flushed; src/model.c:2906-2941). */
 int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16,
                                 int n_books);
@@ -203,7 +212,8 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T,
  * shares that GPU's area, which keeps the last call's contents: calls
  * that overlap on one GPU (other streams, other threads) race; calls
  * ordered on one stream do not.  ids/w/logits as in forward(); NULL
- * leaves them in the area, good until the next call on the GPU. */
+ * leaves them in the area, good until the next call on the GPU.  VQ3R
+ * layers only (WASTE_HIP_EINVAL for a VQ4P one). */
 int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, int T,
                                  float *y, int32_t *ids, float *w, float *logits,
                                  void *stream);

@@ -18,13 +18,14 @@ def rel_err(y, ref):
     return float(np.max(np.abs(y - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
-def gpu_layer(L, max_tokens=1, verify=0, prefill_min=0, records=True):
+def gpu_layer(L, max_tokens=1, verify=0, prefill_min=0, records=True, p6_order=None):
     m = warp_amd.MoeLayer(hidden=L.H, n_experts=L.E, top_k=L.K, moe_inter=L.I,
                           n_shared=L.n_shared, score_func=L.score_func, renorm=L.renorm,
                           routed_scale=L.routed_scale, n_group=L.n_group,
                           topk_group=L.topk_group, layer=getattr(L, "layer", 0),
                           max_tokens=max_tokens, verify_records=verify,
-                          prefill_min_tokens=prefill_min)
+                          prefill_min_tokens=prefill_min, index_bits=getattr(L, "index_bits", 8),
+                          p6_order=p6_order)
     m.set_codebooks(L.books_f16)
     m.set_router(L.router, L.bias)
     if L.n_shared:

@@ -159,6 +159,28 @@ int whip_sk_route(const whip_route_cfg *c, const float *pr, int nsl_r, float *lo
  * clamped to [-127, 127] (src/model.c:3979-4074). */
 int whip_vq_quant_lut(const float *lut, int nv, int stages, int entries, int8_t *q,
                       float *scale, hipStream_t s);
+/* The same for ntab tables back to back: table t at lut + t*nv*stages*
+ * entries, its int8 copy at the same offset of q, its scales at
+ * scale + t*ceil(nv/32). */
+int whip_vq_quant_lut_n(const float *lut, int nv, int stages, int entries, int ntab, int8_t *q,
+                        float *scale, hipStream_t s);
+/* VQ4P tables of rows x kinds inputs: table t = (row t / kinds, kind
+ * t % kinds) from x row t / kinds (bf16 or fp32, row stride x_ld) and books
+ * cb + 4*kind .. + 3 of booksT ([book][8][64] fp32); lut[t][nv][4][64], in
+ * the engine's order (fma: the AVX-512 kernel's chain, else the portable
+ * C one's products and sums). */
+int whip_p6_lutb(const void *x, int x_bf16, int x_ld, int rows, int kinds, const float *booksT, int cb,
+                 int nv, int fma, float *lut, hipStream_t s);
+/* vq_rows_p6 of every pair's matrices: out[p][kind][M] from the record of
+ * expert pair_exp[p] (idx at idx_off[kind], f16 row scales at
+ * sc_off[kind]) through table pair_tok[p]*kinds + kind (per_tok) or p of
+ * q/qs (as whip_vq_quant_lut_n lays them out). */
+int whip_p6_rows_pairs(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok,
+                       int P, int kinds, const uint32_t *idx_off, const uint32_t *sc_off, int M, int nv,
+                       const int8_t *q, const float *qs, int per_tok, int fma, float *out, int *err,
+                       hipStream_t s);
+/* h[p][i] = silu(gu[p][0][i]) * gu[p][1][i], the engine's SwiGLU. */
+int whip_p6_act(const float *gu, int P, int I, float *h, hipStream_t s);
 /* Rows [r_lo, r_hi) (r_lo % 64 == 0) of a VQ4P matrix through lut8/lscale
  * (src/model.c:4076-4114); fma: fold the blocks with one fused
  * multiply-add (the AVX-512 and NEON kernels) instead of a product and a
@@ -257,7 +279,8 @@ typedef struct {
     const uint8_t *rec[WHIP_BIND_MAX];
     uint32_t layer, rec_4k_blocks, off_up, off_down, off_sc;
     int cb;                        /* required codebook id, -1 any          */
-    int book0, n_books;            /* ids the layer holds: [book0, n_books - 9] */
+    int book0, n_books;            /* ids the layer holds: [book0, n_books - nbk] */
+    uint32_t fmt, nbk;             /* the records' format and books per record */
 } whip_bind_args;
 int whip_bind(const uint8_t **recs, const whip_bind_args *a, int *err, hipStream_t s);
 /* err &= ~mask, in stream order. */

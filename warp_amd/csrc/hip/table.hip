@@ -33,10 +33,10 @@ k_bind(const uint8_t **__restrict__ recs, whip_bind_args a, int *__restrict__ er
     const uint32_t magic = q0.x, layer = q0.y & 0xffffu, eid = q0.y >> 16;
     const uint32_t fmt = q0.z & 0xffu, cb = q0.z >> 16, lowrank = q0.w & 0xffffu;
     const bool ok = magic == WASTE_MAGIC_EXPERT && layer == a.layer && eid == (uint32_t)e &&
-                    fmt == WQ_VQ3R && lowrank == 0 && q1.x == a.rec_4k_blocks && q1.y == 48u &&
+                    fmt == a.fmt && lowrank == 0 && q1.x == a.rec_4k_blocks && q1.y == 48u &&
                     q1.z == a.off_up && q1.w == a.off_down && q2.x == a.off_sc &&
                     (a.cb < 0 || cb == (uint32_t)a.cb) && (long)cb >= (long)a.book0 &&
-                    (long)cb + 9L <= (long)a.n_books;
+                    (long)cb + (long)a.nbk <= (long)a.n_books;
     recs[e] = ok ? r : nullptr;
     if (!ok) atomicOr(err, 8);
 }

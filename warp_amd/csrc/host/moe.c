@@ -87,6 +87,15 @@ struct waste_hip_moe {
     int sh_in_combine;           /* the combine runs the shared down        */
     int32_t *d_look;             /* the lookahead's ids                    */
     int look_groups;             /* predict applies the group limit        */
+    /* VQ4P experts (index_bits 6): four stages of 64 entries, 12 books a
+     * record; every T on the decode path */
+    int p6, stages, entries, nbk;
+    struct {
+        float *lut_gu, *lut_d;   /* fp32 tables [T][2][nv_gu][256], [P][nv_d][256] */
+        int8_t *q_gu, *q_d;      /* their int8 copies                      */
+        float *s_gu, *s_d;       /* and scales, one per 32 positions       */
+        float *gu, *h, *down;    /* rows [P][2][I], SwiGLU [P][I], down [P][H] */
+    } p6b;
     /* few-token products on the matrix cores (skinny.hip): column slices of
      * the router, the shared gate/up and the shared down (0: not taken),
      * and the partials' buffer, Td tokens' worth */
@@ -113,7 +122,7 @@ static float f16_book(uint16_t h)
 /* The layer's codebook id is known and its nine books are on the device. */
 static int books_ok(const waste_hip_moe *m)
 {
-    return m->cb >= m->book0 && m->cb + 9 <= m->book0 + m->n_books;
+    return m->cb >= m->book0 && m->cb + m->nbk <= m->book0 + m->n_books;
 }
 
 static int dmalloc(void **p, size_t n)
@@ -145,7 +154,8 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->b.h_sh, m->b.sh_out, m->b.ids, m->b.pair_tok, m->b.pair_exp,
                      m->b.tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
                      m->sh_h16, m->x16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->b.pair_rec,
-                     m->b.rcnt, m->b.xchg, m->sk_mem };
+                     m->b.rcnt, m->b.xchg, m->sk_mem, m->p6b.lut_gu, m->p6b.lut_d, m->p6b.q_gu,
+                     m->p6b.q_d, m->p6b.s_gu, m->p6b.s_d, m->p6b.gu, m->p6b.h, m->p6b.down };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0]) {
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -189,6 +199,9 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
                              cfg->topk_group < 1 || cfg->topk_group > cfg->n_group ||
                              cfg->topk_group * (cfg->n_experts / cfg->n_group) < cfg->top_k))
         return WASTE_HIP_EINVAL;
+    if (cfg->index_bits != 0 && cfg->index_bits != 8 && cfg->index_bits != 6) return WASTE_HIP_EINVAL;
+    if (cfg->index_bits == 6 && cfg->p6_order != WASTE_HIP_ORDER_PORTABLE && cfg->p6_order != WASTE_HIP_ORDER_FMA)
+        return WASTE_HIP_EINVAL;
     if (!waste_hip_device_name()) return WASTE_HIP_ENODEV;
     waste_hip_moe *m = (waste_hip_moe *)calloc(1, sizeof *m);
     if (!m) return WASTE_HIP_ENOMEM;
@@ -196,9 +209,14 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     m->E = cfg->n_experts; m->K = cfg->top_k; m->H = cfg->hidden; m->I = cfg->moe_inter;
     m->SI = cfg->moe_inter * (cfg->n_shared > 0 ? cfg->n_shared : 1);
     m->T = cfg->max_tokens;
+    m->p6 = cfg->index_bits == 6;
+    m->stages = m->p6 ? 4 : 3;
+    m->entries = m->p6 ? 64 : 256;
+    m->nbk = 3 * m->stages;
     {
+        /* VQ4P: the decode kernels take every T (no matrix-core path) */
         const int pm = cfg->prefill_min_tokens > 0 ? cfg->prefill_min_tokens : 32;
-        m->Td = m->T < pm ? m->T : pm;
+        m->Td = m->T < pm || m->p6 ? m->T : pm;
     }
     m->nv_gu = m->H / 8; m->nv_d = m->I / 8;
     m->nch_gu = whip_vq_chunks(m->nv_gu, m->I);
@@ -227,10 +245,24 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->b.pair_exp, (size_t)P * 4);
     rc |= dmalloc((void **)&m->b.pair_w, (size_t)P * 4);
     rc |= dmalloc((void **)&m->b.tok_pairs, (size_t)P * 4);
-    /* + 64 floats: the apply kernels' sink for rows past a split's end */
-    rc |= dmalloc((void **)&m->b.part_gu, ((size_t)Pd * 2 * m->nch_gu * m->I + 64) * 4);
-    rc |= dmalloc((void **)&m->b.h, (size_t)Pd * m->I * 4);
-    rc |= dmalloc((void **)&m->b.part_d, ((size_t)Pd * m->nch_d * m->H + 64) * 4);
+    if (m->p6) {
+        const size_t tg = (size_t)m->nv_gu * 256, td = (size_t)m->nv_d * 256;
+        const size_t bg = (size_t)(m->nv_gu + 31) / 32, bd = (size_t)(m->nv_d + 31) / 32;
+        rc |= dmalloc((void **)&m->p6b.lut_gu, (size_t)m->T * 2 * tg * 4);
+        rc |= dmalloc((void **)&m->p6b.q_gu, (size_t)m->T * 2 * tg);
+        rc |= dmalloc((void **)&m->p6b.s_gu, (size_t)m->T * 2 * bg * 4);
+        rc |= dmalloc((void **)&m->p6b.lut_d, (size_t)P * td * 4);
+        rc |= dmalloc((void **)&m->p6b.q_d, (size_t)P * td);
+        rc |= dmalloc((void **)&m->p6b.s_d, (size_t)P * bd * 4);
+        rc |= dmalloc((void **)&m->p6b.gu, (size_t)P * 2 * m->I * 4);
+        rc |= dmalloc((void **)&m->p6b.h, (size_t)P * m->I * 4);
+        rc |= dmalloc((void **)&m->p6b.down, (size_t)P * m->H * 4);
+    } else {
+        /* + 64 floats: the apply kernels' sink for rows past a split's end */
+        rc |= dmalloc((void **)&m->b.part_gu, ((size_t)Pd * 2 * m->nch_gu * m->I + 64) * 4);
+        rc |= dmalloc((void **)&m->b.h, (size_t)Pd * m->I * 4);
+        rc |= dmalloc((void **)&m->b.part_d, ((size_t)Pd * m->nch_d * m->H + 64) * 4);
+    }
     rc |= dmalloc((void **)&m->err, 64);
     rc |= dmalloc((void **)&m->plogits, (size_t)m->E * 4);
     rc |= dmalloc((void **)&m->pw, 64 * 4);
@@ -354,17 +386,20 @@ int waste_hip_moe_set_codebooks(waste_hip_moe *m, const uint16_t *f16, int n_boo
 
 int waste_hip_moe_set_codebooks_at(waste_hip_moe *m, const uint16_t *f16, int first, int n_books)
 {
-    if (!m || !f16 || n_books < 9 || first < 0 || first > 65535 || n_books > 65536 + 9) return WASTE_HIP_EINVAL;
-    if (m->cb >= 0 && (m->cb < first || m->cb + 9 > first + n_books)) return WASTE_HIP_ERECORD;
-    const size_t per = 256 * 8;
+    if (!m || !f16 || n_books < m->nbk || first < 0 || first > 65535 || n_books > 65536 + m->nbk)
+        return WASTE_HIP_EINVAL;
+    if (m->cb >= 0 && (m->cb < first || m->cb + m->nbk > first + n_books)) return WASTE_HIP_ERECORD;
+    /* books of the layer's geometry: [n_books][entries][8] */
+    const int en = m->entries;
+    const size_t per = (size_t)en * 8;
     float *b = (float *)malloc((size_t)n_books * per * 4);
     float *bt = (float *)malloc((size_t)n_books * per * 4);
     if (!b || !bt) { free(b); free(bt); return WASTE_HIP_ENOMEM; }
     for (size_t i = 0; i < (size_t)n_books * per; i++) b[i] = f16_book(f16[i]);
     for (int k = 0; k < n_books; k++)
-        for (int c = 0; c < 256; c++)
+        for (int c = 0; c < en; c++)
             for (int d = 0; d < 8; d++)
-                bt[(size_t)k * per + (size_t)d * 256 + c] = b[(size_t)k * per + (size_t)c * 8 + d];
+                bt[(size_t)k * per + (size_t)d * en + c] = b[(size_t)k * per + (size_t)c * 8 + d];
     /* the fp16 copy the matrix-core path decodes from: the loader's flush of
      * subnormals to a signed zero, the rest bit for bit */
     uint16_t *h16 = (uint16_t *)malloc((size_t)n_books * per * 2);
@@ -399,8 +434,8 @@ static int check_record(const waste_hip_moe *m, int expert, const uint8_t *rec, 
     if (h.magic != WASTE_MAGIC_EXPERT) return WASTE_HIP_ERECORD;
     if (h.layer != (uint16_t)m->c.layer || h.expert_id != (uint16_t)expert) return WASTE_HIP_ERECORD;
     if ((size_t)h.rec_4k_blocks * WASTE_ALIGN != rec_bytes) return WASTE_HIP_ERECORD;
-    if (h.fmt != WQ_VQ3R || h.lowrank_id != 0) return WASTE_HIP_ERECORD;
-    if (m->n_books && (h.codebook_id < m->book0 || (long)h.codebook_id + 9L > (long)m->book0 + m->n_books))
+    if (h.fmt != (m->p6 ? WQ_VQ4P : WQ_VQ3R) || h.lowrank_id != 0) return WASTE_HIP_ERECORD;
+    if (m->n_books && (h.codebook_id < m->book0 || (long)h.codebook_id + m->nbk > (long)m->book0 + m->n_books))
         return WASTE_HIP_ERECORD;
     if (!(h.gate_off == 48 && h.gate_off < h.up_off && h.up_off < h.down_off &&
           h.down_off < h.chan_corr_off && h.chan_corr_off <= rec_bytes))
@@ -741,12 +776,74 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
     MARK(7);
     return prof_end(m);
 }
+
+/* VQ4P experts (index_bits 6), moe_layer's order at T = 1 and moe_chunk's
+ * above (src/model.c:5876-5910, 7203-7251), on the routing and pair lists
+ * route() left: each token's gate and up tables (fp32, then int8 with one
+ * scale per 32 positions: vq_build_lut), every pair's gate and up rows
+ * through them (vq_rows_p6), SwiGLU, the pair's down table from its
+ * SwiGLU output and its down rows, then the combine and the shared expert
+ * as for VQ3R.  The tables and rows follow the engine's arithmetic in the
+ * layer's p6_order, so each pair's rows are the engine's bit for bit. */
+static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
+{
+    const int K = m->K, H = m->H, I = m->I, P = T * K, fma = m->c.p6_order == WASTE_HIP_ORDER_FMA;
+    const int cb = m->cb - m->book0;
+    MARK(2);
+    CK((hipError_t)whip_p6_lutb(x, x_bf16, H, T, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.lut_gu, s));
+    CK((hipError_t)whip_vq_quant_lut_n(m->p6b.lut_gu, m->nv_gu, 4, 64, 2 * T, m->p6b.q_gu, m->p6b.s_gu, s));
+    const uint32_t gu_idx[2] = { m->off_gate, m->off_up };
+    const uint32_t gu_sc[2] = { m->off_sc, m->off_sc + 2u * (uint32_t)I };
+    CK((hipError_t)whip_p6_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 2, gu_idx, gu_sc, I, m->nv_gu,
+                                      m->p6b.q_gu, m->p6b.s_gu, 1, fma, m->p6b.gu, m->err, s));
+    MARK(3);
+    CK((hipError_t)whip_p6_act(m->p6b.gu, P, I, m->p6b.h, s));
+    MARK(4);
+    CK((hipError_t)whip_p6_lutb(m->p6b.h, 0, I, P, 1, m->d_booksT, cb + 2 * m->stages, m->nv_d, fma,
+                                m->p6b.lut_d, s));
+    CK((hipError_t)whip_vq_quant_lut_n(m->p6b.lut_d, m->nv_d, 4, 64, P, m->p6b.q_d, m->p6b.s_d, s));
+    const uint32_t d_idx[1] = { m->off_down }, d_sc[1] = { m->off_sc + 4u * (uint32_t)I };
+    CK((hipError_t)whip_p6_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, d_sc, H, m->nv_d,
+                                      m->p6b.q_d, m->p6b.s_d, 0, fma, m->p6b.down, m->err, s));
+    MARK(5);
+    /* the combine: each pair's rows are already scaled, one chunk each */
+    if (m->sh_in_combine) {
+        MARK(6);
+        const int rc = whip_combine_sh(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->p6b.down,
+                                       1, H, 0, T > 1, &m->sh[2], m->b.h_sh, y, s);
+        if (rc == 0) {
+            MARK(7);
+            return prof_end(m);
+        }
+        if (rc != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
+        CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->b.h_sh, m->SI, T, m->b.sh_out, NULL, H, s));
+    }
+    const float *shp = m->has_shared ? m->b.sh_out : NULL;
+    int sh_n = 1;
+    if (m->has_shared && !m->sh_done && !m->sh_in_combine) {
+        if (T > 1 && m->b.sk_part) {
+            whip_sk_job j;
+            j.A = m->sh[2]; j.x = m->b.h_sh; j.x_ld = m->SI; j.x_bf16 = 0; j.part = m->b.sk_part;
+            j.nsl = m->sk_d;
+            CK((hipError_t)whip_sk_run(&j, 1, T, s));
+            shp = m->b.sk_part;
+            sh_n = m->sk_d;
+        } else {
+            CK((hipError_t)whip_gemv(&m->sh[2], NULL, m->b.h_sh, m->SI, T, m->b.sh_out, NULL, H, s));
+        }
+    }
+    MARK(6);
+    CK((hipError_t)whip_combine(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->p6b.down, 1, H,
+                                0, T > 1, shp, sh_n, (size_t)T * H, y, s));
+    MARK(7);
+    return prof_end(m);
+}
 #undef MARK
 
 static int ready(const waste_hip_moe *m, const void *x, int T)
 {
     if (!m || !x || T <= 0 || T > m->T) return WASTE_HIP_EINVAL;
-    if (!m->has_router || !m->d_booksT || m->n_books < 9) return WASTE_HIP_EINVAL;
+    if (!m->has_router || !m->d_booksT || m->n_books < m->nbk) return WASTE_HIP_EINVAL;
     return 0;
 }
 
@@ -823,6 +920,7 @@ int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     if (!y || T != m->routed_T) return WASTE_HIP_EINVAL;
     if (!books_ok(m)) return WASTE_HIP_EINVAL;
     hipStream_t s = (hipStream_t)stream;
+    if (m->p6) return experts_p6(m, x, x_bf16, T, y, s);
     if (T <= m->Td) return experts_few(m, x, x_bf16, T, y, s);
     const int r = experts_many(m, x, x_bf16, T, y, s);
     return r ? r : range_fallback(m, x, x_bf16, T, y, s);
@@ -895,7 +993,7 @@ int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, in
 {
     int rc = ready(m, x, T);
     if (rc) return rc;
-    if (!y || !books_ok(m)) return WASTE_HIP_EINVAL;
+    if (!y || !books_ok(m) || m->p6) return WASTE_HIP_EINVAL;   /* VQ4P: forward() only */
     if (T > m->Td || static_layout(m, T, NULL, NULL) > WHIP_SCRATCH_BYTES)
         return WASTE_HIP_ESCRATCH;
     hipStream_t s = (hipStream_t)stream;
@@ -933,7 +1031,7 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *c
     }
     if (codebook_id >= 0) {
         if (m->cb >= 0 && m->cb != codebook_id) return WASTE_HIP_ERECORD;
-        if (m->n_books && (codebook_id < m->book0 || codebook_id + 9 > m->book0 + m->n_books))
+        if (m->n_books && (codebook_id < m->book0 || codebook_id + m->nbk > m->book0 + m->n_books))
             return WASTE_HIP_ERECORD;
         m->cb = codebook_id;
     }
@@ -943,7 +1041,9 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *c
     a.off_up = m->off_up; a.off_down = m->off_down; a.off_sc = m->off_sc;
     a.cb = m->cb;
     a.book0 = m->n_books > 0 ? m->book0 : 0;
-    a.n_books = m->n_books > 0 ? m->book0 + m->n_books : 65536 + 9;
+    a.n_books = m->n_books > 0 ? m->book0 + m->n_books : 65536 + m->nbk;
+    a.fmt = m->p6 ? WQ_VQ4P : WQ_VQ3R;
+    a.nbk = (uint32_t)m->nbk;
     CK((hipError_t)whip_bind(m->d_recs, &a, m->err, (hipStream_t)stream));
     m->pair_rec_ok = 0;
     for (int i = 0; i < n; i++) {
@@ -1104,7 +1204,7 @@ size_t waste_hip_moe_bytes(const waste_hip_moe *m, int T, int n_distinct)
 int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W, void *stream)
 {
     if (!m || expert < 0 || expert >= m->E || kind < 0 || kind > 2 || !W || !m->d_books ||
-        !books_ok(m))
+        !books_ok(m) || m->p6)
         return WASTE_HIP_EINVAL;
     const uint8_t *rec = m->h_recs[expert];
     if (!rec) return WASTE_HIP_EUNBOUND;
