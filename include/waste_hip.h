@@ -443,13 +443,14 @@ int  waste_hip_container_tensor(waste_hip_container *c, const char *name, waste_
  * <prefix>model.layers.<L>.block_sparse_moe.gate.weight and its
  * e_score_correction_bias (when present), the shared expert
  * (.shared_experts.{gate,up,down}_proj.weight, width moe_inter times
- * num_shared_experts or 1), the layer's nine codebooks.  Flags:
+ * num_shared_experts or 1), the layer's codebooks (nine for VQ3R, twelve
+ * for VQ4P, whose layer then follows this host's p6 order).  Flags:
  * WASTE_HIP_CT_RECORDS copies every record of the bank into the layer's
  * slab (otherwise records are bound later, e.g. from an expert cache);
  * WASTE_HIP_CT_GROUP_LIMIT routes with the config's n_group/topk_group
  * (the engine's moe_layer has no group limit, so parity with it wants the
- * flag off).  VQ3R containers without a latent projection only
- * (WASTE_HIP_EINVAL otherwise).  Replaces: the tensor lookups of
+ * flag off).  VQ3R and VQ4P containers without a latent projection
+ * only (WASTE_HIP_EINVAL otherwise).  Replaces: the tensor lookups of
  * moe_layer, src/model.c:5494-5497, 5932-5936. */
 #define WASTE_HIP_CT_RECORDS     1
 #define WASTE_HIP_CT_GROUP_LIMIT 2

@@ -11,9 +11,12 @@ src/model.c:1366-1395); codebooks.bin as 16-byte headers each followed by
 256 x 8 fp16 (src/waste_format.h:139-150); experts-L<n>.bin as the layer's
 4 KiB records in expert order (src/waste_format.h:98-132).
 
-Every MoE layer takes nine books of its own, codebook_base = 9 x its rank
-among the MoE layers, so each records.Layer must be built with that
-cb_base and with layer = its index.
+Every MoE layer takes 3 x stages books of its own (nine for VQ3R, twelve
+for VQ4P), codebook_base = that count x its rank among the MoE layers, so
+each records.Layer must be built with that cb_base and with layer = its
+index.  The layers' format (VQ3R, or VQ4P: index_bits 6, four stages of 64
+entries) is the container's expert_quant, as tools/convert.py:2482-2488
+writes it.
 """
 import json
 import os
@@ -80,9 +83,12 @@ def build(layers, *, n_layers, first_dense, prefix="", text_config=False, vocab=
     trunk = _Trunk()
     trunk.f32(f"{prefix}model.norm.weight", np.ones(L0.H, np.float32))
     files, bank_index, books = {}, {}, []
+    st, en, ib = getattr(L0, "stages", STAGES), getattr(L0, "entries", ENTRIES), getattr(L0, "index_bits", 8)
+    nbk = 3 * st
     for rank, Lyr in enumerate(layers):
         L = first_dense + rank
-        assert Lyr.layer == L and Lyr.cb_base == 9 * rank, "build each layer with its index and cb_base"
+        assert Lyr.layer == L and Lyr.cb_base == nbk * rank, "build each layer with its index and cb_base"
+        assert getattr(Lyr, "index_bits", 8) == ib, "one expert format per container"
         n = moe_names(prefix, L)
         trunk.tensor(n["router"], Lyr.router)
         if Lyr.bias is not None:
@@ -93,10 +99,12 @@ def build(layers, *, n_layers, first_dense, prefix="", text_config=False, vocab=
         files[name] = Lyr.bank()
         bank_index[str(L)] = {"file": name, "experts": Lyr.E, "bytes": len(files[name]),
                               "codebook_base": Lyr.cb_base}
-        books.append(Lyr.books_f16[Lyr.cb_base:Lyr.cb_base + 9])
+        books.append(Lyr.books_f16[Lyr.cb_base:Lyr.cb_base + nbk])
     cb = bytearray()
     for cid, book in enumerate(np.concatenate(books)):
-        cb += struct.pack("<IHBBII", MAGIC_CODEBOOK, cid & 0xFFFF, 4, VEC_DIM, ENTRIES, 0)
+        # the converter writes FMT_VQ3R in every codebook header
+        # (tools/convert.py:1298-1302), whatever the layers' format
+        cb += struct.pack("<IHBBII", MAGIC_CODEBOOK, cid & 0xFFFF, 4, VEC_DIM, en, 0)
         cb += np.ascontiguousarray(book, np.uint16).tobytes()
     files["codebooks.bin"] = bytes(cb)
     files["trunk.bin"] = bytes(trunk.buf)
@@ -105,6 +113,9 @@ def build(layers, *, n_layers, first_dense, prefix="", text_config=False, vocab=
                 "expert_quant": {"fmt": "VQ3R", "stages": STAGES, "vec_dim": VEC_DIM,
                                  "entries": ENTRIES, "index_block": 64, "bits_per_weight": STAGES},
                 "layers": bank_index, "trunk": trunk.index}
+    if ib == 6:
+        manifest["expert_quant"] = {"fmt": "VQ4P", "stages": st, "vec_dim": VEC_DIM, "entries": en,
+                                    "index_block": 64, "index_bits": 6, "bits_per_weight": st * 6 / VEC_DIM}
     if text_config and prefix == "language_model.":
         manifest["tensor_prefix"] = ""            # the reader supplies it for a nested config
     return manifest, files

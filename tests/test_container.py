@@ -308,6 +308,33 @@ def test_vq2r_record_accepted_by_the_reader(tmp_path, fixture):
     assert warp_amd.Container(make(tmp_path, manifest, f)).read_expert(1, 0)[0] == 0
 
 
+def test_vq4p_round_trip(tmp_path):
+    """A VQ4P container (expert_quant VQ4P, index_bits 6: four stages of 64
+    entries, twelve books a layer): its config, books and records read back
+    as written, and a VQ3R record in it is refused (model.c:3660-3666)."""
+    Ls = [Layer(H, I, E, K, seed=120 + r, cb_base=12 * r, layer=1 + r, score_func=1, n_shared=1,
+                shared_fmt=FMT_Q8G, index_bits=6) for r in range(2)]
+    manifest, files = build(Ls, n_layers=3, first_dense=1)
+    c = warp_amd.Container(make(tmp_path, manifest, files), verify=True)
+    cfg = c.config()
+    assert (cfg["stages"], cfg["vec_dim"], cfg["entries"], cfg["index_bits"]) == (4, 8, 64, 6)
+    assert cfg["n_books"] == 24
+    books = c.codebooks()
+    assert books.shape == (24, 64, 8)
+    for r, Lyr in enumerate(Ls):
+        n, cb, rb = c.bank(1 + r)
+        assert (n, cb, rb) == (E, 12 * r, Lyr.rec_bytes)
+        assert np.array_equal(books[cb:cb + 12], Lyr.books_f16[cb:cb + 12])
+        for e in range(E):
+            rc, rec = c.read_expert(1 + r, e)
+            assert rc == 0 and rec.tobytes() == Lyr.records[e]
+    bank = bytearray(files["experts-L1.bin"])
+    bank[0:Ls[0].rec_bytes] = _patch(Ls[0].records[0], 8, "<B", 4)
+    f = dict(files)
+    f["experts-L1.bin"] = bytes(bank)
+    assert warp_amd.Container(make(tmp_path, manifest, f, "c2")).read_expert(1, 0)[0] == warp_amd.ERECORD
+
+
 def test_swapped_records(tmp_path, fixture):
     """A bank whose records are out of order is caught by the identity
     check, never served as another expert."""

@@ -148,3 +148,34 @@ def test_vq4p_records_checked(orc):
     assert m6.status(s) == warp_amd.ERECORD
     m6.close()
     m8.close()
+
+
+def test_vq4p_container_layer(orc, tmp_path):
+    """Two VQ4P layers (with a shared expert, which the engine's layer
+    always reads) written as a container (expert_quant VQ4P, index_bits 6,
+    twelve books a layer) and opened with
+    waste_hip_container_moe: outputs bit-identical to the layers built
+    directly from the same arrays."""
+    say("test_vq4p_container_layer")
+    from container_writer import build, write
+    kw, _ = CASES["p6_softmax"]
+    Ls = [Layer(kw["H"], kw["I"], kw["E"], kw["K"], score_func=1, seed=70 + r, cb_base=12 * r, layer=1 + r,
+                n_shared=1, shared_fmt=FMT_Q4G, index_bits=6) for r in range(2)]
+    manifest, files = build(Ls, n_layers=3, first_dense=1)
+    path = write(str(tmp_path / "ctr"), manifest, files)
+    ct = warp_amd.Container(path, verify=True)
+    assert ct.config()["index_bits"] == 6
+    order = warp_amd.lib().waste_hip_vq_p6_order()
+    for r, L in enumerate(Ls):
+        mc = ct.moe(1 + r, max_tokens=4)
+        md = gpu_layer(L, max_tokens=4, p6_order=order)
+        for T in (1, 4):
+            X = inputs(L, T, 40 + T, False)
+            a = run_forward(torch, mc, L, X)
+            b = run_forward(torch, md, L, X)
+            assert a[0] == 0 and b[0] == 0
+            assert np.array_equal(a[2], b[2])
+            assert np.array_equal(bits(a[1]), bits(b[1])), (r, T)
+        mc.close()
+        md.close()
+    ct.close()
