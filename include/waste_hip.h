@@ -136,10 +136,14 @@ typedef struct {
                             (four stages of 64 entries, twelve books a
                             record), every T on the decode path through
                             the engine's int8 tables (vq_rows_p6)         */
-    int p6_order;        /* VQ4P: WASTE_HIP_ORDER_PORTABLE or _FMA, the
-                            arithmetic of the engine's table build and
-                            fold on a host without / with its AVX-512
-                            kernels (waste_hip_vq_p6_order(): this host's) */
+    int p6_order;        /* VQ4P and VQ2R: WASTE_HIP_ORDER_PORTABLE or _FMA,
+                            the arithmetic of the engine's table build
+                            (and VQ4P's fold) on a host without / with its
+                            AVX-512 kernels (waste_hip_vq_p6_order(): this
+                            host's)                                       */
+    int stages;          /* index_bits 8: 3 (0) VQ3R; 2 VQ2R (two stages of
+                            256 entries, six books a record), every T on
+                            the decode path in the engine's exact order  */
 } waste_hip_moe_cfg;
 
 /* A trunk tensor as the engine holds it (waste_tensor, src/model.h:32-50):
@@ -213,7 +217,7 @@ int waste_hip_moe_forward(waste_hip_moe *m, const void *x, int x_bf16, int T,
  * that overlap on one GPU (other streams, other threads) race; calls
  * ordered on one stream do not.  ids/w/logits as in forward(); NULL
  * leaves them in the area, good until the next call on the GPU.  VQ3R
- * layers only (WASTE_HIP_EINVAL for a VQ4P one). */
+ * layers only (WASTE_HIP_EINVAL for a VQ4P or VQ2R one). */
 int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, int T,
                                  float *y, int32_t *ids, float *w, float *logits,
                                  void *stream);
@@ -444,13 +448,14 @@ int  waste_hip_container_tensor(waste_hip_container *c, const char *name, waste_
  * e_score_correction_bias (when present), the shared expert
  * (.shared_experts.{gate,up,down}_proj.weight, width moe_inter times
  * num_shared_experts or 1), the layer's codebooks (nine for VQ3R, twelve
- * for VQ4P, whose layer then follows this host's p6 order).  Flags:
+ * for VQ4P, six for VQ2R; the last two then follow this host's p6 order).
+ * Flags:
  * WASTE_HIP_CT_RECORDS copies every record of the bank into the layer's
  * slab (otherwise records are bound later, e.g. from an expert cache);
  * WASTE_HIP_CT_GROUP_LIMIT routes with the config's n_group/topk_group
  * (the engine's moe_layer has no group limit, so parity with it wants the
- * flag off).  VQ3R and VQ4P containers without a latent projection
- * only (WASTE_HIP_EINVAL otherwise).  Replaces: the tensor lookups of
+ * flag off).  VQ3R, VQ4P and VQ2R containers without a latent
+ * projection only (WASTE_HIP_EINVAL otherwise).  Replaces: the tensor lookups of
  * moe_layer, src/model.c:5494-5497, 5932-5936. */
 #define WASTE_HIP_CT_RECORDS     1
 #define WASTE_HIP_CT_GROUP_LIMIT 2

@@ -21,6 +21,7 @@
 #define WQ_Q3G 7
 #define WQ_VQ3R 4
 #define WQ_VQ4P 8
+#define WQ_VQ2R 5
 #define MAGIC_EXPERT 0x50584557u
 
 /* ---- expf ----------------------------------------------------------------
@@ -554,9 +555,10 @@ int orc_record_check(const uint8_t *rec, size_t rec_bytes, int layer,
     if (magic != MAGIC_EXPERT) return 1;
     if (lay != (uint16_t)layer || eid != (uint16_t)expert) return 1;
     if ((size_t)rec4k * 4096u != rec_bytes) return 1;
-    /* index_bits 6 (four stages of 64 entries) is VQ4P, else VQ3R
-     * (src/model.c:3660-3666) */
-    if (fmt != (stages == 4 ? WQ_VQ4P : WQ_VQ3R)) return 1;
+    /* index_bits 6 (four stages of 64 entries) is VQ4P; one byte a stage
+     * is VQ3R, or VQ2R in a two-stage container (src/model.c:3660-3666,
+     * docs/FORMAT.md:180) */
+    if (fmt != (stages == 4 ? WQ_VQ4P : stages == 2 ? WQ_VQ2R : WQ_VQ3R)) return 1;
     if (lr != 0) return 1;
     if ((long)cbid + 3L * stages > n_books) return 1;
     if (!(go == 48 && go < uo && uo < dof && dof < co && co <= rec_bytes)) return 1;

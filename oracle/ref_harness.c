@@ -143,12 +143,14 @@ static void put_tensor(waste_tensor *t, const char *name, const ref_tensor *s)
  * table, one expert bank served from a memfd through the engine's own
  * bank_fetch/record_check, and the scratch buffers waste_model_load would
  * size.  NULL on failure. */
-/* The container geometry ref_model builds: 8 (VQ3R, three stages of 256
- * entries) or 6 (VQ4P, four stages of 64, with the int8 table shadows
- * waste_model_load allocates for it, src/model.c:3340-3356). */
-static int ref_ib = 8;
+/* The container geometry ref_model builds: index_bits 8 with three stages
+ * of 256 entries (VQ3R) or two (VQ2R), or 6 (VQ4P, four stages of 64, with
+ * the int8 table shadows waste_model_load allocates for it,
+ * src/model.c:3340-3356). */
+static int ref_ib = 8, ref_st = 3;
 
-void ref_set_index_bits(int ib) { ref_ib = ib == 6 ? 6 : 8; }
+void ref_set_index_bits(int ib) { ref_ib = ib == 6 ? 6 : 8; ref_st = ib == 6 ? 4 : 3; }
+void ref_set_stages(int st) { if (ref_ib == 8 && (st == 2 || st == 3)) ref_st = st; }
 
 static waste_model *ref_model(int hidden, int n_experts, int top_k, int moe_inter, int n_shared,
                               int score_func, int renorm, float routed_scale,
@@ -185,7 +187,7 @@ static waste_model *ref_model(int hidden, int n_experts, int top_k, int moe_inte
     m->codebooksT = (float *)booksT;
     m->n_books = n_books; m->vec_dim = 8;
     m->index_bits = ref_ib;
-    m->stages = ref_ib == 6 ? 4 : 3;
+    m->stages = ref_st;
     m->cb_entries = ref_ib == 6 ? 64 : 256;
     m->expert_m[0] = m->expert_m[1] = I; m->expert_m[2] = H;
     m->expert_n[0] = m->expert_n[1] = H; m->expert_n[2] = I;

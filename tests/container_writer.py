@@ -12,10 +12,10 @@ src/model.c:1366-1395); codebooks.bin as 16-byte headers each followed by
 4 KiB records in expert order (src/waste_format.h:98-132).
 
 Every MoE layer takes 3 x stages books of its own (nine for VQ3R, twelve
-for VQ4P), codebook_base = that count x its rank among the MoE layers, so
+for VQ4P, six for VQ2R), codebook_base = that count x its rank among the MoE layers, so
 each records.Layer must be built with that cb_base and with layer = its
-index.  The layers' format (VQ3R, or VQ4P: index_bits 6, four stages of 64
-entries) is the container's expert_quant, as tools/convert.py:2482-2488
+index.  The layers' format (VQ3R; VQ2R: two stages; or VQ4P: index_bits 6,
+four stages of 64 entries) is the container's expert_quant, as tools/convert.py:2482-2488
 writes it.
 """
 import json
@@ -116,6 +116,9 @@ def build(layers, *, n_layers, first_dense, prefix="", text_config=False, vocab=
     if ib == 6:
         manifest["expert_quant"] = {"fmt": "VQ4P", "stages": st, "vec_dim": VEC_DIM, "entries": en,
                                     "index_block": 64, "index_bits": 6, "bits_per_weight": st * 6 / VEC_DIM}
+    elif st == 2:
+        manifest["expert_quant"] = {"fmt": "VQ2R", "stages": 2, "vec_dim": VEC_DIM, "entries": en,
+                                    "index_block": 64, "index_bits": 8, "bits_per_weight": 2}
     if text_config and prefix == "language_model.":
         manifest["tensor_prefix"] = ""            # the reader supplies it for a nested config
     return manifest, files

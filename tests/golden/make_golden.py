@@ -25,8 +25,9 @@ vq4p.npz (VQ4P, 6-bit codes through the engine's int8 LUT):
   qlut, qq, qsc vq_quant_lut of a planted table (an all-zero block, exact
                 halves under a unit inverse, a lone extreme)
 
-vq4p_layer.npz (whole VQ4P layers: moe_layer and moe_chunk with index_bits 6,
-the tables quantised to int8 and the rows through vq_rows_p6):
+vq_formats.npz (whole layers in the other expert formats: moe_layer and
+moe_chunk with index_bits 6 (VQ4P: the tables quantised to int8 and the rows
+through vq_rows_p6) and with two stages of 256 entries (VQ2R)):
   {case}_digest, {case}_layer_out{o}, {case}_layer_ids{o},
   {case}_chunk_out{o}, {case}_chunk_ids{o}, {case}_chunk_w{o}
 
@@ -34,7 +35,7 @@ q3g.npz (Q3G trunk rows, 3-bit codes plus a guard byte, tools/convert.py:854-892
   rows{o}_{cols}  mvq_rows of order o on the seeded rows of each width
   digest_{cols}   sha256 of the case's packed rows, scales and x
 
-  python tests/golden/make_golden.py [scalars|vq4p|vq4p_layer|q3g]
+  python tests/golden/make_golden.py [scalars|vq4p|vq_formats|q3g]
 """
 import hashlib
 import os
@@ -91,8 +92,8 @@ def main():
     if sys.argv[1:] == ["q3g"]:                     # only q3g.npz
         write_q3g(ref)
         return
-    if sys.argv[1:] == ["vq4p_layer"]:              # only vq4p_layer.npz
-        write_vq4p_layer(orc, ref)
+    if sys.argv[1:] == ["vq_formats"]:              # only vq_formats.npz
+        write_vq_formats(orc, ref)
         return
     if ref.isa != 2:
         print("warning: this host does not run the reference's AVX-512 kernels; order 1 = portable")
@@ -124,28 +125,31 @@ def main():
 
     write_scalars(ref)
     write_vq4p(orc, ref)
-    write_vq4p_layer(orc, ref)
+    write_vq_formats(orc, ref)
     write_q3g(ref)
 
 
-# VQ4P layers: name -> (H, I, E, K, kwargs, T)
-VQ4P_CASES = {
+# VQ4P and VQ2R layers: name -> (H, I, E, K, kwargs, T)
+FORMAT_CASES = {
     "p6_softmax": (256, 128, 16, 4, dict(score_func=1, seed=41, index_bits=6), 3),
     "p6_sigmoid_q8g": (256, 128, 16, 4, dict(score_func=0, renorm=1, routed_scale=2.5, bias=True,
                                              n_shared=1, shared_fmt=FMT_Q8G, seed=42, index_bits=6), 4),
+    "r2_softmax": (256, 128, 16, 4, dict(score_func=1, seed=51, stages=2), 3),
+    "r2_sigmoid_q8g": (256, 128, 16, 4, dict(score_func=0, renorm=1, routed_scale=2.5, bias=True,
+                                             n_shared=1, shared_fmt=FMT_Q8G, seed=52, stages=2), 4),
 }
 
 
-def vq4p_case(name):
-    H, I, E, K, kw, T = VQ4P_CASES[name]
+def format_case(name):
+    H, I, E, K, kw, T = FORMAT_CASES[name]
     L = Layer(H, I, E, K, **kw)
     return L, L.inputs(T, seed=kw["seed"] + 100)
 
 
-def write_vq4p_layer(orc, ref):
+def write_vq_formats(orc, ref):
     out = {}
-    for name in VQ4P_CASES:
-        L, X = vq4p_case(name)
+    for name in FORMAT_CASES:
+        L, X = format_case(name)
         _, bT = orc.books(L.books_f16)
         out[f"{name}_digest"] = np.array(input_digest(L, X))
         for o in (0, 1):
@@ -158,8 +162,8 @@ def write_vq4p_layer(orc, ref):
             out[f"{name}_chunk_out{o}"], out[f"{name}_chunk_ids{o}"], out[f"{name}_chunk_w{o}"] = co, cr, cw
     ref.lib.ref_set_index_bits(8)
     out["isa"] = np.array(ref.isa)
-    np.savez_compressed(os.path.join(HERE, "vq4p_layer.npz"), **out)
-    print("vq4p_layer written")
+    np.savez_compressed(os.path.join(HERE, "vq_formats.npz"), **out)
+    print("vq_formats written")
 
 
 Q3G_WIDTHS = (1024, 1000, 640)

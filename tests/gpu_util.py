@@ -25,7 +25,7 @@ def gpu_layer(L, max_tokens=1, verify=0, prefill_min=0, records=True, p6_order=N
                           topk_group=L.topk_group, layer=getattr(L, "layer", 0),
                           max_tokens=max_tokens, verify_records=verify,
                           prefill_min_tokens=prefill_min, index_bits=getattr(L, "index_bits", 8),
-                          p6_order=p6_order)
+                          p6_order=p6_order, stages=getattr(L, "stages", 0))
     m.set_codebooks(L.books_f16)
     m.set_router(L.router, L.bias)
     if L.n_shared:

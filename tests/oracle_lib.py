@@ -308,6 +308,7 @@ class Ref:
         _sig(L, "ref_init", C.c_int, [])
         _sig(L, "ref_set_order", None, [C.c_int])
         _sig(L, "ref_set_index_bits", None, [C.c_int])
+        _sig(L, "ref_set_stages", None, [C.c_int])
         _sig(L, "ref_vq_rows", None, [fp, u8p, u16p, fp, C.c_int, C.c_int, C.c_int, C.c_int])
         _sig(L, "ref_lutb", None, [fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int])
         _sig(L, "ref_vq_quant_lut", None, [fp, C.c_int, C.c_int, C.c_int, i8p, fp])
@@ -431,6 +432,7 @@ class Ref:
         T = X.shape[0]
         rt = self._rt
         self.lib.ref_set_index_bits(getattr(L, "index_bits", 8))
+        self.lib.ref_set_stages(getattr(L, "stages", 3))
         bank = np.frombuffer(L.bank(), np.uint8)
         out = np.zeros((T, L.H), np.float32)
         route = np.zeros((T, L.K), np.int32)

@@ -16,7 +16,7 @@ import numpy as np
 
 MAGIC_EXPERT = 0x50584557
 MAGIC_CODEBOOK = 0x4B424357
-FMT_F32, FMT_Q8G, FMT_Q4G, FMT_VQ3R, FMT_VQ4P = 0, 2, 3, 4, 8
+FMT_F32, FMT_Q8G, FMT_Q4G, FMT_VQ3R, FMT_VQ2R, FMT_VQ4P = 0, 2, 3, 4, 5, 8
 STAGES, ENTRIES, VEC_DIM, BLOCK = 3, 256, 8, 64
 
 
@@ -79,13 +79,14 @@ from warp_amd.synth import Tensor, f16_bits, quant_q4g, quant_q8g  # noqa: E402,
 
 class Layer:
     """One synthetic MoE layer.  index_bits 8: VQ3R experts (three stages
-    of 256 entries); 6: VQ4P (four stages of 64, the codes packed in three
-    bytes); idx then holds the unpacked codes [M][N/8][4]."""
+    of 256 entries), or VQ2R with stages=2 (two bytes a row and position);
+    6: VQ4P (four stages of 64, the codes packed in three bytes); idx then
+    holds the unpacked codes [M][N/8][4]."""
 
     def __init__(self, H, I, E, K, *, score_func=0, renorm=0, routed_scale=1.0,
                  n_group=1, topk_group=1, n_shared=0, router_fmt=FMT_F32,
                  shared_fmt=FMT_Q8G, bias=False, seed=0, cb_base=0,
-                 book_scale=0.3, subnormal_books=0, layer=0, index_bits=8):
+                 book_scale=0.3, subnormal_books=0, layer=0, index_bits=8, stages=3):
         rng = np.random.default_rng(seed)
         self.H, self.I, self.E, self.K = H, I, E, K
         self.score_func, self.renorm, self.routed_scale = score_func, renorm, routed_scale
@@ -93,7 +94,8 @@ class Layer:
         self.cb_base = cb_base
         self.layer = layer
         self.index_bits = index_bits
-        self.stages, self.entries = (4, 64) if index_bits == 6 else (STAGES, ENTRIES)
+        self.stages, self.entries = (4, 64) if index_bits == 6 else (stages, ENTRIES)
+        assert index_bits == 6 or stages in (2, 3)
         self.n_books = cb_base + 3 * self.stages
         books = (rng.standard_normal((self.n_books, self.entries, VEC_DIM)) * book_scale).astype(np.float32)
         self.books_f16 = f16_bits(books)
@@ -118,7 +120,8 @@ class Layer:
                 self.records.append(make_record(layer, e, cb_base, shapes, [pack_p6(c) for c in il], sl,
                                                 FMT_VQ4P))
             else:
-                self.records.append(make_record(layer, e, cb_base, shapes, il, sl))
+                self.records.append(make_record(layer, e, cb_base, shapes, il, sl,
+                                                FMT_VQ2R if self.stages == 2 else FMT_VQ3R))
         self.rec_bytes = len(self.records[0])
         self.router = Tensor.make(router_fmt, (rng.standard_normal((E, H)) * 0.02).astype(np.float32))
         self.bias = (rng.standard_normal(E) * 0.02).astype(np.float32) if bias else None

@@ -1,6 +1,7 @@
 # SPDX-License-Identifier: Apache-2.0
-"""VQ4P experts (index_bits 6: four stages of 64 entries, the engine's int8
-tables) through the device layer, on an MI355X, through the C ABI.
+"""The other expert formats through the device layer, on an MI355X, through
+the C ABI: VQ4P (index_bits 6: four stages of 64 entries, the engine's int8
+tables) and VQ2R (two stages of 256 entries, fp32 tables).
 
   forward, T = 1 and T > 1   ids and weights bit-exact against the oracle's
                              routing on the device logits; the layer output
@@ -15,8 +16,11 @@ tables) through the device layer, on an MI355X, through the C ABI.
                              expert set: outputs bit-exact as above
   records                    a VQ3R record is refused by a VQ4P layer and a
                              VQ4P record by a VQ3R one
-The oracle's VQ4P layer is pinned by the compiled reference's moe_layer and
-moe_chunk (tests/golden/vq4p_layer.npz).
+  containers                 VQ4P and VQ2R containers opened by
+                             waste_hip_container_moe: layers bit-identical
+                             to the directly built ones
+The oracle's VQ4P and VQ2R layers are pinned by the compiled reference's
+moe_layer and moe_chunk (tests/golden/vq_formats.npz).
 """
 import ctypes as C
 import sys
@@ -46,12 +50,16 @@ def orc():
     return Oracle()
 
 
+FMT = {"p6": dict(index_bits=6), "r2": dict(stages=2)}
 CASES = {
     # OLMoE-like: softmax, no shared expert, fp32 activations
     "p6_softmax": (dict(H=1024, I=512, E=32, K=8, score_func=1, seed=61), False),
     # DeepSeek-V3-like: sigmoid + bias, group limit, a 4-bit shared expert, bf16 activations
     "p6_dsv3": (dict(H=1024, I=512, E=64, K=8, score_func=0, renorm=1, routed_scale=2.5, bias=True, n_group=8,
                      topk_group=4, n_shared=1, shared_fmt=FMT_Q4G, router_fmt=FMT_F32, seed=62), True),
+    "r2_softmax": (dict(H=1024, I=512, E=32, K=8, score_func=1, seed=64), False),
+    "r2_dsv3": (dict(H=1024, I=512, E=64, K=8, score_func=0, renorm=1, routed_scale=2.5, bias=True, n_group=8,
+                     topk_group=4, n_shared=1, shared_fmt=FMT_Q4G, router_fmt=FMT_F32, seed=65), True),
 }
 
 
@@ -59,7 +67,7 @@ def make(name):
     kw, bf16 = CASES[name]
     kw = dict(kw)
     H, I, E, K = kw.pop("H"), kw.pop("I"), kw.pop("E"), kw.pop("K")
-    return Layer(H, I, E, K, index_bits=6, **kw), bf16
+    return Layer(H, I, E, K, **FMT[name[:2]], **kw), bf16
 
 
 def inputs(L, T, seed, bf16):
@@ -80,8 +88,8 @@ def oracle_apply(orc, L, order, X, ids, w, chunk):
 
 @pytest.mark.parametrize("name", list(CASES))
 @pytest.mark.parametrize("order", [0, 1])
-def test_vq4p_layer_forward(orc, name, order):
-    say("test_vq4p_layer_forward", name, order)
+def test_format_layer_forward(orc, name, order):
+    say("test_format_layer_forward", name, order)
     L, bf16 = make(name)
     m = gpu_layer(L, max_tokens=8, p6_order=order)
     for T in (1, 8):
@@ -99,11 +107,12 @@ def test_vq4p_layer_forward(orc, name, order):
     m.close()
 
 
-def test_vq4p_layer_through_cache(orc):
+@pytest.mark.parametrize("name", ["p6_softmax", "r2_softmax"])
+def test_format_layer_through_cache(orc, name):
     """forward_cached over 12 slots for 32 experts: every miss filled from
     pinned host memory, the outputs as forward()'s."""
-    say("test_vq4p_layer_through_cache")
-    L, bf16 = make("p6_softmax")
+    say("test_format_layer_through_cache", name)
+    L, bf16 = make(name)
     order = warp_amd.lib().waste_hip_vq_p6_order()
     m = gpu_layer(L, max_tokens=1, records=False, p6_order=order)
     assert m.bind_table([], [], codebook_id=L.cb_base) == 0
@@ -131,16 +140,22 @@ def test_vq4p_layer_through_cache(orc):
     m.close()
 
 
-def test_vq4p_records_checked(orc):
+def test_format_records_checked(orc):
     """Each layer takes only its own format's records."""
-    say("test_vq4p_records_checked")
+    say("test_format_records_checked")
     L6, _ = make("p6_softmax")
+    L2, _ = make("r2_softmax")
     L8 = Layer(L6.H, L6.I, L6.E, L6.K, score_func=1, seed=63)
     m6 = gpu_layer(L6, records=False)
+    m2 = gpu_layer(L2, records=False)
     m8 = gpu_layer(L8, records=False)
     assert m6.set_expert(0, L8.records[0]) == warp_amd.ERECORD
     assert m8.set_expert(0, L6.records[0]) == warp_amd.ERECORD
+    assert m2.set_expert(0, L8.records[0]) == warp_amd.ERECORD    # the record size differs too
+    assert m8.set_expert(0, L2.records[0]) == warp_amd.ERECORD
     assert m6.set_expert(0, L6.records[0]) == 0
+    assert m2.set_expert(0, L2.records[0]) == 0
+    m2.close()
     # the device-side check of the table path: the wrong format stays unbound
     d8 = torch.from_numpy(np.frombuffer(L8.records[1], np.uint8).copy()).cuda()
     s = torch.cuda.current_stream().cuda_stream
@@ -150,21 +165,24 @@ def test_vq4p_records_checked(orc):
     m8.close()
 
 
-def test_vq4p_container_layer(orc, tmp_path):
-    """Two VQ4P layers (with a shared expert, which the engine's layer
-    always reads) written as a container (expert_quant VQ4P, index_bits 6,
-    twelve books a layer) and opened with
+@pytest.mark.parametrize("fmt", ["p6", "r2"])
+def test_format_container_layer(orc, tmp_path, fmt):
+    """Two layers (with a shared expert, which the engine's layer always
+    reads) written as a VQ4P container (index_bits 6, twelve books a layer)
+    or a VQ2R one (two stages, six books) and opened with
     waste_hip_container_moe: outputs bit-identical to the layers built
     directly from the same arrays."""
-    say("test_vq4p_container_layer")
+    say("test_format_container_layer", fmt)
     from container_writer import build, write
     kw, _ = CASES["p6_softmax"]
-    Ls = [Layer(kw["H"], kw["I"], kw["E"], kw["K"], score_func=1, seed=70 + r, cb_base=12 * r, layer=1 + r,
-                n_shared=1, shared_fmt=FMT_Q4G, index_bits=6) for r in range(2)]
+    nbk = 12 if fmt == "p6" else 6
+    Ls = [Layer(kw["H"], kw["I"], kw["E"], kw["K"], score_func=1, seed=70 + r, cb_base=nbk * r, layer=1 + r,
+                n_shared=1, shared_fmt=FMT_Q4G, **FMT[fmt]) for r in range(2)]
     manifest, files = build(Ls, n_layers=3, first_dense=1)
     path = write(str(tmp_path / "ctr"), manifest, files)
     ct = warp_amd.Container(path, verify=True)
-    assert ct.config()["index_bits"] == 6
+    c = ct.config()
+    assert (c["index_bits"], c["stages"]) == ((6, 4) if fmt == "p6" else (8, 2))
     order = warp_amd.lib().waste_hip_vq_p6_order()
     for r, L in enumerate(Ls):
         mc = ct.moe(1 + r, max_tokens=4)

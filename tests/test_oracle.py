@@ -17,8 +17,8 @@ Pins, per oracle function (oracle/oracle.c):
                     n_group=1 reduction
   orc_act_pair      golden
   orc_moe_layer / orc_moe_chunk   golden (both orders) + fp64 layer bound;
-                    VQ4P experts (int8 tables, vq_rows_p6) golden in both
-                    orders (vq4p_layer.npz)
+                    VQ4P experts (int8 tables, vq_rows_p6) and VQ2R (two
+                    stages) golden in both orders (vq_formats.npz)
   orc_record_check  valid/damaged records, crc32 against zlib
 """
 import ctypes
@@ -29,8 +29,8 @@ import zlib
 import numpy as np
 import pytest
 
-from golden.make_golden import (CASES, Q3G_WIDTHS, VQ4P_CASES, case_layer, input_digest, q3g_digest, q3g_inputs,
-                                vq4p_case)
+from golden.make_golden import (CASES, FORMAT_CASES, Q3G_WIDTHS, case_layer, format_case, input_digest, q3g_digest,
+                                q3g_inputs)
 from oracle_lib import Oracle, fp, i32p, ptr
 from records import FMT_F32, Layer, Tensor, quant_q3g, unblock_indices
 
@@ -441,14 +441,15 @@ def test_device_log1pf_sampled():
     assert " 0 differ" in out, out
 
 
-@pytest.mark.parametrize("name", list(VQ4P_CASES))
-def test_vq4p_layer_golden(orc, name):
+@pytest.mark.parametrize("name", list(FORMAT_CASES))
+def test_format_layer_golden(orc, name):
     """orc_moe_layer and orc_moe_chunk on VQ4P experts (index_bits 6: the
     gate/up/down tables quantised to int8 per 32 positions, the rows
-    through vq_rows_p6) against the compiled reference's moe_layer and
-    moe_chunk, bit for bit in both orders."""
-    g = np.load(os.path.join(GOLD, "vq4p_layer.npz"))
-    L, X = vq4p_case(name)
+    through vq_rows_p6) and on VQ2R experts (two stages of 256 entries)
+    against the compiled reference's moe_layer and moe_chunk, bit for bit
+    in both orders."""
+    g = np.load(os.path.join(GOLD, "vq_formats.npz"))
+    L, X = format_case(name)
     assert input_digest(L, X) == str(g[f"{name}_digest"])
     for o in (0, 1):
         if o == 1 and int(g["isa"]) != 2:

@@ -69,7 +69,7 @@ class MoeCfg(C.Structure):
                 ("renorm", C.c_int), ("routed_scale", C.c_float), ("n_group", C.c_int),
                 ("topk_group", C.c_int), ("layer", C.c_int), ("max_tokens", C.c_int),
                 ("verify_records", C.c_int), ("prefill_min_tokens", C.c_int),
-                ("index_bits", C.c_int), ("p6_order", C.c_int)]
+                ("index_bits", C.c_int), ("p6_order", C.c_int), ("stages", C.c_int)]
 
 
 class HipTensor(C.Structure):
@@ -204,16 +204,17 @@ class MoeLayer:
 
     def __init__(self, *, hidden, n_experts, top_k, moe_inter, n_shared=0, score_func=0,
                  renorm=0, routed_scale=1.0, n_group=1, topk_group=1, layer=0,
-                 max_tokens=1, verify_records=0, prefill_min_tokens=0, index_bits=8, p6_order=None):
-        """index_bits 6: VQ4P experts, whose tables and rows follow the
-        engine's arithmetic in p6_order (None: this host's, as
-        waste_hip_vq_p6_order reports it)."""
+                 max_tokens=1, verify_records=0, prefill_min_tokens=0, index_bits=8, p6_order=None,
+                 stages=0):
+        """index_bits 6: VQ4P experts; stages 2 (index_bits 8): VQ2R.  Their
+        tables and rows follow the engine's arithmetic in p6_order (None:
+        this host's, as waste_hip_vq_p6_order reports it)."""
         self.L = lib()
         if p6_order is None:
-            p6_order = self.L.waste_hip_vq_p6_order() if index_bits == 6 else 0
+            p6_order = self.L.waste_hip_vq_p6_order() if index_bits == 6 or stages == 2 else 0
         self.cfg = MoeCfg(hidden, n_experts, top_k, moe_inter, n_shared, score_func, renorm,
                           routed_scale, n_group, topk_group, layer, max_tokens, verify_records,
-                          prefill_min_tokens, index_bits, p6_order)
+                          prefill_min_tokens, index_bits, p6_order, stages)
         h = C.c_void_p()
         check(self.L.waste_hip_moe_create(C.byref(self.cfg), C.byref(h)), "waste_hip_moe_create")
         self.h = h

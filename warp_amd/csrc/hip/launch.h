@@ -181,6 +181,14 @@ int whip_p6_rows_pairs(const uint8_t *const *recs, const int32_t *pair_exp, cons
                        hipStream_t s);
 /* h[p][i] = silu(gu[p][0][i]) * gu[p][1][i], the engine's SwiGLU. */
 int whip_p6_act(const float *gu, int P, int I, float *h, hipStream_t s);
+/* VQ2R (vq2r.hip): fp32 tables lut[t][nv][st][256] of rows x kinds inputs in
+ * the engine's order, and every pair's rows through them in vq_rows'
+ * order (two stages, two index bytes a row and position). */
+int whip_r2_lutb(const void *x, int x_bf16, int x_ld, int rows, int kinds, int st, const float *booksT, int cb,
+                 int nv, int fma, float *lut, hipStream_t s);
+int whip_r2_rows_pairs(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                       int kinds, const uint32_t *idx_off, const uint32_t *sc_off, int M, int nv, const float *lut,
+                       int per_tok, float *out, int *err, hipStream_t s);
 /* Rows [r_lo, r_hi) (r_lo % 64 == 0) of a VQ4P matrix through lut8/lscale
  * (src/model.c:4076-4114); fma: fold the blocks with one fused
  * multiply-add (the AVX-512 and NEON kernels) instead of a product and a

@@ -37,11 +37,12 @@ int waste_hip_container_moe(waste_hip_container *c, int layer, int max_tokens, i
     if (!c || waste_hip_container_config(c, &g) ||
         waste_hip_container_bank(c, layer, &n_exp, &cb, &rec_bytes) || max_tokens < 1)
         return WASTE_HIP_EINVAL;
-    /* the layer decodes VQ3R (three stages of 256 eight-wide entries) and
-     * VQ4P (index_bits 6: four stages of 64) */
-    const int p6 = g.index_bits == 6;
-    if (g.vec_dim != 8 || g.latent_dim || (p6 ? g.stages != 4 || g.entries != 64
-                                              : g.stages != 3 || g.entries != 256 || g.index_bits != 8))
+    /* the layer decodes VQ3R (three stages of 256 eight-wide entries),
+     * VQ2R (two) and VQ4P (index_bits 6: four stages of 64) */
+    const int p6 = g.index_bits == 6, r2 = !p6 && g.stages == 2;
+    if (g.vec_dim != 8 || g.latent_dim ||
+        (p6 ? g.stages != 4 || g.entries != 64
+            : (g.stages != 3 && g.stages != 2) || g.entries != 256 || g.index_bits != 8))
         return WASTE_HIP_EINVAL;
     const int E = g.n_experts, H = g.hidden, I = g.moe_inter;
     const int SI = I * (g.n_shared ? g.n_shared : 1);
@@ -84,7 +85,8 @@ int waste_hip_container_moe(waste_hip_container *c, int layer, int max_tokens, i
     mc.verify_records = 0;             /* the container's reads check the checksum */
     mc.prefill_min_tokens = prefill_min_tokens;
     mc.index_bits = p6 ? 6 : 8;
-    mc.p6_order = p6 ? waste_hip_vq_p6_order() : 0;   /* the engine's arithmetic on this host */
+    mc.stages = g.stages;
+    mc.p6_order = p6 || r2 ? waste_hip_vq_p6_order() : 0;   /* the engine's arithmetic on this host */
     waste_hip_moe *m = NULL;
     if ((rc = waste_hip_moe_create(&mc, &m))) return rc;
     int n_books = 0;

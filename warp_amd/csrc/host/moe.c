@@ -90,6 +90,8 @@ struct waste_hip_moe {
     /* VQ4P experts (index_bits 6): four stages of 64 entries, 12 books a
      * record; every T on the decode path */
     int p6, stages, entries, nbk;
+    int r2;                      /* VQ2R experts: two stages of 256 entries */
+    int bpp;                     /* index bytes a (row, position)          */
     struct {
         float *lut_gu, *lut_d;   /* fp32 tables [T][2][nv_gu][256], [P][nv_d][256] */
         int8_t *q_gu, *q_d;      /* their int8 copies                      */
@@ -200,7 +202,11 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
                              cfg->topk_group * (cfg->n_experts / cfg->n_group) < cfg->top_k))
         return WASTE_HIP_EINVAL;
     if (cfg->index_bits != 0 && cfg->index_bits != 8 && cfg->index_bits != 6) return WASTE_HIP_EINVAL;
-    if (cfg->index_bits == 6 && cfg->p6_order != WASTE_HIP_ORDER_PORTABLE && cfg->p6_order != WASTE_HIP_ORDER_FMA)
+    if (cfg->index_bits == 6 ? cfg->stages != 0 && cfg->stages != 4
+                             : cfg->stages != 0 && cfg->stages != 3 && cfg->stages != 2)
+        return WASTE_HIP_EINVAL;
+    if ((cfg->index_bits == 6 || cfg->stages == 2) && cfg->p6_order != WASTE_HIP_ORDER_PORTABLE &&
+        cfg->p6_order != WASTE_HIP_ORDER_FMA)
         return WASTE_HIP_EINVAL;
     if (!waste_hip_device_name()) return WASTE_HIP_ENODEV;
     waste_hip_moe *m = (waste_hip_moe *)calloc(1, sizeof *m);
@@ -210,21 +216,23 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     m->SI = cfg->moe_inter * (cfg->n_shared > 0 ? cfg->n_shared : 1);
     m->T = cfg->max_tokens;
     m->p6 = cfg->index_bits == 6;
-    m->stages = m->p6 ? 4 : 3;
+    m->r2 = !m->p6 && cfg->stages == 2;
+    m->stages = m->p6 ? 4 : m->r2 ? 2 : 3;
     m->entries = m->p6 ? 64 : 256;
     m->nbk = 3 * m->stages;
+    m->bpp = m->p6 ? 3 : m->stages;
     {
-        /* VQ4P: the decode kernels take every T (no matrix-core path) */
+        /* VQ4P and VQ2R: the decode path takes every T (no matrix-core path) */
         const int pm = cfg->prefill_min_tokens > 0 ? cfg->prefill_min_tokens : 32;
-        m->Td = m->T < pm || m->p6 ? m->T : pm;
+        m->Td = m->T < pm || m->p6 || m->r2 ? m->T : pm;
     }
     m->nv_gu = m->H / 8; m->nv_d = m->I / 8;
     m->nch_gu = whip_vq_chunks(m->nv_gu, m->I);
     m->nch_d = whip_vq_chunks(m->nv_d, m->H);
     /* canonical record layout (tools/convert.py:942-977): 48 B header,
      * gate, up, down index streams, then f16 scales gate|up|down */
-    m->idx_gu = (size_t)m->I * m->nv_gu * 3;
-    m->idx_d = (size_t)m->H * m->nv_d * 3;
+    m->idx_gu = (size_t)m->I * m->nv_gu * m->bpp;
+    m->idx_d = (size_t)m->H * m->nv_d * m->bpp;
     m->off_gate = 48;
     m->off_up = (uint32_t)(48 + m->idx_gu);
     m->off_down = (uint32_t)(48 + 2 * m->idx_gu);
@@ -245,7 +253,14 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     rc |= dmalloc((void **)&m->b.pair_exp, (size_t)P * 4);
     rc |= dmalloc((void **)&m->b.pair_w, (size_t)P * 4);
     rc |= dmalloc((void **)&m->b.tok_pairs, (size_t)P * 4);
-    if (m->p6) {
+    if (m->r2) {
+        const size_t tg = (size_t)m->nv_gu * 2 * 256, td = (size_t)m->nv_d * 2 * 256;
+        rc |= dmalloc((void **)&m->p6b.lut_gu, (size_t)m->T * 2 * tg * 4);
+        rc |= dmalloc((void **)&m->p6b.lut_d, (size_t)P * td * 4);
+        rc |= dmalloc((void **)&m->p6b.gu, (size_t)P * 2 * m->I * 4);
+        rc |= dmalloc((void **)&m->p6b.h, (size_t)P * m->I * 4);
+        rc |= dmalloc((void **)&m->p6b.down, (size_t)P * m->H * 4);
+    } else if (m->p6) {
         const size_t tg = (size_t)m->nv_gu * 256, td = (size_t)m->nv_d * 256;
         const size_t bg = (size_t)(m->nv_gu + 31) / 32, bd = (size_t)(m->nv_d + 31) / 32;
         rc |= dmalloc((void **)&m->p6b.lut_gu, (size_t)m->T * 2 * tg * 4);
@@ -434,7 +449,7 @@ static int check_record(const waste_hip_moe *m, int expert, const uint8_t *rec, 
     if (h.magic != WASTE_MAGIC_EXPERT) return WASTE_HIP_ERECORD;
     if (h.layer != (uint16_t)m->c.layer || h.expert_id != (uint16_t)expert) return WASTE_HIP_ERECORD;
     if ((size_t)h.rec_4k_blocks * WASTE_ALIGN != rec_bytes) return WASTE_HIP_ERECORD;
-    if (h.fmt != (m->p6 ? WQ_VQ4P : WQ_VQ3R) || h.lowrank_id != 0) return WASTE_HIP_ERECORD;
+    if (h.fmt != (m->p6 ? WQ_VQ4P : m->r2 ? WQ_VQ2R : WQ_VQ3R) || h.lowrank_id != 0) return WASTE_HIP_ERECORD;
     if (m->n_books && (h.codebook_id < m->book0 || (long)h.codebook_id + m->nbk > (long)m->book0 + m->n_books))
         return WASTE_HIP_ERECORD;
     if (!(h.gate_off == 48 && h.gate_off < h.up_off && h.up_off < h.down_off &&
@@ -785,6 +800,8 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
  * SwiGLU output and its down rows, then the combine and the shared expert
  * as for VQ3R.  The tables and rows follow the engine's arithmetic in the
  * layer's p6_order, so each pair's rows are the engine's bit for bit. */
+static int alt_combine(waste_hip_moe *m, int T, float *y, hipStream_t s);
+
 static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
 {
     const int K = m->K, H = m->H, I = m->I, P = T * K, fma = m->c.p6_order == WASTE_HIP_ORDER_FMA;
@@ -806,7 +823,43 @@ static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
     CK((hipError_t)whip_p6_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, d_sc, H, m->nv_d,
                                       m->p6b.q_d, m->p6b.s_d, 0, fma, m->p6b.down, m->err, s));
     MARK(5);
-    /* the combine: each pair's rows are already scaled, one chunk each */
+    return alt_combine(m, T, y, s);
+}
+
+/* VQ2R experts (two stages of 256 entries), the same order as VQ4P's above
+ * with fp32 tables: each token's gate and up tables (vq_build_lut), every
+ * pair's gate and up rows through them (vq_rows' generic loop), SwiGLU,
+ * the pair's down table and rows, the combine.  The tables follow the
+ * engine's build in the layer's order, so each pair's rows are the
+ * engine's bit for bit. */
+static int experts_r2(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
+{
+    const int K = m->K, H = m->H, I = m->I, P = T * K, fma = m->c.p6_order == WASTE_HIP_ORDER_FMA;
+    const int cb = m->cb - m->book0;
+    MARK(2);
+    CK((hipError_t)whip_r2_lutb(x, x_bf16, H, T, 2, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.lut_gu, s));
+    const uint32_t gu_idx[2] = { m->off_gate, m->off_up };
+    const uint32_t gu_sc[2] = { m->off_sc, m->off_sc + 2u * (uint32_t)I };
+    CK((hipError_t)whip_r2_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 2, gu_idx, gu_sc, I, m->nv_gu,
+                                      m->p6b.lut_gu, 1, m->p6b.gu, m->err, s));
+    MARK(3);
+    CK((hipError_t)whip_p6_act(m->p6b.gu, P, I, m->p6b.h, s));
+    MARK(4);
+    CK((hipError_t)whip_r2_lutb(m->p6b.h, 0, I, P, 1, 2, m->d_booksT, cb + 2 * m->stages, m->nv_d, fma,
+                                m->p6b.lut_d, s));
+    const uint32_t d_idx[1] = { m->off_down }, d_sc[1] = { m->off_sc + 4u * (uint32_t)I };
+    CK((hipError_t)whip_r2_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, d_sc, H, m->nv_d,
+                                      m->p6b.lut_d, 0, m->p6b.down, m->err, s));
+    MARK(5);
+    return alt_combine(m, T, y, s);
+}
+
+/* The combine of the VQ4P / VQ2R paths: each pair's down rows in
+ * p6b.down, already scaled, one chunk each; the shared expert as for
+ * VQ3R. */
+static int alt_combine(waste_hip_moe *m, int T, float *y, hipStream_t s)
+{
+    const int K = m->K, H = m->H;
     if (m->sh_in_combine) {
         MARK(6);
         const int rc = whip_combine_sh(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->p6b.down,
@@ -921,6 +974,7 @@ int waste_hip_moe_experts(waste_hip_moe *m, const void *x, int x_bf16, int T, fl
     if (!books_ok(m)) return WASTE_HIP_EINVAL;
     hipStream_t s = (hipStream_t)stream;
     if (m->p6) return experts_p6(m, x, x_bf16, T, y, s);
+    if (m->r2) return experts_r2(m, x, x_bf16, T, y, s);
     if (T <= m->Td) return experts_few(m, x, x_bf16, T, y, s);
     const int r = experts_many(m, x, x_bf16, T, y, s);
     return r ? r : range_fallback(m, x, x_bf16, T, y, s);
@@ -993,7 +1047,7 @@ int waste_hip_moe_forward_static(waste_hip_moe *m, const void *x, int x_bf16, in
 {
     int rc = ready(m, x, T);
     if (rc) return rc;
-    if (!y || !books_ok(m) || m->p6) return WASTE_HIP_EINVAL;   /* VQ4P: forward() only */
+    if (!y || !books_ok(m) || m->p6 || m->r2) return WASTE_HIP_EINVAL;   /* VQ4P / VQ2R: forward() only */
     if (T > m->Td || static_layout(m, T, NULL, NULL) > WHIP_SCRATCH_BYTES)
         return WASTE_HIP_ESCRATCH;
     hipStream_t s = (hipStream_t)stream;
@@ -1042,7 +1096,7 @@ int waste_hip_moe_bind_table(waste_hip_moe *m, const int *experts, const void *c
     a.cb = m->cb;
     a.book0 = m->n_books > 0 ? m->book0 : 0;
     a.n_books = m->n_books > 0 ? m->book0 + m->n_books : 65536 + m->nbk;
-    a.fmt = m->p6 ? WQ_VQ4P : WQ_VQ3R;
+    a.fmt = m->p6 ? WQ_VQ4P : m->r2 ? WQ_VQ2R : WQ_VQ3R;
     a.nbk = (uint32_t)m->nbk;
     CK((hipError_t)whip_bind(m->d_recs, &a, m->err, (hipStream_t)stream));
     m->pair_rec_ok = 0;
@@ -1204,7 +1258,7 @@ size_t waste_hip_moe_bytes(const waste_hip_moe *m, int T, int n_distinct)
 int waste_hip_moe_dequant(waste_hip_moe *m, int expert, int kind, float *W, void *stream)
 {
     if (!m || expert < 0 || expert >= m->E || kind < 0 || kind > 2 || !W || !m->d_books ||
-        !books_ok(m) || m->p6)
+        !books_ok(m) || m->p6 || m->r2)
         return WASTE_HIP_EINVAL;
     const uint8_t *rec = m->h_recs[expert];
     if (!rec) return WASTE_HIP_EUNBOUND;
