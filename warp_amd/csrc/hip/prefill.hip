@@ -148,6 +148,7 @@ extern "C" int whip_sort_pairs(const int32_t *ids, const float *w, int T, int K,
 #define PF_KC 64                     // k per LDS chunk
 #define PF_ALD (PF_KC + 8)           // A row stride in halves (144 B: rows fall on different banks)
 #define PF_BIG 64                    // expert segments this long take the 256 x 256 tile kernel
+#define PF_SHORT 32                  // and segments up to this long the one-tile kernel
 
 enum { DEC_F32 = 0, DEC_Q8 = 2, DEC_Q4 = 3, DEC_VQ = 4 };
 
@@ -201,6 +202,10 @@ __global__ void __launch_bounds__(PF_THREADS) k_pf_gemm(whip_pf_args a)
     const int r0 = blockIdx.z * (MT * 32);           // this workgroup's rows of the segment
     if (r0 >= n_seg) return;
     if (DEC == DEC_VQ && MT == 4 && a.seg_off && n_seg >= PF_BIG) return;   // long segments: k_pf_gemm8
+    // expert segments of at most 32 tokens take the one-tile instantiation
+    // (a quarter of the accumulators, so more workgroups on a CU hide the
+    // index loads' latency); the four-tile one takes those up to PF_BIG
+    if (DEC == DEC_VQ && a.seg_off && (MT == 4 ? n_seg <= PF_SHORT : n_seg > PF_SHORT)) return;
     const int mrows = min(MT * 32, n_seg - r0);
     const int kind = EPI == 0 ? wave >> 2 : 0;
     const int ncol = blockIdx.x * (EPI == 0 ? 128 : 256) + (EPI == 0 ? (wave & 3) : wave) * 32 + (lane & 31);
@@ -674,6 +679,12 @@ extern "C" int whip_pf_gemm(const whip_pf_args *a, int dec, int pair, int mt, in
         else hipLaunchKernelGGL((k_pf_gemm8<1, 0>), grid8, dim3(PF8_THREADS), 0, s, *a);
         const int e = (int)hipGetLastError();
         if (e) return e;
+        // segments of at most PF_SHORT tokens: one 32-token tile each
+        dim3 grid1((a->N + (pair ? 128 : 256) - 1) / (pair ? 128 : 256), segs, 1);
+        if (pair) hipLaunchKernelGGL((k_pf_gemm<DEC_VQ, 0, 1>), grid1, dim3(PF_THREADS), 0, s, *a);
+        else hipLaunchKernelGGL((k_pf_gemm<DEC_VQ, 1, 1>), grid1, dim3(PF_THREADS), 0, s, *a);
+        const int e1 = (int)hipGetLastError();
+        if (e1) return e1;
     }
     const int ntile = pair ? 128 : 256;
     dim3 grid((a->N + ntile - 1) / ntile, segs, mblocks);
