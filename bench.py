@@ -167,7 +167,7 @@ def run_decode(torch, cfg, layers, B, steps, warmup, seed=0):
            "stage_us": {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
            "dominant": {"stage": dom, "kernel": "k_vq_gate_up" if dom == "routed_gate_up" else "k_vq_act_down",
                         "launch_us": round(stage_ms[dom] * 1e3, 2), "algorithmic_bytes": int(dom_bytes),
-                        "achieved_gbps": round(dom_bytes / (stage_ms[dom] * 1e-3) / 1e9, 1)}}
+                        "achieved_gbps": round(dom_bytes / (max(stage_ms[dom], 1e-9) * 1e-3) / 1e9, 1)}}
     return rec, x_all
 
 
@@ -623,6 +623,66 @@ def bench_stack(torch, warp_amd, synth, cfg, books, tokens, n_layers=58, budget_
     return out
 
 
+def bench_formats(torch, warp_amd, synth, cfg, n_layers, steps, warmup, batches=(1, 8)):
+    """The other expert formats through the device layer at the C3 shape:
+    VQ4P (index_bits 6: four stages of 64 entries, int8 tables, rows as
+    vq_rows_p6) and VQ2R (two stages of 256 entries, fp32 tables, rows in
+    vq_rows' order).  Both paths reproduce the engine's arithmetic exactly
+    (the VQ3R tile kernels do not serve them).  One slab of 256 records with
+    random codes (any byte pair or triple decodes to valid codes), valid
+    headers and f16 row scales in [0.01, 0.05), shared by n_layers layer
+    objects as the VQ3R step shares its slab; random books; the same router
+    and shared expert."""
+    import struct
+    H, E, I, K = cfg["hidden"], cfg["n_experts"], cfg["moe_inter"], cfg["top_k"]
+    nv_h, nv_i = H // 8, I // 8
+    router, bias, sh = synth.trunk(cfg, 1)
+    out = {}
+    g = torch.Generator(device="cuda:0").manual_seed(11)
+    for name, ib, st, en, bpp, fmt in (("vq4p", 6, 4, 64, 3, 8), ("vq2r", 8, 2, 256, 2, 5)):
+        idx_gu, idx_d = I * nv_h * bpp, H * nv_i * bpp
+        off_up, off_down, off_sc = 48 + idx_gu, 48 + 2 * idx_gu, 48 + 2 * idx_gu + idx_d
+        rb = (off_sc + 2 * (2 * I + H) + 4095) // 4096 * 4096
+        slab = torch.randint(0, 256, (E, rb), dtype=torch.uint8, device="cuda:0", generator=g)
+        hdr = np.zeros((E, 48), np.uint8)
+        for e in range(E):
+            hdr[e] = np.frombuffer(struct.pack("<IHHBBHHHIIIIIIII", 0x50584557, 0, e, fmt, 0, 0, 0, 0, rb // 4096,
+                                               48, off_up, off_down, off_sc, 0, 0, 0), np.uint8)
+        slab[:, :48] = torch.from_numpy(hdr).to("cuda:0")
+        sc = (torch.rand((E, 2 * I + H), device="cuda:0", generator=g) * 0.04 + 0.01).half()
+        slab[:, off_sc:off_sc + 2 * (2 * I + H)] = sc.view(torch.uint8)
+        rng = np.random.default_rng(12)
+        books = synth.f16_bits((rng.standard_normal((3 * st, en, 8)) * 0.3).astype(np.float32))
+        layers = []
+        for _ in range(n_layers):
+            m = warp_amd.MoeLayer(hidden=H, n_experts=E, top_k=K, moe_inter=I, n_shared=cfg["n_shared"],
+                                  score_func=cfg["score_func"], renorm=cfg["renorm"],
+                                  routed_scale=cfg["routed_scale"], n_group=cfg["n_group"],
+                                  topk_group=cfg["topk_group"], max_tokens=max(batches), index_bits=ib,
+                                  stages=st if ib == 8 else 0)
+            m.set_codebooks(books)
+            m.set_router(router, bias)
+            if sh:
+                m.set_shared(*sh)
+            for e in range(E):
+                rc = m.bind_expert(e, slab[e].data_ptr(), rb)
+                if rc != 0:
+                    raise RuntimeError(f"{name} bind_expert {e}: {rc}")
+            layers.append(m)
+        torch.cuda.synchronize()
+        for bb in batches:
+            r, _ = run_decode(torch, cfg, layers, bb, steps, warmup, seed=100 + bb)
+            out[f"{name}_b{bb}"] = {k: r[k] for k in ("us_per_token", "ms_per_step", "hbm_gbps", "hbm_frac",
+                                                     "bytes_per_step", "distinct_experts_per_step", "stage_us")}
+            log(f"[bench] {name} B={bb}: {r['us_per_token']} us/token, {r['hbm_frac']:.3f} of HBM peak")
+        for m in layers:
+            m.close()
+        del slab
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
+
+
 def measured_traffic(dom, config, batch):
     """HBM bytes per launch of the dominant kernel, as measured by the two
     rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE, each scaled by a copy of
@@ -732,9 +792,10 @@ def main():
                                                 a.prefill_tokens, 5, hot=True)["routed_grouped_gemm"]
         log(f"[bench] prefill {prefill['tokens_per_s']} tok/s")
 
-    vq4p = None
+    vq4p = formats = None
     if a.extra_configs and B == 1:
         vq4p = bench_vq4p(torch, warp_amd)
+        formats = bench_formats(torch, warp_amd, synth, cfg, a.layers, a.steps, a.warmup) if a.config == "dsv3" else None
         log(f"[bench] vq4p rows: {vq4p}")
 
     stack = None
@@ -814,6 +875,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": prefill,
         "vq4p_rows": vq4p,
+        "formats": formats,
         "expert_cache": stack,
     }
     print(json.dumps(out))

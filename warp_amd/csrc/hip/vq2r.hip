@@ -84,8 +84,24 @@ k_r2_rows_pairs(const uint8_t *const *__restrict__ recs, const int32_t *__restri
     const size_t tab = per_tok ? (size_t)pair_tok[p] * kinds + kind : (size_t)p;
     const float *L = lut + tab * nv * 2 * R2_EN;
     const uint16_t *ix = (const uint16_t *)(rec + (kind ? idx_off1 : idx_off0) + (size_t)rb * nv * 128) + lane;
+    // eight positions' codes, then their sixteen entries, are in flight at
+    // once; the sum still runs over the positions in order
     float acc = 0.0f;
-    for (int v = 0; v < nv; v++) {
+    int v = 0;
+    for (; v + 8 <= nv; v += 8) {
+        uint32_t w[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) w[j] = ix[(size_t)(v + j) * 64];
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float *blk = L + (size_t)(v + j) * 2 * R2_EN;
+            t[j] = __fadd_rn(blk[w[j] & 255], blk[R2_EN + (w[j] >> 8)]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc = __fadd_rn(acc, t[j]);
+    }
+    for (; v < nv; v++) {
         const uint32_t w = ix[(size_t)v * 64];
         const float *blk = L + (size_t)v * 2 * R2_EN;
         acc = __fadd_rn(acc, __fadd_rn(blk[w & 255], blk[R2_EN + (w >> 8)]));

@@ -806,6 +806,7 @@ static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
 {
     const int K = m->K, H = m->H, I = m->I, P = T * K, fma = m->c.p6_order == WASTE_HIP_ORDER_FMA;
     const int cb = m->cb - m->book0;
+    m->ktimed = 0;               /* these stages are timed by the events around them */
     MARK(2);
     CK((hipError_t)whip_p6_lutb(x, x_bf16, H, T, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.lut_gu, s));
     CK((hipError_t)whip_vq_quant_lut_n(m->p6b.lut_gu, m->nv_gu, 4, 64, 2 * T, m->p6b.q_gu, m->p6b.s_gu, s));
@@ -836,6 +837,7 @@ static int experts_r2(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
 {
     const int K = m->K, H = m->H, I = m->I, P = T * K, fma = m->c.p6_order == WASTE_HIP_ORDER_FMA;
     const int cb = m->cb - m->book0;
+    m->ktimed = 0;               /* these stages are timed by the events around them */
     MARK(2);
     CK((hipError_t)whip_r2_lutb(x, x_bf16, H, T, 2, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.lut_gu, s));
     const uint32_t gu_idx[2] = { m->off_gate, m->off_up };
