@@ -57,7 +57,11 @@ CASES = {
     # DeepSeek-V3-like: sigmoid + bias, group limit, a 4-bit shared expert, bf16 activations
     "p6_dsv3": (dict(H=1024, I=512, E=64, K=8, score_func=0, renorm=1, routed_scale=2.5, bias=True, n_group=8,
                      topk_group=4, n_shared=1, shared_fmt=FMT_Q4G, router_fmt=FMT_F32, seed=62), True),
+    # ragged: a last scale block of 8 positions (1088 / 8 = 4 * 32 + 8,
+    # 576 / 8 = 2 * 32 + 8) and odd row-block counts (17, 9)
+    "p6_ragged": (dict(H=1088, I=576, E=16, K=4, score_func=1, seed=66), False),
     "r2_softmax": (dict(H=1024, I=512, E=32, K=8, score_func=1, seed=64), False),
+    "r2_ragged": (dict(H=1088, I=576, E=16, K=4, score_func=1, seed=67), False),
     "r2_dsv3": (dict(H=1024, I=512, E=64, K=8, score_func=0, renorm=1, routed_scale=2.5, bias=True, n_group=8,
                      topk_group=4, n_shared=1, shared_fmt=FMT_Q4G, router_fmt=FMT_F32, seed=65), True),
 }

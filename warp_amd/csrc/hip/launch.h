@@ -123,6 +123,22 @@ int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                  const float *part_d, int nch, int H, uint32_t sc_off_down,
                  int skip_zero, const float *sh, int sh_n, size_t sh_stride,
                  float *y, hipStream_t s);
+/* VQ4P down rows for the combine: pair p's row r is the fold, in block
+ * order, of S[(p*nb + b)*H + r] (whip_p6_tiles' sums) with the pair's table
+ * scales ls[p*nb + b] (fma: one fused multiply-add, else a product and a
+ * sum), times the f16 row scale at sc_off of the pair's record; an unbound
+ * expert's rows are zeros. */
+typedef struct {
+    const int16_t *S;
+    const float *ls;
+    int nb;
+    uint32_t sc_off;
+    int fma;
+} whip_fold;
+/* whip_combine / whip_combine_sh with the pairs' down rows folded from f. */
+int whip_combine_fold(const uint8_t *const *recs, const int32_t *pair_exp, const float *pair_w,
+                      const int32_t *tok_pairs, int T, int K, const whip_fold *f, int H, int skip_zero,
+                      const float *sh, int sh_n, size_t sh_stride, float *y, hipStream_t s);
 
 /* ---- products of a few tokens on the matrix cores (skinny.hip) ---- */
 
@@ -164,21 +180,30 @@ int whip_vq_quant_lut(const float *lut, int nv, int stages, int entries, int8_t 
  * scale + t*ceil(nv/32). */
 int whip_vq_quant_lut_n(const float *lut, int nv, int stages, int entries, int ntab, int8_t *q,
                         float *scale, hipStream_t s);
-/* VQ4P tables of rows x kinds inputs: table t = (row t / kinds, kind
- * t % kinds) from x row t / kinds (bf16 or fp32, row stride x_ld) and books
- * cb + 4*kind .. + 3 of booksT ([book][8][64] fp32); lut[t][nv][4][64], in
- * the engine's order (fma: the AVX-512 kernel's chain, else the portable
- * C one's products and sums). */
-int whip_p6_lutb(const void *x, int x_bf16, int x_ld, int rows, int kinds, const float *booksT, int cb,
-                 int nv, int fma, float *lut, hipStream_t s);
-/* vq_rows_p6 of every pair's matrices: out[p][kind][M] from the record of
- * expert pair_exp[p] (idx at idx_off[kind], f16 row scales at
- * sc_off[kind]) through table pair_tok[p]*kinds + kind (per_tok) or p of
- * q/qs (as whip_vq_quant_lut_n lays them out). */
-int whip_p6_rows_pairs(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok,
-                       int P, int kinds, const uint32_t *idx_off, const uint32_t *sc_off, int M, int nv,
-                       const int8_t *q, const float *qs, int per_tok, int fma, float *out, int *err,
-                       hipStream_t s);
+/* VQ4P int8 tables of rows x kinds inputs (vq_build_lut, then
+ * vq_quant_lut): table t = (row t / kinds, kind t % kinds) from x row
+ * t / kinds (bf16 or fp32, row stride x_ld) and books cb + 4*kind .. + 3 of
+ * booksT ([book][8][64] fp32), in the engine's order (fma: the AVX-512
+ * kernel's chain, else the portable C one's products and sums);
+ * q[t][nv][4][64], qs[t][ceil(nv/32)]. */
+int whip_p6_lutq(const void *x, int x_bf16, int x_ld, int rows, int kinds, const float *booksT, int cb,
+                 int nv, int fma, int8_t *q, float *qs, hipStream_t s);
+/* The exact integer sums of every pair's VQ4P rows per 32-position scale
+ * block: S[((p*kinds + kind)*nb + b)*M + r] (int16, nb = ceil(nv/32)) from
+ * the record of expert pair_exp[p] (idx at idx_off[kind]) through table
+ * pair_tok[p]*kinds + kind (per_tok) or p of q (whip_p6_lutq's layout).  An
+ * unbound expert's sums are zeros and raise bit 0 of err. */
+int whip_p6_tiles(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                  int kinds, const uint32_t *idx_off, int M, int nv, const int8_t *q, int per_tok,
+                  int16_t *S, int *err, hipStream_t s);
+/* Each pair's gate and up rows folded from whip_p6_tiles' sums (block order,
+ * the token's table scales qs_gu, the f16 row scales at sc_gate / sc_up of
+ * the record), h = silu(g) * u, and the pair's down table from h (books
+ * cb_d ..): q_d[p][nv_d][4][64], qs_d[p][ceil(nv_d/32)].  I == 8 nv_d. */
+int whip_p6_act_lutq(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                     const int16_t *S, const float *qs_gu, uint32_t sc_gate, uint32_t sc_up, int I, int nv_gu,
+                     const float *booksT, int cb_d, int nv_d, int fma, int8_t *q_d, float *qs_d,
+                     hipStream_t s);
 /* h[p][i] = silu(gu[p][0][i]) * gu[p][1][i], the engine's SwiGLU. */
 int whip_p6_act(const float *gu, int P, int I, float *h, hipStream_t s);
 /* VQ2R (vq2r.hip): fp32 tables lut[t][nv][st][256] of rows x kinds inputs in
@@ -316,6 +341,9 @@ int whip_combine_sh(const uint8_t *const *recs, const int32_t *pair_exp,
                     const float *part_d, int nch, int H, uint32_t sc_off_down,
                     int skip_zero, const whip_mat *shd, const float *h_sh, float *y,
                     hipStream_t s);
+int whip_combine_sh_fold(const uint8_t *const *recs, const int32_t *pair_exp, const float *pair_w,
+                         const int32_t *tok_pairs, int T, int K, const whip_fold *f, int H, int skip_zero,
+                         const whip_mat *shd, const float *h_sh, float *y, hipStream_t s);
 
 /* One token's routing (as whip_route with T = 1, plus pair_rec[j] = the
  * selected expert's record) and a batch-1 product that does not depend on

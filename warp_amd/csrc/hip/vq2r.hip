@@ -6,8 +6,8 @@
 // (src/model.c:3864-3880 through lutb_range: model.c:3815-3854 portable,
 // simd_avx512.c:90-123 with fma) and each row is vq_rows' generic loop
 // (model.c:3966-3970: t = L0[c0] + L1[c1], acc += t over the positions in
-// order, y = acc * f16(scale)).  One lane per row, the tables read through
-// the caches: this path is exact, not fast.
+// order, y = acc * f16(scale)).  One lane per row owns its sum; the tables
+// are read through the caches.
 #include "common.h"
 #include "launch.h"
 
@@ -65,49 +65,94 @@ extern "C" int whip_r2_lutb(const void *x, int x_bf16, int x_ld, int rows, int k
 // scales at sc_off[kind]; its table is pair_tok[p] * kinds + kind (per_tok)
 // or p.  out[p][kind][M].  An unbound expert writes zeros and raises bit 0
 // of err.
-__global__ void __launch_bounds__(64)
+//
+// A row's sum runs over the positions in order, so one lane owns it; the
+// loads do not depend on that order.  Four wavefronts share a 64-row block:
+// each round, wavefront w fetches the codes of positions 64 round + 16 w ..
+// (the next round's already in flight) and their two table entries, and
+// leaves the entries' sums in LDS; wavefront 0 then adds the round's 64
+// positions in order while the others fetch the next round.
+#define R2_WAVES 4
+#define R2_PW 16                       // positions a wavefront fetches a round
+#define R2_ROUND (R2_WAVES * R2_PW)
+
+__global__ void __launch_bounds__(R2_WAVES * 64)
 k_r2_rows_pairs(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
                 const int32_t *__restrict__ pair_tok, int kinds, uint32_t idx_off0, uint32_t idx_off1,
                 uint32_t sc_off0, uint32_t sc_off1, int M, int nv, const float *__restrict__ lut, int per_tok,
                 float *__restrict__ out, int *__restrict__ err)
 {
-    const int p = blockIdx.y, kind = blockIdx.z, rb = blockIdx.x, lane = threadIdx.x;
+    __shared__ float s_t[2][R2_ROUND][64];
+    const int p = blockIdx.y, kind = blockIdx.z, rb = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = rb * 64 + lane;
     const uint8_t *rec = recs[pair_exp[p]];
     float *y = out + ((size_t)p * kinds + kind) * M;
     if (rec == nullptr) {                            // uniform
-        if (r < M) y[r] = 0.0f;
-        if (lane == 0) atomicOr(err, 1);
+        if (tid < 64 && r < M) y[r] = 0.0f;
+        if (tid == 0) atomicOr(err, 1);
         return;
     }
-    if (r >= M) return;
     const size_t tab = per_tok ? (size_t)pair_tok[p] * kinds + kind : (size_t)p;
-    const float *L = lut + tab * nv * 2 * R2_EN;
-    const uint16_t *ix = (const uint16_t *)(rec + (kind ? idx_off1 : idx_off0) + (size_t)rb * nv * 128) + lane;
-    // eight positions' codes, then their sixteen entries, are in flight at
-    // once; the sum still runs over the positions in order
-    float acc = 0.0f;
-    int v = 0;
-    for (; v + 8 <= nv; v += 8) {
-        uint32_t w[8];
+    const float WH_GLOBAL *L = (const float WH_GLOBAL *)(lut + tab * nv * 2 * R2_EN);
+    // rows past M read row 0's codes (in bounds); their sums are not stored
+    const uint16_t WH_GLOBAL *ix =
+        (const uint16_t WH_GLOBAL *)(as_global(rec) + (kind ? idx_off1 : idx_off0) + (size_t)rb * nv * 128) +
+        (r < M ? lane : 0);
+    const int nr = (nv + R2_ROUND - 1) / R2_ROUND;
+    // the codes of this wavefront's positions in round rr (past nv: the last
+    // position's, not added)
+    auto fetch = [&](uint32_t (&w)[R2_PW], int rr) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) w[j] = ix[(size_t)(v + j) * 64];
-        float t[8];
+        for (int k = 0; k < R2_PW; k++) {
+            const int v = min(rr * R2_ROUND + wv * R2_PW + k, nv - 1);
+            w[k] = ix[(size_t)v * 64];
+        }
+    };
+    auto gather = [&](const uint32_t (&w)[R2_PW], int rr, int b) {
+        float g[2 * R2_PW];
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float *blk = L + (size_t)(v + j) * 2 * R2_EN;
-            t[j] = __fadd_rn(blk[w[j] & 255], blk[R2_EN + (w[j] >> 8)]);
+        for (int k = 0; k < R2_PW; k++) {
+            const int v = min(rr * R2_ROUND + wv * R2_PW + k, nv - 1);
+            const float WH_GLOBAL *blk = L + (size_t)v * 2 * R2_EN;
+            g[2 * k] = blk[w[k] & 255];
+            g[2 * k + 1] = blk[R2_EN + (w[k] >> 8)];
         }
 #pragma unroll
-        for (int j = 0; j < 8; j++) acc = __fadd_rn(acc, t[j]);
+        for (int k = 0; k < R2_PW; k++) s_t[b][wv * R2_PW + k][lane] = __fadd_rn(g[2 * k], g[2 * k + 1]);
+    };
+    float acc = 0.0f;
+    auto consume = [&](int rr, int b) {
+        const int n = min(R2_ROUND, nv - rr * R2_ROUND);
+#pragma unroll 8
+        for (int k = 0; k < n; k++) acc = __fadd_rn(acc, s_t[b][k][lane]);
+    };
+    // a round's entries go out before the next round's codes: loads complete
+    // in issue order, so the wait for the entries does not cover the codes
+    uint32_t wA[R2_PW], wB[R2_PW];
+    fetch(wA, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(wB, 1);                                    // past the last round: harmless repeats
+    __builtin_amdgcn_sched_barrier(0);
+    for (int rr = 0; rr < nr; rr += 2) {             // uniform
+        gather(wA, rr, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(wA, rr + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        if (wv == 0) consume(rr, 0);
+        if (rr + 1 >= nr) break;                     // uniform: the whole workgroup
+        gather(wB, rr + 1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(wB, rr + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        if (wv == 0) consume(rr + 1, 1);
     }
-    for (; v < nv; v++) {
-        const uint32_t w = ix[(size_t)v * 64];
-        const float *blk = L + (size_t)v * 2 * R2_EN;
-        acc = __fadd_rn(acc, __fadd_rn(blk[w & 255], blk[R2_EN + (w >> 8)]));
+    if (wv == 0 && r < M) {
+        const uint16_t *sc = (const uint16_t *)(rec + (kind ? sc_off1 : sc_off0));
+        y[r] = __fmul_rn(acc, wh_f16_scale(sc[r]));
     }
-    const uint16_t *sc = (const uint16_t *)(rec + (kind ? sc_off1 : sc_off0));
-    y[r] = __fmul_rn(acc, wh_f16_scale(sc[r]));
 }
 
 extern "C" int whip_r2_rows_pairs(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok,
@@ -118,7 +163,7 @@ extern "C" int whip_r2_rows_pairs(const uint8_t *const *recs, const int32_t *pai
         (kinds > 1 && idx_off[1] % 2))
         return (int)hipErrorInvalidValue;
     const dim3 grid((M + 63) / 64, P, kinds);
-    hipLaunchKernelGGL(k_r2_rows_pairs, grid, dim3(64), 0, s, recs, pair_exp, pair_tok, kinds, idx_off[0],
+    WHIP_LAUNCH(k_r2_rows_pairs, grid, dim3(R2_WAVES * 64), 0, s, recs, pair_exp, pair_tok, kinds, idx_off[0],
                        kinds > 1 ? idx_off[1] : 0, sc_off[0], kinds > 1 ? sc_off[1] : 0, M, nv, lut, per_tok, out,
                        err);
     return (int)hipGetLastError();

@@ -280,7 +280,14 @@ vq_lanes_body(const whip_vq_args &a, int nch, int tiles, int per_wg, int shares)
     // shares > 0: workgroup = (class, share), a share never leaves its class
     int t0, t1;
     if (shares > 0) {
-        const int cls = blockIdx.x / shares, j = blockIdx.x - cls * shares;
+        // ACT: a class's shares each reduce the class's gate/up partials;
+        // with a multiple of eight classes, workgroup w = cls + j * ncls puts
+        // them all on XCD cls % 8, where the second to fourth reads are
+        // served by that XCD's L2 (workgroup w runs on XCD w % 8)
+        const int ncls = gridDim.x / shares;
+        const bool xcd = ACT && ncls % 8 == 0;           // uniform
+        const int cls = xcd ? blockIdx.x % ncls : blockIdx.x / shares;
+        const int j = xcd ? blockIdx.x / ncls : blockIdx.x - cls * shares;
         t0 = cls * tm.tpc + j * per_wg;
         t1 = min(t0 + per_wg, (cls + 1) * tm.tpc);
     } else {
@@ -836,19 +843,50 @@ extern "C" int whip_vq_act(const uint8_t *const *recs, const int32_t *pair_exp, 
 // the down launch scaled its partials already (no record or scale loads;
 // an unbound expert's partials are zeros).  The loads do not wait for the
 // record: every address is valid.
+//
+// FOLD (1: a product and a sum, 2: one fused multiply-add): the pairs' down
+// rows are VQ4P block sums instead of partials, folded here in block order
+// by slice 0 (whip_fold); the other slices hold zeros.
+template <bool FMA>
+__device__ __forceinline__ float4 p6_fold4(const whip_fold &f, int p, int r, int H, const uint8_t *rec)
+{
+    const int16_t *S = f.S + (size_t)p * f.nb * H + r;
+    const float *ls = f.ls + (size_t)p * f.nb;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+    for (int b = 0; b < f.nb; b++) {
+        const uint2 w = *(const uint2 *)(S + (size_t)b * H);
+        const float l = ls[b];
+        const float s4[4] = {(float)(int16_t)(w.x & 0xffff), (float)(int16_t)(w.x >> 16),
+                             (float)(int16_t)(w.y & 0xffff), (float)(int16_t)(w.y >> 16)};
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc[k] = FMA ? __fmaf_rn(l, s4[k], acc[k]) : __fadd_rn(acc[k], __fmul_rn(l, s4[k]));
+    }
+    if (rec == nullptr) return make_float4(0.0f, 0.0f, 0.0f, 0.0f);   // unbound: zeros
+    const uint16_t *sc = (const uint16_t *)(rec + f.sc_off) + r;
+    return make_float4(__fmul_rn(acc[0], wh_f16_scale(sc[0])), __fmul_rn(acc[1], wh_f16_scale(sc[1])),
+                       __fmul_rn(acc[2], wh_f16_scale(sc[2])), __fmul_rn(acc[3], wh_f16_scale(sc[3])));
+}
+
+template <int FOLD>
 __device__ __forceinline__ void
 cmb_gather(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
            const float *__restrict__ pair_w, const int32_t *__restrict__ tok_pairs, int K,
-           const float *__restrict__ part_d, int nch, int H, uint32_t sc_off_down, int skip_zero, int t, int it,
-           int g, int r0, int per, float4 *cred, float4 *csc, float *cw, int *cl)
+           const float *__restrict__ part_d, const whip_fold &f, int nch, int H, uint32_t sc_off_down,
+           int skip_zero, int t, int it, int g, int r0, int per, float4 *cred, float4 *csc, float *cw, int *cl)
 {
     constexpr int G = CMB_ROWS / 4;
     const int j = it / CMB_SLICES, sl = it % CMB_SLICES;
     const int p = gridDim.y == 1 ? j : tok_pairs[t * K + j];
     const float wj = pair_w[p];
     const int rr = r0 < H ? r0 : 0;
-    const int c0 = min(nch, sl * per), c1 = min(nch, c0 + per);
-    float4 v = sum_chunks(part_d + (size_t)p * nch * H + rr, H, c0, c1);
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (FOLD) {
+        if (sl == 0) v = p6_fold4<FOLD == 2>(f, p, rr, H, recs[pair_exp[p]]);
+    } else {
+        const int c0 = min(nch, sl * per), c1 = min(nch, c0 + per);
+        v = sum_chunks(part_d + (size_t)p * nch * H + rr, H, c0, c1);
+    }
     bool live = !(skip_zero && wj == 0.0f);          // else the pair adds nothing
     float4 scv = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     if (sc_off_down) {                               // uniform
@@ -870,10 +908,11 @@ cmb_gather(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ 
     }
 }
 
+template <int FOLD>
 __global__ void __launch_bounds__(256)
 k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
           const float *__restrict__ pair_w, const int32_t *__restrict__ tok_pairs, int K,
-          const float *__restrict__ part_d, int nch, int H, uint32_t sc_off_down,
+          const float *__restrict__ part_d, whip_fold f, int nch, int H, uint32_t sc_off_down,
           int skip_zero, const float *__restrict__ sh, int sh_n, size_t sh_stride, float *__restrict__ y)
 {
     // [K][CMB_SLICES][G] slice sums, [K][G] row scales, [K] weights, [K] live
@@ -900,8 +939,8 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
         }
     }
     for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G)
-        cmb_gather(recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, t, it, g, r0,
-                   per, cred, csc, cw, cl);
+        cmb_gather<FOLD>(recs, pair_exp, pair_w, tok_pairs, K, part_d, f, nch, H, sc_off_down, skip_zero, t, it,
+                         g, r0, per, cred, csc, cw, cl);
     __syncthreads();
     WT_SPAN(3, 1);
     if (tid >= G || r0 >= H) return;
@@ -929,11 +968,11 @@ k_combine(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ p
 }
 
 
-template <int FMT>
+template <int FMT, int FOLD>
 __global__ void __launch_bounds__(256)
 k_combine_sh(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
              const float *__restrict__ pair_w, const int32_t *__restrict__ tok_pairs, int K,
-             const float *__restrict__ part_d, int nch, int H, uint32_t sc_off_down, int skip_zero,
+             const float *__restrict__ part_d, whip_fold f, int nch, int H, uint32_t sc_off_down, int skip_zero,
              whip_mat shd, const float *__restrict__ h_sh, float *__restrict__ y)
 {
     extern __shared__ float4 cred[];
@@ -949,8 +988,8 @@ k_combine_sh(const uint8_t *const *__restrict__ recs, const int32_t *__restrict_
     WT_SPAN(3, 0);
     sh_rows8<FMT>(shd, h_sh + (size_t)t * shd.cols, blockIdx.x * CMB_ROWS, H, shs);
     for (int it = tid / G; it < K * CMB_SLICES; it += 256 / G)
-        cmb_gather(recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, t, it, g, r0,
-                   per, cred, csc, cw, cl);
+        cmb_gather<FOLD>(recs, pair_exp, pair_w, tok_pairs, K, part_d, f, nch, H, sc_off_down, skip_zero, t, it,
+                         g, r0, per, cred, csc, cw, cl);
     __syncthreads();
     if (tid >= G || r0 >= H) return;
     float o[4] = {0, 0, 0, 0};
@@ -979,25 +1018,59 @@ k_combine_sh(const uint8_t *const *__restrict__ recs, const int32_t *__restrict_
 
 WT_READER(whip_trace_vq)
 
+// fold: the VQ4P block sums in place of part_d (nch 1, sc_off_down 0)
+static int combine_sh(const uint8_t *const *recs, const int32_t *pair_exp, const float *pair_w,
+                      const int32_t *tok_pairs, int T, int K, const float *part_d, const whip_fold *fold, int nch,
+                      int H, uint32_t sc_off_down, int skip_zero, const whip_mat *shd, const float *h_sh, float *y,
+                      hipStream_t s)
+{
+    if (H % 4 || K < 1 || K > 64 || shd->rows != H || (uintptr_t)h_sh % 16 || shd->rowbytes % 16 ||
+        (shd->fmt != 0 && (shd->group % 32 || shd->cols % 8)) || (shd->fmt == 0 && shd->cols % 4) ||
+        (shd->fmt != 0 && shd->fmt != 2 && shd->fmt != 3))
+        return (int)hipErrorInvalidValue;
+    const whip_fold f = fold ? *fold : whip_fold{};
+    const int fm = fold ? (fold->fma ? 2 : 1) : 0;
+    dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
+    const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
+#define CS(F, D) WHIP_LAUNCH((k_combine_sh<F, D>), grid, dim3(256), lds, s, recs, pair_exp, pair_w, tok_pairs, K, \
+                             part_d, f, nch, H, sc_off_down, skip_zero, *shd, h_sh, y)
+#define CSF(F) do { if (fm == 2) CS(F, 2); else if (fm == 1) CS(F, 1); else CS(F, 0); } while (0)
+    if (shd->fmt == 3) CSF(3);
+    else if (shd->fmt == 2) CSF(2);
+    else CSF(0);
+#undef CSF
+#undef CS
+    return (int)hipGetLastError();
+}
+
+static int combine(const uint8_t *const *recs, const int32_t *pair_exp, const float *pair_w,
+                   const int32_t *tok_pairs, int T, int K, const float *part_d, const whip_fold *fold, int nch, int H,
+                   uint32_t sc_off_down, int skip_zero, const float *sh, int sh_n, size_t sh_stride, float *y,
+                   hipStream_t s)
+{
+    if (H % 4 || K < 1 || K > 64 || (sh && (sh_n < 1 || sh_stride % 4 || (uintptr_t)sh % 16)))
+        return (int)hipErrorInvalidValue;
+    const whip_fold f = fold ? *fold : whip_fold{};
+    const int fm = fold ? (fold->fma ? 2 : 1) : 0;
+    dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
+    const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
+#define CB(D) WHIP_LAUNCH(k_combine<D>, grid, dim3(256), lds, s, recs, pair_exp, pair_w, tok_pairs, K, part_d, f, \
+                          nch, H, sc_off_down, skip_zero, sh, sh_n, sh_stride, y)
+    if (fm == 2) CB(2);
+    else if (fm == 1) CB(1);
+    else CB(0);
+#undef CB
+    return (int)hipGetLastError();
+}
+
 extern "C" int whip_combine_sh(const uint8_t *const *recs, const int32_t *pair_exp,
                                const float *pair_w, const int32_t *tok_pairs, int T, int K,
                                const float *part_d, int nch, int H, uint32_t sc_off_down,
                                int skip_zero, const whip_mat *shd, const float *h_sh, float *y,
                                hipStream_t s)
 {
-    if (H % 4 || K < 1 || K > 64 || shd->rows != H || (uintptr_t)h_sh % 16 || shd->rowbytes % 16 ||
-        (shd->fmt != 0 && (shd->group % 32 || shd->cols % 8)) || (shd->fmt == 0 && shd->cols % 4) ||
-        (shd->fmt != 0 && shd->fmt != 2 && shd->fmt != 3))
-        return (int)hipErrorInvalidValue;
-    dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
-    const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
-#define CS(F) WHIP_LAUNCH((k_combine_sh<F>), grid, dim3(256), lds, s, recs, pair_exp, pair_w, tok_pairs, K, \
-                                 part_d, nch, H, sc_off_down, skip_zero, *shd, h_sh, y)
-    if (shd->fmt == 3) CS(3);
-    else if (shd->fmt == 2) CS(2);
-    else CS(0);
-#undef CS
-    return (int)hipGetLastError();
+    return combine_sh(recs, pair_exp, pair_w, tok_pairs, T, K, part_d, nullptr, nch, H, sc_off_down, skip_zero, shd,
+                      h_sh, y, s);
 }
 
 extern "C" int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
@@ -1006,14 +1079,25 @@ extern "C" int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                             int skip_zero, const float *sh, int sh_n, size_t sh_stride, float *y,
                             hipStream_t s)
 {
-    if (H % 4 || K < 1 || K > 64 || (sh && (sh_n < 1 || sh_stride % 4 || (uintptr_t)sh % 16)))
-        return (int)hipErrorInvalidValue;
-    dim3 grid((H + CMB_ROWS - 1) / CMB_ROWS, T);
-    const size_t lds = (size_t)K * (CMB_SLICES + 1) * (CMB_ROWS / 4) * sizeof(float4) + (size_t)K * 8;
-    WHIP_LAUNCH(k_combine, grid, dim3(256), lds, s,
-                recs, pair_exp, pair_w, tok_pairs, K, part_d, nch, H, sc_off_down, skip_zero, sh, sh_n,
-                sh_stride, y);
-    return (int)hipGetLastError();
+    return combine(recs, pair_exp, pair_w, tok_pairs, T, K, part_d, nullptr, nch, H, sc_off_down, skip_zero, sh,
+                   sh_n, sh_stride, y, s);
+}
+
+extern "C" int whip_combine_fold(const uint8_t *const *recs, const int32_t *pair_exp, const float *pair_w,
+                                 const int32_t *tok_pairs, int T, int K, const whip_fold *f, int H, int skip_zero,
+                                 const float *sh, int sh_n, size_t sh_stride, float *y, hipStream_t s)
+{
+    if (!f || !f->S || !f->ls || f->nb < 1 || f->sc_off % 2) return (int)hipErrorInvalidValue;
+    return combine(recs, pair_exp, pair_w, tok_pairs, T, K, nullptr, f, 1, H, 0, skip_zero, sh, sh_n, sh_stride, y,
+                   s);
+}
+
+extern "C" int whip_combine_sh_fold(const uint8_t *const *recs, const int32_t *pair_exp, const float *pair_w,
+                                    const int32_t *tok_pairs, int T, int K, const whip_fold *f, int H, int skip_zero,
+                                    const whip_mat *shd, const float *h_sh, float *y, hipStream_t s)
+{
+    if (!f || !f->S || !f->ls || f->nb < 1 || f->sc_off % 2) return (int)hipErrorInvalidValue;
+    return combine_sh(recs, pair_exp, pair_w, tok_pairs, T, K, nullptr, f, 1, H, 0, skip_zero, shd, h_sh, y, s);
 }
 
 // ---- materialised dequantisation (closed form, bit-exact) ------------------

@@ -193,102 +193,311 @@ extern "C" int whip_vq_rows_p6(const uint8_t *idx, const uint16_t *scale, const 
 }
 
 // ---- the device layer's VQ4P experts ------------------------------------------
-// vq_build_lut (src/model.c:3864-3880) for a batch of tables: table
-// t = (input row t / kinds, kind t % kinds) is
-//   lut[t][v][s][e] = sum_d x[8v + d] * C[cb + 4 kind + s][e][d]
-// in the engine's order for `fma`: one fused multiply-add chain over d from
-// zero (lutb_range_avx512, src/simd_avx512.c:90-123), else a rounded product
-// added to the running sum (waste_lutb_range, src/model.c:3815-3854).  A
-// thread owns one (stage, entry) and P6_LV positions; booksT is the books
-// transposed, [book][dim][64 entries], fp32 as the loader converts them.
-#define P6_LV 16
+// Four launches and the combine, each pair's rows the engine's bit for bit:
+//   k_p6_lutq      each token's gate and up tables, int8 per scale block;
+//   k_p6_tiles     every pair's gate and up rows: exact integer block sums;
+//   k_p6_act_lutq  the gate/up folds, SwiGLU and each pair's down table;
+//   k_p6_tiles     every pair's down rows, folded by the combine.
+// The fold of a row's block sums into fp32 runs in block order, so the block
+// sums wait in HBM (int16: a sum is at most 4 * 32 * 127 in magnitude) for
+// the launch that needs the row; the tile launches then stream the index
+// bytes through one staged table per workgroup, with no order between
+// blocks to keep.
+#define P6_TAB (P6_BLK * 4 * P6_EN)    // one scale block's int8 table, 8 KB
+#define P6_MAXB 32                     // gate/up blocks folded from registers
 
+// One scale block of a table: lut[v][s][e] = sum_d x[8v + d] * C[s][e][d]
+// (vq_build_lut, src/model.c:3864-3880) in the engine's order for FMA (one
+// fused multiply-add chain over d from zero: lutb_range_avx512,
+// src/simd_avx512.c:90-123; else a rounded product added to the running
+// sum: waste_lutb_range, src/model.c:3815-3854), then the block's scale
+// max|lut| / 127 and each entry's rint(lut * (127 / max)) clamped to
+// [-127, 127] (vq_quant_lut, src/model.c:3979-4074), as k_vq_quant_lut
+// does.  256 threads, thread (stage, entry); s_x holds the block's n
+// positions (8n values), CT the four stages' books transposed
+// ([stage][dim][64] fp32).  q: the block's first position of the table.
 template <bool FMA>
-__global__ void __launch_bounds__(256)
-k_p6_lutb(const void *__restrict__ x, int x_bf16, int x_ld, int kinds, const float *__restrict__ booksT,
-          int cb, int nv, float *__restrict__ lut)
+__device__ __forceinline__ void p6_lutq_block(const float *s_x, int n, const float *__restrict__ CT,
+                                              int8_t *__restrict__ q, float *__restrict__ scale)
 {
-    const int t = blockIdx.y, row = t / kinds, kind = t - row * kinds;
-    const int st = threadIdx.x >> 6, e = threadIdx.x & 63;
-    const float *CT = booksT + (size_t)(cb + 4 * kind + st) * 8 * P6_EN;
+    __shared__ float s_mx[4];
+    const int tid = threadIdx.x, st = tid >> 6, e = tid & 63;
+    const float *C = CT + (size_t)st * 8 * P6_EN;
     float c[8];
 #pragma unroll
-    for (int d = 0; d < 8; d++) c[d] = CT[d * P6_EN + e];
-    const int v0 = blockIdx.x * P6_LV, v1 = min(nv, v0 + P6_LV);
-    for (int v = v0; v < v1; v++) {
-        float xv[8];
-        if (x_bf16) {
-            const uint16_t *xr = (const uint16_t *)x + (size_t)row * x_ld + (size_t)v * 8;
+    for (int d = 0; d < 8; d++) c[d] = C[d * P6_EN + e];
+    float l[P6_BLK];
+    float mx = 0.0f;
 #pragma unroll
-            for (int d = 0; d < 8; d++) xv[d] = wh_bf16(xr[d]);
-        } else {
-            const float *xr = (const float *)x + (size_t)row * x_ld + (size_t)v * 8;
-#pragma unroll
-            for (int d = 0; d < 8; d++) xv[d] = xr[d];
-        }
+    for (int v = 0; v < P6_BLK; v++) {
         float a = 0.0f;
 #pragma unroll
-        for (int d = 0; d < 8; d++) a = FMA ? __fmaf_rn(xv[d], c[d], a) : __fadd_rn(a, __fmul_rn(xv[d], c[d]));
-        lut[((size_t)t * nv + v) * (4 * P6_EN) + st * P6_EN + e] = a;
+        for (int d = 0; d < 8; d++) {
+            const float xv = s_x[8 * v + d];
+            a = FMA ? __fmaf_rn(xv, c[d], a) : __fadd_rn(a, __fmul_rn(xv, c[d]));
+        }
+        l[v] = a;
+        if (v < n) mx = fmaxf(mx, fabsf(a));
     }
+    // the block's max |entry| (order-free: no NaN survives the fmaxf above)
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+    if (e == 0) s_mx[st] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
+    if (tid == 0) *scale = __fdiv_rn(mx, 127.0f);
+    const float inv = mx > 0.0f ? __fdiv_rn(127.0f, mx) : 0.0f;
+#pragma unroll
+    for (int v = 0; v < P6_BLK; v++)
+        if (v < n) {
+            const float t = rintf(__fmul_rn(l[v], inv));             // half to even, as lrintf
+            q[v * 4 * P6_EN + st * P6_EN + e] = (int8_t)(int)fminf(127.0f, fmaxf(-127.0f, t));
+        }
 }
 
-extern "C" int whip_p6_lutb(const void *x, int x_bf16, int x_ld, int rows, int kinds, const float *booksT, int cb,
-                            int nv, int fma, float *lut, hipStream_t s)
+// Tables of rows x kinds inputs, one scale block per workgroup: table
+// t = (row t / kinds, kind t % kinds) from x row t / kinds (bf16 or fp32)
+// and books cb + 4 kind ..; q[t][nv][4][64], scale[t][nb].
+template <bool FMA>
+__global__ void __launch_bounds__(256)
+k_p6_lutq(const void *__restrict__ x, int x_bf16, int x_ld, int kinds, const float *__restrict__ booksT, int cb,
+          int nv, int8_t *__restrict__ q, float *__restrict__ qs)
+{
+    __shared__ float s_x[8 * P6_BLK];
+    const int t = blockIdx.y, row = t / kinds, kind = t - row * kinds, b = blockIdx.x, i = threadIdx.x;
+    const int v0 = b * P6_BLK, n = min(P6_BLK, nv - v0);
+    float xv = 0.0f;                                 // past the block's positions: zeros, never used
+    if (i < 8 * n) {
+        const size_t o = (size_t)row * x_ld + (size_t)v0 * 8 + i;
+        xv = x_bf16 ? wh_bf16(((const uint16_t *)x)[o]) : ((const float *)x)[o];
+    }
+    s_x[i] = xv;
+    __syncthreads();
+    p6_lutq_block<FMA>(s_x, n, booksT + (size_t)(cb + 4 * kind) * 8 * P6_EN, q + ((size_t)t * nv + v0) * 4 * P6_EN,
+                       qs + (size_t)t * gridDim.x + b);
+}
+
+extern "C" int whip_p6_lutq(const void *x, int x_bf16, int x_ld, int rows, int kinds, const float *booksT, int cb,
+                            int nv, int fma, int8_t *q, float *qs, hipStream_t s)
 {
     if (rows <= 0 || kinds <= 0 || rows * kinds > 65535 || nv <= 0 || x_ld < nv * 8 || cb < 0)
         return (int)hipErrorInvalidValue;
-    const dim3 grid((nv + P6_LV - 1) / P6_LV, rows * kinds);
-    if (fma) hipLaunchKernelGGL(k_p6_lutb<true>, grid, dim3(256), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, lut);
-    else hipLaunchKernelGGL(k_p6_lutb<false>, grid, dim3(256), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, lut);
+    const dim3 grid((nv + P6_BLK - 1) / P6_BLK, rows * kinds);
+    if (fma) WHIP_LAUNCH(k_p6_lutq<true>, grid, dim3(256), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, q, qs);
+    else WHIP_LAUNCH(k_p6_lutq<false>, grid, dim3(256), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, q, qs);
     return (int)hipGetLastError();
 }
 
-// vq_apply's rows (src/model.c:4152-4171) of every pair: grid (row blocks,
-// pairs, kinds).  Pair p's matrix `kind` is at idx_off[kind] of its
-// expert's record, its f16 row scales at sc_off[kind]; its table is
-// pair_tok[p] * kinds + kind (per_tok: the token's gate/up tables) or p
-// (its own, the down projection's).  out[p][kind][M].  An unbound expert
-// writes zeros and raises bit 0 of err.
-template <bool FMA>
+// Block sums of every pair's rows.  A workgroup takes one (pair, kind), a
+// group of up to P6_MAXG consecutive scale blocks and a run of `per` 64-row
+// blocks: it stages the group's tables once, and its wavefronts take the
+// tiles (row block, scale block) in turn, two in flight per wavefront.  A
+// tile is 32 positions of 64 rows, 192 contiguous bytes a position (three
+// code bytes a row).  Lane (quad q = lane % 16, slot k = lane / 16) loads
+// the 12 bytes of rows 4q .. 4q+3 at positions k, k+4, .., k+28 (one
+// 16-lane group per position: eight 12-byte loads a tile), adds four table
+// bytes per row and position, and the four slots' sums meet across lanes
+// (exact integer sums, in any order).  A position's table is 256 bytes,
+// 64 apart in LDS (a 320-byte stride), so the four positions one load
+// instruction reads sit in four disjoint groups of sixteen banks and no two
+// lanes of a group meet in a bank unless they read one dword: the lookups
+// do not conflict.  S[(pk * nb + b) * M + r], pk = pair * kinds + kind.  An
+// unbound expert writes zeros and raises bit 0 of err.
+#define P6_MAXG 6                      // scale blocks a workgroup stages
+#define P6_TS 320                      // LDS bytes a position's table takes
+
 __global__ void __launch_bounds__(P6_THREADS)
-k_p6_rows_pairs(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
-                const int32_t *__restrict__ pair_tok, int kinds, uint32_t idx_off0, uint32_t idx_off1,
-                uint32_t sc_off0, uint32_t sc_off1, int M, int nv, const int8_t *__restrict__ q,
-                const float *__restrict__ qs, int per_tok, float *__restrict__ out, int *__restrict__ err)
+k_p6_tiles(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
+           const int32_t *__restrict__ pair_tok, int kinds, uint32_t idx_off0, uint32_t idx_off1, int M, int nv,
+           int nb, const int8_t *__restrict__ q, int per_tok, int ncb, int ngrp, int shares, int per,
+           int16_t *__restrict__ S, int *__restrict__ err)
 {
-    const int p = blockIdx.y, kind = blockIdx.z, rb = blockIdx.x;
+    __shared__ __align__(16) int8_t s_tab[P6_MAXG * P6_BLK * P6_TS];
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = blockIdx.x % shares, rest = blockIdx.x / shares;
+    const int bg = rest % ngrp, pk = rest / ngrp, kind = pk % kinds, p = pk / kinds;
+    const int b0 = bg * ncb, nbg = min(ncb, nb - b0);
+    const int rb0 = j * per, rb1 = min(M / 64, rb0 + per), ntile = nbg * (rb1 - rb0);
+    int16_t *out = S + ((size_t)pk * nb + b0) * M;   // block b0 + bl at out + bl * M
     const uint8_t *rec = recs[pair_exp[p]];
-    float *y = out + ((size_t)p * kinds + kind) * M;
     if (rec == nullptr) {                            // uniform
-        if (threadIdx.x < 64 && rb * 64 + (int)threadIdx.x < M) y[rb * 64 + threadIdx.x] = 0.0f;
-        if (threadIdx.x == 0) atomicOr(err, 1);
+        for (int bl = 0; bl < nbg; bl++)
+            for (int r = rb0 * 64 + tid; r < rb1 * 64; r += P6_THREADS) out[(size_t)bl * M + r] = 0;
+        if (tid == 0) atomicOr(err, 1);
         return;
     }
     const size_t tab = per_tok ? (size_t)pair_tok[p] * kinds + kind : (size_t)p;
-    const int nblk = (nv + P6_BLK - 1) / P6_BLK;
-    p6_rows<FMA>(rec + (kind ? idx_off1 : idx_off0), (const uint16_t *)(rec + (kind ? sc_off1 : sc_off0)),
-                 q + tab * nv * (4 * P6_EN), qs + tab * nblk, rb, M, nv, y);
+    // the group's tables (positions b0*32 .., 16 uint4 each), to LDS at a
+    // 320-byte stride; the loads go out before any tile's
+    const int v_lo = b0 * P6_BLK, nq = (min(nv, v_lo + nbg * P6_BLK) - v_lo) * 16;
+    const uint4 *tsrc = (const uint4 *)(q + (tab * nv + v_lo) * 4 * P6_EN);
+    constexpr int TV = P6_MAXG * P6_BLK * 16 / P6_THREADS;
+    uint4 tv[TV];
+#pragma unroll
+    for (int k = 0; k < TV; k++) tv[k] = tsrc[tid + k * P6_THREADS < nq ? tid + k * P6_THREADS : 0];
+    g_u8 *mat = as_global(rec) + (kind ? idx_off1 : idx_off0);
+    const int qd = lane & 15, slot = lane >> 4;
+    // tile t: scale block b0 + t % nbg, row block rb0 + t / nbg; positions
+    // past a short block load position 0 (in bounds; their sums not added)
+    auto load = [&](uint3 (&c)[P6_BLK / 4], int t) {
+        const int bl = t % nbg, rb = rb0 + t / nbg;
+        const int n = min(P6_BLK, nv - (b0 + bl) * P6_BLK);
+        g_u8 *ix = mat + ((size_t)rb * nv + (size_t)(b0 + bl) * P6_BLK) * 192 + 12 * qd;
+#pragma unroll
+        for (int i = 0; i < P6_BLK / 4; i++) {
+            const int v = 4 * i + slot;
+            c[i] = *(const uint3 WH_GLOBAL *)(ix + (size_t)(v < n ? v : 0) * 192);
+        }
+    };
+    auto sum_tile = [&](const uint3 (&c)[P6_BLK / 4], int t) {
+        const int bl = t % nbg, rb = rb0 + t / nbg;
+        const int n = min(P6_BLK, nv - (b0 + bl) * P6_BLK);
+        const int8_t *Tb = s_tab + bl * P6_BLK * P6_TS;
+        int s4[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < P6_BLK / 4; i++) {
+            const int v = 4 * i + slot;
+            const uint32_t cc[4] = {c[i].x, __builtin_amdgcn_alignbyte(c[i].y, c[i].x, 3),
+                                    __builtin_amdgcn_alignbyte(c[i].z, c[i].y, 2), c[i].z >> 8};
+            const int8_t *T = Tb + v * P6_TS;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int e = T[cc[k] & 63] + T[P6_EN + ((cc[k] >> 6) & 63)] +
+                              T[2 * P6_EN + ((cc[k] >> 12) & 63)] + T[3 * P6_EN + ((cc[k] >> 18) & 63)];
+                s4[k] += v < n ? e : 0;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const auto a = __builtin_amdgcn_permlane16_swap(s4[k], s4[k], false, false);
+            s4[k] = (int)a[0] + (int)a[1];
+            const auto b = __builtin_amdgcn_permlane32_swap(s4[k], s4[k], false, false);
+            s4[k] = (int)b[0] + (int)b[1];
+        }
+        // each of the four lanes of a quad stores one of its rows
+        const int mine = slot == 0 ? s4[0] : slot == 1 ? s4[1] : slot == 2 ? s4[2] : s4[3];
+        out[(size_t)bl * M + rb * 64 + 4 * qd + slot] = (int16_t)mine;
+    };
+    // the wavefront's tiles wv + 16 i, i < cnt; every load is unconditional
+    // (past the last tile: the last again), and the scheduling barriers keep
+    // each buffer's loads together and in order, so a wait for one buffer
+    // never covers the other's
+    const int cnt = wv < ntile ? (ntile - wv + P6_WAVES - 1) / P6_WAVES : 0;
+    auto tile_at = [&](int i) { return cnt > 0 ? wv + min(i, cnt - 1) * P6_WAVES : 0; };
+    uint3 cA[P6_BLK / 4], cB[P6_BLK / 4];
+    load(cA, tile_at(0));
+    __builtin_amdgcn_sched_barrier(0);
+    load(cB, tile_at(1));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < TV; k++) {                   // past nq: unused bytes
+        const int g = tid + k * P6_THREADS;
+        *(uint4 *)(s_tab + (g >> 4) * P6_TS + (g & 15) * 16) = tv[k];
+    }
+    __syncthreads();
+    for (int i = 0; i < cnt; i += 2) {               // uniform
+        sum_tile(cA, tile_at(i));
+        __builtin_amdgcn_sched_barrier(0);
+        load(cA, tile_at(i + 2));
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < cnt) sum_tile(cB, tile_at(i + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        load(cB, tile_at(i + 3));
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
-extern "C" int whip_p6_rows_pairs(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok,
-                                  int P, int kinds, const uint32_t *idx_off, const uint32_t *sc_off, int M, int nv,
-                                  const int8_t *q, const float *qs, int per_tok, int fma, float *out, int *err,
-                                  hipStream_t s)
+extern "C" int whip_p6_tiles(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                             int kinds, const uint32_t *idx_off, int M, int nv, const int8_t *q, int per_tok,
+                             int16_t *S, int *err, hipStream_t s)
 {
-    if (P <= 0 || P > 65535 || kinds < 1 || kinds > 2 || M <= 0 || nv <= 0 || (uintptr_t)q % 16)
+    if (P <= 0 || kinds < 1 || kinds > 2 || M <= 0 || M % 64 || nv <= 0 || (uintptr_t)q % 16 || idx_off[0] % 4 ||
+        (kinds > 1 && idx_off[1] % 4))
         return (int)hipErrorInvalidValue;
-    const dim3 grid((M + 63) / 64, P, kinds);
-    const uint32_t i1 = kinds > 1 ? idx_off[1] : 0, s1 = kinds > 1 ? sc_off[1] : 0;
-    if (fma)
-        hipLaunchKernelGGL(k_p6_rows_pairs<true>, grid, dim3(P6_THREADS), 0, s, recs, pair_exp, pair_tok, kinds,
-                           idx_off[0], i1, sc_off[0], s1, M, nv, q, qs, per_tok, out, err);
-    else
-        hipLaunchKernelGGL(k_p6_rows_pairs<false>, grid, dim3(P6_THREADS), 0, s, recs, pair_exp, pair_tok, kinds,
-                           idx_off[0], i1, sc_off[0], s1, M, nv, q, qs, per_tok, out, err);
+    const int nb = (nv + P6_BLK - 1) / P6_BLK, nrb = M / 64;
+    // runs of at most 32 row blocks; groups of scale blocks so that the
+    // launch is about one workgroup per CU
+    long shares = (nrb + 31) / 32;
+    const int per = (int)((nrb + shares - 1) / shares);
+    shares = (nrb + per - 1) / per;
+    const long tiles = (long)P * kinds * nb * nrb, want = (tiles + 255) / 256;
+    long ncb = (2 * want + per) / (2 * per);         // rounded
+    if (ncb > P6_MAXG) ncb = P6_MAXG;
+    if (ncb > nb) ncb = nb;
+    if (ncb < 1) ncb = 1;
+    const long ngrp = (nb + ncb - 1) / ncb, grid = (long)P * kinds * ngrp * shares;
+    if (grid > 0x7fffffffL) return (int)hipErrorInvalidValue;
+    const uint32_t i1 = kinds > 1 ? idx_off[1] : 0;
+    WHIP_LAUNCH(k_p6_tiles, dim3((unsigned)grid), dim3(P6_THREADS), 0, s, recs, pair_exp, pair_tok, kinds,
+                idx_off[0], i1, M, nv, nb, q, per_tok, (int)ncb, (int)ngrp, (int)shares, per, S, err);
     return (int)hipGetLastError();
 }
+// The gate/up rows of pair p (I of each), folded from their block sums in
+// block order with the token's table scales and scaled by the row's f16
+// scale (vq_rows_p6's fold, src/model.c:4076-4114), then h = silu(g) * u
+// (waste_act_pair_range), then the pair's down table block from h: a
+// workgroup per (down block, pair), thread i the row 8 v0 + i of h.
+template <bool FMA>
+__global__ void __launch_bounds__(256)
+k_p6_act_lutq(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
+              const int32_t *__restrict__ pair_tok, const int16_t *__restrict__ S, const float *__restrict__ qs_gu,
+              uint32_t sc_gate, uint32_t sc_up, int I, int nb_gu, const float *__restrict__ booksT, int cb_d,
+              int nv_d, int8_t *__restrict__ q_d, float *__restrict__ qs_d)
+{
+    __shared__ float s_x[8 * P6_BLK];
+    const int b = blockIdx.x, p = blockIdx.y, i = threadIdx.x;
+    const int v0 = b * P6_BLK, n = min(P6_BLK, nv_d - v0), r = v0 * 8 + (i < 8 * n ? i : 0);
+    // the rows' block sums go out first (they need no record), then the
+    // record's scales; a thread past the block's rows reads the first row
+    const int16_t *Sg = S + (size_t)p * 2 * nb_gu * I + r, *Su = Sg + (size_t)nb_gu * I;
+    const float *lg = qs_gu + (size_t)pair_tok[p] * 2 * nb_gu, *lu = lg + nb_gu;
+    const uint8_t *rec = recs[pair_exp[p]];
+    float ag = 0.0f, au = 0.0f;
+    for (int k0 = 0; k0 < nb_gu; k0 += P6_MAXB) {    // one round unless nb_gu > P6_MAXB
+        // every block's sums in flight at once, then the folds in order
+        const int kn = min(P6_MAXB, nb_gu - k0);
+        int16_t sg[P6_MAXB], su[P6_MAXB];
+#pragma unroll
+        for (int k = 0; k < P6_MAXB; k++) {
+            const int kk = k0 + (k < kn ? k : 0);
+            sg[k] = Sg[(size_t)kk * I];
+            su[k] = Su[(size_t)kk * I];
+        }
+#pragma unroll
+        for (int k = 0; k < P6_MAXB; k++)
+            if (k < kn) {
+                const float fg = (float)sg[k], fu = (float)su[k];
+                ag = FMA ? __fmaf_rn(lg[k0 + k], fg, ag) : __fadd_rn(ag, __fmul_rn(lg[k0 + k], fg));
+                au = FMA ? __fmaf_rn(lu[k0 + k], fu, au) : __fadd_rn(au, __fmul_rn(lu[k0 + k], fu));
+            }
+    }
+    float g = 0.0f, u = 0.0f;                        // an unbound expert's rows: zeros
+    if (rec != nullptr) {
+        g = __fmul_rn(ag, wh_f16_scale(((const uint16_t *)(rec + sc_gate))[r]));
+        u = __fmul_rn(au, wh_f16_scale(((const uint16_t *)(rec + sc_up))[r]));
+    }
+    s_x[i] = i < 8 * n ? wh_silu_mul(g, u) : 0.0f;
+    __syncthreads();
+    p6_lutq_block<FMA>(s_x, n, booksT + (size_t)cb_d * 8 * P6_EN, q_d + ((size_t)p * nv_d + v0) * 4 * P6_EN,
+                       qs_d + (size_t)p * gridDim.x + b);
+}
 
+extern "C" int whip_p6_act_lutq(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                                const int16_t *S, const float *qs_gu, uint32_t sc_gate, uint32_t sc_up, int I,
+                                int nv_gu, const float *booksT, int cb_d, int nv_d, int fma, int8_t *q_d,
+                                float *qs_d, hipStream_t s)
+{
+    if (P <= 0 || P > 65535 || I <= 0 || I != nv_d * 8 || nv_gu <= 0 || cb_d < 0 || sc_gate % 2 || sc_up % 2)
+        return (int)hipErrorInvalidValue;
+    const int nb_gu = (nv_gu + P6_BLK - 1) / P6_BLK;
+    const dim3 grid((nv_d + P6_BLK - 1) / P6_BLK, P);
+#define AL(F) WHIP_LAUNCH(k_p6_act_lutq<F>, grid, dim3(256), 0, s, recs, pair_exp, pair_tok, S, qs_gu, sc_gate, \
+                          sc_up, I, nb_gu, booksT, cb_d, nv_d, q_d, qs_d)
+    if (fma) AL(true);
+    else AL(false);
+#undef AL
+    return (int)hipGetLastError();
+}
 // waste_act_pair_range (src/model.c): h = silu(g) * u for each pair's rows,
 // gu[p][0][I] the gate rows, gu[p][1][I] the up rows, h[p][I].
 __global__ void __launch_bounds__(256)

@@ -93,10 +93,11 @@ struct waste_hip_moe {
     int r2;                      /* VQ2R experts: two stages of 256 entries */
     int bpp;                     /* index bytes a (row, position)          */
     struct {
-        float *lut_gu, *lut_d;   /* fp32 tables [T][2][nv_gu][256], [P][nv_d][256] */
-        int8_t *q_gu, *q_d;      /* their int8 copies                      */
-        float *s_gu, *s_d;       /* and scales, one per 32 positions       */
-        float *gu, *h, *down;    /* rows [P][2][I], SwiGLU [P][I], down [P][H] */
+        float *lut_gu, *lut_d;   /* VQ2R: fp32 tables [T][2][nv_gu][512], [P][nv_d][512] */
+        int8_t *q_gu, *q_d;      /* VQ4P: int8 tables [T][2][nv_gu][256], [P][nv_d][256] */
+        float *s_gu, *s_d;       /* and their scales, one per 32 positions */
+        int16_t *S_gu, *S_d;     /* VQ4P block sums [P][2][nb_gu][I], [P][nb_d][H] */
+        float *gu, *h, *down;    /* VQ2R: rows [P][2][I], SwiGLU [P][I], down [P][H] */
     } p6b;
     /* few-token products on the matrix cores (skinny.hip): column slices of
      * the router, the shared gate/up and the shared down (0: not taken),
@@ -157,7 +158,8 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->b.tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
                      m->sh_h16, m->x16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->b.pair_rec,
                      m->b.rcnt, m->b.xchg, m->sk_mem, m->p6b.lut_gu, m->p6b.lut_d, m->p6b.q_gu,
-                     m->p6b.q_d, m->p6b.s_gu, m->p6b.s_d, m->p6b.gu, m->p6b.h, m->p6b.down };
+                     m->p6b.q_d, m->p6b.s_gu, m->p6b.s_d, m->p6b.S_gu, m->p6b.S_d, m->p6b.gu, m->p6b.h,
+                     m->p6b.down };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0]) {
         for (int i = 0; i <= WASTE_HIP_STAGES; i++) hipEventDestroy(m->ev[i]);
@@ -263,15 +265,12 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
     } else if (m->p6) {
         const size_t tg = (size_t)m->nv_gu * 256, td = (size_t)m->nv_d * 256;
         const size_t bg = (size_t)(m->nv_gu + 31) / 32, bd = (size_t)(m->nv_d + 31) / 32;
-        rc |= dmalloc((void **)&m->p6b.lut_gu, (size_t)m->T * 2 * tg * 4);
         rc |= dmalloc((void **)&m->p6b.q_gu, (size_t)m->T * 2 * tg);
         rc |= dmalloc((void **)&m->p6b.s_gu, (size_t)m->T * 2 * bg * 4);
-        rc |= dmalloc((void **)&m->p6b.lut_d, (size_t)P * td * 4);
         rc |= dmalloc((void **)&m->p6b.q_d, (size_t)P * td);
         rc |= dmalloc((void **)&m->p6b.s_d, (size_t)P * bd * 4);
-        rc |= dmalloc((void **)&m->p6b.gu, (size_t)P * 2 * m->I * 4);
-        rc |= dmalloc((void **)&m->p6b.h, (size_t)P * m->I * 4);
-        rc |= dmalloc((void **)&m->p6b.down, (size_t)P * m->H * 4);
+        rc |= dmalloc((void **)&m->p6b.S_gu, (size_t)P * 2 * bg * m->I * 2);
+        rc |= dmalloc((void **)&m->p6b.S_d, (size_t)P * bd * m->H * 2);
     } else {
         /* + 64 floats: the apply kernels' sink for rows past a split's end */
         rc |= dmalloc((void **)&m->b.part_gu, ((size_t)Pd * 2 * m->nch_gu * m->I + 64) * 4);
@@ -794,13 +793,16 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
 
 /* VQ4P experts (index_bits 6), moe_layer's order at T = 1 and moe_chunk's
  * above (src/model.c:5876-5910, 7203-7251), on the routing and pair lists
- * route() left: each token's gate and up tables (fp32, then int8 with one
- * scale per 32 positions: vq_build_lut), every pair's gate and up rows
- * through them (vq_rows_p6), SwiGLU, the pair's down table from its
- * SwiGLU output and its down rows, then the combine and the shared expert
- * as for VQ3R.  The tables and rows follow the engine's arithmetic in the
- * layer's p6_order, so each pair's rows are the engine's bit for bit. */
-static int alt_combine(waste_hip_moe *m, int T, float *y, hipStream_t s);
+ * route() left: each token's gate and up tables (fp32 by vq_build_lut, then
+ * int8 with one scale per 32 positions), every pair's gate and up rows
+ * through them (vq_rows_p6: exact integer sums per scale block, folded into
+ * fp32 in block order), SwiGLU, the pair's down table from its SwiGLU
+ * output and its down rows, then the combine and the shared expert as for
+ * VQ3R.  Four launches and the combine: the block sums wait in HBM for the
+ * launch that folds them (the down table build, the combine).  The tables
+ * and folds follow the engine's arithmetic in the layer's p6_order, so each
+ * pair's rows are the engine's bit for bit. */
+static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, hipStream_t s);
 
 static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
 {
@@ -808,23 +810,21 @@ static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
     const int cb = m->cb - m->book0;
     m->ktimed = 0;               /* these stages are timed by the events around them */
     MARK(2);
-    CK((hipError_t)whip_p6_lutb(x, x_bf16, H, T, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.lut_gu, s));
-    CK((hipError_t)whip_vq_quant_lut_n(m->p6b.lut_gu, m->nv_gu, 4, 64, 2 * T, m->p6b.q_gu, m->p6b.s_gu, s));
+    CK((hipError_t)whip_p6_lutq(x, x_bf16, H, T, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.q_gu, m->p6b.s_gu, s));
     const uint32_t gu_idx[2] = { m->off_gate, m->off_up };
-    const uint32_t gu_sc[2] = { m->off_sc, m->off_sc + 2u * (uint32_t)I };
-    CK((hipError_t)whip_p6_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 2, gu_idx, gu_sc, I, m->nv_gu,
-                                      m->p6b.q_gu, m->p6b.s_gu, 1, fma, m->p6b.gu, m->err, s));
+    CK((hipError_t)whip_p6_tiles(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 2, gu_idx, I, m->nv_gu, m->p6b.q_gu,
+                                 1, m->p6b.S_gu, m->err, s));
     MARK(3);
-    CK((hipError_t)whip_p6_act(m->p6b.gu, P, I, m->p6b.h, s));
+    CK((hipError_t)whip_p6_act_lutq(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, m->p6b.S_gu, m->p6b.s_gu,
+                                    m->off_sc, m->off_sc + 2u * (uint32_t)I, I, m->nv_gu, m->d_booksT,
+                                    cb + 2 * m->stages, m->nv_d, fma, m->p6b.q_d, m->p6b.s_d, s));
     MARK(4);
-    CK((hipError_t)whip_p6_lutb(m->p6b.h, 0, I, P, 1, m->d_booksT, cb + 2 * m->stages, m->nv_d, fma,
-                                m->p6b.lut_d, s));
-    CK((hipError_t)whip_vq_quant_lut_n(m->p6b.lut_d, m->nv_d, 4, 64, P, m->p6b.q_d, m->p6b.s_d, s));
-    const uint32_t d_idx[1] = { m->off_down }, d_sc[1] = { m->off_sc + 4u * (uint32_t)I };
-    CK((hipError_t)whip_p6_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, d_sc, H, m->nv_d,
-                                      m->p6b.q_d, m->p6b.s_d, 0, fma, m->p6b.down, m->err, s));
+    const uint32_t d_idx[1] = { m->off_down };
+    CK((hipError_t)whip_p6_tiles(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, H, m->nv_d, m->p6b.q_d, 0,
+                                 m->p6b.S_d, m->err, s));
     MARK(5);
-    return alt_combine(m, T, y, s);
+    const whip_fold f = { m->p6b.S_d, m->p6b.s_d, (m->nv_d + 31) / 32, m->off_sc + 4u * (uint32_t)I, fma };
+    return alt_combine(m, T, y, &f, s);
 }
 
 /* VQ2R experts (two stages of 256 entries), the same order as VQ4P's above
@@ -853,19 +853,21 @@ static int experts_r2(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
     CK((hipError_t)whip_r2_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, d_sc, H, m->nv_d,
                                       m->p6b.lut_d, 0, m->p6b.down, m->err, s));
     MARK(5);
-    return alt_combine(m, T, y, s);
+    return alt_combine(m, T, y, NULL, s);
 }
 
-/* The combine of the VQ4P / VQ2R paths: each pair's down rows in
- * p6b.down, already scaled, one chunk each; the shared expert as for
- * VQ3R. */
-static int alt_combine(waste_hip_moe *m, int T, float *y, hipStream_t s)
+/* The combine of the VQ4P / VQ2R paths: each pair's down rows folded from
+ * f (VQ4P) or in p6b.down, already scaled, one chunk each (VQ2R); the
+ * shared expert as for VQ3R. */
+static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, hipStream_t s)
 {
     const int K = m->K, H = m->H;
     if (m->sh_in_combine) {
         MARK(6);
-        const int rc = whip_combine_sh(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->p6b.down,
-                                       1, H, 0, T > 1, &m->sh[2], m->b.h_sh, y, s);
+        const int rc = f ? whip_combine_sh_fold(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, f, H,
+                                                T > 1, &m->sh[2], m->b.h_sh, y, s)
+                         : whip_combine_sh(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K,
+                                           m->p6b.down, 1, H, 0, T > 1, &m->sh[2], m->b.h_sh, y, s);
         if (rc == 0) {
             MARK(7);
             return prof_end(m);
@@ -888,8 +890,12 @@ static int alt_combine(waste_hip_moe *m, int T, float *y, hipStream_t s)
         }
     }
     MARK(6);
-    CK((hipError_t)whip_combine(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->p6b.down, 1, H,
-                                0, T > 1, shp, sh_n, (size_t)T * H, y, s));
+    if (f)
+        CK((hipError_t)whip_combine_fold(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, f, H, T > 1,
+                                         shp, sh_n, (size_t)T * H, y, s));
+    else
+        CK((hipError_t)whip_combine(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, m->p6b.down, 1,
+                                    H, 0, T > 1, shp, sh_n, (size_t)T * H, y, s));
     MARK(7);
     return prof_end(m);
 }
