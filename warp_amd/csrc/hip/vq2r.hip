@@ -59,22 +59,25 @@ extern "C" int whip_r2_lutb(const void *x, int x_bf16, int x_ld, int rows, int k
     return (int)hipGetLastError();
 }
 
-// vq_rows of every pair's matrices, two stages: grid (row blocks, pairs,
-// kinds), a lane per row.  Pair p's matrix `kind` is at idx_off[kind] of its
-// expert's record (indices blocked [row / 64][v][row % 64][2]), its f16 row
-// scales at sc_off[kind]; its table is pair_tok[p] * kinds + kind (per_tok)
-// or p.  out[p][kind][M].  An unbound expert writes zeros and raises bit 0
-// of err.
+// vq_rows of every pair's matrices, two stages: grid (row-block groups,
+// pairs, kinds), a lane per row.  Pair p's matrix `kind` is at idx_off[kind]
+// of its expert's record (indices blocked [row / 64][v][row % 64][2]), its
+// f16 row scales at sc_off[kind]; its table is pair_tok[p] * kinds + kind
+// (per_tok) or p.  out[p][kind][M].  An unbound expert writes zeros and
+// raises bit 0 of err.
 //
-// A row's sum runs over the positions in order, so one lane owns it; the
-// loads do not depend on that order.  Four wavefronts share a 64-row block:
-// each round, wavefront w fetches the codes of positions 64 round + 16 w ..
-// (the next round's already in flight) and their two table entries, and
-// leaves the entries' sums in LDS; wavefront 0 then adds the round's 64
-// positions in order while the others fetch the next round.
+// A row's sum runs over the positions in order, so one lane owns it.  The
+// table entries a lane needs are random within each position's 2 KB: read
+// through the vector memory path that is one cache-line lookup per lane
+// group, read from LDS a few bank cycles.  So a workgroup of R2_WAVES
+// wavefronts (one 64-row block each, one matrix) streams the table through
+// LDS R2_W positions at a time, double-buffered: each round the next
+// window's entries and codes are in flight while the wavefronts add the
+// current window's.
 #define R2_WAVES 4
-#define R2_PW 16                       // positions a wavefront fetches a round
-#define R2_ROUND (R2_WAVES * R2_PW)
+#define R2_W 8                         // positions a round
+#define R2_WIN (R2_W * 2 * R2_EN)      // floats of a window
+#define R2_TV (R2_WIN / 4 / (R2_WAVES * 64))   // uint4s a thread stages a round
 
 __global__ void __launch_bounds__(R2_WAVES * 64)
 k_r2_rows_pairs(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
@@ -82,7 +85,99 @@ k_r2_rows_pairs(const uint8_t *const *__restrict__ recs, const int32_t *__restri
                 uint32_t sc_off0, uint32_t sc_off1, int M, int nv, const float *__restrict__ lut, int per_tok,
                 float *__restrict__ out, int *__restrict__ err)
 {
-    __shared__ float s_t[2][R2_ROUND][64];
+    __shared__ __align__(16) float s_l[2][R2_WIN];
+    const int p = blockIdx.y, kind = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rb = blockIdx.x * R2_WAVES + wv, r = rb * 64 + lane;
+    const bool live = r < M;
+    const uint8_t *rec = recs[pair_exp[p]];
+    float *y = out + ((size_t)p * kinds + kind) * M;
+    if (rec == nullptr) {                            // uniform
+        if (live) y[r] = 0.0f;
+        if (tid == 0) atomicOr(err, 1);
+        return;
+    }
+    const size_t tab = per_tok ? (size_t)pair_tok[p] * kinds + kind : (size_t)p;
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));   // promoted to registers, unlike uint4 here
+    const v4u WH_GLOBAL *L = (const v4u WH_GLOBAL *)(lut + tab * nv * 2 * R2_EN);
+    // rows past M read row 0's codes (in bounds; not stored)
+    const uint16_t WH_GLOBAL *ix =
+        (const uint16_t WH_GLOBAL *)(as_global(rec) + (kind ? idx_off1 : idx_off0)) +
+        (live ? (size_t)rb * nv * 64 + lane : 0);
+    const int nr = (nv + R2_W - 1) / R2_W, nq = nv * 2 * R2_EN / 4;
+    // round rr: the window's uint4s (past the table: its first ones, unused)
+    // and this lane's codes (past nv: the last position's, not added)
+    auto fetch = [&](v4u (&tv)[R2_TV], uint32_t (&w)[R2_W], int rr) {
+        const int q0 = rr * (R2_WIN / 4);
+#pragma unroll
+        for (int k = 0; k < R2_TV; k++) {
+            const int q = q0 + tid + k * R2_WAVES * 64;
+            tv[k] = L[q < nq ? q : 0];
+        }
+#pragma unroll
+        for (int k = 0; k < R2_W; k++) w[k] = ix[(size_t)min(rr * R2_W + k, nv - 1) * 64];
+    };
+    auto stage = [&](const v4u (&tv)[R2_TV], int b) {
+#pragma unroll
+        for (int k = 0; k < R2_TV; k++) ((v4u *)s_l[b])[tid + k * R2_WAVES * 64] = tv[k];
+    };
+    float acc = 0.0f;
+    auto add = [&](const uint32_t (&w)[R2_W], int rr, int b) {
+        const int n = min(R2_W, nv - rr * R2_W);
+#pragma unroll
+        for (int k = 0; k < R2_W; k++) {
+            const float *blk = s_l[b] + k * 2 * R2_EN;
+            const float t = __fadd_rn(blk[w[k] & 255], blk[R2_EN + (w[k] >> 8)]);
+            acc = k < n ? __fadd_rn(acc, t) : acc;
+        }
+    };
+    v4u tA[R2_TV], tB[R2_TV];
+    uint32_t wA[R2_W], wB[R2_W];
+    fetch(tA, wA, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    stage(tA, 0);
+    fetch(tB, wB, 1);                                // past the last round: harmless repeats
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    for (int rr = 0; rr < nr; rr += 2) {             // uniform
+        add(wA, rr, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        stage(tB, 1);                                // window rr + 1: its loads went out a round ago
+        __syncthreads();                             // (and every wavefront is done with window rr)
+        fetch(tA, wA, rr + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        add(wB, rr + 1, 1);                          // past the last round: adds nothing
+        __builtin_amdgcn_sched_barrier(0);
+        stage(tA, 0);
+        __syncthreads();
+        fetch(tB, wB, rr + 3);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (live) {
+        const uint16_t *sc = (const uint16_t *)(rec + (kind ? sc_off1 : sc_off0));
+        y[r] = __fmul_rn(acc, wh_f16_scale(sc[r]));
+    }
+}
+
+// The same rows with the entries fetched through the vector memory path,
+// for launches with too few rows a table to spread the LDS kernel's
+// workgroups over the CUs: grid (row blocks, pairs, kinds).  Four
+// wavefronts share a 64-row block: each round, wavefront w fetches the
+// codes of positions 64 round + 16 w .. (the next round's already in
+// flight) and their two table entries, and leaves the entries' sums in LDS;
+// wavefront 0 then adds the round's 64 positions in order while the others
+// fetch the next round.
+#define R2F_WAVES 4
+#define R2F_PW 16                       // positions a wavefront fetches a round
+#define R2F_ROUND (R2F_WAVES * R2F_PW)
+
+__global__ void __launch_bounds__(R2F_WAVES * 64)
+k_r2_rows_fetch(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
+                const int32_t *__restrict__ pair_tok, int kinds, uint32_t idx_off0, uint32_t idx_off1,
+                uint32_t sc_off0, uint32_t sc_off1, int M, int nv, const float *__restrict__ lut, int per_tok,
+                float *__restrict__ out, int *__restrict__ err)
+{
+    __shared__ float s_t[2][R2F_ROUND][64];
     const int p = blockIdx.y, kind = blockIdx.z, rb = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = rb * 64 + lane;
@@ -99,37 +194,37 @@ k_r2_rows_pairs(const uint8_t *const *__restrict__ recs, const int32_t *__restri
     const uint16_t WH_GLOBAL *ix =
         (const uint16_t WH_GLOBAL *)(as_global(rec) + (kind ? idx_off1 : idx_off0) + (size_t)rb * nv * 128) +
         (r < M ? lane : 0);
-    const int nr = (nv + R2_ROUND - 1) / R2_ROUND;
+    const int nr = (nv + R2F_ROUND - 1) / R2F_ROUND;
     // the codes of this wavefront's positions in round rr (past nv: the last
     // position's, not added)
-    auto fetch = [&](uint32_t (&w)[R2_PW], int rr) {
+    auto fetch = [&](uint32_t (&w)[R2F_PW], int rr) {
 #pragma unroll
-        for (int k = 0; k < R2_PW; k++) {
-            const int v = min(rr * R2_ROUND + wv * R2_PW + k, nv - 1);
+        for (int k = 0; k < R2F_PW; k++) {
+            const int v = min(rr * R2F_ROUND + wv * R2F_PW + k, nv - 1);
             w[k] = ix[(size_t)v * 64];
         }
     };
-    auto gather = [&](const uint32_t (&w)[R2_PW], int rr, int b) {
-        float g[2 * R2_PW];
+    auto gather = [&](const uint32_t (&w)[R2F_PW], int rr, int b) {
+        float g[2 * R2F_PW];
 #pragma unroll
-        for (int k = 0; k < R2_PW; k++) {
-            const int v = min(rr * R2_ROUND + wv * R2_PW + k, nv - 1);
+        for (int k = 0; k < R2F_PW; k++) {
+            const int v = min(rr * R2F_ROUND + wv * R2F_PW + k, nv - 1);
             const float WH_GLOBAL *blk = L + (size_t)v * 2 * R2_EN;
             g[2 * k] = blk[w[k] & 255];
             g[2 * k + 1] = blk[R2_EN + (w[k] >> 8)];
         }
 #pragma unroll
-        for (int k = 0; k < R2_PW; k++) s_t[b][wv * R2_PW + k][lane] = __fadd_rn(g[2 * k], g[2 * k + 1]);
+        for (int k = 0; k < R2F_PW; k++) s_t[b][wv * R2F_PW + k][lane] = __fadd_rn(g[2 * k], g[2 * k + 1]);
     };
     float acc = 0.0f;
     auto consume = [&](int rr, int b) {
-        const int n = min(R2_ROUND, nv - rr * R2_ROUND);
+        const int n = min(R2F_ROUND, nv - rr * R2F_ROUND);
 #pragma unroll 8
         for (int k = 0; k < n; k++) acc = __fadd_rn(acc, s_t[b][k][lane]);
     };
     // a round's entries go out before the next round's codes: loads complete
     // in issue order, so the wait for the entries does not cover the codes
-    uint32_t wA[R2_PW], wB[R2_PW];
+    uint32_t wA[R2F_PW], wB[R2F_PW];
     fetch(wA, 0);
     __builtin_amdgcn_sched_barrier(0);
     fetch(wB, 1);                                    // past the last round: harmless repeats
@@ -162,9 +257,16 @@ extern "C" int whip_r2_rows_pairs(const uint8_t *const *recs, const int32_t *pai
     if (P <= 0 || P > 65535 || kinds < 1 || kinds > 2 || M <= 0 || nv <= 0 || idx_off[0] % 2 ||
         (kinds > 1 && idx_off[1] % 2))
         return (int)hipErrorInvalidValue;
-    const dim3 grid((M + 63) / 64, P, kinds);
-    WHIP_LAUNCH(k_r2_rows_pairs, grid, dim3(R2_WAVES * 64), 0, s, recs, pair_exp, pair_tok, kinds, idx_off[0],
-                       kinds > 1 ? idx_off[1] : 0, sc_off[0], kinds > 1 ? sc_off[1] : 0, M, nv, lut, per_tok, out,
-                       err);
+    // the LDS kernel stages a table's every window per workgroup: with
+    // fewer than 192 workgroups (one token's gate/up at batch 1) the
+    // fetching kernel, which spreads over four times as many, is faster
+    const int groups = (M + 64 * R2_WAVES - 1) / (64 * R2_WAVES);
+    const uint32_t i1 = kinds > 1 ? idx_off[1] : 0, s1 = kinds > 1 ? sc_off[1] : 0;
+    if ((long)groups * P * kinds >= 192)
+        WHIP_LAUNCH(k_r2_rows_pairs, dim3(groups, P, kinds), dim3(R2_WAVES * 64), 0, s, recs, pair_exp, pair_tok,
+                    kinds, idx_off[0], i1, sc_off[0], s1, M, nv, lut, per_tok, out, err);
+    else
+        WHIP_LAUNCH(k_r2_rows_fetch, dim3((M + 63) / 64, P, kinds), dim3(R2F_WAVES * 64), 0, s, recs, pair_exp,
+                    pair_tok, kinds, idx_off[0], i1, sc_off[0], s1, M, nv, lut, per_tok, out, err);
     return (int)hipGetLastError();
 }
