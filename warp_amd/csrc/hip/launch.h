@@ -124,7 +124,7 @@ int whip_combine(const uint8_t *const *recs, const int32_t *pair_exp,
                  int skip_zero, const float *sh, int sh_n, size_t sh_stride,
                  float *y, hipStream_t s);
 /* VQ4P down rows for the combine: pair p's row r is the fold, in block
- * order, of S[(p*nb + b)*H + r] (whip_p6_tiles' sums) with the pair's table
+ * order, of S[(p*nb + b)*H + r] (whip_p6_down's sums) with the pair's table
  * scales ls[p*nb + b] (fma: one fused multiply-add, else a product and a
  * sum), times the f16 row scale at sc_off of the pair's record; an unbound
  * expert's rows are zeros. */
@@ -188,29 +188,45 @@ int whip_vq_quant_lut_n(const float *lut, int nv, int stages, int entries, int n
  * q[t][nv][4][64], qs[t][ceil(nv/32)]. */
 int whip_p6_lutq(const void *x, int x_bf16, int x_ld, int rows, int kinds, const float *booksT, int cb,
                  int nv, int fma, int8_t *q, float *qs, hipStream_t s);
-/* The exact integer sums of every pair's VQ4P rows per 32-position scale
- * block: S[((p*kinds + kind)*nb + b)*M + r] (int16, nb = ceil(nv/32)) from
- * the record of expert pair_exp[p] (idx at idx_off[kind]) through table
- * pair_tok[p]*kinds + kind (per_tok) or p of q (whip_p6_lutq's layout).  An
- * unbound expert's sums are zeros and raise bit 0 of err. */
-int whip_p6_tiles(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
-                  int kinds, const uint32_t *idx_off, int M, int nv, const int8_t *q, int per_tok,
-                  int16_t *S, int *err, hipStream_t s);
-/* Each pair's gate and up rows folded from whip_p6_tiles' sums (block order,
- * the token's table scales qs_gu, the f16 row scales at sc_gate / sc_up of
- * the record), h = silu(g) * u, and the pair's down table from h (books
- * cb_d ..): q_d[p][nv_d][4][64], qs_d[p][ceil(nv_d/32)].  I == 8 nv_d. */
+/* Each pair's gate and up rows folded from whip_p6_gate_up's sums (block
+ * order, the token's table scales qs_gu, the f16 row scales at sc_gate /
+ * sc_up of the record), h = silu(g) * u, and the pair's down table from h
+ * (books cb_d ..): q_d[p][nv_d][4][64], qs_d[p][ceil(nv_d/32)].  I == 8 nv_d. */
 int whip_p6_act_lutq(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
                      const int16_t *S, const float *qs_gu, uint32_t sc_gate, uint32_t sc_up, int I, int nv_gu,
                      const float *booksT, int cb_d, int nv_d, int fma, int8_t *q_d, float *qs_d,
                      hipStream_t s);
-/* h[p][i] = silu(gu[p][0][i]) * gu[p][1][i], the engine's SwiGLU. */
-int whip_p6_act(const float *gu, int P, int I, float *h, hipStream_t s);
+/* The VQ4P layer's gate/up tile launch: the exact integer sums of every
+ * pair's gate and up rows per 32-position scale block,
+ * S[((p*2 + kind)*nb + b)*I + r] (int16, nb = ceil(nv/32)), from the record
+ * of expert pair_exp[p] (idx at idx_off[kind]) through the token's tables:
+ * whip_p6_lutq's q (table pair_tok[p]*2 + kind), or with q NULL built here
+ * from x row pair_tok[p] (bf16 or fp32, row stride x_ld) and books
+ * cb .. cb+7 of booksT ([book][8][64] fp32) in the engine's order for fma,
+ * their scales written to qs[tok][2][nb].  An unbound expert's sums are
+ * zeros and raise bit 0 of err.  I % 64 == 0. */
+int whip_p6_gate_up(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                    const uint32_t *idx_off, int I, const void *x, int x_bf16, int x_ld, int nv,
+                    const float *booksT, int cb, int fma, const int8_t *q, int16_t *S, float *qs, int *err,
+                    hipStream_t s);
+/* The down tile launch: the sums of each pair's down rows (idx at idx_off;
+ * S[(p*nb + b)*H + r], nb = I/256 rounded up) through its table: q's table
+ * p (whip_p6_act_lutq's), or with q NULL built here as whip_p6_act_lutq
+ * builds it (from Sg / qs_g, nv_g positions, the row scales at sc_gate /
+ * sc_up, books cb .. cb+3), its scales written to qs[p][nb].  H % 64 == 0. */
+int whip_p6_down(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                 uint32_t idx_off, int H, int I, const int16_t *Sg, const float *qs_g, uint32_t sc_gate,
+                 uint32_t sc_up, int nv_g, const float *booksT, int cb, int fma, const int8_t *q, int16_t *S,
+                 float *qs, int *err, hipStream_t s);
 /* VQ2R (vq2r.hip): fp32 tables lut[t][nv][st][256] of rows x kinds inputs in
  * the engine's order, and every pair's rows through them in vq_rows'
  * order (two stages, two index bytes a row and position). */
 int whip_r2_lutb(const void *x, int x_bf16, int x_ld, int rows, int kinds, int st, const float *booksT, int cb,
                  int nv, int fma, float *lut, hipStream_t s);
+/* The down tables of P pairs from their gate and up rows gu[p][2][I]:
+ * h = silu(g) * u, then whip_r2_lutb's tables of h (one kind, books cb ..). */
+int whip_r2_act_lutb(const float *gu, int P, int I, const float *booksT, int cb, int fma, float *lut,
+                     hipStream_t s);
 int whip_r2_rows_pairs(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
                        int kinds, const uint32_t *idx_off, const uint32_t *sc_off, int M, int nv, const float *lut,
                        int per_tok, float *out, int *err, hipStream_t s);

@@ -15,35 +15,47 @@
 #define R2_LV 16
 
 // table t = (input row t / kinds, kind t % kinds): lut[t][v][s][e] =
-// sum_d x[8v + d] * C[cb + st*kind + s][e][d], booksT [book][8][256]
-template <bool FMA>
-__global__ void __launch_bounds__(256)
-k_r2_lutb(const void *__restrict__ x, int x_bf16, int x_ld, int kinds, int st, const float *__restrict__ booksT,
-          int cb, int nv, float *__restrict__ lut)
+// sum_d x[8v + d] * C[cb + 2 kind + s][e][d], booksT [book][8][256], two
+// stages.  ACT: the input row of pair t is h = silu(g) * u of its gate and
+// up rows gu[t][0][.], gu[t][1][.] (waste_act_pair_range), built here.  A
+// workgroup stages its R2_LV positions' inputs in LDS, then thread e builds
+// entry e of both stages for each.
+template <bool FMA, bool ACT>
+__global__ void __launch_bounds__(R2_EN)
+k_r2_lutb(const void *__restrict__ x, int x_bf16, int x_ld, int kinds, const float *__restrict__ booksT, int cb,
+          int nv, float *__restrict__ lut)
 {
+    __shared__ float s_x[R2_LV * 8];
     const int t = blockIdx.y, row = t / kinds, kind = t - row * kinds;
     const int e = threadIdx.x;
-    const int v0 = blockIdx.x * R2_LV, v1 = min(nv, v0 + R2_LV);
-    for (int s = 0; s < st; s++) {
-        const float *CT = booksT + (size_t)(cb + st * kind + s) * 8 * R2_EN;
-        float c[8];
+    const int v0 = blockIdx.x * R2_LV, n = min(R2_LV, nv - v0);
+    float c[2][8];
 #pragma unroll
-        for (int d = 0; d < 8; d++) c[d] = CT[d * R2_EN + e];
-        for (int v = v0; v < v1; v++) {
-            float xv[8];
-            if (x_bf16) {
-                const uint16_t *xr = (const uint16_t *)x + (size_t)row * x_ld + (size_t)v * 8;
+    for (int st = 0; st < 2; st++)
 #pragma unroll
-                for (int d = 0; d < 8; d++) xv[d] = wh_bf16(xr[d]);
-            } else {
-                const float *xr = (const float *)x + (size_t)row * x_ld + (size_t)v * 8;
+        for (int d = 0; d < 8; d++) c[st][d] = booksT[((size_t)(cb + 2 * kind + st) * 8 + d) * R2_EN + e];
+    if (e < 8 * n) {
+        const size_t i = (size_t)v0 * 8 + e;
+        float xv;
+        if (ACT) {
+            const float *gu = (const float *)x + (size_t)row * 2 * x_ld;
+            xv = wh_silu_mul(gu[i], gu[x_ld + i]);
+        } else {
+            xv = x_bf16 ? wh_bf16(((const uint16_t *)x)[(size_t)row * x_ld + i]) : ((const float *)x)[(size_t)row * x_ld + i];
+        }
+        s_x[e] = xv;
+    }
+    __syncthreads();
+    for (int v = 0; v < n; v++) {
 #pragma unroll
-                for (int d = 0; d < 8; d++) xv[d] = xr[d];
-            }
+        for (int st = 0; st < 2; st++) {
             float a = 0.0f;
 #pragma unroll
-            for (int d = 0; d < 8; d++) a = FMA ? __fmaf_rn(xv[d], c[d], a) : __fadd_rn(a, __fmul_rn(xv[d], c[d]));
-            lut[(((size_t)t * nv + v) * st + s) * R2_EN + e] = a;
+            for (int d = 0; d < 8; d++) {
+                const float xd = s_x[v * 8 + d];
+                a = FMA ? __fmaf_rn(xd, c[st][d], a) : __fadd_rn(a, __fmul_rn(xd, c[st][d]));
+            }
+            lut[(((size_t)t * nv + v0 + v) * 2 + st) * R2_EN + e] = a;
         }
     }
 }
@@ -51,11 +63,22 @@ k_r2_lutb(const void *__restrict__ x, int x_bf16, int x_ld, int kinds, int st, c
 extern "C" int whip_r2_lutb(const void *x, int x_bf16, int x_ld, int rows, int kinds, int st, const float *booksT,
                             int cb, int nv, int fma, float *lut, hipStream_t s)
 {
-    if (rows <= 0 || kinds <= 0 || rows * kinds > 65535 || st < 1 || st > 8 || nv <= 0 || x_ld < nv * 8 || cb < 0)
+    if (rows <= 0 || kinds <= 0 || rows * kinds > 65535 || st != 2 || nv <= 0 || x_ld < nv * 8 || cb < 0)
         return (int)hipErrorInvalidValue;
     const dim3 grid((nv + R2_LV - 1) / R2_LV, rows * kinds);
-    if (fma) hipLaunchKernelGGL(k_r2_lutb<true>, grid, dim3(R2_EN), 0, s, x, x_bf16, x_ld, kinds, st, booksT, cb, nv, lut);
-    else hipLaunchKernelGGL(k_r2_lutb<false>, grid, dim3(R2_EN), 0, s, x, x_bf16, x_ld, kinds, st, booksT, cb, nv, lut);
+    if (fma) WHIP_LAUNCH((k_r2_lutb<true, false>), grid, dim3(R2_EN), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, lut);
+    else WHIP_LAUNCH((k_r2_lutb<false, false>), grid, dim3(R2_EN), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, lut);
+    return (int)hipGetLastError();
+}
+
+extern "C" int whip_r2_act_lutb(const float *gu, int P, int I, const float *booksT, int cb, int fma, float *lut,
+                                hipStream_t s)
+{
+    if (P <= 0 || P > 65535 || I <= 0 || I % 8 || cb < 0) return (int)hipErrorInvalidValue;
+    const int nv = I / 8;
+    const dim3 grid((nv + R2_LV - 1) / R2_LV, P);
+    if (fma) WHIP_LAUNCH((k_r2_lutb<true, true>), grid, dim3(R2_EN), 0, s, gu, 0, I, 1, booksT, cb, nv, lut);
+    else WHIP_LAUNCH((k_r2_lutb<false, true>), grid, dim3(R2_EN), 0, s, gu, 0, I, 1, booksT, cb, nv, lut);
     return (int)hipGetLastError();
 }
 

@@ -193,17 +193,41 @@ extern "C" int whip_vq_rows_p6(const uint8_t *idx, const uint16_t *scale, const 
 }
 
 // ---- the device layer's VQ4P experts ------------------------------------------
-// Four launches and the combine, each pair's rows the engine's bit for bit:
-//   k_p6_lutq      each token's gate and up tables, int8 per scale block;
-//   k_p6_tiles     every pair's gate and up rows: exact integer block sums;
-//   k_p6_act_lutq  the gate/up folds, SwiGLU and each pair's down table;
-//   k_p6_tiles     every pair's down rows, folded by the combine.
-// The fold of a row's block sums into fp32 runs in block order, so the block
-// sums wait in HBM (int16: a sum is at most 4 * 32 * 127 in magnitude) for
-// the launch that needs the row; the tile launches then stream the index
-// bytes through one staged table per workgroup, with no order between
-// blocks to keep.
-#define P6_TAB (P6_BLK * 4 * P6_EN)    // one scale block's int8 table, 8 KB
+// Two tile launches and the combine, each pair's rows the engine's bit for
+// bit.  The gate/up launch builds each token's int8 gate and up tables
+// from x and sums every pair's gate and up rows through them; the down
+// launch folds those sums into the pair's gate and up rows, applies SwiGLU,
+// builds the pair's int8 down table from the result and sums the down rows
+// through it; the combine folds the down sums.  A row's sums are exact
+// integers per 32-position scale block (at most 4 * 32 * 127 in magnitude:
+// int16), folded into fp32 in block order, so the sums wait in HBM for the
+// launch that needs the whole row, and the tiles are free to run in any
+// order.
+//
+// A tile workgroup takes one (pair, kind), a group of up to P6_MAXG
+// consecutive scale blocks and a run of `per` 64-row blocks.  It builds the
+// group's tables in LDS (the engine's arithmetic: vq_build_lut's entries,
+// src/model.c:3864-3880, in the order of the layer's p6_order: one fused
+// multiply-add chain over d from zero as lutb_range_avx512,
+// src/simd_avx512.c:90-123, else a rounded product added to the running sum
+// as waste_lutb_range, src/model.c:3815-3854; then vq_quant_lut's block
+// scale max|lut| / 127 and entries rint(lut * (127 / max)) clamped to
+// [-127, 127], src/model.c:3979-4074), while its first tiles are in flight.
+// A tile is 32 positions of 64 rows, 192 contiguous bytes a position (three
+// code bytes a row).  Lane (quad q = lane % 16, slot k = lane / 16) loads
+// the 12 bytes of rows 4q .. 4q+3 at positions k, k+4, .., k+28 (a 16-lane
+// group per position: eight 12-byte loads a tile), adds four table bytes per
+// row and position, and the four slots' sums meet across lanes (exact
+// integer sums, in any order).  A position's table is 256 bytes at a
+// 320-byte stride in LDS, so the four positions one instruction reads sit in
+// four disjoint groups of sixteen banks and two lanes of a group meet in a
+// bank only on one dword: the lookups do not conflict.  Two tiles are in
+// flight per wavefront.  S[(pk * nb + b) * M + r], pk = pair * kinds + kind;
+// the tables' scales qs[tab][b], tab = pair_tok[p] * kinds + kind (the
+// gate/up launch: every pair of a token writes the same values) or p.
+#define P6_MAXG 6                      // scale blocks a workgroup builds (x)
+#define P6_MAXG_ACT 2                  // (SwiGLU: one row's folds per thread)
+#define P6_TS 320                      // LDS bytes a position's table takes
 #define P6_MAXB 32                     // gate/up blocks folded from registers
 
 // One scale block of a table: lut[v][s][e] = sum_d x[8v + d] * C[s][e][d]
@@ -288,150 +312,6 @@ extern "C" int whip_p6_lutq(const void *x, int x_bf16, int x_ld, int rows, int k
     return (int)hipGetLastError();
 }
 
-// Block sums of every pair's rows.  A workgroup takes one (pair, kind), a
-// group of up to P6_MAXG consecutive scale blocks and a run of `per` 64-row
-// blocks: it stages the group's tables once, and its wavefronts take the
-// tiles (row block, scale block) in turn, two in flight per wavefront.  A
-// tile is 32 positions of 64 rows, 192 contiguous bytes a position (three
-// code bytes a row).  Lane (quad q = lane % 16, slot k = lane / 16) loads
-// the 12 bytes of rows 4q .. 4q+3 at positions k, k+4, .., k+28 (one
-// 16-lane group per position: eight 12-byte loads a tile), adds four table
-// bytes per row and position, and the four slots' sums meet across lanes
-// (exact integer sums, in any order).  A position's table is 256 bytes,
-// 64 apart in LDS (a 320-byte stride), so the four positions one load
-// instruction reads sit in four disjoint groups of sixteen banks and no two
-// lanes of a group meet in a bank unless they read one dword: the lookups
-// do not conflict.  S[(pk * nb + b) * M + r], pk = pair * kinds + kind.  An
-// unbound expert writes zeros and raises bit 0 of err.
-#define P6_MAXG 6                      // scale blocks a workgroup stages
-#define P6_TS 320                      // LDS bytes a position's table takes
-
-__global__ void __launch_bounds__(P6_THREADS)
-k_p6_tiles(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
-           const int32_t *__restrict__ pair_tok, int kinds, uint32_t idx_off0, uint32_t idx_off1, int M, int nv,
-           int nb, const int8_t *__restrict__ q, int per_tok, int ncb, int ngrp, int shares, int per,
-           int16_t *__restrict__ S, int *__restrict__ err)
-{
-    __shared__ __align__(16) int8_t s_tab[P6_MAXG * P6_BLK * P6_TS];
-    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int j = blockIdx.x % shares, rest = blockIdx.x / shares;
-    const int bg = rest % ngrp, pk = rest / ngrp, kind = pk % kinds, p = pk / kinds;
-    const int b0 = bg * ncb, nbg = min(ncb, nb - b0);
-    const int rb0 = j * per, rb1 = min(M / 64, rb0 + per), ntile = nbg * (rb1 - rb0);
-    int16_t *out = S + ((size_t)pk * nb + b0) * M;   // block b0 + bl at out + bl * M
-    const uint8_t *rec = recs[pair_exp[p]];
-    if (rec == nullptr) {                            // uniform
-        for (int bl = 0; bl < nbg; bl++)
-            for (int r = rb0 * 64 + tid; r < rb1 * 64; r += P6_THREADS) out[(size_t)bl * M + r] = 0;
-        if (tid == 0) atomicOr(err, 1);
-        return;
-    }
-    const size_t tab = per_tok ? (size_t)pair_tok[p] * kinds + kind : (size_t)p;
-    // the group's tables (positions b0*32 .., 16 uint4 each), to LDS at a
-    // 320-byte stride; the loads go out before any tile's
-    const int v_lo = b0 * P6_BLK, nq = (min(nv, v_lo + nbg * P6_BLK) - v_lo) * 16;
-    const uint4 *tsrc = (const uint4 *)(q + (tab * nv + v_lo) * 4 * P6_EN);
-    constexpr int TV = P6_MAXG * P6_BLK * 16 / P6_THREADS;
-    uint4 tv[TV];
-#pragma unroll
-    for (int k = 0; k < TV; k++) tv[k] = tsrc[tid + k * P6_THREADS < nq ? tid + k * P6_THREADS : 0];
-    g_u8 *mat = as_global(rec) + (kind ? idx_off1 : idx_off0);
-    const int qd = lane & 15, slot = lane >> 4;
-    // tile t: scale block b0 + t % nbg, row block rb0 + t / nbg; positions
-    // past a short block load position 0 (in bounds; their sums not added)
-    auto load = [&](uint3 (&c)[P6_BLK / 4], int t) {
-        const int bl = t % nbg, rb = rb0 + t / nbg;
-        const int n = min(P6_BLK, nv - (b0 + bl) * P6_BLK);
-        g_u8 *ix = mat + ((size_t)rb * nv + (size_t)(b0 + bl) * P6_BLK) * 192 + 12 * qd;
-#pragma unroll
-        for (int i = 0; i < P6_BLK / 4; i++) {
-            const int v = 4 * i + slot;
-            c[i] = *(const uint3 WH_GLOBAL *)(ix + (size_t)(v < n ? v : 0) * 192);
-        }
-    };
-    auto sum_tile = [&](const uint3 (&c)[P6_BLK / 4], int t) {
-        const int bl = t % nbg, rb = rb0 + t / nbg;
-        const int n = min(P6_BLK, nv - (b0 + bl) * P6_BLK);
-        const int8_t *Tb = s_tab + bl * P6_BLK * P6_TS;
-        int s4[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < P6_BLK / 4; i++) {
-            const int v = 4 * i + slot;
-            const uint32_t cc[4] = {c[i].x, __builtin_amdgcn_alignbyte(c[i].y, c[i].x, 3),
-                                    __builtin_amdgcn_alignbyte(c[i].z, c[i].y, 2), c[i].z >> 8};
-            const int8_t *T = Tb + v * P6_TS;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const int e = T[cc[k] & 63] + T[P6_EN + ((cc[k] >> 6) & 63)] +
-                              T[2 * P6_EN + ((cc[k] >> 12) & 63)] + T[3 * P6_EN + ((cc[k] >> 18) & 63)];
-                s4[k] += v < n ? e : 0;
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const auto a = __builtin_amdgcn_permlane16_swap(s4[k], s4[k], false, false);
-            s4[k] = (int)a[0] + (int)a[1];
-            const auto b = __builtin_amdgcn_permlane32_swap(s4[k], s4[k], false, false);
-            s4[k] = (int)b[0] + (int)b[1];
-        }
-        // each of the four lanes of a quad stores one of its rows
-        const int mine = slot == 0 ? s4[0] : slot == 1 ? s4[1] : slot == 2 ? s4[2] : s4[3];
-        out[(size_t)bl * M + rb * 64 + 4 * qd + slot] = (int16_t)mine;
-    };
-    // the wavefront's tiles wv + 16 i, i < cnt; every load is unconditional
-    // (past the last tile: the last again), and the scheduling barriers keep
-    // each buffer's loads together and in order, so a wait for one buffer
-    // never covers the other's
-    const int cnt = wv < ntile ? (ntile - wv + P6_WAVES - 1) / P6_WAVES : 0;
-    auto tile_at = [&](int i) { return cnt > 0 ? wv + min(i, cnt - 1) * P6_WAVES : 0; };
-    uint3 cA[P6_BLK / 4], cB[P6_BLK / 4];
-    load(cA, tile_at(0));
-    __builtin_amdgcn_sched_barrier(0);
-    load(cB, tile_at(1));
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < TV; k++) {                   // past nq: unused bytes
-        const int g = tid + k * P6_THREADS;
-        *(uint4 *)(s_tab + (g >> 4) * P6_TS + (g & 15) * 16) = tv[k];
-    }
-    __syncthreads();
-    for (int i = 0; i < cnt; i += 2) {               // uniform
-        sum_tile(cA, tile_at(i));
-        __builtin_amdgcn_sched_barrier(0);
-        load(cA, tile_at(i + 2));
-        __builtin_amdgcn_sched_barrier(0);
-        if (i + 1 < cnt) sum_tile(cB, tile_at(i + 1));
-        __builtin_amdgcn_sched_barrier(0);
-        load(cB, tile_at(i + 3));
-        __builtin_amdgcn_sched_barrier(0);
-    }
-}
-
-extern "C" int whip_p6_tiles(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
-                             int kinds, const uint32_t *idx_off, int M, int nv, const int8_t *q, int per_tok,
-                             int16_t *S, int *err, hipStream_t s)
-{
-    if (P <= 0 || kinds < 1 || kinds > 2 || M <= 0 || M % 64 || nv <= 0 || (uintptr_t)q % 16 || idx_off[0] % 4 ||
-        (kinds > 1 && idx_off[1] % 4))
-        return (int)hipErrorInvalidValue;
-    const int nb = (nv + P6_BLK - 1) / P6_BLK, nrb = M / 64;
-    // runs of at most 32 row blocks; groups of scale blocks so that the
-    // launch is about one workgroup per CU
-    long shares = (nrb + 31) / 32;
-    const int per = (int)((nrb + shares - 1) / shares);
-    shares = (nrb + per - 1) / per;
-    const long tiles = (long)P * kinds * nb * nrb, want = (tiles + 255) / 256;
-    long ncb = (2 * want + per) / (2 * per);         // rounded
-    if (ncb > P6_MAXG) ncb = P6_MAXG;
-    if (ncb > nb) ncb = nb;
-    if (ncb < 1) ncb = 1;
-    const long ngrp = (nb + ncb - 1) / ncb, grid = (long)P * kinds * ngrp * shares;
-    if (grid > 0x7fffffffL) return (int)hipErrorInvalidValue;
-    const uint32_t i1 = kinds > 1 ? idx_off[1] : 0;
-    WHIP_LAUNCH(k_p6_tiles, dim3((unsigned)grid), dim3(P6_THREADS), 0, s, recs, pair_exp, pair_tok, kinds,
-                idx_off[0], i1, M, nv, nb, q, per_tok, (int)ncb, (int)ngrp, (int)shares, per, S, err);
-    return (int)hipGetLastError();
-}
 // The gate/up rows of pair p (I of each), folded from their block sums in
 // block order with the token's table scales and scaled by the row's f16
 // scale (vq_rows_p6's fold, src/model.c:4076-4114), then h = silu(g) * u
@@ -498,21 +378,291 @@ extern "C" int whip_p6_act_lutq(const uint8_t *const *recs, const int32_t *pair_
 #undef AL
     return (int)hipGetLastError();
 }
-// waste_act_pair_range (src/model.c): h = silu(g) * u for each pair's rows,
-// gu[p][0][I] the gate rows, gu[p][1][I] the up rows, h[p][I].
-__global__ void __launch_bounds__(256)
-k_p6_act(const float *__restrict__ gu, int I, size_t n, float *__restrict__ h)
+
+struct p6_tile_args {
+    const uint8_t *const *recs;
+    const int32_t *pair_exp, *pair_tok;
+    int kinds;
+    uint32_t idx_off0, idx_off1;
+    int M, nv, nb;                     // rows, positions, scale blocks
+    int ncb, ngrp, shares, per;        // the launch's partition
+    int16_t *S;
+    float *qs;
+    int *err;
+    const int8_t *q;                   // P6_Q: the tables, [tab][nv][4][64]
+    const float *booksT;               // [book][8][64] fp32
+    int cb;                            // the first book of kind 0's four
+    const void *x;                     // gate/up: input rows (bf16 or fp32)
+    int x_bf16, x_ld;
+    const int16_t *Sg;                 // down: the gate/up sums [p][2][nb_g][I]
+    const float *qs_g;                 //       and their tables' scales [tok][2][nb_g]
+    uint32_t sc_gate, sc_up;           //       the gate / up row scales in the record
+    int nb_g;
+};
+
+#define P6_Q 0                         // tables read from q
+#define P6_X 1                         // built from x (gate/up)
+#define P6_ACT 2                       // built from SwiGLU of the gate/up sums (down)
+
+template <int MODE, bool FMA>
+__global__ void __launch_bounds__(P6_THREADS)
+k_p6_tiles(p6_tile_args a)
 {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    const size_t p = i / I, r = i - p * I;
-    h[i] = wh_silu_mul(gu[(2 * p) * I + r], gu[(2 * p + 1) * I + r]);
+    constexpr bool ACT = MODE == P6_ACT;
+    __shared__ __align__(16) int8_t s_tab[P6_MAXG * P6_BLK * P6_TS];
+    __shared__ float s_x[MODE == P6_Q ? 1 : P6_MAXG * 8 * P6_BLK];   // each block's 256 inputs
+    __shared__ float s_mx[P6_MAXG][P6_WAVES];
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = blockIdx.x % a.shares, rest = blockIdx.x / a.shares;
+    const int bg = rest % a.ngrp, pk = rest / a.ngrp, kind = pk % a.kinds, p = pk / a.kinds;
+    const int b0 = bg * a.ncb, nbg = min(a.ncb, a.nb - b0);
+    const int rb0 = j * a.per, rb1 = min(a.M / 64, rb0 + a.per), ntile = nbg * (rb1 - rb0);
+    const int M = a.M, nv = a.nv;
+    int16_t *out = a.S + ((size_t)pk * a.nb + b0) * M;   // block b0 + bl at out + bl * M
+    const uint8_t *rec = a.recs[a.pair_exp[p]];
+    if (rec == nullptr) {                            // uniform
+        for (int bl = 0; bl < nbg; bl++)
+            for (int r = rb0 * 64 + tid; r < rb1 * 64; r += P6_THREADS) out[(size_t)bl * M + r] = 0;
+        if (tid == 0) atomicOr(a.err, 1);
+        return;
+    }
+    const int tok = a.pair_tok[p];
+    const size_t tab = a.kinds == 2 ? (size_t)tok * 2 + kind : (size_t)p;
+    g_u8 *mat = as_global(rec) + (kind ? a.idx_off1 : a.idx_off0);
+    const int qd = lane & 15, slot = lane >> 4;
+    // tile t: scale block b0 + t % nbg, row block rb0 + t / nbg; positions
+    // past a short block load position 0 (in bounds; their sums not added)
+    auto load = [&](uint3 (&cc)[P6_BLK / 4], int t) {
+        const int bl = t % nbg, rb = rb0 + t / nbg;
+        const int n = min(P6_BLK, nv - (b0 + bl) * P6_BLK);
+        g_u8 *ix = mat + ((size_t)rb * nv + (size_t)(b0 + bl) * P6_BLK) * 192 + 12 * qd;
+#pragma unroll
+        for (int i = 0; i < P6_BLK / 4; i++) {
+            const int v = 4 * i + slot;
+            cc[i] = *(const uint3 WH_GLOBAL *)(ix + (size_t)(v < n ? v : 0) * 192);
+        }
+    };
+    auto sum_tile = [&](const uint3 (&cc)[P6_BLK / 4], int t) {
+        const int bl = t % nbg, rb = rb0 + t / nbg;
+        const int n = min(P6_BLK, nv - (b0 + bl) * P6_BLK);
+        const int8_t *Tb = s_tab + bl * P6_BLK * P6_TS;
+        int s4[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < P6_BLK / 4; i++) {
+            const int v = 4 * i + slot;
+            const uint32_t w[4] = {cc[i].x, __builtin_amdgcn_alignbyte(cc[i].y, cc[i].x, 3),
+                                   __builtin_amdgcn_alignbyte(cc[i].z, cc[i].y, 2), cc[i].z >> 8};
+            const int8_t *T = Tb + v * P6_TS;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int en = T[w[k] & 63] + T[P6_EN + ((w[k] >> 6) & 63)] + T[2 * P6_EN + ((w[k] >> 12) & 63)] +
+                               T[3 * P6_EN + ((w[k] >> 18) & 63)];
+                s4[k] += v < n ? en : 0;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const auto x1 = __builtin_amdgcn_permlane16_swap(s4[k], s4[k], false, false);
+            s4[k] = (int)x1[0] + (int)x1[1];
+            const auto x2 = __builtin_amdgcn_permlane32_swap(s4[k], s4[k], false, false);
+            s4[k] = (int)x2[0] + (int)x2[1];
+        }
+        // each of the four lanes of a quad stores one of its rows
+        const int mine = slot == 0 ? s4[0] : slot == 1 ? s4[1] : slot == 2 ? s4[2] : s4[3];
+        out[(size_t)bl * M + rb * 64 + 4 * qd + slot] = (int16_t)mine;
+    };
+    // the wavefront's tiles wv + 16 i, i < cnt; every load is unconditional
+    // (past the last tile: the last again), and the scheduling barriers keep
+    // each buffer's loads together and in order, so a wait for one buffer
+    // never covers the other's
+    const int cnt = wv < ntile ? (ntile - wv + P6_WAVES - 1) / P6_WAVES : 0;
+    auto tile_at = [&](int i) { return cnt > 0 ? wv + min(i, cnt - 1) * P6_WAVES : 0; };
+    uint3 cA[P6_BLK / 4], cB[P6_BLK / 4];
+    auto issue = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        load(cA, tile_at(0));
+        __builtin_amdgcn_sched_barrier(0);
+        load(cB, tile_at(1));
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    if (MODE == P6_Q) {
+        // the group's tables (16 uint4s a position; past the group: the
+        // first ones, unused), to LDS at the 320-byte stride
+        const int v_lo = b0 * P6_BLK, nq = (min(nv, v_lo + nbg * P6_BLK) - v_lo) * 16;
+        const uint4 *tsrc = (const uint4 *)(a.q + (tab * nv + v_lo) * 4 * P6_EN);
+        constexpr int TV = P6_MAXG * P6_BLK * 16 / P6_THREADS;
+        uint4 tv[TV];
+#pragma unroll
+        for (int k = 0; k < TV; k++) tv[k] = tsrc[tid + k * P6_THREADS < nq ? tid + k * P6_THREADS : 0];
+        issue();
+#pragma unroll
+        for (int k = 0; k < TV; k++) {
+            const int g = tid + k * P6_THREADS;
+            *(uint4 *)(s_tab + (g >> 4) * P6_TS + (g & 15) * 16) = tv[k];
+        }
+        __syncthreads();
+    } else {
+        // the table builder's books: thread (stage, entry) of tid % 256
+        const int u = tid & 255, st = u >> 6, e = u & 63, quarter = tid >> 8;
+        float c[8];
+        {
+            const float *C = a.booksT + ((size_t)(a.cb + (ACT ? 0 : 4 * kind) + st) * 8) * P6_EN + e;
+#pragma unroll
+            for (int d = 0; d < 8; d++) c[d] = C[d * P6_EN];
+        }
+        // the group's inputs: 8 n values a block (zeros past the block)
+        const int i_hi = min(nv * 8, (b0 + nbg) * 8 * P6_BLK) - b0 * 8 * P6_BLK;
+        if (!ACT) {
+            for (int i = tid; i < nbg * 8 * P6_BLK; i += P6_THREADS) {
+                float xv = 0.0f;
+                if (i < i_hi) {
+                    const size_t o = (size_t)tok * a.x_ld + (size_t)b0 * 8 * P6_BLK + i;
+                    xv = a.x_bf16 ? wh_bf16(((const uint16_t *)a.x)[o]) : ((const float *)a.x)[o];
+                }
+                s_x[i] = xv;
+            }
+        } else if (tid < nbg * 8 * P6_BLK) {
+            // h = silu(g) * u of row r: the gate and up rows folded from their
+            // block sums in block order with the token's table scales, times
+            // the row's f16 scale (vq_rows_p6's fold, src/model.c:4076-4114),
+            // as waste_act_pair_range applies SwiGLU
+            const int I = 8 * nv, r = b0 * 8 * P6_BLK + min(tid, i_hi > 0 ? i_hi - 1 : 0);
+            const int16_t *Sgp = a.Sg + (size_t)p * 2 * a.nb_g * I + r, *Sup = Sgp + (size_t)a.nb_g * I;
+            const float *lg = a.qs_g + (size_t)tok * 2 * a.nb_g, *lu = lg + a.nb_g;
+            float ag = 0.0f, au = 0.0f;
+            for (int k0 = 0; k0 < a.nb_g; k0 += P6_MAXB) {   // one round unless nb_g > P6_MAXB
+                const int kn = min(P6_MAXB, a.nb_g - k0);
+                int16_t sg[P6_MAXB], su[P6_MAXB];
+#pragma unroll
+                for (int k = 0; k < P6_MAXB; k++) {
+                    const int kk = k0 + (k < kn ? k : 0);
+                    sg[k] = Sgp[(size_t)kk * I];
+                    su[k] = Sup[(size_t)kk * I];
+                }
+#pragma unroll
+                for (int k = 0; k < P6_MAXB; k++)
+                    if (k < kn) {
+                        const float fg = (float)sg[k], fu = (float)su[k];
+                        ag = FMA ? __fmaf_rn(lg[k0 + k], fg, ag) : __fadd_rn(ag, __fmul_rn(lg[k0 + k], fg));
+                        au = FMA ? __fmaf_rn(lu[k0 + k], fu, au) : __fadd_rn(au, __fmul_rn(lu[k0 + k], fu));
+                    }
+            }
+            const float g = __fmul_rn(ag, wh_f16_scale(((const uint16_t *)(rec + a.sc_gate))[r]));
+            const float uu = __fmul_rn(au, wh_f16_scale(((const uint16_t *)(rec + a.sc_up))[r]));
+            s_x[tid] = tid < i_hi ? wh_silu_mul(g, uu) : 0.0f;
+        }
+        __syncthreads();
+        issue();
+        // the tables while the first tiles fly: thread (stage, entry) builds
+        // the eight positions quarter*8 .. of each block, twice (once for the
+        // block's max, once to quantize: the same operations, the same values)
+        auto entry = [&](int bl, int v) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                const float xv = s_x[bl * 8 * P6_BLK + v * 8 + d];
+                acc = FMA ? __fmaf_rn(xv, c[d], acc) : __fadd_rn(acc, __fmul_rn(xv, c[d]));
+            }
+            return acc;
+        };
+        for (int bl = 0; bl < nbg; bl++) {           // uniform
+            const int n = min(P6_BLK, nv - (b0 + bl) * P6_BLK);
+            float mx = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int v = quarter * 8 + k;
+                const float l = entry(bl, v);
+                if (v < n) mx = fmaxf(mx, fabsf(l));   // order-free: no NaN survives fmaxf
+            }
+#pragma unroll
+            for (int m = 32; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+            if (lane == 0) s_mx[bl][wv] = mx;
+        }
+        __syncthreads();
+        for (int bl = 0; bl < nbg; bl++) {           // uniform
+            const int n = min(P6_BLK, nv - (b0 + bl) * P6_BLK);
+            float mx = s_mx[bl][0];
+#pragma unroll
+            for (int w = 1; w < P6_WAVES; w++) mx = fmaxf(mx, s_mx[bl][w]);
+            if (tid == 0 && j == 0) a.qs[tab * a.nb + b0 + bl] = __fdiv_rn(mx, 127.0f);
+            const float inv = mx > 0.0f ? __fdiv_rn(127.0f, mx) : 0.0f;
+            int8_t *T = s_tab + bl * P6_BLK * P6_TS + st * P6_EN + e;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int v = quarter * 8 + k;
+                const float t = rintf(__fmul_rn(entry(bl, v), inv));   // half to even, as lrintf
+                T[v * P6_TS] = v < n ? (int8_t)(int)fminf(127.0f, fmaxf(-127.0f, t)) : (int8_t)0;
+            }
+        }
+        __syncthreads();
+    }
+    for (int i = 0; i < cnt; i += 2) {               // uniform
+        sum_tile(cA, tile_at(i));
+        __builtin_amdgcn_sched_barrier(0);
+        load(cA, tile_at(i + 2));
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < cnt) sum_tile(cB, tile_at(i + 1));
+        __builtin_amdgcn_sched_barrier(0);
+        load(cB, tile_at(i + 3));
+        __builtin_amdgcn_sched_barrier(0);
+    }
 }
 
-extern "C" int whip_p6_act(const float *gu, int P, int I, float *h, hipStream_t s)
+// the launch's partition: runs of at most 32 row blocks; groups of scale
+// blocks so that there is about one workgroup per CU
+static int p6_launch(p6_tile_args &a, int P, int mode, int fma, hipStream_t s)
 {
-    if (P <= 0 || I <= 0) return (int)hipErrorInvalidValue;
-    const size_t n = (size_t)P * I;
-    hipLaunchKernelGGL(k_p6_act, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, gu, I, n, h);
+    const int nrb = a.M / 64;
+    a.nb = (a.nv + P6_BLK - 1) / P6_BLK;
+    long shares = (nrb + 31) / 32;
+    a.per = (int)((nrb + shares - 1) / shares);
+    a.shares = (int)((nrb + a.per - 1) / a.per);
+    const long tiles = (long)P * a.kinds * a.nb * nrb, want = (tiles + 255) / 256;
+    const int maxg = mode == P6_ACT ? P6_MAXG_ACT : P6_MAXG;
+    long ncb = (2 * want + a.per) / (2 * a.per);      // rounded
+    if (ncb > maxg) ncb = maxg;
+    if (ncb > a.nb) ncb = a.nb;
+    if (ncb < 1) ncb = 1;
+    a.ncb = (int)ncb;
+    a.ngrp = (a.nb + a.ncb - 1) / a.ncb;
+    const long grid = (long)P * a.kinds * a.ngrp * a.shares;
+    if (grid > 0x7fffffffL) return (int)hipErrorInvalidValue;
+#define TL(A, F) WHIP_LAUNCH((k_p6_tiles<A, F>), dim3((unsigned)grid), dim3(P6_THREADS), 0, s, a)
+    if (mode == P6_Q) TL(P6_Q, false);
+    else if (mode == P6_ACT) { if (fma) TL(P6_ACT, true); else TL(P6_ACT, false); }
+    else { if (fma) TL(P6_X, true); else TL(P6_X, false); }
+#undef TL
     return (int)hipGetLastError();
+}
+
+extern "C" int whip_p6_gate_up(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                               const uint32_t *idx_off, int I, const void *x, int x_bf16, int x_ld, int nv,
+                               const float *booksT, int cb, int fma, const int8_t *q, int16_t *S, float *qs, int *err,
+                               hipStream_t s)
+{
+    if (P <= 0 || I <= 0 || I % 64 || nv <= 0 || idx_off[0] % 4 || idx_off[1] % 4 || (uintptr_t)q % 16 ||
+        (!q && (x_ld < nv * 8 || cb < 0)))
+        return (int)hipErrorInvalidValue;
+    p6_tile_args a = {};
+    a.recs = recs; a.pair_exp = pair_exp; a.pair_tok = pair_tok; a.kinds = 2;
+    a.idx_off0 = idx_off[0]; a.idx_off1 = idx_off[1]; a.M = I; a.nv = nv;
+    a.S = S; a.qs = qs; a.err = err; a.q = q; a.booksT = booksT; a.cb = cb;
+    a.x = x; a.x_bf16 = x_bf16; a.x_ld = x_ld;
+    return p6_launch(a, P, q ? P6_Q : P6_X, fma, s);
+}
+
+extern "C" int whip_p6_down(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
+                            uint32_t idx_off, int H, int I, const int16_t *Sg, const float *qs_g, uint32_t sc_gate,
+                            uint32_t sc_up, int nv_g, const float *booksT, int cb, int fma, const int8_t *q,
+                            int16_t *S, float *qs, int *err, hipStream_t s)
+{
+    if (P <= 0 || H <= 0 || H % 64 || I <= 0 || I % 8 || idx_off % 4 || (uintptr_t)q % 16 ||
+        (!q && (nv_g <= 0 || cb < 0 || sc_gate % 2 || sc_up % 2)))
+        return (int)hipErrorInvalidValue;
+    p6_tile_args a = {};
+    a.recs = recs; a.pair_exp = pair_exp; a.pair_tok = pair_tok; a.kinds = 1;
+    a.idx_off0 = idx_off; a.idx_off1 = idx_off; a.M = H; a.nv = I / 8;
+    a.S = S; a.qs = qs; a.err = err; a.q = q; a.booksT = booksT; a.cb = cb;
+    a.Sg = Sg; a.qs_g = qs_g; a.sc_gate = sc_gate; a.sc_up = sc_up; a.nb_g = (nv_g + P6_BLK - 1) / P6_BLK;
+    return p6_launch(a, P, q ? P6_Q : P6_ACT, fma, s);
 }

@@ -97,7 +97,7 @@ struct waste_hip_moe {
         int8_t *q_gu, *q_d;      /* VQ4P: int8 tables [T][2][nv_gu][256], [P][nv_d][256] */
         float *s_gu, *s_d;       /* and their scales, one per 32 positions */
         int16_t *S_gu, *S_d;     /* VQ4P block sums [P][2][nb_gu][I], [P][nb_d][H] */
-        float *gu, *h, *down;    /* VQ2R: rows [P][2][I], SwiGLU [P][I], down [P][H] */
+        float *gu, *down;        /* VQ2R: rows [P][2][I], down [P][H]      */
     } p6b;
     /* few-token products on the matrix cores (skinny.hip): column slices of
      * the router, the shared gate/up and the shared down (0: not taken),
@@ -158,7 +158,7 @@ void waste_hip_moe_destroy(waste_hip_moe *m)
                      m->b.tok_pairs, m->err, m->pair_pos, m->seg_off, m->order, m->h16,
                      m->sh_h16, m->x16, m->ypair, m->rpart, m->d_books16, m->plogits, m->pw, m->d_look, (void *)m->b.pair_rec,
                      m->b.rcnt, m->b.xchg, m->sk_mem, m->p6b.lut_gu, m->p6b.lut_d, m->p6b.q_gu,
-                     m->p6b.q_d, m->p6b.s_gu, m->p6b.s_d, m->p6b.S_gu, m->p6b.S_d, m->p6b.gu, m->p6b.h,
+                     m->p6b.q_d, m->p6b.s_gu, m->p6b.s_d, m->p6b.S_gu, m->p6b.S_d, m->p6b.gu,
                      m->p6b.down };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) if (bufs[i]) hipFree(bufs[i]);
     if (m->ev[0]) {
@@ -260,14 +260,15 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
         rc |= dmalloc((void **)&m->p6b.lut_gu, (size_t)m->T * 2 * tg * 4);
         rc |= dmalloc((void **)&m->p6b.lut_d, (size_t)P * td * 4);
         rc |= dmalloc((void **)&m->p6b.gu, (size_t)P * 2 * m->I * 4);
-        rc |= dmalloc((void **)&m->p6b.h, (size_t)P * m->I * 4);
         rc |= dmalloc((void **)&m->p6b.down, (size_t)P * m->H * 4);
     } else if (m->p6) {
         const size_t tg = (size_t)m->nv_gu * 256, td = (size_t)m->nv_d * 256;
         const size_t bg = (size_t)(m->nv_gu + 31) / 32, bd = (size_t)(m->nv_d + 31) / 32;
-        rc |= dmalloc((void **)&m->p6b.q_gu, (size_t)m->T * 2 * tg);
+        if (m->T > 1) {
+            rc |= dmalloc((void **)&m->p6b.q_gu, (size_t)m->T * 2 * tg);
+            rc |= dmalloc((void **)&m->p6b.q_d, (size_t)P * td);
+        }
         rc |= dmalloc((void **)&m->p6b.s_gu, (size_t)m->T * 2 * bg * 4);
-        rc |= dmalloc((void **)&m->p6b.q_d, (size_t)P * td);
         rc |= dmalloc((void **)&m->p6b.s_d, (size_t)P * bd * 4);
         rc |= dmalloc((void **)&m->p6b.S_gu, (size_t)P * 2 * bg * m->I * 2);
         rc |= dmalloc((void **)&m->p6b.S_d, (size_t)P * bd * m->H * 2);
@@ -798,30 +799,38 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
  * through them (vq_rows_p6: exact integer sums per scale block, folded into
  * fp32 in block order), SwiGLU, the pair's down table from its SwiGLU
  * output and its down rows, then the combine and the shared expert as for
- * VQ3R.  Four launches and the combine: the block sums wait in HBM for the
- * launch that folds them (the down table build, the combine).  The tables
- * and folds follow the engine's arithmetic in the layer's p6_order, so each
- * pair's rows are the engine's bit for bit. */
+ * VQ3R.  Two launches and the combine: each tile launch builds the tables
+ * it reads, the block sums wait in HBM for the launch that folds them (the
+ * down launch, the combine).  The tables and folds follow the engine's
+ * arithmetic in the layer's p6_order, so each pair's rows are the engine's
+ * bit for bit. */
 static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, hipStream_t s);
 
 static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
 {
     const int K = m->K, H = m->H, I = m->I, P = T * K, fma = m->c.p6_order == WASTE_HIP_ORDER_FMA;
-    const int cb = m->cb - m->book0;
+    const int cb = m->cb - m->book0, cb_d = cb + 2 * m->stages;
+    const uint32_t gu_idx[2] = { m->off_gate, m->off_up };
+    const uint32_t sc_g = m->off_sc, sc_u = m->off_sc + 2u * (uint32_t)I;
+    /* one token: the tile launches build their tables (two launches fewer);
+     * more: the tables once per token and pair, the tiles read them */
+    const int8_t *q_gu = T > 1 ? m->p6b.q_gu : NULL, *q_d = T > 1 ? m->p6b.q_d : NULL;
     m->ktimed = 0;               /* these stages are timed by the events around them */
     MARK(2);
-    CK((hipError_t)whip_p6_lutq(x, x_bf16, H, T, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.q_gu, m->p6b.s_gu, s));
-    const uint32_t gu_idx[2] = { m->off_gate, m->off_up };
-    CK((hipError_t)whip_p6_tiles(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 2, gu_idx, I, m->nv_gu, m->p6b.q_gu,
-                                 1, m->p6b.S_gu, m->err, s));
+    if (q_gu)
+        CK((hipError_t)whip_p6_lutq(x, x_bf16, H, T, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.q_gu, m->p6b.s_gu,
+                                    s));
+    CK((hipError_t)whip_p6_gate_up(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, gu_idx, I, x, x_bf16, H, m->nv_gu,
+                                   m->d_booksT, cb, fma, q_gu, m->p6b.S_gu, m->p6b.s_gu, m->err, s));
     MARK(3);
-    CK((hipError_t)whip_p6_act_lutq(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, m->p6b.S_gu, m->p6b.s_gu,
-                                    m->off_sc, m->off_sc + 2u * (uint32_t)I, I, m->nv_gu, m->d_booksT,
-                                    cb + 2 * m->stages, m->nv_d, fma, m->p6b.q_d, m->p6b.s_d, s));
+    if (q_d)
+        CK((hipError_t)whip_p6_act_lutq(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, m->p6b.S_gu, m->p6b.s_gu, sc_g,
+                                        sc_u, I, m->nv_gu, m->d_booksT, cb_d, m->nv_d, fma, m->p6b.q_d, m->p6b.s_d,
+                                        s));
     MARK(4);
-    const uint32_t d_idx[1] = { m->off_down };
-    CK((hipError_t)whip_p6_tiles(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, H, m->nv_d, m->p6b.q_d, 0,
-                                 m->p6b.S_d, m->err, s));
+    CK((hipError_t)whip_p6_down(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, m->off_down, H, I, m->p6b.S_gu,
+                                m->p6b.s_gu, sc_g, sc_u, m->nv_gu, m->d_booksT, cb_d, fma, q_d, m->p6b.S_d,
+                                m->p6b.s_d, m->err, s));
     MARK(5);
     const whip_fold f = { m->p6b.S_d, m->p6b.s_d, (m->nv_d + 31) / 32, m->off_sc + 4u * (uint32_t)I, fma };
     return alt_combine(m, T, y, &f, s);
@@ -845,10 +854,8 @@ static int experts_r2(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
     CK((hipError_t)whip_r2_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 2, gu_idx, gu_sc, I, m->nv_gu,
                                       m->p6b.lut_gu, 1, m->p6b.gu, m->err, s));
     MARK(3);
-    CK((hipError_t)whip_p6_act(m->p6b.gu, P, I, m->p6b.h, s));
+    CK((hipError_t)whip_r2_act_lutb(m->p6b.gu, P, I, m->d_booksT, cb + 2 * m->stages, fma, m->p6b.lut_d, s));
     MARK(4);
-    CK((hipError_t)whip_r2_lutb(m->p6b.h, 0, I, P, 1, 2, m->d_booksT, cb + 2 * m->stages, m->nv_d, fma,
-                                m->p6b.lut_d, s));
     const uint32_t d_idx[1] = { m->off_down }, d_sc[1] = { m->off_sc + 4u * (uint32_t)I };
     CK((hipError_t)whip_r2_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, d_sc, H, m->nv_d,
                                       m->p6b.lut_d, 0, m->p6b.down, m->err, s));
