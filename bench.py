@@ -717,7 +717,10 @@ def main():
     ap.add_argument("--no-stack-grouped", dest="stack_grouped", action="store_false",
                     help="skip the second stack run, whose lookahead guesses lie within the group limit")
     ap.add_argument("--no-extra-configs", dest="extra_configs", action="store_false",
-                    help="skip the other decode configurations (olmoe B=1, kimi B=1/4/16, dsv3 B=8/32)")
+                    help="skip the other decode configurations (olmoe B=1, kimi B=1/4/16, dsv3 B=8/32) "
+                         "and the other record formats (VQ4P rows, VQ4P and VQ2R layers)")
+    ap.add_argument("--no-decode-configs", dest="decode_configs", action="store_false",
+                    help="skip the other decode configurations (C3 batch 8/32, C1, C2); the formats still run")
     ap.add_argument("--copy-calibrate", type=int, default=0, metavar="MB",
                     help="first copy MB megabytes device to device (a plain copy kernel of known "
                          "size, the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -761,7 +764,7 @@ def main():
     # small shapes with a slab per object so the cycled records do not fit
     # the Infinity Cache
     per_config = None
-    if a.extra_configs and B == 1 and a.config == "dsv3":
+    if a.extra_configs and a.decode_configs and B == 1 and a.config == "dsv3":
         per_config = []
         big = build_layers(torch, warp_amd, synth, cfg, a.layers, 32, slab=slab, books=books)[0]
         for bb in (8, 32):

@@ -489,16 +489,17 @@ k_p6_tiles(p6_tile_args a)
         // the group's tables (16 uint4s a position; past the group: the
         // first ones, unused), to LDS at the 320-byte stride
         const int v_lo = b0 * P6_BLK, nq = (min(nv, v_lo + nbg * P6_BLK) - v_lo) * 16;
-        const uint4 *tsrc = (const uint4 *)(a.q + (tab * nv + v_lo) * 4 * P6_EN);
+        typedef unsigned v4u __attribute__((ext_vector_type(4)));   // kept in registers, unlike uint4 here
+        const v4u *tsrc = (const v4u *)(a.q + (tab * nv + v_lo) * 4 * P6_EN);
         constexpr int TV = P6_MAXG * P6_BLK * 16 / P6_THREADS;
-        uint4 tv[TV];
+        v4u tv[TV];
 #pragma unroll
         for (int k = 0; k < TV; k++) tv[k] = tsrc[tid + k * P6_THREADS < nq ? tid + k * P6_THREADS : 0];
         issue();
 #pragma unroll
         for (int k = 0; k < TV; k++) {
             const int g = tid + k * P6_THREADS;
-            *(uint4 *)(s_tab + (g >> 4) * P6_TS + (g & 15) * 16) = tv[k];
+            *(v4u *)(s_tab + (g >> 4) * P6_TS + (g & 15) * 16) = tv[k];
         }
         __syncthreads();
     } else {
