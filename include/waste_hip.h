@@ -99,7 +99,10 @@ int waste_hip_vq_quant_lut(const float *lut, int nv, int stages, int entries, in
  * aligned), device pointers.  order WASTE_HIP_ORDER_PORTABLE folds the
  * blocks as the portable C kernel does, WASTE_HIP_ORDER_FMA as the AVX-512
  * and NEON kernels do; either is bit-identical to that kernel.  r_lo a
- * multiple of 64.
+ * multiple of 64.  Ranges of fewer than 64 whole 64-row blocks keep their
+ * integer block sums in a device workspace the library allocates on a
+ * stream's first such call (and grows when a call needs more): one per
+ * stream, kept until the process ends.
  * Replaces: the vq_rows_p6 slot, src/model.c:4076-4114,
  * src/simd_avx512.c:129-236, src/kda_neon.c:100-190. */
 #define WASTE_HIP_ORDER_PORTABLE 0

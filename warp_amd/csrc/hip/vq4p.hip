@@ -13,6 +13,10 @@
 // exact integer sum, and the fold either as the portable C kernel does it
 // (a product, then a sum) or as the compilers contract it in the AVX-512
 // and NEON kernels (one fused multiply-add).
+#include <mutex>
+#include <tuple>
+#include <vector>
+
 #include "common.h"
 #include "launch.h"
 
@@ -179,16 +183,33 @@ k_vq_rows_p6(const uint8_t *__restrict__ idx, const uint16_t *__restrict__ scale
     p6_rows<FMA>(idx, scale, lut8, lscale, r_lo / 64 + blockIdx.x, r_hi, nv, y);
 }
 
+// (defined with the layer's tile kernels below)
+static int p6_rows_tiled(const uint8_t *idx, const uint16_t *scale, const int8_t *lut8, const float *lscale,
+                         int r_lo, int nblk, int nv, int fma, float *y, hipStream_t s);
+
 // Rows [r_lo, r_hi) (r_lo a multiple of 64); idx, scale and y are indexed
 // from row 0 of the matrix.  fma: the fold as one fused multiply-add.
+// With fewer than 64 row blocks (one workgroup each would leave most CUs
+// idle) whole blocks go through the tile kernel (their block sums in a
+// workspace, then the fold: two launches); a partial last block, whose
+// codes end at its last row (the engine's record holds no bytes past them),
+// and every block of a taller range through the row kernel above, which
+// reads no further.
 extern "C" int whip_vq_rows_p6(const uint8_t *idx, const uint16_t *scale, const int8_t *lut8,
                                const float *lscale, int r_lo, int r_hi, int nv, int fma, float *y,
                                hipStream_t s)
 {
     if (r_lo < 0 || r_lo % 64 || r_hi <= r_lo || nv <= 0 || (uintptr_t)lut8 % 16) return (int)hipErrorInvalidValue;
-    const dim3 grid((r_hi - r_lo + 63) / 64);
-    if (fma) hipLaunchKernelGGL(k_vq_rows_p6<true>, grid, dim3(P6_THREADS), 0, s, idx, scale, lut8, lscale, r_lo, r_hi, nv, y);
-    else hipLaunchKernelGGL(k_vq_rows_p6<false>, grid, dim3(P6_THREADS), 0, s, idx, scale, lut8, lscale, r_lo, r_hi, nv, y);
+    const int full = (r_hi - r_lo) / 64 < 64 ? (r_hi - r_lo) / 64 : 0, tail = r_lo + 64 * full;
+    if (full > 0) {
+        const int rc = p6_rows_tiled(idx, scale, lut8, lscale, r_lo, full, nv, fma, y, s);
+        if (rc) return rc;
+    }
+    if (tail < r_hi) {
+        const dim3 grid((r_hi - tail + 63) / 64);
+        if (fma) hipLaunchKernelGGL(k_vq_rows_p6<true>, grid, dim3(P6_THREADS), 0, s, idx, scale, lut8, lscale, tail, r_hi, nv, y);
+        else hipLaunchKernelGGL(k_vq_rows_p6<false>, grid, dim3(P6_THREADS), 0, s, idx, scale, lut8, lscale, tail, r_hi, nv, y);
+    }
     return (int)hipGetLastError();
 }
 
@@ -380,6 +401,7 @@ extern "C" int whip_p6_act_lutq(const uint8_t *const *recs, const int32_t *pair_
 }
 
 struct p6_tile_args {
+    const uint8_t *raw;                // set: one matrix at raw (pair 0, table 0; no records)
     const uint8_t *const *recs;
     const int32_t *pair_exp, *pair_tok;
     int kinds;
@@ -419,14 +441,14 @@ k_p6_tiles(p6_tile_args a)
     const int rb0 = j * a.per, rb1 = min(a.M / 64, rb0 + a.per), ntile = nbg * (rb1 - rb0);
     const int M = a.M, nv = a.nv;
     int16_t *out = a.S + ((size_t)pk * a.nb + b0) * M;   // block b0 + bl at out + bl * M
-    const uint8_t *rec = a.recs[a.pair_exp[p]];
+    const uint8_t *rec = a.raw ? a.raw : a.recs[a.pair_exp[p]];
     if (rec == nullptr) {                            // uniform
         for (int bl = 0; bl < nbg; bl++)
             for (int r = rb0 * 64 + tid; r < rb1 * 64; r += P6_THREADS) out[(size_t)bl * M + r] = 0;
         if (tid == 0) atomicOr(a.err, 1);
         return;
     }
-    const int tok = a.pair_tok[p];
+    const int tok = a.raw ? 0 : a.pair_tok[p];
     const size_t tab = a.kinds == 2 ? (size_t)tok * 2 + kind : (size_t)p;
     g_u8 *mat = as_global(rec) + (kind ? a.idx_off1 : a.idx_off0);
     const int qd = lane & 15, slot = lane >> 4;
@@ -626,7 +648,17 @@ static int p6_launch(p6_tile_args &a, int P, int mode, int fma, hipStream_t s)
     if (ncb < 1) ncb = 1;
     a.ncb = (int)ncb;
     a.ngrp = (a.nb + a.ncb - 1) / a.ncb;
-    const long grid = (long)P * a.kinds * a.ngrp * a.shares;
+    // a small problem (one matrix) spreads over more, shorter runs
+    const long groups = (long)P * a.kinds * a.ngrp;
+    if (groups * a.shares < 128) {
+        long sh = (256 + groups - 1) / groups;
+        if (sh > nrb) sh = nrb;
+        if (sh > a.shares) {
+            a.per = (int)((nrb + sh - 1) / sh);
+            a.shares = (nrb + a.per - 1) / a.per;
+        }
+    }
+    const long grid = groups * a.shares;
     if (grid > 0x7fffffffL) return (int)hipErrorInvalidValue;
 #define TL(A, F) WHIP_LAUNCH((k_p6_tiles<A, F>), dim3((unsigned)grid), dim3(P6_THREADS), 0, s, a)
     if (mode == P6_Q) TL(P6_Q, false);
@@ -666,4 +698,84 @@ extern "C" int whip_p6_down(const uint8_t *const *recs, const int32_t *pair_exp,
     a.S = S; a.qs = qs; a.err = err; a.q = q; a.booksT = booksT; a.cb = cb;
     a.Sg = Sg; a.qs_g = qs_g; a.sc_gate = sc_gate; a.sc_up = sc_up; a.nb_g = (nv_g + P6_BLK - 1) / P6_BLK;
     return p6_launch(a, P, q ? P6_Q : P6_ACT, fma, s);
+}
+
+// y[r_lo + i] = fold over the blocks in order of ls[b] * S[b*M + i], times
+// the row's f16 scale (vq_rows_p6's fold), i < M.
+template <bool FMA>
+__global__ void __launch_bounds__(256)
+k_p6_fold(const int16_t *__restrict__ S, int nb, int M, const float *__restrict__ ls,
+          const uint16_t *__restrict__ scale, int r_lo, float *__restrict__ y)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= M) return;
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < nb; k0 += P6_MAXB) {        // every block's sums in flight, then the fold
+        const int kn = min(P6_MAXB, nb - k0);
+        int16_t sv[P6_MAXB];
+#pragma unroll
+        for (int k = 0; k < P6_MAXB; k++) sv[k] = S[(size_t)(k0 + (k < kn ? k : 0)) * M + i];
+#pragma unroll
+        for (int k = 0; k < P6_MAXB; k++)
+            if (k < kn) {
+                const float f = (float)sv[k];
+                acc = FMA ? __fmaf_rn(ls[k0 + k], f, acc) : __fadd_rn(acc, __fmul_rn(ls[k0 + k], f));
+            }
+    }
+    y[r_lo + i] = __fmul_rn(acc, wh_f16_scale(scale[r_lo + i]));
+}
+
+// The block sums' workspace of whip_vq_rows_p6: one per (device, stream),
+// grown when a call needs more (hipFree waits for the device, so the old
+// one is idle by then) and kept until the process ends.  Calls on one
+// stream run in order; calls on different streams never share one.
+static std::mutex g_ws_mu;
+static std::vector<std::tuple<int, hipStream_t, void *, size_t>> g_ws;
+
+static int p6_workspace(hipStream_t s, size_t bytes, void **out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    for (auto &w : g_ws)
+        if (std::get<0>(w) == dev && std::get<1>(w) == s) {
+            if (std::get<3>(w) < bytes) {
+                e = hipFree(std::get<2>(w));
+                std::get<2>(w) = nullptr;
+                std::get<3>(w) = 0;
+                if (e != hipSuccess) return (int)e;
+                e = hipMalloc(&std::get<2>(w), bytes);
+                if (e != hipSuccess) return (int)e;
+                std::get<3>(w) = bytes;
+            }
+            *out = std::get<2>(w);
+            return 0;
+        }
+    void *p = nullptr;
+    e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return (int)e;
+    g_ws.emplace_back(dev, s, p, bytes);
+    *out = p;
+    return 0;
+}
+
+static int p6_rows_tiled(const uint8_t *idx, const uint16_t *scale, const int8_t *lut8, const float *lscale,
+                         int r_lo, int nblk, int nv, int fma, float *y, hipStream_t s)
+{
+    const int M = 64 * nblk, nb = (nv + P6_BLK - 1) / P6_BLK;
+    int16_t *S = nullptr;
+    const int wrc = p6_workspace(s, (size_t)nb * M * sizeof(int16_t), (void **)&S);
+    if (wrc) return wrc;
+    p6_tile_args a = {};
+    a.raw = idx + (size_t)(r_lo / 64) * nv * 192;
+    a.kinds = 1; a.M = M; a.nv = nv; a.S = S; a.q = lut8;
+    int rc = p6_launch(a, 1, P6_Q, fma, s);
+    if (!rc) {
+        const dim3 grid((M + 255) / 256);
+        if (fma) hipLaunchKernelGGL(k_p6_fold<true>, grid, dim3(256), 0, s, S, nb, M, lscale, scale, r_lo, y);
+        else hipLaunchKernelGGL(k_p6_fold<false>, grid, dim3(256), 0, s, S, nb, M, lscale, scale, r_lo, y);
+        rc = (int)hipGetLastError();
+    }
+    return rc;
 }
