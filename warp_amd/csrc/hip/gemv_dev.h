@@ -5,6 +5,7 @@
 // one-launch decode.
 #pragma once
 #include "common.h"
+#include "launch.h"
 
 // elements per 16-byte chunk of a row
 template <int FMT> struct chunk_of;
@@ -145,3 +146,75 @@ __device__ __forceinline__ float chunk_sum136_bf(const uint4 *xw)
     }
     return 136.0f * s;
 }
+
+// The shared expert's down projection, eight rows r0 .. r0+7 per
+// wavefront: each lane a 16-byte chunk of every row per step against the
+// matching slice of x (fp32), then eight wave sums.  Used by the combine
+// (rows of its block) and by the gate/up launches' spare workgroups.
+template <int FMT>
+__device__ __forceinline__ void sh_rows8_acc(const whip_mat &W, const float *x, int r0, int H, int lane,
+                                             float (&acc)[8])
+{
+    constexpr int NE = chunk_of<FMT>::NE, NW = xw_of<FMT, false>::N;
+    const int ng = FMT == 0 ? 1 : (W.cols + W.group - 1) / W.group;
+    const int C = (FMT == 0 ? W.cols : ng * W.group) / NE;
+    const uint8_t *Wq = (const uint8_t *)W.q;
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+    for (int k0 = 0; k0 < C; k0 += 64) {            // uniform
+        const int k = k0 + lane, kc = k < C ? k : 0;
+        uint4 xw[NW], wv[8];
+        uint16_t sv[8];
+        load_xs<FMT, false>(x, W.cols, kc, xw);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int r = min(r0 + i, H - 1);
+            wv[i] = *(const uint4 *)(Wq + (size_t)r * W.rowbytes + (size_t)kc * 16);
+            if (FMT != 0) sv[i] = W.qs[(size_t)r * ng + (size_t)kc * NE / W.group];
+        }
+        if (k < C) {
+            mask_xs<FMT, false>(W.cols, k, xw);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float d = chunk_dot<FMT, false>(wv[i], xw);
+                acc[i] = FMT == 0 ? acc[i] + d : __fmaf_rn(wh_f16_scale(sv[i]), d, acc[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[i] = wave_sum(acc[i]);
+}
+
+// A launch's spare workgroups computing y = W . x (the shared expert's down
+// projection, fp32 x): rows in groups of eight, one group per wavefront at
+// a time; workgroup g of NG, `waves` wavefronts each.
+template <int FMT>
+__device__ __forceinline__ void shd_rows_role(const whip_mat &W, const float *x, float *y, int g, int NG, int waves)
+{
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int H = W.rows, ngr = (H + 7) / 8;
+    for (int rg = g * waves + wv; rg < ngr; rg += NG * waves) {   // wave-uniform
+        float acc[8];
+        sh_rows8_acc<FMT>(W, x, rg * 8, H, lane, acc);
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (rg * 8 + i < H) y[rg * 8 + i] = acc[i];
+    }
+}
+
+__device__ __forceinline__ void shd_rows_any(const whip_mat &W, const float *x, float *y, int g, int NG, int waves)
+{
+    if (W.fmt == 3) shd_rows_role<3>(W, x, y, g, NG, waves);
+    else if (W.fmt == 2) shd_rows_role<2>(W, x, y, g, NG, waves);
+    else shd_rows_role<0>(W, x, y, g, NG, waves);
+}
+
+// whole 16-byte chunks of fp32 x, F32 / Q8G / Q4G rows (what the roles take)
+static inline bool shd_rows_ok(const whip_mat *W, const float *x)
+{
+    return W && x && (uintptr_t)x % 16 == 0 && W->rows >= 1 && W->rowbytes % 16 == 0 &&
+           (W->fmt == 0 || W->fmt == 2 || W->fmt == 3) && (W->fmt == 0 || (W->group % 32 == 0 && W->cols % 8 == 0)) &&
+           (W->fmt != 0 || W->cols % 4 == 0);
+}
+

@@ -204,11 +204,13 @@ int whip_p6_act_lutq(const uint8_t *const *recs, const int32_t *pair_exp, const 
  * from x row pair_tok[p] (bf16 or fp32, row stride x_ld) and books
  * cb .. cb+7 of booksT ([book][8][64] fp32) in the engine's order for fma,
  * their scales written to qs[tok][2][nb].  An unbound expert's sums are
- * zeros and raise bit 0 of err.  I % 64 == 0. */
+ * zeros and raise bit 0 of err.  I % 64 == 0.  With q NULL and shd_y set,
+ * spare workgroups also compute shd_y = shd . shd_x (fp32 x; 16-byte
+ * chunks: refused otherwise). */
 int whip_p6_gate_up(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
                     const uint32_t *idx_off, int I, const void *x, int x_bf16, int x_ld, int nv,
                     const float *booksT, int cb, int fma, const int8_t *q, int16_t *S, float *qs, int *err,
-                    hipStream_t s);
+                    const whip_mat *shd, const float *shd_x, float *shd_y, hipStream_t s);
 /* The down tile launch: the sums of each pair's down rows (idx at idx_off;
  * S[(p*nb + b)*H + r], nb = I/256 rounded up) through its table: q's table
  * p (whip_p6_act_lutq's), or with q NULL built here as whip_p6_act_lutq
@@ -219,10 +221,13 @@ int whip_p6_down(const uint8_t *const *recs, const int32_t *pair_exp, const int3
                  uint32_t sc_up, int nv_g, const float *booksT, int cb, int fma, const int8_t *q, int16_t *S,
                  float *qs, int *err, hipStream_t s);
 /* VQ2R (vq2r.hip): fp32 tables lut[t][nv][st][256] of rows x kinds inputs in
- * the engine's order, and every pair's rows through them in vq_rows'
- * order (two stages, two index bytes a row and position). */
+ * the engine's order (st == 2; shd_y set: spare workgroups also compute
+ * shd_y = shd . shd_x, refused for shapes they do not take), and every
+ * pair's rows through them in vq_rows' order (two stages, two index bytes a
+ * row and position). */
 int whip_r2_lutb(const void *x, int x_bf16, int x_ld, int rows, int kinds, int st, const float *booksT, int cb,
-                 int nv, int fma, float *lut, hipStream_t s);
+                 int nv, int fma, float *lut, const whip_mat *shd, const float *shd_x, float *shd_y,
+                 hipStream_t s);
 /* The down tables of P pairs from their gate and up rows gu[p][2][I]:
  * h = silu(g) * u, then whip_r2_lutb's tables of h (one kind, books cb ..). */
 int whip_r2_act_lutb(const float *gu, int P, int I, const float *booksT, int cb, int fma, float *lut,

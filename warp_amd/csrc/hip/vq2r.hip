@@ -9,6 +9,7 @@
 // order, y = acc * f16(scale)).  One lane per row owns its sum; the tables
 // are read through the caches.
 #include "common.h"
+#include "gemv_dev.h"
 #include "launch.h"
 
 #define R2_EN 256
@@ -23,9 +24,15 @@
 template <bool FMA, bool ACT>
 __global__ void __launch_bounds__(R2_EN)
 k_r2_lutb(const void *__restrict__ x, int x_bf16, int x_ld, int kinds, const float *__restrict__ booksT, int cb,
-          int nv, float *__restrict__ lut)
+          int nv, float *__restrict__ lut, whip_mat shd, const float *__restrict__ shd_x, float *__restrict__ shd_y,
+          int tabs)
 {
     __shared__ float s_x[R2_LV * 8];
+    if (!ACT && (int)blockIdx.y >= tabs) {           // uniform: the rows past the tables' run the shared down
+        shd_rows_any(shd, shd_x, shd_y, (blockIdx.y - tabs) * gridDim.x + blockIdx.x, (gridDim.y - tabs) * gridDim.x,
+                     R2_EN / 64);
+        return;
+    }
     const int t = blockIdx.y, row = t / kinds, kind = t - row * kinds;
     const int e = threadIdx.x;
     const int v0 = blockIdx.x * R2_LV, n = min(R2_LV, nv - v0);
@@ -61,13 +68,26 @@ k_r2_lutb(const void *__restrict__ x, int x_bf16, int x_ld, int kinds, const flo
 }
 
 extern "C" int whip_r2_lutb(const void *x, int x_bf16, int x_ld, int rows, int kinds, int st, const float *booksT,
-                            int cb, int nv, int fma, float *lut, hipStream_t s)
+                            int cb, int nv, int fma, float *lut, const whip_mat *shd, const float *shd_x,
+                            float *shd_y, hipStream_t s)
 {
-    if (rows <= 0 || kinds <= 0 || rows * kinds > 65535 || st != 2 || nv <= 0 || x_ld < nv * 8 || cb < 0)
+    if (rows <= 0 || kinds <= 0 || rows * kinds > 65535 || st != 2 || nv <= 0 || x_ld < nv * 8 || cb < 0 ||
+        (shd_y && !shd_rows_ok(shd, shd_x)))
         return (int)hipErrorInvalidValue;
-    const dim3 grid((nv + R2_LV - 1) / R2_LV, rows * kinds);
-    if (fma) WHIP_LAUNCH((k_r2_lutb<true, false>), grid, dim3(R2_EN), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, lut);
-    else WHIP_LAUNCH((k_r2_lutb<false, false>), grid, dim3(R2_EN), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, lut);
+    const int gx = (nv + R2_LV - 1) / R2_LV, tabs = rows * kinds;
+    // shd_y: rows of spare workgroups (four wavefronts each) for the shared
+    // down projection, to about two workgroups per CU beside the tables'
+    int ry = 0;
+    if (shd_y) {
+        const int spare = 512 - gx * tabs;
+        ry = (spare > 8 * 1 ? spare : 8) / gx + 1;
+    }
+    const dim3 grid(gx, tabs + ry);
+    const whip_mat W = shd_y ? *shd : whip_mat{};
+    if (fma) WHIP_LAUNCH((k_r2_lutb<true, false>), grid, dim3(R2_EN), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, lut,
+                         W, shd_x, shd_y, tabs);
+    else WHIP_LAUNCH((k_r2_lutb<false, false>), grid, dim3(R2_EN), 0, s, x, x_bf16, x_ld, kinds, booksT, cb, nv, lut,
+                     W, shd_x, shd_y, tabs);
     return (int)hipGetLastError();
 }
 
@@ -77,8 +97,10 @@ extern "C" int whip_r2_act_lutb(const float *gu, int P, int I, const float *book
     if (P <= 0 || P > 65535 || I <= 0 || I % 8 || cb < 0) return (int)hipErrorInvalidValue;
     const int nv = I / 8;
     const dim3 grid((nv + R2_LV - 1) / R2_LV, P);
-    if (fma) WHIP_LAUNCH((k_r2_lutb<true, true>), grid, dim3(R2_EN), 0, s, gu, 0, I, 1, booksT, cb, nv, lut);
-    else WHIP_LAUNCH((k_r2_lutb<false, true>), grid, dim3(R2_EN), 0, s, gu, 0, I, 1, booksT, cb, nv, lut);
+    if (fma) WHIP_LAUNCH((k_r2_lutb<true, true>), grid, dim3(R2_EN), 0, s, gu, 0, I, 1, booksT, cb, nv, lut,
+                         whip_mat{}, nullptr, nullptr, P);
+    else WHIP_LAUNCH((k_r2_lutb<false, true>), grid, dim3(R2_EN), 0, s, gu, 0, I, 1, booksT, cb, nv, lut,
+                     whip_mat{}, nullptr, nullptr, P);
     return (int)hipGetLastError();
 }
 

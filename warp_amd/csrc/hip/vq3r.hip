@@ -195,44 +195,6 @@ VQ_KERNEL(k_vq_rows_down)
 
 #include "vq_tile.h"
 
-// The shared expert's down projection, eight rows r0 .. r0+7 per
-// wavefront: each lane a 16-byte chunk of every row per step against the
-// matching slice of x (fp32), then eight wave sums.  Used by the combine
-// (rows of its block) and by the gate/up launch's spare workgroups.
-template <int FMT>
-__device__ __forceinline__ void sh_rows8_acc(const whip_mat &W, const float *x, int r0, int H, int lane,
-                                             float (&acc)[8])
-{
-    constexpr int NE = chunk_of<FMT>::NE, NW = xw_of<FMT, false>::N;
-    const int ng = FMT == 0 ? 1 : (W.cols + W.group - 1) / W.group;
-    const int C = (FMT == 0 ? W.cols : ng * W.group) / NE;
-    const uint8_t *Wq = (const uint8_t *)W.q;
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = 0.0f;
-    for (int k0 = 0; k0 < C; k0 += 64) {            // uniform
-        const int k = k0 + lane, kc = k < C ? k : 0;
-        uint4 xw[NW], wv[8];
-        uint16_t sv[8];
-        load_xs<FMT, false>(x, W.cols, kc, xw);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int r = min(r0 + i, H - 1);
-            wv[i] = *(const uint4 *)(Wq + (size_t)r * W.rowbytes + (size_t)kc * 16);
-            if (FMT != 0) sv[i] = W.qs[(size_t)r * ng + (size_t)kc * NE / W.group];
-        }
-        if (k < C) {
-            mask_xs<FMT, false>(W.cols, k, xw);
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float d = chunk_dot<FMT, false>(wv[i], xw);
-                acc[i] = FMT == 0 ? acc[i] + d : __fmaf_rn(wh_f16_scale(sv[i]), d, acc[i]);
-            }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] = wave_sum(acc[i]);
-}
-
 // rows row0 + 8w .. of the block's wavefront w into shs (LDS)
 template <int FMT>
 __device__ __forceinline__ void sh_rows8(const whip_mat &W, const float *x, int row0, int H, float *shs)

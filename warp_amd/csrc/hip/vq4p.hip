@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "common.h"
+#include "gemv_dev.h"
 #include "launch.h"
 
 #define P6_BLK 32                      // positions per int8 scale block
@@ -416,6 +417,10 @@ struct p6_tile_args {
     int cb;                            // the first book of kind 0's four
     const void *x;                     // gate/up: input rows (bf16 or fp32)
     int x_bf16, x_ld;
+    whip_mat shd;                      // gate/up at one token, shd_y set: workgroups from
+    const float *shd_x;                //   g_tiles on compute shd_y = shd . shd_x (the shared
+    float *shd_y;                      //   expert's down projection) on the CUs the tiles leave
+    int g_tiles;
     const int16_t *Sg;                 // down: the gate/up sums [p][2][nb_g][I]
     const float *qs_g;                 //       and their tables' scales [tok][2][nb_g]
     uint32_t sc_gate, sc_up;           //       the gate / up row scales in the record
@@ -430,6 +435,10 @@ template <int MODE, bool FMA>
 __global__ void __launch_bounds__(P6_THREADS)
 k_p6_tiles(p6_tile_args a)
 {
+    if (MODE == P6_X && a.shd_y && (int)blockIdx.x >= a.g_tiles) {   // uniform
+        shd_rows_any(a.shd, a.shd_x, a.shd_y, blockIdx.x - a.g_tiles, gridDim.x - a.g_tiles, P6_WAVES);
+        return;
+    }
     constexpr bool ACT = MODE == P6_ACT;
     __shared__ __align__(16) int8_t s_tab[P6_MAXG * P6_BLK * P6_TS];
     __shared__ float s_x[MODE == P6_Q ? 1 : P6_MAXG * 8 * P6_BLK];   // each block's 256 inputs
@@ -658,8 +667,18 @@ static int p6_launch(p6_tile_args &a, int P, int mode, int fma, hipStream_t s)
             a.shares = (nrb + a.per - 1) / a.per;
         }
     }
-    const long grid = groups * a.shares;
+    long grid = groups * a.shares;
     if (grid > 0x7fffffffL) return (int)hipErrorInvalidValue;
+    // the shared down projection on the CUs the tiles leave (at least
+    // eight workgroups, which then run where tiles finish first)
+    a.g_tiles = (int)grid;
+    if (a.shd_y) {
+        int n_cu = 256, dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu < 1)
+            n_cu = 256;
+        grid += n_cu - grid > 8 ? n_cu - grid : 8;
+    }
 #define TL(A, F) WHIP_LAUNCH((k_p6_tiles<A, F>), dim3((unsigned)grid), dim3(P6_THREADS), 0, s, a)
     if (mode == P6_Q) TL(P6_Q, false);
     else if (mode == P6_ACT) { if (fma) TL(P6_ACT, true); else TL(P6_ACT, false); }
@@ -671,12 +690,16 @@ static int p6_launch(p6_tile_args &a, int P, int mode, int fma, hipStream_t s)
 extern "C" int whip_p6_gate_up(const uint8_t *const *recs, const int32_t *pair_exp, const int32_t *pair_tok, int P,
                                const uint32_t *idx_off, int I, const void *x, int x_bf16, int x_ld, int nv,
                                const float *booksT, int cb, int fma, const int8_t *q, int16_t *S, float *qs, int *err,
-                               hipStream_t s)
+                               const whip_mat *shd, const float *shd_x, float *shd_y, hipStream_t s)
 {
     if (P <= 0 || I <= 0 || I % 64 || nv <= 0 || idx_off[0] % 4 || idx_off[1] % 4 || (uintptr_t)q % 16 ||
         (!q && (x_ld < nv * 8 || cb < 0)))
         return (int)hipErrorInvalidValue;
+    // the shared down projection rides along only where the tables are
+    // built here (one token), in whole 16-byte chunks
+    if (shd_y && (q || !shd_rows_ok(shd, shd_x))) return (int)hipErrorInvalidValue;
     p6_tile_args a = {};
+    if (shd_y) { a.shd = *shd; a.shd_x = shd_x; a.shd_y = shd_y; }
     a.recs = recs; a.pair_exp = pair_exp; a.pair_tok = pair_tok; a.kinds = 2;
     a.idx_off0 = idx_off[0]; a.idx_off1 = idx_off[1]; a.M = I; a.nv = nv;
     a.S = S; a.qs = qs; a.err = err; a.q = q; a.booksT = booksT; a.cb = cb;

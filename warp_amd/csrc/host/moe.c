@@ -804,7 +804,7 @@ static int experts_few(waste_hip_moe *m, const void *x, int x_bf16, int T, float
  * down launch, the combine).  The tables and folds follow the engine's
  * arithmetic in the layer's p6_order, so each pair's rows are the engine's
  * bit for bit. */
-static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, hipStream_t s);
+static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, int sh_ready, hipStream_t s);
 
 static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
 {
@@ -820,8 +820,21 @@ static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
     if (q_gu)
         CK((hipError_t)whip_p6_lutq(x, x_bf16, H, T, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.q_gu, m->p6b.s_gu,
                                     s));
-    CK((hipError_t)whip_p6_gate_up(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, gu_idx, I, x, x_bf16, H, m->nv_gu,
-                                   m->d_booksT, cb, fma, q_gu, m->p6b.S_gu, m->p6b.s_gu, m->err, s));
+    /* one token whose shared down projection is still to run: the gate/up
+     * launch's spare workgroups take it (it needs only h_sh) */
+    int sh_ready = 0;
+    int grc = -1;
+    if (!q_gu && m->sh_in_combine) {
+        grc = whip_p6_gate_up(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, gu_idx, I, x, x_bf16, H, m->nv_gu,
+                              m->d_booksT, cb, fma, q_gu, m->p6b.S_gu, m->p6b.s_gu, m->err, &m->sh[2], m->b.h_sh,
+                              m->b.sh_out, s);
+        sh_ready = grc == 0;
+        if (grc != 0 && grc != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
+    }
+    if (!sh_ready)
+        CK((hipError_t)whip_p6_gate_up(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, gu_idx, I, x, x_bf16, H,
+                                       m->nv_gu, m->d_booksT, cb, fma, q_gu, m->p6b.S_gu, m->p6b.s_gu, m->err, NULL,
+                                       NULL, NULL, s));
     MARK(3);
     if (q_d)
         CK((hipError_t)whip_p6_act_lutq(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, m->p6b.S_gu, m->p6b.s_gu, sc_g,
@@ -833,7 +846,7 @@ static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
                                 m->p6b.s_d, m->err, s));
     MARK(5);
     const whip_fold f = { m->p6b.S_d, m->p6b.s_d, (m->nv_d + 31) / 32, m->off_sc + 4u * (uint32_t)I, fma };
-    return alt_combine(m, T, y, &f, s);
+    return alt_combine(m, T, y, &f, sh_ready, s);
 }
 
 /* VQ2R experts (two stages of 256 entries), the same order as VQ4P's above
@@ -848,7 +861,18 @@ static int experts_r2(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
     const int cb = m->cb - m->book0;
     m->ktimed = 0;               /* these stages are timed by the events around them */
     MARK(2);
-    CK((hipError_t)whip_r2_lutb(x, x_bf16, H, T, 2, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.lut_gu, s));
+    /* one token whose shared down projection is still to run: the table
+     * launch's spare workgroups take it (it needs only h_sh) */
+    int sh_ready = 0;
+    if (T == 1 && m->sh_in_combine) {
+        const int rc = whip_r2_lutb(x, x_bf16, H, T, 2, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.lut_gu, &m->sh[2],
+                                    m->b.h_sh, m->b.sh_out, s);
+        sh_ready = rc == 0;
+        if (rc != 0 && rc != (int)hipErrorInvalidValue) return WASTE_HIP_EDEVICE;
+    }
+    if (!sh_ready)
+        CK((hipError_t)whip_r2_lutb(x, x_bf16, H, T, 2, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.lut_gu, NULL, NULL,
+                                    NULL, s));
     const uint32_t gu_idx[2] = { m->off_gate, m->off_up };
     const uint32_t gu_sc[2] = { m->off_sc, m->off_sc + 2u * (uint32_t)I };
     CK((hipError_t)whip_r2_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 2, gu_idx, gu_sc, I, m->nv_gu,
@@ -860,16 +884,17 @@ static int experts_r2(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
     CK((hipError_t)whip_r2_rows_pairs(m->d_recs, m->b.pair_exp, m->b.pair_tok, P, 1, d_idx, d_sc, H, m->nv_d,
                                       m->p6b.lut_d, 0, m->p6b.down, m->err, s));
     MARK(5);
-    return alt_combine(m, T, y, NULL, s);
+    return alt_combine(m, T, y, NULL, sh_ready, s);
 }
 
 /* The combine of the VQ4P / VQ2R paths: each pair's down rows folded from
  * f (VQ4P) or in p6b.down, already scaled, one chunk each (VQ2R); the
- * shared expert as for VQ3R. */
-static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, hipStream_t s)
+ * shared expert as for VQ3R (sh_ready: its down projection already in
+ * sh_out). */
+static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, int sh_ready, hipStream_t s)
 {
     const int K = m->K, H = m->H;
-    if (m->sh_in_combine) {
+    if (m->sh_in_combine && !sh_ready) {
         MARK(6);
         const int rc = f ? whip_combine_sh_fold(m->d_recs, m->b.pair_exp, m->b.pair_w, m->b.tok_pairs, T, K, f, H,
                                                 T > 1, &m->sh[2], m->b.h_sh, y, s)
@@ -884,7 +909,7 @@ static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, hi
     }
     const float *shp = m->has_shared ? m->b.sh_out : NULL;
     int sh_n = 1;
-    if (m->has_shared && !m->sh_done && !m->sh_in_combine) {
+    if (m->has_shared && !m->sh_done && !m->sh_in_combine && !sh_ready) {
         if (T > 1 && m->b.sk_part) {
             whip_sk_job j;
             j.A = m->sh[2]; j.x = m->b.h_sh; j.x_ld = m->SI; j.x_bf16 = 0; j.part = m->b.sk_part;
