@@ -12,6 +12,8 @@ tables) and VQ2R (two stages of 256 entries, fp32 tables).
                              routed row then equals the engine's); with a
                              shared expert (a GEMV in another summation
                              order) within 1e-3
+  many pairs                 a VQ4P forward of 40 tokens (its pairs in chunks):
+                             bit-exact as above
   through the expert cache   forward_cached over a cache smaller than the
                              expert set: outputs bit-exact as above
   records                    a VQ3R record is refused by a VQ4P layer and a
@@ -108,6 +110,24 @@ def test_format_layer_forward(orc, name, order):
             assert e <= LAYER_RTOL
         else:
             assert np.array_equal(bits(y), bits(ref)), (T, e)
+    m.close()
+
+
+@pytest.mark.parametrize("order", [0, 1])
+def test_format_layer_many_pairs(orc, order):
+    """A VQ4P forward of 40 tokens (320 pairs) runs its pairs in chunks of
+    256 and folds their down rows before the combine: bit-exact against the
+    oracle's chunk order as at 8 tokens."""
+    say("test_format_layer_many_pairs", order)
+    L, bf16 = make("p6_softmax")
+    m = gpu_layer(L, max_tokens=40, p6_order=order)
+    X = inputs(L, 40, 760, bf16)
+    st, y, ids, w, lg = run_forward(torch, m, L, X, bf16=bf16)
+    assert st == 0
+    check_routing(orc, L, lg, ids, w)
+    ref = oracle_apply(orc, L, order, X, ids, w, 1)
+    say(f"  T=40: rel err {rel_err(y, ref):.3e}")
+    assert np.array_equal(bits(y), bits(ref))
     m.close()
 
 

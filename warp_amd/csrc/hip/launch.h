@@ -220,6 +220,11 @@ int whip_p6_down(const uint8_t *const *recs, const int32_t *pair_exp, const int3
                  uint32_t idx_off, int H, int I, const int16_t *Sg, const float *qs_g, uint32_t sc_gate,
                  uint32_t sc_up, int nv_g, const float *booksT, int cb, int fma, const int8_t *q, int16_t *S,
                  float *qs, int *err, hipStream_t s);
+/* Each pair's down rows y[p][M] folded from whip_p6_down's sums S (nb
+ * blocks a pair) with its table scales ls[p][nb], times the f16 row scale at
+ * sc_off of its record; zeros for an unbound expert. */
+int whip_p6_fold_pairs(const uint8_t *const *recs, const int32_t *pair_exp, int P, const int16_t *S,
+                       const float *ls, int nb, int M, uint32_t sc_off, int fma, float *y, hipStream_t s);
 /* VQ2R (vq2r.hip): fp32 tables lut[t][nv][st][256] of rows x kinds inputs in
  * the engine's order (st == 2; shd_y set: spare workgroups also compute
  * shd_y = shd . shd_x, refused for shapes they do not take), and every

@@ -802,3 +802,45 @@ static int p6_rows_tiled(const uint8_t *idx, const uint16_t *scale, const int8_t
     }
     return rc;
 }
+
+// Each pair's down rows folded from its block sums (whip_p6_down's S, nb
+// blocks of M rows a pair, its table scales ls[p][nb]) in block order, times
+// the row's f16 scale at sc_off of its record; an unbound expert's rows are
+// zeros.  y[p][M]: the rows the combine adds, one chunk each.
+template <bool FMA>
+__global__ void __launch_bounds__(256)
+k_p6_fold_pairs(const uint8_t *const *__restrict__ recs, const int32_t *__restrict__ pair_exp,
+                const int16_t *__restrict__ S, const float *__restrict__ ls, int nb, int M, uint32_t sc_off,
+                float *__restrict__ y)
+{
+    const int p = blockIdx.y, r = blockIdx.x * 256 + threadIdx.x;
+    if (r >= M) return;
+    const uint8_t *rec = recs[pair_exp[p]];
+    const int16_t *Sp = S + (size_t)p * nb * M + r;
+    const float *lp = ls + (size_t)p * nb;
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < nb; k0 += P6_MAXB) {        // every block's sums in flight, then the fold
+        const int kn = min(P6_MAXB, nb - k0);
+        int16_t sv[P6_MAXB];
+#pragma unroll
+        for (int k = 0; k < P6_MAXB; k++) sv[k] = Sp[(size_t)(k0 + (k < kn ? k : 0)) * M];
+#pragma unroll
+        for (int k = 0; k < P6_MAXB; k++)
+            if (k < kn) {
+                const float f = (float)sv[k];
+                acc = FMA ? __fmaf_rn(lp[k0 + k], f, acc) : __fadd_rn(acc, __fmul_rn(lp[k0 + k], f));
+            }
+    }
+    y[(size_t)p * M + r] = rec ? __fmul_rn(acc, wh_f16_scale(((const uint16_t *)(rec + sc_off))[r])) : 0.0f;
+}
+
+extern "C" int whip_p6_fold_pairs(const uint8_t *const *recs, const int32_t *pair_exp, int P, const int16_t *S,
+                                  const float *ls, int nb, int M, uint32_t sc_off, int fma, float *y, hipStream_t s)
+{
+    if (P <= 0 || P > 65535 || nb <= 0 || M <= 0 || sc_off % 2) return (int)hipErrorInvalidValue;
+    const dim3 grid((M + 255) / 256, P);
+    if (fma) WHIP_LAUNCH(k_p6_fold_pairs<true>, grid, dim3(256), 0, s, recs, pair_exp, S, ls, nb, M, sc_off, y);
+    else WHIP_LAUNCH(k_p6_fold_pairs<false>, grid, dim3(256), 0, s, recs, pair_exp, S, ls, nb, M, sc_off, y);
+    return (int)hipGetLastError();
+}
+

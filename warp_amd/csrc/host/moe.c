@@ -26,6 +26,7 @@
 #include <string.h>
 
 #define CK(call) do { if ((call) != hipSuccess) return WASTE_HIP_EDEVICE; } while (0)
+#define P6_PAIR_CHUNK 256        /* VQ4P pairs whose block sums one pass holds */
 
 /* The device buffers one forward writes and reads back: logits, the
  * selection and its pair lists, the expert partials, the shared expert's
@@ -97,7 +98,8 @@ struct waste_hip_moe {
         int8_t *q_gu, *q_d;      /* VQ4P: int8 tables [T][2][nv_gu][256], [P][nv_d][256] */
         float *s_gu, *s_d;       /* and their scales, one per 32 positions */
         int16_t *S_gu, *S_d;     /* VQ4P block sums [P][2][nb_gu][I], [P][nb_d][H] */
-        float *gu, *down;        /* VQ2R: rows [P][2][I], down [P][H]      */
+        float *gu, *down;        /* VQ2R: rows [P][2][I], down [P][H]; VQ4P
+                                    above P6_PAIR_CHUNK pairs: down [P][H] */
     } p6b;
     /* few-token products on the matrix cores (skinny.hip): column slices of
      * the router, the shared gate/up and the shared down (0: not taken),
@@ -262,16 +264,20 @@ int waste_hip_moe_create(const waste_hip_moe_cfg *cfg, waste_hip_moe **out)
         rc |= dmalloc((void **)&m->p6b.gu, (size_t)P * 2 * m->I * 4);
         rc |= dmalloc((void **)&m->p6b.down, (size_t)P * m->H * 4);
     } else if (m->p6) {
+        /* the pair buffers hold one chunk of at most P6_PAIR_CHUNK pairs;
+         * more pairs fold their down rows into p6b.down */
         const size_t tg = (size_t)m->nv_gu * 256, td = (size_t)m->nv_d * 256;
         const size_t bg = (size_t)(m->nv_gu + 31) / 32, bd = (size_t)(m->nv_d + 31) / 32;
+        const size_t Pc = P < P6_PAIR_CHUNK ? (size_t)P : P6_PAIR_CHUNK;
         if (m->T > 1) {
             rc |= dmalloc((void **)&m->p6b.q_gu, (size_t)m->T * 2 * tg);
-            rc |= dmalloc((void **)&m->p6b.q_d, (size_t)P * td);
+            rc |= dmalloc((void **)&m->p6b.q_d, Pc * td);
         }
         rc |= dmalloc((void **)&m->p6b.s_gu, (size_t)m->T * 2 * bg * 4);
-        rc |= dmalloc((void **)&m->p6b.s_d, (size_t)P * bd * 4);
-        rc |= dmalloc((void **)&m->p6b.S_gu, (size_t)P * 2 * bg * m->I * 2);
-        rc |= dmalloc((void **)&m->p6b.S_d, (size_t)P * bd * m->H * 2);
+        rc |= dmalloc((void **)&m->p6b.s_d, Pc * bd * 4);
+        rc |= dmalloc((void **)&m->p6b.S_gu, Pc * 2 * bg * m->I * 2);
+        rc |= dmalloc((void **)&m->p6b.S_d, Pc * bd * m->H * 2);
+        if ((size_t)P > Pc) rc |= dmalloc((void **)&m->p6b.down, (size_t)P * m->H * 4);
     } else {
         /* + 64 floats: the apply kernels' sink for rows past a split's end */
         rc |= dmalloc((void **)&m->b.part_gu, ((size_t)Pd * 2 * m->nch_gu * m->I + 64) * 4);
@@ -809,9 +815,9 @@ static int alt_combine(waste_hip_moe *m, int T, float *y, const whip_fold *f, in
 static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float *y, hipStream_t s)
 {
     const int K = m->K, H = m->H, I = m->I, P = T * K, fma = m->c.p6_order == WASTE_HIP_ORDER_FMA;
-    const int cb = m->cb - m->book0, cb_d = cb + 2 * m->stages;
+    const int cb = m->cb - m->book0, cb_d = cb + 2 * m->stages, nb_d = (m->nv_d + 31) / 32;
     const uint32_t gu_idx[2] = { m->off_gate, m->off_up };
-    const uint32_t sc_g = m->off_sc, sc_u = m->off_sc + 2u * (uint32_t)I;
+    const uint32_t sc_g = m->off_sc, sc_u = m->off_sc + 2u * (uint32_t)I, sc_d = m->off_sc + 4u * (uint32_t)I;
     /* one token: the tile launches build their tables (two launches fewer);
      * more: the tables once per token and pair, the tiles read them */
     const int8_t *q_gu = T > 1 ? m->p6b.q_gu : NULL, *q_d = T > 1 ? m->p6b.q_d : NULL;
@@ -820,6 +826,27 @@ static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
     if (q_gu)
         CK((hipError_t)whip_p6_lutq(x, x_bf16, H, T, 2, m->d_booksT, cb, m->nv_gu, fma, m->p6b.q_gu, m->p6b.s_gu,
                                     s));
+    if (P > P6_PAIR_CHUNK) {
+        /* many pairs: chunks of P6_PAIR_CHUNK pairs, each pair's down rows
+         * folded into p6b.down, which the combine reads */
+        for (int c0 = 0; c0 < P; c0 += P6_PAIR_CHUNK) {
+            const int n = P - c0 < P6_PAIR_CHUNK ? P - c0 : P6_PAIR_CHUNK;
+            const int32_t *pe = m->b.pair_exp + c0, *pt = m->b.pair_tok + c0;
+            CK((hipError_t)whip_p6_gate_up(m->d_recs, pe, pt, n, gu_idx, I, x, x_bf16, H, m->nv_gu, m->d_booksT, cb,
+                                           fma, q_gu, m->p6b.S_gu, m->p6b.s_gu, m->err, NULL, NULL, NULL, s));
+            CK((hipError_t)whip_p6_act_lutq(m->d_recs, pe, pt, n, m->p6b.S_gu, m->p6b.s_gu, sc_g, sc_u, I, m->nv_gu,
+                                            m->d_booksT, cb_d, m->nv_d, fma, m->p6b.q_d, m->p6b.s_d, s));
+            CK((hipError_t)whip_p6_down(m->d_recs, pe, pt, n, m->off_down, H, I, m->p6b.S_gu, m->p6b.s_gu, sc_g,
+                                        sc_u, m->nv_gu, m->d_booksT, cb_d, fma, m->p6b.q_d, m->p6b.S_d, m->p6b.s_d,
+                                        m->err, s));
+            CK((hipError_t)whip_p6_fold_pairs(m->d_recs, pe, n, m->p6b.S_d, m->p6b.s_d, nb_d, H, sc_d, fma,
+                                              m->p6b.down + (size_t)c0 * H, s));
+        }
+        MARK(3);
+        MARK(4);
+        MARK(5);
+        return alt_combine(m, T, y, NULL, 0, s);
+    }
     /* one token whose shared down projection is still to run: the gate/up
      * launch's spare workgroups take it (it needs only h_sh) */
     int sh_ready = 0;
@@ -845,7 +872,7 @@ static int experts_p6(waste_hip_moe *m, const void *x, int x_bf16, int T, float 
                                 m->p6b.s_gu, sc_g, sc_u, m->nv_gu, m->d_booksT, cb_d, fma, q_d, m->p6b.S_d,
                                 m->p6b.s_d, m->err, s));
     MARK(5);
-    const whip_fold f = { m->p6b.S_d, m->p6b.s_d, (m->nv_d + 31) / 32, m->off_sc + 4u * (uint32_t)I, fma };
+    const whip_fold f = { m->p6b.S_d, m->p6b.s_d, nb_d, sc_d, fma };
     return alt_combine(m, T, y, &f, sh_ready, s);
 }
 
