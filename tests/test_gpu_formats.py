@@ -14,6 +14,8 @@ tables) and VQ2R (two stages of 256 entries, fp32 tables).
                              order) within 1e-3
   many pairs                 a VQ4P forward of 40 tokens (its pairs in chunks):
                              bit-exact as above
+  full size                  both formats at the C3 expert shape (7168 x
+                             2048), batch 1 and 8, both orders: bit-exact
   through the expert cache   forward_cached over a cache smaller than the
                              expert set: outputs bit-exact as above
   records                    a VQ3R record is refused by a VQ4P layer and a
@@ -110,6 +112,36 @@ def test_format_layer_forward(orc, name, order):
             assert e <= LAYER_RTOL
         else:
             assert np.array_equal(bits(y), bits(ref)), (T, e)
+    m.close()
+
+
+_FULL = {}
+
+
+def full_layer(fmt):
+    """The DeepSeek-V3 expert shape (hidden 7168, inter 2048), eight experts,
+    top-8 (so batch 8 holds 64 pairs), softmax, no shared expert."""
+    if fmt not in _FULL:
+        _FULL[fmt] = Layer(7168, 2048, 8, 8, score_func=1, seed=81 if fmt == "p6" else 82, **FMT[fmt])
+    return _FULL[fmt]
+
+
+@pytest.mark.parametrize("fmt", ["p6", "r2"])
+@pytest.mark.parametrize("order", [0, 1])
+def test_format_layer_fullsize(orc, fmt, order):
+    """Both formats at the C3 expert shape the bench measures, batch 1 and 8:
+    outputs bit-exact against the oracle in both of the engine's orders."""
+    say("test_format_layer_fullsize", fmt, order)
+    L = full_layer(fmt)
+    m = gpu_layer(L, max_tokens=8, p6_order=order)
+    for T in (1, 8):
+        X = inputs(L, T, 780 + T, False)
+        st, y, ids, w, lg = run_forward(torch, m, L, X)
+        assert st == 0
+        check_routing(orc, L, lg, ids, w)
+        ref = oracle_apply(orc, L, order, X, ids, w, T > 1)
+        say(f"  T={T}: rel err {rel_err(y, ref):.3e}, bit-exact {np.array_equal(bits(y), bits(ref))}")
+        assert np.array_equal(bits(y), bits(ref)), (T, rel_err(y, ref))
     m.close()
 
 
