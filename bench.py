@@ -727,7 +727,7 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build's MoE path runs on a single MI355X and "
-              f"--gpus {a.gpus} is not supported (expert-parallel sharding is described in DESIGN.md).",
+              f"--gpus {a.gpus} is not supported (expert-parallel sharding over several GPUs is not built).",
               file=sys.stderr)
         return 2
 

@@ -5,7 +5,7 @@ import numpy as np
 
 import warp_amd
 
-# The north star's tolerance for layer outputs: max relative error 1e-3 with
+# The tolerance for layer outputs: max relative error 1e-3 with
 # fp32 accumulation, measured normwise (max |y - ref| / max |ref|).
 LAYER_RTOL = 1e-3
 # Router logits are an fp32 GEMV in a different summation order.

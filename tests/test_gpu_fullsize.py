@@ -8,7 +8,7 @@ copied back to the host.
 
 Bars: expert ids/weights bit-exact against the oracle's router on the
 device's logits; router logits max rel error 1e-5; layer output max rel
-error 1e-3 (north star) on the same routing; and the synthetic encoder's
+error 1e-3 on the same routing; and the synthetic encoder's
 stage indices are the nearest entries, checked by brute force.
 """
 import ctypes as C

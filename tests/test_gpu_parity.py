@@ -6,7 +6,7 @@ Bars (written here, per check):
   expert ids and weights       bit-exact against the oracle's router on the
                                device's own fp32 logits
   router logits                max rel error 1e-5 (fp32 GEMV, other order)
-  layer output                 max rel error 1e-3 (north star), on the same
+  layer output                 max rel error 1e-3, on the same
                                routing, fp32 accumulation
   VQ3R batch entry             bit-exact (the engine's exact row order)
 """
