@@ -46,18 +46,19 @@ __device__ __forceinline__ void load_tile(tile_buf &b, g_u8 *base, uint32_t loff
 
 // one tile: 32 rows of this lane's half at its position, then the reduce.
 // The buffer is consumed in place (row half 1's byte swap overwrites it).
-__device__ __forceinline__ float lookup3(const char *L, const uint32_t *d, int j, uint32_t bA0,
-                                         uint32_t bA1, uint32_t bB)
+//
+// The three table reads of rows j and 16 + j (o[st] and o[3 + st]).
+__device__ __forceinline__ void lookup6(const char *L, const uint32_t *d, int j, uint32_t bA0, uint32_t bA1,
+                                        uint32_t bB, float *o)
 {
-    float t[3];
 #pragma unroll
     for (int st = 0; st < 3; st++) {
-        const int byte = 3 * j + st;
         const uint32_t base = st == 0 ? bA0 : st == 1 ? bA1 : bB;
-        const uint32_t a = __builtin_amdgcn_perm(d[byte >> 2], base, 0x03020000u | ((4u + (byte & 3)) << 8));
-        t[st] = *(const float *)(L + a);
+        const int b0 = 3 * j + st, b1 = 3 * (16 + j) + st;
+        o[st] = *(const float *)(L + __builtin_amdgcn_perm(d[b0 >> 2], base, 0x03020000u | ((4u + (b0 & 3)) << 8)));
+        o[3 + st] =
+            *(const float *)(L + __builtin_amdgcn_perm(d[b1 >> 2], base, 0x03020000u | ((4u + (b1 & 3)) << 8)));
     }
-    return (t[0] + t[1]) + t[2];
 }
 
 __device__ __forceinline__ float tile_sum(tile_buf &b, const float *smem, uint32_t bA0, uint32_t bA1,
@@ -76,13 +77,23 @@ __device__ __forceinline__ float tile_sum(tile_buf &b, const float *smem, uint32
     }
     const char *L = (const char *)smem;
     // rows j and 16 + j, folded at once by the first reduce step (a lane
-    // swap at offset 16): e[j] is row j on lanes 0-15, row 16 + j on 16-31
+    // swap at offset 16): e[j] is row j on lanes 0-15, row 16 + j on 16-31.
+    // Software-pipelined: the reads of step j + 1 go out before step j's
+    // are summed, so twelve reads are in flight at each wait instead of
+    // the compiler's own eight-read bursts, each summed as soon as it is
+    // sent (the scheduling barriers keep the order).
     float e[16];
+    float t[2][6];
+    lookup6(L, d, 0, bA0, bA1, bB, t[0]);
 #pragma unroll
     for (int j = 0; j < 16; j++) {
-        const float lo = lookup3(L, d, j, bA0, bA1, bB), hi = lookup3(L, d, 16 + j, bA0, bA1, bB);
+        if (j + 1 < 16) lookup6(L, d, j + 1, bA0, bA1, bB, t[(j + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        const float *c = t[j & 1];
+        const float lo = (c[0] + c[1]) + c[2], hi = (c[3] + c[4]) + c[5];
         const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
         e[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        __builtin_amdgcn_sched_barrier(0);
     }
     const bool b3 = (lane >> 3) & 1, b2 = (lane >> 2) & 1, b0 = lane & 1, b1 = (lane >> 1) & 1;
     float f[8];
