@@ -9,6 +9,9 @@
  * encode; src/vq.c:50-107 nearest-centroid assignment; tools/convert.py:
  * 942-977 record layout), run on generated weights instead of a
  * checkpoint, because a DeepSeek-V3-sized layer holds 11.3 G weights.
+ *
+ * Built into libwaste_hip_synth.so, not into the product library: the
+ * engine never calls these.
  */
 #ifndef WASTE_HIP_SYNTH_H
 #define WASTE_HIP_SYNTH_H

@@ -11,12 +11,15 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 INC = os.path.join(ROOT, "include")
 LIB = os.path.join(ROOT, "warp_amd", "libwaste_hip.so")
+SYNTH_LIB = os.path.join(ROOT, "warp_amd", "libwaste_hip_synth.so")
+# The synthetic record generator's header; its library is separate.
+SYNTH_H = "waste_hip_synth.h"
 
 
-def declared():
+def declared(only=None, skip=()):
     names = []
     for f in sorted(os.listdir(INC)):
-        if not f.endswith(".h"):
+        if not f.endswith(".h") or f in skip or (only and f != only):
             continue
         src = open(os.path.join(INC, f)).read()
         src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
@@ -27,16 +30,29 @@ def declared():
 def test_library_exports_every_declared_symbol():
     assert os.path.exists(LIB), "build first: python -m warp_amd.build"
     lib = ctypes.CDLL(LIB)
-    names = declared()
+    names = declared(skip=(SYNTH_H,))
     assert len(names) >= 15
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
 
 
+def test_product_library_holds_no_generator():
+    """The synthetic record generator is test and benchmark data: its
+    symbols are in libwaste_hip_synth.so and not in the product."""
+    lib = ctypes.CDLL(LIB)
+    synth = declared(only=SYNTH_H)
+    assert len(synth) == 3
+    assert not [n for n in synth if hasattr(lib, n)]
+    slib = ctypes.CDLL(SYNTH_LIB)
+    assert not [n for n in synth if not hasattr(slib, n)]
+    assert not hasattr(slib, "waste_hip_moe_forward")
+
+
 def test_python_mirror_lists_every_symbol():
     import warp_amd
-    assert sorted(warp_amd.EXPORTS) == sorted(n for n in declared() if not n.startswith("waste_hip_synth")) \
-        or set(warp_amd.EXPORTS) <= set(declared())
+    from warp_amd import synth
+    assert sorted(warp_amd.EXPORTS) == declared(skip=(SYNTH_H,))
+    assert sorted(synth.SYNTH_EXPORTS) == declared(only=SYNTH_H)
 
 
 def test_headers_compile_standalone(tmp_path):

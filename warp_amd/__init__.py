@@ -31,14 +31,14 @@ OK, EINVAL, ENODEV, ENOMEM, ERECORD, ECRC, EUNBOUND, EROUTE, EDEVICE, ERANGE, ET
 EFORMAT, EIO = -12, -13
 CT_RECORDS, CT_GROUP_LIMIT = 1, 2
 
-# Every symbol include/waste_hip.h declares.
+# Every symbol include/waste_hip.h declares (include/waste_hip_synth.h's are
+# in libwaste_hip_synth.so: warp_amd.synth).
 EXPORTS = ["waste_hip_device_name", "waste_register_hip", "waste_hip_release_host_buffers",
            "waste_hip_vq3r", "waste_hip_moe_create", "waste_hip_moe_destroy",
            "waste_hip_moe_set_router", "waste_hip_moe_set_shared", "waste_hip_moe_set_codebooks",
            "waste_hip_moe_set_expert", "waste_hip_moe_bind_expert", "waste_hip_moe_forward",
            "waste_hip_moe_status", "waste_hip_moe_bytes", "waste_hip_moe_dequant",
-           "waste_hip_moe_profile", "waste_hip_moe_profile_read", "waste_hip_record_bytes",
-           "waste_hip_synth_codebooks", "waste_hip_synth_records",
+           "waste_hip_moe_profile", "waste_hip_moe_profile_read",
            "waste_hip_moe_route", "waste_hip_moe_experts", "waste_hip_moe_bind_table",
            "waste_hip_moe_predict", "waste_hip_moe_set_lookahead_groups", "waste_hip_moe_forward_cached",
            "waste_hip_moe_forward_static", "waste_hip_moe_static_bytes",

@@ -1,6 +1,8 @@
 # SPDX-License-Identifier: Apache-2.0
 """Builds warp_amd/libwaste_hip.so in-tree: the gfx950 kernels (hipcc) and
-the C host code (gcc), linked against the HIP runtime.
+the C host code (gcc), linked against the HIP runtime.  The synthetic record
+generator (synth.hip, synth.c) links into warp_amd/libwaste_hip_synth.so
+beside it: tests and the benchmark load it, the product does not.
 
     python -m warp_amd.build            # rebuild what changed
     python -m warp_amd.build --force    # rebuild everything
@@ -19,6 +21,10 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libwaste_hip.so")
+# The synthetic record generator (tests and the benchmark's data, not the
+# engine's path) is a library of its own.
+SYNTH_LIB = os.path.join(PKG, "libwaste_hip_synth.so")
+SYNTH_SOURCES = ("synth.hip", "synth.c")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
@@ -64,29 +70,39 @@ def _run(cmd):
     return err
 
 
+def _link(lib, objs, force):
+    # relinked when an object is newer or the object list changed
+    listing = os.path.join(OBJ, os.path.basename(lib) + ".objs")
+    want = "\n".join(objs)
+    have = open(listing).read() if os.path.exists(listing) else None
+    if force or have != want or not os.path.exists(lib) or \
+            any(os.path.getmtime(o) > os.path.getmtime(lib) for o in objs):
+        _run([HIPCC, "--offload-arch=gfx950", "-mcode-object-version=5", "-shared", "-fPIC", "-o", lib + ".tmp"] + objs +
+             ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lpthread"])
+        os.replace(lib + ".tmp", lib)
+        with open(listing, "w") as f:
+            f.write(want)
+
+
 def build(force=False, verbose=False):
+    """Builds libwaste_hip.so (the product) and libwaste_hip_synth.so (the
+    synthetic record generator); returns the product's path."""
     os.makedirs(OBJ, exist_ok=True)
     hip, c = sources()
     deps = headers()
-    jobs, objs = [], []
-    for s in hip:
+    jobs, objs, synth = [], [], []
+    for s in hip + c:
         o = os.path.join(OBJ, os.path.basename(s) + ".o")
-        objs.append(o)
+        (synth if os.path.basename(s) in SYNTH_SOURCES else objs).append(o)
         if force or _stale(s, o, deps):
-            jobs.append([HIPCC] + HIPFLAGS + INC + ["-c", s, "-o", o])
-    for s in c:
-        o = os.path.join(OBJ, os.path.basename(s) + ".o")
-        objs.append(o)
-        if force or _stale(s, o, deps):
-            jobs.append(["gcc"] + CFLAGS + INC + ["-c", s, "-o", o])
+            cc = [HIPCC] + HIPFLAGS if s.endswith(".hip") else ["gcc"] + CFLAGS
+            jobs.append(cc + INC + ["-c", s, "-o", o])
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
         for msg in ex.map(_run, jobs):
             if verbose and msg.strip():
                 print(msg)
-    if force or jobs or not os.path.exists(LIB):
-        _run([HIPCC, "--offload-arch=gfx950", "-mcode-object-version=5", "-shared", "-fPIC", "-o", LIB + ".tmp"] + objs +
-             ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lpthread"])
-        os.replace(LIB + ".tmp", LIB)
+    _link(LIB, objs, force)
+    _link(SYNTH_LIB, synth, force)
     return LIB
 
 

@@ -6,13 +6,20 @@ quantised as the converter does (Q8G: scale = amax/127, Q4G: amax/7, f16
 scales per group of 128, round half to even; tools/convert.py:893-924).
 Expert records are generated and VQ3R-encoded on the device
 (waste_hip_synth_records) against seeded residual k-means codebooks
-(waste_hip_synth_codebooks).
+(waste_hip_synth_codebooks).  Those live in libwaste_hip_synth.so, beside
+the product library and separate from it: test and benchmark data only.
 """
 import ctypes as C
+import os
 
 import numpy as np
 
-from . import WQ_F32, WQ_Q4G, WQ_Q8G, check, lib
+from . import LIB_PATH, WQ_F32, WQ_Q4G, WQ_Q8G, HipError, check
+
+SYNTH_LIB_PATH = os.environ.get("WARP_AMD_SYNTH_LIB") or os.path.join(os.path.dirname(LIB_PATH),
+                                                                      "libwaste_hip_synth.so")
+# Every symbol include/waste_hip_synth.h declares.
+SYNTH_EXPORTS = ["waste_hip_record_bytes", "waste_hip_synth_codebooks", "waste_hip_synth_records"]
 
 # The MoE layer shapes the measurements are quoted on.
 CONFIGS = {
@@ -84,18 +91,26 @@ class Tensor:
         return Tensor(fmt, rows, cols, 128, q, qs, rb)
 
 
+_slib = None
+
+
 def _sigs():
-    L = lib()
-    if not hasattr(L, "_synth_ready"):
-        L.waste_hip_record_bytes.restype = C.c_size_t
-        L.waste_hip_record_bytes.argtypes = [C.c_int, C.c_int]
-        L.waste_hip_synth_codebooks.restype = C.c_int
-        L.waste_hip_synth_codebooks.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_void_p]
-        L.waste_hip_synth_records.restype = C.c_int
-        L.waste_hip_synth_records.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
-                                              C.c_int, C.c_int, C.c_void_p, C.c_float, C.c_void_p,
-                                              C.c_void_p]
-        L._synth_ready = True
+    """The loaded generator library; raises if it has not been built."""
+    global _slib
+    if _slib is not None:
+        return _slib
+    if not os.path.exists(SYNTH_LIB_PATH):
+        raise HipError(f"{SYNTH_LIB_PATH} is missing: build it with `python -m warp_amd.build`")
+    L = C.CDLL(SYNTH_LIB_PATH)
+    L.waste_hip_record_bytes.restype = C.c_size_t
+    L.waste_hip_record_bytes.argtypes = [C.c_int, C.c_int]
+    L.waste_hip_synth_codebooks.restype = C.c_int
+    L.waste_hip_synth_codebooks.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_void_p]
+    L.waste_hip_synth_records.restype = C.c_int
+    L.waste_hip_synth_records.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_int, C.c_int, C.c_void_p,
+                                          C.c_int, C.c_int, C.c_void_p, C.c_float, C.c_void_p,
+                                          C.c_void_p]
+    _slib = L
     return L
 
 
