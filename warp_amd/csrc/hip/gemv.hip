@@ -635,10 +635,12 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
     __shared__ const uint8_t *s_recs[256];
     __shared__ const uint8_t *s_rec[64];
     __shared__ uint64_t s_etab[32];
+    __shared__ int s_late;                            // a logit missed its tag (routing block)
     WT_SPAN(0, 0);
     WT_DECL;
     WT_KEEP(0);
     const int nrb = pk.j[0].nblk, tid = threadIdx.x, E = c.E, K = c.K;
+    if (tid == 0) s_late = 0;                         // the product's barriers order it before the ORs
     const bool routing = (int)blockIdx.x == nrb - 1;  // uniform
     // This launch's tag: one past the last launch's, kept in the word before
     // the exchange (the routing block advances it once every router block
@@ -689,7 +691,13 @@ k_gemv1_xroute(gemv_pack pk, whip_route_cfg c, const float *__restrict__ bias, i
         }
         l = __uint_as_float((uint32_t)v);
     }
-    const int any_late = __syncthreads_or(late);
+    // The OR through LDS and a plain barrier: __syncthreads_or reads the
+    // workgroup size from the kernel's implicit arguments, a scalar load
+    // that here, after the product's stream, misses every cache and sits
+    // on the routing's critical path.
+    if (late) s_late = 1;
+    __syncthreads();
+    const int any_late = s_late;
     if (tid == 0) coh_st(ew, (uint64_t)epoch);       // the next launch's tag follows this one
     if (any_late) {
         if (tid == 0) atomicOr(err, 16);
