@@ -704,17 +704,22 @@ __device__ __forceinline__ void route_fast(const whip_route_cfg &c, float l, flo
         }
     }
     WT_L(3);
-    // each wavefront's keys sorted; its first K are the candidates
+    // each wavefront's keys sorted; its first K are the candidates.  With
+    // one wavefront of experts, wavefront 0 sorts its own keys: no exchange.
+    uint64_t key0 = 0;
     if (wv < ewv) {                                          // uniform
         const uint64_t key = tid < E ? sel_key(kept ? selv : NEG_INF, tid) : 0;
-        const uint64_t srt = ewv == 1 ? key : wave_sort_desc(key, lane);
-        if (ewv > 1 && lane < K) s_cand[wv * K + lane] = srt;
-        if (ewv == 1) s_cand[lane] = key;
+        if (ewv > 1) {
+            const uint64_t srt = wave_sort_desc(key, lane);
+            if (lane < K) s_cand[wv * K + lane] = srt;
+        } else {
+            key0 = key;
+        }
     }
-    __syncthreads();
+    if (ewv > 1) __syncthreads();                            // uniform
     WT_L(4);
     if (wv == 0) {
-        const uint64_t cv = lane < (ewv > 1 ? ewv * K : 64) ? s_cand[lane] : 0;
+        const uint64_t cv = ewv > 1 ? (lane < ewv * K ? s_cand[lane] : 0) : key0;
         const uint64_t srt = wave_sort_desc(cv, lane);
         WT_L(5);
         // lane p < K: the p-th selection; its weight the unbiased score.
